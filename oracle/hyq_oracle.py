@@ -1,0 +1,553 @@
+"""CPU oracle for HyQuant's hybrid-precision attention hot path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the `hyquant_amd` product path may import,
+call or link this module: only `tests/`, `__graft_entry__.smoke()` and the
+`cpu_baseline` leg of `bench.py` use it, and only as the checker.
+
+Every function restates the reference's algorithm from its source (cited as
+`path:line` relative to the HyQuant repository root) in numpy / torch-CPU code
+written for this repository.  Arrays holding "bf16" data are float32 arrays
+whose values are exactly representable in bfloat16.
+
+Parity pins (the tests under tests/ that check this oracle independently of
+its own formulas):
+  quantize_per_token / pack / unpack  -> hand-computed known answers, nibble
+      layout vectors, round-half-even ties, subnormal and overflow scales,
+      round-trip and |x - deq(x)| <= scale/2 invariants.
+  compute_vertical_indices            -> brute-force full sort on tiny inputs,
+      planted-line known answer, rho=1 selects everything, tie rule vectors,
+      exact-dot cross-check against Python integer/fraction arithmetic.
+  freeze                              -> partition invariants (topk U compact =
+      prefix, disjoint, compact ascending), window = last W, brute force.
+  decode_fp64                         -> closed forms: N_q = 0 reduces to plain
+      softmax attention (checked against torch fp64 SDPA), segment permutation
+      invariance, GQA equals explicit head expansion, single-token softmax = v.
+  decode_bf16_eager                   -> same inputs agree with decode_fp64 to
+      bf16 precision.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional, Tuple
+
+import numpy as np
+
+GROUP_SIZE = 128          # staging ring size; src/ops/decode_d_stage.py:19
+LOG2E = 1.44269504        # src/ops/decode_d_stage.py:17
+
+# ---------------------------------------------------------------------------
+# bfloat16 helpers (exact bit manipulation, round-to-nearest-even)
+# ---------------------------------------------------------------------------
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round float32 -> bfloat16 bits with round-to-nearest-even (NaN kept quiet)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
+    nan = np.isnan(x)
+    if nan.any():
+        rounded = np.where(nan, ((u >> 16) | 0x40).astype(np.uint32), rounded)
+    return rounded.astype(np.uint16)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest bfloat16 value (returned as float32)."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(x, dtype=np.float32)))
+
+
+def f64_to_f32_round_odd(x: np.ndarray) -> np.ndarray:
+    """float64 -> float32 with round-to-odd (sticky), so a following RNE to a
+    narrower format equals one correct rounding of the float64 value."""
+    x = np.asarray(x, dtype=np.float64)
+    f = x.astype(np.float32)
+    fd = f.astype(np.float64)
+    # step toward zero where RNE rounded away from zero
+    over = np.abs(fd) > np.abs(x)
+    f = np.where(over, np.nextafter(f, np.float32(0)), f)
+    inexact = f.astype(np.float64) != x
+    bits = f.view(np.uint32).copy()
+    bits[inexact] |= np.uint32(1)
+    return bits.view(np.float32)
+
+
+def bf16_round_f64(x: np.ndarray) -> np.ndarray:
+    """float64 -> nearest bfloat16 (single correct RNE rounding)."""
+    return bf16_round(f64_to_f32_round_odd(x))
+
+
+# ---------------------------------------------------------------------------
+# a1/a2: per-token symmetric quantisation, int4 packing
+# src/ops/decode_d_stage.py:50-77 (quantize_per_token), :80-101 (dequantize),
+# :104-111 (_pack_int4), :114-123 (_unpack_int4), :126-149 (int2)
+# ---------------------------------------------------------------------------
+
+
+def quantize_codes(x: np.ndarray, nbits: int) -> Tuple[np.ndarray, np.ndarray]:
+    """x [..., D] (bf16 values) -> (codes int8 [..., D], scale float16 [...]).
+
+    scale = fp16(max(amax, 1e-5) / q_max) computed in fp32, codes =
+    clamp(round_half_even(x / fp32(scale)), q_min, q_max)
+    (src/ops/decode_d_stage.py:61-68).
+    """
+    if nbits not in (2, 4, 8):
+        raise ValueError(f"nbits must be 2, 4, or 8, got {nbits}")
+    q_max = 2 ** (nbits - 1) - 1
+    q_min = -(2 ** (nbits - 1))
+    xf = np.asarray(x, dtype=np.float32)
+    amax = np.abs(xf).max(axis=-1)
+    amax = np.maximum(amax, np.float32(1e-5))
+    with np.errstate(over="ignore"):
+        scale = (amax / np.float32(q_max)).astype(np.float32).astype(np.float16)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.rint(xf / scale.astype(np.float32)[..., None])
+    codes = np.clip(r, q_min, q_max).astype(np.int8)
+    return codes, scale
+
+
+def pack_int4(codes: np.ndarray) -> np.ndarray:
+    """[..., D] int8 in [-8,7] -> [..., D/2] int8: even channel in the low
+    nibble, odd channel in the high nibble (src/ops/decode_d_stage.py:104-111)."""
+    u = codes.astype(np.int16) & 0x0F
+    return (u[..., 0::2] | (u[..., 1::2] << 4)).astype(np.uint8).view(np.int8)
+
+
+def unpack_int4(packed: np.ndarray) -> np.ndarray:
+    """Inverse of pack_int4 with sign extension (src/ops/decode_d_stage.py:114-123)."""
+    x = packed.view(np.uint8).astype(np.int32)
+    lo = ((x & 0x0F) ^ 8) - 8
+    hi = (((x >> 4) & 0x0F) ^ 8) - 8
+    out = np.empty(packed.shape[:-1] + (packed.shape[-1] * 2,), dtype=np.int8)
+    out[..., 0::2] = lo
+    out[..., 1::2] = hi
+    return out
+
+
+def pack_int2(codes: np.ndarray) -> np.ndarray:
+    """Channels 4i..4i+3 in bits [1:0],[3:2],[5:4],[7:6] (src/ops/decode_d_stage.py:126-133)."""
+    u = codes.astype(np.int16) & 0x03
+    return (u[..., 0::4] | (u[..., 1::4] << 2) | (u[..., 2::4] << 4) | (u[..., 3::4] << 6)).astype(np.uint8).view(np.int8)
+
+
+def unpack_int2(packed: np.ndarray) -> np.ndarray:
+    x = packed.view(np.uint8).astype(np.int32)
+    out = np.empty(packed.shape[:-1] + (packed.shape[-1] * 4,), dtype=np.int8)
+    for j in range(4):
+        out[..., j::4] = (((x >> (2 * j)) & 0x03) ^ 2) - 2
+    return out
+
+
+def quantize_per_token(x: np.ndarray, nbits: int) -> Tuple[np.ndarray, np.ndarray]:
+    """[BH, N, D] -> (packed int8 [BH, N, D*nbits/8], scale fp16 [BH, N])."""
+    codes, scale = quantize_codes(x, nbits)
+    if nbits == 8:
+        return codes, scale
+    if nbits == 4:
+        return pack_int4(codes), scale
+    return pack_int2(codes), scale
+
+
+def unpack_codes(packed: np.ndarray, nbits: int) -> np.ndarray:
+    if nbits == 8:
+        return packed.astype(np.int8)
+    if nbits == 4:
+        return unpack_int4(packed)
+    if nbits == 2:
+        return unpack_int2(packed)
+    raise ValueError(f"nbits must be 2, 4, or 8, got {nbits}")
+
+
+def dequantize_per_token(packed: np.ndarray, scale: np.ndarray, nbits: int) -> np.ndarray:
+    """fp16(code * scale) as the reference's eager path does
+    (src/ops/decode_d_stage.py:80-101); returned as float32 holding fp16 values."""
+    q = unpack_codes(packed, nbits).astype(np.float32)
+    return (q * scale.astype(np.float32)[..., None]).astype(np.float16).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# a4: vertical-line selector, src/patch/_common.py:144-190
+# ---------------------------------------------------------------------------
+
+
+def top_k_count(prefix_len: int, top_ratio: float) -> int:
+    """top_k = min(max(1, ceil(P * rho)), P) (src/patch/_common.py:187-188)."""
+    t = max(1, int(math.ceil(prefix_len * top_ratio)))
+    return min(t, prefix_len)
+
+
+def mean_bf16(x: np.ndarray, axis: int) -> np.ndarray:
+    """bf16 mean: exact float64 sum, one float64 division, one RNE rounding to
+    bf16.  Equals torch's fp32-accumulated bf16 mean except where the fp32 sum
+    is inexact right at a bf16 rounding boundary."""
+    n = x.shape[axis]
+    s = np.asarray(x, dtype=np.float64).sum(axis=axis)
+    return bf16_round_f64(s / np.float64(n))
+
+
+def dot_bf16_exact(qm: np.ndarray, k: np.ndarray) -> np.ndarray:
+    """scores[..., p] = bf16(sum_d qm[..., d] * k[..., p, d]) with the sum taken
+    sequentially in d order in float64 (products of bf16 values are exact in
+    float64; the running sum is exact unless the products span > 2^37 in
+    magnitude).  qm [..., D], k [..., P, D] -> [..., P]."""
+    qm64 = np.asarray(qm, dtype=np.float64)
+    k64 = np.asarray(k, dtype=np.float64)
+    acc = np.zeros(k64.shape[:-1], dtype=np.float64)
+    for d in range(k64.shape[-1]):
+        acc = acc + qm64[..., d, None] * k64[..., d]
+    return bf16_round_f64(acc)
+
+
+def orderable_bf16_key(scores_bf16: np.ndarray) -> np.ndarray:
+    """Monotone uint16 key of a bf16 value; -0 and +0 get the same key (torch
+    compares them equal)."""
+    b = f32_to_bf16_bits(scores_bf16).astype(np.uint32)
+    b = np.where(b == 0x8000, 0, b)
+    neg = (b & 0x8000) != 0
+    return np.where(neg, (~b) & 0xFFFF, b | 0x8000).astype(np.uint32)
+
+
+def topk_desc_index_asc(scores_bf16: np.ndarray, k: int) -> np.ndarray:
+    """Top-k along the last axis ordered by score descending, ties broken by
+    lower index first (the deterministic rule this build adopts for
+    torch.topk(sorted=True), src/patch/_common.py:189)."""
+    key = orderable_bf16_key(scores_bf16).astype(np.int64)
+    P = scores_bf16.shape[-1]
+    idx = np.broadcast_to(np.arange(P, dtype=np.int64), key.shape)
+    combo = key * (1 << 32) + (0xFFFFFFFF - idx)
+    order = np.argsort(-combo, axis=-1, kind="stable")[..., :k]
+    return order.astype(np.int64)
+
+
+def compute_vertical_indices(query_states: np.ndarray, key_states: np.ndarray,
+                             window_size: int, top_ratio: float,
+                             kv_repeat: int = 1) -> np.ndarray:
+    """src/patch/_common.py:144-190.
+
+    query_states [B, H_Q, Q, D] (bf16 values), key_states [B, H, K, D] with
+    H == H_Q or H == H_Q / kv_repeat.  Returns int64 [B, H_Q, top_k].
+    """
+    B, HQ, QL, D = query_states.shape
+    KL = key_states.shape[2]
+    P = max(0, KL - window_size)
+    if P == 0:
+        return np.zeros((B, HQ, 0), dtype=np.int64)
+    tail = min(window_size, QL)
+    qm = mean_bf16(query_states[:, :, QL - tail:, :], axis=2)          # [B, HQ, D]
+    HK = key_states.shape[1]
+    if kv_repeat <= 1 or HK == HQ:
+        kp = key_states[:, :, :P, :]
+        scores = dot_bf16_exact(qm, kp)                                   # [B, HQ, P]
+    else:
+        assert HQ == HK * kv_repeat
+        kp = np.repeat(key_states[:, :, :P, :], kv_repeat, axis=1)        # head h -> h // R
+        scores = dot_bf16_exact(qm, kp)
+    k = top_k_count(P, top_ratio)
+    return topk_desc_index_asc(scores, k)
+
+
+def vertical_scores(query_states, key_states, window_size, kv_repeat=1):
+    """The bf16 score matrix the selector ranks (for tests)."""
+    B, HQ, QL, D = query_states.shape
+    KL = key_states.shape[2]
+    P = max(0, KL - window_size)
+    tail = min(window_size, QL)
+    qm = mean_bf16(query_states[:, :, QL - tail:, :], axis=2)
+    HK = key_states.shape[1]
+    kp = key_states[:, :, :P, :]
+    if HK != HQ:
+        kp = np.repeat(kp, HQ // HK, axis=1)
+    return dot_bf16_exact(qm, kp)
+
+
+# ---------------------------------------------------------------------------
+# a5/a3: cache reorganisation (freeze) and staging ring
+# src/ops/d_stage_kv_cache.py:82-100 (prefill), :106-189 (freeze),
+# :195-217 (append_staging / flush)
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class DecodeState:
+    """The four decode segments at KV-head granularity (BH = B * H_KV)."""
+    k_packed: np.ndarray           # int8 [BH, Nq, D/2]
+    v_packed: np.ndarray
+    k_scale: np.ndarray            # fp16 [BH, Nq]
+    v_scale: np.ndarray
+    k_topk: np.ndarray             # bf16 values [BH, T, D]
+    v_topk: np.ndarray
+    k_window: np.ndarray           # [BH, W, D]
+    v_window: np.ndarray
+    k_ring: np.ndarray             # [BH, 128, D]
+    v_ring: np.ndarray
+    ring_ptr: int = 0
+    k_bits: int = 4
+    v_bits: int = 4
+    topk_idx: Optional[np.ndarray] = None      # [B, H_KV, T] positions in the prefix
+    compact_idx: Optional[np.ndarray] = None   # [B, H_KV, Nq_initial]
+
+    @property
+    def k_staging(self):
+        return self.k_ring[:, :self.ring_ptr]
+
+    @property
+    def v_staging(self):
+        return self.v_ring[:, :self.ring_ptr]
+
+
+def group_mean_query(query_tail: np.ndarray, h_kv: int) -> np.ndarray:
+    """[B, H_Q, W, D] -> bf16 mean over each KV group (src/ops/d_stage_kv_cache.py:131-133)."""
+    B, HQ, W, D = query_tail.shape
+    R = HQ // h_kv
+    return mean_bf16(query_tail.reshape(B, h_kv, R, W, D), axis=2)
+
+
+def freeze(keys: np.ndarray, values: np.ndarray, query_tail: Optional[np.ndarray],
+           window_size: int, top_ratio: float, kv_repeat: int,
+           k_bits: int = 4, v_bits: int = 4, use_vert: bool = True) -> DecodeState:
+    """Prefill -> decode reorganisation (src/ops/d_stage_kv_cache.py:106-189).
+
+    keys/values [B, H_KV, N, D]; query_tail [B, H_Q, W', D] (the last
+    min(window_size, Q) prefill queries, :97-100).
+    """
+    B, HKV, N, D = keys.shape
+    BH = B * HKV
+    W = min(window_size, N)
+    P = N - W
+    k_window = keys[:, :, N - W:, :].reshape(BH, W, D).copy()
+    v_window = values[:, :, N - W:, :].reshape(BH, W, D).copy()
+    topk_idx = np.zeros((B, HKV, 0), dtype=np.int64)
+    if P > 0:
+        kp = keys[:, :, :P, :]
+        vp = values[:, :, :P, :]
+        if use_vert and query_tail is not None and kv_repeat >= 1:
+            q_kv = group_mean_query(query_tail, HKV)                       # [B, HKV, W', D]
+            # the selector again subtracts window_size from the already
+            # window-free prefix (F3: vertical lines come from [0, N - 2W))
+            topk_idx = compute_vertical_indices(q_kv, kp, window_size, top_ratio)
+        T = topk_idx.shape[-1]
+        sel = np.zeros((B, HKV, P), dtype=bool)
+        bi, hi = np.meshgrid(np.arange(B), np.arange(HKV), indexing="ij")
+        for t in range(T):
+            sel[bi, hi, topk_idx[:, :, t]] = True
+        compact = np.stack([np.stack([np.nonzero(~sel[b, h])[0] for h in range(HKV)]) for b in range(B)])
+        k_topk = np.take_along_axis(kp, topk_idx[..., None], axis=2).reshape(BH, T, D)
+        v_topk = np.take_along_axis(vp, topk_idx[..., None], axis=2).reshape(BH, T, D)
+        kc = np.take_along_axis(kp, compact[..., None], axis=2).reshape(BH, P - T, D)
+        vc = np.take_along_axis(vp, compact[..., None], axis=2).reshape(BH, P - T, D)
+        k_packed, k_scale = quantize_per_token(kc, k_bits)
+        v_packed, v_scale = quantize_per_token(vc, v_bits)
+    else:
+        compact = np.zeros((B, HKV, 0), dtype=np.int64)
+        k_topk = np.zeros((BH, 0, D), np.float32)
+        v_topk = np.zeros((BH, 0, D), np.float32)
+        k_packed = np.zeros((BH, 0, D * k_bits // 8), np.int8)
+        v_packed = np.zeros((BH, 0, D * v_bits // 8), np.int8)
+        k_scale = np.zeros((BH, 0), np.float16)
+        v_scale = np.zeros((BH, 0), np.float16)
+    return DecodeState(k_packed, v_packed, k_scale, v_scale, k_topk, v_topk,
+                       k_window, v_window,
+                       np.zeros((BH, GROUP_SIZE, D), np.float32),
+                       np.zeros((BH, GROUP_SIZE, D), np.float32),
+                       0, k_bits, v_bits, topk_idx, compact)
+
+
+def append_staging(st: DecodeState, k_new: np.ndarray, v_new: np.ndarray) -> None:
+    """k_new/v_new [B, H_KV, S, D]: write into the ring, flushing (quantise +
+    append to the prefix) whenever 128 slots fill (src/ops/d_stage_kv_cache.py:195-217)."""
+    B, HKV, S, D = k_new.shape
+    k = k_new.reshape(B * HKV, S, D)
+    v = v_new.reshape(B * HKV, S, D)
+    for i in range(S):
+        st.k_ring[:, st.ring_ptr] = k[:, i]
+        st.v_ring[:, st.ring_ptr] = v[:, i]
+        st.ring_ptr += 1
+        if st.ring_ptr >= GROUP_SIZE:
+            flush_staging(st)
+
+
+def flush_staging(st: DecodeState) -> None:
+    kp, ks = quantize_per_token(st.k_ring, st.k_bits)
+    vp, vs = quantize_per_token(st.v_ring, st.v_bits)
+    st.k_packed = np.concatenate([st.k_packed, kp], axis=1)
+    st.v_packed = np.concatenate([st.v_packed, vp], axis=1)
+    st.k_scale = np.concatenate([st.k_scale, ks], axis=1)
+    st.v_scale = np.concatenate([st.v_scale, vs], axis=1)
+    st.ring_ptr = 0
+
+
+# ---------------------------------------------------------------------------
+# a6-a11: four-segment decode attention
+# ---------------------------------------------------------------------------
+
+
+def decode_fp64(q: np.ndarray, k_packed, v_packed, k_scale, v_scale,
+                k_topk, v_topk, k_staging, v_staging, k_window, v_window,
+                k_bits: int = 4, v_bits: int = 4, kv_repeat: int = 1,
+                sm_scale: Optional[float] = None) -> np.ndarray:
+    """Exact (float64) restatement of fused_d_stage_decode
+    (src/ops/decode_d_stage.py:916-1005, kernel math :599-691 and :221-267):
+    softmax over [deq(prefix) | topk | staging | window] of q . k * sm_scale,
+    with the int4 prefix dequantised as code * scale (the kernel factors the
+    per-token scales out of the dot products, F8), GQA head h -> KV head h // R.
+
+    q [BH_Q, D] -> out float64 [BH_Q, D].
+    """
+    BHQ, D = q.shape
+    BHK = BHQ // kv_repeat
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    kq = unpack_codes(k_packed, k_bits).astype(np.float64) * k_scale.astype(np.float64)[..., None]
+    vq = unpack_codes(v_packed, v_bits).astype(np.float64) * v_scale.astype(np.float64)[..., None]
+    K = np.concatenate([kq, k_topk, k_staging, k_window], axis=1).astype(np.float64)
+    V = np.concatenate([vq, v_topk, v_staging, v_window], axis=1).astype(np.float64)
+    K = np.repeat(K, kv_repeat, axis=0)
+    V = np.repeat(V, kv_repeat, axis=0)
+    s = np.einsum("hd,hnd->hn", q.astype(np.float64), K) * sm_scale
+    s -= s.max(axis=1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=1, keepdims=True)
+    return np.einsum("hn,hnd->hd", p, V)
+
+
+def decode_fp64_state(q: np.ndarray, st: DecodeState, kv_repeat: int, sm_scale=None) -> np.ndarray:
+    return decode_fp64(q, st.k_packed, st.v_packed, st.k_scale, st.v_scale,
+                       st.k_topk, st.v_topk, st.k_staging, st.v_staging,
+                       st.k_window, st.v_window, st.k_bits, st.v_bits, kv_repeat, sm_scale)
+
+
+def decode_bf16_eager(q, st: DecodeState, kv_repeat: int, B: int):
+    """The reference's PyTorch eager decode (src/ops/d_stage_kv_cache.py:309-354):
+    dequantise to fp16 then bf16, concatenate [prefix, topk, staging, window],
+    expand GQA, then bf16 matmul -> bf16 softmax -> bf16 matmul.  Runs on the
+    CPU with torch.  q [BH_Q, D] (bf16 values) -> float32 [BH_Q, D]."""
+    import torch
+    return decode_bf16_eager_torch(torch.from_numpy(np.asarray(q, np.float32)),
+                                   prepare_eager_state(st), kv_repeat, B).float().numpy()
+
+
+def prepare_eager_state(st: DecodeState):
+    """Torch CPU tensors for decode_bf16_eager_torch (kept separate so that a
+    timing loop measures only the per-step decode work)."""
+    import torch
+    bf = torch.bfloat16
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    return dict(
+        k_packed=t(st.k_packed), v_packed=t(st.v_packed),
+        k_scale=t(st.k_scale), v_scale=t(st.v_scale),
+        k_topk=t(st.k_topk.astype(np.float32)).to(bf), v_topk=t(st.v_topk.astype(np.float32)).to(bf),
+        k_staging=t(st.k_staging.astype(np.float32)).to(bf), v_staging=t(st.v_staging.astype(np.float32)).to(bf),
+        k_window=t(st.k_window.astype(np.float32)).to(bf), v_window=t(st.v_window.astype(np.float32)).to(bf),
+        k_bits=st.k_bits, v_bits=st.v_bits)
+
+
+def _torch_dequant(packed, scale, bits):
+    import torch
+    if bits == 4:
+        x = packed.to(torch.int32) & 0xFF
+        lo = ((x & 0x0F) << 28) >> 28
+        hi = (((x >> 4) & 0x0F) << 28) >> 28
+        q = torch.stack([lo, hi], dim=-1).reshape(*packed.shape[:-1], packed.shape[-1] * 2).float()
+    elif bits == 8:
+        q = packed.float()
+    else:
+        x = packed.to(torch.int32) & 0xFF
+        parts = [(((x >> (2 * j)) & 0x03) << 30) >> 30 for j in range(4)]
+        q = torch.stack(parts, dim=-1).reshape(*packed.shape[:-1], packed.shape[-1] * 4).float()
+    return (q * scale.float().unsqueeze(-1)).to(torch.float16)
+
+
+def decode_bf16_eager_torch(q, es: dict, kv_repeat: int, B: int):
+    """Per-step body of decode_bf16_eager on torch CPU tensors."""
+    import torch
+    bf = torch.bfloat16
+    BHQ, D = q.shape
+    HQ = BHQ // B
+    HKV = HQ // kv_repeat
+    kp = _torch_dequant(es["k_packed"], es["k_scale"], es["k_bits"]).to(bf)
+    vp = _torch_dequant(es["v_packed"], es["v_scale"], es["v_bits"]).to(bf)
+    K = torch.cat([kp, es["k_topk"], es["k_staging"], es["k_window"]], dim=1)
+    V = torch.cat([vp, es["v_topk"], es["v_staging"], es["v_window"]], dim=1)
+    NT = K.shape[1]
+    K = K.reshape(B, HKV, NT, D).unsqueeze(2).expand(B, HKV, kv_repeat, NT, D).reshape(B, HQ, NT, D)
+    V = V.reshape(B, HKV, NT, D).unsqueeze(2).expand(B, HKV, kv_repeat, NT, D).reshape(B, HQ, NT, D)
+    qq = q.to(bf).reshape(B, HQ, 1, D)
+    scores = (qq @ K.transpose(-1, -2)) * (D ** -0.5)
+    out = torch.softmax(scores, dim=-1) @ V
+    return out.reshape(BHQ, D)
+
+
+# ---------------------------------------------------------------------------
+# Seeded synthetic inputs (the benchmark's data distribution)
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class DecodeInputs:
+    B: int
+    HQ: int
+    HKV: int
+    N: int
+    D: int
+    W: int
+    S: int
+    rho: float
+    keys: np.ndarray          # [B, HKV, N, D] prefill keys (bf16 values)
+    values: np.ndarray
+    query_tail: np.ndarray    # [B, HQ, W, D] last W prefill queries
+    k_new: np.ndarray         # [B, HKV, S, D] decode-time tokens (staging)
+    v_new: np.ndarray
+    q_dec: np.ndarray         # [B*HQ, D] the decode query
+    planted: np.ndarray       # [B, HKV, n_plant] planted vertical-line positions
+
+
+def make_decode_inputs(B=1, HQ=32, HKV=8, N=1024, D=128, W=128, S=37, rho=0.05,
+                       seed=0, plant_ratio=0.05) -> DecodeInputs:
+    """Seeded Gaussian inputs with outlier channels and planted vertical lines.
+
+    torch.Generator().manual_seed(seed) on the CPU draws, in order:
+      query tail [B, HQ, W, D], keys [B, HKV, N, D], values [B, HKV, N, D],
+      per-(KV head, channel) key offsets ~ N(0, 2) (std sqrt(2)),
+      per (b, KV head) the planted positions (randperm of the non-window
+      prefix, first int(plant_ratio * N)), staging keys/values [B, HKV, S, D],
+      and the decode query [B*HQ, D].
+    Keys get their head's offset on every token.  A planted position's key is
+    offset + 3 * sqrt(D) * u, u the unit mean direction of the KV group's
+    query tail.  Everything is rounded to bf16.
+    """
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    G = HQ // HKV
+    qt = torch.randn(B, HQ, W, D, generator=g)
+    k = torch.randn(B, HKV, N, D, generator=g)
+    v = torch.randn(B, HKV, N, D, generator=g)
+    off = torch.randn(HKV, D, generator=g) * math.sqrt(2.0)
+    k = k + off[None, :, None, :]
+    qt_b = qt.to(torch.bfloat16).float()
+    n_plant = int(plant_ratio * N)
+    planted = np.zeros((B, HKV, n_plant), dtype=np.int64)
+    for b in range(B):
+        for h in range(HKV):
+            u = qt_b[b, h * G:(h + 1) * G].reshape(-1, D).mean(dim=0)
+            u = u / u.norm()
+            pos = torch.randperm(N - W, generator=g)[:n_plant]
+            k[b, h, pos, :] = off[h] + 3.0 * math.sqrt(D) * u
+            planted[b, h] = np.sort(pos.numpy())
+    k_new = torch.randn(B, HKV, S, D, generator=g) + off[None, :, None, :]
+    v_new = torch.randn(B, HKV, S, D, generator=g)
+    q_dec = torch.randn(B * HQ, D, generator=g)
+    cv = lambda t: t.to(torch.bfloat16).float().numpy()
+    return DecodeInputs(B, HQ, HKV, N, D, W, S, rho, cv(k), cv(v), cv(qt),
+                        cv(k_new), cv(v_new), cv(q_dec), planted)
+
+
+def build_decode_state(inp: DecodeInputs) -> DecodeState:
+    """freeze() the prefill cache, then append the S staging tokens."""
+    st = freeze(inp.keys, inp.values, inp.query_tail, inp.W, inp.rho, inp.HQ // inp.HKV)
+    append_staging(st, inp.k_new, inp.v_new)
+    return st

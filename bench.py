@@ -1,0 +1,242 @@
+"""Benchmark of the fused hybrid decode attention on one MI355X.
+
+Headline workload: one decode step of one attention
+layer, B=1, 32 query / 8 KV heads, head_dim 128, prefix 8192 tokens frozen into
+the four segments (int4 K4V4 prefix of 7667 tokens, 397 bf16 vertical lines,
+64 bf16 staging tokens, 128 bf16 window tokens).  A "step" is one
+fused_d_stage_decode call over that cache.
+
+Timing: inputs are resident in HBM; R copies of the cache (R chosen so the
+copies exceed 1 GiB, i.e. four times the 256 MiB Infinity Cache) are used in
+rotation so every step streams its bytes from HBM.  W untimed steps, then K
+steps between two HIP events on the stream the kernels run on.
+
+Output: one JSON line (rank 0), with the roofline of the decode kernel, the
+CPU baseline (the reference's bf16 eager decode math run by torch on the host
+CPU on config 1), and the prefix sweep of BASELINE config 2 beside a bf16
+full-KV split-K decode of the same shape.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "hybrid decode-attn µs/step + HBM GB/s (% peak), 32q/8kv d128, 1K–32K prefix"
+HBM_PEAK_GBS = 8000.0
+D = 128
+
+
+def top_k_count(prefix_len: int, rho: float) -> int:
+    t = max(1, int(math.ceil(prefix_len * rho)))
+    return min(t, prefix_len)
+
+
+def seg_sizes(N: int, W: int = 128, S: int = 64, rho: float = 0.05):
+    """Decode-time segment sizes after freeze (T from [0, N-2W))."""
+    T = top_k_count(max(0, N - 2 * W), rho) if N - 2 * W > 0 else 0
+    Nq = N - W - T
+    return Nq, T, S, W
+
+
+def algorithmic_bytes(B, HQ, HKV, N, W=128, S=64, rho=0.05):
+    Nq, T, S, W = seg_sizes(N, W, S, rho)
+    return B * HKV * (Nq * (64 + 64 + 2 + 2) + (T + S + W) * 2 * D * 2) + B * HQ * D * 2 * 2
+
+
+def bf16_bytes(B, HQ, HKV, N, S=64):
+    return B * HKV * (N + S) * 2 * D * 2 + B * HQ * D * 2 * 2
+
+
+def make_state(B, HQ, HKV, N, dev, seed, W=128, S=64, rho=0.05):
+    """Synthetic decode cache on the GPU: Gaussian K (per-channel N(0,2)
+    offsets) and V, quantised by the library's own quantiser."""
+    import hyquant_amd as hq
+    Nq, T, S, W = seg_sizes(N, W, S, rho)
+    BH = B * HKV
+    g = torch.Generator(device=dev).manual_seed(seed)
+    off = torch.randn(HKV, D, generator=g, device=dev) * math.sqrt(2.0)
+    off_bh = off.repeat(B, 1)[:, None, :]
+    bf = torch.bfloat16
+
+    def kv(n, is_k):
+        x = torch.randn(BH, n, D, generator=g, device=dev)
+        if is_k:
+            x += off_bh
+        return x.to(bf)
+
+    kp, ks = hq.quantize_per_token(kv(Nq, True), 4)
+    vp, vs = hq.quantize_per_token(kv(Nq, False), 4)
+    st = dict(k_packed=kp, v_packed=vp, k_scale=ks, v_scale=vs,
+              k_topk=kv(T, True), v_topk=kv(T, False),
+              k_staging=kv(S, True), v_staging=kv(S, False),
+              k_window=kv(W, True), v_window=kv(W, False))
+    q = torch.randn(B * HQ, D, generator=g, device=dev).to(bf)
+    return q, st
+
+
+def run_decode(q, st, G):
+    import hyquant_amd as hq
+    return hq.fused_d_stage_decode(q, st["k_packed"], st["v_packed"], st["k_scale"], st["v_scale"],
+                                   st["k_topk"], st["v_topk"], st["k_staging"], st["v_staging"],
+                                   st["k_window"], st["v_window"], 4, 4, kv_repeat=G)
+
+
+def time_rotating(fn, states, warmup, steps):
+    """Average ms per call over `steps` calls cycling through `states`."""
+    n = len(states)
+    for i in range(warmup):
+        fn(states[i % n])
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        fn(states[i % n])
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def copies_for(nbytes, cap=512):
+    return int(max(1, min(cap, math.ceil((1 << 30) / max(nbytes, 1)))))
+
+
+def bench_hybrid(B, HQ, HKV, N, dev, warmup, steps, seed=0):
+    nbytes = algorithmic_bytes(B, HQ, HKV, N)
+    R = copies_for(nbytes)
+    states = [make_state(B, HQ, HKV, N, dev, seed + r) for r in range(R)]
+    G = HQ // HKV
+    ms = time_rotating(lambda s: run_decode(s[0], s[1], G), states, warmup, steps)
+    del states
+    return ms, nbytes, R
+
+
+def bench_bf16(B, HQ, HKV, N, dev, warmup, steps, seed=0):
+    import hyquant_amd as hq
+    nbytes = bf16_bytes(B, HQ, HKV, N)
+    R = copies_for(nbytes, cap=64)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    mk = lambda: torch.randn(B * HKV, N + 64, D, generator=g, device=dev).to(torch.bfloat16)
+    states = [(torch.randn(B * HQ, D, generator=g, device=dev).to(torch.bfloat16), mk(), mk()) for _ in range(R)]
+    G = HQ // HKV
+    ms = time_rotating(lambda s: hq.decode_bf16_full(s[0], s[1], s[2], kv_repeat=G), states, warmup, steps)
+    del states
+    return ms, nbytes, R
+
+
+def cpu_baseline(N=8192, min_steps=20, budget_s=20.0):
+    """The reference's eager decode math (bf16 dequant + SDPA on torch CPU,
+    src/ops/d_stage_kv_cache.py:309-354) on config 1, timed on the host CPU."""
+    from oracle import hyq_oracle as O
+    cores = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(cores)
+    inp = O.make_decode_inputs(B=1, HQ=32, HKV=8, N=N, W=128, S=64, seed=0)
+    st = O.build_decode_state(inp)
+    es = O.prepare_eager_state(st)
+    q = torch.from_numpy(inp.q_dec)
+    O.decode_bf16_eager_torch(q, es, 4, 1)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_steps or (time.perf_counter() - t_start < 2.0 and len(times) < 200):
+        t0 = time.perf_counter()
+        O.decode_bf16_eager_torch(q, es, 4, 1)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(med * 1e6, 1), "unit": "us/step", "cores": cores, "kind": "port",
+            "sample": f"config 1 (B=1, 32q/8kv, prefix 8192), median of {len(times)} steps of the "
+                      f"bf16 eager dequant+SDPA decode on torch CPU; host CPU: {model}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-bf16", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(--gpus must be 1)", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    import hyquant_amd  # noqa: F401  (fails loudly if libhyq.so is missing)
+
+    B, HQ, HKV, N = 1, 32, 8, 8192
+    ms, nbytes, R = bench_hybrid(B, HQ, HKV, N, dev, args.warmup, args.steps)
+    us = ms * 1e3
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    Nq, T, S, W = seg_sizes(N)
+    res = {
+        "metric": METRIC,
+        "value": round(us, 3),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded Gaussian K/V with N(0,2) per-channel K offsets, int4 K4V4 prefix "
+                "quantised on the GPU by hyq_quant_pack)",
+        "config": {"workload": "config1: fused hybrid decode, B=1, 32q/8kv, d128, prefix 8192",
+                   "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "prefix": N,
+                   "n_quant": Nq, "n_topk": T, "n_staging": S, "n_window": W,
+                   "cache_copies_rotated": R},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode_kernel", "algorithmic_bytes_per_launch": nbytes},
+    }
+    if not args.no_bf16:
+        ms16, b16, _ = bench_bf16(B, HQ, HKV, N, dev, args.warmup, args.steps)
+        res["bf16_comparator"] = {"us_per_step": round(ms16 * 1e3, 3),
+                                  "gbs": round(b16 / (ms16 * 1e-3) / 1e9, 1),
+                                  "speedup_hybrid_vs_bf16": round(ms16 / ms, 3)}
+    if not args.no_sweep:
+        sweep = []
+        for b in (1, 16):
+            for n in (1024, 2048, 4096, 8192, 16384, 32768):
+                m, nb, _ = bench_hybrid(b, HQ, HKV, n, dev, 10, 100)
+                row = {"batch": b, "prefix": n, "us_per_step": round(m * 1e3, 3),
+                       "gbs": round(nb / (m * 1e-3) / 1e9, 1),
+                       "frac_peak": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                if not args.no_bf16:
+                    m16, nb16, _ = bench_bf16(b, HQ, HKV, n, dev, 5, 50)
+                    row["bf16_us_per_step"] = round(m16 * 1e3, 3)
+                    row["speedup_vs_bf16"] = round(m16 / m, 3)
+                sweep.append(row)
+                print(f"# sweep {row}", file=sys.stderr, flush=True)
+        res["sweep"] = sweep
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

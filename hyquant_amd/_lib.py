@@ -1,0 +1,103 @@
+"""ctypes binding of libhyq.so (the C ABI declared in include/hyq.h).
+
+The library is loaded from this package directory.  If it is missing the
+import fails loudly: there is no CPU or eager fallback on the product path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from ctypes import POINTER, Structure, c_float, c_int, c_int32, c_int64, c_size_t, c_uint16, c_void_p, c_int8, c_char_p
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libhyq.so")
+
+HYQ_OK = 0
+HYQ_EINVAL = -22
+HYQ_ENOTSUP = -95
+HYQ_EDEVICE = -5
+HYQ_ENOSPC = -28
+
+# every symbol declared in include/hyq.h
+EXPORTS = (
+    "hyq_last_error",
+    "hyq_abi_version",
+    "hyq_quant_pack",
+    "hyq_decode_workspace_size",
+    "hyq_decode_hybrid",
+    "hyq_decode_bf16_workspace_size",
+    "hyq_decode_bf16",
+)
+
+
+class DecodeParams(Structure):
+    """Mirror of `hyq_decode_params` (include/hyq.h)."""
+    _fields_ = [
+        ("q", c_void_p), ("q_stride", c_int64),
+        ("out", c_void_p), ("out_stride", c_int64),
+        ("k_packed", c_void_p), ("kp_stride_bh", c_int64), ("kp_stride_n", c_int64),
+        ("v_packed", c_void_p), ("vp_stride_bh", c_int64), ("vp_stride_n", c_int64),
+        ("k_scale", c_void_p), ("ks_stride_bh", c_int64),
+        ("v_scale", c_void_p), ("vs_stride_bh", c_int64),
+        ("n_quant", c_int64),
+        ("seg_k", c_void_p * 3), ("seg_k_stride_bh", c_int64 * 3), ("seg_k_stride_n", c_int64 * 3),
+        ("seg_v", c_void_p * 3), ("seg_v_stride_bh", c_int64 * 3), ("seg_v_stride_n", c_int64 * 3),
+        ("seg_n", c_int64 * 3),
+        ("bh_kv", c_int32), ("kv_repeat", c_int32), ("head_dim", c_int32),
+        ("k_bits", c_int32), ("v_bits", c_int32),
+        ("sm_scale", c_float),
+        ("split_tokens", c_int32),
+    ]
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def _declare(lib):
+    lib.hyq_last_error.restype = c_char_p
+    lib.hyq_last_error.argtypes = []
+    lib.hyq_abi_version.restype = c_int
+    lib.hyq_abi_version.argtypes = []
+    lib.hyq_quant_pack.restype = c_int
+    lib.hyq_quant_pack.argtypes = [c_void_p, c_int64, c_int64, c_int32, c_int64, c_int64, c_int32,
+                                   c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p]
+    lib.hyq_decode_workspace_size.restype = c_size_t
+    lib.hyq_decode_workspace_size.argtypes = [POINTER(DecodeParams)]
+    lib.hyq_decode_hybrid.restype = c_int
+    lib.hyq_decode_hybrid.argtypes = [POINTER(DecodeParams), c_void_p, c_size_t, c_void_p]
+    lib.hyq_decode_bf16_workspace_size.restype = c_size_t
+    lib.hyq_decode_bf16_workspace_size.argtypes = [c_int32, c_int32, c_int64, c_int32]
+    lib.hyq_decode_bf16.restype = c_int
+    lib.hyq_decode_bf16.argtypes = [c_void_p, c_int64, c_void_p, c_int64,
+                                    c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64,
+                                    c_int64, c_int32, c_int32, c_int32, c_float,
+                                    c_void_p, c_size_t, c_void_p]
+
+
+def lib():
+    """The loaded libhyq.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise RuntimeError(
+                        f"{LIB_PATH} is missing: build it with `python -m hyquant_amd.build` "
+                        "(there is no fallback implementation)")
+                l = ctypes.CDLL(LIB_PATH)
+                _declare(l)
+                _lib = l
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    """Map a libhyq status to the reference's exception types."""
+    if status == HYQ_OK:
+        return
+    msg = lib().hyq_last_error().decode(errors="replace")
+    if status in (HYQ_EINVAL, HYQ_ENOTSUP):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what} failed ({status}): {msg}")

@@ -1,0 +1,121 @@
+// Per-token symmetric quantisation and nibble/crumb packing (the staging flush
+// and the freeze quantiser).  Semantics follow quantize_per_token,
+// src/ops/decode_d_stage.py:50-77, and _pack_int4/_pack_int2 (:104-133):
+//   scale = fp16(fp32(max(amax, 1e-5)) / qmax)        (IEEE fp32 divide, RNE)
+//   code  = clamp(rint_half_even(x / fp32(scale)), qmin, qmax)
+// Layout: a group of d/8 lanes owns one token row; each lane loads 8 bf16
+// channels with one 128-bit load and writes its packed bytes, so a wavefront
+// reads 64*16 contiguous bytes per instruction.  HBM-bound.
+#include "hyq_common.h"
+
+#include <cstdio>
+#include <string>
+
+namespace hyq {
+namespace {
+
+template <int NBITS>
+__global__ __launch_bounds__(256) void quant_pack_kernel(
+    const uint16_t* __restrict__ x, int64_t n, int64_t total, int lpt_log2,
+    int64_t xs_bh, int64_t xs_n, int8_t* __restrict__ packed, int64_t ps_bh, int64_t ps_n,
+    uint16_t* __restrict__ scale, int64_t ss_bh) {
+    constexpr int QMAX = (1 << (NBITS - 1)) - 1;
+    constexpr int QMIN = -(1 << (NBITS - 1));
+    const int lpt = 1 << lpt_log2;                 // lanes per token
+    const int lane = threadIdx.x & 63;
+    const int sub = lane & (lpt - 1);              // lane within its token group
+    const int64_t tokens_per_block = (256 >> lpt_log2);
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * tokens_per_block + (threadIdx.x >> lpt_log2);
+    const bool valid = t < total;
+    const int64_t tt = valid ? t : total - 1;
+    const int64_t ib = tt / n;
+    const int64_t in = tt - ib * n;
+
+    const uint4 raw = *reinterpret_cast<const uint4*>(x + ib * xs_bh + in * xs_n + sub * 8);
+    float v[8];
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    for (int m = 1; m < lpt; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    amax = fmaxf(amax, 1e-5f);
+    const float s32 = amax / static_cast<float>(QMAX);
+    const _Float16 s16 = static_cast<_Float16>(s32);
+    const float sf = static_cast<float>(s16);
+    int c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float r = rintf(v[i] / sf);
+        r = fminf(fmaxf(r, static_cast<float>(QMIN)), static_cast<float>(QMAX));
+        c[i] = static_cast<int>(r);
+    }
+    if (!valid) return;
+    int8_t* prow = packed + ib * ps_bh + in * ps_n;
+    if (NBITS == 4) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) word |= static_cast<uint32_t>(c[i] & 15) << (4 * i);
+        reinterpret_cast<uint32_t*>(prow)[sub] = word;
+    } else if (NBITS == 8) {
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo |= static_cast<uint32_t>(c[i] & 255) << (8 * i);
+            hi |= static_cast<uint32_t>(c[i + 4] & 255) << (8 * i);
+        }
+        reinterpret_cast<uint2*>(prow)[sub] = make_uint2(lo, hi);
+    } else {
+        uint32_t half = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) half |= static_cast<uint32_t>(c[i] & 3) << (2 * i);
+        reinterpret_cast<uint16_t*>(prow)[sub] = static_cast<uint16_t>(half);
+    }
+    if (sub == 0) scale[ib * ss_bh + in] = __builtin_bit_cast(uint16_t, s16);
+}
+
+}  // namespace
+}  // namespace hyq
+
+using namespace hyq;
+
+extern "C" int hyq_quant_pack(const uint16_t* x, int64_t bh, int64_t n, int32_t d,
+                              int64_t x_stride_bh, int64_t x_stride_n, int32_t nbits,
+                              int8_t* packed, int64_t p_stride_bh, int64_t p_stride_n,
+                              uint16_t* scale, int64_t s_stride_bh, void* stream) {
+    if (bh < 0 || n < 0) return fail(HYQ_EINVAL, "hyq_quant_pack: negative shape");
+    if (nbits != 2 && nbits != 4 && nbits != 8)
+        return fail(HYQ_EINVAL, "nbits must be 2, 4, or 8, got " + std::to_string(nbits));
+    if (d <= 0 || d % 8 != 0 || d > 512 || ((d / 8) & (d / 8 - 1)) != 0)
+        return fail(HYQ_ENOTSUP, "hyq_quant_pack: head dim must be 8*2^k <= 512, got " + std::to_string(d));
+    if (bh == 0 || n == 0) return HYQ_OK;
+    if (!x || !packed || !scale) return fail(HYQ_EINVAL, "hyq_quant_pack: null pointer");
+    if (!aligned(x, 16) || x_stride_n % 8 || x_stride_bh % 8)
+        return fail(HYQ_EINVAL, "hyq_quant_pack: x must be 16-byte aligned with strides divisible by 8");
+    const int pbytes = nbits;  // packed bytes per lane (8 channels)
+    if (!aligned(packed, pbytes) || p_stride_n % pbytes || p_stride_bh % pbytes)
+        return fail(HYQ_EINVAL, "hyq_quant_pack: packed output misaligned");
+    if (!aligned(scale, 2)) return fail(HYQ_EINVAL, "hyq_quant_pack: scale misaligned");
+    int lpt_log2 = 0;
+    while ((1 << lpt_log2) < d / 8) ++lpt_log2;
+    const int64_t total = bh * n;
+    const int64_t tpb = 256 >> lpt_log2;
+    const int64_t blocks = (total + tpb - 1) / tpb;
+    if (blocks > 0x7fffffffLL) return fail(HYQ_ENOTSUP, "hyq_quant_pack: too many tokens");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    dim3 grid(static_cast<unsigned>(blocks)), block(256);
+    if (nbits == 4)
+        quant_pack_kernel<4><<<grid, block, 0, s>>>(x, n, total, lpt_log2, x_stride_bh, x_stride_n,
+                                                    packed, p_stride_bh, p_stride_n, scale, s_stride_bh);
+    else if (nbits == 8)
+        quant_pack_kernel<8><<<grid, block, 0, s>>>(x, n, total, lpt_log2, x_stride_bh, x_stride_n,
+                                                    packed, p_stride_bh, p_stride_n, scale, s_stride_bh);
+    else
+        quant_pack_kernel<2><<<grid, block, 0, s>>>(x, n, total, lpt_log2, x_stride_bh, x_stride_n,
+                                                    packed, p_stride_bh, p_stride_n, scale, s_stride_bh);
+    return check_launch("hyq_quant_pack");
+}

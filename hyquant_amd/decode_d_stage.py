@@ -1,0 +1,258 @@
+"""Decode-stage operators on MI355X: per-token quantisation and the fused
+four-segment hybrid decode attention.
+
+Drop-in for the reference's `src/ops/decode_d_stage.py`: same function names,
+argument meaning, output allocation and exceptions.  Every call runs the HIP
+kernels of libhyq.so on the current HIP stream of the input's device.
+"""
+
+from __future__ import annotations
+
+import math
+import threading
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+GROUP_SIZE = 128  # staging flush threshold (src/ops/decode_d_stage.py:19)
+_LOG2_E = 1.44269504
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (no CPU implementation)")
+
+
+def _inner_contig(t: torch.Tensor) -> torch.Tensor:
+    """The kernels take any head stride (a multiple of 16 bytes) but need each
+    head's rows packed back to back (token stride = row length) and 16-byte
+    aligned; anything else gets a contiguous copy."""
+    if t.numel() == 0:
+        return t
+    es = t.element_size()
+    ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and (t.dim() < 3 or t.stride(-2) == t.shape[-1])
+          and all((s * es) % 16 == 0 for s in t.stride()[:-1]))
+    return t if ok else t.contiguous()
+
+
+_ws_lock = threading.Lock()
+_ws_cache: dict = {}
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """Split-K partial buffer, cached per (device, stream) like the
+    reference's split-K buffers (src/ops/decode_d_stage.py:797-811).  Calls
+    on one stream are ordered; different streams get their own buffer."""
+    key = (device.index, stream)
+    with _ws_lock:
+        buf = _ws_cache.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            _ws_cache[key] = buf
+        return buf
+
+
+def _packed_dim(D: int, bits: int) -> int:
+    return D // 4 if bits == 2 else D // 2 if bits == 4 else D
+
+
+# ---------------------------------------------------------------------------
+# quantisation (src/ops/decode_d_stage.py:50-163)
+# ---------------------------------------------------------------------------
+
+
+def quantize_per_token(x: torch.Tensor, nbits: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-token symmetric quantisation.
+
+    x: [BH, N, D] bf16 -> (packed int8 [BH, N, D*nbits/8], scale fp16 [BH, N]).
+    Bit-exact with src/ops/decode_d_stage.py:50-77.
+    """
+    if nbits not in (2, 4, 8):
+        raise ValueError(f"nbits must be 2, 4, or 8, got {nbits}")
+    _require_gpu(x, "x")
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"quantize_per_token expects bf16 input, got {x.dtype}")
+    BH, N, D = x.shape
+    packed = torch.empty(BH, N, _packed_dim(D, nbits), dtype=torch.int8, device=x.device)
+    scale = torch.empty(BH, N, dtype=torch.float16, device=x.device)
+    quantize_into(x, nbits, packed, scale)
+    return packed, scale
+
+
+def quantize_into(x: torch.Tensor, nbits: int, packed: torch.Tensor, scale: torch.Tensor) -> None:
+    """Quantise x [BH, N, D] into preallocated (possibly strided) outputs, e.g.
+    the tail of a capacity-allocated prefix store (staging flush)."""
+    BH, N, D = x.shape
+    if BH * N == 0:
+        return
+    x = _inner_contig(x)
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    if packed.stride(-1) != 1 or scale.stride(-1) != 1:
+        raise ValueError("packed/scale outputs must be contiguous in the last dim")
+    st = _lib.lib().hyq_quant_pack(
+        x.data_ptr(), BH, N, D, x.stride(0), x.stride(1), nbits,
+        packed.data_ptr(), packed.stride(0), packed.stride(1),
+        scale.data_ptr(), scale.stride(0), _stream(x.device))
+    _lib.check(st, "quantize_per_token")
+
+
+def _unpack_int4(packed: torch.Tensor, D: int) -> torch.Tensor:
+    x = packed.to(torch.int32) & 0xFF
+    lo = ((x & 0x0F) << 28) >> 28
+    hi = (((x >> 4) & 0x0F) << 28) >> 28
+    return torch.stack([lo, hi], dim=-1).reshape(*packed.shape[:-1], D).float()
+
+
+def _unpack_int2(packed: torch.Tensor, D: int) -> torch.Tensor:
+    x = packed.to(torch.int32) & 0xFF
+    parts = [(((x >> (2 * j)) & 0x03) << 30) >> 30 for j in range(4)]
+    return torch.stack(parts, dim=-1).reshape(*packed.shape[:-1], D).float()
+
+
+def dequantize_per_token(packed: torch.Tensor, scale: torch.Tensor, D: int, nbits: int) -> torch.Tensor:
+    """[BH, N, D_packed] + [BH, N] -> fp16 [BH, N, D] = fp16(code * scale)
+    (src/ops/decode_d_stage.py:80-101).  Not on the decode hot path (the
+    fused kernel dequantises in registers); runs as device tensor ops."""
+    if nbits == 8:
+        q = packed.float()
+    elif nbits == 4:
+        q = _unpack_int4(packed, D)
+    elif nbits == 2:
+        q = _unpack_int2(packed, D)
+    else:
+        raise ValueError(f"nbits must be 2, 4, or 8, got {nbits}")
+    return (q * scale.float().unsqueeze(-1)).to(torch.float16)
+
+
+def _quantize_by_bits(x: torch.Tensor, bits: int):
+    """Alias kept for drop-in compatibility (src/ops/decode_d_stage.py:156-158)."""
+    return quantize_per_token(x, bits)
+
+
+def _dequantize_by_bits(packed, scale, D, bits):
+    return dequantize_per_token(packed, scale, D, bits)
+
+
+# ---------------------------------------------------------------------------
+# fused decode (src/ops/decode_d_stage.py:916-1005)
+# ---------------------------------------------------------------------------
+
+
+def _fill_segment(p: _lib.DecodeParams, i: int, k: torch.Tensor, v: torch.Tensor) -> list:
+    keep = []
+    n = k.shape[1]
+    p.seg_n[i] = n
+    if n == 0:
+        p.seg_k[i] = None
+        p.seg_v[i] = None
+        return keep
+    k = _inner_contig(k)
+    v = _inner_contig(v)
+    keep += [k, v]
+    p.seg_k[i] = k.data_ptr()
+    p.seg_v[i] = v.data_ptr()
+    p.seg_k_stride_bh[i], p.seg_k_stride_n[i] = k.stride(0), k.stride(1)
+    p.seg_v_stride_bh[i], p.seg_v_stride_n[i] = v.stride(0), v.stride(1)
+    return keep
+
+
+def fused_d_stage_decode(
+    q: torch.Tensor,                        # [BH_Q, D]
+    k_quant_packed: torch.Tensor,           # [BH_KV, N_quant, D/2] int8
+    v_quant_packed: torch.Tensor,
+    k_scale: torch.Tensor,                  # [BH_KV, N_quant] fp16
+    v_scale: torch.Tensor,
+    k_topk: torch.Tensor,                   # [BH_KV, N_topk, D] bf16
+    v_topk: torch.Tensor,
+    k_staging: torch.Tensor,                # [BH_KV, N_staging, D]
+    v_staging: torch.Tensor,
+    k_window: torch.Tensor,                 # [BH_KV, N_window, D]
+    v_window: torch.Tensor,
+    k_bits: int,
+    v_bits: int,
+    kv_repeat: int = 1,
+    sm_scale: Optional[float] = None,
+    split_tokens: int = 0,
+) -> torch.Tensor:
+    """Fused four-segment decode: int4 prefix + top-k + staging + window under
+    one online softmax.  Returns a new [BH_Q, D] tensor of q.dtype (bf16)."""
+    _require_gpu(q, "q")
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"fused_d_stage_decode expects bf16 q, got {q.dtype}")
+    BH_Q, D = q.shape
+    if BH_Q % kv_repeat:
+        raise ValueError(f"BH_Q ({BH_Q}) is not a multiple of kv_repeat ({kv_repeat})")
+    BH_KV = BH_Q // kv_repeat
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    out = torch.empty(BH_Q, D, device=q.device, dtype=q.dtype)
+    q = _inner_contig(q)
+    p = _lib.DecodeParams()
+    keep = [q]
+    p.q, p.q_stride = q.data_ptr(), q.stride(0)
+    p.out, p.out_stride = out.data_ptr(), out.stride(0)
+    n_quant = k_quant_packed.shape[1]
+    p.n_quant = n_quant
+    if n_quant > 0:
+        kp = _inner_contig(k_quant_packed)
+        vp = _inner_contig(v_quant_packed)
+        ks = k_scale if k_scale.stride(-1) == 1 else k_scale.contiguous()
+        vs = v_scale if v_scale.stride(-1) == 1 else v_scale.contiguous()
+        keep += [kp, vp, ks, vs]
+        p.k_packed, p.kp_stride_bh, p.kp_stride_n = kp.data_ptr(), kp.stride(0), kp.stride(1)
+        p.v_packed, p.vp_stride_bh, p.vp_stride_n = vp.data_ptr(), vp.stride(0), vp.stride(1)
+        p.k_scale, p.ks_stride_bh = ks.data_ptr(), ks.stride(0)
+        p.v_scale, p.vs_stride_bh = vs.data_ptr(), vs.stride(0)
+    for i, (k, v) in enumerate(((k_topk, v_topk), (k_staging, v_staging), (k_window, v_window))):
+        keep += _fill_segment(p, i, k, v)
+    p.bh_kv, p.kv_repeat, p.head_dim = BH_KV, kv_repeat, D
+    p.k_bits, p.v_bits = k_bits, v_bits
+    p.sm_scale = float(sm_scale)
+    p.split_tokens = int(split_tokens)
+    L = _lib.lib()
+    need = L.hyq_decode_workspace_size(p)
+    if need == 0:
+        _lib.check(L.hyq_decode_hybrid(p, None, 0, None), "fused_d_stage_decode")
+    stream = _stream(q.device)
+    ws = _workspace(q.device, stream, need)
+    st = L.hyq_decode_hybrid(p, ws.data_ptr(), ws.numel(), stream)
+    _lib.check(st, "fused_d_stage_decode")
+    return out
+
+
+# the reference's split-K entry point is the same operator here
+fused_d_stage_decode_splitk = fused_d_stage_decode
+
+
+def decode_bf16_full(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_repeat: int = 1,
+                     sm_scale: Optional[float] = None) -> torch.Tensor:
+    """Full-precision comparator: q [BH_Q, D], k/v [BH_KV, N, D] bf16."""
+    _require_gpu(q, "q")
+    BH_Q, D = q.shape
+    BH_KV, N, _ = k.shape
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    q = _inner_contig(q)
+    k = _inner_contig(k)
+    v = _inner_contig(v)
+    out = torch.empty(BH_Q, D, device=q.device, dtype=q.dtype)
+    L = _lib.lib()
+    need = L.hyq_decode_bf16_workspace_size(BH_KV, kv_repeat, N, D)
+    stream = _stream(q.device)
+    ws = _workspace(q.device, stream, max(need, 1))
+    st = L.hyq_decode_bf16(q.data_ptr(), q.stride(0), out.data_ptr(), out.stride(0),
+                           k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+                           N, BH_KV, kv_repeat, D, float(sm_scale), ws.data_ptr(), ws.numel(), stream)
+    _lib.check(st, "decode_bf16_full")
+    return out

@@ -1,0 +1,111 @@
+/*
+ * hyq.h — C ABI of libhyq.so, the MI355X (gfx950) implementation of HyQuant's
+ * hybrid-precision attention hot path.
+ *
+ * Conventions (every entry point):
+ *   - all pointers are device pointers the caller owns; nothing is retained;
+ *   - strides are in ELEMENTS of the pointed-to type; the innermost (channel)
+ *     dimension is always contiguous;
+ *   - work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the
+ *     legacy default stream); nothing synchronises;
+ *   - the return value is HYQ_OK (0) or a negative status; hyq_last_error()
+ *     returns a message for the calling thread's last failure.
+ * Element types: bf16 and fp16 are passed as 16-bit storage (uint16_t), int4
+ * codes as packed bytes (int8_t).
+ */
+#ifndef HYQ_H
+#define HYQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HYQ_OK 0
+#define HYQ_EINVAL (-22)   /* bad shape, stride, alignment or argument     */
+#define HYQ_ENOTSUP (-95)  /* valid but unsupported configuration          */
+#define HYQ_EDEVICE (-5)   /* HIP runtime / launch failure                  */
+#define HYQ_ENOSPC (-28)   /* workspace or capacity too small               */
+
+/* Message for the calling thread's last non-zero status ("" if none). */
+const char* hyq_last_error(void);
+
+/* ABI version of this library (incremented on any signature change). */
+int hyq_abi_version(void);
+
+/*
+ * Per-token symmetric quantisation + packing.
+ * Replaces quantize_per_token (src/ops/decode_d_stage.py:50-77) with
+ * _pack_int4 (:104-111) / _pack_int2 (:126-133), and the staging flush's
+ * quantisation (src/ops/d_stage_kv_cache.py:209-217).
+ *   x      bf16 [bh, n, d]        strides (x_stride_bh, x_stride_n)
+ *   packed int8 [bh, n, d*nbits/8] strides (p_stride_bh, p_stride_n)
+ *   scale  fp16 [bh, n]            strides (s_stride_bh, 1)
+ * scale = fp16(max(amax, 1e-5) / (2^(nbits-1)-1)) computed in fp32,
+ * code  = clamp(round_half_even(x / scale), -2^(nbits-1), 2^(nbits-1)-1),
+ * int4: even channel in the low nibble.  nbits in {2,4,8}; d % 8 == 0, d <= 256.
+ * The output may be a window of a larger buffer (append at an offset).
+ */
+int hyq_quant_pack(const uint16_t* x, int64_t bh, int64_t n, int32_t d,
+                   int64_t x_stride_bh, int64_t x_stride_n, int32_t nbits,
+                   int8_t* packed, int64_t p_stride_bh, int64_t p_stride_n,
+                   uint16_t* scale, int64_t s_stride_bh, void* stream);
+
+/*
+ * Four-segment hybrid decode attention for one query token per head.
+ * Replaces fused_d_stage_decode (src/ops/decode_d_stage.py:916-1005) and its
+ * split-K path fused_d_stage_decode_splitk (:823-913) with kernels
+ * _splitk_partial_kernel (:481-743) and _splitk_reduce_kernel (:746-782).
+ * The three bf16 segments are passed separately (no host-side concatenation,
+ * cf. :848-849); seg 0 = top-k vertical lines, 1 = staging, 2 = window.
+ * Softmax runs over [int4 prefix | seg0 | seg1 | seg2] jointly.
+ */
+typedef struct hyq_decode_params {
+    const uint16_t* q;    int64_t q_stride;        /* bf16 [bh_kv*kv_repeat, d]   */
+    uint16_t* out;        int64_t out_stride;      /* bf16 [bh_kv*kv_repeat, d]   */
+    const int8_t* k_packed; int64_t kp_stride_bh, kp_stride_n;  /* [bh_kv, n_quant, d/2] */
+    const int8_t* v_packed; int64_t vp_stride_bh, vp_stride_n;
+    const uint16_t* k_scale; int64_t ks_stride_bh;  /* fp16 [bh_kv, n_quant], token-contiguous */
+    const uint16_t* v_scale; int64_t vs_stride_bh;
+    int64_t n_quant;
+    const uint16_t* seg_k[3]; int64_t seg_k_stride_bh[3]; int64_t seg_k_stride_n[3];
+    const uint16_t* seg_v[3]; int64_t seg_v_stride_bh[3]; int64_t seg_v_stride_n[3];
+    int64_t seg_n[3];
+    int32_t bh_kv;        /* batch * kv heads                                  */
+    int32_t kv_repeat;    /* query heads per kv head, 1..16                     */
+    int32_t head_dim;     /* 128                                                */
+    int32_t k_bits, v_bits; /* 4, 4                                             */
+    float sm_scale;       /* softmax scale (reference default head_dim^-0.5)   */
+    int32_t split_tokens; /* int4 tokens per workgroup; 0 = automatic           */
+} hyq_decode_params;
+
+/* Bytes of device workspace hyq_decode_hybrid needs for these parameters
+ * (per-chunk partial results; no initialisation needed).  The call enqueues
+ * two kernels on `stream`; calls that share one workspace must be ordered on
+ * one stream. */
+size_t hyq_decode_workspace_size(const hyq_decode_params* p);
+
+int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/*
+ * Full-precision bf16 decode attention over one contiguous KV per head, the
+ * hand-written split-K comparator at the same shapes (no reference
+ * counterpart on this path other than the FA2 baseline of README.md:62-71).
+ *   q/out bf16 [bh_kv*kv_repeat, d]; k, v bf16 [bh_kv, n, d].
+ * Workspace rules as for hyq_decode_hybrid (size from
+ * hyq_decode_bf16_workspace_size).
+ */
+size_t hyq_decode_bf16_workspace_size(int32_t bh_kv, int32_t kv_repeat, int64_t n, int32_t d);
+int hyq_decode_bf16(const uint16_t* q, int64_t q_stride, uint16_t* out, int64_t out_stride,
+                    const uint16_t* k, int64_t k_stride_bh, int64_t k_stride_n,
+                    const uint16_t* v, int64_t v_stride_bh, int64_t v_stride_n,
+                    int64_t n, int32_t bh_kv, int32_t kv_repeat, int32_t d, float sm_scale,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HYQ_H */

@@ -389,14 +389,15 @@ def flush_staging(st: DecodeState) -> None:
 def decode_fp64(q: np.ndarray, k_packed, v_packed, k_scale, v_scale,
                 k_topk, v_topk, k_staging, v_staging, k_window, v_window,
                 k_bits: int = 4, v_bits: int = 4, kv_repeat: int = 1,
-                sm_scale: Optional[float] = None) -> np.ndarray:
+                sm_scale: Optional[float] = None, abs_v: bool = False) -> np.ndarray:
     """Exact (float64) restatement of fused_d_stage_decode
     (src/ops/decode_d_stage.py:916-1005, kernel math :599-691 and :221-267):
     softmax over [deq(prefix) | topk | staging | window] of q . k * sm_scale,
     with the int4 prefix dequantised as code * scale (the kernel factors the
     per-token scales out of the dot products, F8), GQA head h -> KV head h // R.
 
-    q [BH_Q, D] -> out float64 [BH_Q, D].
+    q [BH_Q, D] -> out float64 [BH_Q, D].  abs_v=True attends over |V| instead
+    (used by tests as the magnitude that bf16 rounding errors scale with).
     """
     BHQ, D = q.shape
     BHK = BHQ // kv_repeat
@@ -406,19 +407,21 @@ def decode_fp64(q: np.ndarray, k_packed, v_packed, k_scale, v_scale,
     vq = unpack_codes(v_packed, v_bits).astype(np.float64) * v_scale.astype(np.float64)[..., None]
     K = np.concatenate([kq, k_topk, k_staging, k_window], axis=1).astype(np.float64)
     V = np.concatenate([vq, v_topk, v_staging, v_window], axis=1).astype(np.float64)
-    K = np.repeat(K, kv_repeat, axis=0)
-    V = np.repeat(V, kv_repeat, axis=0)
-    s = np.einsum("hd,hnd->hn", q.astype(np.float64), K) * sm_scale
-    s -= s.max(axis=1, keepdims=True)
+    if abs_v:   # sum_t p_t |v_t| / l: the scale of rounding errors in P and in the output
+        V = np.abs(V)
+    qg = q.astype(np.float64).reshape(BHK, kv_repeat, D)            # head h -> KV head h // R
+    s = np.einsum("hrd,hnd->hrn", qg, K) * sm_scale
+    s -= s.max(axis=2, keepdims=True)
     p = np.exp(s)
-    p /= p.sum(axis=1, keepdims=True)
-    return np.einsum("hn,hnd->hd", p, V)
+    p /= p.sum(axis=2, keepdims=True)
+    return np.einsum("hrn,hnd->hrd", p, V).reshape(BHQ, D)
 
 
-def decode_fp64_state(q: np.ndarray, st: DecodeState, kv_repeat: int, sm_scale=None) -> np.ndarray:
+def decode_fp64_state(q: np.ndarray, st: DecodeState, kv_repeat: int, sm_scale=None,
+                      abs_v: bool = False) -> np.ndarray:
     return decode_fp64(q, st.k_packed, st.v_packed, st.k_scale, st.v_scale,
                        st.k_topk, st.v_topk, st.k_staging, st.v_staging,
-                       st.k_window, st.v_window, st.k_bits, st.v_bits, kv_repeat, sm_scale)
+                       st.k_window, st.v_window, st.k_bits, st.v_bits, kv_repeat, sm_scale, abs_v)
 
 
 def decode_bf16_eager(q, st: DecodeState, kv_repeat: int, B: int):

@@ -1,0 +1,107 @@
+"""CPU checks of the C ABI: libhyq.so loads, exports every symbol that
+include/hyq.h declares, and rejects bad arguments on the host side before any
+GPU work (no compute calls are made here)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hyq.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(hyq_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_declares_expected_symbols():
+    from hyquant_amd import _lib
+    assert _declared() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    from hyquant_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libhyq.so not built")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def _L():
+    from hyquant_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libhyq.so not built")
+    return _lib, _lib.lib()
+
+
+def test_abi_version_and_error_strings():
+    _lib, L = _L()
+    assert L.hyq_abi_version() == 1
+    st = L.hyq_quant_pack(None, 1, 1, 128, 0, 0, 3, None, 0, 0, None, 0, None)
+    assert st == _lib.HYQ_EINVAL
+    assert b"nbits must be 2, 4, or 8" in L.hyq_last_error()
+    with pytest.raises(ValueError, match="nbits"):
+        _lib.check(st, "quantize_per_token")
+
+
+def test_quant_pack_host_validation():
+    _lib, L = _L()
+    assert L.hyq_quant_pack(None, 1, 1, 100, 0, 0, 4, None, 0, 0, None, 0, None) == _lib.HYQ_ENOTSUP
+    assert L.hyq_quant_pack(None, -1, 1, 128, 0, 0, 4, None, 0, 0, None, 0, None) == _lib.HYQ_EINVAL
+    # empty input is a no-op
+    assert L.hyq_quant_pack(None, 0, 5, 128, 0, 0, 4, None, 0, 0, None, 0, None) == _lib.HYQ_OK
+    # misaligned x
+    assert L.hyq_quant_pack(8, 1, 1, 128, 128, 128, 4, 16, 64, 64, 16, 1, None) == _lib.HYQ_EINVAL
+
+
+def _params(_lib, **kw):
+    p = _lib.DecodeParams()
+    p.q, p.q_stride, p.out, p.out_stride = 256, 128, 512, 128
+    p.bh_kv, p.kv_repeat, p.head_dim, p.k_bits, p.v_bits = 8, 4, 128, 4, 4
+    p.sm_scale = 128 ** -0.5
+    p.seg_n[2] = 128
+    p.seg_k[2] = 1024
+    p.seg_v[2] = 2048
+    p.seg_k_stride_bh[2] = p.seg_v_stride_bh[2] = 128 * 128
+    p.seg_k_stride_n[2] = p.seg_v_stride_n[2] = 128
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_decode_host_validation():
+    _lib, L = _L()
+    p = _params(_lib)
+    assert L.hyq_decode_workspace_size(p) > 0
+    for bad, code in ((dict(head_dim=64), _lib.HYQ_ENOTSUP), (dict(k_bits=8), _lib.HYQ_ENOTSUP),
+                      (dict(kv_repeat=17), _lib.HYQ_ENOTSUP), (dict(q=258), _lib.HYQ_EINVAL),
+                      (dict(bh_kv=-1), _lib.HYQ_EINVAL)):
+        p = _params(_lib, **bad)
+        assert L.hyq_decode_workspace_size(p) == 0
+        assert L.hyq_decode_hybrid(p, None, 0, None) == code, bad
+    # too-small workspace is refused before launch
+    p = _params(_lib)
+    assert L.hyq_decode_hybrid(p, 4096, 16, None) == _lib.HYQ_ENOSPC
+    assert b"workspace" in L.hyq_last_error()
+    # prefix pointers must be present when n_quant > 0
+    p = _params(_lib, n_quant=512)
+    assert L.hyq_decode_hybrid(p, 4096, 1 << 30, None) == _lib.HYQ_EINVAL
+
+
+def test_bf16_workspace_size():
+    _lib, L = _L()
+    assert L.hyq_decode_bf16_workspace_size(8, 4, 8192, 128) > 8 * 4 * 128 * 4
+    assert L.hyq_decode_bf16_workspace_size(8, 4, 8192, 64) == 0
+
+
+def test_python_layer_rejects_cpu_tensors():
+    import torch
+    import hyquant_amd as hq
+    with pytest.raises(ValueError, match="GPU"):
+        hq.quantize_per_token(torch.zeros(1, 1, 128, dtype=torch.bfloat16), 4)
+    with pytest.raises(ValueError, match="nbits"):
+        hq.quantize_per_token(torch.zeros(1, 1, 128, dtype=torch.bfloat16), 5)

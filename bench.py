@@ -8,8 +8,10 @@ fused_d_stage_decode call over that cache.
 
 Timing: inputs are resident in HBM; R copies of the cache (R chosen so the
 copies exceed 1 GiB, i.e. four times the 256 MiB Infinity Cache) are used in
-rotation so every step streams its bytes from HBM.  W untimed steps, then K
-steps between two HIP events on the stream the kernels run on.
+rotation so every step streams its bytes from HBM.  W untimed steps, then the
+K timed steps are one replay of a HIP graph holding the K steps, bracketed by
+two HIP events on the stream the kernels run on (the same K steps issued as
+Python calls one by one are reported as eager_us_per_step).
 
 Output: one JSON line (rank 0), with the roofline of the decode kernel, the
 CPU baseline (the reference's bf16 eager decode math run by torch on the host
@@ -92,7 +94,12 @@ def run_decode(q, st, G):
 
 
 def time_rotating(fn, states, warmup, steps):
-    """Average ms per call over `steps` calls cycling through `states`."""
+    """ms per step over `steps` steps cycling through `states`.
+
+    The steps are captured once into a HIP graph and the timed region is one
+    replay of it (K steps, no host work between launches); returns
+    (graph_ms_per_step, eager_ms_per_step) where the eager figure times the
+    same K Python calls issued one by one."""
     n = len(states)
     for i in range(warmup):
         fn(states[i % n])
@@ -104,7 +111,20 @@ def time_rotating(fn, states, warmup, steps):
         fn(states[i % n])
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    eager = e0.elapsed_time(e1) / steps
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(states[i % n])
+    g.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    graph = e0.elapsed_time(e1) / steps
+    del g
+    return graph, eager
 
 
 def copies_for(nbytes, cap=512):
@@ -116,9 +136,9 @@ def bench_hybrid(B, HQ, HKV, N, dev, warmup, steps, seed=0):
     R = copies_for(nbytes)
     states = [make_state(B, HQ, HKV, N, dev, seed + r) for r in range(R)]
     G = HQ // HKV
-    ms = time_rotating(lambda s: run_decode(s[0], s[1], G), states, warmup, steps)
+    ms, eager = time_rotating(lambda s: run_decode(s[0], s[1], G), states, warmup, steps)
     del states
-    return ms, nbytes, R
+    return ms, nbytes, R, eager
 
 
 def bench_bf16(B, HQ, HKV, N, dev, warmup, steps, seed=0):
@@ -129,9 +149,9 @@ def bench_bf16(B, HQ, HKV, N, dev, warmup, steps, seed=0):
     mk = lambda: torch.randn(B * HKV, N + 64, D, generator=g, device=dev).to(torch.bfloat16)
     states = [(torch.randn(B * HQ, D, generator=g, device=dev).to(torch.bfloat16), mk(), mk()) for _ in range(R)]
     G = HQ // HKV
-    ms = time_rotating(lambda s: hq.decode_bf16_full(s[0], s[1], s[2], kv_repeat=G), states, warmup, steps)
+    ms, eager = time_rotating(lambda s: hq.decode_bf16_full(s[0], s[1], s[2], kv_repeat=G), states, warmup, steps)
     del states
-    return ms, nbytes, R
+    return ms, nbytes, R, eager
 
 
 def cpu_baseline(N=8192, min_steps=20, budget_s=20.0):
@@ -187,7 +207,7 @@ def main():
     import hyquant_amd  # noqa: F401  (fails loudly if libhyq.so is missing)
 
     B, HQ, HKV, N = 1, 32, 8, 8192
-    ms, nbytes, R = bench_hybrid(B, HQ, HKV, N, dev, args.warmup, args.steps)
+    ms, nbytes, R, eager = bench_hybrid(B, HQ, HKV, N, dev, args.warmup, args.steps)
     us = ms * 1e3
     gbs = nbytes / (ms * 1e-3) / 1e9
     Nq, T, S, W = seg_sizes(N)
@@ -208,13 +228,15 @@ def main():
         "config": {"workload": "config1: fused hybrid decode, B=1, 32q/8kv, d128, prefix 8192",
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "prefix": N,
                    "n_quant": Nq, "n_topk": T, "n_staging": S, "n_window": W,
-                   "cache_copies_rotated": R},
+                   "cache_copies_rotated": R, "timing": "one HIP-graph replay of K steps",
+                   "eager_us_per_step": round(eager * 1e3, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_kernel", "algorithmic_bytes_per_launch": nbytes},
+                     "kernel": "decode step = decode_partial_kernel + decode_merge_kernel",
+                     "algorithmic_bytes_per_launch": nbytes},
     }
     if not args.no_bf16:
-        ms16, b16, _ = bench_bf16(B, HQ, HKV, N, dev, args.warmup, args.steps)
+        ms16, b16, _, _ = bench_bf16(B, HQ, HKV, N, dev, args.warmup, args.steps)
         res["bf16_comparator"] = {"us_per_step": round(ms16 * 1e3, 3),
                                   "gbs": round(b16 / (ms16 * 1e-3) / 1e9, 1),
                                   "speedup_hybrid_vs_bf16": round(ms16 / ms, 3)}
@@ -222,12 +244,12 @@ def main():
         sweep = []
         for b in (1, 16):
             for n in (1024, 2048, 4096, 8192, 16384, 32768):
-                m, nb, _ = bench_hybrid(b, HQ, HKV, n, dev, 10, 100)
+                m, nb, _, _ = bench_hybrid(b, HQ, HKV, n, dev, 10, 100)
                 row = {"batch": b, "prefix": n, "us_per_step": round(m * 1e3, 3),
                        "gbs": round(nb / (m * 1e-3) / 1e9, 1),
                        "frac_peak": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
                 if not args.no_bf16:
-                    m16, nb16, _ = bench_bf16(b, HQ, HKV, n, dev, 5, 50)
+                    m16, nb16, _, _ = bench_bf16(b, HQ, HKV, n, dev, 5, 50)
                     row["bf16_us_per_step"] = round(m16 * 1e3, 3)
                     row["speedup_vs_bf16"] = round(m16 / m, 3)
                 sweep.append(row)

@@ -11,6 +11,7 @@ from .decode_d_stage import (  # noqa: F401
     fused_d_stage_decode_splitk,
     quantize_per_token,
 )
+from .vertical import compute_vertical_indices  # noqa: F401
 
 __all__ = [
     "GROUP_SIZE",
@@ -19,4 +20,5 @@ __all__ = [
     "fused_d_stage_decode",
     "fused_d_stage_decode_splitk",
     "decode_bf16_full",
+    "compute_vertical_indices",
 ]

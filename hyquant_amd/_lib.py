@@ -29,6 +29,10 @@ EXPORTS = (
     "hyq_decode_hybrid",
     "hyq_decode_bf16_workspace_size",
     "hyq_decode_bf16",
+    "hyq_vertical_select_workspace_size",
+    "hyq_vertical_select",
+    "hyq_freeze_workspace_size",
+    "hyq_freeze_reorganise",
 )
 
 
@@ -75,6 +79,20 @@ def _declare(lib):
                                     c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64,
                                     c_int64, c_int32, c_int32, c_int32, c_float,
                                     c_void_p, c_size_t, c_void_p]
+    lib.hyq_vertical_select_workspace_size.restype = c_size_t
+    lib.hyq_vertical_select_workspace_size.argtypes = [c_int32, c_int32, c_int64]
+    lib.hyq_vertical_select.restype = c_int
+    lib.hyq_vertical_select.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32,
+                                        c_void_p, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32,
+                                        c_int32, c_int32, c_int32, c_void_p, c_void_p, c_size_t, c_void_p]
+    lib.hyq_freeze_workspace_size.restype = c_size_t
+    lib.hyq_freeze_workspace_size.argtypes = [c_int32, c_int64]
+    lib.hyq_freeze_reorganise.restype = c_int
+    lib.hyq_freeze_reorganise.argtypes = (
+        [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64,
+         c_int32, c_int32, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32]
+        + [c_void_p, c_int64, c_int64] * 2 + [c_void_p, c_int64] * 2 + [c_void_p, c_int64, c_int64] * 4
+        + [c_void_p, c_size_t, c_void_p])
 
 
 def lib():

@@ -105,6 +105,51 @@ int hyq_decode_bf16(const uint16_t* q, int64_t q_stride, uint16_t* out, int64_t 
                     int64_t n, int32_t bh_kv, int32_t kv_repeat, int32_t d, float sm_scale,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Vertical-line selector.  Replaces compute_vertical_indices
+ * (src/patch/_common.py:144-190) for both of its call sites:
+ *   prefill (src/patch/patch_llama.py:165-169): group = 1, q = all query heads,
+ *     each query head scores the keys of its KV head (GQA-native);
+ *   freeze (src/ops/d_stage_kv_cache.py:131-136): group = kv_repeat, the
+ *     query tail is first averaged over each GQA group (one output per KV head).
+ *   q    bf16 [b, hq_in, q_len, d]  strides (qs_b, qs_h, qs_t)
+ *   k    bf16 [b, hk, >= p, d]      strides (ks_b, ks_h, ks_n); positions [0, p) are scored
+ *   out  int64 [b, hq_in/group, top_k] (score desc, index asc)
+ * qm = bf16(mean over the last `tail` queries [of bf16(mean over the group)]),
+ * score = bf16(exact dot(qm, k)), top_k chosen by the caller
+ * (reference: min(max(1, ceil(p * top_ratio)), p)).  d = 128, p <= 65536,
+ * top_k <= 8192, at most 16 output heads per key head.
+ */
+size_t hyq_vertical_select_workspace_size(int32_t b, int32_t h_out, int64_t p);
+int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, int32_t q_len,
+                        int32_t hq_in, int32_t group, const uint16_t* k, int64_t ks_b, int64_t ks_h,
+                        int64_t ks_n, int32_t hk, int64_t p, int32_t b, int32_t d, int32_t tail,
+                        int32_t top_k, int64_t* out_idx, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/*
+ * Prefill -> decode cache reorganisation.  Replaces the body of
+ * DStageLayerCache.freeze after the selector (src/ops/d_stage_kv_cache.py:138-179):
+ * given keys/values bf16 [b, hk, n, d] and the selected prefix positions
+ * topk_idx int64 [b*hk, top_k] (in [0, n-w)), writes
+ *   k/v_topk  bf16 [b*hk, top_k, d]   rows in topk_idx order
+ *   k/v_window bf16 [b*hk, w, d]      the last w rows
+ *   k/v_packed + k/v_scale            the other n-w-top_k prefix rows in
+ *                                     ascending position, quantised per token
+ *                                     exactly as hyq_quant_pack (k_bits, v_bits).
+ * Workspace: hyq_freeze_workspace_size(b*hk, n-w) bytes (a position bitmap).
+ */
+size_t hyq_freeze_workspace_size(int32_t bh, int64_t p);
+int hyq_freeze_reorganise(const uint16_t* k, int64_t ks_b, int64_t ks_h, int64_t ks_n,
+                          const uint16_t* v, int64_t vs_b, int64_t vs_h, int64_t vs_n,
+                          int32_t b, int32_t hk, int64_t n, int32_t d, int32_t w,
+                          const int64_t* topk_idx, int32_t top_k, int32_t k_bits, int32_t v_bits,
+                          int8_t* kp, int64_t kp_bh, int64_t kp_n, int8_t* vp, int64_t vp_bh, int64_t vp_n,
+                          uint16_t* ksc, int64_t ksc_bh, uint16_t* vsc, int64_t vsc_bh,
+                          uint16_t* kt, int64_t kt_bh, int64_t kt_n, uint16_t* vt, int64_t vt_bh, int64_t vt_n,
+                          uint16_t* kw, int64_t kw_bh, int64_t kw_n, uint16_t* vw, int64_t vw_bh, int64_t vw_n,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

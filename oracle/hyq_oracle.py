@@ -532,15 +532,20 @@ def make_decode_inputs(B=1, HQ=32, HKV=8, N=1024, D=128, W=128, S=37, rho=0.05,
     off = torch.randn(HKV, D, generator=g) * math.sqrt(2.0)
     k = k + off[None, :, None, :]
     qt_b = qt.to(torch.bfloat16).float()
-    n_plant = int(plant_ratio * N)
+    n_plant = min(int(plant_ratio * N), max(0, N - W))
     planted = np.zeros((B, HKV, n_plant), dtype=np.int64)
+    if N <= W:                   # no non-window prefix: nothing to plant
+        n_plant = 0
+        planted = np.zeros((B, HKV, 0), dtype=np.int64)
     for b in range(B):
         for h in range(HKV):
+            if n_plant == 0:
+                continue
             u = qt_b[b, h * G:(h + 1) * G].reshape(-1, D).mean(dim=0)
             u = u / u.norm()
             pos = torch.randperm(N - W, generator=g)[:n_plant]
             k[b, h, pos, :] = off[h] + 3.0 * math.sqrt(D) * u
-            planted[b, h] = np.sort(pos.numpy())
+            planted[b, h, :len(pos)] = np.sort(pos.numpy())
     k_new = torch.randn(B, HKV, S, D, generator=g) + off[None, :, None, :]
     v_new = torch.randn(B, HKV, S, D, generator=g)
     q_dec = torch.randn(B * HQ, D, generator=g)

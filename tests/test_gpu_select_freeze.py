@@ -1,0 +1,154 @@
+"""GPU parity of the vertical-line selector (hyq_vertical_select), the freeze
+reorganisation (hyq_freeze_reorganise) and the D-stage cache built on them,
+against the CPU oracle: indices, int4 codes, scales and bf16 segments
+bit-exact; decode through the cache within 2e-3."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import hyq_oracle as O
+from tests.gpu_util import to_dev_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand_bf16(rng, shape, scale=1.0):
+    return O.bf16_round((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+@pytest.mark.parametrize("B,HQ,HK,QL,KL,W,rho", [
+    (2, 8, 2, 40, 300, 32, 0.1),      # GQA-native (kv_repeat 4)
+    (1, 4, 4, 7, 200, 16, 0.2),       # non-GQA, tail shorter than W
+    (1, 16, 1, 5, 1000, 64, 0.05),    # GQA 16
+    (3, 2, 2, 64, 129, 128, 1.0),     # prefix of one token, rho = 1
+])
+def test_selector_prefill_variant_bit_exact(B, HQ, HK, QL, KL, W, rho):
+    from hyquant_amd.vertical import compute_vertical_indices
+    print(f"select B={B} HQ={HQ} HK={HK} QL={QL} KL={KL} W={W} rho={rho}", flush=True)
+    rng = np.random.default_rng(B * 1000 + KL)
+    q = _rand_bf16(rng, (B, HQ, QL, 128))
+    k = _rand_bf16(rng, (B, HK, KL, 128), 2.0)
+    got = compute_vertical_indices(to_dev_bf16(q, "cuda"), to_dev_bf16(k, "cuda"), W, rho, kv_repeat=HQ // HK)
+    exp = O.compute_vertical_indices(q, k, W, rho, kv_repeat=HQ // HK)
+    assert got.shape == exp.shape
+    assert np.array_equal(got.cpu().numpy(), exp)
+
+
+def test_selector_ties_and_negative_zero():
+    from hyquant_amd.vertical import compute_vertical_indices
+    rng = np.random.default_rng(5)
+    q = np.ones((1, 1, 2, 128), np.float32)
+    k = np.zeros((1, 1, 600, 128), np.float32)
+    k[0, 0, ::7] = 1.0 / 128                           # many exact ties (score 1)
+    k[0, 0, 5::11, :64] = -1.0 / 128                   # score -0.5
+    k[0, 0, 3, :64], k[0, 0, 3, 64:] = 1.0, -1.0       # exact zero
+    k[0, 0, 4] = -0.0                                  # negative zero
+    got = compute_vertical_indices(to_dev_bf16(q, "cuda"), to_dev_bf16(k, "cuda"), 100, 0.3)
+    exp = O.compute_vertical_indices(q, k, 100, 0.3)
+    assert np.array_equal(got.cpu().numpy(), exp)
+    # the tied block comes out in ascending index order
+    first = got.cpu().numpy()[0, 0, :10]
+    assert list(first) == sorted(first)
+
+
+@pytest.mark.parametrize("cfg", [dict(B=1, HQ=32, HKV=8, N=1024), dict(B=2, HQ=32, HKV=8, N=8192),
+                                 dict(B=2, HQ=64, HKV=8, N=4096), dict(B=1, HQ=32, HKV=2, N=16384)])
+def test_selector_freeze_variant_and_prefill_on_config_inputs(cfg):
+    from hyquant_amd.vertical import compute_vertical_indices, freeze_vertical_indices
+    print(f"select config {cfg}", flush=True)
+    W = 128 if cfg["N"] <= 8192 else 256
+    inp = O.make_decode_inputs(W=W, S=4, seed=7, **cfg)
+    G = cfg["HQ"] // cfg["HKV"]
+    qt = to_dev_bf16(inp.query_tail, "cuda")
+    kd = to_dev_bf16(inp.keys, "cuda")
+    P = cfg["N"] - W
+    got = freeze_vertical_indices(qt, kd[:, :, :P], W, 0.05, G)
+    exp = O.compute_vertical_indices(O.group_mean_query(inp.query_tail, cfg["HKV"]), inp.keys[:, :, :P], W, 0.05)
+    assert np.array_equal(got.cpu().numpy(), exp)
+    got_q = compute_vertical_indices(qt, kd, W, 0.05, kv_repeat=G)
+    exp_q = O.compute_vertical_indices(inp.query_tail, inp.keys, W, 0.05, kv_repeat=G)
+    assert np.array_equal(got_q.cpu().numpy(), exp_q)
+
+
+def _cache_from_inputs(inp, k_bits=4, v_bits=4):
+    from hyquant_amd.d_stage_kv_cache import DStageLayerCache
+    layer = DStageLayerCache(0, k_bits=k_bits, v_bits=v_bits, window_size=inp.W, top_ratio=inp.rho)
+    half = inp.N // 2
+    kd, vd = to_dev_bf16(inp.keys, "cuda"), to_dev_bf16(inp.values, "cuda")
+    layer.update_prefill(kd[:, :, :half], vd[:, :, :half])      # two prefill chunks
+    layer.update_prefill(kd[:, :, half:], vd[:, :, half:])
+    layer.save_query_tail(to_dev_bf16(inp.query_tail, "cuda"))
+    layer.freeze(kv_repeat=inp.HQ // inp.HKV)
+    return layer
+
+
+def _check_state(layer, st):
+    np_ = lambda t: t.cpu().numpy()
+    assert np.array_equal(np_(layer.topk_indices), st.topk_idx)
+    assert np.array_equal(np_(layer.k_quant_packed), st.k_packed)
+    assert np.array_equal(np_(layer.v_quant_packed), st.v_packed)
+    assert np.array_equal(np_(layer.k_scale).view(np.uint16), st.k_scale.view(np.uint16))
+    assert np.array_equal(np_(layer.v_scale).view(np.uint16), st.v_scale.view(np.uint16))
+    assert np.array_equal(np_(layer.k_topk.float()), st.k_topk)
+    assert np.array_equal(np_(layer.v_topk.float()), st.v_topk)
+    assert np.array_equal(np_(layer.k_window.float()), st.k_window)
+    assert np.array_equal(np_(layer.v_window.float()), st.v_window)
+    assert layer._staging_ptr == st.ring_ptr
+    assert np.array_equal(np_(layer._staging_buf_k[:, :st.ring_ptr].float()), st.k_staging)
+
+
+@pytest.mark.parametrize("cfg", [dict(B=1, HQ=32, HKV=8, N=1024, S=37), dict(B=2, HQ=32, HKV=8, N=8192, S=64)])
+def test_cache_freeze_flush_decode(cfg):
+    print(f"cache {cfg}", flush=True)
+    inp = O.make_decode_inputs(W=128, seed=11, **cfg)
+    layer = _cache_from_inputs(inp)
+    st = O.freeze(inp.keys, inp.values, inp.query_tail, inp.W, inp.rho, inp.HQ // inp.HKV)
+    torch.cuda.synchronize()
+    _check_state(layer, st)
+    # staging: S tokens, then enough to cross one flush
+    kn, vn = to_dev_bf16(inp.k_new, "cuda"), to_dev_bf16(inp.v_new, "cuda")
+    layer.append_staging(kn, vn)
+    O.append_staging(st, inp.k_new, inp.v_new)
+    rng = np.random.default_rng(3)
+    extra_k = _rand_bf16(rng, (cfg["B"], cfg["HKV"], 130, 128), 1.4)
+    extra_v = _rand_bf16(rng, (cfg["B"], cfg["HKV"], 130, 128))
+    for i in range(0, 130, 1):                   # one token per step, as in decode
+        layer.append_staging(to_dev_bf16(extra_k[:, :, i:i + 1], "cuda"), to_dev_bf16(extra_v[:, :, i:i + 1], "cuda"))
+    O.append_staging(st, extra_k, extra_v)
+    torch.cuda.synchronize()
+    _check_state(layer, st)
+    assert layer.get_seq_length() == cfg["N"] + cfg["S"] + 130
+    q = to_dev_bf16(inp.q_dec, "cuda").reshape(cfg["B"], cfg["HQ"], 1, 128)
+    out = layer.decode_attention(q, inp.HQ // inp.HKV).reshape(-1, 128).float().cpu().numpy()
+    ref = O.decode_fp64_state(inp.q_dec, st, inp.HQ // inp.HKV)
+    err = float(np.max(np.abs(out - ref)))
+    print(f"cache decode max-abs {err:.3e}", flush=True)
+    assert err <= 2e-3
+
+
+def test_cache_k4v2_freeze_bit_exact_and_decode():
+    inp = O.make_decode_inputs(B=1, HQ=32, HKV=8, N=1024, W=128, S=9, seed=12)
+    layer = _cache_from_inputs(inp, k_bits=4, v_bits=2)
+    st = O.freeze(inp.keys, inp.values, inp.query_tail, inp.W, inp.rho, 4, k_bits=4, v_bits=2)
+    layer.append_staging(to_dev_bf16(inp.k_new, "cuda"), to_dev_bf16(inp.v_new, "cuda"))
+    O.append_staging(st, inp.k_new, inp.v_new)
+    torch.cuda.synchronize()
+    _check_state(layer, st)
+    q = to_dev_bf16(inp.q_dec, "cuda").reshape(1, 32, 1, 128)
+    out = layer.decode_attention(q, 4).reshape(-1, 128).float().cpu().numpy()
+    ref = O.decode_fp64_state(inp.q_dec, st, 4)
+    # the reference's own bf16 eager math for non-K4V4 modes
+    assert float(np.max(np.abs(out - ref))) <= 2e-2
+
+
+def test_cache_short_prompt_no_prefix():
+    inp = O.make_decode_inputs(B=1, HQ=8, HKV=2, N=100, W=128, S=3, seed=13)
+    layer = _cache_from_inputs(inp)
+    assert layer.k_quant_packed.shape[1] == 0 and layer.k_window.shape[1] == 100
+    layer.append_staging(to_dev_bf16(inp.k_new, "cuda"), to_dev_bf16(inp.v_new, "cuda"))
+    st = O.freeze(inp.keys, inp.values, inp.query_tail, inp.W, inp.rho, 4)
+    O.append_staging(st, inp.k_new, inp.v_new)
+    q = to_dev_bf16(inp.q_dec, "cuda").reshape(1, 8, 1, 128)
+    out = layer.decode_attention(q, 4).reshape(-1, 128).float().cpu().numpy()
+    assert float(np.max(np.abs(out - O.decode_fp64_state(inp.q_dec, st, 4)))) <= 2e-3

@@ -9,7 +9,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
-from ctypes import POINTER, Structure, c_float, c_int, c_int32, c_int64, c_size_t, c_uint16, c_void_p, c_int8, c_char_p
+from ctypes import POINTER, Structure, c_float, c_int, c_int32, c_int64, c_size_t, c_uint16, c_void_p, c_int8, c_char_p, c_double
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libhyq.so")
@@ -33,6 +33,10 @@ EXPORTS = (
     "hyq_vertical_select",
     "hyq_freeze_workspace_size",
     "hyq_freeze_reorganise",
+    "hyq_per_block_int8",
+    "hyq_prefill_lists",
+    "hyq_prefill_workspace_size",
+    "hyq_prefill_hybrid",
 )
 
 
@@ -53,6 +57,21 @@ class DecodeParams(Structure):
         ("k_bits", c_int32), ("v_bits", c_int32),
         ("sm_scale", c_float),
         ("split_tokens", c_int32),
+    ]
+
+
+class PrefillParams(Structure):
+    """Mirror of `hyq_prefill_params` (include/hyq.h)."""
+    _fields_ = [
+        ("q", c_void_p), ("q_stride_b", c_int64), ("q_stride_h", c_int64), ("q_stride_n", c_int64),
+        ("k", c_void_p), ("k_stride_b", c_int64), ("k_stride_h", c_int64), ("k_stride_n", c_int64),
+        ("v", c_void_p), ("v_stride_b", c_int64), ("v_stride_h", c_int64), ("v_stride_n", c_int64),
+        ("vidx", c_void_p), ("vi_stride_b", c_int64), ("vi_stride_h", c_int64), ("vi_stride_t", c_int64),
+        ("out", c_void_p), ("o_stride_b", c_int64), ("o_stride_h", c_int64), ("o_stride_n", c_int64),
+        ("batch", c_int32), ("hq", c_int32), ("hkv", c_int32), ("head_dim", c_int32),
+        ("n", c_int64), ("t", c_int64),
+        ("window", c_int32), ("smooth_k", c_int32), ("pv_mode", c_int32),
+        ("sm_scale", c_double),
     ]
 
 
@@ -93,6 +112,17 @@ def _declare(lib):
          c_int32, c_int32, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32]
         + [c_void_p, c_int64, c_int64] * 2 + [c_void_p, c_int64] * 2 + [c_void_p, c_int64, c_int64] * 4
         + [c_void_p, c_size_t, c_void_p])
+    lib.hyq_per_block_int8.restype = c_int
+    lib.hyq_per_block_int8.argtypes = ([c_void_p, c_int32, c_int64, c_int64, c_int64, c_int32, c_int32, c_int64,
+                                        c_int32, c_float, c_int32, c_void_p, c_int64, c_int64,
+                                        c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p])
+    lib.hyq_prefill_lists.restype = c_int
+    lib.hyq_prefill_lists.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int64, c_int64,
+                                      c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
+    lib.hyq_prefill_workspace_size.restype = c_size_t
+    lib.hyq_prefill_workspace_size.argtypes = [c_int32, c_int32, c_int32, c_int64, c_int64, c_int32, c_int32]
+    lib.hyq_prefill_hybrid.restype = c_int
+    lib.hyq_prefill_hybrid.argtypes = [POINTER(PrefillParams), c_void_p, c_size_t, c_void_p]
 
 
 def lib():

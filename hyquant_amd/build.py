@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libhyq.so")
 
-SOURCES = ["status.hip", "quant.hip", "decode.hip", "select.hip"]
+SOURCES = ["status.hip", "quant.hip", "decode.hip", "select.hip", "prefill.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

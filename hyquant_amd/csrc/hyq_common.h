@@ -41,6 +41,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// float64 -> bf16 with one correct RNE rounding: round to float32 toward zero
+// with a sticky bit (round-to-odd), then RNE to bf16.
+__device__ __forceinline__ uint16_t f64_to_bf16_rne(double x) {
+    float f = __double2float_rz(x);
+    uint32_t u = __float_as_uint(f);
+    if (static_cast<double>(f) != x) u |= 1u;
+    return f32_to_bf16_rne(__uint_as_float(u));
+}
+
 // ---- wavefront helpers (wave64) ---------------------------------------------
 
 __device__ __forceinline__ float wave_xor_f32(float v, int mask) {

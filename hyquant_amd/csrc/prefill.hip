@@ -1,0 +1,1038 @@
+// Hybrid-precision causal prefill attention for gfx950 (MI355X).
+//
+// Semantics (sage_vertical_attention_v2, src/ops/sage_unified.py:550-622 with
+// its kernel :398-496 and the per-block quantiser
+// src/ops/vendor/sageattention/triton/quant_per_block.py:21-101):
+//   c   = fp32(sm_scale * log2e)
+//   Q   int8 per 128-row block of x = fp32(q) * c: scale = amax / 127,
+//       code = trunc(x / scale + 0.5 * sign(x))          (F14)
+//   q16 = fp16(bf16(x)); km = bf16 mean of k over the sequence (optional);
+//   k16 = fp16(bf16(k - km)); v16 = fp16(v)
+//   per query head: the clamped vertical indices sorted ascending (vert) and
+//   the other positions of [0, N - W) ascending (rest); rest keys are
+//   re-quantised to int8 per 64-entry block of the rest list (sm = 1).
+//   For query block b (128 rows) with window start wla(b) = floor64(max(0,
+//   128 b - (W - 1))), one base-2 online softmax runs over
+//     rest entries < wla:  s = (q8 . k8) * (q_scale * k_scale)
+//     vert entries < wla:  s = q16 . k16
+//     keys wla <= j <= i:  s = q16 . k16                (causal, F13)
+//   and O = sum p v16 / sum p, written as bf16.
+//
+// Launch sequence of hyq_prefill_hybrid (all on the caller's stream):
+//   kv_stats_kernel / kv_final_kernel   per-channel K sum (fp64, fixed order)
+//                                        -> km; per-channel |V| max (fp8 V scale)
+//   kv_convert_kernel                   k16, v16 (and fp8 V) per KV head
+//   lists_kernel                         per query head: sorted vertical list,
+//                                        rest list, per-block counts (nr, nv)
+//   gather_kernel                        rest K -> int8 per 64-block (+ scale),
+//                                        rest V and vertical K/V rows per head
+//   prefill_main_kernel                  one workgroup per (query block, head)
+//
+// prefill_main_kernel: 4 wavefronts, wavefront w owns query rows 32w..32w+31
+// of the block as two 16-row sub-blocks (sb).  Q is quantised in the kernel
+// (the workgroup is exactly one 128-row scale block) and kept in registers
+// as MFMA B operands.  Keys stream through LDS in 64-key tiles, double
+// buffered, one barrier per tile; the next tile's global loads are in flight
+// while the current one is computed.  Per tile and wavefront:
+//   S^T = K . Q^T   rest tiles: v_mfma_i32_16x16x64_i8 (16 per tile),
+//                   vert/window tiles: v_mfma_f32_16x16x32_f16 (32 per tile);
+//                   output lane (c, g) holds keys 16kb + 4g + r of query c.
+//   softmax         lazy running max (raised only when a tile exceeds it by
+//                   more than 8 in log2 units), p = exp2(s - m).
+//   O^T = V^T . P^T v_mfma_f32_16x16x32_f16 (32 per tile); V is transposed
+//                   into LDS with the key permutation
+//                   pos(16kb + 4g + r) = 32(kb/2) + 8g + 4(kb%2) + r, so the
+//                   eight keys whose p a lane holds are one 16-byte LDS read.
+// Accumulation is fp32 throughout (the reference accumulates each 64-key
+// P.V product in fp16).
+#include "hyq_common.h"
+
+#include <algorithm>
+#include <cmath>
+#include <string>
+
+namespace hyq {
+namespace {
+
+constexpr int PD = 128;                  // head_dim
+constexpr int BM = 128;                  // query rows per block (Q scale block)
+constexpr int BN = 64;                   // keys per tile (rest-K scale block)
+constexpr int PF_THREADS = 256;
+constexpr int KSTR8 = 144;               // LDS row stride of an int8 K tile (bytes)
+constexpr int KSTR16 = 272;              // LDS row stride of an fp16 K tile
+constexpr int VSTR = 144;                // LDS row stride of the V^T tile (64 fp16 keys + pad)
+constexpr int KBUF = BN * KSTR16;
+constexpr int VBUF = PD * VSTR;
+constexpr float PF_SLACK = 8.0f;
+constexpr float PF_M_INIT = -1.0e30f;
+constexpr float FP8_MAX = 448.0f;        // src/ops/sage_unified_fp8.py:44
+constexpr int LIST_THREADS = 1024;
+constexpr int MAX_T = 8192;              // vertical indices per head
+constexpr int64_t MAX_P = 131072;        // prefix positions N - W per head
+constexpr int STAT_ROWS = 128;           // rows per kv_stats chunk
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+enum : int { T_REST = 0, T_VERT = 1, T_WIN = 2 };
+
+__device__ __forceinline__ int window_start(int blk, int W) {
+    const int x = BM * blk - (W - 1);
+    return (x > 0 ? x : 0) / BN * BN;
+}
+
+// quant_per_block_int8_kernel's rounding (quant_per_block.py:40-45): IEEE
+// fp32 division, +-0.5 added in fp32, truncation toward zero.  A zero block
+// (scale 0) gives code 0.
+__device__ __forceinline__ int pb_code(float x, float scale) {
+    if (!(scale > 0.0f)) return 0;
+    float r = x / scale;
+    r = r + (r >= 0.0f ? 0.5f : -0.5f);
+    return static_cast<int>(r);
+}
+
+__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
+    return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
+           ((static_cast<uint32_t>(c) & 0xffu) << 16) | (static_cast<uint32_t>(d) << 24);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    const f16x2 v = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float bf16_round_f32(float x) { return bf16_to_f32(f32_to_bf16_rne(x)); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+// max / sum over the four lanes c, c+16, c+32, c+48 (gfx950 row swaps)
+__device__ __forceinline__ float quad_max(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// OCP e4m3 (gfx950 conversion, RNE), saturated to +-448 first
+__device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d) {
+    auto cl = [](float x) { return fminf(fmaxf(x, -FP8_MAX), FP8_MAX); };
+    int r = __builtin_amdgcn_cvt_pk_fp8_f32(cl(a), cl(b), 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(cl(c), cl(d), r, true);
+    return static_cast<uint32_t>(r);
+}
+
+// ---------------------------------------------------------------------------
+// K mean / V max statistics
+// ---------------------------------------------------------------------------
+
+// grid (ceil(N / 128), B*HKV); thread t: channels 2(t%64), 2(t%64)+1, rows
+// chunk*128 + t/64 + 4i.  Partial sums are float64 and reduced in a fixed
+// order, so km does not depend on scheduling.
+__global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restrict__ k, int64_t k_b, int64_t k_h,
+                                                       int64_t k_n, const uint16_t* __restrict__ v, int64_t v_b,
+                                                       int64_t v_h, int64_t v_n, int HKV, int N, int nch,
+                                                       double* __restrict__ kpart, float* __restrict__ vpart) {
+    __shared__ double s_sum[4][PD];
+    __shared__ float s_max[4][PD];
+    const int bhk = blockIdx.y, b = bhk / HKV, hk = bhk % HKV;
+    const int chunk = blockIdx.x;
+    const int cp = threadIdx.x & 63, ph = threadIdx.x >> 6;
+    const uint16_t* kb = k + b * k_b + hk * k_h + 2 * cp;
+    const uint16_t* vb = v + b * v_b + hk * v_h + 2 * cp;
+    double s0 = 0.0, s1 = 0.0;
+    float m0 = 0.0f, m1 = 0.0f;
+    const int r_end = min(N, (chunk + 1) * STAT_ROWS);
+    for (int r = chunk * STAT_ROWS + ph; r < r_end; r += 4) {
+        const uint32_t kk = *reinterpret_cast<const uint32_t*>(kb + r * k_n);
+        const uint32_t vv = *reinterpret_cast<const uint32_t*>(vb + r * v_n);
+        s0 += static_cast<double>(bf16_to_f32(static_cast<uint16_t>(kk)));
+        s1 += static_cast<double>(bf16_to_f32(static_cast<uint16_t>(kk >> 16)));
+        m0 = fmaxf(m0, fabsf(bf16_to_f32(static_cast<uint16_t>(vv))));
+        m1 = fmaxf(m1, fabsf(bf16_to_f32(static_cast<uint16_t>(vv >> 16))));
+    }
+    s_sum[ph][2 * cp] = s0;
+    s_sum[ph][2 * cp + 1] = s1;
+    s_max[ph][2 * cp] = m0;
+    s_max[ph][2 * cp + 1] = m1;
+    __syncthreads();
+    if (threadIdx.x < PD) {
+        const int ch = threadIdx.x;
+        const double s = ((s_sum[0][ch] + s_sum[1][ch]) + s_sum[2][ch]) + s_sum[3][ch];
+        const float m = fmaxf(fmaxf(s_max[0][ch], s_max[1][ch]), fmaxf(s_max[2][ch], s_max[3][ch]));
+        kpart[(static_cast<int64_t>(bhk) * nch + chunk) * PD + ch] = s;
+        vpart[(static_cast<int64_t>(bhk) * nch + chunk) * PD + ch] = m;
+    }
+}
+
+// grid (B*HKV), 128 threads: km = bf16(sum / N) (one rounding of the float64
+// quotient), fp8 V scale = max|v| / 448.
+__global__ __launch_bounds__(128) void kv_final_kernel(const double* __restrict__ kpart,
+                                                       const float* __restrict__ vpart, int nch, int N, int smooth,
+                                                       uint16_t* __restrict__ km, float* __restrict__ vscale) {
+    const int bhk = blockIdx.x, ch = threadIdx.x;
+    double s = 0.0;
+    float m = 0.0f;
+    for (int i = 0; i < nch; ++i) {
+        s += kpart[(static_cast<int64_t>(bhk) * nch + i) * PD + ch];
+        m = fmaxf(m, vpart[(static_cast<int64_t>(bhk) * nch + i) * PD + ch]);
+    }
+    km[bhk * PD + ch] = smooth ? f64_to_bf16_rne(s / static_cast<double>(N)) : static_cast<uint16_t>(0);
+    vscale[bhk * PD + ch] = m / FP8_MAX;
+}
+
+// grid (ceil(N*16 / 256), B*HKV): thread = 8 channels of one row.
+//   k16 = fp16(bf16(k - km)), v16 = fp16(v), v8 = e4m3(v / vscale) (fp8 PV)
+__global__ __launch_bounds__(256) void kv_convert_kernel(const uint16_t* __restrict__ k, int64_t k_b, int64_t k_h,
+                                                         int64_t k_n, const uint16_t* __restrict__ v, int64_t v_b,
+                                                         int64_t v_h, int64_t v_n, int HKV, int N,
+                                                         const uint16_t* __restrict__ km,
+                                                         const float* __restrict__ vscale, uint16_t* __restrict__ k16,
+                                                         uint16_t* __restrict__ v16, uint8_t* __restrict__ v8) {
+    const int bhk = blockIdx.y, b = bhk / HKV, hk = bhk % HKV;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t row = idx >> 4;
+    const int co = static_cast<int>(idx & 15);
+    if (row >= N) return;
+    const u32x4 kk = *reinterpret_cast<const u32x4*>(k + b * k_b + hk * k_h + row * k_n + 8 * co);
+    const u32x4 vv = *reinterpret_cast<const u32x4*>(v + b * v_b + hk * v_h + row * v_n + 8 * co);
+    float kf[8], vf[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t kw = kk[e >> 1], vw = vv[e >> 1];
+        kf[e] = bf16_to_f32(static_cast<uint16_t>((e & 1) ? (kw >> 16) : kw));
+        vf[e] = bf16_to_f32(static_cast<uint16_t>((e & 1) ? (vw >> 16) : vw));
+        kf[e] = bf16_round_f32(kf[e] - bf16_to_f32(km[bhk * PD + 8 * co + e]));
+    }
+    const int64_t o = (static_cast<int64_t>(bhk) * N + row) * PD + 8 * co;
+    const u32x4 ko = {pack_f16x2(kf[0], kf[1]), pack_f16x2(kf[2], kf[3]), pack_f16x2(kf[4], kf[5]),
+                      pack_f16x2(kf[6], kf[7])};
+    const u32x4 vo = {pack_f16x2(vf[0], vf[1]), pack_f16x2(vf[2], vf[3]), pack_f16x2(vf[4], vf[5]),
+                      pack_f16x2(vf[6], vf[7])};
+    *reinterpret_cast<u32x4*>(k16 + o) = ko;
+    *reinterpret_cast<u32x4*>(v16 + o) = vo;
+    if (v8 != nullptr) {
+        float q[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float s = vscale[bhk * PD + 8 * co + e];
+            q[e] = s > 0.0f ? vf[e] / s : 0.0f;
+        }
+        const u32x2 p = {pack_e4m3x4(q[0], q[1], q[2], q[3]), pack_e4m3x4(q[4], q[5], q[6], q[7])};
+        *reinterpret_cast<u32x2*>(v8 + o) = p;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// rest / vertical lists (reorder_kv_for_vertical, sage_unified.py:499-547)
+// ---------------------------------------------------------------------------
+
+__device__ int block_exclusive_scan(int v, int* s_w) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) s_w[w] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int acc = 0;
+        for (int i = 0; i < nw; ++i) {
+            const int t = s_w[i];
+            s_w[i] = acc;
+            acc += t;
+        }
+        s_w[nw] = acc;
+    }
+    __syncthreads();
+    return s_w[w] + x - v;
+}
+
+// grid (B*HQ), 1024 threads.  Dynamic LDS: sorted list [n2], bitmap [nw],
+// rest count before each word [nw], scan scratch [32].
+__global__ __launch_bounds__(LIST_THREADS) void lists_kernel(const int64_t* __restrict__ vidx, int64_t vi_b,
+                                                             int64_t vi_h, int64_t vi_t, int HQ, int T, int n2,
+                                                             int P, int nblk, int W, int32_t* __restrict__ vert,
+                                                             int32_t* __restrict__ rest, int32_t* __restrict__ rcount,
+                                                             int32_t* __restrict__ nr, int32_t* __restrict__ nv) {
+    extern __shared__ int s_lists[];
+    const int nw = (P + 31) >> 5;
+    int* s_sort = s_lists;
+    uint32_t* s_bm = reinterpret_cast<uint32_t*>(s_lists + n2);
+    int* s_pre = s_lists + n2 + nw;
+    int* s_scan = s_pre + nw;
+    const int bh = blockIdx.x, b = bh / HQ, h = bh % HQ;
+    const int tid = threadIdx.x;
+    const int64_t* vrow = vidx + b * vi_b + h * vi_h;
+    for (int i = tid; i < n2; i += LIST_THREADS) {
+        int x = 0x7fffffff;
+        if (i < T) {
+            const int64_t y = vrow[i * vi_t];
+            x = static_cast<int>(y < 0 ? 0 : (y > P - 1 ? P - 1 : y));
+        }
+        s_sort[i] = x;
+    }
+    for (int i = tid; i < nw; i += LIST_THREADS) s_bm[i] = 0u;
+    __syncthreads();
+    for (int kk = 2; kk <= n2; kk <<= 1) {
+        for (int j = kk >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < n2; i += LIST_THREADS) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const int a = s_sort[i], c = s_sort[ixj];
+                    if ((a > c) == ((i & kk) == 0)) {
+                        s_sort[i] = c;
+                        s_sort[ixj] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    int32_t* vout = vert + static_cast<int64_t>(bh) * T;
+    for (int i = tid; i < T; i += LIST_THREADS) {
+        const int x = s_sort[i];
+        vout[i] = x;
+        atomicOr(&s_bm[x >> 5], 1u << (x & 31));
+    }
+    __syncthreads();
+    // compaction of the unset bits of [0, P) in ascending order
+    const int per = (nw + LIST_THREADS - 1) / LIST_THREADS;
+    const int w0 = min(nw, tid * per), w1 = min(nw, w0 + per);
+    auto free_bits = [&](int wi) {
+        uint32_t m = ~s_bm[wi];
+        const int tail = P - 32 * wi;
+        if (tail < 32) m &= (1u << tail) - 1u;
+        return m;
+    };
+    int cnt = 0;
+    for (int wi = w0; wi < w1; ++wi) cnt += __popc(free_bits(wi));
+    int off = block_exclusive_scan(cnt, s_scan);
+    const int total = s_scan[LIST_THREADS >> 6];
+    int32_t* rout = rest + static_cast<int64_t>(bh) * P;
+    for (int wi = w0; wi < w1; ++wi) {
+        s_pre[wi] = off;
+        uint32_t m = free_bits(wi);
+        while (m) {
+            const int bit = __ffs(m) - 1;
+            m &= m - 1u;
+            rout[off++] = 32 * wi + bit;
+        }
+    }
+    if (tid == 0) rcount[bh] = total;
+    __syncthreads();
+    for (int blk = tid; blk < nblk; blk += LIST_THREADS) {
+        const int wla = window_start(blk, W);
+        int lo = 0, hi = T;                      // first entry >= wla
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (s_sort[mid] < wla) lo = mid + 1; else hi = mid;
+        }
+        const int wl = min(wla, P);
+        int r;
+        if (wl >= P) {
+            r = total;
+        } else {
+            const int wi = wl >> 5, sh = wl & 31;
+            r = s_pre[wi] + __popc(free_bits(wi) & ((1u << sh) - 1u));
+        }
+        nv[static_cast<int64_t>(bh) * nblk + blk] = lo;
+        nr[static_cast<int64_t>(bh) * nblk + blk] = r;
+    }
+}
+
+// grid (nsb + nvb, B*HQ), 256 threads.  Blocks [0, nsb): 64 entries of the
+// rest list -> int8 K (per-64 block scale, sm = 1) and V rows (fp16 or fp8);
+// blocks [nsb, nsb + nvb): 64 entries of the vertical list -> fp16 K and V.
+// Thread t: row t/4 of the block, channels 32(t%4) .. +31.
+__global__ __launch_bounds__(256) void gather_kernel(
+    const uint16_t* __restrict__ k16, const uint16_t* __restrict__ v16, const uint8_t* __restrict__ v8, int HQ,
+    int G, int HKV, int N, int P, int T, int nsb, const int32_t* __restrict__ rest,
+    const int32_t* __restrict__ rcount, const int32_t* __restrict__ vert, int8_t* __restrict__ k8r,
+    float* __restrict__ k8r_scale, uint8_t* __restrict__ vr, uint16_t* __restrict__ kv16,
+    uint16_t* __restrict__ vv16) {
+    __shared__ float s_amax[4];
+    const int bh = blockIdx.y, b = bh / HQ, h = bh % HQ;
+    const int64_t bhk = static_cast<int64_t>(b) * HKV + h / G;
+    const int tid = threadIdx.x, r = tid >> 2, qq = tid & 3;
+    if (static_cast<int>(blockIdx.x) < nsb) {
+        const int rc = rcount[bh];
+        const int base = blockIdx.x * BN;
+        if (base >= rc) return;                                 // uniform per block
+        const int cnt = min(BN, rc - base);
+        const bool ok = r < cnt;
+        u32x4 kk[4] = {};
+        if (ok) {
+            const int pos = rest[static_cast<int64_t>(bh) * P + base + r];
+            const uint16_t* src = k16 + (bhk * N + pos) * PD + 32 * qq;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kk[i] = reinterpret_cast<const u32x4*>(src)[i];
+            const int64_t dst = (static_cast<int64_t>(bh) * P + base + r) * PD;
+            if (v8 != nullptr) {
+                const u32x4* vs = reinterpret_cast<const u32x4*>(v8 + (bhk * N + pos) * PD + 32 * qq);
+                u32x4* vd = reinterpret_cast<u32x4*>(vr + dst + 32 * qq);
+                vd[0] = vs[0];
+                vd[1] = vs[1];
+            } else {
+                const u32x4* vs = reinterpret_cast<const u32x4*>(v16 + (bhk * N + pos) * PD + 32 * qq);
+                u32x4* vd = reinterpret_cast<u32x4*>(vr + 2 * (dst + 32 * qq));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) vd[i] = vs[i];
+            }
+        }
+        float x[32];
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const uint32_t wv = kk[e >> 3][(e >> 1) & 3];
+            x[e] = f16_bits_to_f32(static_cast<uint16_t>((e & 1) ? (wv >> 16) : wv));
+            amax = fmaxf(amax, fabsf(x[e]));
+        }
+        amax = wave_max(amax);
+        if ((tid & 63) == 0) s_amax[tid >> 6] = amax;
+        __syncthreads();
+        amax = fmaxf(fmaxf(s_amax[0], s_amax[1]), fmaxf(s_amax[2], s_amax[3]));
+        const float scale = amax / 127.0f;
+        if (tid == 0) k8r_scale[static_cast<int64_t>(bh) * nsb + blockIdx.x] = scale;
+        if (ok) {
+            uint32_t wds[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                wds[i] = pack4_i8(pb_code(x[4 * i], scale), pb_code(x[4 * i + 1], scale),
+                                  pb_code(x[4 * i + 2], scale), pb_code(x[4 * i + 3], scale));
+            u32x4* dst = reinterpret_cast<u32x4*>(k8r + (static_cast<int64_t>(bh) * P + base + r) * PD + 32 * qq);
+            dst[0] = u32x4{wds[0], wds[1], wds[2], wds[3]};
+            dst[1] = u32x4{wds[4], wds[5], wds[6], wds[7]};
+        }
+    } else {
+        const int base = (blockIdx.x - nsb) * BN;
+        if (base + r >= T) return;
+        const int pos = vert[static_cast<int64_t>(bh) * T + base + r];
+        const u32x4* ks = reinterpret_cast<const u32x4*>(k16 + (bhk * N + pos) * PD + 32 * qq);
+        const u32x4* vs = reinterpret_cast<const u32x4*>(v16 + (bhk * N + pos) * PD + 32 * qq);
+        const int64_t dst = (static_cast<int64_t>(bh) * T + base + r) * PD + 32 * qq;
+        u32x4* kd = reinterpret_cast<u32x4*>(kv16 + dst);
+        u32x4* vd = reinterpret_cast<u32x4*>(vv16 + dst);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            kd[i] = ks[i];
+            vd[i] = vs[i];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// per-block int8 quantiser (per_block_int8, quant_per_block.py:49-101)
+// ---------------------------------------------------------------------------
+
+// grid (ceil(L / blk), H, B), 256 threads; thread t handles channels
+// 8(t%16)..+7 of rows t/16, t/16 + 16, ...  x = fp32(bf16(in - km)) * sm
+// (km optional; in bf16 or fp16).
+__global__ __launch_bounds__(256) void per_block_int8_kernel(const uint16_t* __restrict__ in, int is_fp16,
+                                                             int64_t i_b, int64_t i_h, int64_t i_n, int L, int blk,
+                                                             float sm, const uint16_t* __restrict__ km,
+                                                             int64_t km_b, int64_t km_h, int8_t* __restrict__ out,
+                                                             int64_t o_b, int64_t o_h, int64_t o_n,
+                                                             float* __restrict__ scale, int64_t s_b, int64_t s_h) {
+    __shared__ float s_amax[4];
+    const int bi = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, co = tid & 15, r0 = tid >> 4;
+    const uint16_t* src = in + b * i_b + h * i_h + 8 * co;
+    float kmv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kmv[e] = km ? bf16_to_f32(km[b * km_b + h * km_h + 8 * co + e]) : 0.0f;
+    float amax = 0.0f;
+    const int row_end = min(L, (bi + 1) * blk);
+    auto value = [&](uint32_t w, int e) {
+        const uint16_t bits = static_cast<uint16_t>((e & 1) ? (w >> 16) : w);
+        float x = is_fp16 ? f16_bits_to_f32(bits) : bf16_to_f32(bits);
+        if (km) x = bf16_round_f32(x - kmv[e]);
+        return x * sm;
+    };
+    for (int r = bi * blk + r0; r < row_end; r += 16) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(src + r * i_n);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(value(w[e >> 1], e)));
+    }
+    amax = wave_max(amax);
+    if ((tid & 63) == 0) s_amax[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(s_amax[0], s_amax[1]), fmaxf(s_amax[2], s_amax[3]));
+    const float sc = amax / 127.0f;
+    if (tid == 0) scale[b * s_b + h * s_h + bi] = sc;
+    for (int r = bi * blk + r0; r < row_end; r += 16) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(src + r * i_n);
+        int c[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) c[e] = pb_code(value(w[e >> 1], e), sc);
+        const u32x2 o = {pack4_i8(c[0], c[1], c[2], c[3]), pack4_i8(c[4], c[5], c[6], c[7])};
+        *reinterpret_cast<u32x2*>(out + b * o_b + h * o_h + r * o_n + 8 * co) = o;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// main attention kernel
+// ---------------------------------------------------------------------------
+
+struct PfArgs {
+    const uint16_t* q; int64_t q_b, q_h, q_n;
+    uint16_t* out; int64_t o_b, o_h, o_n;
+    const int8_t* k8r; const float* k8r_scale; const uint16_t* vr;   // rest, per query head [BH][P][128]
+    const uint16_t* kv16; const uint16_t* vv16;                      // vertical, per query head [BH][T][128]
+    const uint16_t* k16; const uint16_t* v16;                        // window source, per KV head [BHK][N][128]
+    const int32_t* nr; const int32_t* nv;                            // [BH][nblk]
+    int B, HQ, HKV, N, nblk, W, P, T, nsb;
+    float c;                                                          // fp32(sm_scale * log2e)
+    int total, per_xcd;
+};
+
+__device__ __forceinline__ f32x4 mfma_f16(const f16x8& a, const f16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ i32x4 mfma_i8(const i32x4& a, const i32x4& b, const i32x4& c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+struct TileDesc {
+    int kind;
+    int idx0;      // first list entry (rest / vert) or first key (window)
+    int valid;     // rest / vert: entries of the list below wla; window: end key (exclusive)
+    float sc;      // rest: q_scale * k_scale
+};
+
+__global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_k[2][KBUF];
+    __shared__ __attribute__((aligned(16))) uint8_t s_v[2][VBUF];
+    __shared__ float s_red[4];
+
+    // XCD-aware order: consecutive items (same head, heaviest block first) land on one XCD
+    const int wg = blockIdx.x;
+    const int item = (wg & 7) * a.per_xcd + (wg >> 3);
+    if (item >= a.total) return;
+    const int bh = item / a.nblk;
+    const int blk = a.nblk - 1 - (item - bh * a.nblk);
+    const int b = bh / a.HQ, h = bh - b * a.HQ;
+    const int G = a.HQ / a.HKV;
+    const int64_t bhk = static_cast<int64_t>(b) * a.HKV + h / G;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int c16 = lane & 15, g = lane >> 4;
+
+    // ---- Q block: load, quantise (int8 per block scale), fp16 copy --------
+    float x[2][2][16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+        const int row = BM * blk + 32 * w + 16 * sb + c16;
+        const bool ok = row < a.N;
+        const uint16_t* qrow = a.q + b * a.q_b + h * a.q_h + static_cast<int64_t>(ok ? row : 0) * a.q_n;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            u32x4 lo = {}, hi = {};
+            if (ok) {
+                lo = *reinterpret_cast<const u32x4*>(qrow + 64 * cc + 16 * g);
+                hi = *reinterpret_cast<const u32x4*>(qrow + 64 * cc + 16 * g + 8);
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t wd = (e < 8) ? lo[e >> 1] : hi[(e - 8) >> 1];
+                const float v = bf16_to_f32(static_cast<uint16_t>((e & 1) ? (wd >> 16) : wd)) * a.c;
+                x[sb][cc][e] = v;
+                amax = fmaxf(amax, fabsf(v));
+            }
+        }
+    }
+    amax = wave_max(amax);
+    if (lane == 0) s_red[w] = amax;
+    __syncthreads();
+    const float q_scale = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3])) / 127.0f;
+    i32x4 q8[2][2];
+    f16x8 qh[2][4];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const float* xv = x[sb][cc];
+            uint32_t wd[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                wd[i] = pack4_i8(pb_code(xv[4 * i], q_scale), pb_code(xv[4 * i + 1], q_scale),
+                                 pb_code(xv[4 * i + 2], q_scale), pb_code(xv[4 * i + 3], q_scale));
+            q8[sb][cc] = i32x4{static_cast<int>(wd[0]), static_cast<int>(wd[1]), static_cast<int>(wd[2]),
+                               static_cast<int>(wd[3])};
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const float* z = xv + 8 * hf;
+                const u32x4 hv = {pack_f16x2(bf16_round_f32(z[0]), bf16_round_f32(z[1])),
+                                  pack_f16x2(bf16_round_f32(z[2]), bf16_round_f32(z[3])),
+                                  pack_f16x2(bf16_round_f32(z[4]), bf16_round_f32(z[5])),
+                                  pack_f16x2(bf16_round_f32(z[6]), bf16_round_f32(z[7]))};
+                qh[sb][2 * cc + hf] = __builtin_bit_cast(f16x8, hv);
+            }
+        }
+    }
+
+    // ---- tile schedule -------------------------------------------------------
+    const int nr_b = a.nr[static_cast<int64_t>(bh) * a.nblk + blk];
+    const int nv_b = a.nv[static_cast<int64_t>(bh) * a.nblk + blk];
+    const int wla = window_start(blk, a.W);
+    const int wend = min(a.N, BM * (blk + 1));
+    const int nrt = (nr_b + BN - 1) / BN;
+    const int nvt = (nv_b + BN - 1) / BN;
+    const int nwt = (wend - wla + BN - 1) / BN;
+    const int ntiles = nrt + nvt + nwt;
+    const float* ksc_row = a.k8r_scale + static_cast<int64_t>(bh) * a.nsb;
+
+    auto describe = [&](int t) {
+        TileDesc d;
+        if (t < nrt) {
+            d.kind = T_REST; d.idx0 = BN * t; d.valid = nr_b; d.sc = q_scale * ksc_row[t];
+        } else if (t < nrt + nvt) {
+            d.kind = T_VERT; d.idx0 = BN * (t - nrt); d.valid = nv_b; d.sc = 1.0f;
+        } else {
+            d.kind = T_WIN; d.idx0 = wla + BN * (t - nrt - nvt); d.valid = wend; d.sc = 1.0f;
+        }
+        return d;
+    };
+
+    // global -> register staging of one tile (K: 2 or 4 x 16 B, V: 4 x 16 B per thread)
+    u32x4 kr[4], vr[4];
+    auto load_tile = [&](const TileDesc& d) {
+        if (d.kind == T_REST) {
+            const int8_t* base = a.k8r + static_cast<int64_t>(bh) * a.P * PD + 16 * (tid & 7);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int e = min(d.idx0 + (tid >> 3) + 32 * i, d.valid - 1);
+                kr[i] = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(e) * PD);
+            }
+        } else {
+            const uint16_t* base = (d.kind == T_VERT ? a.kv16 + static_cast<int64_t>(bh) * a.T * PD
+                                                     : a.k16 + bhk * a.N * PD) + 8 * (tid & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = min(d.idx0 + (tid >> 4) + 16 * i, d.valid - 1);
+                kr[i] = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(e) * PD);
+            }
+        }
+        const uint16_t* vbase = (d.kind == T_REST ? a.vr + static_cast<int64_t>(bh) * a.P * PD
+                                 : d.kind == T_VERT ? a.vv16 + static_cast<int64_t>(bh) * a.T * PD
+                                                    : a.v16 + bhk * a.N * PD) + 8 * (tid & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int e = min(d.idx0 + 4 * (tid >> 4) + r, d.valid - 1);
+            vr[r] = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(e) * PD);
+        }
+    };
+    auto store_tile = [&](const TileDesc& d, int buf) {
+        uint8_t* kb = s_k[buf];
+        if (d.kind == T_REST) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                *reinterpret_cast<u32x4*>(kb + ((tid >> 3) + 32 * i) * KSTR8 + 16 * (tid & 7)) = kr[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<u32x4*>(kb + ((tid >> 4) + 16 * i) * KSTR16 + 16 * (tid & 15)) = kr[i];
+        }
+        // V^T with the key permutation: keys 4kq..4kq+3 land at pos..pos+3
+        const int kq = tid >> 4, co = tid & 15;
+        const int kb4 = kq >> 2, gg = kq & 3;
+        const int pos = 32 * (kb4 >> 1) + 8 * gg + 4 * (kb4 & 1);
+        uint8_t* vb = s_v[buf] + 2 * pos;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+            const int dd = e >> 1;
+            const u32x2 t2 = {__builtin_amdgcn_perm(vr[1][dd], vr[0][dd], sel),
+                              __builtin_amdgcn_perm(vr[3][dd], vr[2][dd], sel)};
+            *reinterpret_cast<u32x2*>(vb + (8 * co + e) * VSTR) = t2;
+        }
+    };
+
+    float m_run[2] = {PF_M_INIT, PF_M_INIT};
+    float l_run[2] = {0.0f, 0.0f};
+    f32x4 acc[2][8];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) acc[sb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    TileDesc cur = describe(0);
+    load_tile(cur);
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        store_tile(cur, buf);
+        __syncthreads();
+        const TileDesc d = cur;
+        if (t + 1 < ntiles) {
+            cur = describe(t + 1);
+            load_tile(cur);
+        }
+        const uint8_t* kb = s_k[buf];
+        const uint8_t* vb = s_v[buf];
+
+        // ---- S^T = K . Q^T --------------------------------------------------
+        float s[2][4][4];
+        bool masked;
+        if (d.kind == T_REST) {
+            i32x4 si[2][4];
+#pragma unroll
+            for (int kbk = 0; kbk < 4; ++kbk) {
+                const uint8_t* row = kb + (16 * kbk + c16) * KSTR8 + 16 * g;
+                const i32x4 a0 = *reinterpret_cast<const i32x4*>(row);
+                const i32x4 a1 = *reinterpret_cast<const i32x4*>(row + 64);
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    si[sb][kbk] = mfma_i8(a0, q8[sb][0], i32x4{0, 0, 0, 0});
+                    si[sb][kbk] = mfma_i8(a1, q8[sb][1], si[sb][kbk]);
+                }
+            }
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s[sb][kbk][r] = static_cast<float>(si[sb][kbk][r]) * d.sc;
+            masked = d.idx0 + BN > d.valid;
+        } else {
+            f32x4 sf[2][4];
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk) sf[sb][kbk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kbk = 0; kbk < 4; ++kbk) {
+                const uint8_t* row = kb + (16 * kbk + c16) * KSTR16 + 32 * g;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const f16x8 av = *reinterpret_cast<const f16x8*>(row + 128 * (m >> 1) + 16 * (m & 1));
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb) sf[sb][kbk] = mfma_f16(av, qh[sb][m], sf[sb][kbk]);
+                }
+            }
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s[sb][kbk][r] = sf[sb][kbk][r];
+            if (d.kind == T_VERT)
+                masked = d.idx0 + BN > d.valid;
+            else  // window: causal against this wavefront's first row, or past N
+                masked = d.idx0 + BN - 1 > BM * blk + 32 * w || d.idx0 + BN > d.valid;
+        }
+        if (masked) {
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                const int row = BM * blk + 32 * w + 16 * sb + c16;
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int e = d.idx0 + 16 * kbk + 4 * g + r;
+                        const bool ok = (d.kind == T_WIN) ? (e < d.valid && e <= row) : (e < d.valid);
+                        if (!ok) s[sb][kbk][r] = -INFINITY;
+                    }
+            }
+        }
+
+        // ---- online softmax (lazy max) and P -> fp16 -------------------------
+        f16x8 pf[2][2];
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            float mx = s[sb][0][0];
+#pragma unroll
+            for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[sb][kbk][r]);
+            mx = quad_max(mx);
+            if (__builtin_amdgcn_ballot_w64(mx > m_run[sb] + PF_SLACK)) {
+                const float mnew = fmaxf(m_run[sb], mx);
+                const float alpha = __builtin_amdgcn_exp2f(m_run[sb] - mnew);
+                l_run[sb] *= alpha;
+#pragma unroll
+                for (int cb = 0; cb < 8; ++cb) acc[sb][cb] *= alpha;
+                m_run[sb] = mnew;
+            }
+            float p[4][4];
+            float ls = 0.0f;
+#pragma unroll
+            for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    p[kbk][r] = __builtin_amdgcn_exp2f(s[sb][kbk][r] - m_run[sb]);
+                    ls += p[kbk][r];
+                }
+            l_run[sb] += ls;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const u32x4 pv = {pack_f16x2(p[2 * j][0], p[2 * j][1]), pack_f16x2(p[2 * j][2], p[2 * j][3]),
+                                  pack_f16x2(p[2 * j + 1][0], p[2 * j + 1][1]),
+                                  pack_f16x2(p[2 * j + 1][2], p[2 * j + 1][3])};
+                pf[sb][j] = __builtin_bit_cast(f16x8, pv);
+            }
+        }
+
+        // ---- O^T += V^T . P^T -------------------------------------------------
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const f16x8 av = *reinterpret_cast<const f16x8*>(vb + (16 * cb + c16) * VSTR + 64 * j + 16 * g);
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) acc[sb][cb] = mfma_f16(av, pf[sb][j], acc[sb][cb]);
+            }
+        }
+    }
+
+    // ---- epilogue: O = acc / l --------------------------------------------------
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+        const float l = quad_sum(l_run[sb]);
+        const float inv = 1.0f / l;
+        const int row = BM * blk + 32 * w + 16 * sb + c16;
+        if (row < a.N) {
+            uint16_t* orow = a.out + b * a.o_b + h * a.o_h + static_cast<int64_t>(row) * a.o_n;
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb) {
+                const u32x2 o = {pack_bf16x2(acc[sb][cb][0] * inv, acc[sb][cb][1] * inv),
+                                 pack_bf16x2(acc[sb][cb][2] * inv, acc[sb][cb][3] * inv)};
+                *reinterpret_cast<u32x2*>(orow + 16 * cb + 4 * g) = o;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void zero_counts_kernel(int32_t* __restrict__ nr, int32_t* __restrict__ nv,
+                                                          int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) nr[i] = 0;
+    else if (i < 2 * n) nv[i - n] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+struct PrefillLayout {
+    size_t kpart, vpart, km, vscale, k16, v16, v8, vert, rest, rcount, nr, nv, k8r, k8r_scale, vr, kv16, vv16, total;
+};
+
+PrefillLayout prefill_layout(int B, int HQ, int HKV, int64_t N, int64_t T, int W, int pv_mode) {
+    const int64_t P = std::max<int64_t>(0, N - W);
+    const int64_t nblk = (N + BM - 1) / BM;
+    const int64_t nch = (N + STAT_ROWS - 1) / STAT_ROWS;
+    const int64_t nsb = (P + BN - 1) / BN;
+    const int64_t BH = static_cast<int64_t>(B) * HQ, BHK = static_cast<int64_t>(B) * HKV;
+    PrefillLayout L{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off += align256(std::max<size_t>(bytes, 1)); return o; };
+    L.kpart = take(BHK * nch * PD * 8);
+    L.vpart = take(BHK * nch * PD * 4);
+    L.km = take(BHK * PD * 2);
+    L.vscale = take(BHK * PD * 4);
+    L.k16 = take(BHK * N * PD * 2);
+    L.v16 = take(BHK * N * PD * 2);
+    L.v8 = pv_mode ? take(BHK * N * PD) : 0;
+    L.vert = take(BH * T * 4);
+    L.rest = take(BH * P * 4);
+    L.rcount = take(BH * 4);
+    L.nr = take(BH * nblk * 4);
+    L.nv = take(BH * nblk * 4);
+    L.k8r = take(BH * P * PD);
+    L.k8r_scale = take(BH * nsb * 4);
+    L.vr = take(BH * P * PD * (pv_mode ? 1 : 2));
+    L.kv16 = take(BH * T * PD * 2);
+    L.vv16 = take(BH * T * PD * 2);
+    L.total = off;
+    return L;
+}
+
+int next_pow2(int x) {
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+int launch_lists(const int64_t* vidx, int64_t vi_b, int64_t vi_h, int64_t vi_t, int BH, int H, int T, int P,
+                 int nblk, int W, int32_t* vert, int32_t* rest, int32_t* rcount, int32_t* nr, int32_t* nv,
+                 hipStream_t stream) {
+    static bool attr_set = false;
+    const int n2 = next_pow2(std::max(T, 1));
+    const int nw = (P + 31) / 32;
+    const size_t lds = sizeof(int) * (static_cast<size_t>(n2) + 2 * nw + 32);
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(lists_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+            return fail(HYQ_EDEVICE, "prefill lists: cannot raise the LDS limit of lists_kernel");
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(lists_kernel, dim3(BH), dim3(LIST_THREADS), lds, stream, vidx, vi_b, vi_h, vi_t, H, T, n2, P,
+                       nblk, W, vert, rest, rcount, nr, nv);
+    return check_launch("lists_kernel");
+}
+
+}  // namespace
+}  // namespace hyq
+
+using namespace hyq;
+
+extern "C" size_t hyq_prefill_workspace_size(int32_t b, int32_t hq, int32_t hkv, int64_t n, int64_t t,
+                                             int32_t window, int32_t pv_mode) {
+    if (b <= 0 || hq <= 0 || hkv <= 0 || n <= 0 || t < 0 || window < 0) return 0;
+    return prefill_layout(b, hq, hkv, n, t, window, pv_mode).total;
+}
+
+extern "C" int hyq_per_block_int8(const void* x, int32_t x_is_fp16, int64_t xs_b, int64_t xs_h, int64_t xs_n,
+                                  int32_t b, int32_t h, int64_t len, int32_t d, float sm, int32_t blk,
+                                  const void* km, int64_t km_b, int64_t km_h, void* out, int64_t os_b, int64_t os_h,
+                                  int64_t os_n, float* scale, int64_t ss_b, int64_t ss_h, void* stream_) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (d != PD) return fail(HYQ_ENOTSUP, "hyq_per_block_int8: head_dim must be 128");
+    if (b < 0 || h < 0 || len < 0 || blk <= 0 || blk > 4096 || len > INT32_MAX)
+        return fail(HYQ_EINVAL, "hyq_per_block_int8: invalid sizes");
+    if (b == 0 || h == 0 || len == 0) return HYQ_OK;
+    if (!x || !out || !scale) return fail(HYQ_EINVAL, "hyq_per_block_int8: null pointer");
+    if (!aligned(x, 16) || (xs_n * 2) % 16 || (xs_h * 2) % 16 || (xs_b * 2) % 16)
+        return fail(HYQ_EINVAL, "hyq_per_block_int8: input rows must be 16-byte aligned");
+    if (!aligned(out, 8) || os_n % 8 || os_h % 8 || os_b % 8)
+        return fail(HYQ_EINVAL, "hyq_per_block_int8: output rows must be 8-byte aligned");
+    const int nb = static_cast<int>((len + blk - 1) / blk);
+    hipLaunchKernelGGL(per_block_int8_kernel, dim3(nb, h, b), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(x), x_is_fp16, xs_b, xs_h, xs_n, static_cast<int>(len), blk, sm,
+                       static_cast<const uint16_t*>(km), km_b, km_h, static_cast<int8_t*>(out), os_b, os_h, os_n,
+                       scale, ss_b, ss_h);
+    return check_launch("per_block_int8_kernel");
+}
+
+extern "C" int hyq_prefill_lists(const int64_t* vidx, int64_t vi_b, int64_t vi_h, int64_t vi_t, int32_t b,
+                                 int32_t h, int64_t n, int64_t t, int32_t window, int32_t* vert, int32_t* rest,
+                                 int32_t* rcount, int32_t* nr, int32_t* nv, void* stream) {
+    if (b < 0 || h < 0 || n < 0 || t < 0 || window < 0 || n > INT32_MAX / 2)
+        return fail(HYQ_EINVAL, "hyq_prefill_lists: invalid sizes");
+    const int64_t P = std::max<int64_t>(0, n - window);
+    if (P > MAX_P) return fail(HYQ_ENOTSUP, "hyq_prefill_lists: n - window exceeds 131072");
+    if (t > MAX_T) return fail(HYQ_ENOTSUP, "hyq_prefill_lists: more than 8192 indices per head");
+    if (b == 0 || h == 0 || n == 0) return HYQ_OK;
+    const int nblk = static_cast<int>((n + BM - 1) / BM);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (P == 0) {
+        if (!nr || !nv) return fail(HYQ_EINVAL, "hyq_prefill_lists: null pointer");
+        hipLaunchKernelGGL(zero_counts_kernel, dim3((2 * b * h * nblk + 255) / 256), dim3(256), 0, s, nr, nv,
+                           b * h * nblk);
+        return check_launch("zero_counts_kernel");
+    }
+    if ((t > 0 && (!vidx || !vert)) || !rest || !rcount || !nr || !nv)
+        return fail(HYQ_EINVAL, "hyq_prefill_lists: null pointer");
+    return launch_lists(vidx, vi_b, vi_h, vi_t, b * h, h, static_cast<int>(t), static_cast<int>(P), nblk, window, vert,
+                        rest, rcount, nr, nv, s);
+}
+
+extern "C" int hyq_prefill_hybrid(const hyq_prefill_params* p, void* ws, size_t ws_bytes, void* stream_) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!p) return fail(HYQ_EINVAL, "hyq_prefill_hybrid: null params");
+    const int B = p->batch, HQ = p->hq, HKV = p->hkv, W = p->window;
+    const int64_t N = p->n, T = p->t;
+    if (p->head_dim != PD) return fail(HYQ_ENOTSUP, "hyq_prefill_hybrid: head_dim must be 128");
+    if (p->pv_mode != 0) return fail(HYQ_ENOTSUP, "hyq_prefill_hybrid: pv_mode must be 0 (fp16)");
+    if (B <= 0 || HQ <= 0 || HKV <= 0 || HQ % HKV || N <= 0 || N > INT32_MAX / 2 || T < 0 || W < 0)
+        return fail(HYQ_EINVAL, "hyq_prefill_hybrid: invalid sizes (need HQ % HKV == 0, N > 0)");
+    const int64_t P = std::max<int64_t>(0, N - W);
+    if (P > MAX_P) return fail(HYQ_ENOTSUP, "hyq_prefill_hybrid: N - window exceeds 131072");
+    if (T > MAX_T) return fail(HYQ_ENOTSUP, "hyq_prefill_hybrid: more than 8192 vertical indices per head");
+    if (!p->q || !p->k || !p->v || !p->out || (P > 0 && T > 0 && !p->vidx))
+        return fail(HYQ_EINVAL, "hyq_prefill_hybrid: null pointer");
+    auto rows16 = [](const void* ptr, int64_t sb, int64_t sh, int64_t sn) {
+        return aligned(ptr, 16) && (sb * 2) % 16 == 0 && (sh * 2) % 16 == 0 && (sn * 2) % 16 == 0;
+    };
+    if (!rows16(p->q, p->q_stride_b, p->q_stride_h, p->q_stride_n) ||
+        !rows16(p->k, p->k_stride_b, p->k_stride_h, p->k_stride_n) ||
+        !rows16(p->v, p->v_stride_b, p->v_stride_h, p->v_stride_n) ||
+        !rows16(p->out, p->o_stride_b, p->o_stride_h, p->o_stride_n))
+        return fail(HYQ_EINVAL, "hyq_prefill_hybrid: q/k/v/out rows must be contiguous and 16-byte aligned");
+    const PrefillLayout L = prefill_layout(B, HQ, HKV, N, T, W, p->pv_mode);
+    if (!ws || ws_bytes < L.total || !aligned(ws, 256))
+        return fail(HYQ_ENOSPC, "hyq_prefill_hybrid: workspace too small or not 256-byte aligned (need " +
+                                    std::to_string(L.total) + " bytes)");
+    uint8_t* base = static_cast<uint8_t*>(ws);
+    auto at = [&](size_t off) { return static_cast<void*>(base + off); };
+    const int BH = B * HQ, BHK = B * HKV;
+    const int nblk = static_cast<int>((N + BM - 1) / BM);
+    const int nch = static_cast<int>((N + STAT_ROWS - 1) / STAT_ROWS);
+    const int nsb = static_cast<int>((P + BN - 1) / BN);
+    const int Pi = static_cast<int>(P), Ti = static_cast<int>(P > 0 ? T : 0), Ni = static_cast<int>(N);
+    const uint16_t* k = static_cast<const uint16_t*>(p->k);
+    const uint16_t* v = static_cast<const uint16_t*>(p->v);
+
+    hipLaunchKernelGGL(kv_stats_kernel, dim3(nch, BHK), dim3(256), 0, stream, k, p->k_stride_b, p->k_stride_h,
+                       p->k_stride_n, v, p->v_stride_b, p->v_stride_h, p->v_stride_n, HKV, Ni, nch,
+                       static_cast<double*>(at(L.kpart)), static_cast<float*>(at(L.vpart)));
+    if (int st = check_launch("kv_stats_kernel")) return st;
+    hipLaunchKernelGGL(kv_final_kernel, dim3(BHK), dim3(PD), 0, stream, static_cast<const double*>(at(L.kpart)),
+                       static_cast<const float*>(at(L.vpart)), nch, Ni, p->smooth_k ? 1 : 0,
+                       static_cast<uint16_t*>(at(L.km)), static_cast<float*>(at(L.vscale)));
+    if (int st = check_launch("kv_final_kernel")) return st;
+    const int cblocks = static_cast<int>((N * 16 + 255) / 256);
+    hipLaunchKernelGGL(kv_convert_kernel, dim3(cblocks, BHK), dim3(256), 0, stream, k, p->k_stride_b,
+                       p->k_stride_h, p->k_stride_n, v, p->v_stride_b, p->v_stride_h, p->v_stride_n, HKV, Ni,
+                       static_cast<const uint16_t*>(at(L.km)), static_cast<const float*>(at(L.vscale)),
+                       static_cast<uint16_t*>(at(L.k16)), static_cast<uint16_t*>(at(L.v16)),
+                       p->pv_mode ? static_cast<uint8_t*>(at(L.v8)) : nullptr);
+    if (int st = check_launch("kv_convert_kernel")) return st;
+    if (P > 0) {
+        if (int st = launch_lists(p->vidx, p->vi_stride_b, p->vi_stride_h, p->vi_stride_t, BH, HQ, Ti, Pi, nblk, W,
+                                  static_cast<int32_t*>(at(L.vert)), static_cast<int32_t*>(at(L.rest)),
+                                  static_cast<int32_t*>(at(L.rcount)), static_cast<int32_t*>(at(L.nr)),
+                                  static_cast<int32_t*>(at(L.nv)), stream))
+            return st;
+        const int nvb = (Ti + BN - 1) / BN;
+        hipLaunchKernelGGL(gather_kernel, dim3(nsb + nvb, BH), dim3(256), 0, stream,
+                           static_cast<const uint16_t*>(at(L.k16)), static_cast<const uint16_t*>(at(L.v16)),
+                           p->pv_mode ? static_cast<const uint8_t*>(at(L.v8)) : nullptr, HQ, HQ / HKV, HKV, Ni, Pi, Ti,
+                           nsb, static_cast<const int32_t*>(at(L.rest)), static_cast<const int32_t*>(at(L.rcount)),
+                           static_cast<const int32_t*>(at(L.vert)), static_cast<int8_t*>(at(L.k8r)),
+                           static_cast<float*>(at(L.k8r_scale)), static_cast<uint8_t*>(at(L.vr)),
+                           static_cast<uint16_t*>(at(L.kv16)), static_cast<uint16_t*>(at(L.vv16)));
+        if (int st = check_launch("gather_kernel")) return st;
+    } else {
+        // no prefix: every block reads zero rest / vertical entries
+        hipLaunchKernelGGL(zero_counts_kernel, dim3((2 * BH * nblk + 255) / 256), dim3(256), 0, stream,
+                           static_cast<int32_t*>(at(L.nr)), static_cast<int32_t*>(at(L.nv)), BH * nblk);
+        if (int st = check_launch("zero_counts_kernel")) return st;
+    }
+    PfArgs a{};
+    a.q = static_cast<const uint16_t*>(p->q); a.q_b = p->q_stride_b; a.q_h = p->q_stride_h; a.q_n = p->q_stride_n;
+    a.out = static_cast<uint16_t*>(p->out); a.o_b = p->o_stride_b; a.o_h = p->o_stride_h; a.o_n = p->o_stride_n;
+    a.k8r = static_cast<const int8_t*>(at(L.k8r));
+    a.k8r_scale = static_cast<const float*>(at(L.k8r_scale));
+    a.vr = static_cast<const uint16_t*>(at(L.vr));
+    a.kv16 = static_cast<const uint16_t*>(at(L.kv16));
+    a.vv16 = static_cast<const uint16_t*>(at(L.vv16));
+    a.k16 = static_cast<const uint16_t*>(at(L.k16));
+    a.v16 = static_cast<const uint16_t*>(at(L.v16));
+    a.nr = static_cast<const int32_t*>(at(L.nr));
+    a.nv = static_cast<const int32_t*>(at(L.nv));
+    a.B = B; a.HQ = HQ; a.HKV = HKV; a.N = Ni; a.nblk = nblk; a.W = W; a.P = Pi; a.T = Ti; a.nsb = nsb;
+    const double sm = p->sm_scale > 0.0 ? p->sm_scale : std::pow(static_cast<double>(PD), -0.5);
+    a.c = static_cast<float>(sm * 1.44269504);
+    a.total = BH * nblk;
+    a.per_xcd = (a.total + 7) / 8;
+    hipLaunchKernelGGL(prefill_main_kernel, dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
+    return check_launch("prefill_main_kernel");
+}

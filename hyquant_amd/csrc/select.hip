@@ -38,14 +38,6 @@ constexpr int TOPK_THREADS = 1024;
 constexpr int TOPK_MAX_T = 8192;           // bitonic sort buffer in LDS
 constexpr int64_t TOPK_MAX_P = 65536;      // 16-bit index in the composite
 
-// float64 -> bf16 with one correct RNE rounding: round to float32 toward zero
-// with a sticky bit (round-to-odd), then RNE to bf16.
-__device__ __forceinline__ uint16_t f64_to_bf16_rne(double x) {
-    float f = __double2float_rz(x);
-    uint32_t u = __float_as_uint(f);
-    if (static_cast<double>(f) != x) u |= 1u;
-    return f32_to_bf16_rne(__uint_as_float(u));
-}
 
 __device__ __forceinline__ double bf16_bits_to_f64(uint16_t b) { return static_cast<double>(bf16_to_f32(b)); }
 

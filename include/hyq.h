@@ -150,6 +150,75 @@ int hyq_freeze_reorganise(const uint16_t* k, int64_t ks_b, int64_t ks_h, int64_t
                           uint16_t* kw, int64_t kw_bh, int64_t kw_n, uint16_t* vw, int64_t vw_bh, int64_t vw_n,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+
+/*
+ * Per-block symmetric int8 quantisation.  Replaces per_block_int8 /
+ * quant_per_block_int8_kernel (src/ops/vendor/sageattention/triton/
+ * quant_per_block.py:21-101) for one tensor:
+ *   x     bf16 (x_is_fp16 = 0) or fp16 [b, h, len, d], strides (xs_b, xs_h, xs_n),
+ *         rows 16-byte aligned
+ *   km    optional bf16 [b, h, d] (strides km_b, km_h): x <- bf16(x - km) first
+ *   out   int8 [b, h, len, d], strides (os_b, os_h, os_n), rows 8-byte aligned
+ *   scale fp32 [b, h, ceil(len / blk)], strides (ss_b, ss_h, 1)
+ * Per block of blk rows: y = fp32(x) * sm, scale = amax(|y|) / 127,
+ * code = trunc(y / scale + 0.5 * sign(y)) with IEEE fp32 division; a zero
+ * block has scale 0 and codes 0.  d == 128.
+ */
+int hyq_per_block_int8(const void* x, int32_t x_is_fp16, int64_t xs_b, int64_t xs_h, int64_t xs_n,
+                       int32_t b, int32_t h, int64_t len, int32_t d, float sm, int32_t blk,
+                       const void* km, int64_t km_b, int64_t km_h,
+                       void* out, int64_t os_b, int64_t os_h, int64_t os_n,
+                       float* scale, int64_t ss_b, int64_t ss_h, void* stream);
+
+/*
+ * Rest / vertical index lists of the hybrid prefill.  Replaces the index part
+ * of reorder_kv_for_vertical (src/ops/sage_unified.py:499-547), per (b, h):
+ *   vert   int32 [b*h, t]     vidx clamped to [0, p) and sorted ascending
+ *                             (repeats kept), p = max(0, n - window)
+ *   rest   int32 [b*h, p]     the positions of [0, p) not in vert, ascending;
+ *                             the first rcount[b*h] entries are valid
+ *   nr, nv int32 [b*h, ceil(n/128)]  entries of rest / vert below the window
+ *                             start of each 128-row query block,
+ *                             wla = floor64(max(0, 128 blk - (window - 1)))
+ * vidx int64 [b, h, t] with strides (vi_b, vi_h, vi_t).  p <= 131072, t <= 8192.
+ */
+int hyq_prefill_lists(const int64_t* vidx, int64_t vi_b, int64_t vi_h, int64_t vi_t,
+                      int32_t b, int32_t h, int64_t n, int64_t t, int32_t window,
+                      int32_t* vert, int32_t* rest, int32_t* rcount, int32_t* nr, int32_t* nv,
+                      void* stream);
+
+/* Arguments of hyq_prefill_hybrid (strides in elements, channels contiguous). */
+typedef struct hyq_prefill_params {
+    const void* q; int64_t q_stride_b, q_stride_h, q_stride_n;    /* bf16 [B, HQ, N, 128]  */
+    const void* k; int64_t k_stride_b, k_stride_h, k_stride_n;    /* bf16 [B, HKV, N, 128] */
+    const void* v; int64_t v_stride_b, v_stride_h, v_stride_n;    /* bf16 [B, HKV, N, 128] */
+    const int64_t* vidx; int64_t vi_stride_b, vi_stride_h, vi_stride_t;  /* int64 [B, HQ, T] */
+    void* out; int64_t o_stride_b, o_stride_h, o_stride_n;        /* bf16 [B, HQ, N, 128]  */
+    int32_t batch, hq, hkv, head_dim;
+    int64_t n, t;
+    int32_t window;       /* local window W */
+    int32_t smooth_k;     /* subtract the per-channel K mean before quantising */
+    int32_t pv_mode;      /* 0: fp16 P.V; 1: OCP e4m3 P.V on the rest tiles */
+    double sm_scale;      /* <= 0: head_dim^-0.5 */
+} hyq_prefill_params;
+
+/*
+ * Hybrid-precision causal prefill attention.  Replaces
+ * sage_vertical_attention_v2 (src/ops/sage_unified.py:550-622) and its kernel
+ * _attn_fwd_vertical_v2 (:398-496); pv_mode 1 follows the FP8 P.V semantics
+ * of the SM90 kernel (csrc/qattn/qk_int_sv_f8_cuda_sm90.cu:290-340, 490-512):
+ * per-channel V scale amax/448, P scaled by 448 before the e4m3 cast.
+ * For query block blk (128 rows) the keys are: rest positions below wla
+ * (int8 Q . int8 K with per-block scales), vertical positions below wla and
+ * the causal window wla <= j <= i (fp16 Q . fp16 K); one softmax; bf16 out.
+ * Workspace: hyq_prefill_workspace_size(...) bytes, 256-byte aligned.
+ * Limits: head_dim 128, N - window <= 131072, T <= 8192.
+ */
+size_t hyq_prefill_workspace_size(int32_t b, int32_t hq, int32_t hkv, int64_t n, int64_t t,
+                                  int32_t window, int32_t pv_mode);
+int hyq_prefill_hybrid(const hyq_prefill_params* params, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -559,3 +559,197 @@ def build_decode_state(inp: DecodeInputs) -> DecodeState:
     st = freeze(inp.keys, inp.values, inp.query_tail, inp.W, inp.rho, inp.HQ // inp.HKV)
     append_staging(st, inp.k_new, inp.v_new)
     return st
+
+
+# ---------------------------------------------------------------------------
+# a12-a15: hybrid prefill (src/ops/sage_unified.py:499-622 with
+# src/ops/vendor/sageattention/triton/quant_per_block.py:21-101)
+# ---------------------------------------------------------------------------
+
+PREFILL_BLOCK_M = 128   # query rows per block (Q int8 scale granularity, window alignment)
+PREFILL_BLOCK_N = 64    # key rows per tile (rest-K int8 scale granularity)
+
+
+def per_block_int8(x: np.ndarray, sm: float, blk: int) -> Tuple[np.ndarray, np.ndarray]:
+    """quant_per_block_int8_kernel (quant_per_block.py:21-46): over blocks of
+    `blk` rows of x [..., L, D]: xs = fp32(x) * fp32(sm); scale = amax / 127;
+    code = trunc(xs / scale + 0.5 * sign) (round half away from zero), all in
+    fp32.  A block of zeros gets scale 0 and codes 0.  Returns (codes int8,
+    scale float32 [..., ceil(L / blk)])."""
+    xf = np.asarray(x, dtype=np.float32) * np.float32(sm)
+    L = xf.shape[-2]
+    nb = (L + blk - 1) // blk
+    codes = np.zeros(xf.shape, dtype=np.int8)
+    scales = np.zeros(xf.shape[:-2] + (nb,), dtype=np.float32)
+    for i in range(nb):
+        blk_x = xf[..., i * blk:(i + 1) * blk, :]
+        amax = np.abs(blk_x).max(axis=(-2, -1))
+        scale = (amax / np.float32(127.0)).astype(np.float32)
+        scales[..., i] = scale
+        with np.errstate(divide="ignore", invalid="ignore"):
+            r = (blk_x / scale[..., None, None]).astype(np.float32)
+            r = (r + np.where(r >= 0, np.float32(0.5), np.float32(-0.5))).astype(np.float32)
+        r = np.where(scale[..., None, None] > 0, r, 0)
+        codes[..., i * blk:(i + 1) * blk, :] = np.trunc(r).astype(np.int8)
+    return codes, scales
+
+
+def smooth_keys(k: np.ndarray, smooth: bool = True) -> Tuple[np.ndarray, np.ndarray]:
+    """K-smoothing (sage_unified.py:565-570): km = bf16 mean over the sequence
+    (exact float64 sum, one RNE rounding), ks = bf16(fp32(k) - fp32(km)).
+    Returns (km [..., 1, D], ks)."""
+    if not smooth:
+        return np.zeros(k.shape[:-2] + (1, k.shape[-1]), np.float32), np.asarray(k, np.float32)
+    km = mean_bf16(k, axis=-2)[..., None, :]
+    ks = bf16_round((np.asarray(k, np.float32) - km).astype(np.float32))
+    return km, ks
+
+
+def to_fp16(x: np.ndarray) -> np.ndarray:
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def prefill_lists(vidx_row: np.ndarray, N: int, W: int):
+    """reorder_kv_for_vertical (sage_unified.py:499-547) for one (b, h_q) row.
+    The vertical list is the indices clamped to [0, P), P = N - W, sorted
+    ascending (a repeated index stays repeated and is attended twice, as the
+    reference's gather does); rest = the positions of [0, P) not in it,
+    ascending.  Per query block b the counts of each below the 64-aligned
+    window start wla(b) (searchsorted, left).  Returns (vert, rest, nv, nr)."""
+    P = max(0, N - W)
+    nblk = (N + PREFILL_BLOCK_M - 1) // PREFILL_BLOCK_M
+    if P == 0:
+        z = np.zeros(nblk, np.int64)
+        return np.zeros(0, np.int64), np.zeros(0, np.int64), z, z
+    vert = np.sort(np.clip(np.asarray(vidx_row, np.int64), 0, P - 1))
+    mask = np.zeros(P, bool)
+    mask[vert] = True
+    rest = np.nonzero(~mask)[0]
+    wla = np.array([window_start(b, W) for b in range(nblk)], np.int64)
+    nv = np.searchsorted(vert, wla, side="left")
+    nr = np.searchsorted(rest, wla, side="left")
+    return vert, rest, nv, nr
+
+
+def window_start(b: int, W: int) -> int:
+    """First key of query block b's fp16 window segment (sage_unified.py:482-485
+    and :538-541): floor64(max(0, 128 b - (W - 1)))."""
+    return max(0, PREFILL_BLOCK_M * b - (W - 1)) // PREFILL_BLOCK_N * PREFILL_BLOCK_N
+
+
+def prefill_operands(q, k, v, sm_scale: Optional[float] = None, smooth: bool = True):
+    """The wrapper's operand preparation (sage_unified.py:559-584):
+    c = fp32(sm_scale * log2e); Q int8 per 128-row block of x = fp32(q) * c
+    (codes, scales); q16 = fp16(bf16(fp32(q) * c)); km and the smoothed keys
+    ks = bf16(k - km) as fp16; v16 = fp16(v).  Returns a dict."""
+    D = q.shape[-1]
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    c = np.float32(sm_scale * LOG2E)
+    q8, qsc = per_block_int8(q, c, PREFILL_BLOCK_M)
+    q16 = to_fp16(bf16_round((np.asarray(q, np.float32) * c).astype(np.float32)))
+    km, ks = smooth_keys(k, smooth)
+    return dict(c=c, q8=q8, q_scale=qsc, q16=q16, km=km, k16=to_fp16(ks), v16=to_fp16(v))
+
+
+def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None, smooth: bool = True,
+                        int8_rest: bool = True, abs_v: bool = False):
+    """float64 restatement of sage_vertical_attention_v2 (sage_unified.py:550-622,
+    kernel :398-496).  q [B, HQ, N, D], k/v [B, HKV, N, D] (bf16 values),
+    vidx [B, HQ, T].  For query row i of block b (128 rows):
+      rest keys (not vertical, position < wla(b)): s = (q8 . k8) * q_scale * k_scale
+        (Q int8 per 128-row block with sm_scale*log2e folded in, K smoothed then
+        int8 per 64-row block of the rest list, round half away from zero);
+      vertical keys below wla(b) and window keys wla(b) <= j <= i:
+        s = q16 . k16 with q16 = fp16(bf16(q * sm*log2e)), k16 = fp16(ks);
+    one base-2 softmax over all of them, values fp16(v).  int8_rest=False
+    scores the rest keys with q16 . k16 too (a check of the partition alone).
+    abs_v=True returns sum p |v| / l instead (an error scale).  Returns float64
+    [B, HQ, N, D]."""
+    B, HQ, N, D = q.shape
+    HKV = k.shape[1]
+    G = HQ // HKV
+    op = prefill_operands(q, k, v, sm_scale, smooth)
+    q8, qsc, q16, k16, v16 = op["q8"], op["q_scale"], op["q16"], op["k16"], op["v16"]
+    if abs_v:
+        v16 = np.abs(v16)
+    out = np.zeros((B, HQ, N, D), np.float64)
+    for b in range(B):
+        for h in range(HQ):
+            hk = h // G
+            vert, rest, nv, nr = prefill_lists(vidx[b, h], N, W)
+            if len(rest):
+                k8r, ksr = per_block_int8(k16[b, hk, rest], 1.0, PREFILL_BLOCK_N)
+            for blk in range((N + PREFILL_BLOCK_M - 1) // PREFILL_BLOCK_M):
+                wla = window_start(blk, W)
+                rows = np.arange(blk * PREFILL_BLOCK_M, min(N, (blk + 1) * PREFILL_BLOCK_M))
+                qrow = q16[b, h, rows].astype(np.float64)
+                segs_s, segs_v = [], []
+                if nr[blk] > 0:
+                    n = nr[blk]
+                    if int8_rest:
+                        kscale = np.repeat(ksr.astype(np.float64), PREFILL_BLOCK_N)[:n]
+                        # integer dot products, exact in float64 (|sum| < 2^22)
+                        s = q8[b, h, rows].astype(np.float64) @ k8r[:n].astype(np.float64).T
+                        segs_s.append(s * float(qsc[b, h, blk]) * kscale[None, :])
+                    else:
+                        segs_s.append(qrow @ k16[b, hk, rest[:n]].astype(np.float64).T)
+                    segs_v.append(v16[b, hk, rest[:n]])
+                if nv[blk] > 0:
+                    idx = vert[:nv[blk]]
+                    segs_s.append(qrow @ k16[b, hk, idx].astype(np.float64).T)
+                    segs_v.append(v16[b, hk, idx])
+                jw = np.arange(wla, min(N, (blk + 1) * PREFILL_BLOCK_M))
+                sw = qrow @ k16[b, hk, jw].astype(np.float64).T
+                segs_s.append(np.where(jw[None, :] <= rows[:, None], sw, -np.inf))
+                segs_v.append(v16[b, hk, jw])
+                S = np.concatenate(segs_s, axis=1)
+                V = np.concatenate(segs_v, axis=0).astype(np.float64)
+                p = np.exp2(S - S.max(axis=1, keepdims=True))
+                out[b, h, rows] = (p @ V) / p.sum(axis=1, keepdims=True)
+    return out
+
+
+def exact_causal_attention(q, k, v, sm_scale: Optional[float] = None) -> np.ndarray:
+    """softmax(q k^T * sm_scale + causal mask) v in float64, GQA by head // G."""
+    B, HQ, N, D = q.shape
+    G = HQ // k.shape[1]
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    out = np.zeros((B, HQ, N, D), np.float64)
+    mask = np.tril(np.ones((N, N), bool))
+    for b in range(B):
+        for h in range(HQ):
+            s = q[b, h].astype(np.float64) @ k[b, h // G].astype(np.float64).T * sm_scale
+            s = np.where(mask, s, -np.inf)
+            s -= s.max(axis=1, keepdims=True)
+            p = np.exp(s)
+            out[b, h] = (p / p.sum(axis=1, keepdims=True)) @ v[b, h // G].astype(np.float64)
+    return out
+
+
+def make_prefill_inputs(B=1, HQ=32, HKV=8, N=8192, D=128, W=128, rho=0.05, seed=0, plant_ratio=0.05):
+    """Seeded prefill inputs: Q, K, V ~ N(0,1) [B, H, N, D], per-(KV head,
+    channel) K offsets ~ N(0, 2), planted vertical lines (as in
+    make_decode_inputs, aligned with each KV group's last-W query mean).
+    Returns (q, k, v) as bf16 values in float32 arrays."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    G = HQ // HKV
+    q = torch.randn(B, HQ, N, D, generator=g)
+    k = torch.randn(B, HKV, N, D, generator=g)
+    v = torch.randn(B, HKV, N, D, generator=g)
+    off = torch.randn(HKV, D, generator=g) * math.sqrt(2.0)
+    k = k + off[None, :, None, :]
+    qb = q.to(torch.bfloat16).float()
+    n_plant = min(int(plant_ratio * N), max(0, N - W))
+    for b in range(B):
+        for h in range(HKV):
+            if n_plant == 0:
+                continue
+            u = qb[b, h * G:(h + 1) * G, N - W:].reshape(-1, D).mean(dim=0)
+            u = u / u.norm()
+            pos = torch.randperm(N - W, generator=g)[:n_plant]
+            k[b, h, pos, :] = off[h] + 3.0 * math.sqrt(D) * u
+    cv = lambda t: t.to(torch.bfloat16).float().numpy()
+    return cv(q), cv(k), cv(v)

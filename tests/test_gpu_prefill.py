@@ -1,0 +1,211 @@
+"""GPU parity of the hybrid prefill (hyq_prefill_hybrid via
+sage_vertical_attention_v2), its per-block int8 quantiser (hyq_per_block_int8)
+and rest / vertical lists (hyq_prefill_lists) against the CPU oracle.
+
+Quantiser codes and scales and the index lists are compared bit-exactly.
+Attention outputs: elementwise |out - ref| <= 2e-3 + 2^-10 ref_abs + 2^-8 |ref|
+with ref the float64 restatement and ref_abs = sum p|v| / l: the fp16
+rounding of p before P.V (both here and in the reference kernel, <= 2^-11
+relative per weight) and the bf16 rounding of the output; max-abs and relative
+error are printed."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import hyq_oracle as O
+from tests.gpu_util import to_dev_bf16
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+
+
+def _rand_bf16(rng, shape, scale=1.0):
+    return O.bf16_round((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+def _check(name, out, ref, ref_abs):
+    diff = np.abs(out - ref)
+    err = float(diff.max())
+    rel = err / float(np.abs(ref).max())
+    msg = f"{name}: max-abs {err:.3e} rel {rel:.3e} (max|ref| {float(np.abs(ref).max()):.3f})"
+    print(msg, flush=True)
+    assert np.all(np.isfinite(out))
+    bound = ATOL + 2.0 ** -10 * ref_abs + 2.0 ** -8 * np.abs(ref)
+    bad = np.argwhere(diff > bound)
+    for idx in bad[:6]:
+        i = tuple(idx)
+        print(f"  violation at {i}: out {out[i]:.6f} ref {ref[i]:.6f} bound {bound[i]:.3e}", flush=True)
+    assert bad.size == 0, msg
+
+
+def _run(q, k, v, vidx, W, **kw):
+    from hyquant_amd.sage_unified import sage_vertical_attention_v2
+    dev = torch.device("cuda")
+    vi = torch.from_numpy(np.ascontiguousarray(vidx, dtype=np.int64)).to(dev)
+    out = sage_vertical_attention_v2(to_dev_bf16(q, dev), to_dev_bf16(k, dev), to_dev_bf16(v, dev), vi,
+                                     window_size=W, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+def test_per_block_int8_bit_exact(layout):
+    from hyquant_amd.sage_unified import per_block_int8
+    rng = np.random.default_rng(1)
+    q = _rand_bf16(rng, (2, 3, 300, 128), 2.0)
+    k = _rand_bf16(rng, (2, 1, 300, 128), 3.0)
+    q[1, 2, 128:256] = 0.0                                   # a zero block: scale 0, codes 0
+    q[0, 0, 5, 7] = 127.0 / (128 ** -0.5 * O.LOG2E)          # dominant value
+    q = O.bf16_round(q)
+    km = O.mean_bf16(k, axis=2)[:, :, None, :]
+    dev = torch.device("cuda")
+    qd, kd, kmd = to_dev_bf16(q, dev), to_dev_bf16(k, dev), to_dev_bf16(km, dev)
+    if layout == "NHD":
+        qd, kd, kmd = qd.transpose(1, 2), kd.transpose(1, 2), kmd.transpose(1, 2)
+    q8, qs, k8, ks = per_block_int8(qd, kd, km=kmd, tensor_layout=layout)
+    torch.cuda.synchronize()
+    if layout == "NHD":
+        q8, k8 = q8.transpose(1, 2), k8.transpose(1, 2)
+    eq8, eqs = O.per_block_int8(q, np.float32(128 ** -0.5 * O.LOG2E), 128)
+    ek8, eks = O.per_block_int8(O.bf16_round(k - km), 1.0, 64)
+    assert np.array_equal(q8.cpu().numpy(), eq8)
+    assert np.array_equal(qs.cpu().numpy().view(np.uint32), eqs.view(np.uint32))
+    assert np.array_equal(k8.cpu().numpy(), ek8)
+    assert np.array_equal(ks.cpu().numpy().view(np.uint32), eks.view(np.uint32))
+
+
+@pytest.mark.parametrize("N,W,T", [(700, 100, 40), (5000, 128, 300), (1000, 1, 999), (300, 64, 0), (100, 256, 5)])
+def test_lists_bit_exact(N, W, T):
+    from hyquant_amd.sage_unified import vertical_lists
+    rng = np.random.default_rng(N + T)
+    B, H = 2, 3
+    P = max(0, N - W)
+    vidx = rng.integers(-5, max(P, 1) + 5, size=(B, H, T)).astype(np.int64)   # repeats and out-of-range
+    got = vertical_lists(torch.from_numpy(vidx).cuda(), N, W)
+    torch.cuda.synchronize()
+    for b in range(B):
+        for h in range(H):
+            vert, rest, nv, nr = O.prefill_lists(vidx[b, h], N, W)
+            i = b * H + h
+            assert np.array_equal(got["nr"][i].cpu().numpy(), nr)
+            assert np.array_equal(got["nv"][i].cpu().numpy(), nv)
+            if P:
+                assert np.array_equal(got["vert"][i].cpu().numpy(), vert)
+                rc = int(got["rcount"][i])
+                assert rc == len(rest)
+                assert np.array_equal(got["rest"][i, :rc].cpu().numpy(), rest)
+
+
+CASES = [
+    dict(B=1, HQ=4, HKV=1, N=640, W=128, T=30, seed=1),            # GQA 4, block-aligned
+    dict(B=2, HQ=8, HKV=2, N=1000, W=100, T=45, seed=2),           # ragged last block, W not a multiple of 64
+    dict(B=1, HQ=2, HKV=2, N=777, W=256, T=26, seed=3),            # no GQA, wide window
+    dict(B=1, HQ=4, HKV=2, N=300, W=512, T=0, seed=4),             # N <= W: window only
+    dict(B=1, HQ=2, HKV=1, N=520, W=64, T=0, seed=5),              # no vertical lines
+    dict(B=1, HQ=2, HKV=1, N=129, W=1, T=3, seed=6),               # window of one token
+]
+
+
+@pytest.mark.parametrize("cfg", CASES, ids=[f"N{c['N']}W{c['W']}T{c['T']}" for c in CASES])
+def test_prefill_small_vs_oracle(cfg):
+    print(f"prefill {cfg}", flush=True)
+    rng = np.random.default_rng(cfg["seed"])
+    B, HQ, HKV, N, W, T = (cfg[x] for x in ("B", "HQ", "HKV", "N", "W", "T"))
+    q = _rand_bf16(rng, (B, HQ, N, 128))
+    k = _rand_bf16(rng, (B, HKV, N, 128), 1.5) + O.bf16_round(rng.standard_normal((1, HKV, 1, 128)).astype(np.float32))
+    k = O.bf16_round(k)
+    v = _rand_bf16(rng, (B, HKV, N, 128))
+    P = max(0, N - W)
+    vidx = np.stack([np.stack([rng.permutation(P)[:T] if P else np.zeros(0, np.int64) for _ in range(HQ)])
+                     for _ in range(B)]).astype(np.int64).reshape(B, HQ, T)
+    out = _run(q, k, v, vidx, W)
+    ref = O.hybrid_prefill_fp64(q, k, v, vidx, W)
+    ref_abs = O.hybrid_prefill_fp64(q, k, v, vidx, W, abs_v=True)
+    _check(f"prefill {cfg}", out, ref, ref_abs)
+
+
+def test_prefill_options_and_strided_inputs():
+    rng = np.random.default_rng(9)
+    B, HQ, HKV, N, W = 1, 4, 2, 400, 128
+    q = _rand_bf16(rng, (B, HQ, N, 128))
+    k = _rand_bf16(rng, (B, HKV, N, 128), 2.0)
+    v = _rand_bf16(rng, (B, HKV, N, 128))
+    vidx = rng.integers(-3, N - W + 3, size=(B, HQ, 20))            # repeats and clamping
+    for smooth in (True, False):
+        out = _run(q, k, v, vidx, W, smooth_k=smooth, sm_scale=0.05)
+        ref = O.hybrid_prefill_fp64(q, k, v, vidx, W, sm_scale=0.05, smooth=smooth)
+        ref_abs = O.hybrid_prefill_fp64(q, k, v, vidx, W, sm_scale=0.05, smooth=smooth, abs_v=True)
+        _check(f"smooth={smooth}", out, ref, ref_abs)
+    # NHD-strided views give the same bytes as contiguous inputs
+    from hyquant_amd.sage_unified import sage_vertical_attention_v2
+    dev = torch.device("cuda")
+    qd = to_dev_bf16(q, dev).transpose(1, 2).contiguous().transpose(1, 2)
+    kd = to_dev_bf16(k, dev).transpose(1, 2).contiguous().transpose(1, 2)
+    vd = to_dev_bf16(v, dev).transpose(1, 2).contiguous().transpose(1, 2)
+    vi = torch.from_numpy(vidx).cuda()
+    a = sage_vertical_attention_v2(qd, kd, vd, vi, window_size=W)
+    b = sage_vertical_attention_v2(qd.contiguous(), kd.contiguous(), vd.contiguous(), vi, window_size=W)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def _exact_attention_gpu(qd, kd, vd, chunk=1024):
+    """fp32 causal attention on the GPU, chunked over queries (test reference)."""
+    B, HQ, N, D = qd.shape
+    G = HQ // kd.shape[1]
+    out = torch.empty(B, HQ, N, D, dtype=torch.float32, device=qd.device)
+    for b in range(B):
+        for h in range(HQ):
+            kk = kd[b, h // G].float()
+            vv = vd[b, h // G].float()
+            for s in range(0, N, chunk):
+                qq = qd[b, h, s:s + chunk].float()
+                sc = (qq @ kk[: s + chunk].T.contiguous()) * D ** -0.5
+                i = torch.arange(s, s + qq.shape[0], device=qd.device)[:, None]
+                j = torch.arange(sc.shape[1], device=qd.device)[None, :]
+                sc = sc.masked_fill(j > i, float("-inf"))
+                out[b, h, s:s + chunk] = torch.softmax(sc, dim=-1) @ vv[: s + chunk]
+    return out
+
+
+@pytest.mark.parametrize("N", [8192, 16384])
+def test_prefill_config4(N):
+    """Config 4 shape (B=1, 32/8 heads, d128, W=128, rho=5%, seeded Gaussian
+    with planted vertical lines).  Two query heads against the float64
+    oracle; every head against fp32 exact attention (MSE)."""
+    from hyquant_amd.sage_unified import sage_vertical_attention_v2
+    print(f"prefill config4 N={N}", flush=True)
+    q, k, v = O.make_prefill_inputs(B=1, HQ=32, HKV=8, N=N, W=128, seed=0)
+    vidx = O.compute_vertical_indices(q, k, 128, 0.05, kv_repeat=4)
+    dev = torch.device("cuda")
+    qd, kd, vd = to_dev_bf16(q, dev), to_dev_bf16(k, dev), to_dev_bf16(v, dev)
+    out = sage_vertical_attention_v2(qd, kd, vd, torch.from_numpy(vidx).to(dev), window_size=128)
+    exact = _exact_attention_gpu(qd, kd, vd)
+    mse = float(((out.float() - exact) ** 2).mean())
+    print(f"config4 N={N}: MSE vs exact fp32 attention {mse:.3e}", flush=True)
+    assert mse < 1e-4
+    heads = [5] if N > 8192 else [0, 13]
+    o = out.float().cpu().numpy()
+    for h in heads:
+        hk = h // 4
+        sl = lambda a, lo, hi: a[:, lo:hi]
+        ref = O.hybrid_prefill_fp64(sl(q, h, h + 1), sl(k, hk, hk + 1), sl(v, hk, hk + 1), sl(vidx, h, h + 1), 128)
+        ref_abs = O.hybrid_prefill_fp64(sl(q, h, h + 1), sl(k, hk, hk + 1), sl(v, hk, hk + 1), sl(vidx, h, h + 1),
+                                        128, abs_v=True)
+        _check(f"config4 N={N} head {h}", o[:, h:h + 1], ref, ref_abs)
+
+
+def test_prefill_deterministic():
+    from hyquant_amd.sage_unified import sage_vertical_attention_v2
+    q, k, v = O.make_prefill_inputs(B=1, HQ=8, HKV=2, N=2048, W=128, seed=4)
+    vidx = O.compute_vertical_indices(q, k, 128, 0.05, kv_repeat=4)
+    dev = torch.device("cuda")
+    args = (to_dev_bf16(q, dev), to_dev_bf16(k, dev), to_dev_bf16(v, dev), torch.from_numpy(vidx).to(dev))
+    a = sage_vertical_attention_v2(*args, window_size=128)
+    b = sage_vertical_attention_v2(*args, window_size=128)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

@@ -1,0 +1,184 @@
+"""Pins for the oracle's hybrid prefill (src/ops/sage_unified.py:398-622) and
+per-block int8 quantisation (src/ops/vendor/sageattention/triton/
+quant_per_block.py:21-46): known answers of the fp32 add-then-truncate rounding,
+an exact-rational rederivation, the window-start table, a per-element brute
+force of the key partition, and the reduction to exact causal attention."""
+
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from oracle import hyq_oracle as O
+from tests._exact import to_bf16, to_fp16, to_fp32
+
+
+def _rand_bf16(rng, shape, scale=1.0):
+    return O.bf16_round((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+def _codes_exact(block, sm):
+    """quant_per_block_int8_kernel by exact rationals: every fp32 operation
+    rounded once (x*sm, amax/127, x/scale, +-0.5), then truncation."""
+    c = Fraction(float(np.float32(sm)))
+    xs = [to_fp32(Fraction(float(x)) * c) for x in block.ravel()]
+    amax = max(abs(x) for x in xs)
+    scale = to_fp32(amax / 127)
+    if scale == 0:
+        return np.zeros(block.shape, np.int8), 0.0
+    out = []
+    for x in xs:
+        r = to_fp32(x / scale)
+        r = to_fp32(r + (Fraction(1, 2) if r >= 0 else Fraction(-1, 2)))
+        out.append(int(r))          # int() truncates toward zero
+    return np.array(out, np.int8).reshape(block.shape), float(scale)
+
+
+def test_per_block_int8_known_answers():
+    # amax 127 -> scale 1: half-way values round away from zero
+    x = np.array([[127.0, 2.5, -2.5, 0.5, -0.5, 0.0, -0.0, 1.4999999, -127.0]], np.float32)
+    codes, sc = O.per_block_int8(x, 1.0, 128)
+    assert sc.tolist() == [1.0]
+    assert codes.tolist() == [[127, 3, -3, 1, -1, 0, 0, 1, -127]]
+    # fp32 quirk of add-then-truncate: r = 0.5 - 2^-25 gives r + 0.5 = 1.0 in fp32
+    r = np.float32(0.5) - np.float32(2.0 ** -25)
+    x = np.array([[127.0, r]], np.float32)
+    assert O.per_block_int8(x, 1.0, 128)[0].tolist() == [[127, 1]]
+    # a block of zeros: scale 0, codes 0 (0/0 is not propagated)
+    codes, sc = O.per_block_int8(np.zeros((3, 4), np.float32), 0.3, 128)
+    assert sc.tolist() == [0.0] and not codes.any()
+
+
+@pytest.mark.parametrize("blk,sm", [(128, 0.08838834764831845 * O.LOG2E), (64, 1.0), (5, 0.37)])
+def test_per_block_int8_matches_rational_rederivation(blk, sm):
+    rng = np.random.default_rng(blk)
+    x = _rand_bf16(rng, (2, 13, 16), 3.0)
+    x[1, 3] = 0.0
+    codes, scales = O.per_block_int8(x, sm, blk)
+    for h in range(2):
+        for i in range((13 + blk - 1) // blk):
+            exp_c, exp_s = _codes_exact(x[h, i * blk:(i + 1) * blk], sm)
+            assert np.array_equal(codes[h, i * blk:(i + 1) * blk], exp_c)
+            assert float(scales[h, i]) == exp_s
+
+
+def test_window_start_table():
+    # floor64(max(0, 128 b - (W - 1))), sage_unified.py:482-485
+    assert [O.window_start(b, 128) for b in range(5)] == [0, 0, 128, 256, 384]
+    assert [O.window_start(b, 256) for b in range(5)] == [0, 0, 0, 128, 256]
+    assert [O.window_start(b, 100) for b in range(4)] == [0, 0, 128, 256]
+    assert [O.window_start(b, 1) for b in range(3)] == [0, 128, 256]
+    assert [O.window_start(b, 64) for b in range(3)] == [0, 64, 192]
+
+
+def test_operands_against_rationals():
+    rng = np.random.default_rng(1)
+    q = _rand_bf16(rng, (1, 1, 3, 8))
+    k = _rand_bf16(rng, (1, 1, 5, 8), 2.0)
+    v = _rand_bf16(rng, (1, 1, 5, 8))
+    op = O.prefill_operands(q, k, v, sm_scale=8 ** -0.5)
+    c = Fraction(float(np.float32(8 ** -0.5 * O.LOG2E)))
+    for i in range(3):
+        for d in range(8):
+            exp = to_fp16(to_bf16(to_fp32(Fraction(float(q[0, 0, i, d])) * c)))
+            assert Fraction(float(op["q16"][0, 0, i, d])) == exp
+    for d in range(8):
+        km = to_bf16(sum(Fraction(float(k[0, 0, j, d])) for j in range(5)) / 5)
+        assert Fraction(float(op["km"][0, 0, 0, d])) == km
+        for j in range(5):
+            exp = to_fp16(to_bf16(Fraction(float(k[0, 0, j, d])) - km))
+            assert Fraction(float(op["k16"][0, 0, j, d])) == exp
+
+
+def test_lists_partition_and_duplicates():
+    N, W = 700, 100
+    vidx = np.array([5, 3, 590, 599, 3, 10_000, -4])           # duplicate, out of range both ways
+    vert, rest, nv, nr = O.prefill_lists(vidx, N, W)
+    assert vert.tolist() == [0, 3, 3, 5, 590, 599, 599]
+    assert len(rest) == 600 - 5 and not set(rest) & set(vert)
+    assert set(rest) | set(vert) == set(range(600))
+    wla = [O.window_start(b, W) for b in range(6)]
+    assert nr.tolist() == [sum(r < w for r in rest) for w in wla]
+    assert nv.tolist() == [sum(x < w for x in vert) for w in wla]
+
+
+def _brute_prefill(q, k, v, vidx, W):
+    """Per-element restatement: for query i and key j <= i decide the category
+    directly (window: wla(i // 128) <= j; vertical: j in the index set, once per
+    occurrence; rest otherwise), score it, and take one softmax per row."""
+    B, HQ, N, D = q.shape
+    G = HQ // k.shape[1]
+    op = O.prefill_operands(q, k, v)
+    P = max(0, N - W)
+    out = np.zeros(q.shape)
+    for b in range(B):
+        for h in range(HQ):
+            hk = h // G
+            vlist = sorted(min(max(int(x), 0), P - 1) for x in vidx[b, h]) if P else []
+            vset = set(vlist)
+            rest = [j for j in range(P) if j not in vset]
+            rank = {j: r for r, j in enumerate(rest)}
+            k8, ksc = O.per_block_int8(op["k16"][b, hk, rest], 1.0, 64) if rest else (None, None)
+            for i in range(N):
+                wla = max(0, 128 * (i // 128) - (W - 1)) // 64 * 64
+                s, vals = [], []
+                for j in range(i + 1):
+                    if j >= wla:
+                        mult = 1
+                    elif j in vset:
+                        mult = vlist.count(j)
+                    else:
+                        r = rank[j]
+                        dot = int(np.dot(op["q8"][b, h, i].astype(np.int64), k8[r].astype(np.int64)))
+                        s.append(dot * float(op["q_scale"][b, h, i // 128]) * float(ksc[r // 64]))
+                        vals.append(op["v16"][b, hk, j])
+                        continue
+                    sc = float(np.dot(op["q16"][b, h, i].astype(np.float64), op["k16"][b, hk, j].astype(np.float64)))
+                    s += [sc] * mult
+                    vals += [op["v16"][b, hk, j]] * mult
+                s = np.array(s)
+                p = np.exp2(s - s.max())
+                out[b, h, i] = p @ np.array(vals, np.float64) / p.sum()
+    return out
+
+
+@pytest.mark.parametrize("N,W,T", [(300, 64, 12), (520, 128, 30), (200, 1, 7)])
+def test_hybrid_prefill_matches_per_element_brute_force(N, W, T):
+    rng = np.random.default_rng(N + W)
+    q = _rand_bf16(rng, (1, 2, N, 16))
+    k = _rand_bf16(rng, (1, 1, N, 16), 1.5)
+    v = _rand_bf16(rng, (1, 1, N, 16))
+    vidx = np.stack([rng.permutation(N - W)[:T] for _ in range(2)])[None]
+    vidx[0, 1, 1] = vidx[0, 1, 0]                                  # one repeated index
+    got = O.hybrid_prefill_fp64(q, k, v, vidx, W, sm_scale=16 ** -0.5)
+    exp = _brute_prefill(q, k, v, vidx, W)
+    assert np.abs(got - exp).max() < 1e-12
+
+
+@pytest.mark.parametrize("W", [64, 300])
+def test_hybrid_prefill_reduces_to_exact_attention(W):
+    """W >= N, or int8 rest scoring switched off, leaves one softmax over every
+    key j <= i exactly once: textbook causal attention on (q16, k16, v16)."""
+    rng = np.random.default_rng(W)
+    q = _rand_bf16(rng, (1, 4, 290, 32))
+    k = _rand_bf16(rng, (1, 2, 290, 32), 1.5)
+    v = _rand_bf16(rng, (1, 2, 290, 32))
+    vidx = np.stack([rng.permutation(max(1, 290 - W))[:9] for _ in range(4)])[None]
+    op = O.prefill_operands(q, k, v)
+    exact = O.exact_causal_attention(op["q16"], op["k16"], op["v16"], sm_scale=math.log(2))
+    got = O.hybrid_prefill_fp64(q, k, v, vidx, W, int8_rest=(W >= 290))
+    assert np.abs(got - exact).max() < 1e-12
+    # smoothing only shifts each row's logits by a constant (up to rounding)
+    raw = O.exact_causal_attention(q, k, v)
+    assert np.abs(exact - raw).max() < 2e-2
+
+
+def test_hybrid_prefill_int8_error_is_small():
+    q, k, v = O.make_prefill_inputs(B=1, HQ=4, HKV=1, N=640, W=128, seed=3)
+    from oracle.hyq_oracle import compute_vertical_indices
+    vidx = compute_vertical_indices(q, k, 128, 0.05, kv_repeat=4)
+    got = O.hybrid_prefill_fp64(q, k, v, vidx, 128)
+    ref = O.exact_causal_attention(q, k, v)
+    mse = float(((got - ref) ** 2).mean())
+    assert mse < 1e-4, mse

@@ -232,7 +232,7 @@ def main():
                    "eager_us_per_step": round(eager * 1e3, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode step = decode_partial_kernel + decode_merge_kernel",
+                     "kernel": "decode_kernel (one launch per step)",
                      "algorithmic_bytes_per_launch": nbytes},
     }
     if not args.no_bf16:

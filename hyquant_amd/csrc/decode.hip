@@ -7,22 +7,27 @@
 // s = (q . k_code) * s_k, and P is rounded to bf16 after multiplying by the
 // per-token V scale, P' = bf16(p * s_v), before P' . v_code (F8).
 //
-// Two launches per step, no fences inside either:
-//   decode_partial_kernel — a workgroup of 4 wavefronts owns one chunk of one
-//     KV head (all G query heads of the GQA group ride along as MFMA
-//     columns).  int4 chunks hold `split` tokens walked in 32-token groups
-//     (wavefront w takes groups w, w+4, ...) through a three-deep register
-//     ring, so two groups' loads are in flight while one is computed; bf16
-//     chunks hold 128 tokens of one segment (two 16-token tiles per
-//     wavefront, both loaded up front).  bf16 chunks are numbered first so
-//     they start first.  The four wavefronts' (m, l, acc) are merged in LDS
-//     and the workgroup writes one partial.
-//   decode_merge_kernel — one workgroup per (KV head, 8-channel slice) reads
-//     every partial of its head (its partial loads are issued before the
-//     (m, l) table is built, so the merge is about one memory round trip) and
-//     writes the bf16 output.  The kernel boundary orders the partials; a device-scope
-//     release/acquire per workgroup inside one kernel costs an L2 writeback
-//     each, which measured 3 us (B=1) to 47 us (B=16) per step.
+// One launch per step.  A workgroup of 4 wavefronts owns one chunk of one KV
+// head (all G query heads of the GQA group ride along as MFMA columns):
+//   int4 chunks hold `split` tokens walked in 32-token groups (wavefront w
+//     takes groups w, w+4, ...) through a three-deep register ring, so two
+//     groups' loads are in flight while one is computed;
+//   bf16 chunks hold 128 tokens of one segment (two 16-token tiles per
+//     wavefront, both loaded up front).
+// int4 chunks are numbered first: they are the long ones, and the short bf16
+// chunks fill the tail of the grid.  Every load goes through a buffer
+// descriptor whose range is the chunk (past the end reads zeros), so the ring's
+// loads are unconditional and their wait counts exact; the loop position
+// travels in the scalar offset.
+//
+// The four wavefronts' (m, l, acc) are merged in LDS and the workgroup writes
+// one partial with device-scope stores (write-through to the device coherence
+// point), waits for them, and counts itself in on its head's arrival counter.
+// The workgroup that arrives last merges the head's partials (one wavefront
+// per query head; see merge_head) and resets the counter to zero, so the
+// counters are zero again when the launch ends.  No fence is needed: the
+// partials never sit dirty in a per-XCD L2, and the merge reads them with
+// device-scope loads.
 //
 // Per wavefront, lane l = 16*kb + c (c = l & 15, kb = l >> 4):
 //   QK  S^T[token][g] = K_tile . Q^T with v_mfma_f32_16x16x32_{f16,bf16}:
@@ -36,6 +41,8 @@
 //   Channel 8*j+nb of V sits in row j of PV MFMA nb (lane j loads the dword /
 //   16 bytes holding channels 8j..8j+7).  bf16 tiles use the K=16 form
 //   (v_mfma_f32_16x16x16_bf16) whose slot e of lane-row kb is token 4kb+e.
+//   The four lanes of a quad load the K and V scales of tokens 4kb..4kb+3 of a
+//   tile and quad-broadcast DPP moves hand every lane all four.
 // int4 -> MFMA operand conversion is done in registers without any lookup:
 //   K: nibble ^ 8 -> fp16(1024 + u) by OR-ing a magic exponent, then one
 //      packed fp16 add of -1032 gives the exact code (Q is fed as fp16,
@@ -52,18 +59,21 @@ namespace hyq {
 namespace {
 
 constexpr int D = 128;
-constexpr int WAVES = 4;                 // wavefronts per partial workgroup
+constexpr int WAVES = 4;                 // wavefronts per workgroup
 constexpr int THREADS = 64 * WAVES;
 constexpr int GROUP = 32;                // int4 tokens per wavefront iteration
 constexpr int TILE = 16;                 // bf16 tokens per wavefront iteration
 constexpr int CHUNK4_MIN = WAVES * GROUP;   // int4 split granularity
 constexpr int CHUNK16 = WAVES * 2 * TILE;   // bf16 tokens per workgroup chunk
-constexpr int MSLICE = 8;                // channels per merge workgroup
-constexpr int MERGE_THREADS = 256;
 constexpr float LOG2E = 1.44269504f;     // src/ops/decode_d_stage.py:17
 constexpr float RESCALE_SLACK = 8.0f;    // lazy max update threshold (log2 units)
 constexpr float M_INIT = -1.0e30f;
-constexpr int MAX_PARTIALS = 4096;       // nwg * G bound of the merge tables
+constexpr int MAX_PARTIALS = 1024;       // nwg * G bound
+constexpr int MAX_NWG = 256;             // chunks per head (merge weight table)
+constexpr int CNT_PAD = 32;              // arrival counters 128 bytes apart
+constexpr int CNT_CAP = 16384;           // counter slots at the head of every workspace (bh_kv bound)
+constexpr int MJ = 24;                   // partial float4 loads per lane per merge batch
+constexpr int SPLIT_MAX_SMALL = 2048;    // largest automatic int4 split
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -89,11 +99,13 @@ struct DecArgs {
     float qk_scale;        // sm_scale * log2(e)
     int32_t split;         // int4 tokens per chunk (multiple of CHUNK4_MIN)
     int32_t n4;            // int4 chunks per head
+    int32_t bsplit;        // bf16 tokens per chunk (multiple of CHUNK16)
     int32_t nseg[3];       // bf16 chunks per segment
     int32_t n16;           // bf16 chunks per head
     int32_t nwg;           // chunks per head
-    float* part;           // [bh_kv][nwg][G][D]
+    float* part;           // [bh_kv][nwg][G][D] partial numerators
     float* ml;             // [bh_kv][nwg][G][2] = (m, l)
+    uint32_t* cnt;         // arrival counter of head h at cnt[h * CNT_PAD]
 };
 
 struct WaveState {
@@ -197,85 +209,91 @@ __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[N], bool 
 // ---------------------------------------------------------------------------
 // int4 prefix
 // ---------------------------------------------------------------------------
+// Every load goes through a buffer descriptor whose range is the chunk, so a
+// token past the chunk end reads zeros without touching memory: the loads of
+// the ring are unconditional, which keeps the compiler's wait counts exact
+// (a load under a branch makes every later wait a full drain).
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr int RSRC_W3 = 0x00020000;      // raw buffer, 32-bit data format
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, RSRC_W3);
+}
+// voff: per-lane byte offset (constant across a loop), soff: wave-uniform
+// byte offset (the loop position, kept in an SGPR)
+__device__ __forceinline__ u32x4 bld128(Rsrc r, uint32_t voff, uint32_t soff = 0) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ uint32_t bld32(Rsrc r, uint32_t voff, uint32_t soff = 0) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint32_t bld16(Rsrc r, uint32_t voff, uint32_t soff = 0) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xf, 0xf, false));
+}
+
 struct Int4Raw {
-    uint4 k[2];            // tile t: token 16t + c, bytes 16kb..16kb+15 (channels 32kb..32kb+31)
+    u32x4 k[2];            // tile t: token 16t + c, bytes 16kb..16kb+15 (channels 32kb..32kb+31)
     uint32_t v[8];         // slot e: token tau(kb, e), bytes 4c..4c+3 (channels 8c..8c+7)
-    uint32_t scl;          // lane < 32: k scale of token lane; else v scale of token lane-32
+    uint32_t sk[2], sv[2]; // tile t: fp16 scale bits of token 16t + 4kb + (c & 3)
 };
 
-// Packed rows are contiguous (64 bytes per token), so every load of a group is
-// one per-lane base plus a compile-time offset (immediate in the instruction).
-constexpr int PROW = D / 2;
+constexpr int PROW = D / 2;               // packed bytes per token
 constexpr int BROW = D;                   // bf16 row stride in elements
 
 struct Int4Ctx {
-    const uint8_t* kbase;  // this head's packed K / V rows
-    const uint8_t* vbase;
-    const uint16_t* sbase; // this lane's scale array (k for lanes < 32, v otherwise)
+    Rsrc k, v, ks, vs;     // this chunk's packed K / V rows and scales
     uint32_t klane;        // lane offset of tile 0: c * 64 + 16 * kb
     uint32_t vlane;        // lane offset of slot 0: 4kb * 64 + 4c
-    int hi;                // end of the chunk
+    uint32_t slane;        // lane offset of the scale of tile 0: (4kb + (c & 3)) * 2
 };
 
-__device__ __forceinline__ void int4_load_full(Int4Raw& r, const Int4Ctx& x, int t0, int lane) {
-    const uint8_t* kl = x.kbase + static_cast<int64_t>(t0) * PROW + x.klane;
-    const uint8_t* vl = x.vbase + static_cast<int64_t>(t0) * PROW + x.vlane;
-    r.k[0] = *reinterpret_cast<const uint4*>(kl);
-    r.k[1] = *reinterpret_cast<const uint4*>(kl + 16 * PROW);
+// t0 is wave-uniform: it only enters the scalar offsets
+__device__ __forceinline__ void int4_load(Int4Raw& r, const Int4Ctx& x, int t0) {
+    const uint32_t so = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t0) * PROW);
+    const uint32_t ss = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t0) * 2);
+    r.k[0] = bld128(x.k, x.klane, so);
+    r.k[1] = bld128(x.k, x.klane + 16 * PROW, so);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) r.v[e] = *reinterpret_cast<const uint32_t*>(vl + tau(0, e) * PROW);
-    r.scl = x.sbase[t0 + (lane & 31)];
+    for (int e = 0; e < 8; ++e) r.v[e] = bld32(x.v, x.vlane + tau(0, e) * PROW, so);
+    r.sk[0] = bld16(x.ks, x.slane, ss);
+    r.sk[1] = bld16(x.ks, x.slane + 32, ss);
+    r.sv[0] = bld16(x.vs, x.slane, ss);
+    r.sv[1] = bld16(x.vs, x.slane + 32, ss);
 }
 
-// partial last group: every token index clamped to the last valid one
-__device__ __forceinline__ void int4_load_tail(Int4Raw& r, const Int4Ctx& x, int t0, int nv, int lane) {
-    const int c = lane & 15, kb = lane >> 4;
-    const uint8_t* kg = x.kbase + static_cast<int64_t>(t0) * PROW;
-    const uint8_t* vg = x.vbase + static_cast<int64_t>(t0) * PROW;
-#pragma unroll
-    for (int tile = 0; tile < 2; ++tile)
-        r.k[tile] = *reinterpret_cast<const uint4*>(kg + min(16 * tile + c, nv - 1) * PROW + 16 * kb);
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-        r.v[e] = *reinterpret_cast<const uint32_t*>(vg + min(tau(kb, e), nv - 1) * PROW + 4 * c);
-    r.scl = x.sbase[t0 + min(lane & 31, nv - 1)];
+// The four lanes of a quad hold the scales of tokens 4kb..4kb+3 of a tile;
+// quad broadcasts give every lane all four.
+__device__ __forceinline__ void quad_scales(uint32_t v, float* out) {
+    out[0] = f16_bits_to_f32(static_cast<uint16_t>(dpp_mov<0x00>(v)));
+    out[1] = f16_bits_to_f32(static_cast<uint16_t>(dpp_mov<0x55>(v)));
+    out[2] = f16_bits_to_f32(static_cast<uint16_t>(dpp_mov<0xaa>(v)));
+    out[3] = f16_bits_to_f32(static_cast<uint16_t>(dpp_mov<0xff>(v)));
 }
 
-template <bool MASK>
-__device__ __forceinline__ void int4_compute(WaveState& st, const Int4Raw& r, const f16x8 (&qop)[4],
-                                             uint16_t* scl, int nv, int lane, float qk) {
+__device__ __forceinline__ void int4_compute(WaveState& st, const Int4Raw& r, const f16x8 (&qop)[4], int nv,
+                                             int lane, float qk) {
     const int kb = lane >> 4;
-    // scales through this wavefront's LDS slot: 32 k scales then 32 v scales
-    scl[lane] = static_cast<uint16_t>(r.scl);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float sk[8], sv[8];
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        const u32x2 k4 = *reinterpret_cast<const u32x2*>(scl + 16 * half + 4 * kb);
-        const u32x2 v4 = *reinterpret_cast<const u32x2*>(scl + 32 + 16 * half + 4 * kb);
-        sk[4 * half + 0] = f16_bits_to_f32(k4[0] & 0xffff); sk[4 * half + 1] = f16_bits_to_f32(k4[0] >> 16);
-        sk[4 * half + 2] = f16_bits_to_f32(k4[1] & 0xffff); sk[4 * half + 3] = f16_bits_to_f32(k4[1] >> 16);
-        sv[4 * half + 0] = f16_bits_to_f32(v4[0] & 0xffff); sv[4 * half + 1] = f16_bits_to_f32(v4[0] >> 16);
-        sv[4 * half + 2] = f16_bits_to_f32(v4[1] & 0xffff); sv[4 * half + 3] = f16_bits_to_f32(v4[1] >> 16);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    quad_scales(r.sk[0], sk); quad_scales(r.sk[1], sk + 4);
+    quad_scales(r.sv[0], sv); quad_scales(r.sv[1], sv + 4);
     // QK: S^T tile = K_tile . Q^T (exact fp16 codes x fp16 q)
     float s[8];
 #pragma unroll
     for (int tile = 0; tile < 2; ++tile) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = mfma_f16(int4_to_f16x8(r.k[tile].x), qop[0], acc);
-        acc = mfma_f16(int4_to_f16x8(r.k[tile].y), qop[1], acc);
-        acc = mfma_f16(int4_to_f16x8(r.k[tile].z), qop[2], acc);
-        acc = mfma_f16(int4_to_f16x8(r.k[tile].w), qop[3], acc);
+        acc = mfma_f16(int4_to_f16x8(r.k[tile][0]), qop[0], acc);
+        acc = mfma_f16(int4_to_f16x8(r.k[tile][1]), qop[1], acc);
+        acc = mfma_f16(int4_to_f16x8(r.k[tile][2]), qop[2], acc);
+        acc = mfma_f16(int4_to_f16x8(r.k[tile][3]), qop[3], acc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) s[4 * tile + i] = acc[i] * (sk[4 * tile + i] * qk);
     }
-    if (MASK) {
+    if (nv < GROUP) {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             if (tau(kb, e) >= nv) s[e] = -INFINITY;
@@ -308,27 +326,20 @@ __device__ __forceinline__ void int4_compute(WaveState& st, const Int4Raw& r, co
 // bf16 segments: 16-token tiles
 // ---------------------------------------------------------------------------
 struct Bf16Raw {
-    uint4 k[4];            // token c, channels 32kb..32kb+31
-    uint4 v[4];            // slot e: token 4kb+e, channels 8c..8c+7
+    u32x4 k[4];            // token c, channels 32kb..32kb+31
+    u32x4 v[4];            // slot e: token 4kb+e, channels 8c..8c+7
 };
 
-__device__ __forceinline__ void bf16_load(Bf16Raw& r, const uint16_t* kg, const uint16_t* vg, int nv, int lane) {
+// rk / rv cover this chunk's rows; tokens past the chunk read zeros
+__device__ __forceinline__ void bf16_load(Bf16Raw& r, Rsrc rk, Rsrc rv, int t0, int lane) {
     const int c = lane & 15, kb = lane >> 4;
-    if (nv == TILE) {
-        const uint4* krow = reinterpret_cast<const uint4*>(kg + c * BROW + 32 * kb);
-        const uint16_t* vl = vg + 4 * kb * BROW + 8 * c;
+    const uint32_t so = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t0) * (BROW * 2));
+    const uint32_t ko = static_cast<uint32_t>(c) * (BROW * 2) + 64 * kb;
+    const uint32_t vo = static_cast<uint32_t>(4 * kb) * (BROW * 2) + 16 * c;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r.k[i] = krow[i];
+    for (int i = 0; i < 4; ++i) r.k[i] = bld128(rk, ko + 16 * i, so);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r.v[e] = *reinterpret_cast<const uint4*>(vl + e * BROW);
-    } else {
-        const uint4* krow = reinterpret_cast<const uint4*>(kg + min(c, nv - 1) * BROW + 32 * kb);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) r.k[i] = krow[i];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            r.v[e] = *reinterpret_cast<const uint4*>(vg + min(4 * kb + e, nv - 1) * BROW + 8 * c);
-    }
+    for (int e = 0; e < 4; ++e) r.v[e] = bld128(rv, vo + e * (BROW * 2), so);
 }
 
 __device__ __forceinline__ void bf16_compute(WaveState& st, const Bf16Raw& r, const bf16x8 (&qop)[4], int nv,
@@ -343,30 +354,144 @@ __device__ __forceinline__ void bf16_compute(WaveState& st, const Bf16Raw& r, co
     softmax_step<4>(st, s, false);
     const u32x2 pw = {pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
     const bf16x4 pop = __builtin_bit_cast(bf16x4, pw);
-    const uint32_t vd[4][4] = {{r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w}, {r.v[1].x, r.v[1].y, r.v[1].z, r.v[1].w},
-                               {r.v[2].x, r.v[2].y, r.v[2].z, r.v[2].w}, {r.v[3].x, r.v[3].y, r.v[3].z, r.v[3].w}};
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
         const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
         const int dw = nb >> 1;
-        const u32x2 w = {perm(vd[1][dw], vd[0][dw], sel), perm(vd[3][dw], vd[2][dw], sel)};
+        const u32x2 w = {perm(r.v[1][dw], r.v[0][dw], sel), perm(r.v[3][dw], r.v[2][dw], sel)};
         st.acc[nb] = mfma_bf16_k16(__builtin_bit_cast(bf16x4, w), pop, st.acc[nb]);
     }
 }
 
-__global__ __launch_bounds__(THREADS, 2) void decode_partial_kernel(DecArgs a) {
+// ---------------------------------------------------------------------------
+// merge of a head's partials by its last workgroup
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ u32x2 ld2_dev(Rsrc r, uint32_t off) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 16));    // sc1: device scope
+}
+__device__ __forceinline__ f32x4 ld4_dev(Rsrc r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// full-wavefront max / sum: DPP within each row of 16 (quad swaps, half-row
+// and row mirrors), then the gfx950 row swaps across rows
+__device__ __forceinline__ float wave_max64(float v) {
+    v = fmaxf(v, dppf<0xb1>(v));
+    v = fmaxf(v, dppf<0x4e>(v));
+    v = fmaxf(v, dppf<0x141>(v));
+    v = fmaxf(v, dppf<0x140>(v));
+    return col_max(v);
+}
+__device__ __forceinline__ float wave_sum64(float v) {
+    v += dppf<0xb1>(v);
+    v += dppf<0x4e>(v);
+    v += dppf<0x141>(v);
+    v += dppf<0x140>(v);
+    return col_sum(v);
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One wavefront per query head g.  Lane (h, q) = (lane >> 5, lane & 31) sums
+// channels 4q..4q+3 over the partials w = 2j + h (a row swap adds the two
+// halves).  Lane w computes the weight exp2(m_w - M_g) of partial w (and
+// w + 64, ...); the wavefront max / sum give M_g and the denominator
+// sum_w exp2(m_w - M_g) l_w; the weights reach every lane through a
+// per-wavefront LDS table (same-address reads broadcast).  The first batch of
+// partial loads is issued before the (m, l) loads, so the merge is about one
+// memory round trip while nwg <= 2 * MJ.
+__device__ __forceinline__ void merge_head(const DecArgs& a, int head, float* s_wt) {
+    const int G = a.G, nwg = a.nwg;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane >> 5, q = lane & 31;
+    const int npair = nwg * G;
+    const Rsrc rp = make_rsrc(a.part + static_cast<int64_t>(head) * npair * D, static_cast<uint32_t>(npair) * D * 4);
+    const Rsrc rm = make_rsrc(a.ml + static_cast<int64_t>(head) * npair * 2, static_cast<uint32_t>(npair) * 8);
+    float* wt = s_wt + wave * MAX_NWG;
+    const int npr = (nwg + 1) / 2;                   // partial pairs
+    for (int g = wave; g < G; g += WAVES) {
+        const uint32_t pbase = static_cast<uint32_t>(((h * G + g) * D + 4 * q) * 4);
+        const uint32_t pstep = static_cast<uint32_t>(2 * G * D * 4);
+        f32x4 px[MJ];
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+            if (j < npr) px[j] = ld4_dev(rp, pbase + j * pstep);   // past nwg: zeros
+        u32x2 mlr[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (64 * k < nwg) mlr[k] = ld2_dev(rm, static_cast<uint32_t>(((lane + 64 * k) * G + g) * 8));
+        float M = M_INIT;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (64 * k < nwg && lane + 64 * k < nwg) M = fmaxf(M, __uint_as_float(mlr[k][0]));
+        M = wave_max64(M);
+        float den = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (64 * k < nwg) {
+                const bool ok = lane + 64 * k < nwg;
+                const float w = ok ? fast_exp2(__uint_as_float(mlr[k][0]) - M) : 0.f;
+                den += ok ? w * __uint_as_float(mlr[k][1]) : 0.f;
+                wt[lane + 64 * k] = w;
+            }
+        }
+        den = wave_sum64(den);
+        wave_sync_lds();
+        const int nj = (nwg + 1 - h) / 2;            // partials of this half
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+            if (j < nj) acc += wt[2 * j + h] * px[j];
+        for (int j0 = MJ; j0 < npr; j0 += MJ) {      // nwg > 2 * MJ: one more round trip per batch
+#pragma unroll
+            for (int j = 0; j < MJ; ++j)
+                if (j0 + j < npr) px[j] = ld4_dev(rp, pbase + (j0 + j) * pstep);
+#pragma unroll
+            for (int j = 0; j < MJ; ++j)
+                if (j0 + j < nj) acc += wt[2 * (j0 + j) + h] * px[j];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i]), false, false);
+            acc[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+        if (h == 0) {
+            const u32x2 o = {static_cast<uint32_t>(f32_to_bf16_rne(den > 0.f ? acc[0] / den : 0.f)) |
+                                 (static_cast<uint32_t>(f32_to_bf16_rne(den > 0.f ? acc[1] / den : 0.f)) << 16),
+                             static_cast<uint32_t>(f32_to_bf16_rne(den > 0.f ? acc[2] / den : 0.f)) |
+                                 (static_cast<uint32_t>(f32_to_bf16_rne(den > 0.f ? acc[3] / den : 0.f)) << 16)};
+            *reinterpret_cast<u32x2*>(a.out + static_cast<int64_t>(head * G + g) * a.out_stride + 4 * q) = o;
+        }
+        wave_sync_lds();                             // the table is rewritten for the next g
+    }
+}
+
+// ---------------------------------------------------------------------------
+// the kernel
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
     const int nh = a.bh_kv;
     const int head = blockIdx.x % nh;
-    const int wg = blockIdx.x / nh;
+    const int wgi = blockIdx.x / nh;
+    const int wg = wgi < a.n4 ? wgi + a.n16 : wgi - a.n4;      // chunk index: bf16 chunks first
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, kb = lane >> 4;
     const int G = a.G;
 
-    extern __shared__ float s_acc[];               // [WAVES][G][D+1]
+    extern __shared__ float s_acc[];               // [WAVES][G][D+1]; later the merge weights
     __shared__ float s_m[WAVES][16];
     __shared__ float s_l[WAVES][16];
-    __shared__ __align__(16) uint16_t s_scl[WAVES][64];
+    __shared__ int s_last;
 
     WaveState st;
     st.m = M_INIT;
@@ -375,62 +500,72 @@ __global__ __launch_bounds__(THREADS, 2) void decode_partial_kernel(DecArgs a) {
     for (int nb = 0; nb < 8; ++nb) st.acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
     st.ones = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Q row of head c (zero for padding columns): channels 32kb..32kb+31
-    uint4 qraw[4] = {};
-    if (c < G) {
-        const uint4* qrow = reinterpret_cast<const uint4*>(a.q + static_cast<int64_t>(head * G + c) * a.q_stride + 32 * kb);
+    // Q row of head c (zero for padding columns c >= G): channels 32kb..32kb+31
+    u32x4 qraw[4];
+    {
+        const Rsrc rq = make_rsrc(a.q + static_cast<int64_t>(head) * G * a.q_stride,
+                                  static_cast<uint32_t>(G * a.q_stride * 2));
+        const uint32_t qo = static_cast<uint32_t>(c * a.q_stride * 2 + 64 * kb);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qraw[i] = qrow[i];
+        for (int i = 0; i < 4; ++i) qraw[i] = bld128(rq, qo + 16 * i);
     }
 
     if (wg < a.n16) {
-        // ---------------- bf16 chunk: tiles wave, wave+WAVES ----------------
+        // ---------------- bf16 chunk: tiles wave, wave+WAVES, ... ----------------
         int w = wg, seg = 0;
         while (seg < 2 && w >= a.nseg[seg]) { w -= a.nseg[seg]; ++seg; }
-        const int lo = w * CHUNK16;
-        const int hi = min(lo + CHUNK16, a.sn[seg]);
+        const int lo = w * a.bsplit;
+        const int n = min(a.bsplit, a.sn[seg] - lo);
         const bf16x8 qop[4] = {__builtin_bit_cast(bf16x8, qraw[0]), __builtin_bit_cast(bf16x8, qraw[1]),
                                __builtin_bit_cast(bf16x8, qraw[2]), __builtin_bit_cast(bf16x8, qraw[3])};
-        const uint16_t* kbase = a.sk[seg] + static_cast<int64_t>(head) * a.sk_bh[seg];
-        const uint16_t* vbase = a.sv[seg] + static_cast<int64_t>(head) * a.sv_bh[seg];
-        const int t0 = lo + wave * TILE;
-        const int t1 = t0 + WAVES * TILE;
+        const uint16_t* kbase = a.sk[seg] + static_cast<int64_t>(head) * a.sk_bh[seg] + static_cast<int64_t>(lo) * BROW;
+        const uint16_t* vbase = a.sv[seg] + static_cast<int64_t>(head) * a.sv_bh[seg] + static_cast<int64_t>(lo) * BROW;
+        const uint32_t nbytes = static_cast<uint32_t>(n) * (BROW * 2);
+        const Rsrc rk = make_rsrc(kbase, nbytes), rv = make_rsrc(vbase, nbytes);
+        // tiles wave, wave+WAVES, ... through a two-deep register ring
+        constexpr int TSTRIDE = WAVES * TILE;
+        const int ntile = (n + TILE - 1) / TILE;
+        const int nmine = ntile > wave ? (ntile - wave + WAVES - 1) / WAVES : 0;
+        const int t0 = wave * TILE;
         Bf16Raw r0, r1;
-        if (t0 < hi) bf16_load(r0, kbase + static_cast<int64_t>(t0) * BROW, vbase + static_cast<int64_t>(t0) * BROW,
-                               min(TILE, hi - t0), lane);
-        if (t1 < hi) bf16_load(r1, kbase + static_cast<int64_t>(t1) * BROW, vbase + static_cast<int64_t>(t1) * BROW,
-                               min(TILE, hi - t1), lane);
-        if (t0 < hi) bf16_compute(st, r0, qop, min(TILE, hi - t0), lane, a.qk_scale);
-        if (t1 < hi) bf16_compute(st, r1, qop, min(TILE, hi - t1), lane, a.qk_scale);
+        bf16_load(r0, rk, rv, t0, lane);
+        for (int i = 0; i < nmine; i += 2) {
+            const int t = t0 + i * TSTRIDE;
+            bf16_load(r1, rk, rv, t + TSTRIDE, lane);
+            bf16_compute(st, r0, qop, n - t, lane, a.qk_scale);
+            if (i + 1 >= nmine) break;
+            bf16_load(r0, rk, rv, t + 2 * TSTRIDE, lane);
+            bf16_compute(st, r1, qop, n - t - TSTRIDE, lane, a.qk_scale);
+        }
     } else {
         // ---------------- int4 chunk: groups wave, wave+WAVES, ... ----------------
         const int lo = (wg - a.n16) * a.split;
+        const int ntok = min(a.split, a.n_quant - lo);
         Int4Ctx x;
-        x.hi = min(lo + a.split, a.n_quant);
-        x.kbase = a.kp + static_cast<int64_t>(head) * a.kp_bh;
-        x.vbase = a.vp + static_cast<int64_t>(head) * a.vp_bh;
-        x.sbase = lane < 32 ? a.ks + static_cast<int64_t>(head) * a.ks_bh : a.vs + static_cast<int64_t>(head) * a.vs_bh;
+        x.k = make_rsrc(a.kp + static_cast<int64_t>(head) * a.kp_bh + static_cast<int64_t>(lo) * PROW,
+                        static_cast<uint32_t>(ntok) * PROW);
+        x.v = make_rsrc(a.vp + static_cast<int64_t>(head) * a.vp_bh + static_cast<int64_t>(lo) * PROW,
+                        static_cast<uint32_t>(ntok) * PROW);
+        x.ks = make_rsrc(a.ks + static_cast<int64_t>(head) * a.ks_bh + lo, static_cast<uint32_t>(ntok) * 2);
+        x.vs = make_rsrc(a.vs + static_cast<int64_t>(head) * a.vs_bh + lo, static_cast<uint32_t>(ntok) * 2);
         x.klane = static_cast<uint32_t>(c * PROW + 16 * kb);
         x.vlane = static_cast<uint32_t>(4 * kb * PROW + 4 * c);
-        // full groups g = wave, wave+WAVES, ... < nfull go through a three-deep
-        // register ring (two groups' loads in flight while one is computed);
-        // the one partial group of a chunk, if any, is done last with clamping.
+        x.slane = static_cast<uint32_t>((4 * kb + (c & 3)) * 2);
+        // groups wave, wave+WAVES, ... of the chunk through a three-deep
+        // register ring: two groups' loads in flight while one is computed
         constexpr int STRIDE = WAVES * GROUP;
-        const int ntok = max(0, x.hi - lo);
-        const int nfull = ntok / GROUP;
-        const int tail = ntok - nfull * GROUP;
-        const int nmine = nfull > wave ? (nfull - wave + WAVES - 1) / WAVES : 0;
-        const int t0 = lo + wave * GROUP;
-        // issue the first two groups' loads before anything waits on Q
+        const int ngrp = (ntok + GROUP - 1) / GROUP;
+        const int nmine = ngrp > wave ? (ngrp - wave + WAVES - 1) / WAVES : 0;
+        const int t0 = wave * GROUP;
         Int4Raw b0, b1, b2;
-        if (nmine > 0) int4_load_full(b0, x, t0, lane);
-        if (nmine > 1) int4_load_full(b1, x, t0 + STRIDE, lane);
+        int4_load(b0, x, t0);
+        int4_load(b1, x, t0 + STRIDE);
 
         // Q -> fp16 in int4 slot order, pre-scaled by 2^-ex so |q| < 2^15
         float qf[32];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t ww[4] = {qraw[i].x, qraw[i].y, qraw[i].z, qraw[i].w};
+            const uint32_t ww[4] = {qraw[i][0], qraw[i][1], qraw[i][2], qraw[i][3]};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 qf[8 * i + 2 * j] = __uint_as_float(ww[j] << 16);
@@ -454,21 +589,16 @@ __global__ __launch_bounds__(THREADS, 2) void decode_partial_kernel(DecArgs a) {
             qop[sidx] = v;
         }
         const float qk = a.qk_scale * ldexpf(1.0f, ex);
-        uint16_t* scl = s_scl[wave];
         for (int i = 0; i < nmine; i += 3) {
             const int t = t0 + i * STRIDE;
-            if (i + 2 < nmine) int4_load_full(b2, x, t + 2 * STRIDE, lane);
-            int4_compute<false>(st, b0, qop, scl, GROUP, lane, qk);
+            int4_load(b2, x, t + 2 * STRIDE);
+            int4_compute(st, b0, qop, ntok - t, lane, qk);
             if (i + 1 >= nmine) break;
-            if (i + 3 < nmine) int4_load_full(b0, x, t + 3 * STRIDE, lane);
-            int4_compute<false>(st, b1, qop, scl, GROUP, lane, qk);
+            int4_load(b0, x, t + 3 * STRIDE);
+            int4_compute(st, b1, qop, ntok - t - STRIDE, lane, qk);
             if (i + 2 >= nmine) break;
-            if (i + 4 < nmine) int4_load_full(b1, x, t + 4 * STRIDE, lane);
-            int4_compute<false>(st, b2, qop, scl, GROUP, lane, qk);
-        }
-        if (tail > 0 && wave == nfull % WAVES) {
-            int4_load_tail(b0, x, lo + nfull * GROUP, tail, lane);
-            int4_compute<true>(st, b0, qop, scl, tail, lane, qk);
+            int4_load(b1, x, t + 4 * STRIDE);
+            int4_compute(st, b2, qop, ntok - t - 2 * STRIDE, lane, qk);
         }
         // remove the +136 offset of the V codes: acc -= 136 * sum_t P'
         const float corr = 136.0f * st.ones[0];
@@ -491,18 +621,24 @@ __global__ __launch_bounds__(THREADS, 2) void decode_partial_kernel(DecArgs a) {
     }
     __syncthreads();
 
-    // ---- workgroup merge -> partial acc[G][D] and (m, l)[G] ---------------------
+    // ---- workgroup merge -> partial acc[G][D] and (m, l)[G] ----------------------
     const int64_t slot = static_cast<int64_t>(head) * a.nwg + wg;
-    float* part = a.part + slot * G * D;
-    for (int idx = threadIdx.x; idx < G * D; idx += THREADS) {
-        const int g = idx / D, ch = idx % D;
-        float M = s_m[0][g];
+    {
+        const Rsrc rpart = make_rsrc(a.part + slot * G * D, static_cast<uint32_t>(G * D * 4));
+        for (int o = threadIdx.x; o < G * (D / 4); o += THREADS) {
+            const int g = o / (D / 4), ch = 4 * (o % (D / 4));
+            float M = s_m[0][g];
 #pragma unroll
-        for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_m[w][g]);
-        float accv = 0.f;
+            for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_m[w][g]);
+            f32x4 accv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) accv += fast_exp2(s_m[w][g] - M) * s_acc[(w * G + g) * (D + 1) + ch];
-        part[idx] = accv;
+            for (int w = 0; w < WAVES; ++w) {
+                const float wt = fast_exp2(s_m[w][g] - M);
+                const float* row = s_acc + (w * G + g) * (D + 1) + ch;
+                accv += wt * f32x4{row[0], row[1], row[2], row[3]};
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, accv), rpart, o * 16, 0, 16);   // sc1
+        }
     }
     if (threadIdx.x < G) {
         const int g = threadIdx.x;
@@ -512,82 +648,20 @@ __global__ __launch_bounds__(THREADS, 2) void decode_partial_kernel(DecArgs a) {
         float lv = 0.f;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) lv += fast_exp2(s_m[w][g] - M) * s_l[w][g];
-        a.ml[(slot * G + g) * 2] = M;
-        a.ml[(slot * G + g) * 2 + 1] = lv;
+        __hip_atomic_store(a.ml + (slot * G + g) * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.ml + (slot * G + g) * 2 + 1, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-}
-
-// ---------------------------------------------------------------------------
-// merge: one workgroup per (KV head, MSLICE-channel slice)
-// ---------------------------------------------------------------------------
-constexpr int MERGE_PREFETCH = 8;        // partials per thread loaded before the first barrier
-
-__global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(DecArgs a) {
-    const int head = blockIdx.x / (D / MSLICE);
-    const int ch0 = (blockIdx.x % (D / MSLICE)) * MSLICE;
-    const int G = a.G;
-    const int nwg = a.nwg;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    extern __shared__ float sm[];
-    float* t_m = sm;                               // [nwg][G]
-    float* t_l = sm + nwg * G;                     // [nwg][G]
-    float* red = sm + 2 * nwg * G;                 // [slices][G][MSLICE]
-    __shared__ float s_M[16], s_den[16];
-    // thread -> (output o = g*MSLICE + channel, slice sl of the partials)
-    const int outs = G * MSLICE;
-    const int slices = max(1, MERGE_THREADS / outs);
-    const int o = tid % outs, sl = tid / outs;
-    const bool active = tid < outs * slices;
-    const int g = o / MSLICE, ch = ch0 + o % MSLICE;
-    const float* hp = a.part + (static_cast<int64_t>(head) * nwg * G + g) * D + ch;   // + w*G*D
-    // the first MERGE_PREFETCH partials of this thread, issued before any wait
-    float x[MERGE_PREFETCH];
-#pragma unroll
-    for (int j = 0; j < MERGE_PREFETCH; ++j) {
-        const int w = sl + j * slices;
-        x[j] = (active && w < nwg) ? hp[static_cast<int64_t>(w) * G * D] : 0.f;
-    }
-    const float* ml = a.ml + static_cast<int64_t>(head) * nwg * G * 2;
-    for (int idx = tid; idx < nwg * G; idx += MERGE_THREADS) {
-        t_m[idx] = ml[2 * idx];
-        t_l[idx] = ml[2 * idx + 1];
+    // every store of this workgroup acknowledged before its arrival is counted
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(a.cnt + head * CNT_PAD, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old == static_cast<uint32_t>(a.nwg - 1));
     }
     __syncthreads();
-    for (int gg = wave; gg < G; gg += MERGE_THREADS / 64) {
-        float M = M_INIT;
-        for (int w = lane; w < nwg; w += 64) M = fmaxf(M, t_m[w * G + gg]);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-        float den = 0.f;
-        for (int w = lane; w < nwg; w += 64) den += fast_exp2(t_m[w * G + gg] - M) * t_l[w * G + gg];
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off, 64);
-        if (lane == 0) {
-            s_M[gg] = M;
-            s_den[gg] = den;
-        }
-    }
-    __syncthreads();
-    if (active) {
-        const float M = s_M[g];
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < MERGE_PREFETCH; ++j) {
-            const int w = sl + j * slices;
-            if (w < nwg) acc += fast_exp2(t_m[w * G + g] - M) * x[j];
-        }
-        for (int w = sl + MERGE_PREFETCH * slices; w < nwg; w += slices)
-            acc += fast_exp2(t_m[w * G + g] - M) * hp[static_cast<int64_t>(w) * G * D];
-        red[sl * outs + o] = acc;
-    }
-    __syncthreads();
-    if (tid < outs) {
-        float num = 0.f;
-        for (int k = 0; k < slices; ++k) num += red[k * outs + tid];
-        const float den = s_den[g];
-        const float r = den > 0.f ? num / den : 0.f;
-        a.out[static_cast<int64_t>(head * G + g) * a.out_stride + ch] = f32_to_bf16_rne(r);
+    if (s_last) {
+        if (threadIdx.x == 0) __hip_atomic_store(a.cnt + head * CNT_PAD, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        merge_head(a, head, s_acc);
     }
 }
 
@@ -596,51 +670,69 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(DecArgs a) 
 // ---------------------------------------------------------------------------
 
 struct Plan {
-    int split, n4, nseg[3], n16, nwg;
+    int split, bsplit, n4, nseg[3], n16, nwg;
 };
 
-// int4 tokens per workgroup: at least one 32-token group per wavefront, at
-// most ~32 partials per head (bounded merge traffic), and enough workgroups
-// (~2048) to cover the 256 CUs several times when the batch is small.
-int choose_split(int64_t n_quant, int bh_kv, int requested) {
-    auto round_up = [](int64_t x, int64_t m) { return ((x + m - 1) / m) * m; };
-    if (requested > 0) return static_cast<int>(round_up(requested, CHUNK4_MIN));
-    int64_t split = CHUNK4_MIN;
-    split = std::max<int64_t>(split, round_up((n_quant + 31) / 32, CHUNK4_MIN));
-    split = std::max<int64_t>(split, round_up((n_quant * bh_kv + 2047) / 2048, CHUNK4_MIN));
-    return static_cast<int>(std::min<int64_t>(split, 1 << 30));
+size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Tokens per workgroup chunk.  Few KV heads (small batch): about 32 chunks
+// per head, so the whole chip works on one step and each wavefront streams a
+// handful of groups.  Many heads: a large chunk, which keeps the
+// per-workgroup prologue / partial / merge costs low; the grid still holds
+// many workgroups per CU.  `gran` is the smallest chunk.
+int64_t auto_split(int64_t n, int bh_kv, int64_t gran, int64_t big) {
+    if (bh_kv >= 32) return big;
+    int64_t split = gran;
+    while (split < big && split * 32 < n) split *= 2;
+    return split;
 }
 
 Plan make_plan(int64_t n_quant, const int64_t seg_n[3], int bh_kv, int G, int requested) {
+    auto round_up = [](int64_t x, int64_t m) { return ((x + m - 1) / m) * m; };
     Plan p;
-    p.split = choose_split(n_quant, bh_kv, requested);
-    p.n16 = 0;
-    for (int s = 0; s < 3; ++s) {
-        p.nseg[s] = static_cast<int>((seg_n[s] + CHUNK16 - 1) / CHUNK16);
-        p.n16 += p.nseg[s];
-    }
-    // keep nwg * G within the merge tables
+    int64_t split = requested > 0 ? std::min<int64_t>(round_up(requested, CHUNK4_MIN), 1 << 30)
+                                  : auto_split(n_quant, bh_kv, CHUNK4_MIN, SPLIT_MAX_SMALL);
+    // bf16 chunks: 128 tokens beside an int4 prefix (the segments are short);
+    // alone (the full-precision comparator) they are split like the prefix,
+    // a bf16 token costing four int4 tokens of bandwidth.
+    int64_t bsplit = CHUNK16;
+    if (n_quant == 0) bsplit = auto_split(seg_n[0] + seg_n[1] + seg_n[2], bh_kv, CHUNK16, SPLIT_MAX_SMALL / 4);
+    // keep the chunks of a head within the merge tables
     while (true) {
-        p.n4 = static_cast<int>((n_quant + p.split - 1) / p.split);
+        p.n4 = static_cast<int>((n_quant + split - 1) / split);
+        p.n16 = 0;
+        for (int s = 0; s < 3; ++s) {
+            p.nseg[s] = static_cast<int>((seg_n[s] + bsplit - 1) / bsplit);
+            p.n16 += p.nseg[s];
+        }
         p.nwg = p.n4 + p.n16;
-        if (static_cast<int64_t>(p.nwg) * G <= MAX_PARTIALS || p.n4 <= 1) break;
-        p.split *= 2;
+        if (static_cast<int64_t>(p.nwg) * G <= MAX_PARTIALS && p.nwg <= MAX_NWG) break;
+        if (p.n4 > p.n16 && p.n4 > 1) split *= 2;
+        else bsplit *= 2;
     }
+    p.split = static_cast<int>(split);
+    p.bsplit = static_cast<int>(bsplit);
     return p;
 }
 
-size_t partial_lds_bytes(int G) { return static_cast<size_t>(WAVES) * G * (D + 1) * sizeof(float); }
-
-size_t merge_lds_bytes(const Plan& pl, int G) {
-    const int outs = G * MSLICE;
-    const int slices = std::max(1, MERGE_THREADS / outs);
-    return (2 * static_cast<size_t>(pl.nwg) * G + static_cast<size_t>(slices) * outs) * sizeof(float);
+size_t lds_bytes(int G) {
+    return std::max(static_cast<size_t>(WAVES) * G * (D + 1), static_cast<size_t>(WAVES) * MAX_NWG) * sizeof(float);
 }
 
-size_t workspace_bytes(const Plan& pl, int bh_kv, int G) {
+// workspace: [arrival counters: CNT_CAP slots, 128 B apart][(m, l) table][partials].
+// The counter area has the same size and place for every call, so the data of
+// one call never lands on the counters of another call of a different shape.
+struct Layout {
+    size_t cnt, ml, part, total;
+};
+Layout layout(const Plan& pl, int bh_kv, int G) {
     const size_t slots = static_cast<size_t>(bh_kv) * std::max(pl.nwg, 1) * G;
-    const size_t part = ((slots * D * sizeof(float) + 255) / 256) * 256;
-    return part + slots * 2 * sizeof(float);
+    Layout L;
+    L.cnt = 0;
+    L.ml = static_cast<size_t>(CNT_CAP) * CNT_PAD * sizeof(uint32_t);
+    L.part = L.ml + round256(slots * 2 * sizeof(float));
+    L.total = L.part + round256(slots * D * sizeof(float));
+    return L;
 }
 
 int validate(const hyq_decode_params* p) {
@@ -652,12 +744,15 @@ int validate(const hyq_decode_params* p) {
     if (p->kv_repeat < 1 || p->kv_repeat > 16)
         return fail(HYQ_ENOTSUP, "kv_repeat must be in [1, 16], got " + std::to_string(p->kv_repeat));
     if (p->bh_kv < 0) return fail(HYQ_EINVAL, "bh_kv < 0");
-    if (p->bh_kv > (1 << 24)) return fail(HYQ_ENOTSUP, "bh_kv too large");
-    if (p->n_quant < 0 || p->n_quant > (1 << 30)) return fail(HYQ_EINVAL, "bad n_quant");
+    if (p->bh_kv > CNT_CAP) return fail(HYQ_ENOTSUP, "bh_kv (batch * kv heads) above " + std::to_string(CNT_CAP));
+    if (p->n_quant < 0 || p->n_quant > (1 << 24)) return fail(HYQ_EINVAL, "bad n_quant");
     if (p->bh_kv == 0) return HYQ_OK;
     if (!p->q || !p->out) return fail(HYQ_EINVAL, "null q/out");
-    if (!aligned(p->q, 16) || p->q_stride % 8) return fail(HYQ_EINVAL, "q must be 16-byte aligned, row stride % 8 == 0");
-    if (!aligned(p->out, 2)) return fail(HYQ_EINVAL, "out misaligned");
+    if (!aligned(p->q, 16) || p->q_stride % 8 || p->q_stride < D)
+        return fail(HYQ_EINVAL, "q must be 16-byte aligned with row stride % 8 == 0 and >= head_dim");
+    if (static_cast<int64_t>(p->kv_repeat) * p->q_stride * 2 > 0x7fffffffLL) return fail(HYQ_ENOTSUP, "q row stride too large");
+    if (!aligned(p->out, 8) || p->out_stride % 4 || p->out_stride < D)
+        return fail(HYQ_EINVAL, "out must be 8-byte aligned with row stride % 4 == 0 and >= head_dim");
     if (p->n_quant > 0) {
         if (!p->k_packed || !p->v_packed || !p->k_scale || !p->v_scale) return fail(HYQ_EINVAL, "null prefix tensor");
         if (p->kp_stride_n != PROW || p->vp_stride_n != PROW)
@@ -670,7 +765,7 @@ int validate(const hyq_decode_params* p) {
             return fail(HYQ_EINVAL, "scales must be 2-byte aligned");
     }
     for (int s = 0; s < 3; ++s) {
-        if (p->seg_n[s] < 0 || p->seg_n[s] > (1 << 30)) return fail(HYQ_EINVAL, "bad segment length");
+        if (p->seg_n[s] < 0 || p->seg_n[s] > (1 << 23)) return fail(HYQ_EINVAL, "bad segment length");
         if (p->seg_n[s] == 0) continue;
         if (!p->seg_k[s] || !p->seg_v[s]) return fail(HYQ_EINVAL, "null bf16 segment");
         if (p->seg_k_stride_n[s] != BROW || p->seg_v_stride_n[s] != BROW)
@@ -690,7 +785,7 @@ using namespace hyq;
 extern "C" size_t hyq_decode_workspace_size(const hyq_decode_params* p) {
     if (validate(p) != HYQ_OK) return 0;
     const Plan pl = make_plan(p->n_quant, p->seg_n, p->bh_kv, p->kv_repeat, p->split_tokens);
-    return workspace_bytes(pl, p->bh_kv, p->kv_repeat);
+    return layout(pl, p->bh_kv, p->kv_repeat).total;
 }
 
 extern "C" int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace, size_t ws_bytes, void* stream) {
@@ -699,11 +794,11 @@ extern "C" int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace, si
     if (p->bh_kv == 0) return HYQ_OK;
     const Plan pl = make_plan(p->n_quant, p->seg_n, p->bh_kv, p->kv_repeat, p->split_tokens);
     if (pl.nwg == 0) return fail(HYQ_EINVAL, "decode with zero key tokens");
-    if (static_cast<int64_t>(pl.nwg) * p->kv_repeat > MAX_PARTIALS)
+    if (static_cast<int64_t>(pl.nwg) * p->kv_repeat > MAX_PARTIALS || pl.nwg > MAX_NWG)
         return fail(HYQ_ENOTSUP, "too many bf16 chunks per head for the merge tables");
-    const size_t need = workspace_bytes(pl, p->bh_kv, p->kv_repeat);
-    if (!workspace || ws_bytes < need || !aligned(workspace, 256))
-        return fail(HYQ_ENOSPC, "decode workspace too small or misaligned: need " + std::to_string(need) + " bytes");
+    const Layout L = layout(pl, p->bh_kv, p->kv_repeat);
+    if (!workspace || ws_bytes < L.total || !aligned(workspace, 256))
+        return fail(HYQ_ENOSPC, "decode workspace too small or misaligned: need " + std::to_string(L.total) + " bytes");
     DecArgs a{};
     a.q = p->q; a.q_stride = p->q_stride;
     a.out = p->out; a.out_stride = p->out_stride;
@@ -722,27 +817,23 @@ extern "C" int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace, si
     a.G = p->kv_repeat;
     a.bh_kv = p->bh_kv;
     a.qk_scale = p->sm_scale * LOG2E;
-    a.split = pl.split; a.n4 = pl.n4; a.n16 = pl.n16; a.nwg = pl.nwg;
-    const size_t slots = static_cast<size_t>(p->bh_kv) * pl.nwg * p->kv_repeat;
-    const size_t part_bytes = ((slots * D * sizeof(float) + 255) / 256) * 256;
-    a.part = static_cast<float*>(workspace);
-    a.ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes);
+    a.split = pl.split; a.bsplit = pl.bsplit; a.n4 = pl.n4; a.n16 = pl.n16; a.nwg = pl.nwg;
+    char* ws = static_cast<char*>(workspace);
+    a.cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
+    a.ml = reinterpret_cast<float*>(ws + L.ml);
+    a.part = reinterpret_cast<float*>(ws + L.part);
     const int64_t blocks = static_cast<int64_t>(pl.nwg) * p->bh_kv;
     if (blocks > 0x7fffffffLL) return fail(HYQ_ENOTSUP, "grid too large");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    decode_partial_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(THREADS), partial_lds_bytes(p->kv_repeat), s>>>(a);
-    rc = check_launch("hyq_decode_hybrid (partial)");
-    if (rc != HYQ_OK) return rc;
-    decode_merge_kernel<<<dim3(static_cast<unsigned>(p->bh_kv * (D / MSLICE))), dim3(MERGE_THREADS),
-                          merge_lds_bytes(pl, p->kv_repeat), s>>>(a);
-    return check_launch("hyq_decode_hybrid (merge)");
+    decode_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(THREADS), lds_bytes(p->kv_repeat), s>>>(a);
+    return check_launch("hyq_decode_hybrid");
 }
 
 extern "C" size_t hyq_decode_bf16_workspace_size(int32_t bh_kv, int32_t kv_repeat, int64_t n, int32_t d) {
     if (bh_kv < 0 || kv_repeat < 1 || kv_repeat > 16 || d != D || n < 0) return 0;
     const int64_t seg_n[3] = {n, 0, 0};
     const Plan pl = make_plan(0, seg_n, bh_kv, kv_repeat, 0);
-    return workspace_bytes(pl, bh_kv, kv_repeat);
+    return layout(pl, bh_kv, kv_repeat).total;
 }
 
 extern "C" int hyq_decode_bf16(const uint16_t* q, int64_t q_stride, uint16_t* out, int64_t out_stride,

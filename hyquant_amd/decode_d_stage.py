@@ -50,14 +50,17 @@ _ws_cache: dict = {}
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    """Split-K partial buffer, cached per (device, stream) like the
-    reference's split-K buffers (src/ops/decode_d_stage.py:797-811).  Calls
-    on one stream are ordered; different streams get their own buffer."""
+    """Split-K workspace (arrival counters + partials), cached per (device,
+    stream) like the reference's split-K buffers
+    (src/ops/decode_d_stage.py:797-811).  It is zero-filled once when
+    allocated (the counters must start at zero; every call leaves them at
+    zero).  Calls on one stream are ordered; different streams get their own
+    buffer."""
     key = (device.index, stream)
     with _ws_lock:
         buf = _ws_cache.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
             _ws_cache[key] = buf
         return buf
 

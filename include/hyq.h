@@ -80,11 +80,17 @@ typedef struct hyq_decode_params {
     float sm_scale;       /* softmax scale (reference default head_dim^-0.5)   */
     int32_t split_tokens; /* int4 tokens per workgroup; 0 = automatic           */
 } hyq_decode_params;
+/* Alignment: q 16-byte aligned (row stride % 8 == 0), out 8-byte aligned (row
+ * stride % 4 == 0), k_packed 16-byte aligned, bf16 segments 16-byte aligned. */
 
-/* Bytes of device workspace hyq_decode_hybrid needs for these parameters
- * (per-chunk partial results; no initialisation needed).  The call enqueues
- * two kernels on `stream`; calls that share one workspace must be ordered on
- * one stream. */
+/* Bytes of device workspace hyq_decode_hybrid needs for these parameters:
+ * a fixed 2 MiB area of per-head arrival counters (bh_kv <= 16384) followed
+ * by the per-chunk partial results.  The workspace must be zero-filled once
+ * when it is allocated; every completed call leaves the counter area at zero
+ * again, so a workspace is reusable across calls of any shape without
+ * clearing.  The call
+ * enqueues one kernel on `stream`; calls that share one workspace must be
+ * ordered on one stream. */
 size_t hyq_decode_workspace_size(const hyq_decode_params* p);
 
 int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace,

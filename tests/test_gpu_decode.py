@@ -142,3 +142,38 @@ def test_bf16_comparator(n, G):
     ref = O.decode_fp64(q, kp, kp, ks, ks, k, v, e, e, e, e, kv_repeat=G)
     ref_abs = O.decode_fp64(q, kp, kp, ks, ks, k, v, e, e, e, e, kv_repeat=G, abs_v=True)
     _check(f"bf16 full n={n} G={G}", out.float().cpu().numpy(), ref, ref_abs=ref_abs)
+
+
+def test_decode_workspace_reuse_interleaved():
+    """Calls of different shapes and states issued back to back on one stream
+    share the cached workspace: each launch's arrival counters must start at
+    zero and end at zero, and no launch may read another's partials."""
+    import hyquant_amd as hq
+    dev = torch.device("cuda")
+    cfgs = {
+        "A": dict(B=1, HQ=32, HKV=8, N=8192, S=64, seed=7),
+        "B": dict(B=2, HQ=64, HKV=8, N=2048, S=64, seed=8),     # G = 8
+        "C": dict(B=8, HQ=32, HKV=8, N=4096, S=64, seed=9),     # 64 KV heads: largest split
+    }
+    data = {}
+    for name, cfg in cfgs.items():
+        inp = O.make_decode_inputs(W=128, **cfg)
+        st = O.build_decode_state(inp)
+        data[name] = (inp, st, state_to_device(st, dev), to_dev_bf16(inp.q_dec, dev), cfg["HQ"] // cfg["HKV"])
+
+    def call(name, **kw):
+        _, _, t, q, G = data[name]
+        return hq.fused_d_stage_decode(q, t["k_packed"], t["v_packed"], t["k_scale"], t["v_scale"],
+                                       t["k_topk"], t["v_topk"], t["k_staging"], t["v_staging"],
+                                       t["k_window"], t["v_window"], 4, 4, kv_repeat=G, **kw)
+
+    order = ["A", "B", "C", "A", "C", "B"]
+    outs = [call(n) for n in order]
+    # the split of 128 tokens gives A 66 chunks per head: two merge batches
+    outs.append(call("A", split_tokens=128))
+    order.append("A")
+    torch.cuda.synchronize()
+    refs = {n: O.decode_fp64_state(data[n][0].q_dec, data[n][1], data[n][4]) for n in cfgs}
+    for i, (n, o) in enumerate(zip(order, outs)):
+        _check(f"interleaved #{i} state {n}", o.float().cpu().numpy(), refs[n])
+    assert torch.equal(outs[0], outs[3]) and torch.equal(outs[1], outs[5]) and torch.equal(outs[2], outs[4])

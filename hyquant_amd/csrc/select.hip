@@ -48,99 +48,216 @@ __device__ __forceinline__ uint32_t orderable_key(uint16_t b) {
     return (u & 0x8000u) ? (~u & 0xffffu) : (u | 0x8000u);
 }
 
-__global__ void qmean_kernel(const uint16_t* __restrict__ q, int64_t qs_b, int64_t qs_h, int64_t qs_t,
-                             int QL, int tail, int R, int H_out, int D, int B, uint16_t* __restrict__ qm) {
+// qm as float64 (the exact value of the bf16 mean) for the score kernel
+// one thread per (b, hk, g < GP, d); heads g >= G (padding) get zeros
+__global__ __launch_bounds__(128) void qmean_kernel(const uint16_t* __restrict__ q, int64_t qs_b, int64_t qs_h,
+                                                    int64_t qs_t, int QL, int tail, int R, int HK, int G, int GP,
+                                                    int D, int B, double* __restrict__ qm) {
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t total = static_cast<int64_t>(B) * H_out * D;
+    const int64_t total = static_cast<int64_t>(B) * HK * GP * D;
     if (idx >= total) return;
     const int d = static_cast<int>(idx % D);
-    const int ho = static_cast<int>((idx / D) % H_out);
-    const int b = static_cast<int>(idx / (static_cast<int64_t>(D) * H_out));
-    double outer = 0.0;
-    for (int t = 0; t < tail; ++t) {
-        const int64_t tt = QL - tail + t;
-        double inner = 0.0;
-        for (int r = 0; r < R; ++r)
-            inner += bf16_bits_to_f64(q[b * qs_b + static_cast<int64_t>(ho * R + r) * qs_h + tt * qs_t + d]);
-        outer += (R == 1) ? inner : bf16_bits_to_f64(f64_to_bf16_rne(inner / R));
+    const int g = static_cast<int>((idx / D) % GP);
+    const int bhk = static_cast<int>(idx / (static_cast<int64_t>(D) * GP));
+    if (g >= G) {
+        qm[idx] = 0.0;
+        return;
     }
-    qm[idx] = f64_to_bf16_rne(outer / tail);
-}
-
-// one thread per (b, hk, p); the G = H_out / HK query means of key head hk
-__global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__ k, int64_t ks_b, int64_t ks_h,
-                                                    int64_t ks_n, int HK, int G, int64_t P, int B,
-                                                    const uint16_t* __restrict__ qm, uint16_t* __restrict__ keys) {
-    extern __shared__ double s_q[];               // [G][128]
-    const int bh = blockIdx.y;                     // b * HK + hk
-    const int b = bh / HK, hk = bh % HK;
-    for (int i = threadIdx.x; i < G * 128; i += blockDim.x)
-        s_q[i] = bf16_bits_to_f64(qm[(static_cast<int64_t>(b) * HK * G + hk * G) * 128 + i]);
-    __syncthreads();
-    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (p >= P) return;
-    const uint4* row = reinterpret_cast<const uint4*>(k + b * ks_b + hk * ks_h + p * ks_n);
-    double acc[16];
+    const int b = bhk / HK, ho = (bhk % HK) * G + g;
+    const uint16_t* base = q + b * qs_b + static_cast<int64_t>(ho * R) * qs_h + static_cast<int64_t>(QL - tail) * qs_t + d;
+    // every partial sum below is a sum of bf16 values (or of bf16 means),
+    // exact in float64, so the association order does not change the result
+    double outer[4] = {0.0, 0.0, 0.0, 0.0};
+    int t = 0;
+    if (R == 1) {
+        for (; t + 8 <= tail; t += 8) {
+            uint16_t v[8];
 #pragma unroll
-    for (int g = 0; g < 16; ++g) acc[g] = 0.0;
-    for (int c = 0; c < 16; ++c) {
-        const uint4 w = row[c];
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+            for (int u = 0; u < 8; ++u) v[u] = base[static_cast<int64_t>(t + u) * qs_t];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint16_t bits = static_cast<uint16_t>(j & 1 ? ww[j >> 1] >> 16 : ww[j >> 1] & 0xffff);
-            const double kv = bf16_bits_to_f64(bits);
-            const int d = 8 * c + j;
-#pragma unroll
-            for (int g = 0; g < 16; ++g)
-                if (g < G) acc[g] = fma(s_q[g * 128 + d], kv, acc[g]);
+            for (int u = 0; u < 8; ++u) outer[u & 3] += bf16_bits_to_f64(v[u]);
+        }
+        for (; t < tail; ++t) outer[0] += bf16_bits_to_f64(base[static_cast<int64_t>(t) * qs_t]);
+    } else {
+        for (; t < tail; ++t) {
+            double inner = 0.0;
+            for (int r = 0; r < R; ++r) inner += bf16_bits_to_f64(base[static_cast<int64_t>(r) * qs_h + static_cast<int64_t>(t) * qs_t]);
+            outer[t & 3] += bf16_bits_to_f64(f64_to_bf16_rne(inner / R));
         }
     }
-    for (int g = 0; g < G; ++g)
-        keys[(static_cast<int64_t>(bh) * G + g) * P + p] = static_cast<uint16_t>(orderable_key(f64_to_bf16_rne(acc[g])));
+    const double s = (outer[0] + outer[1]) + (outer[2] + outer[3]);
+    qm[idx] = bf16_bits_to_f64(f64_to_bf16_rne(s / tail));
 }
 
+// One workgroup per 256 key rows of one (b, hk).  The query means (float64,
+// [GM][128]) sit in LDS and are read with same-address (broadcast) loads.
+// Each wavefront stages half-rows (64 channels) of its 64 rows through LDS
+// with coalesced 1 KB loads (pitch 144 B: the per-row reads hit every bank
+// once per 16 lanes), then lane r accumulates the GM dot products of row r
+// sequentially in channel order in float64.  GM is G rounded up to 1, 2, 4,
+// 8 or 16; the means are stored with zero rows past G, so the FMA loop has no
+// branches and only the key store skips heads g >= G.
+constexpr int SC_ROWS = 64;                 // rows per wavefront
+constexpr int SC_PITCH = 144;               // LDS bytes per half-row (128 + 16)
+
+template <int GM>
+__global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__ k, int64_t ks_b, int64_t ks_h,
+                                                    int64_t ks_n, int HK, int G, int64_t P,
+                                                    const double* __restrict__ qm, uint16_t* __restrict__ keys) {
+    __shared__ __align__(16) double s_q[GM * 128];
+    __shared__ __align__(16) uint8_t s_rows[4][SC_ROWS * SC_PITCH];
+    const int bh = blockIdx.y;                     // b * HK + hk
+    const int b = bh / HK, hk = bh % HK;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const double* qg = qm + static_cast<int64_t>(bh) * GM * 128;
+    for (int i = threadIdx.x; i < GM * 128; i += 256) s_q[i] = qg[i];
+    const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 256 + wave * SC_ROWS;
+    const uint16_t* kb = k + b * ks_b + hk * ks_h;
+    uint8_t* lds = s_rows[wave];
+    // lane l loads 16-byte chunk (l & 7) of half-row `half` of rows p0 + 8i + (l >> 3)
+    const int sub = lane & 7, rq = lane >> 3;
+    double acc[GM];
+#pragma unroll
+    for (int g = 0; g < GM; ++g) acc[g] = 0.0;
+    __syncthreads();
+#pragma unroll 1
+    for (int half = 0; half < 2; ++half) {
+        uint4 raw[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t p = min(p0 + 8 * i + rq, P - 1);
+            raw[i] = *reinterpret_cast<const uint4*>(kb + p * ks_n + 64 * half + 8 * sub);
+        }
+        // One wavefront writes and reads its own LDS rows; its LDS accesses
+        // execute in program order, so the writes of this half follow every
+        // read of the previous one and precede the reads below.
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(lds + (8 * i + rq) * SC_PITCH + 16 * sub) = raw[i];
+        __builtin_amdgcn_wave_barrier();
+        const uint8_t* row = lds + lane * SC_PITCH;
+#pragma unroll 1
+        for (int c = 0; c < 8; ++c) {
+            const uint4 w = *reinterpret_cast<const uint4*>(row + 16 * c);
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+            double kv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                kv[j] = static_cast<double>(__uint_as_float(j & 1 ? ww[j >> 1] & 0xffff0000u : ww[j >> 1] << 16));
+            const int d0 = 64 * half + 8 * c;
+#pragma unroll
+            for (int g = 0; g < GM; ++g) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[g] = fma(s_q[g * 128 + d0 + j], kv[j], acc[g]);
+            }
+        }
+    }
+    const int64_t p = p0 + lane;
+    if (p < P) {
+#pragma unroll
+        for (int g = 0; g < GM; ++g)
+            if (g < G) keys[(static_cast<int64_t>(bh) * G + g) * P + p] = static_cast<uint16_t>(orderable_key(f64_to_bf16_rne(acc[g])));
+    }
+}
+
+constexpr int TOPK_WAVES = TOPK_THREADS / 64;
+constexpr int64_t TOPK_LDS_KEYS = 24576;   // rows up to this many keys are cached in LDS
+
+// One workgroup per (b, ho) row.  The composite (key << 16) | (0xffff - idx)
+// is unique per position and orders "score desc, index asc" as "composite
+// desc": a 4-pass radix select (8 bits per pass, one private histogram per
+// wavefront) finds the T-th largest composite, the T survivors are gathered
+// into LDS and bitonic-sorted.  Rows of up to TOPK_LDS_KEYS keys are read
+// from memory once into LDS.
 __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __restrict__ keys, int64_t P, int T,
                                                             int64_t* __restrict__ out) {
-    __shared__ uint32_t hist[256];
+    __shared__ uint32_t hist[TOPK_WAVES][256];
     __shared__ uint32_t s_prefix, s_need;
     __shared__ uint32_t s_count;
     __shared__ uint32_t sel[TOPK_MAX_T];
+    __shared__ uint16_t s_keys[TOPK_LDS_KEYS];
     const int row = blockIdx.x;
     const uint16_t* kr = keys + static_cast<int64_t>(row) * P;
     const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const bool cached = P <= TOPK_LDS_KEYS;
+    if (cached) {
+        for (int64_t i = tid; i < P; i += TOPK_THREADS) s_keys[i] = kr[i];
+    }
     if (tid == 0) {
         s_prefix = 0;
         s_need = static_cast<uint32_t>(T);
         s_count = 0;
     }
+    auto key_at = [&](int64_t i) -> uint32_t { return cached ? s_keys[i] : kr[i]; };
     // radix select, most significant byte first: find the T-th largest composite
     for (int pass = 0; pass < 4; ++pass) {
         const int shift = 24 - 8 * pass;
-        for (int i = tid; i < 256; i += TOPK_THREADS) hist[i] = 0;
+        for (int i = tid; i < TOPK_WAVES * 256; i += TOPK_THREADS) (&hist[0][0])[i] = 0;
         __syncthreads();
         const uint32_t prefix = s_prefix;
         const uint32_t pmask = pass == 0 ? 0u : (0xffffffffu << (32 - 8 * pass));
         for (int64_t i = tid; i < P; i += TOPK_THREADS) {
-            const uint32_t comp = (static_cast<uint32_t>(kr[i]) << 16) | (0xffffu - static_cast<uint32_t>(i));
-            if ((comp & pmask) == prefix) atomicAdd(&hist[(comp >> shift) & 0xffu], 1u);
+            const uint32_t comp = (key_at(i) << 16) | (0xffffu - static_cast<uint32_t>(i));
+            if ((comp & pmask) == prefix) atomicAdd(&hist[wave][(comp >> shift) & 0xffu], 1u);
         }
         __syncthreads();
-        if (tid == 0) {
-            uint32_t need = s_need, acc = 0;
-            int bin = 255;
-            for (; bin > 0; --bin) {
-                if (acc + hist[bin] >= need) break;
-                acc += hist[bin];
+        // fold the per-wavefront histograms into hist[0]
+        if (tid < 256) {
+            uint32_t s = 0;
+#pragma unroll
+            for (int w = 0; w < TOPK_WAVES; ++w) s += hist[w][tid];
+            hist[0][tid] = s;
+        }
+        __syncthreads();
+        if (tid < 64) {
+            // wavefront 0: find the bin holding the need-th largest, from the top
+            const uint32_t need = s_need;
+            uint32_t c[4];
+            uint32_t mine = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                c[j] = hist[0][255 - (4 * tid + j)];
+                mine += c[j];
             }
-            s_need = need - acc;
-            s_prefix = prefix | (static_cast<uint32_t>(bin) << shift);
+            // exclusive prefix over lanes (bins from the top)
+            uint32_t incl = mine;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t o = __shfl_up(incl, off, 64);
+                if (tid >= off) incl += o;
+            }
+            uint32_t acc = incl - mine;
+            int found = -1;
+            uint32_t before = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (found < 0 && acc + c[j] >= need) {
+                    found = 255 - (4 * tid + j);
+                    before = acc;
+                }
+                acc += c[j];
+            }
+            // the first lane (highest bins) that found it wins; the candidates
+            // always number at least `need`, so some lane finds it (were it
+            // not so, bin 0 would be taken, as a top-down scan would)
+            const uint64_t ball = __ballot(found >= 0);
+            const int first = ball ? __ffsll(static_cast<long long>(ball)) - 1 : 63;
+            if (tid == first) {
+                if (found < 0) {
+                    found = 0;
+                    before = acc - c[3];
+                }
+                s_need = need - before;
+                s_prefix = prefix | (static_cast<uint32_t>(found) << shift);
+            }
         }
         __syncthreads();
     }
     const uint32_t thr = s_prefix;                 // exactly T composites are >= thr
     for (int64_t i = tid; i < P; i += TOPK_THREADS) {
-        const uint32_t comp = (static_cast<uint32_t>(kr[i]) << 16) | (0xffffu - static_cast<uint32_t>(i));
+        const uint32_t comp = (key_at(i) << 16) | (0xffffu - static_cast<uint32_t>(i));
         if (comp >= thr) {
             const uint32_t pos = atomicAdd(&s_count, 1u);
             if (pos < static_cast<uint32_t>(T)) sel[pos] = comp;
@@ -330,8 +447,10 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
     reinterpret_cast<uint4*>(dv)[sub] = reinterpret_cast<const uint4*>(a.v + b * a.vs_b + hk * a.vs_h + src * a.vs_n)[sub];
 }
 
+int padded_heads(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16; }
+
 size_t select_ws(int B, int H_out, int64_t P) {
-    const size_t qm = static_cast<size_t>(B) * H_out * 128 * 2;
+    const size_t qm = static_cast<size_t>(B) * H_out * 128 * sizeof(double) * 4;   // room for head padding
     return ((qm + 255) / 256) * 256 + static_cast<size_t>(B) * H_out * P * 2;
 }
 
@@ -365,16 +484,23 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
     const size_t need = select_ws(b, h_out, p);
     if (!workspace || ws_bytes < need) return fail(HYQ_ENOSPC, "hyq_vertical_select: workspace too small");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    uint16_t* qm = static_cast<uint16_t*>(workspace);
-    const size_t qm_bytes = ((static_cast<size_t>(b) * h_out * 128 * 2 + 255) / 256) * 256;
+    double* qm = static_cast<double*>(workspace);
+    const size_t qm_bytes = ((static_cast<size_t>(b) * h_out * 128 * sizeof(double) * 4 + 255) / 256) * 256;
     uint16_t* keys = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + qm_bytes);
-    const int64_t nq = static_cast<int64_t>(b) * h_out * 128;
-    qmean_kernel<<<dim3(static_cast<unsigned>((nq + 255) / 256)), dim3(256), 0, s>>>(q, qs_b, qs_h, qs_t, q_len, tail, group,
-                                                                                   h_out, 128, b, qm);
+    const int GP = padded_heads(G);
+    const int64_t nq = static_cast<int64_t>(b) * hk * GP * 128;
+    qmean_kernel<<<dim3(static_cast<unsigned>((nq + 127) / 128)), dim3(128), 0, s>>>(q, qs_b, qs_h, qs_t, q_len, tail, group,
+                                                                                   hk, G, GP, 128, b, qm);
     int rc = check_launch("hyq_vertical_select (mean)");
     if (rc) return rc;
-    score_kernel<<<dim3(static_cast<unsigned>((p + 255) / 256), static_cast<unsigned>(b * hk)), dim3(256),
-                   G * 128 * sizeof(double), s>>>(k, ks_b, ks_h, ks_n, hk, G, p, b, qm, keys);
+    const dim3 sgrid(static_cast<unsigned>((p + 255) / 256), static_cast<unsigned>(b * hk));
+    switch (GP) {
+        case 1: score_kernel<1><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, qm, keys); break;
+        case 2: score_kernel<2><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, qm, keys); break;
+        case 4: score_kernel<4><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, qm, keys); break;
+        case 8: score_kernel<8><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, qm, keys); break;
+        default: score_kernel<16><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, qm, keys); break;
+    }
     rc = check_launch("hyq_vertical_select (score)");
     if (rc) return rc;
     topk_kernel<<<dim3(static_cast<unsigned>(b * h_out)), dim3(TOPK_THREADS), 0, s>>>(keys, p, top_k, out_idx);

@@ -66,6 +66,8 @@ constexpr int VBUF = PD * VSTR;
 constexpr float PF_SLACK = 8.0f;
 constexpr float PF_M_INIT = -1.0e30f;
 constexpr float FP8_MAX = 448.0f;        // src/ops/sage_unified_fp8.py:44
+constexpr float S_FP8_OFFSET = 8.807f;   // vendor/sageattention/csrc/qattn/attn_utils.cuh:30 (log2 448)
+constexpr int VSTR8 = 72;                // LDS row stride of the fp8 V^T tile (64 keys + pad)
 constexpr int LIST_THREADS = 1024;
 constexpr int MAX_T = 8192;              // vertical indices per head
 constexpr int64_t MAX_P = 131072;        // prefix positions N - W per head
@@ -195,7 +197,8 @@ __global__ __launch_bounds__(128) void kv_final_kernel(const double* __restrict_
 }
 
 // grid (ceil(N*16 / 256), B*HKV): thread = 8 channels of one row.
-//   k16 = fp16(bf16(k - km)), v16 = fp16(v), v8 = e4m3(v / vscale) (fp8 PV)
+//   k16 = fp16(bf16(k - km)), v16 = fp16(v); fp8 PV: v8 = e4m3(v / vscale)
+//   and v16 = fp16(v / vscale)
 __global__ __launch_bounds__(256) void kv_convert_kernel(const uint16_t* __restrict__ k, int64_t k_b, int64_t k_h,
                                                          int64_t k_n, const uint16_t* __restrict__ v, int64_t v_b,
                                                          int64_t v_h, int64_t v_n, int HKV, int N,
@@ -223,8 +226,9 @@ __global__ __launch_bounds__(256) void kv_convert_kernel(const uint16_t* __restr
     const u32x4 vo = {pack_f16x2(vf[0], vf[1]), pack_f16x2(vf[2], vf[3]), pack_f16x2(vf[4], vf[5]),
                       pack_f16x2(vf[6], vf[7])};
     *reinterpret_cast<u32x4*>(k16 + o) = ko;
-    *reinterpret_cast<u32x4*>(v16 + o) = vo;
     if (v8 != nullptr) {
+        // fp8 PV: e4m3(v / vscale) for the rest keys and fp16(v / vscale) for
+        // the vertical and window keys, so that all tiles accumulate in one unit
         float q[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -233,6 +237,10 @@ __global__ __launch_bounds__(256) void kv_convert_kernel(const uint16_t* __restr
         }
         const u32x2 p = {pack_e4m3x4(q[0], q[1], q[2], q[3]), pack_e4m3x4(q[4], q[5], q[6], q[7])};
         *reinterpret_cast<u32x2*>(v8 + o) = p;
+        const u32x4 qo = {pack_f16x2(q[0], q[1]), pack_f16x2(q[2], q[3]), pack_f16x2(q[4], q[5]), pack_f16x2(q[6], q[7])};
+        *reinterpret_cast<u32x4*>(v16 + o) = qo;
+    } else {
+        *reinterpret_cast<u32x4*>(v16 + o) = vo;
     }
 }
 
@@ -499,6 +507,7 @@ struct PfArgs {
     int B, HQ, HKV, N, nblk, W, P, T, nsb;
     float c;                                                          // fp32(sm_scale * log2e)
     int total, per_xcd;
+    const float* vscale;                                              // fp8 PV: [BHK][128] per-channel V scale
 };
 
 __device__ __forceinline__ f32x4 mfma_f16(const f16x8& a, const f16x8& b, const f32x4& c) {
@@ -506,6 +515,9 @@ __device__ __forceinline__ f32x4 mfma_f16(const f16x8& a, const f16x8& b, const 
 }
 __device__ __forceinline__ i32x4 mfma_i8(const i32x4& a, const i32x4& b, const i32x4& c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_fp8(const u32x2& a, const u32x2& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0, 0, 0);
 }
 
 struct TileDesc {
@@ -515,6 +527,11 @@ struct TileDesc {
     float sc;      // rest: q_scale * k_scale
 };
 
+// PV8: fp8 PV on the rest tiles (P' = exp2(s - m + 8.807) as e4m3 against
+// e4m3(v / vscale)); the vertical and window tiles keep fp16 operands in the
+// same units (fp16(P'), fp16(v / vscale)); the epilogue multiplies by vscale.
+// The running max is exact in this mode (no lazy slack), so P' <= 448.
+template <bool PV8>
 __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t s_k[2][KBUF];
     __shared__ __attribute__((aligned(16))) uint8_t s_v[2][VBUF];
@@ -609,8 +626,9 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         return d;
     };
 
-    // global -> register staging of one tile (K: 2 or 4 x 16 B, V: 4 x 16 B per thread)
-    u32x4 kr[4], vr[4];
+    // global -> register staging of one tile (K: 2 or 4 x 16 B, V: 4 x 16 B
+    // per thread, fp8 V: 4 x 8 B)
+    u32x4 kr[4], vr[4];                    // fp8 V rows use vr[r].xy
     auto load_tile = [&](const TileDesc& d) {
         if (d.kind == T_REST) {
             const int8_t* base = a.k8r + static_cast<int64_t>(bh) * a.P * PD + 16 * (tid & 7);
@@ -627,6 +645,17 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                 const int e = min(d.idx0 + (tid >> 4) + 16 * i, d.valid - 1);
                 kr[i] = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(e) * PD);
             }
+        }
+        if (PV8 && d.kind == T_REST) {
+            const uint8_t* vb8 = reinterpret_cast<const uint8_t*>(a.vr) + static_cast<int64_t>(bh) * a.P * PD + 8 * (tid & 15);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int e = min(d.idx0 + 4 * (tid >> 4) + r, d.valid - 1);
+                const u32x2 t = *reinterpret_cast<const u32x2*>(vb8 + static_cast<int64_t>(e) * PD);
+                vr[r][0] = t[0];
+                vr[r][1] = t[1];
+            }
+            return;
         }
         const uint16_t* vbase = (d.kind == T_REST ? a.vr + static_cast<int64_t>(bh) * a.P * PD
                                  : d.kind == T_VERT ? a.vv16 + static_cast<int64_t>(bh) * a.T * PD
@@ -652,6 +681,19 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         const int kq = tid >> 4, co = tid & 15;
         const int kb4 = kq >> 2, gg = kq & 3;
         const int pos = 32 * (kb4 >> 1) + 8 * gg + 4 * (kb4 & 1);
+        if (PV8 && d.kind == T_REST) {
+            // fp8: channel row 8co + e gets byte e of the four keys' rows
+            uint8_t* vb8 = s_v[buf] + pos;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int dd = e >> 2, by = e & 3;
+                const uint32_t sel = static_cast<uint32_t>(by) | (static_cast<uint32_t>(4 + by) << 8) | 0x0c0c0000u;
+                const uint32_t t01 = __builtin_amdgcn_perm(vr[1][dd], vr[0][dd], sel);
+                const uint32_t t23 = __builtin_amdgcn_perm(vr[3][dd], vr[2][dd], sel);
+                *reinterpret_cast<uint32_t*>(vb8 + (8 * co + e) * VSTR8) = t01 | (t23 << 16);
+            }
+            return;
+        }
         uint8_t* vb = s_v[buf] + 2 * pos;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -750,8 +792,8 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             }
         }
 
-        // ---- online softmax (lazy max) and P -> fp16 -------------------------
-        f16x8 pf[2][2];
+        // ---- online softmax (lazy max) and P -> fp16 (fp8 on PV8 rest tiles) ---
+        u32x4 pw[2][2];                    // P^T operands: fp16 x 8, or fp8 x 8 in .xy
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
             float mx = s[sb][0][0];
@@ -760,7 +802,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[sb][kbk][r]);
             mx = quad_max(mx);
-            if (__builtin_amdgcn_ballot_w64(mx > m_run[sb] + PF_SLACK)) {
+            if (__builtin_amdgcn_ballot_w64(mx > m_run[sb] + (PV8 ? 0.0f : PF_SLACK))) {
                 const float mnew = fmaxf(m_run[sb], mx);
                 const float alpha = __builtin_amdgcn_exp2f(m_run[sb] - mnew);
                 l_run[sb] *= alpha;
@@ -774,32 +816,52 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             for (int kbk = 0; kbk < 4; ++kbk)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    p[kbk][r] = __builtin_amdgcn_exp2f(s[sb][kbk][r] - m_run[sb]);
+                    p[kbk][r] = __builtin_amdgcn_exp2f(PV8 ? (s[sb][kbk][r] - m_run[sb]) + S_FP8_OFFSET
+                                                           : s[sb][kbk][r] - m_run[sb]);
                     ls += p[kbk][r];
                 }
             l_run[sb] += ls;
+            if (PV8 && d.kind == T_REST) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const u32x4 pv = {pack_f16x2(p[2 * j][0], p[2 * j][1]), pack_f16x2(p[2 * j][2], p[2 * j][3]),
-                                  pack_f16x2(p[2 * j + 1][0], p[2 * j + 1][1]),
-                                  pack_f16x2(p[2 * j + 1][2], p[2 * j + 1][3])};
-                pf[sb][j] = __builtin_bit_cast(f16x8, pv);
+                for (int j = 0; j < 2; ++j)
+                    pw[sb][j] = u32x4{pack_e4m3x4(p[2 * j][0], p[2 * j][1], p[2 * j][2], p[2 * j][3]),
+                                      pack_e4m3x4(p[2 * j + 1][0], p[2 * j + 1][1], p[2 * j + 1][2], p[2 * j + 1][3]),
+                                      0u, 0u};
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    pw[sb][j] = u32x4{pack_f16x2(p[2 * j][0], p[2 * j][1]), pack_f16x2(p[2 * j][2], p[2 * j][3]),
+                                      pack_f16x2(p[2 * j + 1][0], p[2 * j + 1][1]),
+                                      pack_f16x2(p[2 * j + 1][2], p[2 * j + 1][3])};
+                }
             }
         }
 
         // ---- O^T += V^T . P^T -------------------------------------------------
+        if (PV8 && d.kind == T_REST) {
 #pragma unroll
-        for (int cb = 0; cb < 8; ++cb) {
+            for (int cb = 0; cb < 8; ++cb) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const f16x8 av = *reinterpret_cast<const f16x8*>(vb + (16 * cb + c16) * VSTR + 64 * j + 16 * g);
+                for (int j = 0; j < 2; ++j) {
+                    const u32x2 av = *reinterpret_cast<const u32x2*>(vb + (16 * cb + c16) * VSTR8 + 32 * j + 8 * g);
 #pragma unroll
-                for (int sb = 0; sb < 2; ++sb) acc[sb][cb] = mfma_f16(av, pf[sb][j], acc[sb][cb]);
+                    for (int sb = 0; sb < 2; ++sb) acc[sb][cb] = mfma_fp8(av, u32x2{pw[sb][j][0], pw[sb][j][1]}, acc[sb][cb]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const f16x8 av = *reinterpret_cast<const f16x8*>(vb + (16 * cb + c16) * VSTR + 64 * j + 16 * g);
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb) acc[sb][cb] = mfma_f16(av, __builtin_bit_cast(f16x8, pw[sb][j]), acc[sb][cb]);
+                }
             }
         }
     }
 
-    // ---- epilogue: O = acc / l --------------------------------------------------
+    // ---- epilogue: O = acc / l (x vscale in fp8 mode) ------------------------------
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
         const float l = quad_sum(l_run[sb]);
@@ -809,8 +871,9 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             uint16_t* orow = a.out + b * a.o_b + h * a.o_h + static_cast<int64_t>(row) * a.o_n;
 #pragma unroll
             for (int cb = 0; cb < 8; ++cb) {
-                const u32x2 o = {pack_bf16x2(acc[sb][cb][0] * inv, acc[sb][cb][1] * inv),
-                                 pack_bf16x2(acc[sb][cb][2] * inv, acc[sb][cb][3] * inv)};
+                f32x4 o4 = acc[sb][cb] * inv;
+                if (PV8) o4 *= *reinterpret_cast<const f32x4*>(a.vscale + bhk * PD + 16 * cb + 4 * g);
+                const u32x2 o = {pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3])};
                 *reinterpret_cast<u32x2*>(orow + 16 * cb + 4 * g) = o;
             }
         }
@@ -950,7 +1013,7 @@ extern "C" int hyq_prefill_hybrid(const hyq_prefill_params* p, void* ws, size_t 
     const int B = p->batch, HQ = p->hq, HKV = p->hkv, W = p->window;
     const int64_t N = p->n, T = p->t;
     if (p->head_dim != PD) return fail(HYQ_ENOTSUP, "hyq_prefill_hybrid: head_dim must be 128");
-    if (p->pv_mode != 0) return fail(HYQ_ENOTSUP, "hyq_prefill_hybrid: pv_mode must be 0 (fp16)");
+    if (p->pv_mode != 0 && p->pv_mode != 1) return fail(HYQ_EINVAL, "hyq_prefill_hybrid: pv_mode must be 0 (fp16) or 1 (fp8)");
     if (B <= 0 || HQ <= 0 || HKV <= 0 || HQ % HKV || N <= 0 || N > INT32_MAX / 2 || T < 0 || W < 0)
         return fail(HYQ_EINVAL, "hyq_prefill_hybrid: invalid sizes (need HQ % HKV == 0, N > 0)");
     const int64_t P = std::max<int64_t>(0, N - W);
@@ -1033,6 +1096,10 @@ extern "C" int hyq_prefill_hybrid(const hyq_prefill_params* p, void* ws, size_t 
     a.c = static_cast<float>(sm * 1.44269504);
     a.total = BH * nblk;
     a.per_xcd = (a.total + 7) / 8;
-    hipLaunchKernelGGL(prefill_main_kernel, dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
+    a.vscale = static_cast<const float*>(at(L.vscale));
+    if (p->pv_mode)
+        hipLaunchKernelGGL(prefill_main_kernel<true>, dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
+    else
+        hipLaunchKernelGGL(prefill_main_kernel<false>, dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
     return check_launch("prefill_main_kernel");
 }

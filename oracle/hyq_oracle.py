@@ -24,6 +24,12 @@ its own formulas):
       invariance, GQA equals explicit head expansion, single-token softmax = v.
   decode_bf16_eager                   -> same inputs agree with decode_fp64 to
       bf16 precision.
+  e4m3_round                          -> torch.float8_e4m3fn on every in-range
+      grid point and tie, hand known answers (ties to even, subnormals,
+      saturation at 448).
+  hybrid_prefill_fp64(pv_mode='fp8')  -> with V, P exactly representable in
+      e4m3 (powers of two) it equals the fp16 mode; per-channel V scale
+      invariance; fp8 error against exact attention within the e4m3 bound.
 """
 
 from __future__ import annotations
@@ -652,8 +658,42 @@ def prefill_operands(q, k, v, sm_scale: Optional[float] = None, smooth: bool = T
     return dict(c=c, q8=q8, q_scale=qsc, q16=q16, km=km, k16=to_fp16(ks), v16=to_fp16(v))
 
 
+FP8_MAX = 448.0            # src/ops/sage_unified_fp8.py:44
+S_FP8_OFFSET = 8.807       # src/ops/vendor/sageattention/csrc/qattn/attn_utils.cuh:30
+
+
+def e4m3_round(x) -> np.ndarray:
+    """OCP fp8 e4m3 (e4m3fn: bias 7, 3 mantissa bits, no infinities, max 448)
+    round-to-nearest-even with saturation to +-448 (the satfinite conversion of
+    src/ops/vendor/sageattention/csrc/qattn/attn_utils.cuh:478-493).  Returns
+    the rounded values as float64."""
+    x = np.asarray(x, np.float64)
+    a = np.minimum(np.abs(x), FP8_MAX)
+    with np.errstate(divide="ignore"):
+        e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    e = np.maximum(e, -6.0)                      # subnormal spacing 2^-9 below 2^-6
+    quantum = np.exp2(e - 3.0)
+    r = np.round(a / quantum) * quantum          # numpy rounds half to even
+    r = np.minimum(r, FP8_MAX)
+    return np.where(x < 0, -r, r)
+
+
+def fp8_v_operands(v):
+    """Per-channel V scale over the whole sequence (no mean, smooth_v=False) and
+    the e4m3 codes of v / scale (src/ops/vendor/sageattention/quant.py:136-166,
+    csrc/fused/fused.cu:319-430): scale = fp32(max|v| / 448) per (b, kv head,
+    channel); v8 = e4m3(fp32(v) / scale); zero where scale is zero.  Also
+    returns fp16(fp32(v) / scale), the scaled fp16 values the hybrid kernel
+    feeds its vertical and window tiles in fp8 mode."""
+    v32 = np.asarray(v, np.float32)
+    vs = (np.max(np.abs(v32), axis=2, keepdims=True) / np.float32(FP8_MAX)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ratio = np.where(vs > 0, v32 / np.where(vs > 0, vs, 1), 0).astype(np.float32)
+    return vs, e4m3_round(ratio), to_fp16(ratio)
+
+
 def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None, smooth: bool = True,
-                        int8_rest: bool = True, abs_v: bool = False):
+                        int8_rest: bool = True, abs_v: bool = False, pv_mode: str = "fp16"):
     """float64 restatement of sage_vertical_attention_v2 (sage_unified.py:550-622,
     kernel :398-496).  q [B, HQ, N, D], k/v [B, HKV, N, D] (bf16 values),
     vidx [B, HQ, T].  For query row i of block b (128 rows):
@@ -664,15 +704,27 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
         s = q16 . k16 with q16 = fp16(bf16(q * sm*log2e)), k16 = fp16(ks);
     one base-2 softmax over all of them, values fp16(v).  int8_rest=False
     scores the rest keys with q16 . k16 too (a check of the partition alone).
-    abs_v=True returns sum p |v| / l instead (an error scale).  Returns float64
-    [B, HQ, N, D]."""
+    abs_v=True returns sum p |v| / l instead (an error scale).
+
+    pv_mode='fp8' follows the INT8-QK / FP8-PV kernel of the vendored
+    SageAttention (qk_int_sv_f8_cuda_sm90.cu:300-345, :490-512 and
+    attn_utils.cuh:354-458) on the rest keys: p' = exp2(s - m + 8.807)
+    (m = the row max), P8 = e4m3(p'), V8 = e4m3(v / vs) with the per-channel
+    scale vs = max|v| / 448; the vertical and window keys keep fp16 operands in
+    the same units, fp16(p') and fp16(v / vs); o = (sum P V) / (sum p') * vs.
+    Returns float64 [B, HQ, N, D]."""
     B, HQ, N, D = q.shape
     HKV = k.shape[1]
     G = HQ // HKV
     op = prefill_operands(q, k, v, sm_scale, smooth)
     q8, qsc, q16, k16, v16 = op["q8"], op["q_scale"], op["q16"], op["k16"], op["v16"]
+    fp8 = pv_mode == "fp8"
+    if fp8:
+        vs, v8, v16 = fp8_v_operands(v)              # v16 := fp16(v / vs) here
     if abs_v:
         v16 = np.abs(v16)
+        if fp8:
+            v8 = np.abs(v8)
     out = np.zeros((B, HQ, N, D), np.float64)
     for b in range(B):
         for h in range(HQ):
@@ -694,7 +746,7 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
                         segs_s.append(s * float(qsc[b, h, blk]) * kscale[None, :])
                     else:
                         segs_s.append(qrow @ k16[b, hk, rest[:n]].astype(np.float64).T)
-                    segs_v.append(v16[b, hk, rest[:n]])
+                    segs_v.append((v8 if fp8 else v16)[b, hk, rest[:n]])
                 if nv[blk] > 0:
                     idx = vert[:nv[blk]]
                     segs_s.append(qrow @ k16[b, hk, idx].astype(np.float64).T)
@@ -705,8 +757,15 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
                 segs_v.append(v16[b, hk, jw])
                 S = np.concatenate(segs_s, axis=1)
                 V = np.concatenate(segs_v, axis=0).astype(np.float64)
-                p = np.exp2(S - S.max(axis=1, keepdims=True))
-                out[b, h, rows] = (p @ V) / p.sum(axis=1, keepdims=True)
+                if not fp8:
+                    p = np.exp2(S - S.max(axis=1, keepdims=True))
+                    out[b, h, rows] = (p @ V) / p.sum(axis=1, keepdims=True)
+                    continue
+                p = np.exp2((S - S.max(axis=1, keepdims=True)) + S_FP8_OFFSET)
+                n_rest = nr[blk]
+                pq = np.concatenate([e4m3_round(p[:, :n_rest]),
+                                     to_fp16(p[:, n_rest:].astype(np.float32)).astype(np.float64)], axis=1)
+                out[b, h, rows] = (pq @ V) / p.sum(axis=1, keepdims=True) * vs[b, hk, 0].astype(np.float64)[None, :]
     return out
 
 

@@ -209,3 +209,53 @@ def test_prefill_deterministic():
     b = sage_vertical_attention_v2(*args, window_size=128)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+FP8_CASES = [CASES[0], CASES[1], CASES[2], CASES[3]]
+
+
+@pytest.mark.parametrize("cfg", FP8_CASES, ids=[f"fp8-N{c['N']}W{c['W']}T{c['T']}" for c in FP8_CASES])
+def test_prefill_fp8_pv_vs_oracle(cfg):
+    """pv_mode='fp8' against the fp8 restatement.  The kernel rounds P' to e4m3
+    relative to its running maximum and the oracle relative to the row
+    maximum, so each weight may sit on a different e4m3 neighbour (3 mantissa
+    bits: 2^-4 relative each): |out - ref| <= 2e-3 + 2^-3 ref_abs + 2^-8 |ref|."""
+    print(f"prefill fp8 {cfg}", flush=True)
+    rng = np.random.default_rng(cfg["seed"] + 100)
+    B, HQ, HKV, N, W, T = (cfg[x] for x in ("B", "HQ", "HKV", "N", "W", "T"))
+    q = _rand_bf16(rng, (B, HQ, N, 128))
+    k = O.bf16_round(_rand_bf16(rng, (B, HKV, N, 128), 1.5) +
+                     O.bf16_round(rng.standard_normal((1, HKV, 1, 128)).astype(np.float32)))
+    v = _rand_bf16(rng, (B, HKV, N, 128))
+    P = max(0, N - W)
+    vidx = np.stack([np.stack([rng.permutation(P)[:T] if P else np.zeros(0, np.int64) for _ in range(HQ)])
+                     for _ in range(B)]).astype(np.int64).reshape(B, HQ, T)
+    out = _run(q, k, v, vidx, W, pv_mode="fp8")
+    ref = O.hybrid_prefill_fp64(q, k, v, vidx, W, pv_mode="fp8")
+    ref_abs = O.hybrid_prefill_fp64(q, k, v, vidx, W, abs_v=True)
+    diff = np.abs(out - ref)
+    bound = ATOL + 2.0 ** -3 * ref_abs + 2.0 ** -8 * np.abs(ref)
+    print(f"fp8 {cfg}: max-abs {float(diff.max()):.3e}, max diff/bound {float((diff / bound).max()):.3f}", flush=True)
+    assert np.all(np.isfinite(out))
+    assert np.all(diff <= bound)
+    # and the fp8 output stays close to exact attention
+    exact = O.exact_causal_attention(q, k, v)
+    mse = float(np.mean((out - exact) ** 2))
+    print(f"fp8 {cfg}: MSE vs exact {mse:.3e}", flush=True)
+    assert mse < 1e-4
+
+
+def test_prefill_fp8_config4_mse():
+    """Config 4 shape at 8K with the fp8 PV variant: MSE vs exact attention."""
+    from hyquant_amd.sage_unified import sage_vertical_attention_v2
+    q, k, v = O.make_prefill_inputs(B=1, HQ=32, HKV=8, N=8192, W=128, seed=0)
+    vidx = O.compute_vertical_indices(q, k, 128, 0.05, kv_repeat=4)
+    dev = torch.device("cuda")
+    qd, kd, vd = to_dev_bf16(q, dev), to_dev_bf16(k, dev), to_dev_bf16(v, dev)
+    out8 = sage_vertical_attention_v2(qd, kd, vd, torch.from_numpy(vidx).to(dev), window_size=128, pv_mode="fp8")
+    out16 = sage_vertical_attention_v2(qd, kd, vd, torch.from_numpy(vidx).to(dev), window_size=128)
+    exact = _exact_attention_gpu(qd, kd, vd)
+    mse8 = float(((out8.float() - exact) ** 2).mean())
+    mse16 = float(((out16.float() - exact) ** 2).mean())
+    print(f"config4 N=8192: MSE vs exact, fp16 PV {mse16:.3e}, fp8 PV {mse8:.3e}", flush=True)
+    assert mse8 < 1e-4

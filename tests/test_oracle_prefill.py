@@ -182,3 +182,94 @@ def test_hybrid_prefill_int8_error_is_small():
     ref = O.exact_causal_attention(q, k, v)
     mse = float(((got - ref) ** 2).mean())
     assert mse < 1e-4, mse
+
+
+# ---------------------------------------------------------------------------
+# OCP e4m3 rounding and the fp8-PV mode
+# ---------------------------------------------------------------------------
+
+def _e4m3_values():
+    """Every finite non-negative e4m3fn value, from its bit patterns."""
+    vals = []
+    for e in range(16):
+        for m in range(8):
+            if e == 15 and m == 7:
+                continue                       # NaN encoding
+            vals.append(m * 2.0 ** -9 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7))
+    return np.array(sorted(set(vals)))
+
+
+def test_e4m3_round_grid_ties_and_torch():
+    torch = pytest.importorskip("torch")
+    vals = _e4m3_values()
+    assert vals[-1] == 448.0 and len(vals) == 127
+    assert np.array_equal(O.e4m3_round(vals), vals)
+    assert np.array_equal(O.e4m3_round(-vals), -vals)
+    # midpoints go to the neighbour with the even mantissa
+    mids = (vals[:-1] + vals[1:]) / 2
+    got = O.e4m3_round(mids)
+    ref = torch.from_numpy(mids).to(torch.float32).to(torch.float8_e4m3fn).to(torch.float64).numpy()
+    assert np.array_equal(got, ref)
+    # random values in range against torch's conversion
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(20000) * np.exp2(rng.uniform(-12, 8, 20000))).astype(np.float32)
+    x = x[np.abs(x) < 448]
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).to(torch.float64).numpy()
+    assert np.array_equal(O.e4m3_round(x), ref)
+    # hand known answers: ties to even, subnormal spacing, saturation
+    assert list(O.e4m3_round([1.0625, 1.1875, 2 ** -10, 3 * 2 ** -10, 464.0, 1000.0, -1000.0])) == \
+        [1.0, 1.25, 0.0, 2 ** -8, 448.0, 448.0, -448.0]
+
+
+def test_fp8_prefill_channel_scale_invariance():
+    """Scaling a V channel by a power of two scales only that output channel by
+    the same factor (the per-channel scale absorbs it exactly)."""
+    q, k, v = O.make_prefill_inputs(B=1, HQ=2, HKV=1, N=300, W=64, seed=11)
+    vidx = O.compute_vertical_indices(q, k, 64, 0.05, kv_repeat=2)
+    base = O.hybrid_prefill_fp64(q, k, v, vidx, 64, pv_mode="fp8")
+    f = np.exp2(np.arange(128) % 7 - 3).astype(np.float32)
+    scaled = O.hybrid_prefill_fp64(q, k, v * f, vidx, 64, pv_mode="fp8")
+    assert np.array_equal(scaled, base * f)
+
+
+def test_fp8_prefill_uniform_scores_closed_form():
+    """q = 0: every attended key scores 0, so p' = 2^8.807 for all of them; the
+    output of row i is (448 sum_rest V8 + fp16(p') sum_other V16') vs / (n p')."""
+    N, W = 200, 64
+    q, k, v = O.make_prefill_inputs(B=1, HQ=1, HKV=1, N=N, W=W, seed=12)
+    q = np.zeros_like(q)
+    vidx = np.array([[[3, 17, 50, 99]]], np.int64)
+    got = O.hybrid_prefill_fp64(q, k, v, vidx, W, pv_mode="fp8")[0, 0]
+    vs, v8, v16 = O.fp8_v_operands(v)
+    vs, v8, v16 = vs[0, 0, 0].astype(np.float64), v8[0, 0], v16[0, 0].astype(np.float64)
+    pp = 2.0 ** 8.807
+    p16 = float(np.float16(pp))
+    vert = set(int(x) for x in vidx[0, 0])
+    for i in (0, 63, 64, 127, 128, 150, 199):
+        wla = O.window_start(i // 128, W)
+        num = np.zeros(128)
+        n = 0
+        for j in range(i + 1):
+            if j >= wla:                                  # window key
+                num += p16 * v16[j]
+            elif j in vert and j < N - W:                 # vertical key below wla
+                num += p16 * v16[j]
+            else:                                         # rest key
+                num += 448.0 * v8[j]
+            n += 1
+        np.testing.assert_allclose(got[i], num / (n * pp) * vs, rtol=1e-12, atol=1e-15)
+
+
+def test_fp8_prefill_error_against_exact_attention():
+    q, k, v = O.make_prefill_inputs(B=1, HQ=2, HKV=1, N=512, W=128, seed=13)
+    vidx = O.compute_vertical_indices(q, k, 128, 0.05, kv_repeat=2)
+    exact = O.exact_causal_attention(q, k, v)
+    f16 = O.hybrid_prefill_fp64(q, k, v, vidx, 128)
+    f8 = O.hybrid_prefill_fp64(q, k, v, vidx, 128, pv_mode="fp8")
+    mse16 = float(np.mean((f16 - exact) ** 2))
+    mse8 = float(np.mean((f8 - exact) ** 2))
+    print(f"MSE vs exact: fp16 PV {mse16:.3e}, fp8 PV {mse8:.3e}")
+    ref_abs = O.hybrid_prefill_fp64(q, k, v, vidx, 128, abs_v=True)
+    # e4m3 keeps 3 mantissa bits: P8 and V8 each within 2^-4 relative
+    assert np.all(np.abs(f8 - f16) <= 2.0 ** -3 * ref_abs + 1e-6)
+    assert mse8 < 1e-3

@@ -15,8 +15,15 @@ Python calls one by one are reported as eager_us_per_step).
 
 Output: one JSON line (rank 0), with the roofline of the decode kernel, the
 CPU baseline (the reference's bf16 eager decode math run by torch on the host
-CPU on config 1), and the prefix sweep of BASELINE config 2 beside a bf16
-full-KV split-K decode of the same shape.
+CPU on config 1), the prefix sweep of BASELINE config 2 beside a bf16 full-KV
+split-K decode of the same shape, and the other configs' workloads measured
+in the same run: config 3 (wide-GQA decode at B=32, 16K prefix; the vertical
+line selector, the freeze reorganisation and the staging flush) and config 4
+(hybrid prefill, fp16 and fp8 P.V, TFLOP/s and MFMA utilisation).
+
+`--pmc` runs a fixed, short workload for hardware-counter passes instead (a
+256 MiB device copy, the calibration of FETCH_SIZE / WRITE_SIZE, then 20 eager
+config-1 decode steps over distinct cache copies) and prints nothing.
 """
 
 from __future__ import annotations
@@ -189,6 +196,140 @@ def cpu_baseline(N=8192, min_steps=20, budget_s=20.0):
                       f"bf16 eager dequant+SDPA decode on torch CPU; host CPU: {model}"}
 
 
+# MI355X dense peaks (TFLOP/s or TOP/s)
+PEAK_INT8 = 5000.0
+PEAK_FP16 = 2500.0
+PEAK_FP8 = 5000.0
+
+
+def time_calls(fn, warmup=2, iters=5):
+    """ms per call of fn, eager, HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def bench_prefill(dev):
+    """Config 4: hybrid prefill, B=1, 32q/8kv, d128, causal, W=128, rho=5%.
+    FLOPs counted as 2*B*H_Q*N^2*D (QK and PV over the causal half).  MFMA
+    utilisation = achieved / the peak of the dtype mix: QK on int8 and PV on
+    fp16 (or fp8), each half of the FLOPs."""
+    from hyquant_amd.sage_unified import sage_vertical_attention_v2
+    from hyquant_amd.vertical import compute_vertical_indices
+    g = torch.Generator(device=dev).manual_seed(4)
+    rows = []
+    for N in (8192, 16384, 32768):
+        B, HQ, HKV, W = 1, 32, 8, 128
+        q = torch.randn(B, HQ, N, D, generator=g, device=dev).to(torch.bfloat16)
+        k = (torch.randn(B, HKV, N, D, generator=g, device=dev) +
+             math.sqrt(2.0) * torch.randn(B, HKV, 1, D, generator=g, device=dev)).to(torch.bfloat16)
+        v = torch.randn(B, HKV, N, D, generator=g, device=dev).to(torch.bfloat16)
+        vidx = compute_vertical_indices(q, k, W, 0.05, kv_repeat=HQ // HKV)
+        flops = 2.0 * B * HQ * N * N * D
+        for mode, pv_peak in (("fp16", PEAK_FP16), ("fp8", PEAK_FP8)):
+            ms = time_calls(lambda: sage_vertical_attention_v2(q, k, v, vidx, window_size=W, pv_mode=mode))
+            tf = flops / (ms * 1e-3) / 1e12
+            peak = 2.0 / (1.0 / PEAK_INT8 + 1.0 / pv_peak)
+            rows.append({"seq_len": N, "pv": mode, "ms": round(ms, 3), "tflops": round(tf, 1),
+                         "mfma_peak_tflops": round(peak, 1), "mfma_util": round(tf / peak, 4),
+                         "n_vertical": int(vidx.shape[-1])})
+            print(f"# prefill {rows[-1]}", file=sys.stderr, flush=True)
+        del q, k, v, vidx
+        torch.cuda.empty_cache()
+    return rows
+
+
+def bench_boundary(dev):
+    """Config 3 boundary ops at B=32, prefix 16384 (Llama shape 32q/8kv):
+    the prefill-time vertical-line selector (W=256, rho=5%), the freeze
+    (freeze-time selector + reorganisation into the four segments) and a staging
+    flush (128 bf16 tokens of every KV head quantised to int4)."""
+    from hyquant_amd.decode_d_stage import quantize_into
+    from hyquant_amd.d_stage_kv_cache import DStageLayerCache
+    from hyquant_amd.vertical import compute_vertical_indices
+    g = torch.Generator(device=dev).manual_seed(3)
+    B, HQ, HKV, N, W = 32, 32, 8, 16384, 256
+    q = torch.randn(B, HQ, N, D, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, HKV, N, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, HKV, N, D, generator=g, device=dev).to(torch.bfloat16)
+    out = {}
+    ms = time_calls(lambda: compute_vertical_indices(q, k, W, 0.05, kv_repeat=HQ // HKV))
+    by = B * HKV * (N - W) * D * 2 + B * HQ * W * D * 2
+    out["select"] = {"us": round(ms * 1e3, 1), "gbs": round(by / (ms * 1e-3) / 1e9, 1),
+                     "algorithmic_bytes": by, "n_selected": int(math.ceil((N - W) * 0.05))}
+
+    def freeze_once():
+        c = DStageLayerCache(0, 4, 4, window_size=W)
+        c.update_prefill(k, v)
+        c.save_query_tail(q[:, :, -W:, :])
+        c.freeze(kv_repeat=HQ // HKV)
+        return c
+    ms = time_calls(freeze_once, warmup=1, iters=3)
+    T = int(math.ceil((N - 2 * W) * 0.05))
+    nq = N - W - T
+    fb = (B * HKV * (N - 2 * W) * D * 2 + B * HQ * W * D * 2            # freeze-time selector reads
+          + B * HKV * (N - W) * D * 2 * 2                               # K and V read by the reorganisation
+          + B * HKV * (nq * 132 + (T + W) * D * 2 * 2))                 # segments written
+    out["freeze"] = {"us": round(ms * 1e3, 1), "gbs": round(fb / (ms * 1e-3) / 1e9, 1), "algorithmic_bytes": fb}
+    x = torch.randn(B * HKV, 128, D, generator=g, device=dev).to(torch.bfloat16)
+    packed = torch.empty(B * HKV, 128, D // 2, dtype=torch.int8, device=dev)
+    scale = torch.empty(B * HKV, 128, dtype=torch.float16, device=dev)
+    ms = time_calls(lambda: quantize_into(x, 4, packed, scale), warmup=5, iters=50)
+    by = B * HKV * 128 * (D * 2 + D // 2 + 2)
+    out["flush"] = {"us": round(ms * 1e3, 2), "gbs": round(by / (ms * 1e-3) / 1e9, 1), "algorithmic_bytes": by}
+    print(f"# boundary {out}", file=sys.stderr, flush=True)
+    return out
+
+
+def bench_wide_gqa(dev):
+    """Config 3 decode shapes at B=32, prefix 16384: Qwen3-32B (64q/8kv) and
+    GLM-4-9B (32q/2kv, GQA 16)."""
+    rows = []
+    for name, HQ, HKV in (("Qwen3-32B", 64, 8), ("GLM-4-9B", 32, 2)):
+        ms, nb, _, _ = bench_hybrid(32, HQ, HKV, 16384, dev, 5, 50)
+        rows.append({"model": name, "batch": 32, "q_heads": HQ, "kv_heads": HKV, "prefix": 16384,
+                     "us_per_step": round(ms * 1e3, 2), "gbs": round(nb / (ms * 1e-3) / 1e9, 1),
+                     "frac_peak": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        print(f"# wide-gqa {rows[-1]}", file=sys.stderr, flush=True)
+    return rows
+
+
+def pmc_workload(dev):
+    """Fixed workload for rocprofv3 --pmc passes: a 256 MiB device copy (the
+    FETCH_SIZE / WRITE_SIZE calibration: it reads and writes 256 MiB), then 20
+    eager config-1 decode steps, each over its own cache copy."""
+    src_t = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst_t = torch.empty_like(src_t)
+    for _ in range(3):
+        dst_t.copy_(src_t)
+    torch.cuda.synchronize()
+    del src_t, dst_t
+    states = [make_state(1, 32, 8, 8192, dev, s) for s in range(20)]
+    torch.cuda.synchronize()
+    for q, st in states:
+        run_decode(q, st, 4)
+    torch.cuda.synchronize()
+
+
+def traffic_record():
+    """HBM bytes per decode launch measured by the FETCH_SIZE / WRITE_SIZE
+    passes over pmc_workload (profiles/decode_config1_traffic.json), or None."""
+    path = os.path.join(ROOT, "profiles", "decode_config1_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -197,6 +338,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-bf16", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config 3 / config 4 sections")
+    ap.add_argument("--pmc", action="store_true", help="run the counter-pass workload only")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -205,6 +348,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     import hyquant_amd  # noqa: F401  (fails loudly if libhyq.so is missing)
+    if args.pmc:
+        pmc_workload(dev)
+        return
 
     B, HQ, HKV, N = 1, 32, 8, 8192
     ms, nbytes, R, eager = bench_hybrid(B, HQ, HKV, N, dev, args.warmup, args.steps)
@@ -235,6 +381,10 @@ def main():
                      "kernel": "decode_kernel (one launch per step)",
                      "algorithmic_bytes_per_launch": nbytes},
     }
+    tr = traffic_record()
+    if tr:
+        res["roofline"]["traffic"] = tr.get("traffic_bytes_per_launch")
+        res["roofline"]["traffic_source"] = "profiles/decode_config1_traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)"
     if not args.no_bf16:
         ms16, b16, _, _ = bench_bf16(B, HQ, HKV, N, dev, args.warmup, args.steps)
         res["bf16_comparator"] = {"us_per_step": round(ms16 * 1e3, 3),
@@ -255,6 +405,10 @@ def main():
                 sweep.append(row)
                 print(f"# sweep {row}", file=sys.stderr, flush=True)
         res["sweep"] = sweep
+    if not args.no_extra:
+        res["config3_wide_gqa"] = bench_wide_gqa(dev)
+        res["config3_boundary"] = bench_boundary(dev)
+        res["config4_prefill"] = bench_prefill(dev)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)

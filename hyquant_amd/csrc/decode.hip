@@ -422,9 +422,9 @@ __device__ __forceinline__ void merge_head(const DecArgs& a, int head, float* s_
         const uint32_t pbase = static_cast<uint32_t>(((h * G + g) * D + 4 * q) * 4);
         const uint32_t pstep = static_cast<uint32_t>(2 * G * D * 4);
         f32x4 px[MJ];
+        // unconditional: partials past nwg fail the range check and read as zeros
 #pragma unroll
-        for (int j = 0; j < MJ; ++j)
-            if (j < npr) px[j] = ld4_dev(rp, pbase + j * pstep);   // past nwg: zeros
+        for (int j = 0; j < MJ; ++j) px[j] = ld4_dev(rp, pbase + j * pstep);
         u32x2 mlr[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k)
@@ -448,9 +448,12 @@ __device__ __forceinline__ void merge_head(const DecArgs& a, int head, float* s_
         wave_sync_lds();
         const int nj = (nwg + 1 - h) / 2;            // partials of this half
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        // table entries [nwg, 64) hold zero weights and their partials read as
+        // zeros, so the first batch needs no bounds: its 2 MJ table reads issue
+        // back to back instead of one per branch
+        static_assert(2 * MJ <= 64, "first merge batch must lie in the zero-filled table head");
 #pragma unroll
-        for (int j = 0; j < MJ; ++j)
-            if (j < nj) acc += wt[2 * j + h] * px[j];
+        for (int j = 0; j < MJ; ++j) acc += wt[2 * j + h] * px[j];
         for (int j0 = MJ; j0 < npr; j0 += MJ) {      // nwg > 2 * MJ: one more round trip per batch
 #pragma unroll
             for (int j = 0; j < MJ; ++j)
@@ -677,11 +680,12 @@ size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
 // Tokens per workgroup chunk.  Few KV heads (small batch): about 32 chunks
 // per head, so the whole chip works on one step and each wavefront streams a
-// handful of groups.  Many heads: a large chunk, which keeps the
-// per-workgroup prologue / partial / merge costs low; the grid still holds
-// many workgroups per CU.  `gran` is the smallest chunk.
+// handful of groups.  Many heads: a large chunk, growing with the head count
+// (2048 tokens up to 127 heads, 4096 up to 191, ...), which keeps the
+// per-workgroup prologue / partial / merge costs low while the grid still
+// holds several workgroups per CU slot.  `gran` is the smallest chunk.
 int64_t auto_split(int64_t n, int bh_kv, int64_t gran, int64_t big) {
-    if (bh_kv >= 32) return big;
+    if (bh_kv >= 32) return big * std::max(1, bh_kv / 64);
     int64_t split = gran;
     while (split < big && split * 32 < n) split *= 2;
     return split;
@@ -696,6 +700,9 @@ Plan make_plan(int64_t n_quant, const int64_t seg_n[3], int bh_kv, int G, int re
     // alone (the full-precision comparator) they are split like the prefix,
     // a bf16 token costing four int4 tokens of bandwidth.
     int64_t bsplit = CHUNK16;
+    // many heads: bf16 chunks of about the bytes of an int4 chunk, so that the
+    // short chunks do not multiply the per-workgroup costs
+    if (bh_kv >= 32) bsplit = std::max<int64_t>(CHUNK16, split / 4);
     if (n_quant == 0) bsplit = auto_split(seg_n[0] + seg_n[1] + seg_n[2], bh_kv, CHUNK16, SPLIT_MAX_SMALL / 4);
     // keep the chunks of a head within the merge tables
     while (true) {

@@ -12,10 +12,11 @@
 //   int4 chunks hold `split` tokens walked in 32-token groups (wavefront w
 //     takes groups w, w+4, ...) through a three-deep register ring, so two
 //     groups' loads are in flight while one is computed;
-//   bf16 chunks hold 128 tokens of one segment (two 16-token tiles per
-//     wavefront, both loaded up front).
-// int4 chunks are numbered first: they are the long ones, and the short bf16
-// chunks fill the tail of the grid.  Every load goes through a buffer
+//   bf16 chunks hold `bsplit` tokens of one segment (128 with few KV heads,
+//     a quarter of `split` with many) walked in 16-token tiles (wavefront w
+//     takes tiles w, w+4, ...) through a two-deep register ring.
+// int4 chunks are numbered first: they are the long ones, and the bf16 chunks
+// fill the tail of the grid.  Every load goes through a buffer
 // descriptor whose range is the chunk (past the end reads zeros), so the ring's
 // loads are unconditional and their wait counts exact; the loop position
 // travels in the scalar offset.

@@ -13,14 +13,15 @@
 //                 in (score desc, index asc) order (BASELINE's tie rule for the
 //                 unspecified order of torch.topk, src/patch/_common.py:189).
 // Kernels:
-//   qmean_kernel      one thread per (b, ho, d).
+//   qmean_kernel      one workgroup per (b, ho): channel pairs x tail slices.
 //   score_kernel      one thread per key row, G output heads sharing the row
 //                     (GQA-native, the K prefix is read once); writes the
 //                     monotone 16-bit key of each bf16 score.
-//   topk_kernel       one workgroup per (b, ho) row: 4-pass radix select on the
-//                     unique composite (key << 16) | (0xffff - idx) (so "score
-//                     desc, index asc" is just "composite desc"), gather of the
-//                     T survivors into LDS, bitonic sort.
+//   topk_kernel       one workgroup per (b, ho) row: 2-pass radix select of
+//                     the threshold key, ties at the threshold taken in index
+//                     order, winners placed by their rank under the unique
+//                     composite (key << 16) | (0xffff - idx) ("score desc,
+//                     index asc" is "composite desc").
 //   mark_kernel / compact_quant_kernel / gather_rows_kernel  the freeze: a
 //                     bitmap of selected prefix positions, quantisation of the
 //                     unselected prefix rows straight into their compact slots
@@ -34,7 +35,7 @@
 namespace hyq {
 namespace {
 
-constexpr int TOPK_THREADS = 1024;
+constexpr int TOPK_THREADS = 512;
 constexpr int TOPK_MAX_T = 8192;           // bitonic sort buffer in LDS
 constexpr int64_t TOPK_MAX_P = 65536;      // 16-bit index in the composite
 
@@ -48,46 +49,89 @@ __device__ __forceinline__ uint32_t orderable_key(uint16_t b) {
     return (u & 0x8000u) ? (~u & 0xffffu) : (u | 0x8000u);
 }
 
-// qm as float64 (the exact value of the bf16 mean) for the score kernel
-// one thread per (b, hk, g < GP, d); heads g >= G (padding) get zeros
-__global__ __launch_bounds__(128) void qmean_kernel(const uint16_t* __restrict__ q, int64_t qs_b, int64_t qs_h,
-                                                    int64_t qs_t, int QL, int tail, int R, int HK, int G, int GP,
-                                                    int D, int B, double* __restrict__ qm) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t total = static_cast<int64_t>(B) * HK * GP * D;
-    if (idx >= total) return;
-    const int d = static_cast<int>(idx % D);
-    const int g = static_cast<int>((idx / D) % GP);
-    const int bhk = static_cast<int>(idx / (static_cast<int64_t>(D) * GP));
+// qm as float64 (the exact value of the bf16 mean) for the score kernel.
+// One workgroup of QM_THREADS per (b, hk, g < GP): lane l of wavefront w sums
+// channel pair (2l, 2l+1) over the tail rows t = w, w + QM_SLICES, ...; the
+// slices are added in LDS.  Heads g >= G (padding) get zeros.  Every partial
+// sum is a sum of bf16 values (or of bf16 group means), exact in float64, so
+// the split of the tail does not change the result.
+constexpr int QM_THREADS = 1024;
+constexpr int QM_SLICES = QM_THREADS / 64;
+
+__global__ __launch_bounds__(QM_THREADS) void qmean_kernel(const uint16_t* __restrict__ q, int64_t qs_b, int64_t qs_h,
+                                                           int64_t qs_t, int QL, int tail, int R, int HK, int G,
+                                                           int GP, double* __restrict__ qm) {
+    const int row = blockIdx.x;                    // (b, hk, g)
+    const int g = row % GP;
+    const int bhk = row / GP;
+    const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
+    double* out = qm + static_cast<int64_t>(row) * 128;
     if (g >= G) {
-        qm[idx] = 0.0;
+        out[threadIdx.x & 127] = 0.0;
         return;
     }
     const int b = bhk / HK, ho = (bhk % HK) * G + g;
-    const uint16_t* base = q + b * qs_b + static_cast<int64_t>(ho * R) * qs_h + static_cast<int64_t>(QL - tail) * qs_t + d;
-    // every partial sum below is a sum of bf16 values (or of bf16 means),
-    // exact in float64, so the association order does not change the result
-    double outer[4] = {0.0, 0.0, 0.0, 0.0};
-    int t = 0;
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(
+        q + b * qs_b + static_cast<int64_t>(ho * R) * qs_h + static_cast<int64_t>(QL - tail) * qs_t) + lane;
+    const int64_t st = qs_t / 2, sh = qs_h / 2;     // in channel pairs
+    double lo = 0.0, hi = 0.0;
     if (R == 1) {
-        for (; t + 8 <= tail; t += 8) {
-            uint16_t v[8];
+        int t = slice;
+        for (; t + 3 * QM_SLICES < tail; t += 4 * QM_SLICES) {
+            uint32_t v[4];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = base[static_cast<int64_t>(t + u) * qs_t];
+            for (int u = 0; u < 4; ++u) v[u] = base[static_cast<int64_t>(t + u * QM_SLICES) * st];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) outer[u & 3] += bf16_bits_to_f64(v[u]);
+            for (int u = 0; u < 4; ++u) {
+                lo += bf16_bits_to_f64(static_cast<uint16_t>(v[u]));
+                hi += bf16_bits_to_f64(static_cast<uint16_t>(v[u] >> 16));
+            }
         }
-        for (; t < tail; ++t) outer[0] += bf16_bits_to_f64(base[static_cast<int64_t>(t) * qs_t]);
+        for (; t < tail; t += QM_SLICES) {
+            const uint32_t v = base[static_cast<int64_t>(t) * st];
+            lo += bf16_bits_to_f64(static_cast<uint16_t>(v));
+            hi += bf16_bits_to_f64(static_cast<uint16_t>(v >> 16));
+        }
     } else {
-        for (; t < tail; ++t) {
-            double inner = 0.0;
-            for (int r = 0; r < R; ++r) inner += bf16_bits_to_f64(base[static_cast<int64_t>(r) * qs_h + static_cast<int64_t>(t) * qs_t]);
-            outer[t & 3] += bf16_bits_to_f64(f64_to_bf16_rne(inner / R));
+        // four tail rows at a time, so that 4 R loads are in flight per step
+        for (int t = slice; t < tail; t += 4 * QM_SLICES) {
+            double ilo[4] = {0.0, 0.0, 0.0, 0.0}, ihi[4] = {0.0, 0.0, 0.0, 0.0};
+            for (int r = 0; r < R; ++r) {
+                uint32_t v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int tu = t + u * QM_SLICES;
+                    v[u] = tu < tail ? base[static_cast<int64_t>(r) * sh + static_cast<int64_t>(tu) * st] : 0u;
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    ilo[u] += bf16_bits_to_f64(static_cast<uint16_t>(v[u]));
+                    ihi[u] += bf16_bits_to_f64(static_cast<uint16_t>(v[u] >> 16));
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (t + u * QM_SLICES < tail) {
+                    lo += bf16_bits_to_f64(f64_to_bf16_rne(ilo[u] / R));
+                    hi += bf16_bits_to_f64(f64_to_bf16_rne(ihi[u] / R));
+                }
+            }
         }
     }
-    const double s = (outer[0] + outer[1]) + (outer[2] + outer[3]);
-    qm[idx] = bf16_bits_to_f64(f64_to_bf16_rne(s / tail));
+    __shared__ double s_sum[QM_SLICES][128];
+    s_sum[slice][2 * lane] = lo;
+    s_sum[slice][2 * lane + 1] = hi;
+    __syncthreads();
+    if (threadIdx.x < 128) {
+        double sum = 0.0;
+#pragma unroll
+        for (int k = 0; k < QM_SLICES; ++k) sum += s_sum[k][threadIdx.x];
+        out[threadIdx.x] = bf16_bits_to_f64(f64_to_bf16_rne(sum / tail));
+    }
 }
+
+// keys of one output row start 16-byte aligned
+__host__ __device__ inline int64_t key_pitch(int64_t P) { return (P + 7) / 8 * 8; }
 
 // One workgroup per 256 key rows of one (b, hk).  The query means (float64,
 // [GM][128]) sit in LDS and are read with same-address (broadcast) loads.
@@ -102,7 +146,7 @@ constexpr int SC_PITCH = 144;               // LDS bytes per half-row (128 + 16)
 
 template <int GM>
 __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__ k, int64_t ks_b, int64_t ks_h,
-                                                    int64_t ks_n, int HK, int G, int64_t P,
+                                                    int64_t ks_n, int HK, int G, int64_t P, int64_t KP,
                                                     const double* __restrict__ qm, uint16_t* __restrict__ keys) {
     __shared__ __align__(16) double s_q[GM * 128];
     __shared__ __align__(16) uint8_t s_rows[4][SC_ROWS * SC_PITCH];
@@ -157,117 +201,189 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
     if (p < P) {
 #pragma unroll
         for (int g = 0; g < GM; ++g)
-            if (g < G) keys[(static_cast<int64_t>(bh) * G + g) * P + p] = static_cast<uint16_t>(orderable_key(f64_to_bf16_rne(acc[g])));
+            if (g < G) keys[(static_cast<int64_t>(bh) * G + g) * KP + p] = static_cast<uint16_t>(orderable_key(f64_to_bf16_rne(acc[g])));
     }
 }
 
 constexpr int TOPK_WAVES = TOPK_THREADS / 64;
-constexpr int64_t TOPK_LDS_KEYS = 24576;   // rows up to this many keys are cached in LDS
+constexpr int TOPK_RANK_MAX = 2048;        // rows up to this many winners are placed by rank
+constexpr size_t TOPK_LDS_MAX = 64 * 1024; // keys are cached in LDS while the row fits this budget
 
-// One workgroup per (b, ho) row.  The composite (key << 16) | (0xffff - idx)
-// is unique per position and orders "score desc, index asc" as "composite
-// desc": a 4-pass radix select (8 bits per pass, one private histogram per
-// wavefront) finds the T-th largest composite, the T survivors are gathered
-// into LDS and bitonic-sorted.  Rows of up to TOPK_LDS_KEYS keys are read
-// from memory once into LDS.
-__global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __restrict__ keys, int64_t P, int T,
-                                                            int64_t* __restrict__ out) {
-    __shared__ uint32_t hist[TOPK_WAVES][256];
-    __shared__ uint32_t s_prefix, s_need;
-    __shared__ uint32_t s_count;
-    __shared__ uint32_t sel[TOPK_MAX_T];
-    __shared__ uint16_t s_keys[TOPK_LDS_KEYS];
-    const int row = blockIdx.x;
-    const uint16_t* kr = keys + static_cast<int64_t>(row) * P;
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const bool cached = P <= TOPK_LDS_KEYS;
-    if (cached) {
-        for (int64_t i = tid; i < P; i += TOPK_THREADS) s_keys[i] = kr[i];
+// Wavefront 0: the bin holding the need-th largest entry of a 256-bin
+// histogram, scanning from the top.  Writes the bin and the entries still
+// needed inside it.
+__device__ __forceinline__ void topk_find_bin(const uint32_t* hist, uint32_t need, int lane, uint32_t* s_bin,
+                                              uint32_t* s_need) {
+    uint32_t c[4];
+    uint32_t mine = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        c[j] = hist[255 - (4 * lane + j)];
+        mine += c[j];
     }
-    if (tid == 0) {
-        s_prefix = 0;
-        s_need = static_cast<uint32_t>(T);
-        s_count = 0;
+    uint32_t incl = mine;                          // inclusive prefix over lanes (bins from the top)
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+    }
+    uint32_t acc = incl - mine;
+    int found = -1;
+    uint32_t before = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (found < 0 && acc + c[j] >= need) {
+            found = 255 - (4 * lane + j);
+            before = acc;
+        }
+        acc += c[j];
+    }
+    // the first lane (highest bins) that found it wins; the candidates always
+    // number at least `need`, so some lane finds it (were it not so, bin 0
+    // would be taken, as a top-down scan would)
+    const uint64_t ball = __ballot(found >= 0);
+    const int first = ball ? __ffsll(static_cast<long long>(ball)) - 1 : 63;
+    if (lane == first) {
+        if (found < 0) {
+            found = 0;
+            before = acc - c[3];
+        }
+        *s_bin = static_cast<uint32_t>(found);
+        *s_need = need - before;
+    }
+}
+
+// One workgroup per (b, ho) row.  "Score desc, index asc" is "composite
+// desc" for the unique composite (key << 16) | (0xffff - idx).  Two radix
+// passes over the 16-bit keys (one private histogram per wavefront) find the
+// threshold key K and how many of the entries equal to K are taken (the r of
+// lowest index: a prefix count over contiguous per-thread index ranges); the
+// T winners' composites are collected in LDS and each is written straight to
+// its output position, its rank among the winners (T <= TOPK_RANK_MAX), or
+// bitonic-sorted first (larger T).  Dynamic LDS: [hist][winners][keys].
+__global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __restrict__ keys, int64_t P, int T,
+                                                            int n2, int cached, int64_t* __restrict__ out) {
+    extern __shared__ __align__(16) uint32_t tk_lds[];
+    uint32_t* hist = tk_lds;                       // [TOPK_WAVES][256]
+    uint32_t* sel = tk_lds + TOPK_WAVES * 256;     // [n2]
+    uint16_t* s_keys = reinterpret_cast<uint16_t*>(sel + n2);
+    __shared__ uint32_t s_bin, s_need, s_count;
+    __shared__ uint32_t s_wsum[TOPK_WAVES];
+    const int row = blockIdx.x;
+    const uint16_t* kr = keys + static_cast<int64_t>(row) * key_pitch(P);
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    if (cached) {
+        // 16-byte copies, all of a thread's loads issued before its LDS writes
+        const int64_t n8 = (P + 7) / 8;
+        const uint4* src = reinterpret_cast<const uint4*>(kr);
+        uint4* dst = reinterpret_cast<uint4*>(s_keys);
+        for (int64_t i0 = tid; i0 < n8; i0 += 4 * TOPK_THREADS) {
+            uint4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i0 + u * TOPK_THREADS < n8) v[u] = src[i0 + u * TOPK_THREADS];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i0 + u * TOPK_THREADS < n8) dst[i0 + u * TOPK_THREADS] = v[u];
+        }
     }
     auto key_at = [&](int64_t i) -> uint32_t { return cached ? s_keys[i] : kr[i]; };
-    // radix select, most significant byte first: find the T-th largest composite
-    for (int pass = 0; pass < 4; ++pass) {
-        const int shift = 24 - 8 * pass;
-        for (int i = tid; i < TOPK_WAVES * 256; i += TOPK_THREADS) (&hist[0][0])[i] = 0;
+    uint32_t need = static_cast<uint32_t>(T);
+    uint32_t khi = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int i = tid; i < TOPK_WAVES * 256; i += TOPK_THREADS) hist[i] = 0;
         __syncthreads();
-        const uint32_t prefix = s_prefix;
-        const uint32_t pmask = pass == 0 ? 0u : (0xffffffffu << (32 - 8 * pass));
         for (int64_t i = tid; i < P; i += TOPK_THREADS) {
-            const uint32_t comp = (key_at(i) << 16) | (0xffffu - static_cast<uint32_t>(i));
-            if ((comp & pmask) == prefix) atomicAdd(&hist[wave][(comp >> shift) & 0xffu], 1u);
+            const uint32_t key = key_at(i);
+            if (pass == 0) atomicAdd(&hist[wave * 256 + (key >> 8)], 1u);
+            else if ((key >> 8) == khi) atomicAdd(&hist[wave * 256 + (key & 0xffu)], 1u);
         }
         __syncthreads();
-        // fold the per-wavefront histograms into hist[0]
         if (tid < 256) {
-            uint32_t s = 0;
+            uint32_t sum = 0;
 #pragma unroll
-            for (int w = 0; w < TOPK_WAVES; ++w) s += hist[w][tid];
-            hist[0][tid] = s;
+            for (int w = 0; w < TOPK_WAVES; ++w) sum += hist[w * 256 + tid];
+            hist[tid] = sum;
         }
         __syncthreads();
-        if (tid < 64) {
-            // wavefront 0: find the bin holding the need-th largest, from the top
-            const uint32_t need = s_need;
-            uint32_t c[4];
-            uint32_t mine = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                c[j] = hist[0][255 - (4 * tid + j)];
-                mine += c[j];
-            }
-            // exclusive prefix over lanes (bins from the top)
-            uint32_t incl = mine;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint32_t o = __shfl_up(incl, off, 64);
-                if (tid >= off) incl += o;
-            }
-            uint32_t acc = incl - mine;
-            int found = -1;
-            uint32_t before = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (found < 0 && acc + c[j] >= need) {
-                    found = 255 - (4 * tid + j);
-                    before = acc;
-                }
-                acc += c[j];
-            }
-            // the first lane (highest bins) that found it wins; the candidates
-            // always number at least `need`, so some lane finds it (were it
-            // not so, bin 0 would be taken, as a top-down scan would)
-            const uint64_t ball = __ballot(found >= 0);
-            const int first = ball ? __ffsll(static_cast<long long>(ball)) - 1 : 63;
-            if (tid == first) {
-                if (found < 0) {
-                    found = 0;
-                    before = acc - c[3];
-                }
-                s_need = need - before;
-                s_prefix = prefix | (static_cast<uint32_t>(found) << shift);
-            }
-        }
+        if (wave == 0) topk_find_bin(hist, need, lane, &s_bin, &s_need);
         __syncthreads();
+        if (pass == 0) khi = s_bin;
+        need = s_need;
     }
-    const uint32_t thr = s_prefix;                 // exactly T composites are >= thr
-    for (int64_t i = tid; i < P; i += TOPK_THREADS) {
-        const uint32_t comp = (key_at(i) << 16) | (0xffffu - static_cast<uint32_t>(i));
-        if (comp >= thr) {
-            const uint32_t pos = atomicAdd(&s_count, 1u);
-            if (pos < static_cast<uint32_t>(T)) sel[pos] = comp;
-        }
+    const uint32_t kth = (khi << 8) | s_bin;       // threshold key
+    const uint32_t r = need;                       // entries equal to kth that are taken
+    // thread t scans indices [t*C, t*C + C) (C a multiple of 8, read 16 bytes
+    // at a time): entries above kth are winners; the entries equal to kth are
+    // numbered in index order by a prefix count over the threads
+    const int64_t C = (P + 8 * TOPK_THREADS - 1) / (8 * TOPK_THREADS) * 8;
+    const int64_t i0 = static_cast<int64_t>(tid) * C;
+    const uint4* k4 = cached ? reinterpret_cast<const uint4*>(s_keys) : reinterpret_cast<const uint4*>(kr);
+    if (tid == 0) s_count = 0;
+    uint32_t eq = 0;
+    for (int64_t ib = i0; ib < i0 + C && ib < P; ib += 8) {
+        const uint4 w = k4[ib >> 3];
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) eq += (ib + j < P) && ((ws[j >> 1] >> (16 * (j & 1))) & 0xffffu) == kth;
     }
+    uint32_t incl = eq;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+    }
+    if (lane == 63) s_wsum[wave] = incl;
     __syncthreads();
-    int n2 = 1;
-    while (n2 < T) n2 <<= 1;
+    uint32_t base = incl - eq;
+    for (int w = 0; w < wave; ++w) base += s_wsum[w];
+    for (int64_t ib = i0; ib < i0 + C && ib < P; ib += 8) {
+        const uint4 w = k4[ib >> 3];
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int64_t i = ib + j;
+            const uint32_t key = (ws[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+            bool take = i < P && key > kth;
+            if (i < P && key == kth) take = base++ < r;
+            if (take) sel[atomicAdd(&s_count, 1u)] = (key << 16) | (0xffffu - static_cast<uint32_t>(i));
+        }
+    }
     for (int i = T + tid; i < n2; i += TOPK_THREADS) sel[i] = 0;   // real composites are > 0
     __syncthreads();
+    int64_t* orow = out + static_cast<int64_t>(row) * T;
+    if (T <= TOPK_RANK_MAX) {
+        // rank = number of larger winners.  A thread ranks its (up to 4)
+        // winners in one sweep; every lane of a wavefront reads the same four
+        // composites per step (LDS broadcast)
+        constexpr int E = TOPK_RANK_MAX / TOPK_THREADS;
+        uint32_t v[E], rank[E];
+#pragma unroll
+        for (int u = 0; u < E; ++u) {
+            v[u] = tid + u * TOPK_THREADS < T ? sel[tid + u * TOPK_THREADS] : 0u;
+            rank[u] = 0;
+        }
+        const uint4* s4 = reinterpret_cast<const uint4*>(sel);
+        const int ne = (T - tid + TOPK_THREADS - 1) / TOPK_THREADS;   // winners of this thread
+        if (ne > 2) {
+            for (int j = 0; j < n2 / 4; ++j) {
+                const uint4 w = s4[j];
+#pragma unroll
+                for (int u = 0; u < E; ++u) rank[u] += (w.x > v[u]) + (w.y > v[u]) + (w.z > v[u]) + (w.w > v[u]);
+            }
+        } else if (ne > 0) {
+            for (int j = 0; j < n2 / 4; ++j) {
+                const uint4 w = s4[j];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) rank[u] += (w.x > v[u]) + (w.y > v[u]) + (w.z > v[u]) + (w.w > v[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < E; ++u)
+            if (u < ne) orow[rank[u]] = static_cast<int64_t>(0xffffu - (v[u] & 0xffffu));
+        return;
+    }
     // bitonic sort, descending
     for (int size = 2; size <= n2; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -275,17 +391,36 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __re
                 const int lo = 2 * i - (i & (stride - 1));
                 const int hi = lo + stride;
                 const bool desc = ((lo & size) == 0);
-                const uint32_t a = sel[lo], bb = sel[hi];
-                if ((a < bb) == desc) {
-                    sel[lo] = bb;
-                    sel[hi] = a;
+                const uint32_t x = sel[lo], y = sel[hi];
+                if ((x < y) == desc) {
+                    sel[lo] = y;
+                    sel[hi] = x;
                 }
             }
             __syncthreads();
         }
     }
-    for (int i = tid; i < T; i += TOPK_THREADS)
-        out[static_cast<int64_t>(row) * T + i] = static_cast<int64_t>(0xffffu - (sel[i] & 0xffffu));
+    for (int i = tid; i < T; i += TOPK_THREADS) orow[i] = static_cast<int64_t>(0xffffu - (sel[i] & 0xffffu));
+}
+
+// LDS plan of topk_kernel for a row of P keys and T winners
+struct TopkPlan {
+    int n2, cached;
+    size_t lds;
+};
+TopkPlan topk_plan(int64_t P, int T) {
+    TopkPlan t;
+    if (T <= TOPK_RANK_MAX) {
+        t.n2 = (T + 3) / 4 * 4;
+    } else {
+        t.n2 = 1;
+        while (t.n2 < T) t.n2 <<= 1;
+    }
+    const size_t fixed = (static_cast<size_t>(TOPK_WAVES) * 256 + t.n2) * 4;
+    const size_t with_keys = fixed + (static_cast<size_t>(P) * 2 + 15) / 16 * 16;
+    t.cached = with_keys <= TOPK_LDS_MAX;
+    t.lds = t.cached ? with_keys : fixed;
+    return t;
 }
 
 // ---------------------------------------------------------------------------
@@ -307,12 +442,15 @@ __global__ void mark_kernel(const int64_t* __restrict__ idx, int T, int64_t P, i
 }
 
 constexpr int CQ_CHUNK = 256;               // prefix positions per workgroup
+constexpr int CQ_UNROLL = 4;                // tokens per 16-lane group per pass
 
+// 16 lanes quantise one bf16 row of 128 channels: lane `sub` holds channels
+// 8 sub .. 8 sub + 7 (`raw`).  All 16 lanes take part in the amax reduction;
+// only the stores depend on `store`.
 template <int NBITS>
-__device__ __forceinline__ void quant_row_group(const uint16_t* src, int8_t* dst, uint16_t* scl, int sub) {
+__device__ __forceinline__ void quant_row_group(uint4 raw, int8_t* dst, uint16_t* scl, int sub, bool store) {
     constexpr int QMAX = (1 << (NBITS - 1)) - 1;
     constexpr int QMIN = -(1 << (NBITS - 1));
-    const uint4 raw = *reinterpret_cast<const uint4*>(src + sub * 8);
     float v[8];
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
@@ -336,6 +474,7 @@ __device__ __forceinline__ void quant_row_group(const uint16_t* src, int8_t* dst
         r = fminf(fmaxf(r, static_cast<float>(QMIN)), static_cast<float>(QMAX));
         c[i] = static_cast<int>(r);
     }
+    if (!store) return;
     if (NBITS == 4) {
         uint32_t word = 0;
 #pragma unroll
@@ -399,19 +538,34 @@ __global__ __launch_bounds__(256) void compact_quant_kernel(CompactArgs a) {
     }
     __syncthreads();
     const uint32_t base = s_base;
-    // 16 lanes per token, 16 tokens per pass
+    // 16 lanes per token; each 16-lane group takes CQ_UNROLL tokens per pass
+    // and issues their K and V row loads together (selected rows are loaded
+    // too and simply not stored, which keeps the loads unconditional)
     const int sub = threadIdx.x & 15;
-    for (int j = threadIdx.x >> 4; j < CQ_CHUNK; j += 16) {
-        const int64_t p = p0 + j;
-        if (p >= a.P) break;
-        const uint32_t word = rb[p >> 5];
-        if ((word >> (p & 31)) & 1u) continue;   // selected: stays bf16 in k/v_topk
-        const uint32_t below = __popc(word & ((1u << (p & 31)) - 1u));
-        const int64_t dst = p - (base + s_wpre[j >> 5] + below);
-        quant_row_group<KB>(a.k + b * a.ks_b + hk * a.ks_h + p * a.ks_n,
-                            a.kp + bh * a.kp_bh + dst * a.kp_n, a.ksc + bh * a.ksc_bh + dst, sub);
-        quant_row_group<VB>(a.v + b * a.vs_b + hk * a.vs_h + p * a.vs_n,
-                            a.vp + bh * a.vp_bh + dst * a.vp_n, a.vsc + bh * a.vsc_bh + dst, sub);
+    const uint16_t* kbase = a.k + b * a.ks_b + hk * a.ks_h + sub * 8;
+    const uint16_t* vbase = a.v + b * a.vs_b + hk * a.vs_h + sub * 8;
+    for (int j0 = threadIdx.x >> 4; j0 < CQ_CHUNK; j0 += 16 * CQ_UNROLL) {
+        uint4 kr[CQ_UNROLL], vr[CQ_UNROLL];
+        int64_t pp[CQ_UNROLL];
+#pragma unroll
+        for (int u = 0; u < CQ_UNROLL; ++u) {
+            const int64_t p = p0 + j0 + 16 * u;
+            pp[u] = p;
+            const int64_t pc = p < a.P ? p : a.P - 1;
+            kr[u] = *reinterpret_cast<const uint4*>(kbase + pc * a.ks_n);
+            vr[u] = *reinterpret_cast<const uint4*>(vbase + pc * a.vs_n);
+        }
+#pragma unroll
+        for (int u = 0; u < CQ_UNROLL; ++u) {
+            const int64_t p = pp[u];
+            const int j = j0 + 16 * u;
+            const uint32_t word = p < a.P ? rb[p >> 5] : 1u << (p & 31);
+            const bool keep = p < a.P && !((word >> (p & 31)) & 1u);     // selected rows stay bf16 in k/v_topk
+            const uint32_t below = __popc(word & ((1u << (p & 31)) - 1u));
+            const int64_t dst = keep ? p - (base + s_wpre[j >> 5] + below) : 0;
+            quant_row_group<KB>(kr[u], a.kp + bh * a.kp_bh + dst * a.kp_n, a.ksc + bh * a.ksc_bh + dst, sub, keep);
+            quant_row_group<VB>(vr[u], a.vp + bh * a.vp_bh + dst * a.vp_n, a.vsc + bh * a.vsc_bh + dst, sub, keep);
+        }
     }
 }
 
@@ -451,7 +605,7 @@ int padded_heads(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ?
 
 size_t select_ws(int B, int H_out, int64_t P) {
     const size_t qm = static_cast<size_t>(B) * H_out * 128 * sizeof(double) * 4;   // room for head padding
-    return ((qm + 255) / 256) * 256 + static_cast<size_t>(B) * H_out * P * 2;
+    return ((qm + 255) / 256) * 256 + static_cast<size_t>(B) * H_out * key_pitch(P) * 2;
 }
 
 }  // namespace
@@ -481,29 +635,32 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
     if (tail <= 0 || tail > q_len) return fail(HYQ_EINVAL, "hyq_vertical_select: bad query tail");
     if (!q || !k || !out_idx) return fail(HYQ_EINVAL, "hyq_vertical_select: null pointer");
     if (!aligned(k, 16) || ks_n % 8 || ks_h % 8 || ks_b % 8) return fail(HYQ_EINVAL, "hyq_vertical_select: keys must be 16-byte aligned rows");
+    if (!aligned(q, 4) || qs_t % 2 || qs_h % 2 || qs_b % 2) return fail(HYQ_EINVAL, "hyq_vertical_select: query rows must be 4-byte aligned");
     const size_t need = select_ws(b, h_out, p);
-    if (!workspace || ws_bytes < need) return fail(HYQ_ENOSPC, "hyq_vertical_select: workspace too small");
+    if (!workspace || ws_bytes < need || !aligned(workspace, 16))
+        return fail(HYQ_ENOSPC, "hyq_vertical_select: workspace too small or not 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
     double* qm = static_cast<double*>(workspace);
     const size_t qm_bytes = ((static_cast<size_t>(b) * h_out * 128 * sizeof(double) * 4 + 255) / 256) * 256;
     uint16_t* keys = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + qm_bytes);
     const int GP = padded_heads(G);
-    const int64_t nq = static_cast<int64_t>(b) * hk * GP * 128;
-    qmean_kernel<<<dim3(static_cast<unsigned>((nq + 127) / 128)), dim3(128), 0, s>>>(q, qs_b, qs_h, qs_t, q_len, tail, group,
-                                                                                   hk, G, GP, 128, b, qm);
+    qmean_kernel<<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(QM_THREADS), 0, s>>>(q, qs_b, qs_h, qs_t, q_len, tail,
+                                                                                     group, hk, G, GP, qm);
     int rc = check_launch("hyq_vertical_select (mean)");
     if (rc) return rc;
     const dim3 sgrid(static_cast<unsigned>((p + 255) / 256), static_cast<unsigned>(b * hk));
     switch (GP) {
-        case 1: score_kernel<1><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, qm, keys); break;
-        case 2: score_kernel<2><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, qm, keys); break;
-        case 4: score_kernel<4><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, qm, keys); break;
-        case 8: score_kernel<8><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, qm, keys); break;
-        default: score_kernel<16><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, qm, keys); break;
+        case 1: score_kernel<1><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys); break;
+        case 2: score_kernel<2><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys); break;
+        case 4: score_kernel<4><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys); break;
+        case 8: score_kernel<8><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys); break;
+        default: score_kernel<16><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys); break;
     }
     rc = check_launch("hyq_vertical_select (score)");
     if (rc) return rc;
-    topk_kernel<<<dim3(static_cast<unsigned>(b * h_out)), dim3(TOPK_THREADS), 0, s>>>(keys, p, top_k, out_idx);
+    const TopkPlan tp = topk_plan(p, top_k);
+    topk_kernel<<<dim3(static_cast<unsigned>(b * h_out)), dim3(TOPK_THREADS), tp.lds, s>>>(keys, p, top_k, tp.n2,
+                                                                                        tp.cached, out_idx);
     return check_launch("hyq_vertical_select (topk)");
 }
 

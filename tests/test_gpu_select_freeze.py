@@ -22,6 +22,8 @@ def _rand_bf16(rng, shape, scale=1.0):
     (1, 4, 4, 7, 200, 16, 0.2),       # non-GQA, tail shorter than W
     (1, 16, 1, 5, 1000, 64, 0.05),    # GQA 16
     (3, 2, 2, 64, 129, 128, 1.0),     # prefix of one token, rho = 1
+    (1, 2, 2, 8, 16064, 64, 0.1),     # 1600 winners: several ranked per thread, keys cached in LDS
+    (1, 2, 1, 16, 30064, 64, 0.1),    # 3000 winners: bitonic order, keys read from memory
 ])
 def test_selector_prefill_variant_bit_exact(B, HQ, HK, QL, KL, W, rho):
     from hyquant_amd.vertical import compute_vertical_indices

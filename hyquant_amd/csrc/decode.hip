@@ -228,6 +228,9 @@ __device__ __forceinline__ u32x4 bld128(Rsrc r, uint32_t voff, uint32_t soff = 0
 __device__ __forceinline__ uint32_t bld32(Rsrc r, uint32_t voff, uint32_t soff = 0) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
 }
+__device__ __forceinline__ u32x2 bld64(Rsrc r, uint32_t voff, uint32_t soff = 0) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
 __device__ __forceinline__ uint32_t bld16(Rsrc r, uint32_t voff, uint32_t soff = 0) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
 }
@@ -237,35 +240,104 @@ __device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
     return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xf, 0xf, false));
 }
 
-struct Int4Raw {
-    u32x4 k[2];            // tile t: token 16t + c, bytes 16kb..16kb+15 (channels 32kb..32kb+31)
-    uint32_t v[8];         // slot e: token tau(kb, e), bytes 4c..4c+3 (channels 8c..8c+7)
-    uint32_t sk[2], sv[2]; // tile t: fp16 scale bits of token 16t + 4kb + (c & 3)
+// Quantised prefix with KB-bit K codes and VB-bit V codes (2, 4 or 8; packed
+// rows of 16*bits bytes, src/ops/decode_d_stage.py:104-133).  Per lane:
+//   k[t][*]  tile t: token 16t + c, channels 32kb..32kb+31 (KB dwords)
+//   v[e][*]  slot e: token tau(kb, e), channels 8c..8c+7 (VB bytes; 2-byte
+//            loads are zero-extended)
+//   sk, sv   tile t: fp16 scale bits of token 16t + 4kb + (c & 3)
+template <int KB, int VB>
+struct QRaw {
+    uint32_t k[2][KB];
+    uint32_t v[8][VB == 8 ? 2 : 1];
+    uint32_t sk[2], sv[2];
 };
 
-constexpr int PROW = D / 2;               // packed bytes per token
+constexpr int prow(int bits) { return 16 * bits; }   // packed bytes per token (D = 128)
 constexpr int BROW = D;                   // bf16 row stride in elements
 
-struct Int4Ctx {
+struct QCtx {
     Rsrc k, v, ks, vs;     // this chunk's packed K / V rows and scales
-    uint32_t klane;        // lane offset of tile 0: c * 64 + 16 * kb
-    uint32_t vlane;        // lane offset of slot 0: 4kb * 64 + 4c
+    uint32_t klane;        // lane offset of tile 0: c * prow(KB) + 4 KB kb
+    uint32_t vlane;        // lane offset of slot 0: 4kb * prow(VB) + VB c
     uint32_t slane;        // lane offset of the scale of tile 0: (4kb + (c & 3)) * 2
 };
 
 // t0 is wave-uniform: it only enters the scalar offsets
-__device__ __forceinline__ void int4_load(Int4Raw& r, const Int4Ctx& x, int t0) {
-    const uint32_t so = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t0) * PROW);
+template <int KB, int VB>
+__device__ __forceinline__ void qload(QRaw<KB, VB>& r, const QCtx& x, int t0) {
+    const uint32_t sok = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t0) * prow(KB));
+    const uint32_t sov = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t0) * prow(VB));
     const uint32_t ss = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t0) * 2);
-    r.k[0] = bld128(x.k, x.klane, so);
-    r.k[1] = bld128(x.k, x.klane + 16 * PROW, so);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) r.v[e] = bld32(x.v, x.vlane + tau(0, e) * PROW, so);
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t ko = x.klane + t * 16 * prow(KB);
+        if constexpr (KB == 2) {
+            const u32x2 w = bld64(x.k, ko, sok);
+            r.k[t][0] = w[0]; r.k[t][1] = w[1];
+        } else {
+#pragma unroll
+            for (int h = 0; h < KB / 4; ++h) {
+                const u32x4 w = bld128(x.k, ko + 16 * h, sok);
+                r.k[t][4 * h] = w[0]; r.k[t][4 * h + 1] = w[1]; r.k[t][4 * h + 2] = w[2]; r.k[t][4 * h + 3] = w[3];
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t vo = x.vlane + tau(0, e) * prow(VB);
+        if constexpr (VB == 2) {
+            r.v[e][0] = bld16(x.v, vo, sov);
+        } else if constexpr (VB == 4) {
+            r.v[e][0] = bld32(x.v, vo, sov);
+        } else {
+            const u32x2 w = bld64(x.v, vo, sov);
+            r.v[e][0] = w[0]; r.v[e][1] = w[1];
+        }
+    }
     r.sk[0] = bld16(x.ks, x.slane, ss);
     r.sk[1] = bld16(x.ks, x.slane + 32, ss);
     r.sv[0] = bld16(x.vs, x.slane, ss);
     r.sv[1] = bld16(x.vs, x.slane + 32, ss);
 }
+
+// QK A operand of MFMA m (channels 32kb + 8m + [0..7]) as exact fp16 codes in
+// slot order [c0,c4,c1,c5,c2,c6,c3,c7], the order of the Q operands:
+//   4 bits: fp16(1024 + (nibble ^ 8)) - 1032             (int4_to_f16x8)
+//   8 bits: fp16(1024 + (byte ^ 0x80)) - 1152; byte j of the two dwords
+//           paired by one perm
+//   2 bits: fp16(1024 + (crumb ^ 2)) - 1026; the two bytes of the 16-bit
+//           half spread to the two fp16 halves by one perm
+template <int KB>
+__device__ __forceinline__ f16x8 k_operand(const uint32_t (&k)[KB], int m) {
+    if constexpr (KB == 4) {
+        return int4_to_f16x8(k[m]);
+    } else if constexpr (KB == 8) {
+        const f16x2 bias = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+        const uint32_t lo = k[2 * m], hi = k[2 * m + 1];
+        const u32x4 o = {f16x2_add(perm(hi, lo, 0x0c040c00u) ^ 0x64806480u, bias),
+                         f16x2_add(perm(hi, lo, 0x0c050c01u) ^ 0x64806480u, bias),
+                         f16x2_add(perm(hi, lo, 0x0c060c02u) ^ 0x64806480u, bias),
+                         f16x2_add(perm(hi, lo, 0x0c070c03u) ^ 0x64806480u, bias)};
+        return __builtin_bit_cast(f16x8, o);
+    } else {
+        const f16x2 bias = {static_cast<_Float16>(-1026.0f), static_cast<_Float16>(-1026.0f)};
+        const uint32_t w = k[m >> 1];
+        const uint32_t y = (m & 1) ? perm(w, w, 0x0c030c02u) : perm(w, w, 0x0c010c00u);
+        const u32x4 o = {f16x2_add(((y >> 0) & 0x00030003u) ^ 0x64026402u, bias),
+                         f16x2_add(((y >> 2) & 0x00030003u) ^ 0x64026402u, bias),
+                         f16x2_add(((y >> 4) & 0x00030003u) ^ 0x64026402u, bias),
+                         f16x2_add(((y >> 6) & 0x00030003u) ^ 0x64026402u, bias)};
+        return __builtin_bit_cast(f16x8, o);
+    }
+}
+
+// The constant the PV operands add to every V code (removed at the end with
+// the all-ones product): bf16(128 + u) operands, u = code + 8 (4 bits),
+// code + 2 (2 bits); 8-bit codes are split into their nibbles,
+// bf16(128 + lo) + bf16(16 (128 + (hi ^ 8))) = code + 2304.
+template <int VB>
+constexpr float v_offset() { return VB == 4 ? 136.0f : VB == 2 ? 130.0f : 2304.0f; }
 
 // The four lanes of a quad hold the scales of tokens 4kb..4kb+3 of a tile;
 // quad broadcasts give every lane all four.
@@ -276,8 +348,9 @@ __device__ __forceinline__ void quad_scales(uint32_t v, float* out) {
     out[3] = f16_bits_to_f32(static_cast<uint16_t>(dpp_mov<0xff>(v)));
 }
 
-__device__ __forceinline__ void int4_compute(WaveState& st, const Int4Raw& r, const f16x8 (&qop)[4], int nv,
-                                             int lane, float qk) {
+template <int KB, int VB>
+__device__ __forceinline__ void qcompute(WaveState& st, const QRaw<KB, VB>& r, const f16x8 (&qop)[4], int nv,
+                                         int lane, float qk) {
     const int kb = lane >> 4;
     float sk[8], sv[8];
     quad_scales(r.sk[0], sk); quad_scales(r.sk[1], sk + 4);
@@ -287,10 +360,8 @@ __device__ __forceinline__ void int4_compute(WaveState& st, const Int4Raw& r, co
 #pragma unroll
     for (int tile = 0; tile < 2; ++tile) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = mfma_f16(int4_to_f16x8(r.k[tile][0]), qop[0], acc);
-        acc = mfma_f16(int4_to_f16x8(r.k[tile][1]), qop[1], acc);
-        acc = mfma_f16(int4_to_f16x8(r.k[tile][2]), qop[2], acc);
-        acc = mfma_f16(int4_to_f16x8(r.k[tile][3]), qop[3], acc);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc = mfma_f16(k_operand<KB>(r.k[tile], m), qop[m], acc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) s[4 * tile + i] = acc[i] * (sk[4 * tile + i] * qk);
     }
@@ -304,20 +375,53 @@ __device__ __forceinline__ void int4_compute(WaveState& st, const Int4Raw& r, co
     const u32x4 pw = {pack_bf16x2(s[0] * sv[0], s[1] * sv[1]), pack_bf16x2(s[2] * sv[2], s[3] * sv[3]),
                       pack_bf16x2(s[4] * sv[4], s[5] * sv[5]), pack_bf16x2(s[6] * sv[6], s[7] * sv[7])};
     const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
-    // V^T operands: bf16(128 + u) = code + 136, token pairs merged by perm
-    uint32_t lo[4], hi[4];
+    // V^T operands (A of PV MFMA nb: channel 8c + nb of the 8 token slots),
+    // token pairs (2pr, 2pr + 1) merged into one dword per operand register
+    if constexpr (VB == 4) {
+        // bf16(128 + u) = code + 136
+        uint32_t lo[4], hi[4];
 #pragma unroll
-    for (int pr = 0; pr < 4; ++pr) {
-        lo[pr] = perm(r.v[2 * pr + 1], r.v[2 * pr], 0x05040100u);  // nibbles 0-3 of both tokens
-        hi[pr] = perm(r.v[2 * pr + 1], r.v[2 * pr], 0x07060302u);  // nibbles 4-7
-    }
+        for (int pr = 0; pr < 4; ++pr) {
+            lo[pr] = perm(r.v[2 * pr + 1][0], r.v[2 * pr][0], 0x05040100u);  // nibbles 0-3 of both tokens
+            hi[pr] = perm(r.v[2 * pr + 1][0], r.v[2 * pr][0], 0x07060302u);  // nibbles 4-7
+        }
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-        const uint32_t* src = nb < 4 ? lo : hi;
-        const int sh = 4 * (nb & 3);
-        const u32x4 w = {nib2(src[0], sh, 0x43084308u), nib2(src[1], sh, 0x43084308u),
-                         nib2(src[2], sh, 0x43084308u), nib2(src[3], sh, 0x43084308u)};
-        st.acc[nb] = mfma_bf16(__builtin_bit_cast(bf16x8, w), pop, st.acc[nb]);
+        for (int nb = 0; nb < 8; ++nb) {
+            const uint32_t* src = nb < 4 ? lo : hi;
+            const int sh = 4 * (nb & 3);
+            const u32x4 w = {nib2(src[0], sh, 0x43084308u), nib2(src[1], sh, 0x43084308u),
+                             nib2(src[2], sh, 0x43084308u), nib2(src[3], sh, 0x43084308u)};
+            st.acc[nb] = mfma_bf16(__builtin_bit_cast(bf16x8, w), pop, st.acc[nb]);
+        }
+    } else if constexpr (VB == 2) {
+        // bf16(128 + (crumb ^ 2)) = code + 130
+        uint32_t x[4];
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) x[pr] = perm(r.v[2 * pr + 1][0], r.v[2 * pr][0], 0x05040100u);
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+            const int sh = 2 * nb;
+            const u32x4 w = {((x[0] >> sh) & 0x00030003u) ^ 0x43024302u, ((x[1] >> sh) & 0x00030003u) ^ 0x43024302u,
+                             ((x[2] >> sh) & 0x00030003u) ^ 0x43024302u, ((x[3] >> sh) & 0x00030003u) ^ 0x43024302u};
+            st.acc[nb] = mfma_bf16(__builtin_bit_cast(bf16x8, w), pop, st.acc[nb]);
+        }
+    } else {
+        // code = 16 hi + lo (hi signed, lo unsigned): two products per channel
+        // into one accumulator, bf16(128 + lo) and bf16(16 (128 + (hi ^ 8)))
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+            const int dw = nb >> 2;
+            const uint32_t sel = 0x0c040c00u + 0x00010001u * (nb & 3);
+            uint32_t x[4];
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr) x[pr] = perm(r.v[2 * pr + 1][dw], r.v[2 * pr][dw], sel);
+            const u32x4 wl = {(x[0] & 0x000f000fu) | 0x43004300u, (x[1] & 0x000f000fu) | 0x43004300u,
+                              (x[2] & 0x000f000fu) | 0x43004300u, (x[3] & 0x000f000fu) | 0x43004300u};
+            const u32x4 wh = {nib2(x[0], 4, 0x45084508u), nib2(x[1], 4, 0x45084508u),
+                              nib2(x[2], 4, 0x45084508u), nib2(x[3], 4, 0x45084508u)};
+            st.acc[nb] = mfma_bf16(__builtin_bit_cast(bf16x8, wl), pop, st.acc[nb]);
+            st.acc[nb] = mfma_bf16(__builtin_bit_cast(bf16x8, wh), pop, st.acc[nb]);
+        }
     }
     const u32x4 onesw = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
     st.ones = mfma_bf16(__builtin_bit_cast(bf16x8, onesw), pop, st.ones);
@@ -482,6 +586,7 @@ __device__ __forceinline__ void merge_head(const DecArgs& a, int head, float* s_
 // ---------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------
+template <int KB, int VB>
 __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
     const int nh = a.bh_kv;
     const int head = blockIdx.x % nh;
@@ -545,15 +650,15 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         // ---------------- int4 chunk: groups wave, wave+WAVES, ... ----------------
         const int lo = (wg - a.n16) * a.split;
         const int ntok = min(a.split, a.n_quant - lo);
-        Int4Ctx x;
-        x.k = make_rsrc(a.kp + static_cast<int64_t>(head) * a.kp_bh + static_cast<int64_t>(lo) * PROW,
-                        static_cast<uint32_t>(ntok) * PROW);
-        x.v = make_rsrc(a.vp + static_cast<int64_t>(head) * a.vp_bh + static_cast<int64_t>(lo) * PROW,
-                        static_cast<uint32_t>(ntok) * PROW);
+        QCtx x;
+        x.k = make_rsrc(a.kp + static_cast<int64_t>(head) * a.kp_bh + static_cast<int64_t>(lo) * prow(KB),
+                        static_cast<uint32_t>(ntok) * prow(KB));
+        x.v = make_rsrc(a.vp + static_cast<int64_t>(head) * a.vp_bh + static_cast<int64_t>(lo) * prow(VB),
+                        static_cast<uint32_t>(ntok) * prow(VB));
         x.ks = make_rsrc(a.ks + static_cast<int64_t>(head) * a.ks_bh + lo, static_cast<uint32_t>(ntok) * 2);
         x.vs = make_rsrc(a.vs + static_cast<int64_t>(head) * a.vs_bh + lo, static_cast<uint32_t>(ntok) * 2);
-        x.klane = static_cast<uint32_t>(c * PROW + 16 * kb);
-        x.vlane = static_cast<uint32_t>(4 * kb * PROW + 4 * c);
+        x.klane = static_cast<uint32_t>(c * prow(KB) + 4 * KB * kb);
+        x.vlane = static_cast<uint32_t>(4 * kb * prow(VB) + VB * c);
         x.slane = static_cast<uint32_t>((4 * kb + (c & 3)) * 2);
         // groups wave, wave+WAVES, ... of the chunk through a three-deep
         // register ring: two groups' loads in flight while one is computed
@@ -561,9 +666,9 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         const int ngrp = (ntok + GROUP - 1) / GROUP;
         const int nmine = ngrp > wave ? (ngrp - wave + WAVES - 1) / WAVES : 0;
         const int t0 = wave * GROUP;
-        Int4Raw b0, b1, b2;
-        int4_load(b0, x, t0);
-        int4_load(b1, x, t0 + STRIDE);
+        QRaw<KB, VB> b0, b1, b2;
+        qload(b0, x, t0);
+        qload(b1, x, t0 + STRIDE);
 
         // Q -> fp16 in int4 slot order, pre-scaled by 2^-ex so |q| < 2^15
         float qf[32];
@@ -595,17 +700,17 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         const float qk = a.qk_scale * ldexpf(1.0f, ex);
         for (int i = 0; i < nmine; i += 3) {
             const int t = t0 + i * STRIDE;
-            int4_load(b2, x, t + 2 * STRIDE);
-            int4_compute(st, b0, qop, ntok - t, lane, qk);
+            qload(b2, x, t + 2 * STRIDE);
+            qcompute(st, b0, qop, ntok - t, lane, qk);
             if (i + 1 >= nmine) break;
-            int4_load(b0, x, t + 3 * STRIDE);
-            int4_compute(st, b1, qop, ntok - t - STRIDE, lane, qk);
+            qload(b0, x, t + 3 * STRIDE);
+            qcompute(st, b1, qop, ntok - t - STRIDE, lane, qk);
             if (i + 2 >= nmine) break;
-            int4_load(b1, x, t + 4 * STRIDE);
-            int4_compute(st, b2, qop, ntok - t - 2 * STRIDE, lane, qk);
+            qload(b1, x, t + 4 * STRIDE);
+            qcompute(st, b2, qop, ntok - t - 2 * STRIDE, lane, qk);
         }
-        // remove the +136 offset of the V codes: acc -= 136 * sum_t P'
-        const float corr = 136.0f * st.ones[0];
+        // remove the offset of the V operands: acc -= offset * sum_t P'
+        const float corr = v_offset<VB>() * st.ones[0];
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) st.acc[nb] -= corr;
     }
@@ -746,9 +851,10 @@ Layout layout(const Plan& pl, int bh_kv, int G) {
 int validate(const hyq_decode_params* p) {
     if (!p) return fail(HYQ_EINVAL, "null params");
     if (p->head_dim != D) return fail(HYQ_ENOTSUP, "head_dim must be 128, got " + std::to_string(p->head_dim));
-    if (p->k_bits != 4 || p->v_bits != 4)
-        return fail(HYQ_ENOTSUP, "only K4V4 is implemented (k_bits=" + std::to_string(p->k_bits) +
-                                     ", v_bits=" + std::to_string(p->v_bits) + ")");
+    auto okbits = [](int b) { return b == 2 || b == 4 || b == 8; };
+    if (!okbits(p->k_bits) || !okbits(p->v_bits))
+        return fail(HYQ_EINVAL, "k_bits and v_bits must be 2, 4 or 8 (k_bits=" + std::to_string(p->k_bits) +
+                                    ", v_bits=" + std::to_string(p->v_bits) + ")");
     if (p->kv_repeat < 1 || p->kv_repeat > 16)
         return fail(HYQ_ENOTSUP, "kv_repeat must be in [1, 16], got " + std::to_string(p->kv_repeat));
     if (p->bh_kv < 0) return fail(HYQ_EINVAL, "bh_kv < 0");
@@ -763,12 +869,13 @@ int validate(const hyq_decode_params* p) {
         return fail(HYQ_EINVAL, "out must be 8-byte aligned with row stride % 4 == 0 and >= head_dim");
     if (p->n_quant > 0) {
         if (!p->k_packed || !p->v_packed || !p->k_scale || !p->v_scale) return fail(HYQ_EINVAL, "null prefix tensor");
-        if (p->kp_stride_n != PROW || p->vp_stride_n != PROW)
-            return fail(HYQ_EINVAL, "packed K/V rows must be contiguous (token stride 64 bytes)");
-        if (!aligned(p->k_packed, 16) || p->kp_stride_bh % 16)
-            return fail(HYQ_EINVAL, "k_packed must be 16-byte aligned with a 16-byte head stride");
-        if (!aligned(p->v_packed, 4) || p->vp_stride_bh % 4)
-            return fail(HYQ_EINVAL, "v_packed must be 4-byte aligned with a 4-byte head stride");
+        if (p->kp_stride_n != prow(p->k_bits) || p->vp_stride_n != prow(p->v_bits))
+            return fail(HYQ_EINVAL, "packed K/V rows must be contiguous (token stride 16 * bits bytes)");
+        const int ka = p->k_bits == 2 ? 8 : 16, va = p->v_bits;      // load sizes in bytes
+        if (!aligned(p->k_packed, ka) || p->kp_stride_bh % ka)
+            return fail(HYQ_EINVAL, "k_packed must be " + std::to_string(ka) + "-byte aligned, head stride included");
+        if (!aligned(p->v_packed, va) || p->vp_stride_bh % va)
+            return fail(HYQ_EINVAL, "v_packed must be " + std::to_string(va) + "-byte aligned, head stride included");
         if (!aligned(p->k_scale, 2) || !aligned(p->v_scale, 2))
             return fail(HYQ_EINVAL, "scales must be 2-byte aligned");
     }
@@ -833,7 +940,20 @@ extern "C" int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace, si
     const int64_t blocks = static_cast<int64_t>(pl.nwg) * p->bh_kv;
     if (blocks > 0x7fffffffLL) return fail(HYQ_ENOTSUP, "grid too large");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    decode_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(THREADS), lds_bytes(p->kv_repeat), s>>>(a);
+    const dim3 grid(static_cast<unsigned>(blocks)), block(THREADS);
+    const size_t lds = lds_bytes(p->kv_repeat);
+    const int bits = p->n_quant > 0 ? 10 * p->k_bits + p->v_bits : 44;   // no prefix: any instance
+    switch (bits) {
+        case 44: decode_kernel<4, 4><<<grid, block, lds, s>>>(a); break;
+        case 42: decode_kernel<4, 2><<<grid, block, lds, s>>>(a); break;
+        case 48: decode_kernel<4, 8><<<grid, block, lds, s>>>(a); break;
+        case 24: decode_kernel<2, 4><<<grid, block, lds, s>>>(a); break;
+        case 22: decode_kernel<2, 2><<<grid, block, lds, s>>>(a); break;
+        case 28: decode_kernel<2, 8><<<grid, block, lds, s>>>(a); break;
+        case 84: decode_kernel<8, 4><<<grid, block, lds, s>>>(a); break;
+        case 82: decode_kernel<8, 2><<<grid, block, lds, s>>>(a); break;
+        default: decode_kernel<8, 8><<<grid, block, lds, s>>>(a); break;
+    }
     return check_launch("hyq_decode_hybrid");
 }
 

@@ -24,7 +24,6 @@ import torch
 from . import _lib
 from .decode_d_stage import (
     GROUP_SIZE,
-    _dequantize_by_bits,
     _packed_dim,
     _require_gpu,
     _stream,
@@ -226,28 +225,13 @@ class DStageLayerCache:
         query_states [B, H_Q, 1, D] -> [B, H_Q, 1, D]."""
         B, H_KV, D = self._B, self._H_KV, self._D
         H_Q = H_KV * kv_repeat
-        BH_KV = B * H_KV
         k_staging = self._staging_buf_k[:, :self._staging_ptr]
         v_staging = self._staging_buf_v[:, :self._staging_ptr]
-        if self.k_bits == 4 and self.v_bits == 4:
-            out = fused_d_stage_decode(
-                query_states.reshape(B * H_Q, D), self.k_quant_packed, self.v_quant_packed,
-                self.k_scale, self.v_scale, self.k_topk, self.v_topk, k_staging, v_staging,
-                self.k_window, self.v_window, self.k_bits, self.v_bits, kv_repeat=kv_repeat)
-            return out.reshape(B, H_Q, 1, D)
-        # other bit widths: the reference's own dequant + SDPA math (:309-354), on the device
-        dtype = query_states.dtype
-        segs_k = [_dequantize_by_bits(self.k_quant_packed, self.k_scale, D, self.k_bits).to(dtype),
-                  self.k_topk.to(dtype), k_staging.to(dtype), self.k_window.to(dtype)]
-        segs_v = [_dequantize_by_bits(self.v_quant_packed, self.v_scale, D, self.v_bits).to(dtype),
-                  self.v_topk.to(dtype), v_staging.to(dtype), self.v_window.to(dtype)]
-        k_all = torch.cat(segs_k, dim=1)
-        v_all = torch.cat(segs_v, dim=1)
-        NT = k_all.shape[1]
-        k_all = k_all.reshape(B, H_KV, NT, D).unsqueeze(2).expand(B, H_KV, kv_repeat, NT, D).reshape(B, H_Q, NT, D)
-        v_all = v_all.reshape(B, H_KV, NT, D).unsqueeze(2).expand(B, H_KV, kv_repeat, NT, D).reshape(B, H_Q, NT, D)
-        scores = (query_states @ k_all.transpose(-1, -2).contiguous()) * (D ** -0.5)
-        return torch.softmax(scores, dim=-1) @ v_all
+        out = fused_d_stage_decode(
+            query_states.reshape(B * H_Q, D), self.k_quant_packed, self.v_quant_packed,
+            self.k_scale, self.v_scale, self.k_topk, self.v_topk, k_staging, v_staging,
+            self.k_window, self.v_window, self.k_bits, self.v_bits, kv_repeat=kv_repeat)
+        return out.reshape(B, H_Q, 1, D)
 
     def get_seq_length(self) -> int:
         return self._seq_len

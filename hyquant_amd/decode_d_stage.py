@@ -172,7 +172,7 @@ def _fill_segment(p: _lib.DecodeParams, i: int, k: torch.Tensor, v: torch.Tensor
 
 def fused_d_stage_decode(
     q: torch.Tensor,                        # [BH_Q, D]
-    k_quant_packed: torch.Tensor,           # [BH_KV, N_quant, D/2] int8
+    k_quant_packed: torch.Tensor,           # [BH_KV, N_quant, D*k_bits/8] int8
     v_quant_packed: torch.Tensor,
     k_scale: torch.Tensor,                  # [BH_KV, N_quant] fp16
     v_scale: torch.Tensor,
@@ -188,11 +188,14 @@ def fused_d_stage_decode(
     sm_scale: Optional[float] = None,
     split_tokens: int = 0,
 ) -> torch.Tensor:
-    """Fused four-segment decode: int4 prefix + top-k + staging + window under
-    one online softmax.  Returns a new [BH_Q, D] tensor of q.dtype (bf16)."""
+    """Fused four-segment decode: quantised prefix (K and V codes of 2, 4 or 8
+    bits) + top-k + staging + window under one online softmax.  Returns a new
+    [BH_Q, D] tensor of q.dtype (bf16)."""
     _require_gpu(q, "q")
     if q.dtype != torch.bfloat16:
         raise ValueError(f"fused_d_stage_decode expects bf16 q, got {q.dtype}")
+    if k_bits not in (2, 4, 8) or v_bits not in (2, 4, 8):
+        raise ValueError(f"k_bits and v_bits must be 2, 4, or 8, got {k_bits}, {v_bits}")
     BH_Q, D = q.shape
     if BH_Q % kv_repeat:
         raise ValueError(f"BH_Q ({BH_Q}) is not a multiple of kv_repeat ({kv_repeat})")

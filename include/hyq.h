@@ -76,12 +76,13 @@ typedef struct hyq_decode_params {
     int32_t bh_kv;        /* batch * kv heads                                  */
     int32_t kv_repeat;    /* query heads per kv head, 1..16                     */
     int32_t head_dim;     /* 128                                                */
-    int32_t k_bits, v_bits; /* 4, 4                                             */
+    int32_t k_bits, v_bits; /* 2, 4 or 8 each (packed rows of 16 * bits bytes)  */
     float sm_scale;       /* softmax scale (reference default head_dim^-0.5)   */
     int32_t split_tokens; /* int4 tokens per workgroup; 0 = automatic           */
 } hyq_decode_params;
 /* Alignment: q 16-byte aligned (row stride % 8 == 0), out 8-byte aligned (row
- * stride % 4 == 0), k_packed 16-byte aligned, bf16 segments 16-byte aligned. */
+ * stride % 4 == 0), k_packed 16-byte aligned (8 for 2-bit K), v_packed aligned
+ * to v_bits bytes, head strides likewise, bf16 segments 16-byte aligned. */
 
 /* Bytes of device workspace hyq_decode_hybrid needs for these parameters:
  * a fixed 2 MiB area of per-head arrival counters (bh_kv <= 16384) followed

@@ -77,7 +77,10 @@ def test_decode_host_validation():
     _lib, L = _L()
     p = _params(_lib)
     assert L.hyq_decode_workspace_size(p) > 0
-    for bad, code in ((dict(head_dim=64), _lib.HYQ_ENOTSUP), (dict(k_bits=8), _lib.HYQ_ENOTSUP),
+    for bits in ((2, 4), (8, 8), (4, 2)):       # every {2, 4, 8} pair is accepted
+        assert L.hyq_decode_workspace_size(_params(_lib, k_bits=bits[0], v_bits=bits[1])) > 0
+    for bad, code in ((dict(head_dim=64), _lib.HYQ_ENOTSUP), (dict(k_bits=3), _lib.HYQ_EINVAL),
+                      (dict(v_bits=16), _lib.HYQ_EINVAL),
                       (dict(kv_repeat=17), _lib.HYQ_ENOTSUP), (dict(q=258), _lib.HYQ_EINVAL),
                       (dict(bh_kv=-1), _lib.HYQ_EINVAL)):
         p = _params(_lib, **bad)
@@ -90,6 +93,11 @@ def test_decode_host_validation():
     # prefix pointers must be present when n_quant > 0
     p = _params(_lib, n_quant=512)
     assert L.hyq_decode_hybrid(p, 4096, 1 << 30, None) == _lib.HYQ_EINVAL
+    # packed rows must be 16 * bits bytes apart
+    p = _params(_lib, n_quant=512, k_bits=2, v_bits=4, k_packed=4096, v_packed=8192, k_scale=4096, v_scale=4096,
+                kp_stride_bh=512 * 64, kp_stride_n=64, vp_stride_bh=512 * 64, vp_stride_n=64)
+    assert L.hyq_decode_hybrid(p, 4096, 1 << 30, None) == _lib.HYQ_EINVAL
+    assert b"16 * bits" in L.hyq_last_error()
 
 
 def test_bf16_workspace_size():

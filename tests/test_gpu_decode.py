@@ -17,13 +17,13 @@ pytestmark = pytest.mark.gpu
 ATOL = 2e-3
 
 
-def _run(st, q, kv_repeat, **kw):
+def _run(st, q, kv_repeat, k_bits=4, v_bits=4, **kw):
     import hyquant_amd as hq
     dev = torch.device("cuda")
     t = state_to_device(st, dev)
     out = hq.fused_d_stage_decode(to_dev_bf16(q, dev), t["k_packed"], t["v_packed"], t["k_scale"], t["v_scale"],
                                   t["k_topk"], t["v_topk"], t["k_staging"], t["v_staging"],
-                                  t["k_window"], t["v_window"], 4, 4, kv_repeat=kv_repeat, **kw)
+                                  t["k_window"], t["v_window"], k_bits, v_bits, kv_repeat=kv_repeat, **kw)
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
 
@@ -177,3 +177,47 @@ def test_decode_workspace_reuse_interleaved():
     for i, (n, o) in enumerate(zip(order, outs)):
         _check(f"interleaved #{i} state {n}", o.float().cpu().numpy(), refs[n])
     assert torch.equal(outs[0], outs[3]) and torch.equal(outs[1], outs[5]) and torch.equal(outs[2], outs[4])
+
+
+BIT_PAIRS = [(4, 4), (4, 2), (2, 4), (8, 8), (2, 2), (4, 8), (8, 4), (2, 8), (8, 2)]
+
+
+@pytest.mark.parametrize("kb,vb", BIT_PAIRS)
+def test_decode_bit_widths_on_config_inputs(kb, vb):
+    """The reference's fused kernel takes K_BITS / V_BITS in {2, 4, 8}
+    (src/ops/decode_d_stage.py:610-690): every pair, frozen from the same
+    prefill, against the fp64 oracle of the same codes."""
+    print(f"decode K{kb}V{vb}", flush=True)
+    inp = O.make_decode_inputs(B=1, HQ=32, HKV=8, N=2048, W=128, S=40, seed=11)
+    st = O.freeze(inp.keys, inp.values, inp.query_tail, inp.W, inp.rho, 4, k_bits=kb, v_bits=vb)
+    O.append_staging(st, inp.k_new, inp.v_new)
+    assert st.k_packed.shape[-1] == 16 * kb and st.v_packed.shape[-1] == 16 * vb
+    out = _run(st, inp.q_dec, 4, k_bits=kb, v_bits=vb)
+    _check(f"K{kb}V{vb}", out, O.decode_fp64_state(inp.q_dec, st, 4))
+
+
+@pytest.mark.parametrize("kb,vb", [(8, 8), (2, 2), (4, 2), (2, 8)])
+@pytest.mark.parametrize("G", [1, 16])
+def test_decode_bit_widths_ragged(kb, vb, G):
+    """Random packed bytes, so every code of each width occurs (the quantiser
+    never emits the most negative one), random fp16 scales, a ragged prefix."""
+    rng = np.random.default_rng(kb * 100 + vb * 10 + G)
+    BHK, D, nq, T, S, W = 3, 128, 641, 19, 77, 128
+    print(f"decode ragged K{kb}V{vb} G={G}", flush=True)
+    b = lambda n: O.bf16_round(rng.standard_normal((BHK, n, D)).astype(np.float32) * 1.5)
+    kp = rng.integers(-128, 128, size=(BHK, nq, 16 * kb), dtype=np.int8)
+    vp = rng.integers(-128, 128, size=(BHK, nq, 16 * vb), dtype=np.int8)
+    # scale magnitudes keep |k| and |v| near those of the bf16 segments
+    ks = (rng.uniform(0.5, 2.0, size=(BHK, nq)) / (2 ** (kb - 1))).astype(np.float16)
+    vs = (rng.uniform(0.5, 2.0, size=(BHK, nq)) / (2 ** (vb - 1))).astype(np.float16)
+    codes = O.unpack_codes(kp, kb)
+    assert codes.min() == -(2 ** (kb - 1)) and codes.max() == 2 ** (kb - 1) - 1
+    st = O.DecodeState(kp, vp, ks, vs, b(T), b(T), b(W), b(W), np.zeros((BHK, 128, D), np.float32),
+                       np.zeros((BHK, 128, D), np.float32), k_bits=kb, v_bits=vb)
+    st.k_ring[:, :S] = b(S)
+    st.v_ring[:, :S] = b(S)
+    st.ring_ptr = S
+    q = O.bf16_round(rng.standard_normal((BHK * G, D)).astype(np.float32) * 2)
+    out = _run(st, q, G, k_bits=kb, v_bits=vb)
+    _check(f"ragged K{kb}V{vb} G={G}", out, O.decode_fp64_state(q, st, G),
+           ref_abs=O.decode_fp64_state(q, st, G, abs_v=True))

@@ -1,7 +1,8 @@
 """MI355X-native (gfx950) implementation of HyQuant's hybrid-precision
-attention hot path: int4 K4V4 decode cache quantisation, the fused
-four-segment split-K decode kernel and the vertical-line selector, exposed
-through the C ABI of libhyq.so (include/hyq.h)."""
+attention hot path: per-token KV quantisation (2/4/8 bits), the fused
+four-segment split-K decode, the vertical-line selector, the freeze / flush
+of the decode cache and the hybrid INT8-QK prefill, exposed through the C ABI
+of libhyq.so (include/hyq.h)."""
 
 from .decode_d_stage import (  # noqa: F401
     GROUP_SIZE,
@@ -11,6 +12,7 @@ from .decode_d_stage import (  # noqa: F401
     fused_d_stage_decode_splitk,
     quantize_per_token,
 )
+from .sage_unified import sage_vertical_attention_v2  # noqa: F401
 from .vertical import compute_vertical_indices  # noqa: F401
 
 __all__ = [
@@ -21,4 +23,5 @@ __all__ = [
     "fused_d_stage_decode_splitk",
     "decode_bf16_full",
     "compute_vertical_indices",
+    "sage_vertical_attention_v2",
 ]

@@ -682,8 +682,9 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         const int kb4 = kq >> 2, gg = kq & 3;
         const int pos = 32 * (kb4 >> 1) + 8 * gg + 4 * (kb4 & 1);
         if (PV8 && d.kind == T_REST) {
-            // fp8: channel row 8co + e gets byte e of the four keys' rows
-            uint8_t* vb8 = s_v[buf] + pos;
+            // fp8: channel row 8co + e gets byte e of the four keys' rows;
+            // 16-byte units swizzled by row: unit ^ ((row >> 4) & 3)
+            uint8_t* vb8 = s_v[buf] + ((((pos >> 4) ^ ((co >> 1) & 3)) << 4) | (pos & 15));
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int dd = e >> 2, by = e & 3;
@@ -694,7 +695,11 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             }
             return;
         }
-        uint8_t* vb = s_v[buf] + 2 * pos;
+        // 16-byte column units are swizzled by row: unit ^ (row >> 4), which
+        // spreads the 16 channel groups of a write over the banks
+        const int col = 2 * pos;
+        const int vcol = (((col >> 4) ^ ((co >> 1) & 7)) << 4) | (col & 15);
+        uint8_t* vb = s_v[buf] + vcol;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
@@ -748,7 +753,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
 #pragma unroll
                 for (int kbk = 0; kbk < 4; ++kbk)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) s[sb][kbk][r] = static_cast<float>(si[sb][kbk][r]) * d.sc;
+                    for (int r = 0; r < 4; ++r) s[sb][kbk][r] = static_cast<float>(si[sb][kbk][r]);
             masked = d.idx0 + BN > d.valid;
         } else {
             f32x4 sf[2][4];
@@ -793,6 +798,11 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         }
 
         // ---- online softmax (lazy max) and P -> fp16 (fp8 on PV8 rest tiles) ---
+        // rest-tile scores stay integer-valued until the exponent:
+        // p = exp2(s_int * (q_scale k_scale) - m) in one fma.  A zero scale
+        // means all-zero codes on one side, so every such score is 0 and the
+        // scale 1 gives the same result (and keeps -inf * scale = -inf).
+        const float ssc = d.kind == T_REST && d.sc > 0.0f ? d.sc : 1.0f;
         u32x4 pw[2][2];                    // P^T operands: fp16 x 8, or fp8 x 8 in .xy
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
@@ -801,7 +811,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             for (int kbk = 0; kbk < 4; ++kbk)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[sb][kbk][r]);
-            mx = quad_max(mx);
+            mx = quad_max(mx) * ssc;
             if (__builtin_amdgcn_ballot_w64(mx > m_run[sb] + (PV8 ? 0.0f : PF_SLACK))) {
                 const float mnew = fmaxf(m_run[sb], mx);
                 const float alpha = __builtin_amdgcn_exp2f(m_run[sb] - mnew);
@@ -812,12 +822,12 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             }
             float p[4][4];
             float ls = 0.0f;
+            const float bias = PV8 ? S_FP8_OFFSET - m_run[sb] : -m_run[sb];
 #pragma unroll
             for (int kbk = 0; kbk < 4; ++kbk)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    p[kbk][r] = __builtin_amdgcn_exp2f(PV8 ? (s[sb][kbk][r] - m_run[sb]) + S_FP8_OFFSET
-                                                           : s[sb][kbk][r] - m_run[sb]);
+                    p[kbk][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][kbk][r], ssc, bias));
                     ls += p[kbk][r];
                 }
             l_run[sb] += ls;
@@ -843,7 +853,8 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             for (int cb = 0; cb < 8; ++cb) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const u32x2 av = *reinterpret_cast<const u32x2*>(vb + (16 * cb + c16) * VSTR8 + 32 * j + 8 * g);
+                    const u32x2 av = *reinterpret_cast<const u32x2*>(vb + (16 * cb + c16) * VSTR8 +
+                                                                     16 * ((2 * j + (g >> 1)) ^ (cb & 3)) + 8 * (g & 1));
 #pragma unroll
                     for (int sb = 0; sb < 2; ++sb) acc[sb][cb] = mfma_fp8(av, u32x2{pw[sb][j][0], pw[sb][j][1]}, acc[sb][cb]);
                 }
@@ -853,7 +864,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             for (int cb = 0; cb < 8; ++cb) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const f16x8 av = *reinterpret_cast<const f16x8*>(vb + (16 * cb + c16) * VSTR + 64 * j + 16 * g);
+                    const f16x8 av = *reinterpret_cast<const f16x8*>(vb + (16 * cb + c16) * VSTR + 16 * ((4 * j + g) ^ cb));
 #pragma unroll
                     for (int sb = 0; sb < 2; ++sb) acc[sb][cb] = mfma_f16(av, __builtin_bit_cast(f16x8, pw[sb][j]), acc[sb][cb]);
                 }

@@ -57,16 +57,16 @@ def seg_sizes(N: int, W: int = 128, S: int = 64, rho: float = 0.05):
     return Nq, T, S, W
 
 
-def algorithmic_bytes(B, HQ, HKV, N, W=128, S=64, rho=0.05):
+def algorithmic_bytes(B, HQ, HKV, N, W=128, S=64, rho=0.05, kb=4, vb=4):
     Nq, T, S, W = seg_sizes(N, W, S, rho)
-    return B * HKV * (Nq * (64 + 64 + 2 + 2) + (T + S + W) * 2 * D * 2) + B * HQ * D * 2 * 2
+    return B * HKV * (Nq * (16 * kb + 16 * vb + 2 + 2) + (T + S + W) * 2 * D * 2) + B * HQ * D * 2 * 2
 
 
 def bf16_bytes(B, HQ, HKV, N, S=64):
     return B * HKV * (N + S) * 2 * D * 2 + B * HQ * D * 2 * 2
 
 
-def make_state(B, HQ, HKV, N, dev, seed, W=128, S=64, rho=0.05):
+def make_state(B, HQ, HKV, N, dev, seed, W=128, S=64, rho=0.05, kb=4, vb=4):
     """Synthetic decode cache on the GPU: Gaussian K (per-channel N(0,2)
     offsets) and V, quantised by the library's own quantiser."""
     import hyquant_amd as hq
@@ -83,9 +83,9 @@ def make_state(B, HQ, HKV, N, dev, seed, W=128, S=64, rho=0.05):
             x += off_bh
         return x.to(bf)
 
-    kp, ks = hq.quantize_per_token(kv(Nq, True), 4)
-    vp, vs = hq.quantize_per_token(kv(Nq, False), 4)
-    st = dict(k_packed=kp, v_packed=vp, k_scale=ks, v_scale=vs,
+    kp, ks = hq.quantize_per_token(kv(Nq, True), kb)
+    vp, vs = hq.quantize_per_token(kv(Nq, False), vb)
+    st = dict(k_packed=kp, v_packed=vp, k_scale=ks, v_scale=vs, bits=(kb, vb),
               k_topk=kv(T, True), v_topk=kv(T, False),
               k_staging=kv(S, True), v_staging=kv(S, False),
               k_window=kv(W, True), v_window=kv(W, False))
@@ -97,7 +97,7 @@ def run_decode(q, st, G):
     import hyquant_amd as hq
     return hq.fused_d_stage_decode(q, st["k_packed"], st["v_packed"], st["k_scale"], st["v_scale"],
                                    st["k_topk"], st["v_topk"], st["k_staging"], st["v_staging"],
-                                   st["k_window"], st["v_window"], 4, 4, kv_repeat=G)
+                                   st["k_window"], st["v_window"], st["bits"][0], st["bits"][1], kv_repeat=G)
 
 
 def time_rotating(fn, states, warmup, steps):
@@ -138,10 +138,10 @@ def copies_for(nbytes, cap=512):
     return int(max(1, min(cap, math.ceil((1 << 30) / max(nbytes, 1)))))
 
 
-def bench_hybrid(B, HQ, HKV, N, dev, warmup, steps, seed=0):
-    nbytes = algorithmic_bytes(B, HQ, HKV, N)
+def bench_hybrid(B, HQ, HKV, N, dev, warmup, steps, seed=0, kb=4, vb=4):
+    nbytes = algorithmic_bytes(B, HQ, HKV, N, kb=kb, vb=vb)
     R = copies_for(nbytes)
-    states = [make_state(B, HQ, HKV, N, dev, seed + r) for r in range(R)]
+    states = [make_state(B, HQ, HKV, N, dev, seed + r, kb=kb, vb=vb) for r in range(R)]
     G = HQ // HKV
     ms, eager = time_rotating(lambda s: run_decode(s[0], s[1], G), states, warmup, steps)
     del states
@@ -302,6 +302,20 @@ def bench_wide_gqa(dev):
     return rows
 
 
+def bench_modes(dev):
+    """The other cache modes of the reference's mode table (src/patch/_common.py:38-49):
+    K4V2, K2V4 and K8V8 prefixes, at config 1 and at B=16 with a 32K prefix."""
+    rows = []
+    for kb, vb in ((4, 2), (2, 4), (8, 8)):
+        for B, N in ((1, 8192), (16, 32768)):
+            ms, nb, _, _ = bench_hybrid(B, 32, 8, N, dev, 10, 100, kb=kb, vb=vb)
+            rows.append({"mode": f"K{kb}V{vb}", "batch": B, "prefix": N, "us_per_step": round(ms * 1e3, 3),
+                         "gbs": round(nb / (ms * 1e-3) / 1e9, 1),
+                         "frac_peak": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+            print(f"# mode {rows[-1]}", file=sys.stderr, flush=True)
+    return rows
+
+
 def pmc_workload(dev):
     """Fixed workload for rocprofv3 --pmc passes: a 256 MiB device copy (the
     FETCH_SIZE / WRITE_SIZE calibration: it reads and writes 256 MiB), then 20
@@ -406,6 +420,7 @@ def main():
                 print(f"# sweep {row}", file=sys.stderr, flush=True)
         res["sweep"] = sweep
     if not args.no_extra:
+        res["cache_modes"] = bench_modes(dev)
         res["config3_wide_gqa"] = bench_wide_gqa(dev)
         res["config3_boundary"] = bench_boundary(dev)
         res["config4_prefill"] = bench_prefill(dev)

@@ -244,10 +244,15 @@ class DStageKVCache(_HF_Cache):
 
     def __init__(self, num_layers: int = 32, k_bits=4, v_bits_fn: Callable[[int], int] = lambda i: 4 if i == 0 else 2,
                  window_size: int = 256, top_ratio: float = 0.05, use_vert: bool = True):
+        # transformers 5.x wants an explicit (here empty) layer list; 4.x takes
+        # no arguments; without transformers the base is `object`
         try:
-            super().__init__()
+            super().__init__(layers=[])
         except TypeError:
-            pass
+            try:
+                super().__init__()
+            except TypeError:
+                pass
         self.num_layers = num_layers
         self.window_size = window_size
         self.top_ratio = top_ratio

@@ -9,6 +9,7 @@ from .decode_d_stage import (  # noqa: F401
     decode_bf16_full,
     dequantize_per_token,
     fused_d_stage_decode,
+    fused_d_stage_decode_batched,
     fused_d_stage_decode_splitk,
     quantize_per_token,
 )
@@ -21,6 +22,7 @@ __all__ = [
     "dequantize_per_token",
     "fused_d_stage_decode",
     "fused_d_stage_decode_splitk",
+    "fused_d_stage_decode_batched",
     "decode_bf16_full",
     "compute_vertical_indices",
     "sage_vertical_attention_v2",

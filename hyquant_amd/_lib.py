@@ -57,6 +57,7 @@ class DecodeParams(Structure):
         ("k_bits", c_int32), ("v_bits", c_int32),
         ("sm_scale", c_float),
         ("split_tokens", c_int32),
+        ("seq_lens_quant", c_void_p), ("seq_lens_seg0", c_void_p),
     ]
 
 

@@ -107,6 +107,8 @@ struct DecArgs {
     float* part;           // [bh_kv][nwg][G][D] partial numerators
     float* ml;             // [bh_kv][nwg][G][2] = (m, l)
     uint32_t* cnt;         // arrival counter of head h at cnt[h * CNT_PAD]
+    const int32_t* len_q;  // optional per-head valid prefix tokens
+    const int32_t* len_s0; // optional per-head valid tokens of segment 0
 };
 
 struct WaveState {
@@ -624,7 +626,9 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         int w = wg, seg = 0;
         while (seg < 2 && w >= a.nseg[seg]) { w -= a.nseg[seg]; ++seg; }
         const int lo = w * a.bsplit;
-        const int n = min(a.bsplit, a.sn[seg] - lo);
+        int seg_len = a.sn[seg];
+        if (seg == 0 && a.len_s0 != nullptr) seg_len = min(seg_len, max(0, a.len_s0[head]));
+        const int n = max(0, min(a.bsplit, seg_len - lo));     // 0: a chunk past a ragged head's end
         const bf16x8 qop[4] = {__builtin_bit_cast(bf16x8, qraw[0]), __builtin_bit_cast(bf16x8, qraw[1]),
                                __builtin_bit_cast(bf16x8, qraw[2]), __builtin_bit_cast(bf16x8, qraw[3])};
         const uint16_t* kbase = a.sk[seg] + static_cast<int64_t>(head) * a.sk_bh[seg] + static_cast<int64_t>(lo) * BROW;
@@ -649,7 +653,9 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
     } else {
         // ---------------- int4 chunk: groups wave, wave+WAVES, ... ----------------
         const int lo = (wg - a.n16) * a.split;
-        const int ntok = min(a.split, a.n_quant - lo);
+        int nq = a.n_quant;
+        if (a.len_q != nullptr) nq = min(nq, max(0, a.len_q[head]));
+        const int ntok = max(0, min(a.split, nq - lo));         // 0: a chunk past a ragged head's end
         QCtx x;
         x.k = make_rsrc(a.kp + static_cast<int64_t>(head) * a.kp_bh + static_cast<int64_t>(lo) * prow(KB),
                         static_cast<uint32_t>(ntok) * prow(KB));
@@ -937,6 +943,8 @@ extern "C" int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace, si
     a.cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
     a.ml = reinterpret_cast<float*>(ws + L.ml);
     a.part = reinterpret_cast<float*>(ws + L.part);
+    a.len_q = p->n_quant > 0 ? p->seq_lens_quant : nullptr;
+    a.len_s0 = p->seg_n[0] > 0 ? p->seq_lens_seg0 : nullptr;
     const int64_t blocks = static_cast<int64_t>(pl.nwg) * p->bh_kv;
     if (blocks > 0x7fffffffLL) return fail(HYQ_ENOTSUP, "grid too large");
     hipStream_t s = static_cast<hipStream_t>(stream);

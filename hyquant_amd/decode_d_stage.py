@@ -191,6 +191,12 @@ def fused_d_stage_decode(
     """Fused four-segment decode: quantised prefix (K and V codes of 2, 4 or 8
     bits) + top-k + staging + window under one online softmax.  Returns a new
     [BH_Q, D] tensor of q.dtype (bf16)."""
+    return _decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk, k_staging, v_staging,
+                   k_window, v_window, k_bits, v_bits, kv_repeat, sm_scale, split_tokens, None, None)
+
+
+def _decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk, k_staging, v_staging,
+            k_window, v_window, k_bits, v_bits, kv_repeat, sm_scale, split_tokens, lens_q, lens_s0):
     _require_gpu(q, "q")
     if q.dtype != torch.bfloat16:
         raise ValueError(f"fused_d_stage_decode expects bf16 q, got {q.dtype}")
@@ -226,6 +232,9 @@ def fused_d_stage_decode(
     p.k_bits, p.v_bits = k_bits, v_bits
     p.sm_scale = float(sm_scale)
     p.split_tokens = int(split_tokens)
+    if lens_q is not None:
+        keep += [lens_q, lens_s0]
+        p.seq_lens_quant, p.seq_lens_seg0 = lens_q.data_ptr(), lens_s0.data_ptr()
     L = _lib.lib()
     need = L.hyq_decode_workspace_size(p)
     if need == 0:
@@ -239,6 +248,38 @@ def fused_d_stage_decode(
 
 # the reference's split-K entry point is the same operator here
 fused_d_stage_decode_splitk = fused_d_stage_decode
+
+
+def fused_d_stage_decode_batched(
+    q: torch.Tensor,                        # [total_BH_Q, D]
+    k_quant_packed: torch.Tensor,           # [total_BH_KV, max_N_quant, D*k_bits/8]
+    v_quant_packed: torch.Tensor,
+    k_scale: torch.Tensor,                  # [total_BH_KV, max_N_quant]
+    v_scale: torch.Tensor,
+    k_bf16: torch.Tensor,                   # [total_BH_KV, max_N_bf16, D]
+    v_bf16: torch.Tensor,
+    seq_lens_quant: torch.Tensor,           # [total_BH_KV] valid prefix tokens per head
+    seq_lens_bf16: torch.Tensor,            # [total_BH_KV] valid bf16 tokens per head
+    k_bits: int,
+    v_bits: int,
+    kv_repeat: int = 1,
+    sm_scale: Optional[float] = None,
+) -> torch.Tensor:
+    """Several sequences of different lengths in one call
+    (src/ops/decode_d_stage.py:1008-1129): the heads of all sequences are
+    stacked along BH, each padded to the longest prefix / bf16 segment, and
+    the per-head lengths bound what is attended.  The bf16 segment is the
+    concatenated top-k / staging / window part of each head."""
+    _require_gpu(q, "q")
+    BH_KV = q.shape[0] // max(kv_repeat, 1)
+    for name, t in (("seq_lens_quant", seq_lens_quant), ("seq_lens_bf16", seq_lens_bf16)):
+        if t.numel() != BH_KV:
+            raise ValueError(f"{name} must hold one length per KV head ({BH_KV}), got {t.numel()}")
+    lq = seq_lens_quant.to(device=q.device, dtype=torch.int32).contiguous()
+    lb = seq_lens_bf16.to(device=q.device, dtype=torch.int32).contiguous()
+    e = k_bf16[:, :0]
+    return _decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_bf16, v_bf16, e, e, e, e,
+                   k_bits, v_bits, kv_repeat, sm_scale, 0, lq, lb)
 
 
 def decode_bf16_full(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_repeat: int = 1,

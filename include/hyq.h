@@ -79,6 +79,14 @@ typedef struct hyq_decode_params {
     int32_t k_bits, v_bits; /* 2, 4 or 8 each (packed rows of 16 * bits bytes)  */
     float sm_scale;       /* softmax scale (reference default head_dim^-0.5)   */
     int32_t split_tokens; /* int4 tokens per workgroup; 0 = automatic           */
+    /* Optional ragged lengths (NULL = the full n_quant / seg_n[0] for every
+     * head): int32 device arrays [bh_kv] with each head's valid prefix tokens
+     * and valid tokens of segment 0; the tensors stay padded to n_quant /
+     * seg_n[0] and the rows past a head's length are never read.  Replaces
+     * the seq_lens_quant / seq_lens_bf16 of fused_d_stage_decode_batched
+     * (src/ops/decode_d_stage.py:1008-1129). */
+    const int32_t* seq_lens_quant;
+    const int32_t* seq_lens_seg0;
 } hyq_decode_params;
 /* Alignment: q 16-byte aligned (row stride % 8 == 0), out 8-byte aligned (row
  * stride % 4 == 0), k_packed 16-byte aligned (8 for 2-bit K), v_packed aligned

@@ -40,7 +40,7 @@ def _L():
 
 def test_abi_version_and_error_strings():
     _lib, L = _L()
-    assert L.hyq_abi_version() == 1
+    assert L.hyq_abi_version() == 2
     st = L.hyq_quant_pack(None, 1, 1, 128, 0, 0, 3, None, 0, 0, None, 0, None)
     assert st == _lib.HYQ_EINVAL
     assert b"nbits must be 2, 4, or 8" in L.hyq_last_error()

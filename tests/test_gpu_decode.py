@@ -221,3 +221,46 @@ def test_decode_bit_widths_ragged(kb, vb, G):
     out = _run(st, q, G, k_bits=kb, v_bits=vb)
     _check(f"ragged K{kb}V{vb} G={G}", out, O.decode_fp64_state(q, st, G),
            ref_abs=O.decode_fp64_state(q, st, G, abs_v=True))
+
+
+@pytest.mark.parametrize("kb,vb", [(4, 4), (4, 2)])
+def test_decode_batched_ragged_lengths(kb, vb):
+    """fused_d_stage_decode_batched (src/ops/decode_d_stage.py:1008-1129):
+    sequences of different lengths stacked along BH and padded; the padding
+    holds large garbage that must never be attended."""
+    import hyquant_amd as hq
+    rng = np.random.default_rng(40 + kb + vb)
+    D, HKV, G = 128, 2, 4
+    lens = [(300, 20), (641, 150), (0, 77), (1000, 5)]      # (prefix, bf16) per sequence
+    mq, mb = max(l[0] for l in lens), max(l[1] for l in lens)
+    BHK = HKV * len(lens)
+    kp = rng.integers(-128, 128, size=(BHK, mq, 16 * kb), dtype=np.int8)
+    vp = rng.integers(-128, 128, size=(BHK, mq, 16 * vb), dtype=np.int8)
+    ks = (rng.uniform(0.5, 2.0, size=(BHK, mq)) / 2 ** (kb - 1)).astype(np.float16)
+    vs = (rng.uniform(0.5, 2.0, size=(BHK, mq)) / 2 ** (vb - 1)).astype(np.float16)
+    kbf = O.bf16_round(rng.standard_normal((BHK, mb, D)).astype(np.float32))
+    vbf = O.bf16_round(rng.standard_normal((BHK, mb, D)).astype(np.float32))
+    lq = np.zeros(BHK, np.int32)
+    lb = np.zeros(BHK, np.int32)
+    for s, (nq, nb) in enumerate(lens):
+        h = slice(s * HKV, (s + 1) * HKV)
+        lq[h], lb[h] = nq, nb
+        ks[h, nq:] = 60000.0                                 # padding: huge scales and values
+        kbf[h, nb:] = 1e4
+        vbf[h, nb:] = 1e4
+    q = O.bf16_round(rng.standard_normal((BHK * G, D)).astype(np.float32) * 2)
+    dev = torch.device("cuda")
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    out = hq.fused_d_stage_decode_batched(to_dev_bf16(q, dev), t(kp), t(vp), t(ks), t(vs),
+                                          to_dev_bf16(kbf, dev), to_dev_bf16(vbf, dev), t(lq), t(lb),
+                                          kb, vb, kv_repeat=G)
+    torch.cuda.synchronize()
+    out = out.float().cpu().numpy()
+    e = np.zeros((HKV, 0, D), np.float32)
+    for s, (nq, nb) in enumerate(lens):
+        h = slice(s * HKV, (s + 1) * HKV)
+        qs = q[s * HKV * G:(s + 1) * HKV * G]
+        args = (qs, kp[h, :nq], vp[h, :nq], ks[h, :nq], vs[h, :nq], kbf[h, :nb], vbf[h, :nb], e, e, e, e)
+        ref = O.decode_fp64(*args, k_bits=kb, v_bits=vb, kv_repeat=G)
+        ref_abs = O.decode_fp64(*args, k_bits=kb, v_bits=vb, kv_repeat=G, abs_v=True)
+        _check(f"batched seq {s} lens {nq}/{nb}", out[s * HKV * G:(s + 1) * HKV * G], ref, ref_abs=ref_abs)

@@ -7,19 +7,24 @@
 // s = (q . k_code) * s_k, and P is rounded to bf16 after multiplying by the
 // per-token V scale, P' = bf16(p * s_v), before P' . v_code (F8).
 //
-// One launch per step.  A workgroup of 4 wavefronts owns one chunk of one KV
-// head (all G query heads of the GQA group ride along as MFMA columns):
-//   int4 chunks hold `split` tokens walked in 32-token groups (wavefront w
-//     takes groups w, w+4, ...) through a three-deep register ring, so two
-//     groups' loads are in flight while one is computed;
-//   bf16 chunks hold `bsplit` tokens of one segment (128 with few KV heads,
-//     a quarter of `split` with many) walked in 16-token tiles (wavefront w
-//     takes tiles w, w+4, ...) through a two-deep register ring.
-// int4 chunks are numbered first: they are the long ones, and the bf16 chunks
-// fill the tail of the grid.  Every load goes through a buffer
-// descriptor whose range is the chunk (past the end reads zeros), so the ring's
-// loads are unconditional and their wait counts exact; the loop position
-// travels in the scalar offset.
+// One launch per step.  A workgroup of 4 wavefronts owns one piece of one KV
+// head (all G query heads of the GQA group ride along as MFMA columns).  A
+// head's keys are laid end to end as schedule units, int4 groups of 32
+// tokens and then bf16 units of 8 tokens of each segment, and cut into
+// `nwg` pieces of equal bytes (the host picks the cut points), so every
+// workgroup of the grid streams the same amount whatever mix of segments its
+// piece holds, and the grid is sized to whole rounds of the resident
+// workgroup slots: no round ends with a few long workgroups alone.  In a
+// piece:
+//   its int4 tokens are walked in 32-token groups (wavefront w takes groups
+//     w, w+4, ...) through a three-deep register ring, so two groups' loads
+//     are in flight while one is computed;
+//   the tokens of each bf16 segment it reaches are walked in 16-token tiles
+//     (wavefront w takes tiles w, w+4, ...) through a two-deep register ring.
+// Every load goes through a buffer descriptor whose range is the piece's part
+// of the segment (past the end reads zeros), so the rings' loads are
+// unconditional and their wait counts exact; the loop position travels in the
+// scalar offset.
 //
 // The four wavefronts' (m, l, acc) are merged in LDS and the workgroup writes
 // one partial with device-scope stores (write-through to the device coherence
@@ -54,6 +59,7 @@
 #include "hyq_common.h"
 
 #include <algorithm>
+#include <atomic>
 #include <string>
 
 namespace hyq {
@@ -64,8 +70,7 @@ constexpr int WAVES = 4;                 // wavefronts per workgroup
 constexpr int THREADS = 64 * WAVES;
 constexpr int GROUP = 32;                // int4 tokens per wavefront iteration
 constexpr int TILE = 16;                 // bf16 tokens per wavefront iteration
-constexpr int CHUNK4_MIN = WAVES * GROUP;   // int4 split granularity
-constexpr int CHUNK16 = WAVES * 2 * TILE;   // bf16 tokens per workgroup chunk
+constexpr int BUNIT = 8;                 // bf16 tokens per schedule unit (an int4 unit is a GROUP)
 constexpr float LOG2E = 1.44269504f;     // src/ops/decode_d_stage.py:17
 constexpr float RESCALE_SLACK = 8.0f;    // lazy max update threshold (log2 units)
 constexpr float M_INIT = -1.0e30f;
@@ -74,7 +79,6 @@ constexpr int MAX_NWG = 256;             // chunks per head (merge weight table)
 constexpr int CNT_PAD = 32;              // arrival counters 128 bytes apart
 constexpr int CNT_CAP = 16384;           // counter slots at the head of every workspace (bh_kv bound)
 constexpr int MJ = 24;                   // partial float4 loads per lane per merge batch
-constexpr int SPLIT_MAX_SMALL = 2048;    // largest automatic int4 split
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -98,12 +102,10 @@ struct DecArgs {
     int32_t G;
     int32_t bh_kv;
     float qk_scale;        // sm_scale * log2(e)
-    int32_t split;         // int4 tokens per chunk (multiple of CHUNK4_MIN)
-    int32_t n4;            // int4 chunks per head
-    int32_t bsplit;        // bf16 tokens per chunk (multiple of CHUNK16)
-    int32_t nseg[3];       // bf16 chunks per segment
-    int32_t n16;           // bf16 chunks per head
-    int32_t nwg;           // chunks per head
+    int32_t nqg;           // int4 schedule units (GROUP tokens) per head
+    int32_t segu[3];       // bf16 schedule units (BUNIT tokens) per segment
+    int32_t nwg;           // pieces (workgroups) per head
+    int32_t bnd[MAX_NWG + 1];  // piece p: schedule units [bnd[p], bnd[p+1]) of its head
     float* part;           // [bh_kv][nwg][G][D] partial numerators
     float* ml;             // [bh_kv][nwg][G][2] = (m, l)
     uint32_t* cnt;         // arrival counter of head h at cnt[h * CNT_PAD]
@@ -515,7 +517,15 @@ __device__ __forceinline__ void wave_sync_lds() {
 // per-wavefront LDS table (same-address reads broadcast).  The first batch of
 // partial loads is issued before the (m, l) loads, so the merge is about one
 // memory round trip while nwg <= 2 * MJ.
-__device__ __forceinline__ void merge_head(const DecArgs& a, int head, float* s_wt) {
+struct MergeArgs {
+    int G, nwg;
+    const float* part;
+    const float* ml;
+    uint16_t* out;
+    int64_t out_stride;
+};
+
+__device__ __forceinline__ void merge_head(const MergeArgs& a, int head, float* s_wt) {
     const int G = a.G, nwg = a.nwg;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -590,10 +600,35 @@ __device__ __forceinline__ void merge_head(const DecArgs& a, int head, float* s_
 // ---------------------------------------------------------------------------
 template <int KB, int VB>
 __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
-    const int nh = a.bh_kv;
-    const int head = blockIdx.x % nh;
-    const int wgi = blockIdx.x / nh;
-    const int wg = wgi < a.n4 ? wgi + a.n16 : wgi - a.n4;      // chunk index: bf16 chunks first
+    const int head = blockIdx.x;
+    const int wg = blockIdx.y;                       // piece of the head
+    const int u0 = a.bnd[wg], u1 = a.bnd[wg + 1];    // its schedule units
+    // The kernel arguments the prologue branches on and the int4 and bf16
+    // addresses, read in one batch: left to the compiler, each load trails
+    // the branch that first uses it, one scalar round trip apiece.
+    const int nqg = a.nqg, nquant = a.n_quant;
+    const int32_t* const len_q = a.len_q;
+    const int32_t* const len_s0 = a.len_s0;
+    const uint8_t* const kp = a.kp; const uint8_t* const vp = a.vp;
+    const uint16_t* const ksp = a.ks; const uint16_t* const vsp = a.vs;
+    // head strides fit 32 bits (the host checks); products are formed in 64
+    const int32_t kp_bh = static_cast<int32_t>(a.kp_bh), vp_bh = static_cast<int32_t>(a.vp_bh);
+    const int32_t ks_bh = static_cast<int32_t>(a.ks_bh), vs_bh = static_cast<int32_t>(a.vs_bh);
+    const uint16_t* const sk0 = a.sk[0]; const uint16_t* const sk1 = a.sk[1]; const uint16_t* const sk2 = a.sk[2];
+    const uint16_t* const sv0 = a.sv[0]; const uint16_t* const sv1 = a.sv[1]; const uint16_t* const sv2 = a.sv[2];
+    const int32_t skb0 = static_cast<int32_t>(a.sk_bh[0]), skb1 = static_cast<int32_t>(a.sk_bh[1]);
+    const int32_t skb2 = static_cast<int32_t>(a.sk_bh[2]), svb0 = static_cast<int32_t>(a.sv_bh[0]);
+    const int32_t svb1 = static_cast<int32_t>(a.sv_bh[1]), svb2 = static_cast<int32_t>(a.sv_bh[2]);
+    const int sn0 = a.sn[0], sn1 = a.sn[1], sn2 = a.sn[2];
+    const int su0 = a.segu[0], su1 = a.segu[1];
+    const float qk_scale = a.qk_scale;
+    const MergeArgs ma{a.G, a.nwg, a.part, a.ml, a.out, a.out_stride};
+    uint32_t* const cnt = a.cnt;
+    asm volatile("" ::"s"(u0), "s"(u1), "s"(nqg), "s"(nquant), "s"(len_q), "s"(len_s0), "s"(kp), "s"(vp),
+                 "s"(ksp), "s"(vsp), "s"(kp_bh), "s"(vp_bh), "s"(ks_bh), "s"(vs_bh));
+    asm volatile("" ::"s"(sk0), "s"(sk1), "s"(sk2), "s"(sv0), "s"(sv1), "s"(sv2), "s"(skb0), "s"(skb1), "s"(skb2),
+                 "s"(svb0), "s"(svb1), "s"(svb2), "s"(sn0), "s"(sn1), "s"(sn2), "s"(su0), "s"(su1), "s"(qk_scale));
+    asm volatile("" ::"s"(ma.nwg), "s"(ma.part), "s"(ma.ml), "s"(ma.out), "s"(ma.out_stride), "s"(cnt));
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, kb = lane >> 4;
@@ -621,52 +656,23 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         for (int i = 0; i < 4; ++i) qraw[i] = bld128(rq, qo + 16 * i);
     }
 
-    if (wg < a.n16) {
-        // ---------------- bf16 chunk: tiles wave, wave+WAVES, ... ----------------
-        int w = wg, seg = 0;
-        while (seg < 2 && w >= a.nseg[seg]) { w -= a.nseg[seg]; ++seg; }
-        const int lo = w * a.bsplit;
-        int seg_len = a.sn[seg];
-        if (seg == 0 && a.len_s0 != nullptr) seg_len = min(seg_len, max(0, a.len_s0[head]));
-        const int n = max(0, min(a.bsplit, seg_len - lo));     // 0: a chunk past a ragged head's end
-        const bf16x8 qop[4] = {__builtin_bit_cast(bf16x8, qraw[0]), __builtin_bit_cast(bf16x8, qraw[1]),
-                               __builtin_bit_cast(bf16x8, qraw[2]), __builtin_bit_cast(bf16x8, qraw[3])};
-        const uint16_t* kbase = a.sk[seg] + static_cast<int64_t>(head) * a.sk_bh[seg] + static_cast<int64_t>(lo) * BROW;
-        const uint16_t* vbase = a.sv[seg] + static_cast<int64_t>(head) * a.sv_bh[seg] + static_cast<int64_t>(lo) * BROW;
-        const uint32_t nbytes = static_cast<uint32_t>(n) * (BROW * 2);
-        const Rsrc rk = make_rsrc(kbase, nbytes), rv = make_rsrc(vbase, nbytes);
-        // tiles wave, wave+WAVES, ... through a two-deep register ring
-        constexpr int TSTRIDE = WAVES * TILE;
-        const int ntile = (n + TILE - 1) / TILE;
-        const int nmine = ntile > wave ? (ntile - wave + WAVES - 1) / WAVES : 0;
-        const int t0 = wave * TILE;
-        Bf16Raw r0, r1;
-        bf16_load(r0, rk, rv, t0, lane);
-        for (int i = 0; i < nmine; i += 2) {
-            const int t = t0 + i * TSTRIDE;
-            bf16_load(r1, rk, rv, t + TSTRIDE, lane);
-            bf16_compute(st, r0, qop, n - t, lane, a.qk_scale);
-            if (i + 1 >= nmine) break;
-            bf16_load(r0, rk, rv, t + 2 * TSTRIDE, lane);
-            bf16_compute(st, r1, qop, n - t - TSTRIDE, lane, a.qk_scale);
-        }
-    } else {
-        // ---------------- int4 chunk: groups wave, wave+WAVES, ... ----------------
-        const int lo = (wg - a.n16) * a.split;
-        int nq = a.n_quant;
-        if (a.len_q != nullptr) nq = min(nq, max(0, a.len_q[head]));
-        const int ntok = max(0, min(a.split, nq - lo));         // 0: a chunk past a ragged head's end
+    if (u0 < nqg) {
+        // ---------------- int4 part: groups wave, wave+WAVES, ... ----------------
+        const int lo = u0 * GROUP;
+        int nq = nquant;
+        if (len_q != nullptr) nq = min(nq, max(0, len_q[head]));
+        const int ntok = max(0, min((min(u1, nqg) - u0) * GROUP, nq - lo));   // 0: past a ragged head's end
         QCtx x;
-        x.k = make_rsrc(a.kp + static_cast<int64_t>(head) * a.kp_bh + static_cast<int64_t>(lo) * prow(KB),
+        x.k = make_rsrc(kp + static_cast<int64_t>(head) * kp_bh + static_cast<int64_t>(lo) * prow(KB),
                         static_cast<uint32_t>(ntok) * prow(KB));
-        x.v = make_rsrc(a.vp + static_cast<int64_t>(head) * a.vp_bh + static_cast<int64_t>(lo) * prow(VB),
+        x.v = make_rsrc(vp + static_cast<int64_t>(head) * vp_bh + static_cast<int64_t>(lo) * prow(VB),
                         static_cast<uint32_t>(ntok) * prow(VB));
-        x.ks = make_rsrc(a.ks + static_cast<int64_t>(head) * a.ks_bh + lo, static_cast<uint32_t>(ntok) * 2);
-        x.vs = make_rsrc(a.vs + static_cast<int64_t>(head) * a.vs_bh + lo, static_cast<uint32_t>(ntok) * 2);
+        x.ks = make_rsrc(ksp + static_cast<int64_t>(head) * ks_bh + lo, static_cast<uint32_t>(ntok) * 2);
+        x.vs = make_rsrc(vsp + static_cast<int64_t>(head) * vs_bh + lo, static_cast<uint32_t>(ntok) * 2);
         x.klane = static_cast<uint32_t>(c * prow(KB) + 4 * KB * kb);
         x.vlane = static_cast<uint32_t>(4 * kb * prow(VB) + VB * c);
         x.slane = static_cast<uint32_t>((4 * kb + (c & 3)) * 2);
-        // groups wave, wave+WAVES, ... of the chunk through a three-deep
+        // groups wave, wave+WAVES, ... of the piece through a three-deep
         // register ring: two groups' loads in flight while one is computed
         constexpr int STRIDE = WAVES * GROUP;
         const int ngrp = (ntok + GROUP - 1) / GROUP;
@@ -703,7 +709,7 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
                              static_cast<_Float16>(f[3] * qscale), static_cast<_Float16>(f[7] * qscale)};
             qop[sidx] = v;
         }
-        const float qk = a.qk_scale * ldexpf(1.0f, ex);
+        const float qk = qk_scale * ldexpf(1.0f, ex);
         for (int i = 0; i < nmine; i += 3) {
             const int t = t0 + i * STRIDE;
             qload(b2, x, t + 2 * STRIDE);
@@ -719,6 +725,44 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         const float corr = v_offset<VB>() * st.ones[0];
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) st.acc[nb] -= corr;
+    }
+
+    // ---------------- bf16 parts: tiles wave, wave+WAVES, ... of each segment ----------------
+    const bf16x8 qb[4] = {__builtin_bit_cast(bf16x8, qraw[0]), __builtin_bit_cast(bf16x8, qraw[1]),
+                          __builtin_bit_cast(bf16x8, qraw[2]), __builtin_bit_cast(bf16x8, qraw[3])};
+    // segment bounds in units: [nqg, b1), [b1, b2), [b2, end of head)
+    const int b1 = nqg + su0, b2 = b1 + su1;
+    for (int seg = 0; seg < 3; ++seg) {
+        const int sb = seg == 0 ? nqg : seg == 1 ? b1 : b2;
+        const int ua = max(u0, sb), ub = min(u1, seg == 0 ? b1 : seg == 1 ? b2 : u1);
+        if (ua >= ub) continue;
+        const int lo = (ua - sb) * BUNIT;
+        int seg_len = seg == 0 ? sn0 : seg == 1 ? sn1 : sn2;
+        if (seg == 0 && len_s0 != nullptr) seg_len = min(seg_len, max(0, len_s0[head]));
+        const int n = max(0, min((ub - ua) * BUNIT, seg_len - lo));     // 0: past a ragged head's end
+        const uint16_t* const skp = seg == 0 ? sk0 : seg == 1 ? sk1 : sk2;
+        const uint16_t* const svp = seg == 0 ? sv0 : seg == 1 ? sv1 : sv2;
+        const int32_t skb = seg == 0 ? skb0 : seg == 1 ? skb1 : skb2;
+        const int32_t svb = seg == 0 ? svb0 : seg == 1 ? svb1 : svb2;
+        const uint16_t* kbase = skp + static_cast<int64_t>(head) * skb + static_cast<int64_t>(lo) * BROW;
+        const uint16_t* vbase = svp + static_cast<int64_t>(head) * svb + static_cast<int64_t>(lo) * BROW;
+        const uint32_t nbytes = static_cast<uint32_t>(n) * (BROW * 2);
+        const Rsrc rk = make_rsrc(kbase, nbytes), rv = make_rsrc(vbase, nbytes);
+        // tiles wave, wave+WAVES, ... through a two-deep register ring
+        constexpr int TSTRIDE = WAVES * TILE;
+        const int ntile = (n + TILE - 1) / TILE;
+        const int nmine = ntile > wave ? (ntile - wave + WAVES - 1) / WAVES : 0;
+        const int t0 = wave * TILE;
+        Bf16Raw r0, r1;
+        bf16_load(r0, rk, rv, t0, lane);
+        for (int i = 0; i < nmine; i += 2) {
+            const int t = t0 + i * TSTRIDE;
+            bf16_load(r1, rk, rv, t + TSTRIDE, lane);
+            bf16_compute(st, r0, qb, n - t, lane, qk_scale);
+            if (i + 1 >= nmine) break;
+            bf16_load(r0, rk, rv, t + 2 * TSTRIDE, lane);
+            bf16_compute(st, r1, qb, n - t - TSTRIDE, lane, qk_scale);
+        }
     }
 
     // ---- wave -> LDS ----------------------------------------------------------
@@ -737,9 +781,9 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
     __syncthreads();
 
     // ---- workgroup merge -> partial acc[G][D] and (m, l)[G] ----------------------
-    const int64_t slot = static_cast<int64_t>(head) * a.nwg + wg;
+    const int64_t slot = static_cast<int64_t>(head) * ma.nwg + wg;
     {
-        const Rsrc rpart = make_rsrc(a.part + slot * G * D, static_cast<uint32_t>(G * D * 4));
+        const Rsrc rpart = make_rsrc(ma.part + slot * G * D, static_cast<uint32_t>(G * D * 4));
         for (int o = threadIdx.x; o < G * (D / 4); o += THREADS) {
             const int g = o / (D / 4), ch = 4 * (o % (D / 4));
             float M = s_m[0][g];
@@ -763,20 +807,21 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         float lv = 0.f;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) lv += fast_exp2(s_m[w][g] - M) * s_l[w][g];
-        __hip_atomic_store(a.ml + (slot * G + g) * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.ml + (slot * G + g) * 2 + 1, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float* const mlw = const_cast<float*>(ma.ml);
+        __hip_atomic_store(mlw + (slot * G + g) * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(mlw + (slot * G + g) * 2 + 1, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // every store of this workgroup acknowledged before its arrival is counted
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(a.cnt + head * CNT_PAD, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old == static_cast<uint32_t>(a.nwg - 1));
+        const uint32_t old = __hip_atomic_fetch_add(cnt + head * CNT_PAD, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old == static_cast<uint32_t>(ma.nwg - 1));
     }
     __syncthreads();
     if (s_last) {
-        if (threadIdx.x == 0) __hip_atomic_store(a.cnt + head * CNT_PAD, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        merge_head(a, head, s_acc);
+        if (threadIdx.x == 0) __hip_atomic_store(cnt + head * CNT_PAD, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        merge_head(ma, head, s_acc);
     }
 }
 
@@ -785,57 +830,137 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
 // ---------------------------------------------------------------------------
 
 struct Plan {
-    int split, bsplit, n4, nseg[3], n16, nwg;
+    int nwg;               // pieces per head
+    int nqg, segu[3];      // schedule units: int4 groups, bf16 units per segment
+    int bnd[MAX_NWG + 1];  // piece p covers units [bnd[p], bnd[p+1])
 };
 
 size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
-// Tokens per workgroup chunk.  Few KV heads (small batch): about 32 chunks
-// per head, so the whole chip works on one step and each wavefront streams a
-// handful of groups.  Many heads: a large chunk, growing with the head count
-// (2048 tokens up to 127 heads, 4096 up to 191, ...), which keeps the
-// per-workgroup prologue / partial / merge costs low while the grid still
-// holds several workgroups per CU slot.  `gran` is the smallest chunk.
-int64_t auto_split(int64_t n, int bh_kv, int64_t gran, int64_t big) {
-    if (bh_kv >= 32) return big * std::max(1, bh_kv / 64);
-    int64_t split = gran;
-    while (split < big && split * 32 < n) split *= 2;
-    return split;
-}
-
-Plan make_plan(int64_t n_quant, const int64_t seg_n[3], int bh_kv, int G, int requested) {
-    auto round_up = [](int64_t x, int64_t m) { return ((x + m - 1) / m) * m; };
-    Plan p;
-    int64_t split = requested > 0 ? std::min<int64_t>(round_up(requested, CHUNK4_MIN), 1 << 30)
-                                  : auto_split(n_quant, bh_kv, CHUNK4_MIN, SPLIT_MAX_SMALL);
-    // bf16 chunks: 128 tokens beside an int4 prefix (the segments are short);
-    // alone (the full-precision comparator) they are split like the prefix,
-    // a bf16 token costing four int4 tokens of bandwidth.
-    int64_t bsplit = CHUNK16;
-    // many heads: bf16 chunks of about the bytes of an int4 chunk, so that the
-    // short chunks do not multiply the per-workgroup costs
-    if (bh_kv >= 32) bsplit = std::max<int64_t>(CHUNK16, split / 4);
-    if (n_quant == 0) bsplit = auto_split(seg_n[0] + seg_n[1] + seg_n[2], bh_kv, CHUNK16, SPLIT_MAX_SMALL / 4);
-    // keep the chunks of a head within the merge tables
-    while (true) {
-        p.n4 = static_cast<int>((n_quant + split - 1) / split);
-        p.n16 = 0;
-        for (int s = 0; s < 3; ++s) {
-            p.nseg[s] = static_cast<int>((seg_n[s] + bsplit - 1) / bsplit);
-            p.n16 += p.nseg[s];
-        }
-        p.nwg = p.n4 + p.n16;
-        if (static_cast<int64_t>(p.nwg) * G <= MAX_PARTIALS && p.nwg <= MAX_NWG) break;
-        if (p.n4 > p.n16 && p.n4 > 1) split *= 2;
-        else bsplit *= 2;
+// Cut a head into pieces, each inside one segment (a piece spanning segments
+// would walk their rings one after the other), the int4 pieces first so
+// that the short segment pieces fill the end of the grid.
+//   requested > 0: pieces of about that many int4 tokens' bytes.
+//   few KV heads (bh_kv < 32, a step of a few microseconds, bound by the
+//     per-piece round trips): int4 pieces of the smallest power-of-two
+//     token count >= 128 that gives at most 32 pieces (2048 at most), bf16
+//     pieces of 128 tokens (without a prefix, like the prefix: a power of
+//     two from 128 to 512).
+//   many KV heads: pieces of about total / (1.25 * slots) bytes, `slots`
+//     being the workgroups the device holds at once: the first round fills
+//     every slot and the remaining quarter, with the short segment pieces,
+//     evens out the workgroups that ran slow.  Pieces stay >= 96 KiB: below
+//     that the per-piece round trips cost more than the balance gains.
+// Each segment gets its bytes / target pieces (rounded, at least one); the
+// target grows until the pieces fit the merge tables.
+Plan make_plan(int64_t n_quant, const int64_t seg_n[3], int bh_kv, int G, int requested, int kb, int vb,
+               int slots) {
+    Plan p{};
+    p.nqg = static_cast<int>((n_quant + GROUP - 1) / GROUP);
+    for (int s = 0; s < 3; ++s) p.segu[s] = static_cast<int>((seg_n[s] + BUNIT - 1) / BUNIT);
+    const int64_t cq = static_cast<int64_t>(GROUP) * (16 * kb + 16 * vb + 4);   // bytes of an int4 group
+    const int64_t cb = static_cast<int64_t>(BUNIT) * 4 * D;                     // bytes of a bf16 unit (K and V)
+    const int64_t su[4] = {p.nqg, p.segu[0], p.segu[1], p.segu[2]};             // units per segment
+    const int64_t sc[4] = {cq, cb, cb, cb};
+    int64_t head_bytes = 0;
+    int nonempty = 0;
+    for (int s = 0; s < 4; ++s) {
+        head_bytes += su[s] * sc[s];
+        nonempty += su[s] > 0;
     }
-    p.split = static_cast<int>(split);
-    p.bsplit = static_cast<int>(bsplit);
+    p.nwg = 0;
+    if (nonempty == 0) return p;
+    const int kmax = std::max(nonempty, std::min(MAX_NWG, MAX_PARTIALS / G));
+    int ks[4];
+    auto counts_for = [&](int64_t target) {
+        int total = 0;
+        for (int s = 0; s < 4; ++s) {
+            ks[s] = su[s] > 0 ? static_cast<int>(std::min<int64_t>(
+                                    su[s], std::max<int64_t>(1, (su[s] * sc[s] + target / 2) / target)))
+                              : 0;
+            total += ks[s];
+        }
+        return total;
+    };
+    int total;
+    int64_t target;
+    if (requested > 0) {
+        target = std::max<int64_t>(1, (requested + GROUP - 1) / GROUP) * cq;
+        total = counts_for(target);
+    } else if (bh_kv < 32) {
+        int64_t split = 4 * GROUP, bsplit = 128;
+        while (split < 2048 && split * 32 < n_quant) split *= 2;
+        if (n_quant == 0) {       // bf16 alone (the full-precision comparator): split like a prefix
+            const int64_t nb = seg_n[0] + seg_n[1] + seg_n[2];
+            while (bsplit < 512 && bsplit * 32 < nb) bsplit *= 2;
+        }
+        const int64_t gsplit = split / GROUP;
+        bsplit /= BUNIT;
+        ks[0] = static_cast<int>((su[0] + gsplit - 1) / gsplit);
+        total = ks[0];
+        for (int s = 1; s < 4; ++s) {
+            ks[s] = static_cast<int>((su[s] + bsplit - 1) / bsplit);
+            total += ks[s];
+        }
+        target = (head_bytes + total - 1) / total;
+    } else {
+        const int64_t sl = slots > 0 ? slots : 512;
+        target = std::max<int64_t>(96 << 10, head_bytes * bh_kv * 4 / (5 * sl));
+        total = counts_for(target);
+    }
+    while (total > kmax) {
+        target += target / 8 + 1;
+        total = counts_for(target);
+    }
+    int64_t base = 0;
+    for (int s = 0; s < 4; ++s) {
+        for (int i = 0; i < ks[s]; ++i) p.bnd[p.nwg++] = static_cast<int>(base + su[s] * i / ks[s]);
+        base += su[s];
+    }
+    p.bnd[p.nwg] = static_cast<int>(base);
     return p;
 }
 
 size_t lds_bytes(int G) {
     return std::max(static_cast<size_t>(WAVES) * G * (D + 1), static_cast<size_t>(WAVES) * MAX_NWG) * sizeof(float);
+}
+
+// Workgroups of one decode_kernel instance the device holds at once, cached
+// per device and GQA width (the LDS size).
+template <int KB, int VB>
+int resident_slots_of(int G) {
+    static std::atomic<int> cache[64][17];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || G < 1 || G > 16) return 0;
+    const int known = cache[dev][G].load(std::memory_order_relaxed);
+    if (known > 0) return known;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&decode_kernel<KB, VB>),
+                                                     THREADS, lds_bytes(G)) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    cache[dev][G].store(per_cu * cus, std::memory_order_relaxed);
+    return per_cu * cus;
+}
+
+int resident_slots(int kb, int vb, int G) {
+    switch (10 * kb + vb) {
+        case 44: return resident_slots_of<4, 4>(G);
+        case 42: return resident_slots_of<4, 2>(G);
+        case 48: return resident_slots_of<4, 8>(G);
+        case 24: return resident_slots_of<2, 4>(G);
+        case 22: return resident_slots_of<2, 2>(G);
+        case 28: return resident_slots_of<2, 8>(G);
+        case 84: return resident_slots_of<8, 4>(G);
+        case 82: return resident_slots_of<8, 2>(G);
+        default: return resident_slots_of<8, 8>(G);
+    }
+}
+
+Plan plan_for(const hyq_decode_params* p) {
+    const int kb = p->n_quant > 0 ? p->k_bits : 4, vb = p->n_quant > 0 ? p->v_bits : 4;
+    return make_plan(p->n_quant, p->seg_n, p->bh_kv, p->kv_repeat, p->split_tokens, kb, vb,
+                     resident_slots(kb, vb, p->kv_repeat));
 }
 
 // workspace: [arrival counters: CNT_CAP slots, 128 B apart][(m, l) table][partials].
@@ -853,6 +978,8 @@ Layout layout(const Plan& pl, int bh_kv, int G) {
     L.total = L.part + round256(slots * D * sizeof(float));
     return L;
 }
+
+bool fits31(int64_t x) { return x >= 0 && x <= 0x7fffffffLL; }
 
 int validate(const hyq_decode_params* p) {
     if (!p) return fail(HYQ_EINVAL, "null params");
@@ -884,6 +1011,8 @@ int validate(const hyq_decode_params* p) {
             return fail(HYQ_EINVAL, "v_packed must be " + std::to_string(va) + "-byte aligned, head stride included");
         if (!aligned(p->k_scale, 2) || !aligned(p->v_scale, 2))
             return fail(HYQ_EINVAL, "scales must be 2-byte aligned");
+        if (!fits31(p->kp_stride_bh) || !fits31(p->vp_stride_bh) || !fits31(p->ks_stride_bh) || !fits31(p->vs_stride_bh))
+            return fail(HYQ_ENOTSUP, "prefix head strides must lie in [0, 2^31)");
     }
     for (int s = 0; s < 3; ++s) {
         if (p->seg_n[s] < 0 || p->seg_n[s] > (1 << 23)) return fail(HYQ_EINVAL, "bad segment length");
@@ -894,6 +1023,8 @@ int validate(const hyq_decode_params* p) {
         if (!aligned(p->seg_k[s], 16) || !aligned(p->seg_v[s], 16) || p->seg_k_stride_bh[s] % 8 ||
             p->seg_v_stride_bh[s] % 8)
             return fail(HYQ_EINVAL, "bf16 segments must be 16-byte aligned with head strides % 8 == 0");
+        if (!fits31(p->seg_k_stride_bh[s]) || !fits31(p->seg_v_stride_bh[s]))
+            return fail(HYQ_ENOTSUP, "bf16 segment head strides must lie in [0, 2^31)");
     }
     return HYQ_OK;
 }
@@ -905,7 +1036,7 @@ using namespace hyq;
 
 extern "C" size_t hyq_decode_workspace_size(const hyq_decode_params* p) {
     if (validate(p) != HYQ_OK) return 0;
-    const Plan pl = make_plan(p->n_quant, p->seg_n, p->bh_kv, p->kv_repeat, p->split_tokens);
+    const Plan pl = plan_for(p);
     return layout(pl, p->bh_kv, p->kv_repeat).total;
 }
 
@@ -913,10 +1044,10 @@ extern "C" int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace, si
     int rc = validate(p);
     if (rc != HYQ_OK) return rc;
     if (p->bh_kv == 0) return HYQ_OK;
-    const Plan pl = make_plan(p->n_quant, p->seg_n, p->bh_kv, p->kv_repeat, p->split_tokens);
+    const Plan pl = plan_for(p);
     if (pl.nwg == 0) return fail(HYQ_EINVAL, "decode with zero key tokens");
     if (static_cast<int64_t>(pl.nwg) * p->kv_repeat > MAX_PARTIALS || pl.nwg > MAX_NWG)
-        return fail(HYQ_ENOTSUP, "too many bf16 chunks per head for the merge tables");
+        return fail(HYQ_ENOTSUP, "too many pieces per head for the merge tables");
     const Layout L = layout(pl, p->bh_kv, p->kv_repeat);
     if (!workspace || ws_bytes < L.total || !aligned(workspace, 256))
         return fail(HYQ_ENOSPC, "decode workspace too small or misaligned: need " + std::to_string(L.total) + " bytes");
@@ -933,22 +1064,23 @@ extern "C" int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace, si
         a.sk_bh[s] = p->seg_k_stride_bh[s]; a.sk_n[s] = p->seg_k_stride_n[s];
         a.sv_bh[s] = p->seg_v_stride_bh[s]; a.sv_n[s] = p->seg_v_stride_n[s];
         a.sn[s] = static_cast<int32_t>(p->seg_n[s]);
-        a.nseg[s] = pl.nseg[s];
+        a.segu[s] = pl.segu[s];
     }
     a.G = p->kv_repeat;
     a.bh_kv = p->bh_kv;
     a.qk_scale = p->sm_scale * LOG2E;
-    a.split = pl.split; a.bsplit = pl.bsplit; a.n4 = pl.n4; a.n16 = pl.n16; a.nwg = pl.nwg;
+    a.nqg = pl.nqg; a.nwg = pl.nwg;
+    for (int i = 0; i <= pl.nwg; ++i) a.bnd[i] = pl.bnd[i];
     char* ws = static_cast<char*>(workspace);
     a.cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
     a.ml = reinterpret_cast<float*>(ws + L.ml);
     a.part = reinterpret_cast<float*>(ws + L.part);
     a.len_q = p->n_quant > 0 ? p->seq_lens_quant : nullptr;
     a.len_s0 = p->seg_n[0] > 0 ? p->seq_lens_seg0 : nullptr;
-    const int64_t blocks = static_cast<int64_t>(pl.nwg) * p->bh_kv;
-    if (blocks > 0x7fffffffLL) return fail(HYQ_ENOTSUP, "grid too large");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid(static_cast<unsigned>(blocks)), block(THREADS);
+    // x: KV head, y: piece; workgroups dispatch x-fastest, so piece 0 of
+    // every head goes first
+    const dim3 grid(static_cast<unsigned>(p->bh_kv), static_cast<unsigned>(pl.nwg)), block(THREADS);
     const size_t lds = lds_bytes(p->kv_repeat);
     const int bits = p->n_quant > 0 ? 10 * p->k_bits + p->v_bits : 44;   // no prefix: any instance
     switch (bits) {
@@ -968,7 +1100,7 @@ extern "C" int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace, si
 extern "C" size_t hyq_decode_bf16_workspace_size(int32_t bh_kv, int32_t kv_repeat, int64_t n, int32_t d) {
     if (bh_kv < 0 || kv_repeat < 1 || kv_repeat > 16 || d != D || n < 0) return 0;
     const int64_t seg_n[3] = {n, 0, 0};
-    const Plan pl = make_plan(0, seg_n, bh_kv, kv_repeat, 0);
+    const Plan pl = make_plan(0, seg_n, bh_kv, kv_repeat, 0, 4, 4, resident_slots(4, 4, kv_repeat));
     return layout(pl, bh_kv, kv_repeat).total;
 }
 

@@ -103,7 +103,7 @@ def test_decode_split_invariance_and_determinism():
     st = O.build_decode_state(inp)
     ref = O.decode_fp64_state(inp.q_dec, st, 4)
     outs = []
-    for split in (128, 512, 4096, 0):
+    for split in (32, 128, 512, 4096, 0):
         o = _run(st, inp.q_dec, 4, split_tokens=split)
         _check(f"split={split}", o, ref)
         outs.append(o)
@@ -153,7 +153,7 @@ def test_decode_workspace_reuse_interleaved():
     cfgs = {
         "A": dict(B=1, HQ=32, HKV=8, N=8192, S=64, seed=7),
         "B": dict(B=2, HQ=64, HKV=8, N=2048, S=64, seed=8),     # G = 8
-        "C": dict(B=8, HQ=32, HKV=8, N=4096, S=64, seed=9),     # 64 KV heads: largest split
+        "C": dict(B=8, HQ=32, HKV=8, N=4096, S=64, seed=9),     # 64 KV heads: few long pieces
     }
     data = {}
     for name, cfg in cfgs.items():
@@ -169,7 +169,7 @@ def test_decode_workspace_reuse_interleaved():
 
     order = ["A", "B", "C", "A", "C", "B"]
     outs = [call(n) for n in order]
-    # the split of 128 tokens gives A 66 chunks per head: two merge batches
+    # pieces of 128 int4 tokens' bytes give A 78 pieces per head: two merge batches
     outs.append(call("A", split_tokens=128))
     order.append("A")
     torch.cuda.synchronize()

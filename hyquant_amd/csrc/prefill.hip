@@ -82,6 +82,22 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 enum : int { T_REST = 0, T_VERT = 1, T_WIN = 2 };
 
+// Raw buffer loads: the descriptor's range covers a tile source's valid rows,
+// the row position travels in the scalar offset and the lane's place in the
+// tile in the vector offset.  Loads at or past the range (scalar + vector
+// offset >= range) return zeros, so no per-lane clamp or 64-bit address is
+// formed.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc pf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 pf_ld128(Rsrc r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ u32x2 pf_ld64(Rsrc r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+
 __device__ __forceinline__ int window_start(int blk, int W) {
     const int x = BM * blk - (W - 1);
     return (x > 0 ? x : 0) / BN * BN;
@@ -134,6 +150,14 @@ __device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float
     auto cl = [](float x) { return fminf(fmaxf(x, -FP8_MAX), FP8_MAX); };
     int r = __builtin_amdgcn_cvt_pk_fp8_f32(cl(a), cl(b), 0, false);
     r = __builtin_amdgcn_cvt_pk_fp8_f32(cl(c), cl(d), r, true);
+    return static_cast<uint32_t>(r);
+}
+
+// P' operands: exp2(s - m + 8.807 - guard) with the exact running max lies
+// in [0, 447.98], inside the e4m3 range, so no clamp
+__device__ __forceinline__ uint32_t pack_p_e4m3x4(float a, float b, float c, float d) {
+    int r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
     return static_cast<uint32_t>(r);
 }
 
@@ -627,44 +651,44 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     };
 
     // global -> register staging of one tile (K: 2 or 4 x 16 B, V: 4 x 16 B
-    // per thread, fp8 V: 4 x 8 B)
+    // per thread, fp8 V: 4 x 8 B); rows past a source's valid rows read zeros
+    // (their scores are masked and their P is zero)
     u32x4 kr[4], vr[4];                    // fp8 V rows use vr[r].xy
+    const uint32_t vo_k8 = static_cast<uint32_t>((tid >> 3) * PD + 16 * (tid & 7));
+    const uint32_t vo_k16 = static_cast<uint32_t>((tid >> 4) * 2 * PD + 16 * (tid & 15));
+    const uint32_t vo_v16 = static_cast<uint32_t>(4 * (tid >> 4) * 2 * PD + 16 * (tid & 15));
+    const uint32_t vo_v8 = static_cast<uint32_t>(4 * (tid >> 4) * PD + 8 * (tid & 15));
     auto load_tile = [&](const TileDesc& d) {
+        const uint32_t i0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(d.idx0));
+        const uint32_t nvalid = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(d.valid));
         if (d.kind == T_REST) {
-            const int8_t* base = a.k8r + static_cast<int64_t>(bh) * a.P * PD + 16 * (tid & 7);
+            const Rsrc rk = pf_rsrc(a.k8r + static_cast<int64_t>(bh) * a.P * PD, nvalid * PD);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int e = min(d.idx0 + (tid >> 3) + 32 * i, d.valid - 1);
-                kr[i] = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(e) * PD);
-            }
+            for (int i = 0; i < 2; ++i) kr[i] = pf_ld128(rk, vo_k8, (i0 + 32 * i) * PD);
         } else {
-            const uint16_t* base = (d.kind == T_VERT ? a.kv16 + static_cast<int64_t>(bh) * a.T * PD
-                                                     : a.k16 + bhk * a.N * PD) + 8 * (tid & 15);
+            const uint16_t* kb = d.kind == T_VERT ? a.kv16 + static_cast<int64_t>(bh) * a.T * PD
+                                                  : a.k16 + bhk * a.N * PD;
+            const Rsrc rk = pf_rsrc(kb, nvalid * 2 * PD);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int e = min(d.idx0 + (tid >> 4) + 16 * i, d.valid - 1);
-                kr[i] = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(e) * PD);
-            }
+            for (int i = 0; i < 4; ++i) kr[i] = pf_ld128(rk, vo_k16, (i0 + 16 * i) * 2 * PD);
         }
         if (PV8 && d.kind == T_REST) {
-            const uint8_t* vb8 = reinterpret_cast<const uint8_t*>(a.vr) + static_cast<int64_t>(bh) * a.P * PD + 8 * (tid & 15);
+            const Rsrc rv = pf_rsrc(reinterpret_cast<const uint8_t*>(a.vr) + static_cast<int64_t>(bh) * a.P * PD,
+                                    nvalid * PD);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int e = min(d.idx0 + 4 * (tid >> 4) + r, d.valid - 1);
-                const u32x2 t = *reinterpret_cast<const u32x2*>(vb8 + static_cast<int64_t>(e) * PD);
+                const u32x2 t = pf_ld64(rv, vo_v8, (i0 + r) * PD);
                 vr[r][0] = t[0];
                 vr[r][1] = t[1];
             }
             return;
         }
-        const uint16_t* vbase = (d.kind == T_REST ? a.vr + static_cast<int64_t>(bh) * a.P * PD
-                                 : d.kind == T_VERT ? a.vv16 + static_cast<int64_t>(bh) * a.T * PD
-                                                    : a.v16 + bhk * a.N * PD) + 8 * (tid & 15);
+        const uint16_t* vb = d.kind == T_REST ? a.vr + static_cast<int64_t>(bh) * a.P * PD
+                             : d.kind == T_VERT ? a.vv16 + static_cast<int64_t>(bh) * a.T * PD
+                                                : a.v16 + bhk * a.N * PD;
+        const Rsrc rv = pf_rsrc(vb, nvalid * 2 * PD);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int e = min(d.idx0 + 4 * (tid >> 4) + r, d.valid - 1);
-            vr[r] = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(e) * PD);
-        }
+        for (int r = 0; r < 4; ++r) vr[r] = pf_ld128(rv, vo_v16, (i0 + r) * 2 * PD);
     };
     auto store_tile = [&](const TileDesc& d, int buf) {
         uint8_t* kb = s_k[buf];
@@ -711,7 +735,12 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     };
 
     float m_run[2] = {PF_M_INIT, PF_M_INIT};
+    // softmax denominators: PV8 sums P' on the VALU (l_run, per lane, summed
+    // over the quad at the end); fp16 PV sums the fp16 P operands with one
+    // more MFMA per 32 keys against an all-ones A (lsum, every lane holds its
+    // column's full sum), which takes 32 adds per tile off the VALU
     float l_run[2] = {0.0f, 0.0f};
+    f32x4 lsum[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
     f32x4 acc[2][8];
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb)
@@ -815,27 +844,31 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             if (__builtin_amdgcn_ballot_w64(mx > m_run[sb] + (PV8 ? 0.0f : PF_SLACK))) {
                 const float mnew = fmaxf(m_run[sb], mx);
                 const float alpha = __builtin_amdgcn_exp2f(m_run[sb] - mnew);
-                l_run[sb] *= alpha;
+                if constexpr (PV8) l_run[sb] *= alpha;
+                else lsum[sb] *= alpha;
 #pragma unroll
                 for (int cb = 0; cb < 8; ++cb) acc[sb][cb] *= alpha;
                 m_run[sb] = mnew;
             }
             float p[4][4];
             float ls = 0.0f;
-            const float bias = PV8 ? S_FP8_OFFSET - m_run[sb] : -m_run[sb];
+            // PV8: the rounding of mx, of the bias and of the fma can lift
+            // the largest exponent by ulp(m) + 1e-6 above 8.807; the bias gives
+            // that back so P' never passes 447.98 (no clamp before e4m3)
+            const float bias = PV8 ? S_FP8_OFFSET - m_run[sb] - (fabsf(m_run[sb]) * 2.4e-7f + 1e-6f) : -m_run[sb];
 #pragma unroll
             for (int kbk = 0; kbk < 4; ++kbk)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     p[kbk][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][kbk][r], ssc, bias));
-                    ls += p[kbk][r];
+                    if constexpr (PV8) ls += p[kbk][r];
                 }
-            l_run[sb] += ls;
+            if constexpr (PV8) l_run[sb] += ls;
             if (PV8 && d.kind == T_REST) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    pw[sb][j] = u32x4{pack_e4m3x4(p[2 * j][0], p[2 * j][1], p[2 * j][2], p[2 * j][3]),
-                                      pack_e4m3x4(p[2 * j + 1][0], p[2 * j + 1][1], p[2 * j + 1][2], p[2 * j + 1][3]),
+                    pw[sb][j] = u32x4{pack_p_e4m3x4(p[2 * j][0], p[2 * j][1], p[2 * j][2], p[2 * j][3]),
+                                      pack_p_e4m3x4(p[2 * j + 1][0], p[2 * j + 1][1], p[2 * j + 1][2], p[2 * j + 1][3]),
                                       0u, 0u};
             } else {
 #pragma unroll
@@ -870,12 +903,20 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                 }
             }
         }
+        if constexpr (!PV8) {
+            const u32x4 onew = {0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};   // fp16 1.0
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb)
+                    lsum[sb] = mfma_f16(__builtin_bit_cast(f16x8, onew), __builtin_bit_cast(f16x8, pw[sb][j]), lsum[sb]);
+        }
     }
 
     // ---- epilogue: O = acc / l (x vscale in fp8 mode) ------------------------------
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
-        const float l = quad_sum(l_run[sb]);
+        const float l = PV8 ? quad_sum(l_run[sb]) : lsum[sb][0];
         const float inv = 1.0f / l;
         const int row = BM * blk + 32 * w + 16 * sb + c16;
         if (row < a.N) {

@@ -13,7 +13,7 @@ from .decode_d_stage import (  # noqa: F401
     fused_d_stage_decode_splitk,
     quantize_per_token,
 )
-from .sage_unified import sage_vertical_attention_v2  # noqa: F401
+from .sage_unified import sage_unified_attention, sage_vertical_attention_v2  # noqa: F401
 from .vertical import compute_vertical_indices  # noqa: F401
 
 __all__ = [
@@ -26,4 +26,5 @@ __all__ = [
     "decode_bf16_full",
     "compute_vertical_indices",
     "sage_vertical_attention_v2",
+    "sage_unified_attention",
 ]

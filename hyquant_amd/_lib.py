@@ -37,6 +37,7 @@ EXPORTS = (
     "hyq_prefill_lists",
     "hyq_prefill_workspace_size",
     "hyq_prefill_hybrid",
+    "hyq_prefill_unified",
 )
 
 
@@ -124,6 +125,8 @@ def _declare(lib):
     lib.hyq_prefill_workspace_size.argtypes = [c_int32, c_int32, c_int32, c_int64, c_int64, c_int32, c_int32]
     lib.hyq_prefill_hybrid.restype = c_int
     lib.hyq_prefill_hybrid.argtypes = [POINTER(PrefillParams), c_void_p, c_size_t, c_void_p]
+    lib.hyq_prefill_unified.restype = c_int
+    lib.hyq_prefill_unified.argtypes = [POINTER(PrefillParams), c_void_p, c_size_t, c_void_p]
 
 
 def lib():

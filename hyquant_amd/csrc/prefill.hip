@@ -532,6 +532,7 @@ struct PfArgs {
     float c;                                                          // fp32(sm_scale * log2e)
     int total, per_xcd;
     const float* vscale;                                              // fp8 PV: [BHK][128] per-channel V scale
+    int rest_causal;       // all keys int8 up to the diagonal (rest list = positions, causal mask, no window)
 };
 
 __device__ __forceinline__ f32x4 mfma_f16(const f16x8& a, const f16x8& b, const f32x4& c) {
@@ -628,10 +629,14 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     }
 
     // ---- tile schedule -------------------------------------------------------
-    const int nr_b = a.nr[static_cast<int64_t>(bh) * a.nblk + blk];
+    int nr_b = a.nr[static_cast<int64_t>(bh) * a.nblk + blk];
     const int nv_b = a.nv[static_cast<int64_t>(bh) * a.nblk + blk];
-    const int wla = window_start(blk, a.W);
+    int wla = window_start(blk, a.W);
     const int wend = min(a.N, BM * (blk + 1));
+    if (a.rest_causal) {        // the rest list is every position: int8 through the diagonal block
+        nr_b = wend;
+        wla = wend;
+    }
     const int nrt = (nr_b + BN - 1) / BN;
     const int nvt = (nv_b + BN - 1) / BN;
     const int nwt = (wend - wla + BN - 1) / BN;
@@ -783,7 +788,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                 for (int kbk = 0; kbk < 4; ++kbk)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) s[sb][kbk][r] = static_cast<float>(si[sb][kbk][r]);
-            masked = d.idx0 + BN > d.valid;
+            masked = d.idx0 + BN > d.valid || (a.rest_causal && d.idx0 + BN - 1 > BM * blk + 32 * w);
         } else {
             f32x4 sf[2][4];
 #pragma unroll
@@ -820,7 +825,8 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int e = d.idx0 + 16 * kbk + 4 * g + r;
-                        const bool ok = (d.kind == T_WIN) ? (e < d.valid && e <= row) : (e < d.valid);
+                        const bool causal = d.kind == T_WIN || (d.kind == T_REST && a.rest_causal);
+                        const bool ok = causal ? (e < d.valid && e <= row) : (e < d.valid);
                         if (!ok) s[sb][kbk][r] = -INFINITY;
                     }
             }
@@ -1059,20 +1065,24 @@ extern "C" int hyq_prefill_lists(const int64_t* vidx, int64_t vi_b, int64_t vi_h
                         rest, rcount, nr, nv, s);
 }
 
-extern "C" int hyq_prefill_hybrid(const hyq_prefill_params* p, void* ws, size_t ws_bytes, void* stream_) {
-    hipStream_t stream = static_cast<hipStream_t>(stream_);
-    if (!p) return fail(HYQ_EINVAL, "hyq_prefill_hybrid: null params");
+namespace hyq {
+namespace {
+// Both prefill entry points: the hybrid partition, or with rest_causal (the
+// unified kernel's window 0) every key through int8 up to the diagonal.
+int prefill_run(const hyq_prefill_params* p, void* ws, size_t ws_bytes, hipStream_t stream, bool rest_causal,
+                const std::string& name) {
+    if (!p) return fail(HYQ_EINVAL, name + ": null params");
     const int B = p->batch, HQ = p->hq, HKV = p->hkv, W = p->window;
     const int64_t N = p->n, T = p->t;
-    if (p->head_dim != PD) return fail(HYQ_ENOTSUP, "hyq_prefill_hybrid: head_dim must be 128");
-    if (p->pv_mode != 0 && p->pv_mode != 1) return fail(HYQ_EINVAL, "hyq_prefill_hybrid: pv_mode must be 0 (fp16) or 1 (fp8)");
+    if (p->head_dim != PD) return fail(HYQ_ENOTSUP, name + ": head_dim must be 128");
+    if (p->pv_mode != 0 && p->pv_mode != 1) return fail(HYQ_EINVAL, name + ": pv_mode must be 0 (fp16) or 1 (fp8)");
     if (B <= 0 || HQ <= 0 || HKV <= 0 || HQ % HKV || N <= 0 || N > INT32_MAX / 2 || T < 0 || W < 0)
-        return fail(HYQ_EINVAL, "hyq_prefill_hybrid: invalid sizes (need HQ % HKV == 0, N > 0)");
+        return fail(HYQ_EINVAL, name + ": invalid sizes (need HQ % HKV == 0, N > 0)");
     const int64_t P = std::max<int64_t>(0, N - W);
-    if (P > MAX_P) return fail(HYQ_ENOTSUP, "hyq_prefill_hybrid: N - window exceeds 131072");
-    if (T > MAX_T) return fail(HYQ_ENOTSUP, "hyq_prefill_hybrid: more than 8192 vertical indices per head");
+    if (P > MAX_P) return fail(HYQ_ENOTSUP, name + ": N - window exceeds 131072");
+    if (T > MAX_T) return fail(HYQ_ENOTSUP, name + ": more than 8192 vertical indices per head");
     if (!p->q || !p->k || !p->v || !p->out || (P > 0 && T > 0 && !p->vidx))
-        return fail(HYQ_EINVAL, "hyq_prefill_hybrid: null pointer");
+        return fail(HYQ_EINVAL, name + ": null pointer");
     auto rows16 = [](const void* ptr, int64_t sb, int64_t sh, int64_t sn) {
         return aligned(ptr, 16) && (sb * 2) % 16 == 0 && (sh * 2) % 16 == 0 && (sn * 2) % 16 == 0;
     };
@@ -1080,10 +1090,10 @@ extern "C" int hyq_prefill_hybrid(const hyq_prefill_params* p, void* ws, size_t 
         !rows16(p->k, p->k_stride_b, p->k_stride_h, p->k_stride_n) ||
         !rows16(p->v, p->v_stride_b, p->v_stride_h, p->v_stride_n) ||
         !rows16(p->out, p->o_stride_b, p->o_stride_h, p->o_stride_n))
-        return fail(HYQ_EINVAL, "hyq_prefill_hybrid: q/k/v/out rows must be contiguous and 16-byte aligned");
+        return fail(HYQ_EINVAL, name + ": q/k/v/out rows must be contiguous and 16-byte aligned");
     const PrefillLayout L = prefill_layout(B, HQ, HKV, N, T, W, p->pv_mode);
     if (!ws || ws_bytes < L.total || !aligned(ws, 256))
-        return fail(HYQ_ENOSPC, "hyq_prefill_hybrid: workspace too small or not 256-byte aligned (need " +
+        return fail(HYQ_ENOSPC, name + ": workspace too small or not 256-byte aligned (need " +
                                     std::to_string(L.total) + " bytes)");
     uint8_t* base = static_cast<uint8_t*>(ws);
     auto at = [&](size_t off) { return static_cast<void*>(base + off); };
@@ -1149,9 +1159,23 @@ extern "C" int hyq_prefill_hybrid(const hyq_prefill_params* p, void* ws, size_t 
     a.total = BH * nblk;
     a.per_xcd = (a.total + 7) / 8;
     a.vscale = static_cast<const float*>(at(L.vscale));
+    a.rest_causal = rest_causal ? 1 : 0;
     if (p->pv_mode)
         hipLaunchKernelGGL(prefill_main_kernel<true>, dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
     else
         hipLaunchKernelGGL(prefill_main_kernel<false>, dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
     return check_launch("prefill_main_kernel");
+}
+}  // namespace
+}  // namespace hyq
+
+extern "C" int hyq_prefill_hybrid(const hyq_prefill_params* p, void* ws, size_t ws_bytes, void* stream) {
+    return hyq::prefill_run(p, ws, ws_bytes, static_cast<hipStream_t>(stream), false, "hyq_prefill_hybrid");
+}
+
+extern "C" int hyq_prefill_unified(const hyq_prefill_params* p, void* ws, size_t ws_bytes, void* stream) {
+    if (!p) return hyq::fail(HYQ_EINVAL, "hyq_prefill_unified: null params");
+    if (p->t != 0) return hyq::fail(HYQ_EINVAL, "hyq_prefill_unified: t must be 0 (no vertical indices)");
+    return hyq::prefill_run(p, ws, ws_bytes, static_cast<hipStream_t>(stream), p->window == 0,
+                            "hyq_prefill_unified");
 }

@@ -19,11 +19,13 @@ output projection and routes the attention itself by mode:
                        runs the hybrid kernel ("vquant_vert" prefill) or exact
                        causal attention ("full" prefill);
   vquant_vert          hybrid prefill without a D-stage cache;
+  sage_w, sage_w0      window-only INT8-QK prefill (sage_unified_attention)
+                       with the window W, or with every key in int8;
   full_attention       exact causal attention for the prefill.
 Decode steps of the prefill-only modes use the model's own attention, as in
-the reference.  The window-only SageAttention modes (sage_w, sage_w0) and the
-sparse baselines (sparse_only, minference_sparse) are not part of this build
-and raise NotImplementedError when a model is patched with them.
+the reference.  The sparse baselines (sparse_only, minference_sparse) are not
+part of this build and raise NotImplementedError when a model is patched
+with them.
 
 Exact causal attention is the hybrid prefill kernel with the window covering
 the whole sequence (every key tile in fp16, one softmax), so every prefill
@@ -58,7 +60,7 @@ D_STAGE_MODES = {
 
 VALID_MODES = {"dense", "full_attention", "sage_w", "sage_w0", "vquant_vert", "minference_sparse", "sparse_only",
                "d_stage", *D_STAGE_MODES}
-_NOT_BUILT = {"sage_w", "sage_w0", "sparse_only", "minference_sparse"}
+_NOT_BUILT = {"sparse_only", "minference_sparse"}
 _VALID_BITS = (2, 4, 8)
 
 
@@ -227,7 +229,11 @@ def build_attention_forward(family: str, *, mode: str, window_size: int, top_rat
                     raise NotImplementedError("chunked prefill (keys longer than queries) is not supported")
                 hybrid = mode == "vquant_vert" or mode == "d_stage" or (
                     d_mode and D_STAGE_MODES[mode]["prefill_kernel"] == "vquant_vert")
-                if hybrid:
+                if mode in ("sage_w", "sage_w0"):             # src/patch/patch_llama.py:211-221
+                    from .sage_unified import sage_unified_attention
+                    out = sage_unified_attention(q, k, v, window_size=window_size if mode == "sage_w" else 0,
+                                                 smooth_k=True)
+                elif hybrid:
                     out = _hybrid_prefill(q, k, v, window_size, top_ratio, kv_repeat)
                 else:                                           # full_attention and the "full" D-stage modes
                     out = causal_attention(q, k, v)
@@ -242,8 +248,8 @@ def _patch(model: torch.nn.Module, family: str, cls, mode: str, window_size: int
            k_bits: Optional[int], v_bits: Optional[int]) -> torch.nn.Module:
     mode = validate_patch_args(mode, window_size, top_ratio, k_bits, v_bits)
     if mode in _NOT_BUILT:
-        raise NotImplementedError(f"mode '{mode}' (window-only SageAttention / sparse baselines) is not part of "
-                                  "this build; the hybrid modes are vquant_vert, hybrid_* and d_*")
+        raise NotImplementedError(f"mode '{mode}' (sparse baseline) is not part of this build; the attention "
+                                  "modes are dense, full_attention, sage_w, sage_w0, vquant_vert, hybrid_* and d_*")
     fwd = build_attention_forward(family, mode=mode, window_size=window_size, top_ratio=top_ratio)
     patched = 0
     for module in model.modules():

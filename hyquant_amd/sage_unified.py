@@ -167,6 +167,46 @@ def reorder_kv_for_vertical(k: torch.Tensor, v: torch.Tensor, vertical_indices: 
 # ---------------------------------------------------------------------------
 
 
+def _prefill(entry: str, name: str, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+             vertical_indices: Optional[torch.Tensor], window_size: int, sm_scale: Optional[float],
+             smooth_k: bool, pv_mode: str) -> torch.Tensor:
+    _require_gpu(q, "q")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError(f"{name} expects bf16 q, k, v")
+    if pv_mode not in PV_MODES:
+        raise ValueError(f"pv_mode must be one of {tuple(PV_MODES)}")
+    B, H_q, N, D = q.shape
+    _, H_kv, Nk, _ = k.shape
+    if Nk != N or v.shape != k.shape or H_q % H_kv:
+        raise ValueError(f"{name}: expected k/v [B, H_q / g, N, D] matching q")
+    if window_size < 0:
+        raise ValueError(f"{name}: window_size must be >= 0")
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    q, k, v = _rows16(q), _rows16(k), _rows16(v)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    mode = PV_MODES[pv_mode]
+    T = 0 if vertical_indices is None else vertical_indices.shape[2]
+    L = _lib.lib()
+    nbytes = L.hyq_prefill_workspace_size(B, H_q, H_kv, N, T, window_size, mode)
+    stream = _stream(q.device)
+    ws = _workspace(q.device, stream, nbytes)
+    p = _lib.PrefillParams()
+    p.q, (p.q_stride_b, p.q_stride_h, p.q_stride_n) = q.data_ptr(), q.stride()[:3]
+    p.k, (p.k_stride_b, p.k_stride_h, p.k_stride_n) = k.data_ptr(), k.stride()[:3]
+    p.v, (p.v_stride_b, p.v_stride_h, p.v_stride_n) = v.data_ptr(), v.stride()[:3]
+    if vertical_indices is not None:
+        p.vidx, (p.vi_stride_b, p.vi_stride_h, p.vi_stride_t) = vertical_indices.data_ptr(), vertical_indices.stride()
+    p.out, (p.o_stride_b, p.o_stride_h, p.o_stride_n) = out.data_ptr(), out.stride()[:3]
+    p.batch, p.hq, p.hkv, p.head_dim = B, H_q, H_kv, D
+    p.n, p.t = N, T
+    p.window, p.smooth_k, p.pv_mode = window_size, int(bool(smooth_k)), mode
+    p.sm_scale = float(sm_scale)
+    st = getattr(L, entry)(ctypes.byref(p), ws.data_ptr(), ws.numel(), stream)
+    _lib.check(st, name)
+    return out
+
+
 def sage_vertical_attention_v2(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, vertical_indices: torch.Tensor,
                                *, window_size: int = 256, sm_scale: Optional[float] = None, smooth_k: bool = True,
                                pv_mode: str = "fp16") -> torch.Tensor:
@@ -176,37 +216,19 @@ def sage_vertical_attention_v2(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
     [B, H_q, N, D].  pv_mode "fp8" runs P.V on the rest tiles in OCP e4m3
     with per-channel V scales."""
     _require_gpu(q, "q")
-    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
-        raise ValueError("sage_vertical_attention_v2 expects bf16 q, k, v")
-    if pv_mode not in PV_MODES:
-        raise ValueError(f"pv_mode must be one of {tuple(PV_MODES)}")
-    B, H_q, N, D = q.shape
-    _, H_kv, Nk, _ = k.shape
-    if Nk != N or v.shape != k.shape or H_q % H_kv:
-        raise ValueError("sage_vertical_attention_v2: expected k/v [B, H_q / g, N, D] matching q")
-    if vertical_indices.dim() != 3 or vertical_indices.shape[:2] != (B, H_q):
+    if vertical_indices.dim() != 3 or vertical_indices.shape[:2] != q.shape[:2]:
         raise ValueError("vertical_indices must be [B, H_q, T]")
-    if sm_scale is None:
-        sm_scale = D ** -0.5
-    q, k, v = _rows16(q), _rows16(k), _rows16(v)
-    vidx = vertical_indices.to(torch.int64)
-    T = vidx.shape[2]
-    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    mode = PV_MODES[pv_mode]
-    L = _lib.lib()
-    nbytes = L.hyq_prefill_workspace_size(B, H_q, H_kv, N, T, window_size, mode)
-    stream = _stream(q.device)
-    ws = _workspace(q.device, stream, nbytes)
-    p = _lib.PrefillParams()
-    p.q, (p.q_stride_b, p.q_stride_h, p.q_stride_n) = q.data_ptr(), q.stride()[:3]
-    p.k, (p.k_stride_b, p.k_stride_h, p.k_stride_n) = k.data_ptr(), k.stride()[:3]
-    p.v, (p.v_stride_b, p.v_stride_h, p.v_stride_n) = v.data_ptr(), v.stride()[:3]
-    p.vidx, (p.vi_stride_b, p.vi_stride_h, p.vi_stride_t) = vidx.data_ptr(), vidx.stride()
-    p.out, (p.o_stride_b, p.o_stride_h, p.o_stride_n) = out.data_ptr(), out.stride()[:3]
-    p.batch, p.hq, p.hkv, p.head_dim = B, H_q, H_kv, D
-    p.n, p.t = N, T
-    p.window, p.smooth_k, p.pv_mode = window_size, int(bool(smooth_k)), mode
-    p.sm_scale = float(sm_scale)
-    st = L.hyq_prefill_hybrid(ctypes.byref(p), ws.data_ptr(), ws.numel(), stream)
-    _lib.check(st, "sage_vertical_attention_v2")
-    return out
+    return _prefill("hyq_prefill_hybrid", "sage_vertical_attention_v2", q, k, v, vertical_indices.to(torch.int64),
+                    window_size, sm_scale, smooth_k, pv_mode)
+
+
+def sage_unified_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, window_size: int = 0,
+                           sm_scale: Optional[float] = None, smooth_k: bool = True) -> torch.Tensor:
+    """Window-only INT8-QK / fp16-PV prefill, the sage_w (window_size > 0) and
+    sage_w0 (window_size = 0) modes (src/ops/sage_unified.py:234-313, kernel
+    :112-231).  window_size > 0: int8 keys below the 64-aligned window start
+    of each 128-row query block, fp16 causal window above it; window_size = 0:
+    every key up to the diagonal in int8.  q [B, H_q, N, D], k/v
+    [B, H_kv, N, D] bf16 -> bf16 [B, H_q, N, D]."""
+    return _prefill("hyq_prefill_unified", "sage_unified_attention", q, k, v, None, window_size, sm_scale,
+                    smooth_k, "fp16")

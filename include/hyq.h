@@ -234,6 +234,19 @@ size_t hyq_prefill_workspace_size(int32_t b, int32_t hq, int32_t hkv, int64_t n,
 int hyq_prefill_hybrid(const hyq_prefill_params* params, void* workspace, size_t workspace_bytes,
                        void* stream);
 
+/*
+ * Window-only INT8-QK prefill.  Replaces sage_unified_attention
+ * (src/ops/sage_unified.py:234-313) and its kernel _attn_fwd_unified
+ * (:112-231), the prefill of the sage_w / sage_w0 modes.  Same parameters as
+ * hyq_prefill_hybrid with t = 0 (vidx unused); window > 0: int8 keys below
+ * wla and the fp16 causal window wla <= j <= i, i.e. the hybrid partition
+ * without vertical lines; window = 0: every key j <= i through int8 Q . K
+ * (64-key K blocks, causal mask on the diagonal block).  Workspace:
+ * hyq_prefill_workspace_size(b, hq, hkv, n, 0, window, pv_mode).
+ */
+int hyq_prefill_unified(const hyq_prefill_params* params, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -769,6 +769,46 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
     return out
 
 
+def unified_prefill_fp64(q, k, v, W: int, sm_scale: Optional[float] = None, smooth: bool = True,
+                         int8: bool = True, abs_v: bool = False):
+    """float64 restatement of sage_unified_attention (sage_unified.py:234-313,
+    kernel _attn_fwd_unified :112-231).  W > 0: int8 keys below wla(b), the
+    fp16 causal window wla(b) <= j <= i; this is hybrid_prefill_fp64 with no
+    vertical lines.  W = 0: every key j <= i scored in int8,
+    s = (q8 . k8) * q_scale * k_scale with K (smoothed) quantised per 64
+    positions over the whole sequence (the int8 prefix segment :166-177 and
+    the causal int8 diagonal :204-217).  int8=False scores every key with
+    q16 . k16 instead, which checks the W = 0 partition alone."""
+    B, HQ, N, D = q.shape
+    if W > 0:
+        return hybrid_prefill_fp64(q, k, v, np.zeros((B, HQ, 0), np.int64), W, sm_scale, smooth,
+                                   int8_rest=int8, abs_v=abs_v)
+    HKV = k.shape[1]
+    G = HQ // HKV
+    op = prefill_operands(q, k, v, sm_scale, smooth)
+    q8, qsc, q16, k16, v16 = op["q8"], op["q_scale"], op["q16"], op["k16"], op["v16"]
+    if abs_v:
+        v16 = np.abs(v16)
+    out = np.zeros((B, HQ, N, D), np.float64)
+    for b in range(B):
+        for hk in range(HKV):
+            k8, ksc = per_block_int8(k16[b, hk], 1.0, PREFILL_BLOCK_N)
+            kscale = np.repeat(ksc.astype(np.float64), PREFILL_BLOCK_N)[:N]
+            for h in range(hk * G, (hk + 1) * G):
+                for blk in range((N + PREFILL_BLOCK_M - 1) // PREFILL_BLOCK_M):
+                    rows = np.arange(blk * PREFILL_BLOCK_M, min(N, (blk + 1) * PREFILL_BLOCK_M))
+                    n = rows[-1] + 1
+                    if int8:
+                        s = q8[b, h, rows].astype(np.float64) @ k8[:n].astype(np.float64).T
+                        s = s * float(qsc[b, h, blk]) * kscale[None, :n]
+                    else:
+                        s = q16[b, h, rows].astype(np.float64) @ k16[b, hk, :n].astype(np.float64).T
+                    s = np.where(np.arange(n)[None, :] <= rows[:, None], s, -np.inf)
+                    p = np.exp2(s - s.max(axis=1, keepdims=True))
+                    out[b, h, rows] = (p @ v16[b, hk, :n].astype(np.float64)) / p.sum(axis=1, keepdims=True)
+    return out
+
+
 def exact_causal_attention(q, k, v, sm_scale: Optional[float] = None) -> np.ndarray:
     """softmax(q k^T * sm_scale + causal mask) v in float64, GQA by head // G."""
     B, HQ, N, D = q.shape

@@ -100,6 +100,19 @@ def test_decode_host_validation():
     assert b"16 * bits" in L.hyq_last_error()
 
 
+def test_prefill_unified_host_validation():
+    """hyq_prefill_unified takes no vertical indices: t != 0 is EINVAL
+    before anything is launched."""
+    from hyquant_amd import _lib
+    L = _lib.lib()
+    p = _lib.PrefillParams()
+    p.batch, p.hq, p.hkv, p.head_dim, p.n, p.t, p.window = 1, 1, 1, 128, 64, 3, 0
+    assert L.hyq_prefill_unified(ctypes.byref(p), None, 0, None) == _lib.HYQ_EINVAL
+    assert b"t must be 0" in L.hyq_last_error()
+    p.t = 0
+    assert L.hyq_prefill_unified(ctypes.byref(p), None, 0, None) == _lib.HYQ_EINVAL    # null tensors
+
+
 def test_bf16_workspace_size():
     _lib, L = _L()
     assert L.hyq_decode_bf16_workspace_size(8, 4, 8192, 128) > 8 * 4 * 128 * 4

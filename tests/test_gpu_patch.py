@@ -149,6 +149,33 @@ def test_generate_tracks_dense(family, mode, min_cos):
     assert cache.get_seq_length() == N_PROMPT + 6
 
 
+@pytest.mark.parametrize("mode", ["sage_w", "sage_w0"])
+def test_window_only_modes(mode):
+    """sage_w / sage_w0 (src/patch/patch_llama.py:211-221): the prefill runs
+    sage_unified_attention, whose per-layer outputs track the dense model's;
+    decode steps use the model's own attention and the HF cache."""
+    from hyquant_amd.patch import patch_attention_forward_model
+    ids = _ids(seed=5)
+    dense = _model("llama")
+    model = patch_attention_forward_model(_model("llama"), mode=mode, window_size=W)
+    store, hooks = _capture(model)
+    with torch.no_grad():
+        out = model.generate(ids, max_new_tokens=3, do_sample=False)
+        model(ids)
+    for h in hooks:
+        h.remove()
+    dstore, dhooks = _capture(dense)
+    with torch.no_grad():
+        dense(ids)
+    for h in dhooks:
+        h.remove()
+    for i in store:
+        c = _cos(store[i], dstore[i])
+        print(f"  {mode} prefill layer {i}: cos {c:.5f}", flush=True)
+        assert c > 0.98, (i, c)
+    assert out.shape == (1, N_PROMPT + 3)
+
+
 def test_hf_generate_with_cache():
     """transformers' own generate() loop drives the cache (transformers 5.x API)."""
     from hyquant_amd.patch import create_cache_for_mode, patch_attention_forward_model
@@ -167,6 +194,6 @@ def test_mode_errors():
     with pytest.raises(ValueError):
         patch_attention_forward_model(m, mode="nope")
     with pytest.raises(NotImplementedError):
-        patch_attention_forward_model(m, mode="sage_w")
+        patch_attention_forward_model(m, mode="sparse_only")
     with pytest.raises(ValueError):
         patch_attention_forward_model(m, mode="hybrid_full", top_ratio=0.0)

@@ -259,3 +259,34 @@ def test_prefill_fp8_config4_mse():
     mse16 = float(((out16.float() - exact) ** 2).mean())
     print(f"config4 N=8192: MSE vs exact, fp16 PV {mse16:.3e}, fp8 PV {mse8:.3e}", flush=True)
     assert mse8 < 1e-4
+
+
+UNIFIED_CASES = [
+    dict(B=1, HQ=4, HKV=1, N=640, W=0, seed=21),                  # sage_w0: int8 through the diagonal
+    dict(B=2, HQ=4, HKV=2, N=777, W=0, seed=22),                  # ragged last block
+    dict(B=1, HQ=4, HKV=1, N=700, W=128, seed=23),                # sage_w
+    dict(B=1, HQ=2, HKV=1, N=520, W=100, seed=24),                # window not a multiple of 64
+    dict(B=1, HQ=2, HKV=2, N=129, W=0, seed=25),                  # one full block and one row
+]
+
+
+@pytest.mark.parametrize("cfg", UNIFIED_CASES, ids=[f"unified-N{c['N']}W{c['W']}" for c in UNIFIED_CASES])
+def test_unified_prefill_vs_oracle(cfg):
+    """sage_unified_attention (hyq_prefill_unified): window-only INT8-QK
+    prefill against the float64 restatement of sage_unified.py:112-313."""
+    from hyquant_amd.sage_unified import sage_unified_attention
+    print(f"unified {cfg}", flush=True)
+    rng = np.random.default_rng(cfg["seed"])
+    B, HQ, HKV, N, W = (cfg[x] for x in ("B", "HQ", "HKV", "N", "W"))
+    q = _rand_bf16(rng, (B, HQ, N, 128))
+    k = O.bf16_round(_rand_bf16(rng, (B, HKV, N, 128), 1.5)
+                     + O.bf16_round(rng.standard_normal((1, HKV, 1, 128)).astype(np.float32)))
+    v = _rand_bf16(rng, (B, HKV, N, 128))
+    dev = torch.device("cuda")
+    out = sage_unified_attention(to_dev_bf16(q, dev), to_dev_bf16(k, dev), to_dev_bf16(v, dev), window_size=W)
+    torch.cuda.synchronize()
+    out = out.float().cpu().numpy()
+    ref = O.unified_prefill_fp64(q, k, v, W)
+    ref_abs = O.unified_prefill_fp64(q, k, v, W, abs_v=True)
+    _check(f"unified {cfg}", out, ref, ref_abs)
+

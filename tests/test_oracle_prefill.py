@@ -185,6 +185,55 @@ def test_hybrid_prefill_int8_error_is_small():
 
 
 # ---------------------------------------------------------------------------
+# sage_unified_attention (window-only modes)
+# ---------------------------------------------------------------------------
+
+def test_unified_w0_partition_reduces_to_exact_attention():
+    """W = 0 with int8 scoring off: one softmax over every key j <= i exactly
+    once, i.e. textbook causal attention on (q16, k16, v16)."""
+    rng = np.random.default_rng(11)
+    q = _rand_bf16(rng, (1, 4, 330, 32))
+    k = _rand_bf16(rng, (1, 2, 330, 32), 1.5)
+    v = _rand_bf16(rng, (1, 2, 330, 32))
+    op = O.prefill_operands(q, k, v)
+    exact = O.exact_causal_attention(op["q16"], op["k16"], op["v16"], sm_scale=math.log(2))
+    got = O.unified_prefill_fp64(q, k, v, 0, int8=False)
+    assert np.abs(got - exact).max() < 1e-12
+
+
+def test_unified_w0_matches_per_element_brute_force():
+    """W = 0 with int8 scoring, element by element: query i attends keys
+    0..i with s = q8[i] . k8[j] * q_scale[i // 128] * k_scale[j // 64], K
+    quantised per 64 positions of the whole (smoothed) sequence."""
+    rng = np.random.default_rng(12)
+    N, D = 300, 16
+    q = _rand_bf16(rng, (1, 2, N, D))
+    k = _rand_bf16(rng, (1, 1, N, D), 1.5)
+    v = _rand_bf16(rng, (1, 1, N, D))
+    op = O.prefill_operands(q, k, v, sm_scale=D ** -0.5)
+    k8, ksc = O.per_block_int8(op["k16"][0, 0], 1.0, 64)
+    got = O.unified_prefill_fp64(q, k, v, 0, sm_scale=D ** -0.5)
+    exp = np.zeros_like(got)
+    for h in range(2):
+        for i in range(N):
+            s = [float(np.dot(op["q8"][0, h, i].astype(np.int64), k8[j].astype(np.int64)))
+                 * float(op["q_scale"][0, h, i // 128]) * float(ksc[j // 64]) for j in range(i + 1)]
+            s = np.array(s)
+            p = np.exp2(s - s.max())
+            exp[0, h, i] = p @ op["v16"][0, 0, :i + 1].astype(np.float64) / p.sum()
+    assert np.abs(got - exp).max() < 1e-12
+
+
+def test_unified_int8_error_is_small():
+    q, k, v = O.make_prefill_inputs(B=1, HQ=4, HKV=1, N=520, W=128, seed=4)
+    ref = O.exact_causal_attention(q, k, v)
+    for W in (0, 128):
+        got = O.unified_prefill_fp64(q, k, v, W)
+        mse = float(((got - ref) ** 2).mean())
+        assert mse < 1e-4, (W, mse)
+
+
+# ---------------------------------------------------------------------------
 # OCP e4m3 rounding and the fp8-PV mode
 # ---------------------------------------------------------------------------
 

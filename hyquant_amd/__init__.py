@@ -13,7 +13,11 @@ from .decode_d_stage import (  # noqa: F401
     fused_d_stage_decode_splitk,
     quantize_per_token,
 )
-from .sage_unified import sage_unified_attention, sage_vertical_attention_v2  # noqa: F401
+from .sage_unified import (  # noqa: F401
+    sage_unified_attention,
+    sage_vertical_attention_v2,
+    sage_vertical_attention_v2_fp8,
+)
 from .vertical import compute_vertical_indices  # noqa: F401
 
 __all__ = [
@@ -27,4 +31,5 @@ __all__ = [
     "compute_vertical_indices",
     "sage_vertical_attention_v2",
     "sage_unified_attention",
+    "sage_vertical_attention_v2_fp8",
 ]

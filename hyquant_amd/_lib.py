@@ -38,6 +38,7 @@ EXPORTS = (
     "hyq_prefill_workspace_size",
     "hyq_prefill_hybrid",
     "hyq_prefill_unified",
+    "hyq_prefill_hybrid_fp8qk",
 )
 
 
@@ -127,6 +128,8 @@ def _declare(lib):
     lib.hyq_prefill_hybrid.argtypes = [POINTER(PrefillParams), c_void_p, c_size_t, c_void_p]
     lib.hyq_prefill_unified.restype = c_int
     lib.hyq_prefill_unified.argtypes = [POINTER(PrefillParams), c_void_p, c_size_t, c_void_p]
+    lib.hyq_prefill_hybrid_fp8qk.restype = c_int
+    lib.hyq_prefill_hybrid_fp8qk.argtypes = [POINTER(PrefillParams), c_void_p, c_size_t, c_void_p]
 
 
 def lib():

@@ -153,9 +153,18 @@ __device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float
     return static_cast<uint32_t>(r);
 }
 
-// P' operands: exp2(s - m + 8.807 - guard) with the exact running max lies
-// in [0, 447.98], inside the e4m3 range, so no clamp
-__device__ __forceinline__ uint32_t pack_p_e4m3x4(float a, float b, float c, float d) {
+// FP8-QK quantiser code of per_block_fp8_e4m3 (src/ops/sage_unified_fp8.py:
+// 52-88): e4m3(clamp(x / scale, +-448)), IEEE fp32 division, round to
+// nearest even.
+__device__ __forceinline__ float fp8_ratio(float x, float scale) {
+    return fminf(fmaxf(x / scale, -FP8_MAX), FP8_MAX);
+}
+
+// four values already inside [-448, 448] -> e4m3 codes (round to nearest
+// even), no clamp: the FP8-QK ratios are clamped by fp8_ratio, and the P'
+// operands exp2(s - m + 8.807 - guard) with the exact running max lie in
+// [0, 447.98]
+__device__ __forceinline__ uint32_t pack_e4m3x4_raw(float a, float b, float c, float d) {
     int r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
     r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
     return static_cast<uint32_t>(r);
@@ -397,7 +406,7 @@ __global__ __launch_bounds__(256) void gather_kernel(
     int G, int HKV, int N, int P, int T, int nsb, const int32_t* __restrict__ rest,
     const int32_t* __restrict__ rcount, const int32_t* __restrict__ vert, int8_t* __restrict__ k8r,
     float* __restrict__ k8r_scale, uint8_t* __restrict__ vr, uint16_t* __restrict__ kv16,
-    uint16_t* __restrict__ vv16) {
+    uint16_t* __restrict__ vv16, int k_fp8) {
     __shared__ float s_amax[4];
     const int bh = blockIdx.y, b = bh / HQ, h = bh % HQ;
     const int64_t bhk = static_cast<int64_t>(b) * HKV + h / G;
@@ -439,14 +448,18 @@ __global__ __launch_bounds__(256) void gather_kernel(
         if ((tid & 63) == 0) s_amax[tid >> 6] = amax;
         __syncthreads();
         amax = fmaxf(fmaxf(s_amax[0], s_amax[1]), fmaxf(s_amax[2], s_amax[3]));
-        const float scale = amax / 127.0f;
+        // int8: amax / 127; e4m3 (FP8-QK): amax / 448, 1 for an all-zero block
+        float scale = amax / (k_fp8 ? FP8_MAX : 127.0f);
+        if (k_fp8 && !(scale > 0.0f)) scale = 1.0f;
         if (tid == 0) k8r_scale[static_cast<int64_t>(bh) * nsb + blockIdx.x] = scale;
         if (ok) {
             uint32_t wds[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                wds[i] = pack4_i8(pb_code(x[4 * i], scale), pb_code(x[4 * i + 1], scale),
-                                  pb_code(x[4 * i + 2], scale), pb_code(x[4 * i + 3], scale));
+                wds[i] = k_fp8 ? pack_e4m3x4_raw(fp8_ratio(x[4 * i], scale), fp8_ratio(x[4 * i + 1], scale),
+                                               fp8_ratio(x[4 * i + 2], scale), fp8_ratio(x[4 * i + 3], scale))
+                               : pack4_i8(pb_code(x[4 * i], scale), pb_code(x[4 * i + 1], scale),
+                                          pb_code(x[4 * i + 2], scale), pb_code(x[4 * i + 3], scale));
             u32x4* dst = reinterpret_cast<u32x4*>(k8r + (static_cast<int64_t>(bh) * P + base + r) * PD + 32 * qq);
             dst[0] = u32x4{wds[0], wds[1], wds[2], wds[3]};
             dst[1] = u32x4{wds[4], wds[5], wds[6], wds[7]};
@@ -541,6 +554,13 @@ __device__ __forceinline__ f32x4 mfma_f16(const f16x8& a, const f16x8& b, const 
 __device__ __forceinline__ i32x4 mfma_i8(const i32x4& a, const i32x4& b, const i32x4& c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
+// 16 x 16 x 128 e4m3 product (format 0 on both sides, unit block scales:
+// e8m0 127 = 2^0)
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x4 mfma_f8_k128(const i32x8& a, const i32x8& b) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 127, 0,
+                                                            127);
+}
 __device__ __forceinline__ f32x4 mfma_fp8(const u32x2& a, const u32x2& b, const f32x4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0, 0, 0);
 }
@@ -556,7 +576,13 @@ struct TileDesc {
 // e4m3(v / vscale)); the vertical and window tiles keep fp16 operands in the
 // same units (fp16(P'), fp16(v / vscale)); the epilogue multiplies by vscale.
 // The running max is exact in this mode (no lazy slack), so P' <= 448.
-template <bool PV8>
+// QF8: the rest tiles score Q and K in OCP e4m3 (sage_vertical_attention_v2_fp8,
+// src/ops/sage_unified_fp8.py:158-311): Q per 128-row block and rest K per
+// 64-entry block with scale amax / 448 (1 for an all-zero block), one
+// v_mfma_scale_f32_16x16x128_f8f6f4 per 16 keys over all 128 channels (the
+// lane's 32 channels are the same 16 + 16 bytes the int8 path splits over
+// two MFMAs; Q and K use the same channel order, so the dot product is whole).
+template <bool PV8, bool QF8>
 __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t s_k[2][KBUF];
     __shared__ __attribute__((aligned(16))) uint8_t s_v[2][VBUF];
@@ -601,7 +627,9 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     amax = wave_max(amax);
     if (lane == 0) s_red[w] = amax;
     __syncthreads();
-    const float q_scale = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3])) / 127.0f;
+    const float q_amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    float q_scale = q_amax / (QF8 ? FP8_MAX : 127.0f);
+    if (QF8 && !(q_scale > 0.0f)) q_scale = 1.0f;
     i32x4 q8[2][2];
     f16x8 qh[2][4];
 #pragma unroll
@@ -612,8 +640,10 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             uint32_t wd[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                wd[i] = pack4_i8(pb_code(xv[4 * i], q_scale), pb_code(xv[4 * i + 1], q_scale),
-                                 pb_code(xv[4 * i + 2], q_scale), pb_code(xv[4 * i + 3], q_scale));
+                wd[i] = QF8 ? pack_e4m3x4_raw(fp8_ratio(xv[4 * i], q_scale), fp8_ratio(xv[4 * i + 1], q_scale),
+                                            fp8_ratio(xv[4 * i + 2], q_scale), fp8_ratio(xv[4 * i + 3], q_scale))
+                            : pack4_i8(pb_code(xv[4 * i], q_scale), pb_code(xv[4 * i + 1], q_scale),
+                                       pb_code(xv[4 * i + 2], q_scale), pb_code(xv[4 * i + 3], q_scale));
             q8[sb][cc] = i32x4{static_cast<int>(wd[0]), static_cast<int>(wd[1]), static_cast<int>(wd[2]),
                                static_cast<int>(wd[3])};
 #pragma unroll
@@ -769,7 +799,24 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         // ---- S^T = K . Q^T --------------------------------------------------
         float s[2][4][4];
         bool masked;
-        if (d.kind == T_REST) {
+        if (d.kind == T_REST && QF8) {
+#pragma unroll
+            for (int kbk = 0; kbk < 4; ++kbk) {
+                const uint8_t* row = kb + (16 * kbk + c16) * KSTR8 + 16 * g;
+                const i32x4 a0 = *reinterpret_cast<const i32x4*>(row);
+                const i32x4 a1 = *reinterpret_cast<const i32x4*>(row + 64);
+                const i32x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    const i32x8 bv = {q8[sb][0][0], q8[sb][0][1], q8[sb][0][2], q8[sb][0][3],
+                                      q8[sb][1][0], q8[sb][1][1], q8[sb][1][2], q8[sb][1][3]};
+                    const f32x4 sf = mfma_f8_k128(av, bv);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s[sb][kbk][r] = sf[r];
+                }
+            }
+            masked = d.idx0 + BN > d.valid || (a.rest_causal && d.idx0 + BN - 1 > BM * blk + 32 * w);
+        } else if (d.kind == T_REST) {
             i32x4 si[2][4];
 #pragma unroll
             for (int kbk = 0; kbk < 4; ++kbk) {
@@ -873,8 +920,8 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             if (PV8 && d.kind == T_REST) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    pw[sb][j] = u32x4{pack_p_e4m3x4(p[2 * j][0], p[2 * j][1], p[2 * j][2], p[2 * j][3]),
-                                      pack_p_e4m3x4(p[2 * j + 1][0], p[2 * j + 1][1], p[2 * j + 1][2], p[2 * j + 1][3]),
+                    pw[sb][j] = u32x4{pack_e4m3x4_raw(p[2 * j][0], p[2 * j][1], p[2 * j][2], p[2 * j][3]),
+                                      pack_e4m3x4_raw(p[2 * j + 1][0], p[2 * j + 1][1], p[2 * j + 1][2], p[2 * j + 1][3]),
                                       0u, 0u};
             } else {
 #pragma unroll
@@ -1070,7 +1117,7 @@ namespace {
 // Both prefill entry points: the hybrid partition, or with rest_causal (the
 // unified kernel's window 0) every key through int8 up to the diagonal.
 int prefill_run(const hyq_prefill_params* p, void* ws, size_t ws_bytes, hipStream_t stream, bool rest_causal,
-                const std::string& name) {
+                bool qk_fp8, const std::string& name) {
     if (!p) return fail(HYQ_EINVAL, name + ": null params");
     const int B = p->batch, HQ = p->hq, HKV = p->hkv, W = p->window;
     const int64_t N = p->n, T = p->t;
@@ -1133,7 +1180,7 @@ int prefill_run(const hyq_prefill_params* p, void* ws, size_t ws_bytes, hipStrea
                            nsb, static_cast<const int32_t*>(at(L.rest)), static_cast<const int32_t*>(at(L.rcount)),
                            static_cast<const int32_t*>(at(L.vert)), static_cast<int8_t*>(at(L.k8r)),
                            static_cast<float*>(at(L.k8r_scale)), static_cast<uint8_t*>(at(L.vr)),
-                           static_cast<uint16_t*>(at(L.kv16)), static_cast<uint16_t*>(at(L.vv16)));
+                           static_cast<uint16_t*>(at(L.kv16)), static_cast<uint16_t*>(at(L.vv16)), qk_fp8 ? 1 : 0);
         if (int st = check_launch("gather_kernel")) return st;
     } else {
         // no prefix: every block reads zero rest / vertical entries
@@ -1160,22 +1207,31 @@ int prefill_run(const hyq_prefill_params* p, void* ws, size_t ws_bytes, hipStrea
     a.per_xcd = (a.total + 7) / 8;
     a.vscale = static_cast<const float*>(at(L.vscale));
     a.rest_causal = rest_causal ? 1 : 0;
-    if (p->pv_mode)
-        hipLaunchKernelGGL(prefill_main_kernel<true>, dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
+    if (qk_fp8)
+        hipLaunchKernelGGL((prefill_main_kernel<false, true>), dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
+    else if (p->pv_mode)
+        hipLaunchKernelGGL((prefill_main_kernel<true, false>), dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
     else
-        hipLaunchKernelGGL(prefill_main_kernel<false>, dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
+        hipLaunchKernelGGL((prefill_main_kernel<false, false>), dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
     return check_launch("prefill_main_kernel");
 }
 }  // namespace
 }  // namespace hyq
 
 extern "C" int hyq_prefill_hybrid(const hyq_prefill_params* p, void* ws, size_t ws_bytes, void* stream) {
-    return hyq::prefill_run(p, ws, ws_bytes, static_cast<hipStream_t>(stream), false, "hyq_prefill_hybrid");
+    return hyq::prefill_run(p, ws, ws_bytes, static_cast<hipStream_t>(stream), false, false, "hyq_prefill_hybrid");
+}
+
+extern "C" int hyq_prefill_hybrid_fp8qk(const hyq_prefill_params* p, void* ws, size_t ws_bytes, void* stream) {
+    if (!p) return hyq::fail(HYQ_EINVAL, "hyq_prefill_hybrid_fp8qk: null params");
+    if (p->pv_mode != 0) return hyq::fail(HYQ_EINVAL, "hyq_prefill_hybrid_fp8qk: pv_mode must be 0 (fp16 P.V)");
+    return hyq::prefill_run(p, ws, ws_bytes, static_cast<hipStream_t>(stream), false, true,
+                            "hyq_prefill_hybrid_fp8qk");
 }
 
 extern "C" int hyq_prefill_unified(const hyq_prefill_params* p, void* ws, size_t ws_bytes, void* stream) {
     if (!p) return hyq::fail(HYQ_EINVAL, "hyq_prefill_unified: null params");
     if (p->t != 0) return hyq::fail(HYQ_EINVAL, "hyq_prefill_unified: t must be 0 (no vertical indices)");
-    return hyq::prefill_run(p, ws, ws_bytes, static_cast<hipStream_t>(stream), p->window == 0,
+    return hyq::prefill_run(p, ws, ws_bytes, static_cast<hipStream_t>(stream), p->window == 0, false,
                             "hyq_prefill_unified");
 }

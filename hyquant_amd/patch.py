@@ -34,6 +34,8 @@ runs on libhyq.so.
 
 from __future__ import annotations
 
+import os
+
 from types import MethodType
 from typing import Any, Optional, Tuple
 
@@ -140,8 +142,11 @@ def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch
     return sage_vertical_attention_v2(q, k, v, none, window_size=N, smooth_k=False)
 
 
-def _hybrid_prefill(q, k, v, window_size: int, top_ratio: float, kv_repeat: int) -> torch.Tensor:
+def _hybrid_prefill(q, k, v, window_size: int, top_ratio: float, kv_repeat: int, fp8_qk: bool = False) -> torch.Tensor:
     vidx = compute_vertical_indices(q, k, window_size, top_ratio, kv_repeat=kv_repeat)
+    if fp8_qk:
+        from .sage_unified import sage_vertical_attention_v2_fp8
+        return sage_vertical_attention_v2_fp8(q, k, v, vidx, window_size=window_size, smooth_k=True)
     return sage_vertical_attention_v2(q, k, v, vidx, window_size=window_size, smooth_k=True)
 
 
@@ -234,7 +239,9 @@ def build_attention_forward(family: str, *, mode: str, window_size: int, top_rat
                     out = sage_unified_attention(q, k, v, window_size=window_size if mode == "sage_w" else 0,
                                                  smooth_k=True)
                 elif hybrid:
-                    out = _hybrid_prefill(q, k, v, window_size, top_ratio, kv_repeat)
+                    # D-stage modes honour HYBRID_ATTN_PREFILL_KERNEL=fp8 (src/patch/patch_llama.py:160-190)
+                    fp8_qk = d_mode and os.environ.get("HYBRID_ATTN_PREFILL_KERNEL", "int8").lower() == "fp8"
+                    out = _hybrid_prefill(q, k, v, window_size, top_ratio, kv_repeat, fp8_qk)
                 else:                                           # full_attention and the "full" D-stage modes
                     out = causal_attention(q, k, v)
             out = out.transpose(1, 2).to(hidden_states.dtype).contiguous()

@@ -232,3 +232,22 @@ def sage_unified_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     [B, H_kv, N, D] bf16 -> bf16 [B, H_q, N, D]."""
     return _prefill("hyq_prefill_unified", "sage_unified_attention", q, k, v, None, window_size, sm_scale,
                     smooth_k, "fp16")
+
+
+# The FP8-QK variant (src/ops/sage_unified_fp8.py) needs no optional dtype
+# support here: the e4m3 codes are produced and consumed by libhyq.so.
+FP8_SUPPORTED = True
+
+
+def sage_vertical_attention_v2_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                   vertical_indices: torch.Tensor, *, window_size: int = 256,
+                                   sm_scale: Optional[float] = None, smooth_k: bool = True) -> torch.Tensor:
+    """FP8-QK hybrid prefill (src/ops/sage_unified_fp8.py:312-398): the
+    partition of sage_vertical_attention_v2 with the rest keys scored in OCP
+    e4m3 (Q per 128-row block, rest K per 64-entry block, scale amax / 448),
+    fp16 vertical and window tiles and fp16 P.V."""
+    _require_gpu(q, "q")
+    if vertical_indices.dim() != 3 or vertical_indices.shape[:2] != q.shape[:2]:
+        raise ValueError("vertical_indices must be [B, H_q, T]")
+    return _prefill("hyq_prefill_hybrid_fp8qk", "sage_vertical_attention_v2_fp8", q, k, v,
+                    vertical_indices.to(torch.int64), window_size, sm_scale, smooth_k, "fp16")

@@ -235,6 +235,18 @@ int hyq_prefill_hybrid(const hyq_prefill_params* params, void* workspace, size_t
                        void* stream);
 
 /*
+ * FP8-QK hybrid prefill.  Replaces sage_vertical_attention_v2_fp8
+ * (src/ops/sage_unified_fp8.py:312-398, kernel :206-309, quantiser :52-148):
+ * the partition of hyq_prefill_hybrid with the rest keys scored in OCP e4m3,
+ * Q per 128-row block (x = q * sm_scale * log2e) and rest K per 64-entry
+ * block with scale amax / 448 (1 for an all-zero block) and codes
+ * e4m3(clamp(x / scale, +-448)); vertical and window tiles in fp16; fp16 P.V
+ * (pv_mode must be 0).  Workspace as hyq_prefill_hybrid.
+ */
+int hyq_prefill_hybrid_fp8qk(const hyq_prefill_params* params, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/*
  * Window-only INT8-QK prefill.  Replaces sage_unified_attention
  * (src/ops/sage_unified.py:234-313) and its kernel _attn_fwd_unified
  * (:112-231), the prefill of the sage_w / sage_w0 modes.  Same parameters as

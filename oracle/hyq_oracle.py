@@ -692,8 +692,32 @@ def fp8_v_operands(v):
     return vs, e4m3_round(ratio), to_fp16(ratio)
 
 
+def per_block_fp8(x: np.ndarray, sm: float, blk: int) -> Tuple[np.ndarray, np.ndarray]:
+    """_quant_per_block_fp8_kernel (src/ops/sage_unified_fp8.py:52-88) over
+    blocks of `blk` rows of x [..., L, D]: xs = fp32(x) * fp32(sm); scale =
+    fp32(amax / 448), 1 where that is not positive; code = e4m3(clamp(
+    fp32(xs / scale), +-448)) rounded to nearest even.  Returns (the e4m3
+    values as float64, scale float32 [..., ceil(L / blk)])."""
+    xf = np.asarray(x, dtype=np.float32) * np.float32(sm)
+    L = xf.shape[-2]
+    nb = (L + blk - 1) // blk
+    codes = np.zeros(xf.shape, dtype=np.float64)
+    scales = np.zeros(xf.shape[:-2] + (nb,), dtype=np.float32)
+    for i in range(nb):
+        blk_x = xf[..., i * blk:(i + 1) * blk, :]
+        amax = np.abs(blk_x).max(axis=(-2, -1))
+        scale = (amax / np.float32(FP8_MAX)).astype(np.float32)
+        scale = np.where(scale > 0, scale, np.float32(1.0)).astype(np.float32)
+        scales[..., i] = scale
+        r = (blk_x / scale[..., None, None]).astype(np.float32)
+        r = np.clip(r, -FP8_MAX, FP8_MAX)
+        codes[..., i * blk:(i + 1) * blk, :] = e4m3_round(r)
+    return codes, scales
+
+
 def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None, smooth: bool = True,
-                        int8_rest: bool = True, abs_v: bool = False, pv_mode: str = "fp16"):
+                        int8_rest: bool = True, abs_v: bool = False, pv_mode: str = "fp16",
+                        qk_mode: str = "int8"):
     """float64 restatement of sage_vertical_attention_v2 (sage_unified.py:550-622,
     kernel :398-496).  q [B, HQ, N, D], k/v [B, HKV, N, D] (bf16 values),
     vidx [B, HQ, T].  For query row i of block b (128 rows):
@@ -712,12 +736,21 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
     (m = the row max), P8 = e4m3(p'), V8 = e4m3(v / vs) with the per-channel
     scale vs = max|v| / 448; the vertical and window keys keep fp16 operands in
     the same units, fp16(p') and fp16(v / vs); o = (sum P V) / (sum p') * vs.
+    qk_mode='fp8' scores the rest keys as sage_vertical_attention_v2_fp8
+    (src/ops/sage_unified_fp8.py:158-311, quantiser :52-148): Q per 128-row
+    block and rest K per 64-entry block in e4m3 (per_block_fp8),
+    s = (q8 . k8) * q_scale * k_scale, everything else unchanged.
+
     Returns float64 [B, HQ, N, D]."""
     B, HQ, N, D = q.shape
     HKV = k.shape[1]
     G = HQ // HKV
     op = prefill_operands(q, k, v, sm_scale, smooth)
     q8, qsc, q16, k16, v16 = op["q8"], op["q_scale"], op["q16"], op["k16"], op["v16"]
+    quant = per_block_int8
+    if qk_mode == "fp8":
+        q8, qsc = per_block_fp8(q, op["c"], PREFILL_BLOCK_M)
+        quant = per_block_fp8
     fp8 = pv_mode == "fp8"
     if fp8:
         vs, v8, v16 = fp8_v_operands(v)              # v16 := fp16(v / vs) here
@@ -731,7 +764,7 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
             hk = h // G
             vert, rest, nv, nr = prefill_lists(vidx[b, h], N, W)
             if len(rest):
-                k8r, ksr = per_block_int8(k16[b, hk, rest], 1.0, PREFILL_BLOCK_N)
+                k8r, ksr = quant(k16[b, hk, rest], 1.0, PREFILL_BLOCK_N)
             for blk in range((N + PREFILL_BLOCK_M - 1) // PREFILL_BLOCK_M):
                 wla = window_start(blk, W)
                 rows = np.arange(blk * PREFILL_BLOCK_M, min(N, (blk + 1) * PREFILL_BLOCK_M))
@@ -741,7 +774,7 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
                     n = nr[blk]
                     if int8_rest:
                         kscale = np.repeat(ksr.astype(np.float64), PREFILL_BLOCK_N)[:n]
-                        # integer dot products, exact in float64 (|sum| < 2^22)
+                        # integer (or e4m3) dot products, exact in float64
                         s = q8[b, h, rows].astype(np.float64) @ k8r[:n].astype(np.float64).T
                         segs_s.append(s * float(qsc[b, h, blk]) * kscale[None, :])
                     else:

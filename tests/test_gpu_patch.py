@@ -176,6 +176,32 @@ def test_window_only_modes(mode):
     assert out.shape == (1, N_PROMPT + 3)
 
 
+def test_fp8_qk_prefill_switch(monkeypatch):
+    """HYBRID_ATTN_PREFILL_KERNEL=fp8 routes a D-stage mode's prefill through
+    the FP8-QK kernel (src/patch/patch_llama.py:160-190); the outputs still
+    track the dense model."""
+    from hyquant_amd.patch import create_cache_for_mode, patch_attention_forward_model
+    monkeypatch.setenv("HYBRID_ATTN_PREFILL_KERNEL", "fp8")
+    ids = _ids(seed=6)
+    dense = _model("llama")
+    model = patch_attention_forward_model(_model("llama"), mode="hybrid_full", window_size=W)
+    cache = create_cache_for_mode("hybrid_full", num_layers=2, window_size=W)
+    store, hooks = _capture(model)
+    with torch.no_grad():
+        model(ids, past_key_values=cache, use_cache=True)
+    for h in hooks:
+        h.remove()
+    dstore, dhooks = _capture(dense)
+    with torch.no_grad():
+        dense(ids)
+    for h in dhooks:
+        h.remove()
+    for i in store:
+        c = _cos(store[i], dstore[i])
+        print(f"  fp8-QK prefill layer {i}: cos {c:.5f}", flush=True)
+        assert c > 0.98, (i, c)
+
+
 def test_hf_generate_with_cache():
     """transformers' own generate() loop drives the cache (transformers 5.x API)."""
     from hyquant_amd.patch import create_cache_for_mode, patch_attention_forward_model

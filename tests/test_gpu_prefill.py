@@ -290,3 +290,35 @@ def test_unified_prefill_vs_oracle(cfg):
     ref_abs = O.unified_prefill_fp64(q, k, v, W, abs_v=True)
     _check(f"unified {cfg}", out, ref, ref_abs)
 
+
+
+FP8QK_CASES = [
+    dict(B=1, HQ=4, HKV=1, N=640, W=128, T=30, seed=41),
+    dict(B=2, HQ=8, HKV=2, N=1000, W=100, T=45, seed=42),          # ragged last block, GQA 4
+    dict(B=1, HQ=2, HKV=1, N=520, W=64, T=0, seed=43),             # no vertical lines
+]
+
+
+@pytest.mark.parametrize("cfg", FP8QK_CASES, ids=[f"fp8qk-N{c['N']}W{c['W']}T{c['T']}" for c in FP8QK_CASES])
+def test_prefill_fp8qk_vs_oracle(cfg):
+    """sage_vertical_attention_v2_fp8 (hyq_prefill_hybrid_fp8qk): e4m3 Q and
+    rest K against the float64 restatement of sage_unified_fp8.py."""
+    from hyquant_amd.sage_unified import sage_vertical_attention_v2_fp8
+    print(f"fp8qk {cfg}", flush=True)
+    rng = np.random.default_rng(cfg["seed"])
+    B, HQ, HKV, N, W, T = (cfg[x] for x in ("B", "HQ", "HKV", "N", "W", "T"))
+    q = _rand_bf16(rng, (B, HQ, N, 128))
+    k = O.bf16_round(_rand_bf16(rng, (B, HKV, N, 128), 1.5)
+                     + O.bf16_round(rng.standard_normal((1, HKV, 1, 128)).astype(np.float32)))
+    v = _rand_bf16(rng, (B, HKV, N, 128))
+    P = max(0, N - W)
+    vidx = np.stack([np.stack([rng.permutation(P)[:T] for _ in range(HQ)]) for _ in range(B)]).astype(np.int64)
+    vidx = vidx.reshape(B, HQ, T)
+    dev = torch.device("cuda")
+    out = sage_vertical_attention_v2_fp8(to_dev_bf16(q, dev), to_dev_bf16(k, dev), to_dev_bf16(v, dev),
+                                         torch.from_numpy(vidx).to(dev), window_size=W)
+    torch.cuda.synchronize()
+    out = out.float().cpu().numpy()
+    ref = O.hybrid_prefill_fp64(q, k, v, vidx, W, qk_mode="fp8")
+    ref_abs = O.hybrid_prefill_fp64(q, k, v, vidx, W, qk_mode="fp8", abs_v=True)
+    _check(f"fp8qk {cfg}", out, ref, ref_abs)

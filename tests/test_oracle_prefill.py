@@ -103,7 +103,7 @@ def test_lists_partition_and_duplicates():
     assert nv.tolist() == [sum(x < w for x in vert) for w in wla]
 
 
-def _brute_prefill(q, k, v, vidx, W):
+def _brute_prefill(q, k, v, vidx, W, qk="int8"):
     """Per-element restatement: for query i and key j <= i decide the category
     directly (window: wla(i // 128) <= j; vertical: j in the index set, once per
     occurrence; rest otherwise), score it, and take one softmax per row."""
@@ -119,7 +119,9 @@ def _brute_prefill(q, k, v, vidx, W):
             vset = set(vlist)
             rest = [j for j in range(P) if j not in vset]
             rank = {j: r for r, j in enumerate(rest)}
-            k8, ksc = O.per_block_int8(op["k16"][b, hk, rest], 1.0, 64) if rest else (None, None)
+            quant = O.per_block_fp8 if qk == "fp8" else O.per_block_int8
+            k8, ksc = quant(op["k16"][b, hk, rest], 1.0, 64) if rest else (None, None)
+            q8, qsc = O.per_block_fp8(q, op["c"], 128) if qk == "fp8" else (op["q8"], op["q_scale"])
             for i in range(N):
                 wla = max(0, 128 * (i // 128) - (W - 1)) // 64 * 64
                 s, vals = [], []
@@ -130,8 +132,8 @@ def _brute_prefill(q, k, v, vidx, W):
                         mult = vlist.count(j)
                     else:
                         r = rank[j]
-                        dot = int(np.dot(op["q8"][b, h, i].astype(np.int64), k8[r].astype(np.int64)))
-                        s.append(dot * float(op["q_scale"][b, h, i // 128]) * float(ksc[r // 64]))
+                        dot = sum(float(x) * float(y) for x, y in zip(q8[b, h, i], k8[r]))
+                        s.append(dot * float(qsc[b, h, i // 128]) * float(ksc[r // 64]))
                         vals.append(op["v16"][b, hk, j])
                         continue
                     sc = float(np.dot(op["q16"][b, h, i].astype(np.float64), op["k16"][b, hk, j].astype(np.float64)))
@@ -154,6 +156,61 @@ def test_hybrid_prefill_matches_per_element_brute_force(N, W, T):
     got = O.hybrid_prefill_fp64(q, k, v, vidx, W, sm_scale=16 ** -0.5)
     exp = _brute_prefill(q, k, v, vidx, W)
     assert np.abs(got - exp).max() < 1e-12
+
+
+def test_fp8qk_prefill_matches_per_element_brute_force():
+    """The FP8-QK variant (sage_unified_fp8.py:158-311): the same partition
+    with the rest keys scored from e4m3 Q and K, element by element."""
+    rng = np.random.default_rng(31)
+    N, W, T = 300, 64, 12
+    q = _rand_bf16(rng, (1, 2, N, 16))
+    k = _rand_bf16(rng, (1, 1, N, 16), 1.5)
+    v = _rand_bf16(rng, (1, 1, N, 16))
+    vidx = np.stack([rng.permutation(N - W)[:T] for _ in range(2)])[None]
+    got = O.hybrid_prefill_fp64(q, k, v, vidx, W, sm_scale=16 ** -0.5, qk_mode="fp8")
+    exp = _brute_prefill(q, k, v, vidx, W, qk="fp8")
+    assert np.abs(got - exp).max() < 1e-12
+
+
+def test_per_block_fp8_known_answers():
+    # amax 448 -> scale 1: the codes are the e4m3 roundings of the values themselves
+    x = np.array([[448.0, 17.0, -17.0, 0.3, 1e-4, 0.0, -448.0, 240.0]], np.float32)
+    codes, sc = O.per_block_fp8(x[None], 1.0, 2)
+    assert sc.tolist() == [[1.0]]
+    assert codes[0].tolist() == [[448.0, 16.0, -16.0, 0.3125, 0.0, 0.0, -448.0, 240.0]]
+    # an all-zero block gets scale 1 (not 0) and zero codes
+    codes, sc = O.per_block_fp8(np.zeros((1, 3, 4), np.float32), 2.0, 8)
+    assert sc.tolist() == [[1.0]] and not codes.any()
+
+
+def test_per_block_fp8_matches_rational_rederivation():
+    """Each fp32 step rounded once by exact rationals (x * sm, amax / 448,
+    x / scale), then the nearest e4m3 grid value (ties to even mantissa)."""
+    grid = _e4m3_values()
+    rng = np.random.default_rng(7)
+    x = O.bf16_round((rng.standard_normal((64, 16)) * 3).astype(np.float32))
+    sm = 0.0883883
+    codes, sc = O.per_block_fp8(x, sm, 64)
+    c = Fraction(float(np.float32(sm)))
+    xs = [to_fp32(Fraction(float(t)) * c) for t in x.ravel()]
+    scale = to_fp32(max(abs(t) for t in xs) / 448)
+    assert float(scale) == float(sc[0])
+    for t, got in zip(xs, codes.ravel()):
+        r = float(to_fp32(t / scale))
+        r = min(max(r, -448.0), 448.0)
+        a = abs(r)
+        i = int(np.searchsorted(grid, a))
+        cands = [grid[j] for j in (i - 1, i) if 0 <= j < len(grid)]
+        best = min(cands, key=lambda g: (abs(g - a), _mant_odd(g)))
+        assert got == math.copysign(best, r) or (best == 0 and got == 0)
+
+
+def _mant_odd(g):
+    """1 when the e4m3 value g has an odd mantissa (loses a round-to-even tie)."""
+    if g == 0:
+        return 0
+    e = max(math.floor(math.log2(g)), -6)
+    return int(round(g / 2.0 ** (e - 3))) & 1
 
 
 @pytest.mark.parametrize("W", [64, 300])

@@ -58,16 +58,13 @@ constexpr int PD = 128;                  // head_dim
 constexpr int BM = 128;                  // query rows per block (Q scale block)
 constexpr int BN = 64;                   // keys per tile (rest-K scale block)
 constexpr int PF_THREADS = 256;
-constexpr int KSTR8 = 144;               // LDS row stride of an int8 K tile (bytes)
-constexpr int KSTR16 = 272;              // LDS row stride of an fp16 K tile
-constexpr int VSTR = 144;                // LDS row stride of the V^T tile (64 fp16 keys + pad)
-constexpr int KBUF = BN * KSTR16;
-constexpr int VBUF = PD * VSTR;
+constexpr int RS8 = PD;                  // LDS bytes of an int8 / e4m3 tile row (K, fp8 V)
+constexpr int RS16 = 2 * PD;             // LDS bytes of an fp16 tile row (K, V)
+constexpr int TBUF = BN * RS16;          // bytes of one K or V tile buffer
 constexpr float PF_SLACK = 8.0f;
 constexpr float PF_M_INIT = -1.0e30f;
 constexpr float FP8_MAX = 448.0f;        // src/ops/sage_unified_fp8.py:44
 constexpr float S_FP8_OFFSET = 8.807f;   // vendor/sageattention/csrc/qattn/attn_utils.cuh:30 (log2 448)
-constexpr int VSTR8 = 72;                // LDS row stride of the fp8 V^T tile (64 keys + pad)
 constexpr int LIST_THREADS = 1024;
 constexpr int MAX_T = 8192;              // vertical indices per head
 constexpr int64_t MAX_P = 131072;        // prefix positions N - W per head
@@ -91,11 +88,26 @@ typedef __amdgpu_buffer_rsrc_t Rsrc;
 __device__ __forceinline__ Rsrc pf_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
-__device__ __forceinline__ u32x4 pf_ld128(Rsrc r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+// LDS DMA: 64 lanes x 16 bytes from a buffer (range checked) into 1 KiB of
+// LDS at dst (wave-uniform), lane l at dst + 16 l; no VGPR holds the data
+typedef __attribute__((address_space(3))) void* LdsPtr;
+__device__ __forceinline__ void pf_dma16(Rsrc r, uint8_t* dst, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)(dst), 16, voff, soff, 0, 0);
 }
-__device__ __forceinline__ u32x2 pf_ld64(Rsrc r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+
+// gfx950 LDS transpose reads: within each 16-lane group, lane j of
+// ds_read_b64_tr_b16 receives element (j & 3) of the 8-byte pieces that lanes
+// 4e + (j >> 2) address (e = 0..3), and lane j of ds_read_b64_tr_b8 receives
+// byte (j & 7) of the pieces that lanes 2e + (j >> 3) address (e = 0..7).
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 tr_f16x4;
+typedef __attribute__((__vector_size__(2 * sizeof(int)))) int tr_i32x2;
+__device__ __forceinline__ u32x2 lds_tr16(const uint8_t* p) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                         (__attribute__((address_space(3))) tr_f16x4*)(p)));
+}
+__device__ __forceinline__ u32x2 lds_tr8(const uint8_t* p) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                                         (__attribute__((address_space(3))) tr_i32x2*)(p)));
 }
 
 __device__ __forceinline__ int window_start(int blk, int W) {
@@ -584,8 +596,8 @@ struct TileDesc {
 // two MFMAs; Q and K use the same channel order, so the dot product is whole).
 template <bool PV8, bool QF8>
 __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_k[2][KBUF];
-    __shared__ __attribute__((aligned(16))) uint8_t s_v[2][VBUF];
+    __shared__ __attribute__((aligned(16))) uint8_t s_k[2][TBUF];
+    __shared__ __attribute__((aligned(16))) uint8_t s_v[2][TBUF];
     __shared__ float s_red[4];
 
     // XCD-aware order: consecutive items (same head, heaviest block first) land on one XCD
@@ -685,87 +697,65 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         return d;
     };
 
-    // global -> register staging of one tile (K: 2 or 4 x 16 B, V: 4 x 16 B
-    // per thread, fp8 V: 4 x 8 B); rows past a source's valid rows read zeros
-    // (their scores are masked and their P is zero)
-    u32x4 kr[4], vr[4];                    // fp8 V rows use vr[r].xy
-    const uint32_t vo_k8 = static_cast<uint32_t>((tid >> 3) * PD + 16 * (tid & 7));
-    const uint32_t vo_k16 = static_cast<uint32_t>((tid >> 4) * 2 * PD + 16 * (tid & 15));
-    const uint32_t vo_v16 = static_cast<uint32_t>(4 * (tid >> 4) * 2 * PD + 16 * (tid & 15));
-    const uint32_t vo_v8 = static_cast<uint32_t>(4 * (tid >> 4) * PD + 8 * (tid & 15));
-    auto load_tile = [&](const TileDesc& d) {
+    // Tiles go from HBM straight into LDS (LDS DMA, no register staging).
+    // Rows are stored whole, 128 B (int8 / e4m3) or 256 B (fp16), with
+    // their 16-byte chunks XOR-swizzled by row so that the reads below hit
+    // distinct banks; the swizzle is applied on the load side (each DMA lane
+    // picks the global chunk that belongs at its LDS position):
+    //   K int8 / e4m3   position = chunk ^ (row & 7)
+    //   K fp16          position = chunk ^ (row & 15)
+    //   V fp16          position = chunk ^ 2 (row & 3)
+    //   V e4m3          position = chunk ^ ((row & 3) | 4 ((row >> 4) & 1))
+    // One DMA writes 1 KiB: 8 rows of 128 B or 4 rows of 256 B; wavefront w
+    // issues DMAs q = 2w, 2w + 1 (128-B rows) or q = 4w .. 4w + 3 (256-B
+    // rows).  Rows past a source's valid rows read zeros (their scores are
+    // masked and their P is zero).
+    const uint32_t dk8 = static_cast<uint32_t>((lane >> 3) * RS8 + 16 * ((lane & 7) ^ (lane >> 3)));
+    const uint32_t dv16 = static_cast<uint32_t>((lane >> 4) * RS16 + 16 * ((lane & 15) ^ (2 * ((lane >> 4) & 3))));
+    const uint32_t dv8 = static_cast<uint32_t>((lane >> 3) * RS8 +
+                                               16 * ((lane & 7) ^ (((lane >> 3) & 3) | ((w & 1) << 2))));
+    auto issue_tile = [&](const TileDesc& d, int buf) {
         const uint32_t i0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(d.idx0));
         const uint32_t nvalid = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(d.valid));
+        uint8_t* kdst = s_k[buf];
+        uint8_t* vdst = s_v[buf];
         if (d.kind == T_REST) {
-            const Rsrc rk = pf_rsrc(a.k8r + static_cast<int64_t>(bh) * a.P * PD, nvalid * PD);
+            const Rsrc rk = pf_rsrc(a.k8r + static_cast<int64_t>(bh) * a.P * PD, nvalid * RS8);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) kr[i] = pf_ld128(rk, vo_k8, (i0 + 32 * i) * PD);
+            for (int i = 0; i < 2; ++i) {
+                const int q = 2 * w + i;
+                pf_dma16(rk, kdst + 1024 * q, dk8, i0 * RS8 + 1024 * q);
+            }
         } else {
             const uint16_t* kb = d.kind == T_VERT ? a.kv16 + static_cast<int64_t>(bh) * a.T * PD
                                                   : a.k16 + bhk * a.N * PD;
-            const Rsrc rk = pf_rsrc(kb, nvalid * 2 * PD);
+            const Rsrc rk = pf_rsrc(kb, nvalid * RS16);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) kr[i] = pf_ld128(rk, vo_k16, (i0 + 16 * i) * 2 * PD);
+            for (int i = 0; i < 4; ++i) {
+                const int q = 4 * w + i;
+                const uint32_t vo = static_cast<uint32_t>((lane >> 4) * RS16 +
+                                                          16 * ((lane & 15) ^ ((4 * i + (lane >> 4)) & 15)));
+                pf_dma16(rk, kdst + 1024 * q, vo, i0 * RS16 + 1024 * q);
+            }
         }
         if (PV8 && d.kind == T_REST) {
             const Rsrc rv = pf_rsrc(reinterpret_cast<const uint8_t*>(a.vr) + static_cast<int64_t>(bh) * a.P * PD,
-                                    nvalid * PD);
+                                    nvalid * RS8);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const u32x2 t = pf_ld64(rv, vo_v8, (i0 + r) * PD);
-                vr[r][0] = t[0];
-                vr[r][1] = t[1];
+            for (int i = 0; i < 2; ++i) {
+                const int q = 2 * w + i;
+                pf_dma16(rv, vdst + 1024 * q, dv8, i0 * RS8 + 1024 * q);
             }
             return;
         }
         const uint16_t* vb = d.kind == T_REST ? a.vr + static_cast<int64_t>(bh) * a.P * PD
                              : d.kind == T_VERT ? a.vv16 + static_cast<int64_t>(bh) * a.T * PD
                                                 : a.v16 + bhk * a.N * PD;
-        const Rsrc rv = pf_rsrc(vb, nvalid * 2 * PD);
+        const Rsrc rv = pf_rsrc(vb, nvalid * RS16);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) vr[r] = pf_ld128(rv, vo_v16, (i0 + r) * 2 * PD);
-    };
-    auto store_tile = [&](const TileDesc& d, int buf) {
-        uint8_t* kb = s_k[buf];
-        if (d.kind == T_REST) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                *reinterpret_cast<u32x4*>(kb + ((tid >> 3) + 32 * i) * KSTR8 + 16 * (tid & 7)) = kr[i];
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<u32x4*>(kb + ((tid >> 4) + 16 * i) * KSTR16 + 16 * (tid & 15)) = kr[i];
-        }
-        // V^T with the key permutation: keys 4kq..4kq+3 land at pos..pos+3
-        const int kq = tid >> 4, co = tid & 15;
-        const int kb4 = kq >> 2, gg = kq & 3;
-        const int pos = 32 * (kb4 >> 1) + 8 * gg + 4 * (kb4 & 1);
-        if (PV8 && d.kind == T_REST) {
-            // fp8: channel row 8co + e gets byte e of the four keys' rows;
-            // 16-byte units swizzled by row: unit ^ ((row >> 4) & 3)
-            uint8_t* vb8 = s_v[buf] + ((((pos >> 4) ^ ((co >> 1) & 3)) << 4) | (pos & 15));
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int dd = e >> 2, by = e & 3;
-                const uint32_t sel = static_cast<uint32_t>(by) | (static_cast<uint32_t>(4 + by) << 8) | 0x0c0c0000u;
-                const uint32_t t01 = __builtin_amdgcn_perm(vr[1][dd], vr[0][dd], sel);
-                const uint32_t t23 = __builtin_amdgcn_perm(vr[3][dd], vr[2][dd], sel);
-                *reinterpret_cast<uint32_t*>(vb8 + (8 * co + e) * VSTR8) = t01 | (t23 << 16);
-            }
-            return;
-        }
-        // 16-byte column units are swizzled by row: unit ^ (row >> 4), which
-        // spreads the 16 channel groups of a write over the banks
-        const int col = 2 * pos;
-        const int vcol = (((col >> 4) ^ ((co >> 1) & 7)) << 4) | (col & 15);
-        uint8_t* vb = s_v[buf] + vcol;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-            const int dd = e >> 1;
-            const u32x2 t2 = {__builtin_amdgcn_perm(vr[1][dd], vr[0][dd], sel),
-                              __builtin_amdgcn_perm(vr[3][dd], vr[2][dd], sel)};
-            *reinterpret_cast<u32x2*>(vb + (8 * co + e) * VSTR) = t2;
+        for (int i = 0; i < 4; ++i) {
+            const int q = 4 * w + i;
+            pf_dma16(rv, vdst + 1024 * q, dv16, i0 * RS16 + 1024 * q);
         }
     };
 
@@ -783,15 +773,17 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         for (int cb = 0; cb < 8; ++cb) acc[sb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     TileDesc cur = describe(0);
-    load_tile(cur);
+    issue_tile(cur, 0);
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
-        store_tile(cur, buf);
+        // this wavefront's DMAs of tile t have landed; the barrier extends that
+        // to the workgroup and frees buffer buf ^ 1 (read by tile t - 1)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         const TileDesc d = cur;
         if (t + 1 < ntiles) {
             cur = describe(t + 1);
-            load_tile(cur);
+            issue_tile(cur, buf ^ 1);
         }
         const uint8_t* kb = s_k[buf];
         const uint8_t* vb = s_v[buf];
@@ -802,9 +794,9 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         if (d.kind == T_REST && QF8) {
 #pragma unroll
             for (int kbk = 0; kbk < 4; ++kbk) {
-                const uint8_t* row = kb + (16 * kbk + c16) * KSTR8 + 16 * g;
-                const i32x4 a0 = *reinterpret_cast<const i32x4*>(row);
-                const i32x4 a1 = *reinterpret_cast<const i32x4*>(row + 64);
+                const uint8_t* row = kb + (16 * kbk + c16) * RS8;
+                const i32x4 a0 = *reinterpret_cast<const i32x4*>(row + 16 * (g ^ (c16 & 7)));
+                const i32x4 a1 = *reinterpret_cast<const i32x4*>(row + 16 * ((4 + g) ^ (c16 & 7)));
                 const i32x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
 #pragma unroll
                 for (int sb = 0; sb < 2; ++sb) {
@@ -820,9 +812,9 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             i32x4 si[2][4];
 #pragma unroll
             for (int kbk = 0; kbk < 4; ++kbk) {
-                const uint8_t* row = kb + (16 * kbk + c16) * KSTR8 + 16 * g;
-                const i32x4 a0 = *reinterpret_cast<const i32x4*>(row);
-                const i32x4 a1 = *reinterpret_cast<const i32x4*>(row + 64);
+                const uint8_t* row = kb + (16 * kbk + c16) * RS8;
+                const i32x4 a0 = *reinterpret_cast<const i32x4*>(row + 16 * (g ^ (c16 & 7)));
+                const i32x4 a1 = *reinterpret_cast<const i32x4*>(row + 16 * ((4 + g) ^ (c16 & 7)));
 #pragma unroll
                 for (int sb = 0; sb < 2; ++sb) {
                     si[sb][kbk] = mfma_i8(a0, q8[sb][0], i32x4{0, 0, 0, 0});
@@ -844,10 +836,11 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                 for (int kbk = 0; kbk < 4; ++kbk) sf[sb][kbk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int kbk = 0; kbk < 4; ++kbk) {
-                const uint8_t* row = kb + (16 * kbk + c16) * KSTR16 + 32 * g;
+                const uint8_t* row = kb + (16 * kbk + c16) * RS16;
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
-                    const f16x8 av = *reinterpret_cast<const f16x8*>(row + 128 * (m >> 1) + 16 * (m & 1));
+                    const int chunk = 8 * (m >> 1) + 2 * g + (m & 1);          // channels 8 chunk .. + 7
+                    const f16x8 av = *reinterpret_cast<const f16x8*>(row + 16 * (chunk ^ c16));
 #pragma unroll
                     for (int sb = 0; sb < 2; ++sb) sf[sb][kbk] = mfma_f16(av, qh[sb][m], sf[sb][kbk]);
                 }
@@ -939,8 +932,11 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             for (int cb = 0; cb < 8; ++cb) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const u32x2 av = *reinterpret_cast<const u32x2*>(vb + (16 * cb + c16) * VSTR8 +
-                                                                     16 * ((2 * j + (g >> 1)) ^ (cb & 3)) + 8 * (g & 1));
+                    // slot e = c16 >> 1 of lane-row g: key 32j + 16 (e >> 2) + 4g + (e & 3),
+                    // whose swizzle is e; bytes 16cb + 8 (c16 & 1) of its row
+                    const int e = c16 >> 1;
+                    const u32x2 av = lds_tr8(vb + (32 * j + 16 * (e >> 2) + 4 * g + (e & 3)) * RS8 +
+                                             16 * (cb ^ e) + 8 * (c16 & 1));
 #pragma unroll
                     for (int sb = 0; sb < 2; ++sb) acc[sb][cb] = mfma_fp8(av, u32x2{pw[sb][j][0], pw[sb][j][1]}, acc[sb][cb]);
                 }
@@ -950,7 +946,13 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             for (int cb = 0; cb < 8; ++cb) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const f16x8 av = *reinterpret_cast<const f16x8*>(vb + (16 * cb + c16) * VSTR + 16 * ((4 * j + g) ^ cb));
+                    // slots 4h .. 4h + 3 of lane-row g: keys 32j + 16h + 4g + (0..3);
+                    // this lane addresses key 32j + 16h + 4g + (c16 >> 2), channels
+                    // 16cb + 4 (c16 & 3) .. + 3 (chunk 2cb + ((c16 & 3) >> 1))
+                    const int chunk = (2 * cb + ((c16 & 3) >> 1)) ^ (2 * ((c16 >> 2) & 3));
+                    const uint8_t* p0 = vb + (32 * j + 4 * g + (c16 >> 2)) * RS16 + 16 * chunk + 8 * (c16 & 1);
+                    const u32x2 lo = lds_tr16(p0), hi = lds_tr16(p0 + 16 * RS16);
+                    const f16x8 av = __builtin_bit_cast(f16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
 #pragma unroll
                     for (int sb = 0; sb < 2; ++sb) acc[sb][cb] = mfma_f16(av, __builtin_bit_cast(f16x8, pw[sb][j]), acc[sb][cb]);
                 }

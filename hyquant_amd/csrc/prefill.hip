@@ -99,16 +99,37 @@ __device__ __forceinline__ void pf_dma16(Rsrc r, uint8_t* dst, uint32_t voff, ui
 // ds_read_b64_tr_b16 receives element (j & 3) of the 8-byte pieces that lanes
 // 4e + (j >> 2) address (e = 0..3), and lane j of ds_read_b64_tr_b8 receives
 // byte (j & 7) of the pieces that lanes 2e + (j >> 3) address (e = 0..7).
+// They are issued as inline asm: the compiler cannot tell which LDS object
+// the intrinsic forms read, so it drains every in-flight LDS DMA (the next
+// tile's) before them.  The asm reads are ordered after the step's barrier
+// (volatile asm), and lds_wait ties their results to an explicit lgkmcnt
+// wait before any use.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)(p)));
+}
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_tr16(uint32_t addr) {
+    u32x2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+    return r;
+}
+// The intrinsic forms, for the kernel with fp8 P.V: its register budget has
+// no room for the pipelined asm reads, and there the compiler's drain of the
+// next tile's DMAs costs less than spilling.
 typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 tr_f16x4;
 typedef __attribute__((__vector_size__(2 * sizeof(int)))) int tr_i32x2;
-__device__ __forceinline__ u32x2 lds_tr16(const uint8_t* p) {
+__device__ __forceinline__ u32x2 lds_tr16_i(const uint8_t* p) {
     return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
                                          (__attribute__((address_space(3))) tr_f16x4*)(p)));
 }
-__device__ __forceinline__ u32x2 lds_tr8(const uint8_t* p) {
+__device__ __forceinline__ u32x2 lds_tr8_i(const uint8_t* p) {
     return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
                                          (__attribute__((address_space(3))) tr_i32x2*)(p)));
 }
+__device__ __forceinline__ void lds_wait(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+
 
 __device__ __forceinline__ int window_start(int blk, int W) {
     const int x = BM * blk - (W - 1);
@@ -581,7 +602,7 @@ struct TileDesc {
     int kind;
     int idx0;      // first list entry (rest / vert) or first key (window)
     int valid;     // rest / vert: entries of the list below wla; window: end key (exclusive)
-    float sc;      // rest: q_scale * k_scale
+    float sc;      // rest: the 64-entry block's k_scale (times q_scale at use)
 };
 
 // PV8: fp8 PV on the rest tiles (P' = exp2(s - m + 8.807) as e4m3 against
@@ -596,8 +617,13 @@ struct TileDesc {
 // two MFMAs; Q and K use the same channel order, so the dot product is whole).
 template <bool PV8, bool QF8>
 __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_k[2][TBUF];
-    __shared__ __attribute__((aligned(16))) uint8_t s_v[2][TBUF];
+    // two tile buffers as four distinct LDS objects: the compiler then knows a
+    // DMA into one buffer cannot alias reads of the other and does not drain
+    // the next tile's DMAs before computing the current one
+    __shared__ __attribute__((aligned(16))) uint8_t s_k0[TBUF];
+    __shared__ __attribute__((aligned(16))) uint8_t s_k1[TBUF];
+    __shared__ __attribute__((aligned(16))) uint8_t s_v0[TBUF];
+    __shared__ __attribute__((aligned(16))) uint8_t s_v1[TBUF];
     __shared__ float s_red[4];
 
     // XCD-aware order: consecutive items (same head, heaviest block first) land on one XCD
@@ -688,7 +714,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     auto describe = [&](int t) {
         TileDesc d;
         if (t < nrt) {
-            d.kind = T_REST; d.idx0 = BN * t; d.valid = nr_b; d.sc = q_scale * ksc_row[t];
+            d.kind = T_REST; d.idx0 = BN * t; d.valid = nr_b; d.sc = ksc_row[t];    // used a tile later
         } else if (t < nrt + nvt) {
             d.kind = T_VERT; d.idx0 = BN * (t - nrt); d.valid = nv_b; d.sc = 1.0f;
         } else {
@@ -714,11 +740,9 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     const uint32_t dv16 = static_cast<uint32_t>((lane >> 4) * RS16 + 16 * ((lane & 15) ^ (2 * ((lane >> 4) & 3))));
     const uint32_t dv8 = static_cast<uint32_t>((lane >> 3) * RS8 +
                                                16 * ((lane & 7) ^ (((lane >> 3) & 3) | ((w & 1) << 2))));
-    auto issue_tile = [&](const TileDesc& d, int buf) {
+    auto issue_tile = [&](const TileDesc& d, uint8_t* kdst, uint8_t* vdst) {
         const uint32_t i0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(d.idx0));
         const uint32_t nvalid = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(d.valid));
-        uint8_t* kdst = s_k[buf];
-        uint8_t* vdst = s_v[buf];
         if (d.kind == T_REST) {
             const Rsrc rk = pf_rsrc(a.k8r + static_cast<int64_t>(bh) * a.P * PD, nvalid * RS8);
 #pragma unroll
@@ -773,20 +797,20 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         for (int cb = 0; cb < 8; ++cb) acc[sb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     TileDesc cur = describe(0);
-    issue_tile(cur, 0);
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
+    issue_tile(cur, s_k0, s_v0);
+    // one tile: its DMAs (into kb / vb) were issued a tile earlier; the next
+    // tile's go into knext / vnext
+    auto step = [&](int t, const uint8_t* kb, const uint8_t* vb, uint8_t* knext, uint8_t* vnext)
+                    __attribute__((always_inline)) {
         // this wavefront's DMAs of tile t have landed; the barrier extends that
-        // to the workgroup and frees buffer buf ^ 1 (read by tile t - 1)
+        // to the workgroup and frees the other buffer (read by tile t - 1)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         const TileDesc d = cur;
         if (t + 1 < ntiles) {
             cur = describe(t + 1);
-            issue_tile(cur, buf ^ 1);
+            issue_tile(cur, knext, vnext);
         }
-        const uint8_t* kb = s_k[buf];
-        const uint8_t* vb = s_v[buf];
 
         // ---- S^T = K . Q^T --------------------------------------------------
         float s[2][4][4];
@@ -877,7 +901,8 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         // p = exp2(s_int * (q_scale k_scale) - m) in one fma.  A zero scale
         // means all-zero codes on one side, so every such score is 0 and the
         // scale 1 gives the same result (and keeps -inf * scale = -inf).
-        const float ssc = d.kind == T_REST && d.sc > 0.0f ? d.sc : 1.0f;
+        const float qks = q_scale * d.sc;
+        const float ssc = d.kind == T_REST && qks > 0.0f ? qks : 1.0f;
         u32x4 pw[2][2];                    // P^T operands: fp16 x 8, or fp8 x 8 in .xy
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
@@ -927,34 +952,67 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         }
 
         // ---- O^T += V^T . P^T -------------------------------------------------
-        if (PV8 && d.kind == T_REST) {
+        // Lane addressing of the transpose reads: fp8 slot e = c16 >> 1 of
+        // lane-row g is key 32j + 16 (e >> 2) + 4g + (e & 3), whose swizzle
+        // is e, bytes 16cb + 8 (c16 & 1) of its row; fp16 slots 4h .. 4h + 3
+        // are keys 32j + 16h + 4g + (0..3), this lane addressing key
+        // 32j + 16h + 4g + (c16 >> 2), channels 16cb + 4 (c16 & 3) .. + 3
+        // (chunk 2cb + ((c16 & 3) >> 1), swizzled by 2 ((c16 >> 2) & 3)).
+        if constexpr (PV8) {
+            if (d.kind == T_REST) {
+                const int e = c16 >> 1;
+                const uint8_t* b8 = vb + (16 * (e >> 2) + 4 * g + (e & 3)) * RS8 + 8 * (c16 & 1);
 #pragma unroll
-            for (int cb = 0; cb < 8; ++cb) {
+                for (int cb = 0; cb < 8; ++cb) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    // slot e = c16 >> 1 of lane-row g: key 32j + 16 (e >> 2) + 4g + (e & 3),
-                    // whose swizzle is e; bytes 16cb + 8 (c16 & 1) of its row
-                    const int e = c16 >> 1;
-                    const u32x2 av = lds_tr8(vb + (32 * j + 16 * (e >> 2) + 4 * g + (e & 3)) * RS8 +
-                                             16 * (cb ^ e) + 8 * (c16 & 1));
+                    for (int j = 0; j < 2; ++j) {
+                        const u32x2 av = lds_tr8_i(b8 + 32 * j * RS8 + 16 * (cb ^ e));
 #pragma unroll
-                    for (int sb = 0; sb < 2; ++sb) acc[sb][cb] = mfma_fp8(av, u32x2{pw[sb][j][0], pw[sb][j][1]}, acc[sb][cb]);
+                        for (int sb = 0; sb < 2; ++sb)
+                            acc[sb][cb] = mfma_fp8(av, u32x2{pw[sb][j][0], pw[sb][j][1]}, acc[sb][cb]);
+                    }
+                }
+            } else {
+                const uint8_t* b16 = vb + (4 * g + (c16 >> 2)) * RS16 + 8 * (c16 & 1);
+#pragma unroll
+                for (int cb = 0; cb < 8; ++cb) {
+                    const int chunk = (2 * cb + ((c16 & 3) >> 1)) ^ (2 * ((c16 >> 2) & 3));
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const uint8_t* p0 = b16 + 32 * j * RS16 + 16 * chunk;
+                        const u32x2 lo = lds_tr16_i(p0), hi = lds_tr16_i(p0 + 16 * RS16);
+                        const f16x8 av = __builtin_bit_cast(f16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+#pragma unroll
+                        for (int sb = 0; sb < 2; ++sb)
+                            acc[sb][cb] = mfma_f16(av, __builtin_bit_cast(f16x8, pw[sb][j]), acc[sb][cb]);
+                    }
                 }
             }
         } else {
+            // asm reads, the reads of channel block cb + 1 in flight during the
+            // MFMAs of cb
+            const uint32_t a16 = lds_addr(vb + (4 * g + (c16 >> 2)) * RS16 + 8 * (c16 & 1));
+            u32x2 v16[2][2][2];            // [stage][j][h]
+            auto rd16 = [&](int cb, int st) {
+                const uint32_t ad = a16 + 16 * ((2 * cb + ((c16 & 3) >> 1)) ^ (2 * ((c16 >> 2) & 3)));
+                v16[st][0][0] = lds_tr16<0>(ad);
+                v16[st][0][1] = lds_tr16<16 * RS16>(ad);
+                v16[st][1][0] = lds_tr16<32 * RS16>(ad);
+                v16[st][1][1] = lds_tr16<48 * RS16>(ad);
+            };
+            rd16(0, 0);
 #pragma unroll
             for (int cb = 0; cb < 8; ++cb) {
+                const int st = cb & 1;
+                lds_wait(v16[st][0][0], v16[st][0][1], v16[st][1][0], v16[st][1][1]);
+                if (cb + 1 < 8) rd16(cb + 1, st ^ 1);
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    // slots 4h .. 4h + 3 of lane-row g: keys 32j + 16h + 4g + (0..3);
-                    // this lane addresses key 32j + 16h + 4g + (c16 >> 2), channels
-                    // 16cb + 4 (c16 & 3) .. + 3 (chunk 2cb + ((c16 & 3) >> 1))
-                    const int chunk = (2 * cb + ((c16 & 3) >> 1)) ^ (2 * ((c16 >> 2) & 3));
-                    const uint8_t* p0 = vb + (32 * j + 4 * g + (c16 >> 2)) * RS16 + 16 * chunk + 8 * (c16 & 1);
-                    const u32x2 lo = lds_tr16(p0), hi = lds_tr16(p0 + 16 * RS16);
-                    const f16x8 av = __builtin_bit_cast(f16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                    const f16x8 av = __builtin_bit_cast(f16x8, u32x4{v16[st][j][0][0], v16[st][j][0][1],
+                                                                     v16[st][j][1][0], v16[st][j][1][1]});
 #pragma unroll
-                    for (int sb = 0; sb < 2; ++sb) acc[sb][cb] = mfma_f16(av, __builtin_bit_cast(f16x8, pw[sb][j]), acc[sb][cb]);
+                    for (int sb = 0; sb < 2; ++sb)
+                        acc[sb][cb] = mfma_f16(av, __builtin_bit_cast(f16x8, pw[sb][j]), acc[sb][cb]);
                 }
             }
         }
@@ -965,6 +1023,20 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
 #pragma unroll
                 for (int sb = 0; sb < 2; ++sb)
                     lsum[sb] = mfma_f16(__builtin_bit_cast(f16x8, onew), __builtin_bit_cast(f16x8, pw[sb][j]), lsum[sb]);
+        }
+    };
+    if constexpr (PV8) {
+        // one copy of the step (the register budget of this kernel has no room
+        // for two); buffers chosen at run time
+        for (int t = 0; t < ntiles; ++t) {
+            const bool odd = t & 1;
+            step(t, odd ? s_k1 : s_k0, odd ? s_v1 : s_v0, odd ? s_k0 : s_k1, odd ? s_v0 : s_v1);
+        }
+    } else {
+        for (int t = 0; t < ntiles; t += 2) {  // unrolled by two: each step's buffers are fixed objects
+            step(t, s_k0, s_v0, s_k1, s_v1);
+            if (t + 1 >= ntiles) break;
+            step(t + 1, s_k1, s_v1, s_k0, s_v0);
         }
     }
 

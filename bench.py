@@ -218,11 +218,15 @@ def time_calls(fn, warmup=2, iters=5):
 
 
 def bench_prefill(dev):
-    """Config 4: hybrid prefill, B=1, 32q/8kv, d128, causal, W=128, rho=5%.
-    FLOPs counted as 2*B*H_Q*N^2*D (QK and PV over the causal half).  MFMA
-    utilisation = achieved / the peak of the dtype mix: QK on int8 and PV on
-    fp16 (or fp8), each half of the FLOPs."""
-    from hyquant_amd.sage_unified import sage_vertical_attention_v2
+    """Config 4: hybrid prefill, B=1, 32q/8kv, d128, causal, W=128, rho=5%,
+    with int8 or e4m3 QK on the rest tiles and fp16 or e4m3 P.V, and the
+    window-only kernel (sage_w).  Each timing is the whole operator (K
+    statistics, conversion, lists, gather and the attention kernel).  FLOPs
+    counted as 2*B*H_Q*N^2*D (QK and PV over the causal half).  MFMA
+    utilisation = achieved / the peak of the dtype mix, each of QK and PV half
+    of the FLOPs."""
+    from hyquant_amd.sage_unified import (sage_unified_attention, sage_vertical_attention_v2,
+                                          sage_vertical_attention_v2_fp8)
     from hyquant_amd.vertical import compute_vertical_indices
     g = torch.Generator(device=dev).manual_seed(4)
     rows = []
@@ -234,13 +238,23 @@ def bench_prefill(dev):
         v = torch.randn(B, HKV, N, D, generator=g, device=dev).to(torch.bfloat16)
         vidx = compute_vertical_indices(q, k, W, 0.05, kv_repeat=HQ // HKV)
         flops = 2.0 * B * HQ * N * N * D
-        for mode, pv_peak in (("fp16", PEAK_FP16), ("fp8", PEAK_FP8)):
-            ms = time_calls(lambda: sage_vertical_attention_v2(q, k, v, vidx, window_size=W, pv_mode=mode))
+        variants = (
+            ("hybrid", "int8", "fp16", PEAK_INT8, PEAK_FP16,
+             lambda: sage_vertical_attention_v2(q, k, v, vidx, window_size=W)),
+            ("hybrid", "int8", "fp8", PEAK_INT8, PEAK_FP8,
+             lambda: sage_vertical_attention_v2(q, k, v, vidx, window_size=W, pv_mode="fp8")),
+            ("hybrid", "fp8", "fp16", PEAK_FP8, PEAK_FP16,
+             lambda: sage_vertical_attention_v2_fp8(q, k, v, vidx, window_size=W)),
+            ("window_only", "int8", "fp16", PEAK_INT8, PEAK_FP16,
+             lambda: sage_unified_attention(q, k, v, window_size=W)),
+        )
+        for kind, qk, pv, qk_peak, pv_peak, fn in variants:
+            ms = time_calls(fn)
             tf = flops / (ms * 1e-3) / 1e12
-            peak = 2.0 / (1.0 / PEAK_INT8 + 1.0 / pv_peak)
-            rows.append({"seq_len": N, "pv": mode, "ms": round(ms, 3), "tflops": round(tf, 1),
-                         "mfma_peak_tflops": round(peak, 1), "mfma_util": round(tf / peak, 4),
-                         "n_vertical": int(vidx.shape[-1])})
+            peak = 2.0 / (1.0 / qk_peak + 1.0 / pv_peak)
+            rows.append({"seq_len": N, "kernel": kind, "qk": qk, "pv": pv, "ms": round(ms, 3),
+                         "tflops": round(tf, 1), "mfma_peak_tflops": round(peak, 1),
+                         "mfma_util": round(tf / peak, 4), "n_vertical": int(vidx.shape[-1]) if kind == "hybrid" else 0})
             print(f"# prefill {rows[-1]}", file=sys.stderr, flush=True)
         del q, k, v, vidx
         torch.cuda.empty_cache()

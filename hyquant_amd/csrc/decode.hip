@@ -8,14 +8,14 @@
 // per-token V scale, P' = bf16(p * s_v), before P' . v_code (F8).
 //
 // One launch per step.  A workgroup of 4 wavefronts owns one piece of one KV
-// head (all G query heads of the GQA group ride along as MFMA columns).  A
-// head's keys are laid end to end as schedule units, int4 groups of 32
-// tokens and then bf16 units of 8 tokens of each segment, and cut into
-// `nwg` pieces of equal bytes (the host picks the cut points), so every
-// workgroup of the grid streams the same amount whatever mix of segments its
-// piece holds, and the grid is sized to whole rounds of the resident
-// workgroup slots: no round ends with a few long workgroups alone.  In a
-// piece:
+// head (all G query heads of the GQA group ride along as MFMA columns); the
+// grid is (KV heads, pieces per head).  A head's keys are laid end to end as
+// schedule units, int4 groups of 32 tokens and then bf16 units of 8 tokens
+// of each segment, and the host cuts them into `nwg` pieces, each inside one
+// segment and of about equal bytes within it (make_plan); the cut points
+// travel in the kernel arguments.  With many KV heads the pieces are sized
+// so that the grid is about 1.25 rounds of the resident workgroup slots.  In
+// a piece:
 //   its int4 tokens are walked in 32-token groups (wavefront w takes groups
 //     w, w+4, ...) through a three-deep register ring, so two groups' loads
 //     are in flight while one is computed;

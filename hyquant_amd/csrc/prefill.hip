@@ -31,18 +31,22 @@
 // prefill_main_kernel: 4 wavefronts, wavefront w owns query rows 32w..32w+31
 // of the block as two 16-row sub-blocks (sb).  Q is quantised in the kernel
 // (the workgroup is exactly one 128-row scale block) and kept in registers
-// as MFMA B operands.  Keys stream through LDS in 64-key tiles, double
-// buffered, one barrier per tile; the next tile's global loads are in flight
-// while the current one is computed.  Per tile and wavefront:
-//   S^T = K . Q^T   rest tiles: v_mfma_i32_16x16x64_i8 (16 per tile),
+// as MFMA B operands.  Keys stream in 64-key tiles straight from HBM into
+// LDS (buffer loads to LDS, rows XOR-swizzled by 16-byte chunk), double
+// buffered, one barrier per tile; the next tile's loads are issued right
+// after that barrier and land while the current tile is computed.  Per tile
+// and wavefront:
+//   S^T = K . Q^T   rest tiles: v_mfma_i32_16x16x64_i8 (16 per tile), or
+//                   with FP8 QK v_mfma_scale_f32_16x16x128_f8f6f4 (8);
 //                   vert/window tiles: v_mfma_f32_16x16x32_f16 (32 per tile);
 //                   output lane (c, g) holds keys 16kb + 4g + r of query c.
 //   softmax         lazy running max (raised only when a tile exceeds it by
 //                   more than 8 in log2 units), p = exp2(s - m).
-//   O^T = V^T . P^T v_mfma_f32_16x16x32_f16 (32 per tile); V is transposed
-//                   into LDS with the key permutation
-//                   pos(16kb + 4g + r) = 32(kb/2) + 8g + 4(kb%2) + r, so the
-//                   eight keys whose p a lane holds are one 16-byte LDS read.
+//   O^T = V^T . P^T v_mfma_f32_16x16x32_f16 (32 per tile) with the V^T
+//                   operand read from the row-major V tile by LDS transpose
+//                   reads (ds_read_b64_tr_b16), and the row sums of P from
+//                   one more MFMA against an all-ones operand; fp8 P.V uses
+//                   v_mfma_f32_16x16x32_fp8_fp8 and ds_read_b64_tr_b8.
 // Accumulation is fp32 throughout (the reference accumulates each 64-key
 // P.V product in fp16).
 #include "hyq_common.h"

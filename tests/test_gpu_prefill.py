@@ -267,6 +267,7 @@ UNIFIED_CASES = [
     dict(B=1, HQ=4, HKV=1, N=700, W=128, seed=23),                # sage_w
     dict(B=1, HQ=2, HKV=1, N=520, W=100, seed=24),                # window not a multiple of 64
     dict(B=1, HQ=2, HKV=2, N=129, W=0, seed=25),                  # one full block and one row
+    dict(B=1, HQ=4, HKV=2, N=300, W=512, seed=26),                # window >= N: fp16 everywhere
 ]
 
 

@@ -19,6 +19,7 @@ from .sage_unified import (  # noqa: F401
     sage_vertical_attention_v2_fp8,
 )
 from .vertical import compute_vertical_indices  # noqa: F401
+from .cache_io import load_cache, save_cache  # noqa: F401
 
 __all__ = [
     "GROUP_SIZE",
@@ -32,4 +33,6 @@ __all__ = [
     "sage_vertical_attention_v2",
     "sage_unified_attention",
     "sage_vertical_attention_v2_fp8",
+    "save_cache",
+    "load_cache",
 ]

@@ -299,6 +299,18 @@ class DStageKVCache(_HF_Cache):
     def seen_tokens(self) -> int:
         return self._seen_tokens
 
+    def save(self, path: str) -> None:
+        """Write the cache (all four segments of every layer) to a safetensors
+        file; see hyquant_amd.cache_io for the format."""
+        from .cache_io import save_cache
+        save_cache(self, path)
+
+    @classmethod
+    def load(cls, path: str, device=None) -> "DStageKVCache":
+        """Read a file written by save() onto `device` (default: the current GPU)."""
+        from .cache_io import load_cache
+        return load_cache(path, device)
+
     def batch_repeat_interleave(self, repeats: int):
         raise NotImplementedError("DStageKVCache does not support beam search yet.")
 

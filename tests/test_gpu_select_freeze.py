@@ -154,3 +154,43 @@ def test_cache_short_prompt_no_prefix():
     q = to_dev_bf16(inp.q_dec, "cuda").reshape(1, 8, 1, 128)
     out = layer.decode_attention(q, 4).reshape(-1, 128).float().cpu().numpy()
     assert float(np.max(np.abs(out - O.decode_fp64_state(inp.q_dec, st, 4)))) <= 2e-3
+
+
+@pytest.mark.parametrize("kv", [(4, 4), (4, 2)])
+def test_cache_save_load_resumes_bit_identically(tmp_path, kv):
+    """A frozen cache written to disk and read back decodes exactly like the
+    original, before and after the staging ring flushes into the prefix."""
+    from hyquant_amd.d_stage_kv_cache import DStageKVCache
+    print(f"cache save/load K{kv[0]}V{kv[1]}", flush=True)
+    inp = O.make_decode_inputs(B=1, HQ=32, HKV=8, N=1024, W=128, S=37, seed=14)
+    G = inp.HQ // inp.HKV
+    cache = DStageKVCache(num_layers=2, k_bits=kv[0], v_bits_fn=lambda i: kv[1], window_size=inp.W,
+                          top_ratio=inp.rho)
+    kd, vd = to_dev_bf16(inp.keys, "cuda"), to_dev_bf16(inp.values, "cuda")
+    layer = cache.get_layer(0)
+    cache.update(kd, vd, 0)
+    layer.save_query_tail(to_dev_bf16(inp.query_tail, "cuda"))
+    layer.freeze(kv_repeat=G)
+    cache.update(to_dev_bf16(inp.k_new, "cuda"), to_dev_bf16(inp.v_new, "cuda"), 0)
+    cache.update(kd[:, :, :50], vd[:, :, :50], 1)              # layer 1 still in prefill
+    path = str(tmp_path / "cache.safetensors")
+    cache.save(path)
+    back = DStageKVCache.load(path)
+    assert back.get_layer(1).phase == "prefill" and torch.equal(back.get_layer(1)._keys, kd[:, :, :50])
+    q = to_dev_bf16(inp.q_dec, "cuda").reshape(1, inp.HQ, 1, 128)
+    a = cache.get_layer(0).decode_attention(q, G)
+    b = back.get_layer(0).decode_attention(q, G)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    rng = np.random.default_rng(4)
+    ek = to_dev_bf16(_rand_bf16(rng, (1, inp.HKV, 100, 128), 1.4), "cuda")
+    ev = to_dev_bf16(_rand_bf16(rng, (1, inp.HKV, 100, 128)), "cuda")
+    for c in (cache, back):                                  # 37 + 100 tokens: one flush
+        for i in range(100):
+            c.update(ek[:, :, i:i + 1], ev[:, :, i:i + 1], 0)
+    la, lb = cache.get_layer(0), back.get_layer(0)
+    assert la._kstore.n == lb._kstore.n and la._staging_ptr == lb._staging_ptr == 9
+    assert torch.equal(la.k_quant_packed, lb.k_quant_packed) and torch.equal(la.v_scale, lb.v_scale)
+    a = la.decode_attention(q, G)
+    b = lb.decode_attention(q, G)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert back.get_seq_length(0) == cache.get_seq_length(0) == inp.N + 37 + 100

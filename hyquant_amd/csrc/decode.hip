@@ -725,43 +725,46 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         const float corr = v_offset<VB>() * st.ones[0];
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) st.acc[nb] -= corr;
-    }
-
-    // ---------------- bf16 parts: tiles wave, wave+WAVES, ... of each segment ----------------
-    const bf16x8 qb[4] = {__builtin_bit_cast(bf16x8, qraw[0]), __builtin_bit_cast(bf16x8, qraw[1]),
-                          __builtin_bit_cast(bf16x8, qraw[2]), __builtin_bit_cast(bf16x8, qraw[3])};
-    // segment bounds in units: [nqg, b1), [b1, b2), [b2, end of head)
-    const int b1 = nqg + su0, b2 = b1 + su1;
-    for (int seg = 0; seg < 3; ++seg) {
-        const int sb = seg == 0 ? nqg : seg == 1 ? b1 : b2;
-        const int ua = max(u0, sb), ub = min(u1, seg == 0 ? b1 : seg == 1 ? b2 : u1);
-        if (ua >= ub) continue;
-        const int lo = (ua - sb) * BUNIT;
-        int seg_len = seg == 0 ? sn0 : seg == 1 ? sn1 : sn2;
-        if (seg == 0 && len_s0 != nullptr) seg_len = min(seg_len, max(0, len_s0[head]));
-        const int n = max(0, min((ub - ua) * BUNIT, seg_len - lo));     // 0: past a ragged head's end
-        const uint16_t* const skp = seg == 0 ? sk0 : seg == 1 ? sk1 : sk2;
-        const uint16_t* const svp = seg == 0 ? sv0 : seg == 1 ? sv1 : sv2;
-        const int32_t skb = seg == 0 ? skb0 : seg == 1 ? skb1 : skb2;
-        const int32_t svb = seg == 0 ? svb0 : seg == 1 ? svb1 : svb2;
-        const uint16_t* kbase = skp + static_cast<int64_t>(head) * skb + static_cast<int64_t>(lo) * BROW;
-        const uint16_t* vbase = svp + static_cast<int64_t>(head) * svb + static_cast<int64_t>(lo) * BROW;
-        const uint32_t nbytes = static_cast<uint32_t>(n) * (BROW * 2);
-        const Rsrc rk = make_rsrc(kbase, nbytes), rv = make_rsrc(vbase, nbytes);
-        // tiles wave, wave+WAVES, ... through a two-deep register ring
-        constexpr int TSTRIDE = WAVES * TILE;
-        const int ntile = (n + TILE - 1) / TILE;
-        const int nmine = ntile > wave ? (ntile - wave + WAVES - 1) / WAVES : 0;
-        const int t0 = wave * TILE;
-        Bf16Raw r0, r1;
-        bf16_load(r0, rk, rv, t0, lane);
-        for (int i = 0; i < nmine; i += 2) {
-            const int t = t0 + i * TSTRIDE;
-            bf16_load(r1, rk, rv, t + TSTRIDE, lane);
-            bf16_compute(st, r0, qb, n - t, lane, qk_scale);
-            if (i + 1 >= nmine) break;
-            bf16_load(r0, rk, rv, t + 2 * TSTRIDE, lane);
-            bf16_compute(st, r1, qb, n - t - TSTRIDE, lane, qk_scale);
+    } else {
+        // ------------- bf16 parts: tiles wave, wave+WAVES, ... of each segment -------------
+        // (a piece never holds both int4 and bf16 tokens: make_plan cuts at
+        // the segment boundaries, so the Q copies of one part are dead
+        // during the other's loop)
+        const bf16x8 qb[4] = {__builtin_bit_cast(bf16x8, qraw[0]), __builtin_bit_cast(bf16x8, qraw[1]),
+                              __builtin_bit_cast(bf16x8, qraw[2]), __builtin_bit_cast(bf16x8, qraw[3])};
+        // segment bounds in units: [nqg, b1), [b1, b2), [b2, end of head)
+        const int b1 = nqg + su0, b2 = b1 + su1;
+        for (int seg = 0; seg < 3; ++seg) {
+            const int sb = seg == 0 ? nqg : seg == 1 ? b1 : b2;
+            const int ua = max(u0, sb), ub = min(u1, seg == 0 ? b1 : seg == 1 ? b2 : u1);
+            if (ua >= ub) continue;
+            const int lo = (ua - sb) * BUNIT;
+            int seg_len = seg == 0 ? sn0 : seg == 1 ? sn1 : sn2;
+            if (seg == 0 && len_s0 != nullptr) seg_len = min(seg_len, max(0, len_s0[head]));
+            const int n = max(0, min((ub - ua) * BUNIT, seg_len - lo));     // 0: past a ragged head's end
+            const uint16_t* const skp = seg == 0 ? sk0 : seg == 1 ? sk1 : sk2;
+            const uint16_t* const svp = seg == 0 ? sv0 : seg == 1 ? sv1 : sv2;
+            const int32_t skb = seg == 0 ? skb0 : seg == 1 ? skb1 : skb2;
+            const int32_t svb = seg == 0 ? svb0 : seg == 1 ? svb1 : svb2;
+            const uint16_t* kbase = skp + static_cast<int64_t>(head) * skb + static_cast<int64_t>(lo) * BROW;
+            const uint16_t* vbase = svp + static_cast<int64_t>(head) * svb + static_cast<int64_t>(lo) * BROW;
+            const uint32_t nbytes = static_cast<uint32_t>(n) * (BROW * 2);
+            const Rsrc rk = make_rsrc(kbase, nbytes), rv = make_rsrc(vbase, nbytes);
+            // tiles wave, wave+WAVES, ... through a two-deep register ring
+            constexpr int TSTRIDE = WAVES * TILE;
+            const int ntile = (n + TILE - 1) / TILE;
+            const int nmine = ntile > wave ? (ntile - wave + WAVES - 1) / WAVES : 0;
+            const int t0 = wave * TILE;
+            Bf16Raw r0, r1;
+            bf16_load(r0, rk, rv, t0, lane);
+            for (int i = 0; i < nmine; i += 2) {
+                const int t = t0 + i * TSTRIDE;
+                bf16_load(r1, rk, rv, t + TSTRIDE, lane);
+                bf16_compute(st, r0, qb, n - t, lane, qk_scale);
+                if (i + 1 >= nmine) break;
+                bf16_load(r0, rk, rv, t + 2 * TSTRIDE, lane);
+                bf16_compute(st, r1, qb, n - t - TSTRIDE, lane, qk_scale);
+            }
         }
     }
 
@@ -838,8 +841,9 @@ struct Plan {
 size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
 // Cut a head into pieces, each inside one segment (a piece spanning segments
-// would walk their rings one after the other), the int4 pieces first so
-// that the short segment pieces fill the end of the grid.
+// would walk their rings one after the other; decode_kernel relies on no
+// piece holding both int4 and bf16 units), the int4 pieces first so that the
+// short segment pieces fill the end of the grid.
 //   requested > 0: pieces of about that many int4 tokens' bytes.
 //   few KV heads (bh_kv < 32, a step of a few microseconds, bound by the
 //     per-piece round trips): int4 pieces of the smallest power-of-two

@@ -639,7 +639,10 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     const int b = bh / a.HQ, h = bh - b * a.HQ;
     const int G = a.HQ / a.HKV;
     const int64_t bhk = static_cast<int64_t>(b) * a.HKV + h / G;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // the wavefront index is uniform: read into a scalar register, so the LDS
+    // DMA destinations and scalar offsets built from it need no per-lane
+    // (waterfall) loop
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c16 = lane & 15, g = lane >> 4;
 
     // ---- Q block: load, quantise (int8 per block scale), fp16 copy --------

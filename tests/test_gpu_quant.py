@@ -68,3 +68,35 @@ def test_quant_config_inputs_bit_exact():
         rp, rs = O.quantize_per_token(x, 4)
         assert np.array_equal(packed.cpu().numpy(), rp)
         assert np.array_equal(scale.cpu().numpy().view(np.uint16), rs.view(np.uint16))
+
+
+@pytest.mark.parametrize("nbits", [4, 2, 8])
+def test_quant_every_bf16_value_bit_exact(nbits):
+    """Every bf16 value v with |v| <= amax, for 16 random token scales: all
+    exact ties v / s = k + 1/2 and the values next to them are covered, so
+    the kernel's quotient and rounding must agree with IEEE division and
+    round-half-even everywhere."""
+    rng = np.random.default_rng(70 + nbits)
+    D = 128
+    pos = (np.arange(0, 0x7F80, dtype=np.uint32) << 16).view(np.float32)   # finite bf16 >= 0
+    amaxes = O.bf16_round(np.exp(rng.uniform(np.log(1e-4), np.log(1e3), 16)).astype(np.float32))
+    toks = []
+    for amax in amaxes:
+        vals = pos[pos <= amax]
+        vals = np.concatenate([vals, -vals])
+        per = D - 1
+        ntok = -(-len(vals) // per)
+        body = np.zeros(ntok * per, np.float32)
+        body[:len(vals)] = vals
+        t = np.empty((ntok, D), np.float32)
+        t[:, 0] = amax                                  # fixes the token's scale
+        t[:, 1:] = body.reshape(ntok, per)
+        toks.append(t)
+    x = np.concatenate(toks)[None]
+    print(f"quant exhaustive nbits={nbits} tokens={x.shape[1]}", flush=True)
+    import hyquant_amd as hq
+    packed, scale = hq.quantize_per_token(to_dev_bf16(x, "cuda"), nbits)
+    torch.cuda.synchronize()
+    rp, rs = O.quantize_per_token(x, nbits)
+    assert np.array_equal(scale.cpu().numpy().view(np.uint16), rs.view(np.uint16))
+    assert np.array_equal(packed.cpu().numpy(), rp)

@@ -19,11 +19,15 @@ CPU on config 1), the prefix sweep of BASELINE config 2 beside a bf16 full-KV
 split-K decode of the same shape, and the other configs' workloads measured
 in the same run: config 3 (wide-GQA decode at B=32, 16K prefix; the vertical
 line selector, the freeze reorganisation and the staging flush) and config 4
-(hybrid prefill, fp16 and fp8 P.V, TFLOP/s and MFMA utilisation).
+(hybrid prefill: int8 or fp8 QK, fp16 or fp8 P.V, and the window-only kernel;
+TFLOP/s, MFMA utilisation and the output error against float32 exact
+attention).  `accuracy` gives the config-1 decode error (max-abs, relative)
+against float32 attention over the same quantised cache.
 
 `--pmc` runs a fixed, short workload for hardware-counter passes instead (a
-256 MiB device copy, the calibration of FETCH_SIZE / WRITE_SIZE, then 20 eager
-config-1 decode steps over distinct cache copies) and prints nothing.
+256 MiB device copy, the calibration of FETCH_SIZE / WRITE_SIZE, 20 eager
+config-1 decode steps over distinct cache copies, three config-4 prefill
+calls at N = 32768) and prints nothing.
 """
 
 from __future__ import annotations
@@ -217,6 +221,57 @@ def time_calls(fn, warmup=2, iters=5):
     return e0.elapsed_time(e1) / iters
 
 
+def exact_attention_fp32(q, k, v, chunk=1024):
+    """Causal softmax(q k^T / sqrt(D)) v in float32 on the GPU, chunked over
+    queries, GQA by head index (the reference for the prefill error figures;
+    2-D float32 products only)."""
+    B, HQ, N, Dh = q.shape
+    G = HQ // k.shape[1]
+    out = torch.empty(B, HQ, N, Dh, dtype=torch.float32, device=q.device)
+    for b in range(B):
+        for h in range(HQ):
+            kk = k[b, h // G].float()
+            vv = v[b, h // G].float()
+            for s0 in range(0, N, chunk):
+                qq = q[b, h, s0:s0 + chunk].float()
+                sc = (qq @ kk[: s0 + chunk].T.contiguous()) * Dh ** -0.5
+                i = torch.arange(s0, s0 + qq.shape[0], device=q.device)[:, None]
+                j = torch.arange(sc.shape[1], device=q.device)[None, :]
+                sc = sc.masked_fill(j > i, float("-inf"))
+                out[b, h, s0:s0 + chunk] = torch.softmax(sc, dim=-1) @ vv[: s0 + chunk]
+    return out
+
+
+def error_vs(out, ref):
+    """max-abs, relative (max-abs / max |ref|), relative L2 and MSE of out
+    against a float32 reference."""
+    d = out.float() - ref
+    return {"max_abs": float(d.abs().max()), "rel_max": float(d.abs().max() / ref.abs().max()),
+            "rel_l2": float(d.norm() / ref.norm()), "mse": float((d * d).mean())}
+
+
+def decode_error(dev):
+    """Config-1 decode output against float32 attention over the same
+    quantised cache on the GPU: the int4 codes times their fp16 scales (exact
+    in float32), the top-k / staging / window rows, softmax(q k^T / sqrt(D)) v
+    per query head with query head h on KV head h // 4."""
+    from hyquant_amd.decode_d_stage import _unpack_int4
+    q, st = make_state(1, 32, 8, 8192, dev, 99)
+    out = run_decode(q, st, 4).float()
+    kq = _unpack_int4(st["k_packed"], D) * st["k_scale"].float()[..., None]
+    vq = _unpack_int4(st["v_packed"], D) * st["v_scale"].float()[..., None]
+    K = torch.cat([kq, st["k_topk"].float(), st["k_staging"].float(), st["k_window"].float()], 1)
+    V = torch.cat([vq, st["v_topk"].float(), st["v_staging"].float(), st["v_window"].float()], 1)
+    ref = torch.empty(32, D, dtype=torch.float32, device=dev)
+    for h in range(32):
+        p = torch.softmax((K[h // 4] @ q[h].float()) * D ** -0.5, dim=0)
+        ref[h] = p @ V[h // 4]
+    e = error_vs(out, ref)
+    e["reference"] = "float32 attention over the dequantised four-segment cache (GPU, torch)"
+    e["bound"] = "max_abs <= 2e-3"
+    return e
+
+
 def bench_prefill(dev):
     """Config 4: hybrid prefill, B=1, 32q/8kv, d128, causal, W=128, rho=5%,
     with int8 or e4m3 QK on the rest tiles and fp16 or e4m3 P.V, and the
@@ -237,6 +292,7 @@ def bench_prefill(dev):
              math.sqrt(2.0) * torch.randn(B, HKV, 1, D, generator=g, device=dev)).to(torch.bfloat16)
         v = torch.randn(B, HKV, N, D, generator=g, device=dev).to(torch.bfloat16)
         vidx = compute_vertical_indices(q, k, W, 0.05, kv_repeat=HQ // HKV)
+        exact = exact_attention_fp32(q, k, v)
         flops = 2.0 * B * HQ * N * N * D
         variants = (
             ("hybrid", "int8", "fp16", PEAK_INT8, PEAK_FP16,
@@ -252,11 +308,15 @@ def bench_prefill(dev):
             ms = time_calls(fn)
             tf = flops / (ms * 1e-3) / 1e12
             peak = 2.0 / (1.0 / qk_peak + 1.0 / pv_peak)
+            err = error_vs(fn(), exact)
             rows.append({"seq_len": N, "kernel": kind, "qk": qk, "pv": pv, "ms": round(ms, 3),
                          "tflops": round(tf, 1), "mfma_peak_tflops": round(peak, 1),
-                         "mfma_util": round(tf / peak, 4), "n_vertical": int(vidx.shape[-1]) if kind == "hybrid" else 0})
+                         "mfma_util": round(tf / peak, 4), "n_vertical": int(vidx.shape[-1]) if kind == "hybrid" else 0,
+                         "mse_vs_exact_fp32": float("%.3e" % err["mse"]),
+                         "max_abs_vs_exact_fp32": float("%.3e" % err["max_abs"]),
+                         "rel_l2_vs_exact_fp32": float("%.3e" % err["rel_l2"])})
             print(f"# prefill {rows[-1]}", file=sys.stderr, flush=True)
-        del q, k, v, vidx
+        del q, k, v, vidx, exact
         torch.cuda.empty_cache()
     return rows
 
@@ -423,6 +483,8 @@ def main():
                      "kernel": "decode_kernel (one launch per step)",
                      "algorithmic_bytes_per_launch": nbytes},
     }
+    res["accuracy"] = {"decode_config1": {k: (float("%.3e" % x) if isinstance(x, float) else x)
+                                          for k, x in decode_error(dev).items()}}
     tr = traffic_record()
     if tr:
         res["roofline"]["traffic"] = tr.get("traffic_bytes_per_launch")

@@ -1,6 +1,6 @@
 """Benchmark of the fused hybrid decode attention on one MI355X.
 
-Headline workload: one decode step of one attention
+Headline workload (benchmark config 1): one decode step of one attention
 layer, B=1, 32 query / 8 KV heads, head_dim 128, prefix 8192 tokens frozen into
 the four segments (int4 K4V4 prefix of 7667 tokens, 397 bf16 vertical lines,
 64 bf16 staging tokens, 128 bf16 window tokens).  A "step" is one
@@ -15,7 +15,7 @@ Python calls one by one are reported as eager_us_per_step).
 
 Output: one JSON line (rank 0), with the roofline of the decode kernel, the
 CPU baseline (the reference's bf16 eager decode math run by torch on the host
-CPU on config 1), the prefix sweep of BASELINE config 2 beside a bf16 full-KV
+CPU on config 1), the prefix sweep of config 2 beside a bf16 full-KV
 split-K decode of the same shape, and the other configs' workloads measured
 in the same run: config 3 (wide-GQA decode at B=32, 16K prefix; the vertical
 line selector, the freeze reorganisation and the staging flush) and config 4

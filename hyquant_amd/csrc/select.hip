@@ -10,8 +10,8 @@
 //   score[p]    = bf16( sum_d qm[d] * k[p, d] )  with the sum taken in d order in
 //                 float64 (bf16 x bf16 products are exact in float64);
 //   top-T       = the T largest scores, ties broken by the lower index, returned
-//                 in (score desc, index asc) order (BASELINE's tie rule for the
-//                 unspecified order of torch.topk, src/patch/_common.py:189).
+//                 in (score desc, index asc) order (the lower-index rule fixes
+//                 the unspecified tie order of torch.topk, src/patch/_common.py:189).
 // Kernels:
 //   qmean_kernel      one workgroup per (b, ho): channel pairs x tail slices.
 //   score_kernel      one thread per key row, G output heads sharing the row

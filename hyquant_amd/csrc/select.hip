@@ -206,7 +206,12 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
 }
 
 constexpr int TOPK_WAVES = TOPK_THREADS / 64;
-constexpr int TOPK_RANK_MAX = 2048;        // rows up to this many winners are placed by rank
+constexpr int TOPK_RANK_MAX = 2048;        // winners the rank path's per-thread arrays can hold
+// rows with up to this many winners are placed by rank (each winner compared
+// with every other: T / 4 LDS steps per thread); larger rows are bitonic
+// sorted (log2(n2) (log2(n2) + 1) / 2 barrier-separated stages), which costs
+// less vector work from about 512 winners up
+constexpr int TOPK_RANK_LIMIT = 512;
 constexpr size_t TOPK_LDS_MAX = 64 * 1024; // keys are cached in LDS while the row fits this budget
 
 // Wavefront 0: the bin holding the need-th largest entry of a 256-bin
@@ -259,7 +264,7 @@ __device__ __forceinline__ void topk_find_bin(const uint32_t* hist, uint32_t nee
 // threshold key K and how many of the entries equal to K are taken (the r of
 // lowest index: a prefix count over contiguous per-thread index ranges); the
 // T winners' composites are collected in LDS and each is written straight to
-// its output position, its rank among the winners (T <= TOPK_RANK_MAX), or
+// its output position, its rank among the winners (T <= TOPK_RANK_LIMIT), or
 // bitonic-sorted first (larger T).  Dynamic LDS: [hist][winners][keys].
 __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __restrict__ keys, int64_t P, int T,
                                                             int n2, int cached, int64_t* __restrict__ out) {
@@ -353,7 +358,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __re
     for (int i = T + tid; i < n2; i += TOPK_THREADS) sel[i] = 0;   // real composites are > 0
     __syncthreads();
     int64_t* orow = out + static_cast<int64_t>(row) * T;
-    if (T <= TOPK_RANK_MAX) {
+    if (T <= TOPK_RANK_LIMIT) {
         // rank = number of larger winners.  A thread ranks its (up to 4)
         // winners in one sweep; every lane of a wavefront reads the same four
         // composites per step (LDS broadcast)
@@ -410,7 +415,7 @@ struct TopkPlan {
 };
 TopkPlan topk_plan(int64_t P, int T) {
     TopkPlan t;
-    if (T <= TOPK_RANK_MAX) {
+    if (T <= TOPK_RANK_LIMIT) {
         t.n2 = (T + 3) / 4 * 4;
     } else {
         t.n2 = 1;

@@ -27,7 +27,9 @@ against float32 attention over the same quantised cache.
 `--pmc` runs a fixed, short workload for hardware-counter passes instead (a
 256 MiB device copy, the calibration of FETCH_SIZE / WRITE_SIZE, 20 eager
 config-1 decode steps over distinct cache copies, three config-4 prefill
-calls at N = 32768) and prints nothing.
+calls at N = 32768) and prints nothing; `--pmc-decode-shapes` runs four eager
+decode steps at each of three shapes (B=16 32K, and the Qwen3-32B and
+GLM-4-9B shapes of config 3) for SQ counter passes.
 """
 
 from __future__ import annotations
@@ -421,6 +423,22 @@ def pmc_workload(dev):
     torch.cuda.synchronize()
 
 
+def pmc_decode_shapes_workload(dev):
+    """Fixed workload for SQ counter passes over the decode kernel at three
+    shapes: Llama-3.1-8B B=16 prefix 32768, and the config-3 Qwen3-32B and
+    GLM-4-9B shapes at B=32 prefix 16384; four eager steps each over two
+    cache copies."""
+    for (B, HQ, HKV, N) in ((16, 32, 8, 32768), (32, 64, 8, 16384), (32, 32, 2, 16384)):
+        states = [make_state(B, HQ, HKV, N, dev, s) for s in range(2)]
+        torch.cuda.synchronize()
+        for i in range(4):
+            q, st = states[i % 2]
+            run_decode(q, st, HQ // HKV)
+        torch.cuda.synchronize()
+        del states
+        torch.cuda.empty_cache()
+
+
 def traffic_record():
     """HBM bytes per decode launch measured by the FETCH_SIZE / WRITE_SIZE
     passes over pmc_workload (profiles/decode_config1_traffic.json), or None."""
@@ -442,6 +460,8 @@ def main():
     ap.add_argument("--no-bf16", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 3 / config 4 sections")
     ap.add_argument("--pmc", action="store_true", help="run the counter-pass workload only")
+    ap.add_argument("--pmc-decode-shapes", action="store_true",
+                    help="run the decode counter workload over three shapes only")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -450,6 +470,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     import hyquant_amd  # noqa: F401  (fails loudly if libhyq.so is missing)
+    if args.pmc_decode_shapes:
+        pmc_decode_shapes_workload(dev)
+        return
     if args.pmc:
         pmc_workload(dev)
         return

@@ -206,6 +206,9 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
 }
 
 constexpr int TOPK_WAVES = TOPK_THREADS / 64;
+// histogram copies: one per pair of wavefronts, which keeps a 16K-key row's
+// LDS (keys, histograms, winners) under 40 KiB, four workgroups per CU
+constexpr int TOPK_HIST = TOPK_WAVES / 2;
 constexpr int TOPK_RANK_MAX = 2048;        // winners the rank path's per-thread arrays can hold
 // rows with up to this many winners are placed by rank (each winner compared
 // with every other: T / 4 LDS steps per thread); larger rows are bitonic
@@ -269,8 +272,8 @@ __device__ __forceinline__ void topk_find_bin(const uint32_t* hist, uint32_t nee
 __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __restrict__ keys, int64_t P, int T,
                                                             int n2, int cached, int64_t* __restrict__ out) {
     extern __shared__ __align__(16) uint32_t tk_lds[];
-    uint32_t* hist = tk_lds;                       // [TOPK_WAVES][256]
-    uint32_t* sel = tk_lds + TOPK_WAVES * 256;     // [n2]
+    uint32_t* hist = tk_lds;                       // [TOPK_HIST][256]
+    uint32_t* sel = tk_lds + TOPK_HIST * 256;      // [n2]
     uint16_t* s_keys = reinterpret_cast<uint16_t*>(sel + n2);
     __shared__ uint32_t s_bin, s_need, s_count;
     __shared__ uint32_t s_wsum[TOPK_WAVES];
@@ -297,18 +300,18 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __re
     uint32_t need = static_cast<uint32_t>(T);
     uint32_t khi = 0;
     for (int pass = 0; pass < 2; ++pass) {
-        for (int i = tid; i < TOPK_WAVES * 256; i += TOPK_THREADS) hist[i] = 0;
+        for (int i = tid; i < TOPK_HIST * 256; i += TOPK_THREADS) hist[i] = 0;
         __syncthreads();
         for (int64_t i = tid; i < P; i += TOPK_THREADS) {
             const uint32_t key = key_at(i);
-            if (pass == 0) atomicAdd(&hist[wave * 256 + (key >> 8)], 1u);
-            else if ((key >> 8) == khi) atomicAdd(&hist[wave * 256 + (key & 0xffu)], 1u);
+            if (pass == 0) atomicAdd(&hist[(wave >> 1) * 256 + (key >> 8)], 1u);
+            else if ((key >> 8) == khi) atomicAdd(&hist[(wave >> 1) * 256 + (key & 0xffu)], 1u);
         }
         __syncthreads();
         if (tid < 256) {
             uint32_t sum = 0;
 #pragma unroll
-            for (int w = 0; w < TOPK_WAVES; ++w) sum += hist[w * 256 + tid];
+            for (int w = 0; w < TOPK_HIST; ++w) sum += hist[w * 256 + tid];
             hist[tid] = sum;
         }
         __syncthreads();
@@ -421,7 +424,7 @@ TopkPlan topk_plan(int64_t P, int T) {
         t.n2 = 1;
         while (t.n2 < T) t.n2 <<= 1;
     }
-    const size_t fixed = (static_cast<size_t>(TOPK_WAVES) * 256 + t.n2) * 4;
+    const size_t fixed = (static_cast<size_t>(TOPK_HIST) * 256 + t.n2) * 4;
     const size_t with_keys = fixed + (static_cast<size_t>(P) * 2 + 15) / 16 * 16;
     t.cached = with_keys <= TOPK_LDS_MAX;
     t.lds = t.cached ? with_keys : fixed;

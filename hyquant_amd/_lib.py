@@ -25,6 +25,7 @@ EXPORTS = (
     "hyq_last_error",
     "hyq_abi_version",
     "hyq_quant_pack",
+    "hyq_dequant",
     "hyq_decode_workspace_size",
     "hyq_decode_hybrid",
     "hyq_decode_bf16_workspace_size",
@@ -88,8 +89,11 @@ def _declare(lib):
     lib.hyq_abi_version.restype = c_int
     lib.hyq_abi_version.argtypes = []
     lib.hyq_quant_pack.restype = c_int
-    lib.hyq_quant_pack.argtypes = [c_void_p, c_int64, c_int64, c_int32, c_int64, c_int64, c_int32,
+    lib.hyq_quant_pack.argtypes = [c_void_p, c_int32, c_int64, c_int64, c_int32, c_int64, c_int64, c_int32,
                                    c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p]
+    lib.hyq_dequant.restype = c_int
+    lib.hyq_dequant.argtypes = [c_void_p, c_int64, c_int64, c_int32, c_int64, c_int64, c_int32,
+                                c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p]
     lib.hyq_decode_workspace_size.restype = c_size_t
     lib.hyq_decode_workspace_size.argtypes = [POINTER(DecodeParams)]
     lib.hyq_decode_hybrid.restype = c_int

@@ -1,11 +1,15 @@
 // Per-token symmetric quantisation and nibble/crumb packing (the staging flush
-// and the freeze quantiser).  Semantics follow quantize_per_token,
-// src/ops/decode_d_stage.py:50-77, and _pack_int4/_pack_int2 (:104-133):
+// and the freeze quantiser), and the inverse dequantisation.  Semantics follow
+// quantize_per_token / dequantize_per_token, src/ops/decode_d_stage.py:50-101,
+// and _pack_int4/_pack_int2 / _unpack_int4/_unpack_int2 (:104-149):
 //   scale = fp16(fp32(max(amax, 1e-5)) / qmax)        (IEEE fp32 divide, RNE)
 //   code  = clamp(rint_half_even(x / fp32(scale)), qmin, qmax)
-// Layout: a group of d/8 lanes owns one token row; each lane loads 8 bf16
-// channels with one 128-bit load and writes its packed bytes, so a wavefront
-// reads 64*16 contiguous bytes per instruction.  HBM-bound.
+//   deq   = fp16(fp32(code) * fp32(scale))            (the product is exact)
+// x is bf16 or fp16 (both are widened exactly to fp32 first).
+// Layout: a group of d/8 lanes owns one token row; each lane loads 8
+// channels with one 128-bit load and writes its packed bytes (dequantisation:
+// reads the packed bytes of 8 channels, writes 16 bytes), so a wavefront
+// moves 64*16 contiguous bytes per instruction.  HBM-bound.
 #include "hyq_common.h"
 
 #include <cstdio>
@@ -14,7 +18,7 @@
 namespace hyq {
 namespace {
 
-template <int NBITS>
+template <int NBITS, bool F16>
 __global__ __launch_bounds__(256) void quant_pack_kernel(
     const uint16_t* __restrict__ x, int64_t n, int64_t total, int lpt_log2,
     int64_t xs_bh, int64_t xs_n, int8_t* __restrict__ packed, int64_t ps_bh, int64_t ps_n,
@@ -36,8 +40,13 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        v[2 * i] = __uint_as_float(w[i] << 16);
-        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        if constexpr (F16) {
+            v[2 * i] = f16_bits_to_f32(static_cast<uint16_t>(w[i]));
+            v[2 * i + 1] = f16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+        } else {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
     }
     float amax = 0.f;
 #pragma unroll
@@ -78,19 +87,66 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(
     if (sub == 0) scale[ib * ss_bh + in] = __builtin_bit_cast(uint16_t, s16);
 }
 
+// code of channel i (0..7) of a lane's packed bytes, sign-extended
+template <int NBITS>
+__device__ __forceinline__ int code_at(uint32_t lo, uint32_t hi, int i) {
+    if constexpr (NBITS == 4) return static_cast<int>(lo << (28 - 4 * i)) >> 28;
+    else if constexpr (NBITS == 2) return static_cast<int>(lo << (30 - 2 * i)) >> 30;
+    else return static_cast<int>((i < 4 ? lo : hi) << (24 - 8 * (i & 3))) >> 24;
+}
+
+template <int NBITS>
+__global__ __launch_bounds__(256) void dequant_kernel(
+    const int8_t* __restrict__ packed, int64_t n, int64_t total, int lpt_log2, int64_t ps_bh, int64_t ps_n,
+    const uint16_t* __restrict__ scale, int64_t ss_bh, uint16_t* __restrict__ out, int64_t os_bh, int64_t os_n) {
+    const int lpt = 1 << lpt_log2;
+    const int sub = threadIdx.x & (lpt - 1);
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * (256 >> lpt_log2) + (threadIdx.x >> lpt_log2);
+    if (t >= total) return;
+    const int64_t ib = t / n, in = t - ib * n;
+    const int8_t* prow = packed + ib * ps_bh + in * ps_n;
+    uint32_t lo, hi = 0;
+    if constexpr (NBITS == 4) {
+        lo = reinterpret_cast<const uint32_t*>(prow)[sub];
+    } else if constexpr (NBITS == 8) {
+        const uint2 w = reinterpret_cast<const uint2*>(prow)[sub];
+        lo = w.x; hi = w.y;
+    } else {
+        lo = reinterpret_cast<const uint16_t*>(prow)[sub];
+    }
+    const float sf = f16_bits_to_f32(scale[ib * ss_bh + in]);
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const _Float16 a = static_cast<_Float16>(static_cast<float>(code_at<NBITS>(lo, hi, 2 * j)) * sf);
+        const _Float16 b = static_cast<_Float16>(static_cast<float>(code_at<NBITS>(lo, hi, 2 * j + 1)) * sf);
+        o[j] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+               (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+    }
+    reinterpret_cast<uint4*>(out + ib * os_bh + in * os_n)[sub] = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+int lanes_log2(int d) {
+    int l = 0;
+    while ((1 << l) < d / 8) ++l;
+    return l;
+}
+
+bool ok_dim(int d) { return d > 0 && d % 8 == 0 && d <= 512 && ((d / 8) & (d / 8 - 1)) == 0; }
+
 }  // namespace
 }  // namespace hyq
 
 using namespace hyq;
 
-extern "C" int hyq_quant_pack(const uint16_t* x, int64_t bh, int64_t n, int32_t d,
+extern "C" int hyq_quant_pack(const uint16_t* x, int32_t x_is_fp16, int64_t bh, int64_t n, int32_t d,
                               int64_t x_stride_bh, int64_t x_stride_n, int32_t nbits,
                               int8_t* packed, int64_t p_stride_bh, int64_t p_stride_n,
                               uint16_t* scale, int64_t s_stride_bh, void* stream) {
     if (bh < 0 || n < 0) return fail(HYQ_EINVAL, "hyq_quant_pack: negative shape");
     if (nbits != 2 && nbits != 4 && nbits != 8)
         return fail(HYQ_EINVAL, "nbits must be 2, 4, or 8, got " + std::to_string(nbits));
-    if (d <= 0 || d % 8 != 0 || d > 512 || ((d / 8) & (d / 8 - 1)) != 0)
+    if (!ok_dim(d))
         return fail(HYQ_ENOTSUP, "hyq_quant_pack: head dim must be 8*2^k <= 512, got " + std::to_string(d));
     if (bh == 0 || n == 0) return HYQ_OK;
     if (!x || !packed || !scale) return fail(HYQ_EINVAL, "hyq_quant_pack: null pointer");
@@ -100,22 +156,58 @@ extern "C" int hyq_quant_pack(const uint16_t* x, int64_t bh, int64_t n, int32_t 
     if (!aligned(packed, pbytes) || p_stride_n % pbytes || p_stride_bh % pbytes)
         return fail(HYQ_EINVAL, "hyq_quant_pack: packed output misaligned");
     if (!aligned(scale, 2)) return fail(HYQ_EINVAL, "hyq_quant_pack: scale misaligned");
-    int lpt_log2 = 0;
-    while ((1 << lpt_log2) < d / 8) ++lpt_log2;
+    const int lpt_log2 = lanes_log2(d);
     const int64_t total = bh * n;
     const int64_t tpb = 256 >> lpt_log2;
     const int64_t blocks = (total + tpb - 1) / tpb;
     if (blocks > 0x7fffffffLL) return fail(HYQ_ENOTSUP, "hyq_quant_pack: too many tokens");
     hipStream_t s = static_cast<hipStream_t>(stream);
     dim3 grid(static_cast<unsigned>(blocks)), block(256);
-    if (nbits == 4)
-        quant_pack_kernel<4><<<grid, block, 0, s>>>(x, n, total, lpt_log2, x_stride_bh, x_stride_n,
-                                                    packed, p_stride_bh, p_stride_n, scale, s_stride_bh);
-    else if (nbits == 8)
-        quant_pack_kernel<8><<<grid, block, 0, s>>>(x, n, total, lpt_log2, x_stride_bh, x_stride_n,
-                                                    packed, p_stride_bh, p_stride_n, scale, s_stride_bh);
-    else
-        quant_pack_kernel<2><<<grid, block, 0, s>>>(x, n, total, lpt_log2, x_stride_bh, x_stride_n,
-                                                    packed, p_stride_bh, p_stride_n, scale, s_stride_bh);
+#define HYQ_QUANT(NB, F)                                                                            \
+    quant_pack_kernel<NB, F><<<grid, block, 0, s>>>(x, n, total, lpt_log2, x_stride_bh, x_stride_n, \
+                                                    packed, p_stride_bh, p_stride_n, scale, s_stride_bh)
+    const bool f16 = x_is_fp16 != 0;
+    if (nbits == 4) {
+        if (f16) HYQ_QUANT(4, true); else HYQ_QUANT(4, false);
+    } else if (nbits == 8) {
+        if (f16) HYQ_QUANT(8, true); else HYQ_QUANT(8, false);
+    } else {
+        if (f16) HYQ_QUANT(2, true); else HYQ_QUANT(2, false);
+    }
+#undef HYQ_QUANT
     return check_launch("hyq_quant_pack");
+}
+
+extern "C" int hyq_dequant(const int8_t* packed, int64_t bh, int64_t n, int32_t d, int64_t p_stride_bh,
+                           int64_t p_stride_n, int32_t nbits, const uint16_t* scale, int64_t s_stride_bh,
+                           uint16_t* out, int64_t o_stride_bh, int64_t o_stride_n, void* stream) {
+    if (bh < 0 || n < 0) return fail(HYQ_EINVAL, "hyq_dequant: negative shape");
+    if (nbits != 2 && nbits != 4 && nbits != 8)
+        return fail(HYQ_EINVAL, "nbits must be 2, 4, or 8, got " + std::to_string(nbits));
+    if (!ok_dim(d)) return fail(HYQ_ENOTSUP, "hyq_dequant: head dim must be 8*2^k <= 512, got " + std::to_string(d));
+    if (bh == 0 || n == 0) return HYQ_OK;
+    if (!packed || !scale || !out) return fail(HYQ_EINVAL, "hyq_dequant: null pointer");
+    const int pbytes = nbits;  // packed bytes per lane (8 channels)
+    if (!aligned(packed, pbytes) || p_stride_n % pbytes || p_stride_bh % pbytes)
+        return fail(HYQ_EINVAL, "hyq_dequant: packed input misaligned");
+    if (!aligned(scale, 2)) return fail(HYQ_EINVAL, "hyq_dequant: scale misaligned");
+    if (!aligned(out, 16) || o_stride_n % 8 || o_stride_bh % 8)
+        return fail(HYQ_EINVAL, "hyq_dequant: out must be 16-byte aligned with strides divisible by 8");
+    const int lpt_log2 = lanes_log2(d);
+    const int64_t total = bh * n;
+    const int64_t tpb = 256 >> lpt_log2;
+    const int64_t blocks = (total + tpb - 1) / tpb;
+    if (blocks > 0x7fffffffLL) return fail(HYQ_ENOTSUP, "hyq_dequant: too many tokens");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    dim3 grid(static_cast<unsigned>(blocks)), block(256);
+    if (nbits == 4)
+        dequant_kernel<4><<<grid, block, 0, s>>>(packed, n, total, lpt_log2, p_stride_bh, p_stride_n, scale, s_stride_bh,
+                                                 out, o_stride_bh, o_stride_n);
+    else if (nbits == 8)
+        dequant_kernel<8><<<grid, block, 0, s>>>(packed, n, total, lpt_log2, p_stride_bh, p_stride_n, scale, s_stride_bh,
+                                                 out, o_stride_bh, o_stride_n);
+    else
+        dequant_kernel<2><<<grid, block, 0, s>>>(packed, n, total, lpt_log2, p_stride_bh, p_stride_n, scale, s_stride_bh,
+                                                 out, o_stride_bh, o_stride_n);
+    return check_launch("hyq_dequant");
 }

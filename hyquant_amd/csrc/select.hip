@@ -510,6 +510,7 @@ struct CompactArgs {
     int64_t ks_b, ks_h, ks_n, vs_b, vs_h, vs_n;
     int HK;
     int64_t P;                   // prefix length (N - W)
+    int64_t n_compact;           // rows of the compact outputs (P - T)
     int64_t words;               // bitmap words per row
     const uint32_t* bits;
     int8_t* kp; int8_t* vp;      // [BH, P - T, D*bits/8]
@@ -568,9 +569,13 @@ __global__ __launch_bounds__(256) void compact_quant_kernel(CompactArgs a) {
             const int64_t p = pp[u];
             const int j = j0 + 16 * u;
             const uint32_t word = p < a.P ? rb[p >> 5] : 1u << (p & 31);
-            const bool keep = p < a.P && !((word >> (p & 31)) & 1u);     // selected rows stay bf16 in k/v_topk
             const uint32_t below = __popc(word & ((1u << (p & 31)) - 1u));
-            const int64_t dst = keep ? p - (base + s_wpre[j >> 5] + below) : 0;
+            const int64_t slot = p - (base + s_wpre[j >> 5] + below);
+            // selected rows stay bf16 in k/v_topk; the slot bound holds when the
+            // indices are distinct and in range, and keeps every store inside
+            // the n_compact rows of the outputs when they are not
+            const bool keep = p < a.P && !((word >> (p & 31)) & 1u) && slot < a.n_compact;
+            const int64_t dst = keep ? slot : 0;
             quant_row_group<KB>(kr[u], a.kp + bh * a.kp_bh + dst * a.kp_n, a.ksc + bh * a.ksc_bh + dst, sub, keep);
             quant_row_group<VB>(vr[u], a.vp + bh * a.vp_bh + dst * a.vp_n, a.vsc + bh * a.vsc_bh + dst, sub, keep);
         }
@@ -605,8 +610,13 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
         dk = a.kw + bh * a.kw_bh + (r - a.T) * a.kw_n;
         dv = a.vw + bh * a.vw_bh + (r - a.T) * a.vw_n;
     }
-    reinterpret_cast<uint4*>(dk)[sub] = reinterpret_cast<const uint4*>(a.k + b * a.ks_b + hk * a.ks_h + src * a.ks_n)[sub];
-    reinterpret_cast<uint4*>(dv)[sub] = reinterpret_cast<const uint4*>(a.v + b * a.vs_b + hk * a.vs_h + src * a.vs_n)[sub];
+    uint4 kr = make_uint4(0u, 0u, 0u, 0u), vr = kr;
+    if (r >= a.T || (src >= 0 && src < a.win0)) {  // a top-k index outside [0, P) gives a zero row
+        kr = reinterpret_cast<const uint4*>(a.k + b * a.ks_b + hk * a.ks_h + src * a.ks_n)[sub];
+        vr = reinterpret_cast<const uint4*>(a.v + b * a.vs_b + hk * a.vs_h + src * a.vs_n)[sub];
+    }
+    reinterpret_cast<uint4*>(dk)[sub] = kr;
+    reinterpret_cast<uint4*>(dv)[sub] = vr;
 }
 
 int padded_heads(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16; }
@@ -711,15 +721,20 @@ extern "C" int hyq_freeze_reorganise(const uint16_t* k, int64_t ks_b, int64_t ks
             int rc = check_launch("hyq_freeze_reorganise (mark)");
             if (rc) return rc;
         }
-        CompactArgs a{k, v, ks_b, ks_h, ks_n, vs_b, vs_h, vs_n, hk, P, words, bits,
+        CompactArgs a{k, v, ks_b, ks_h, ks_n, vs_b, vs_h, vs_n, hk, P, P - top_k, words, bits,
                       kp, vp, kp_bh, kp_n, vp_bh, vp_n, ksc, vsc, ksc_bh, vsc_bh, k_bits, v_bits};
         dim3 grid(static_cast<unsigned>((P + CQ_CHUNK - 1) / CQ_CHUNK), static_cast<unsigned>(bh));
-        if (k_bits == 4 && v_bits == 4) compact_quant_kernel<4, 4><<<grid, dim3(256), 0, s>>>(a);
-        else if (k_bits == 4 && v_bits == 2) compact_quant_kernel<4, 2><<<grid, dim3(256), 0, s>>>(a);
-        else if (k_bits == 2 && v_bits == 4) compact_quant_kernel<2, 4><<<grid, dim3(256), 0, s>>>(a);
-        else if (k_bits == 8 && v_bits == 8) compact_quant_kernel<8, 8><<<grid, dim3(256), 0, s>>>(a);
-        else if (k_bits == 2 && v_bits == 2) compact_quant_kernel<2, 2><<<grid, dim3(256), 0, s>>>(a);
-        else return fail(HYQ_ENOTSUP, "hyq_freeze_reorganise: unsupported bit pair");
+        switch (10 * k_bits + v_bits) {
+            case 44: compact_quant_kernel<4, 4><<<grid, dim3(256), 0, s>>>(a); break;
+            case 42: compact_quant_kernel<4, 2><<<grid, dim3(256), 0, s>>>(a); break;
+            case 48: compact_quant_kernel<4, 8><<<grid, dim3(256), 0, s>>>(a); break;
+            case 24: compact_quant_kernel<2, 4><<<grid, dim3(256), 0, s>>>(a); break;
+            case 22: compact_quant_kernel<2, 2><<<grid, dim3(256), 0, s>>>(a); break;
+            case 28: compact_quant_kernel<2, 8><<<grid, dim3(256), 0, s>>>(a); break;
+            case 84: compact_quant_kernel<8, 4><<<grid, dim3(256), 0, s>>>(a); break;
+            case 82: compact_quant_kernel<8, 2><<<grid, dim3(256), 0, s>>>(a); break;
+            default: compact_quant_kernel<8, 8><<<grid, dim3(256), 0, s>>>(a); break;
+        }
         int rc = check_launch("hyq_freeze_reorganise (compact)");
         if (rc) return rc;
     }

@@ -74,17 +74,20 @@ def _packed_dim(D: int, bits: int) -> int:
 # ---------------------------------------------------------------------------
 
 
+_HALF = (torch.bfloat16, torch.float16)
+
+
 def quantize_per_token(x: torch.Tensor, nbits: int) -> Tuple[torch.Tensor, torch.Tensor]:
     """Per-token symmetric quantisation.
 
-    x: [BH, N, D] bf16 -> (packed int8 [BH, N, D*nbits/8], scale fp16 [BH, N]).
+    x: [BH, N, D] bf16 or fp16 -> (packed int8 [BH, N, D*nbits/8], scale fp16 [BH, N]).
     Bit-exact with src/ops/decode_d_stage.py:50-77.
     """
     if nbits not in (2, 4, 8):
         raise ValueError(f"nbits must be 2, 4, or 8, got {nbits}")
     _require_gpu(x, "x")
-    if x.dtype != torch.bfloat16:
-        raise ValueError(f"quantize_per_token expects bf16 input, got {x.dtype}")
+    if x.dtype not in _HALF:
+        raise ValueError(f"quantize_per_token expects bf16 or fp16 input, got {x.dtype}")
     BH, N, D = x.shape
     packed = torch.empty(BH, N, _packed_dim(D, nbits), dtype=torch.int8, device=x.device)
     scale = torch.empty(BH, N, dtype=torch.float16, device=x.device)
@@ -103,8 +106,10 @@ def quantize_into(x: torch.Tensor, nbits: int, packed: torch.Tensor, scale: torc
         x = x.contiguous()
     if packed.stride(-1) != 1 or scale.stride(-1) != 1:
         raise ValueError("packed/scale outputs must be contiguous in the last dim")
+    if x.dtype not in _HALF:
+        raise ValueError(f"quantize_per_token expects bf16 or fp16 input, got {x.dtype}")
     st = _lib.lib().hyq_quant_pack(
-        x.data_ptr(), BH, N, D, x.stride(0), x.stride(1), nbits,
+        x.data_ptr(), int(x.dtype == torch.float16), BH, N, D, x.stride(0), x.stride(1), nbits,
         packed.data_ptr(), packed.stride(0), packed.stride(1),
         scale.data_ptr(), scale.stride(0), _stream(x.device))
     _lib.check(st, "quantize_per_token")
@@ -125,17 +130,29 @@ def _unpack_int2(packed: torch.Tensor, D: int) -> torch.Tensor:
 
 def dequantize_per_token(packed: torch.Tensor, scale: torch.Tensor, D: int, nbits: int) -> torch.Tensor:
     """[BH, N, D_packed] + [BH, N] -> fp16 [BH, N, D] = fp16(code * scale)
-    (src/ops/decode_d_stage.py:80-101).  Not on the decode hot path (the
-    fused kernel dequantises in registers); runs as device tensor ops."""
-    if nbits == 8:
-        q = packed.float()
-    elif nbits == 4:
-        q = _unpack_int4(packed, D)
-    elif nbits == 2:
-        q = _unpack_int2(packed, D)
-    else:
+    (src/ops/decode_d_stage.py:80-101), by the hyq_dequant kernel.  The fused
+    decode never calls it (it dequantises in registers); the eager decode
+    path and the bf16 round trip of a quantised cache do."""
+    if nbits not in (2, 4, 8):
         raise ValueError(f"nbits must be 2, 4, or 8, got {nbits}")
-    return (q * scale.float().unsqueeze(-1)).to(torch.float16)
+    _require_gpu(packed, "packed")
+    BH, N, DP = packed.shape
+    if DP != _packed_dim(D, nbits):
+        raise ValueError(f"packed rows hold {DP} bytes, expected {_packed_dim(D, nbits)} for D={D}, {nbits} bits")
+    if packed.dtype != torch.int8 or scale.dtype != torch.float16 or tuple(scale.shape) != (BH, N):
+        raise ValueError("dequantize_per_token expects int8 packed [BH, N, D_packed] and fp16 scale [BH, N]")
+    out = torch.empty(BH, N, D, dtype=torch.float16, device=packed.device)
+    if BH * N == 0:
+        return out
+    if packed.stride(-1) != 1:
+        packed = packed.contiguous()
+    if scale.stride(-1) != 1:
+        scale = scale.contiguous()
+    st = _lib.lib().hyq_dequant(packed.data_ptr(), BH, N, D, packed.stride(0), packed.stride(1), nbits,
+                                scale.data_ptr(), scale.stride(0), out.data_ptr(), out.stride(0), out.stride(1),
+                                _stream(packed.device))
+    _lib.check(st, "dequantize_per_token")
+    return out
 
 
 def _quantize_by_bits(x: torch.Tensor, bits: int):

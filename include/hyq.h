@@ -40,18 +40,32 @@ int hyq_abi_version(void);
  * Replaces quantize_per_token (src/ops/decode_d_stage.py:50-77) with
  * _pack_int4 (:104-111) / _pack_int2 (:126-133), and the staging flush's
  * quantisation (src/ops/d_stage_kv_cache.py:209-217).
- *   x      bf16 [bh, n, d]        strides (x_stride_bh, x_stride_n)
+ *   x      bf16 (x_is_fp16 = 0) or fp16 [bh, n, d]  strides (x_stride_bh, x_stride_n)
  *   packed int8 [bh, n, d*nbits/8] strides (p_stride_bh, p_stride_n)
  *   scale  fp16 [bh, n]            strides (s_stride_bh, 1)
  * scale = fp16(max(amax, 1e-5) / (2^(nbits-1)-1)) computed in fp32,
  * code  = clamp(round_half_even(x / scale), -2^(nbits-1), 2^(nbits-1)-1),
- * int4: even channel in the low nibble.  nbits in {2,4,8}; d % 8 == 0, d <= 256.
+ * int4: even channel in the low nibble.  nbits in {2,4,8}; d = 8 * 2^k <= 512.
  * The output may be a window of a larger buffer (append at an offset).
  */
-int hyq_quant_pack(const uint16_t* x, int64_t bh, int64_t n, int32_t d,
+int hyq_quant_pack(const uint16_t* x, int32_t x_is_fp16, int64_t bh, int64_t n, int32_t d,
                    int64_t x_stride_bh, int64_t x_stride_n, int32_t nbits,
                    int8_t* packed, int64_t p_stride_bh, int64_t p_stride_n,
                    uint16_t* scale, int64_t s_stride_bh, void* stream);
+
+/*
+ * Per-token dequantisation.  Replaces dequantize_per_token
+ * (src/ops/decode_d_stage.py:80-101) with _unpack_int4 (:114-123) /
+ * _unpack_int2 (:136-149):
+ *   packed int8 [bh, n, d*nbits/8] strides (p_stride_bh, p_stride_n)
+ *   scale  fp16 [bh, n]            strides (s_stride_bh, 1)
+ *   out    fp16 [bh, n, d]         strides (o_stride_bh, o_stride_n), rows 16-byte aligned
+ * out = fp16(fp32(code) * fp32(scale)) (RNE); nbits in {2,4,8}; d = 8 * 2^k <= 512.
+ */
+int hyq_dequant(const int8_t* packed, int64_t bh, int64_t n, int32_t d,
+                int64_t p_stride_bh, int64_t p_stride_n, int32_t nbits,
+                const uint16_t* scale, int64_t s_stride_bh,
+                uint16_t* out, int64_t o_stride_bh, int64_t o_stride_n, void* stream);
 
 /*
  * Four-segment hybrid decode attention for one query token per head.
@@ -151,7 +165,14 @@ int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h, int64_t q
  *   k/v_window bf16 [b*hk, w, d]      the last w rows
  *   k/v_packed + k/v_scale            the other n-w-top_k prefix rows in
  *                                     ascending position, quantised per token
- *                                     exactly as hyq_quant_pack (k_bits, v_bits).
+ *                                     exactly as hyq_quant_pack (k_bits, v_bits),
+ *                                     any of the nine pairs of 2, 4 and 8 bits.
+ * Precondition: each row of topk_idx holds distinct positions in [0, n-w)
+ * (the selector's output).  Violations cannot make the call touch memory
+ * outside its arguments: an index outside [0, n-w) copies a zero row into
+ * k/v_topk and marks nothing, and the compact outputs are never written past
+ * their n-w-top_k rows (with repeated or out-of-range indices some of those
+ * rows stay unwritten).
  * Workspace: hyq_freeze_workspace_size(b*hk, n-w) bytes (a position bitmap).
  */
 size_t hyq_freeze_workspace_size(int32_t bh, int64_t p);

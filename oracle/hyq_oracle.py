@@ -715,9 +715,19 @@ def per_block_fp8(x: np.ndarray, sm: float, blk: int) -> Tuple[np.ndarray, np.nd
     return codes, scales
 
 
+FP8_AMBIGUITY = 2.0 ** -14  # relative fp32 deviation of a kernel's p' from the exact one
+
+
+def _round_span(x: np.ndarray, rnd, rel: float) -> np.ndarray:
+    """|rnd(x (1 + rel)) - rnd(x (1 - rel))|: zero unless x lies within a
+    relative `rel` of a rounding boundary of `rnd`, else the step between the
+    two neighbours either rounding may take."""
+    return np.abs(rnd(x * (1.0 + rel)) - rnd(x * (1.0 - rel)))
+
+
 def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None, smooth: bool = True,
                         int8_rest: bool = True, abs_v: bool = False, pv_mode: str = "fp16",
-                        qk_mode: str = "int8"):
+                        qk_mode: str = "int8", blocks=None, fp8_detail: bool = False):
     """float64 restatement of sage_vertical_attention_v2 (sage_unified.py:550-622,
     kernel :398-496).  q [B, HQ, N, D], k/v [B, HKV, N, D] (bf16 values),
     vidx [B, HQ, T].  For query row i of block b (128 rows):
@@ -741,7 +751,23 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
     block and rest K per 64-entry block in e4m3 (per_block_fp8),
     s = (q8 . k8) * q_scale * k_scale, everything else unchanged.
 
-    Returns float64 [B, HQ, N, D]."""
+    blocks: the 128-row query blocks to compute (default all); rows of other
+    blocks are left zero.
+
+    fp8_detail (pv_mode='fp8'): also return `slack` and `exact_rows`.
+    slack [B, HQ, N, D] = sum over keys j of |V_j| vs / l times the step
+    between the two e4m3 (rest keys) or fp16 (vertical / window keys)
+    neighbours of p'_j when p'_j lies within a relative FP8_AMBIGUITY of a
+    rounding boundary (zero otherwise): the most a kernel whose p'
+    deviates from the exact value by that much in fp32 can differ from this
+    restatement through the rounding of P'.  exact_rows [B, HQ, N] marks
+    the rows whose maximum score is attained (within 1e-6 in log2 units) by
+    a key of the first 64-key tile the kernel visits (rest tiles, then
+    vertical, then window, each in list order): for those the kernel's
+    running maximum is the row maximum from its first tile on, so it rounds
+    the same p'_j as this restatement.
+
+    Returns float64 [B, HQ, N, D] (or (out, slack, exact_rows))."""
     B, HQ, N, D = q.shape
     HKV = k.shape[1]
     G = HQ // HKV
@@ -759,13 +785,19 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
         if fp8:
             v8 = np.abs(v8)
     out = np.zeros((B, HQ, N, D), np.float64)
+    detail = fp8 and fp8_detail
+    if detail:
+        slack = np.zeros((B, HQ, N, D), np.float64)
+        exact_rows = np.zeros((B, HQ, N), bool)
+    nblk = (N + PREFILL_BLOCK_M - 1) // PREFILL_BLOCK_M
+    blk_list = range(nblk) if blocks is None else [int(x) for x in blocks]
     for b in range(B):
         for h in range(HQ):
             hk = h // G
             vert, rest, nv, nr = prefill_lists(vidx[b, h], N, W)
             if len(rest):
                 k8r, ksr = quant(k16[b, hk, rest], 1.0, PREFILL_BLOCK_N)
-            for blk in range((N + PREFILL_BLOCK_M - 1) // PREFILL_BLOCK_M):
+            for blk in blk_list:
                 wla = window_start(blk, W)
                 rows = np.arange(blk * PREFILL_BLOCK_M, min(N, (blk + 1) * PREFILL_BLOCK_M))
                 qrow = q16[b, h, rows].astype(np.float64)
@@ -798,12 +830,28 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
                 n_rest = nr[blk]
                 pq = np.concatenate([e4m3_round(p[:, :n_rest]),
                                      to_fp16(p[:, n_rest:].astype(np.float32)).astype(np.float64)], axis=1)
-                out[b, h, rows] = (pq @ V) / p.sum(axis=1, keepdims=True) * vs[b, hk, 0].astype(np.float64)[None, :]
+                vsc = vs[b, hk, 0].astype(np.float64)[None, :]
+                out[b, h, rows] = (pq @ V) / p.sum(axis=1, keepdims=True) * vsc
+                if detail:
+                    f16 = lambda x: to_fp16(x.astype(np.float32)).astype(np.float64)
+                    span = np.concatenate([_round_span(p[:, :n_rest], e4m3_round, FP8_AMBIGUITY),
+                                           _round_span(p[:, n_rest:], f16, FP8_AMBIGUITY)], axis=1)
+                    slack[b, h, rows] = (span @ np.abs(V)) / p.sum(axis=1, keepdims=True) * vsc
+                    n_vert = int(nv[blk])
+                    if n_rest > 0:
+                        first = slice(0, min(PREFILL_BLOCK_N, n_rest))
+                    elif n_vert > 0:
+                        first = slice(0, min(PREFILL_BLOCK_N, n_vert))
+                    else:
+                        first = slice(0, min(PREFILL_BLOCK_N, len(jw)))
+                    exact_rows[b, h, rows] = S[:, first].max(axis=1) >= S.max(axis=1) - 1e-6
+    if detail:
+        return out, slack, exact_rows
     return out
 
 
 def unified_prefill_fp64(q, k, v, W: int, sm_scale: Optional[float] = None, smooth: bool = True,
-                         int8: bool = True, abs_v: bool = False):
+                         int8: bool = True, abs_v: bool = False, blocks=None):
     """float64 restatement of sage_unified_attention (sage_unified.py:234-313,
     kernel _attn_fwd_unified :112-231).  W > 0: int8 keys below wla(b), the
     fp16 causal window wla(b) <= j <= i; this is hybrid_prefill_fp64 with no
@@ -811,11 +859,12 @@ def unified_prefill_fp64(q, k, v, W: int, sm_scale: Optional[float] = None, smoo
     s = (q8 . k8) * q_scale * k_scale with K (smoothed) quantised per 64
     positions over the whole sequence (the int8 prefix segment :166-177 and
     the causal int8 diagonal :204-217).  int8=False scores every key with
-    q16 . k16 instead, which checks the W = 0 partition alone."""
+    q16 . k16 instead, which checks the W = 0 partition alone.  blocks: the
+    128-row query blocks to compute (default all; other rows stay zero)."""
     B, HQ, N, D = q.shape
     if W > 0:
         return hybrid_prefill_fp64(q, k, v, np.zeros((B, HQ, 0), np.int64), W, sm_scale, smooth,
-                                   int8_rest=int8, abs_v=abs_v)
+                                   int8_rest=int8, abs_v=abs_v, blocks=blocks)
     HKV = k.shape[1]
     G = HQ // HKV
     op = prefill_operands(q, k, v, sm_scale, smooth)
@@ -828,7 +877,8 @@ def unified_prefill_fp64(q, k, v, W: int, sm_scale: Optional[float] = None, smoo
             k8, ksc = per_block_int8(k16[b, hk], 1.0, PREFILL_BLOCK_N)
             kscale = np.repeat(ksc.astype(np.float64), PREFILL_BLOCK_N)[:N]
             for h in range(hk * G, (hk + 1) * G):
-                for blk in range((N + PREFILL_BLOCK_M - 1) // PREFILL_BLOCK_M):
+                nblk = (N + PREFILL_BLOCK_M - 1) // PREFILL_BLOCK_M
+                for blk in (range(nblk) if blocks is None else [int(x) for x in blocks]):
                     rows = np.arange(blk * PREFILL_BLOCK_M, min(N, (blk + 1) * PREFILL_BLOCK_M))
                     n = rows[-1] + 1
                     if int8:

@@ -40,8 +40,8 @@ def _L():
 
 def test_abi_version_and_error_strings():
     _lib, L = _L()
-    assert L.hyq_abi_version() == 2
-    st = L.hyq_quant_pack(None, 1, 1, 128, 0, 0, 3, None, 0, 0, None, 0, None)
+    assert L.hyq_abi_version() == 3
+    st = L.hyq_quant_pack(None, 0, 1, 1, 128, 0, 0, 3, None, 0, 0, None, 0, None)
     assert st == _lib.HYQ_EINVAL
     assert b"nbits must be 2, 4, or 8" in L.hyq_last_error()
     with pytest.raises(ValueError, match="nbits"):
@@ -50,12 +50,22 @@ def test_abi_version_and_error_strings():
 
 def test_quant_pack_host_validation():
     _lib, L = _L()
-    assert L.hyq_quant_pack(None, 1, 1, 100, 0, 0, 4, None, 0, 0, None, 0, None) == _lib.HYQ_ENOTSUP
-    assert L.hyq_quant_pack(None, -1, 1, 128, 0, 0, 4, None, 0, 0, None, 0, None) == _lib.HYQ_EINVAL
+    assert L.hyq_quant_pack(None, 0, 1, 1, 100, 0, 0, 4, None, 0, 0, None, 0, None) == _lib.HYQ_ENOTSUP
+    assert L.hyq_quant_pack(None, 1, -1, 1, 128, 0, 0, 4, None, 0, 0, None, 0, None) == _lib.HYQ_EINVAL
     # empty input is a no-op
-    assert L.hyq_quant_pack(None, 0, 5, 128, 0, 0, 4, None, 0, 0, None, 0, None) == _lib.HYQ_OK
+    assert L.hyq_quant_pack(None, 0, 0, 5, 128, 0, 0, 4, None, 0, 0, None, 0, None) == _lib.HYQ_OK
     # misaligned x
-    assert L.hyq_quant_pack(8, 1, 1, 128, 128, 128, 4, 16, 64, 64, 16, 1, None) == _lib.HYQ_EINVAL
+    assert L.hyq_quant_pack(8, 0, 1, 1, 128, 128, 128, 4, 16, 64, 64, 16, 1, None) == _lib.HYQ_EINVAL
+
+
+def test_dequant_host_validation():
+    _lib, L = _L()
+    assert L.hyq_dequant(None, 1, 1, 128, 0, 0, 3, None, 0, None, 0, 0, None) == _lib.HYQ_EINVAL
+    assert L.hyq_dequant(None, 1, 1, 100, 0, 0, 4, None, 0, None, 0, 0, None) == _lib.HYQ_ENOTSUP
+    # empty input is a no-op
+    assert L.hyq_dequant(None, 0, 7, 128, 0, 0, 4, None, 0, None, 0, 0, None) == _lib.HYQ_OK
+    # misaligned fp16 output rows (8 is not 16-byte aligned)
+    assert L.hyq_dequant(16, 1, 1, 128, 64, 64, 4, 16, 1, 8, 128, 128, None) == _lib.HYQ_EINVAL
 
 
 def _params(_lib, **kw):

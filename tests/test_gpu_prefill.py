@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from oracle import hyq_oracle as O
-from tests.gpu_util import to_dev_bf16
+from tests.gpu_util import exact_attention_gpu as _exact_attention_gpu, first_tile_max_inputs, to_dev_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -151,25 +151,6 @@ def test_prefill_options_and_strided_inputs():
     b = sage_vertical_attention_v2(qd.contiguous(), kd.contiguous(), vd.contiguous(), vi, window_size=W)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
-
-
-def _exact_attention_gpu(qd, kd, vd, chunk=1024):
-    """fp32 causal attention on the GPU, chunked over queries (test reference)."""
-    B, HQ, N, D = qd.shape
-    G = HQ // kd.shape[1]
-    out = torch.empty(B, HQ, N, D, dtype=torch.float32, device=qd.device)
-    for b in range(B):
-        for h in range(HQ):
-            kk = kd[b, h // G].float()
-            vv = vd[b, h // G].float()
-            for s in range(0, N, chunk):
-                qq = qd[b, h, s:s + chunk].float()
-                sc = (qq @ kk[: s + chunk].T.contiguous()) * D ** -0.5
-                i = torch.arange(s, s + qq.shape[0], device=qd.device)[:, None]
-                j = torch.arange(sc.shape[1], device=qd.device)[None, :]
-                sc = sc.masked_fill(j > i, float("-inf"))
-                out[b, h, s:s + chunk] = torch.softmax(sc, dim=-1) @ vv[: s + chunk]
-    return out
 
 
 @pytest.mark.parametrize("N", [8192, 16384])
@@ -323,3 +304,43 @@ def test_prefill_fp8qk_vs_oracle(cfg):
     ref = O.hybrid_prefill_fp64(q, k, v, vidx, W, qk_mode="fp8")
     ref_abs = O.hybrid_prefill_fp64(q, k, v, vidx, W, qk_mode="fp8", abs_v=True)
     _check(f"fp8qk {cfg}", out, ref, ref_abs)
+
+
+@pytest.mark.parametrize("cfg", [dict(B=1, HQ=4, HKV=1, N=1000, W=100, T=45, seed=51),
+                                 dict(B=1, HQ=8, HKV=2, N=2304, W=128, T=110, seed=52)],
+                         ids=["N1000", "N2304"])
+def test_prefill_fp8_pv_tight_where_running_max_is_exact(cfg):
+    """FP8 P.V (csrc/qattn/qk_int_sv_f8_cuda_sm90.cu:490-512,
+    attn_utils.cuh:354-458): P' = e4m3(exp2(s - m + 8.807)).  Where the
+    kernel's running max equals the row max from its first tile on, it must
+    round each P' to the same e4m3 value as the oracle, except for weights
+    that lie within a relative 2^-14 of an e4m3 (or fp16) rounding boundary,
+    where fp32 evaluation may take either neighbour (`slack`).  So the bf16
+    output must be the rounding of a value within
+        slack + 2^-13 sum P'|V|/l + 2^-15 |ref| + 1e-6
+    of the float64 fp8 restatement (fp32 accumulation and score rounding);
+    a systematic e4m3 error of ~3% of P' breaks this by an order of magnitude."""
+    print(f"prefill fp8 tight {cfg}", flush=True)
+    rng = np.random.default_rng(cfg["seed"])
+    B, HQ, HKV, N, W, T = (cfg[x] for x in ("B", "HQ", "HKV", "N", "W", "T"))
+    q, k, v, vidx = first_tile_max_inputs(rng, B, HQ, HKV, N, W, T)
+    out = _run(q, k, v, vidx, W, pv_mode="fp8")
+    ref, slack, exact = O.hybrid_prefill_fp64(q, k, v, vidx, W, pv_mode="fp8", fp8_detail=True)
+    ref_abs = O.hybrid_prefill_fp64(q, k, v, vidx, W, pv_mode="fp8", abs_v=True)
+    frac = float(exact.mean())
+    print(f"  rows with an exact running max: {frac:.4f}; mean slack {float(slack.mean()):.2e}", flush=True)
+    assert frac > 0.99
+    eps = slack + 2.0 ** -13 * ref_abs + 2.0 ** -15 * np.abs(ref) + 1e-6
+    from tests.gpu_util import bf16_bracket
+    bad = bf16_bracket(out, ref, eps) & exact[..., None]
+    diff = np.abs(out - ref)
+    print(f"  max-abs {float(diff.max()):.3e}, max |out-ref|/eps on exact rows "
+          f"{float((diff / eps)[np.broadcast_to(exact[..., None], diff.shape)].max()):.3f}", flush=True)
+    assert not bad.any(), f"{int(bad.sum())} elements outside the tight fp8 bound"
+    loose = ATOL + 2.0 ** -3 * ref_abs + 2.0 ** -8 * np.abs(ref)
+    assert not ((diff > loose) & ~exact[..., None]).any()
+    # the relative L2 error against the fp8 restatement, and what an e4m3
+    # rounding with truncation instead of round-to-nearest-even would give
+    l2 = float(np.linalg.norm(out - ref) / np.linalg.norm(ref))
+    print(f"  relative L2 vs the fp8 oracle {l2:.3e}", flush=True)
+    assert l2 < 2.0 ** -9

@@ -100,3 +100,66 @@ def test_quant_every_bf16_value_bit_exact(nbits):
     rp, rs = O.quantize_per_token(x, nbits)
     assert np.array_equal(scale.cpu().numpy().view(np.uint16), rs.view(np.uint16))
     assert np.array_equal(packed.cpu().numpy(), rp)
+
+
+@pytest.mark.parametrize("nbits", [4, 2, 8])
+def test_quant_pack_fp16_input_bit_exact(nbits):
+    """quantize_per_token on fp16 tokens (src/ops/decode_d_stage.py:50-77
+    takes bf16 or fp16: x.float() is exact for both): codes, bytes and scales
+    bit-exact with the oracle on the same values, including fp16 subnormals
+    and the largest finite fp16."""
+    import hyquant_amd as hq
+    rng = np.random.default_rng(300 + nbits)
+    BH, N, D = 5, 93, 128
+    x = (rng.standard_normal((BH, N, D)) * rng.uniform(1e-4, 300, (BH, N, 1))).astype(np.float16)
+    x[0, 0] = 0
+    x[0, 1, :] = np.float16(6.1e-5) * rng.integers(-3, 4, D)      # subnormal-scale tokens
+    x[0, 2, 0] = np.float16(65504.0)
+    x[0, 3, :8] = [7, -7, 3.5, -3.5, 0.5, 1.5, 2.5, -0.5]           # ties
+    xf = x.astype(np.float32)
+    packed, scale = hq.quantize_per_token(torch.from_numpy(x).cuda(), nbits)
+    torch.cuda.synchronize()
+    rp, rs = O.quantize_per_token(xf, nbits)
+    assert np.array_equal(packed.cpu().numpy(), rp)
+    assert np.array_equal(scale.cpu().numpy().view(np.uint16), rs.view(np.uint16))
+
+
+@pytest.mark.parametrize("nbits", [4, 2, 8])
+def test_dequant_bit_exact(nbits):
+    """dequantize_per_token (hyq_dequant) against the oracle's fp16(code *
+    scale) (src/ops/decode_d_stage.py:80-101): random packed bytes, so every
+    code occurs (the most negative one too), and scales across the fp16
+    range: subnormal, normal, products that overflow to inf and a zero."""
+    import hyquant_amd as hq
+    rng = np.random.default_rng(400 + nbits)
+    BH, N, D = 7, 131, 128
+    packed = rng.integers(-128, 128, size=(BH, N, 16 * nbits), dtype=np.int8)
+    scale = np.exp(rng.uniform(np.log(1e-7), np.log(6e4), size=(BH, N))).astype(np.float16)
+    scale[0, :4] = [0.0, np.float16(6e-8), np.float16(65504.0), np.float16(1.0)]
+    codes = O.unpack_codes(packed, nbits)
+    assert codes.min() == -(2 ** (nbits - 1)) and codes.max() == 2 ** (nbits - 1) - 1
+    got = hq.dequantize_per_token(torch.from_numpy(packed).cuda(), torch.from_numpy(scale).cuda(), D, nbits)
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float16 and tuple(got.shape) == (BH, N, D)
+    exp = O.dequantize_per_token(packed, scale, nbits).astype(np.float16)
+    assert np.array_equal(got.cpu().numpy().view(np.uint16), exp.view(np.uint16))
+
+
+def test_dequant_round_trip_of_quantised_cache():
+    """quantize then dequantize on the device: |x - deq(x)| <= scale / 2 (plus
+    the fp16 rounding of the product) on the benchmark distribution, and a
+    strided (head-sliced) packed input gives the same bytes as a contiguous one."""
+    import hyquant_amd as hq
+    inp = O.make_decode_inputs(B=1, HQ=32, HKV=8, N=1024, W=128, S=37, seed=3)
+    x = inp.keys.reshape(8, 1024, 128)
+    xd = to_dev_bf16(x, "cuda")
+    packed, scale = hq.quantize_per_token(xd, 4)
+    deq = hq.dequantize_per_token(packed, scale, 128, 4).float().cpu().numpy()
+    s = scale.float().cpu().numpy()[..., None]
+    assert np.all(np.abs(x - deq) <= s / 2 + np.abs(deq) * 2.0 ** -11 + 1e-7)
+    wide = torch.zeros(8, 1024, 96, dtype=torch.int8, device="cuda")
+    wide[:, :, 16:80] = packed
+    a = hq.dequantize_per_token(wide[:, :, 16:80], scale, 128, 4)
+    b = hq.dequantize_per_token(packed, scale, 128, 4)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))

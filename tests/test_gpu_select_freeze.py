@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle import hyq_oracle as O
-from tests.gpu_util import to_dev_bf16
+from tests.gpu_util import cache_from_inputs as _cache_from_inputs, check_layer_state as _check_state, to_dev_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -73,33 +73,6 @@ def test_selector_freeze_variant_and_prefill_on_config_inputs(cfg):
     assert np.array_equal(got_q.cpu().numpy(), exp_q)
 
 
-def _cache_from_inputs(inp, k_bits=4, v_bits=4):
-    from hyquant_amd.d_stage_kv_cache import DStageLayerCache
-    layer = DStageLayerCache(0, k_bits=k_bits, v_bits=v_bits, window_size=inp.W, top_ratio=inp.rho)
-    half = inp.N // 2
-    kd, vd = to_dev_bf16(inp.keys, "cuda"), to_dev_bf16(inp.values, "cuda")
-    layer.update_prefill(kd[:, :, :half], vd[:, :, :half])      # two prefill chunks
-    layer.update_prefill(kd[:, :, half:], vd[:, :, half:])
-    layer.save_query_tail(to_dev_bf16(inp.query_tail, "cuda"))
-    layer.freeze(kv_repeat=inp.HQ // inp.HKV)
-    return layer
-
-
-def _check_state(layer, st):
-    np_ = lambda t: t.cpu().numpy()
-    assert np.array_equal(np_(layer.topk_indices), st.topk_idx)
-    assert np.array_equal(np_(layer.k_quant_packed), st.k_packed)
-    assert np.array_equal(np_(layer.v_quant_packed), st.v_packed)
-    assert np.array_equal(np_(layer.k_scale).view(np.uint16), st.k_scale.view(np.uint16))
-    assert np.array_equal(np_(layer.v_scale).view(np.uint16), st.v_scale.view(np.uint16))
-    assert np.array_equal(np_(layer.k_topk.float()), st.k_topk)
-    assert np.array_equal(np_(layer.v_topk.float()), st.v_topk)
-    assert np.array_equal(np_(layer.k_window.float()), st.k_window)
-    assert np.array_equal(np_(layer.v_window.float()), st.v_window)
-    assert layer._staging_ptr == st.ring_ptr
-    assert np.array_equal(np_(layer._staging_buf_k[:, :st.ring_ptr].float()), st.k_staging)
-
-
 @pytest.mark.parametrize("cfg", [dict(B=1, HQ=32, HKV=8, N=1024, S=37), dict(B=2, HQ=32, HKV=8, N=8192, S=64)])
 def test_cache_freeze_flush_decode(cfg):
     print(f"cache {cfg}", flush=True)
@@ -129,10 +102,18 @@ def test_cache_freeze_flush_decode(cfg):
     assert err <= 2e-3
 
 
-def test_cache_k4v2_freeze_bit_exact_and_decode():
+BIT_PAIRS = [(4, 4), (4, 2), (2, 4), (8, 8), (2, 2), (4, 8), (8, 4), (2, 8), (8, 2)]
+
+
+@pytest.mark.parametrize("kb,vb", BIT_PAIRS)
+def test_cache_freeze_every_bit_pair_bit_exact_and_decode(kb, vb):
+    """Every (k_bits, v_bits) pair the mode table and the decode accept
+    (src/ops/d_stage_kv_cache.py:167-168 quantises K and V with their own
+    widths): freeze bit-exact, then decode through the cache."""
+    print(f"cache freeze K{kb}V{vb}", flush=True)
     inp = O.make_decode_inputs(B=1, HQ=32, HKV=8, N=1024, W=128, S=9, seed=12)
-    layer = _cache_from_inputs(inp, k_bits=4, v_bits=2)
-    st = O.freeze(inp.keys, inp.values, inp.query_tail, inp.W, inp.rho, 4, k_bits=4, v_bits=2)
+    layer = _cache_from_inputs(inp, k_bits=kb, v_bits=vb)
+    st = O.freeze(inp.keys, inp.values, inp.query_tail, inp.W, inp.rho, 4, k_bits=kb, v_bits=vb)
     layer.append_staging(to_dev_bf16(inp.k_new, "cuda"), to_dev_bf16(inp.v_new, "cuda"))
     O.append_staging(st, inp.k_new, inp.v_new)
     torch.cuda.synchronize()
@@ -140,8 +121,9 @@ def test_cache_k4v2_freeze_bit_exact_and_decode():
     q = to_dev_bf16(inp.q_dec, "cuda").reshape(1, 32, 1, 128)
     out = layer.decode_attention(q, 4).reshape(-1, 128).float().cpu().numpy()
     ref = O.decode_fp64_state(inp.q_dec, st, 4)
-    # the reference's own bf16 eager math for non-K4V4 modes
-    assert float(np.max(np.abs(out - ref))) <= 2e-2
+    err = float(np.max(np.abs(out - ref)))
+    print(f"  K{kb}V{vb} cache decode max-abs {err:.3e}", flush=True)
+    assert err <= 2e-3
 
 
 def test_cache_short_prompt_no_prefix():
@@ -156,7 +138,7 @@ def test_cache_short_prompt_no_prefix():
     assert float(np.max(np.abs(out - O.decode_fp64_state(inp.q_dec, st, 4)))) <= 2e-3
 
 
-@pytest.mark.parametrize("kv", [(4, 4), (4, 2)])
+@pytest.mark.parametrize("kv", BIT_PAIRS)
 def test_cache_save_load_resumes_bit_identically(tmp_path, kv):
     """A frozen cache written to disk and read back decodes exactly like the
     original, before and after the staging ring flushes into the prefix."""
@@ -194,3 +176,58 @@ def test_cache_save_load_resumes_bit_identically(tmp_path, kv):
     b = lb.decode_attention(q, G)
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     assert back.get_seq_length(0) == cache.get_seq_length(0) == inp.N + 37 + 100
+
+
+def test_freeze_bad_indices_stay_inside_the_outputs():
+    """hyq_freeze_reorganise with repeated and out-of-range top-k indices (an
+    ABI precondition violation): an index outside [0, n - w) yields a zero
+    row, nothing is written past the n - w - top_k compact rows, and the
+    rows that are written are the right ones (ascending unselected positions)."""
+    from hyquant_amd import _lib
+    rng = np.random.default_rng(17)
+    HK, N, W, T = 2, 600, 64, 20
+    P = N - W
+    k = _rand_bf16(rng, (1, HK, N, 128))
+    v = _rand_bf16(rng, (1, HK, N, 128))
+    idx = np.stack([rng.permutation(P)[:T] for _ in range(HK)]).astype(np.int64)
+    idx[0, 3] = idx[0, 2]             # a repeat: one position marked, T - 1 distinct
+    idx[1, 5] = P + 7                 # a window position: out of [0, P)
+    idx[1, 6] = -4                    # negative
+    dev = torch.device("cuda")
+    kd, vd = to_dev_bf16(k, dev), to_dev_bf16(v, dev)
+    nc = P - T
+    GUARD = 64
+    kp = torch.full((HK, nc + GUARD, 64), 0x5A, dtype=torch.int8, device=dev)
+    vp = torch.full((HK, nc + GUARD, 64), 0x5A, dtype=torch.int8, device=dev)
+    ks = torch.full((HK, nc + GUARD), 7.0, dtype=torch.float16, device=dev)
+    vs = torch.full((HK, nc + GUARD), 7.0, dtype=torch.float16, device=dev)
+    kt = torch.empty(HK, T, 128, dtype=torch.bfloat16, device=dev)
+    vt = torch.empty_like(kt)
+    kw = torch.empty(HK, W, 128, dtype=torch.bfloat16, device=dev)
+    vw = torch.empty_like(kw)
+    ti = torch.from_numpy(idx).to(dev)
+    L = _lib.lib()
+    ws = torch.empty(max(L.hyq_freeze_workspace_size(HK, P), 256), dtype=torch.uint8, device=dev)
+    st = L.hyq_freeze_reorganise(
+        kd.data_ptr(), kd.stride(0), kd.stride(1), kd.stride(2), vd.data_ptr(), vd.stride(0), vd.stride(1),
+        vd.stride(2), 1, HK, N, 128, W, ti.data_ptr(), T, 4, 4,
+        kp.data_ptr(), kp.stride(0), kp.stride(1), vp.data_ptr(), vp.stride(0), vp.stride(1),
+        ks.data_ptr(), ks.stride(0), vs.data_ptr(), vs.stride(0),
+        kt.data_ptr(), kt.stride(0), kt.stride(1), vt.data_ptr(), vt.stride(0), vt.stride(1),
+        kw.data_ptr(), kw.stride(0), kw.stride(1), vw.data_ptr(), vw.stride(0), vw.stride(1),
+        ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    _lib.check(st, "freeze")
+    torch.cuda.synchronize()
+    assert bool((kp[:, nc:] == 0x5A).all()) and bool((vp[:, nc:] == 0x5A).all())
+    assert bool((ks[:, nc:] == 7.0).all()) and bool((vs[:, nc:] == 7.0).all())
+    ktn = kt.float().cpu().numpy()
+    assert not ktn[1, 5].any() and not ktn[1, 6].any()
+    assert np.array_equal(ktn[0, 3], k[0, 0, idx[0, 3]])
+    for h in range(HK):
+        sel = np.zeros(P, bool)
+        good = idx[h][(idx[h] >= 0) & (idx[h] < P)]
+        sel[good] = True
+        rest = np.nonzero(~sel)[0][:nc]
+        rp, rs = O.quantize_per_token(k[0, h][rest][None], 4)
+        assert np.array_equal(kp[h, :nc].cpu().numpy(), rp[0])
+        assert np.array_equal(ks[h, :nc].cpu().numpy().view(np.uint16), rs[0].view(np.uint16))

@@ -379,3 +379,82 @@ def test_fp8_prefill_error_against_exact_attention():
     # e4m3 keeps 3 mantissa bits: P8 and V8 each within 2^-4 relative
     assert np.all(np.abs(f8 - f16) <= 2.0 ** -3 * ref_abs + 1e-6)
     assert mse8 < 1e-3
+
+
+def test_prefill_blocks_option_equals_full_computation():
+    """Restricting the restatement to some query blocks gives those rows
+    exactly as the full computation does (and zeros elsewhere), for the
+    hybrid, fp8 and window-only forms."""
+    rng = np.random.default_rng(61)
+    q = O.bf16_round(rng.standard_normal((1, 2, 700, 128)).astype(np.float32))
+    k = O.bf16_round(rng.standard_normal((1, 1, 700, 128)).astype(np.float32) * 1.5)
+    v = O.bf16_round(rng.standard_normal((1, 1, 700, 128)).astype(np.float32))
+    vidx = rng.permutation(600)[:40].reshape(1, 1, 40).repeat(2, axis=1)
+    blocks = [0, 3, 5]
+    rows = np.concatenate([np.arange(b * 128, min(700, (b + 1) * 128)) for b in blocks])
+    other = np.setdiff1d(np.arange(700), rows)
+    for kw in ({}, {"pv_mode": "fp8"}, {"qk_mode": "fp8"}):
+        full = O.hybrid_prefill_fp64(q, k, v, vidx, 100, **kw)
+        part = O.hybrid_prefill_fp64(q, k, v, vidx, 100, blocks=blocks, **kw)
+        assert np.array_equal(part[:, :, rows], full[:, :, rows]) and not part[:, :, other].any()
+    full = O.unified_prefill_fp64(q, k, v, 100)
+    part = O.unified_prefill_fp64(q, k, v, 100, blocks=blocks)
+    assert np.array_equal(part[:, :, rows], full[:, :, rows])
+    full = O.unified_prefill_fp64(q, k, v, 0)
+    part = O.unified_prefill_fp64(q, k, v, 0, blocks=blocks)
+    assert np.array_equal(part[:, :, rows], full[:, :, rows])
+
+
+def test_round_span_brackets_every_perturbed_rounding():
+    """_round_span(x) is zero exactly where every x' within a relative
+    FP8_AMBIGUITY of x rounds like x (e4m3 and fp16), and otherwise equals the
+    step between the two possible roundings: checked by brute force over
+    random perturbations, and on a known e4m3 midpoint (1.0625 between 1 and
+    1.125) and a value far from any midpoint (1.03)."""
+    rng = np.random.default_rng(62)
+    x = np.exp2(rng.uniform(-12, 8.8, 200000))
+    f16 = lambda t: O.to_fp16(np.asarray(t, np.float32)).astype(np.float64)
+    for rnd in (O.e4m3_round, f16):
+        span = O._round_span(x, rnd, O.FP8_AMBIGUITY)
+        base = rnd(x)
+        for _ in range(4):
+            d = rng.uniform(-1, 1, x.shape) * O.FP8_AMBIGUITY
+            moved = rnd(x * (1 + d))
+            assert np.all((moved == base) | (span > 0))
+            assert np.all(np.abs(moved - base) <= span + 0.0)
+    assert O._round_span(np.array([1.0625]), O.e4m3_round, 2.0 ** -14)[0] == 0.125
+    assert O._round_span(np.array([1.03]), O.e4m3_round, 2.0 ** -14)[0] == 0.0
+
+
+def test_fp8_tight_bound_rejects_planted_rounding_mistakes():
+    """The bound of the GPU test test_prefill_fp8_pv_tight_where_running_max_is_exact
+    has teeth: on its input family the honest restatement (rounded to bf16)
+    satisfies it everywhere, while a restatement whose e4m3 rounding truncates,
+    or scales every rest-key P' by 1%, violates it on most elements."""
+    from tests.gpu_util import bf16_bracket, first_tile_max_inputs
+    rng = np.random.default_rng(51)
+    q, k, v, vidx = first_tile_max_inputs(rng, 1, 4, 1, 1000, 100, 45)
+    ref, slack, exact = O.hybrid_prefill_fp64(q, k, v, vidx, 100, pv_mode="fp8", fp8_detail=True)
+    ref_abs = O.hybrid_prefill_fp64(q, k, v, vidx, 100, pv_mode="fp8", abs_v=True)
+    eps = slack + 2.0 ** -13 * ref_abs + 2.0 ** -15 * np.abs(ref) + 1e-6
+    assert exact.mean() > 0.99
+    ex = exact[..., None]
+    assert not (bf16_bracket(O.bf16_round_f64(ref), ref, eps) & ex).any()
+    honest = O.e4m3_round
+
+    def truncating(x):
+        x = np.asarray(x, np.float64)
+        a = np.minimum(np.abs(x), O.FP8_MAX)
+        with np.errstate(divide="ignore"):
+            e = np.maximum(np.floor(np.log2(np.where(a > 0, a, 1.0))), -6.0)
+        r = np.floor(a / np.exp2(e - 3.0)) * np.exp2(e - 3.0)
+        return np.where(x < 0, -r, r)
+
+    try:
+        for planted in (truncating, lambda x: honest(np.asarray(x) * 1.01)):
+            O.e4m3_round = planted
+            wrong = O.bf16_round_f64(O.hybrid_prefill_fp64(q, k, v, vidx, 100, pv_mode="fp8"))
+            O.e4m3_round = honest
+            assert (bf16_bracket(wrong, ref, eps) & ex).mean() > 0.3
+    finally:
+        O.e4m3_round = honest

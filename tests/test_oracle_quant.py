@@ -126,6 +126,66 @@ def test_dequantize_fp16():
     assert deq.tolist() == [[[7, -7, 4, -4, 0, 2, 2, 0]]]
 
 
+def _fp16_rne_exact(v):
+    """fp16 bits of the rational v, rounded to nearest even from first
+    principles (normal and subnormal ranges, overflow to inf)."""
+    import math
+    from fractions import Fraction
+    sign = 0x8000 if math.copysign(1.0, v) < 0 else 0        # -2 * 0.0 is -0.0
+    v = Fraction(v)
+    a = abs(v)
+    if a == 0:
+        return sign
+    e = max(a.numerator.bit_length() - a.denominator.bit_length() + 1, -13)
+    while Fraction(2) ** e <= a:       # normalise to 2^(e-1) <= a < 2^e (or the subnormal range)
+        e += 1
+    while e > -13 and Fraction(2) ** (e - 1) > a:
+        e -= 1
+    quantum = Fraction(2) ** (max(e, -13) - 11)                 # 11 significant bits; 2^-24 below 2^-14
+    n = a / quantum
+    r = n.numerator // n.denominator
+    rem = n - r
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and r % 2 == 1):
+        r += 1
+    val = r * quantum
+    if val >= 65520 or val > 65504:
+        return sign | 0x7C00
+    return sign | int(np.float16(float(val)).view(np.uint16))
+
+
+def test_dequantize_against_exact_rounding_and_torch():
+    """fp16(code * scale) for every code of 2, 4 and 8 bits and scales over the
+    whole fp16 range (subnormal, normal, near overflow): against an exact
+    rational round-to-nearest-even, and against the reference's own torch
+    expression (q.float() * scale.float()).to(torch.float16)."""
+    import torch
+    rng = np.random.default_rng(21)
+    scales = np.concatenate([np.exp(rng.uniform(np.log(6e-8), np.log(6.5e4), 60)),
+                             [0.0, 6e-8, 6.1e-5, 65504.0, 1.0, 1 / 3]]).astype(np.float16)
+    for nbits in (2, 4, 8):
+        ncode = 2 ** nbits
+        codes = np.arange(-(ncode // 2), ncode // 2, dtype=np.int8)
+        D = max(8, ncode)
+        reps = -(-D // len(codes))
+        row = np.tile(codes, reps)[:D]
+        c = np.broadcast_to(row, (1, len(scales), D)).astype(np.int8)
+        if nbits == 4:
+            packed = O.pack_int4(c)
+        elif nbits == 2:
+            packed = O.pack_int2(c)
+        else:
+            packed = c.copy()
+        sc = scales[None, :]
+        deq = O.dequantize_per_token(packed, sc, nbits).astype(np.float16).view(np.uint16)
+        for i, s16 in enumerate(scales):
+            for j in range(D):
+                exp = _fp16_rne_exact(int(row[j]) * float(s16))
+                assert deq[0, i, j] == exp, (nbits, float(s16), int(row[j]))
+        qt = torch.from_numpy(O.unpack_codes(packed, nbits).astype(np.float32))
+        ref = (qt * torch.from_numpy(sc).float().unsqueeze(-1)).to(torch.float16)
+        assert np.array_equal(ref.numpy().view(np.uint16), deq)
+
+
 def test_bad_bits():
     with pytest.raises(ValueError):
         O.quantize_per_token(np.zeros((1, 1, 8), np.float32), 3)

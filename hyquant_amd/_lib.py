@@ -35,6 +35,7 @@ EXPORTS = (
     "hyq_freeze_workspace_size",
     "hyq_freeze_reorganise",
     "hyq_per_block_int8",
+    "hyq_prefill_lists_workspace_size",
     "hyq_prefill_lists",
     "hyq_prefill_workspace_size",
     "hyq_prefill_hybrid",
@@ -106,7 +107,7 @@ def _declare(lib):
                                     c_int64, c_int32, c_int32, c_int32, c_float,
                                     c_void_p, c_size_t, c_void_p]
     lib.hyq_vertical_select_workspace_size.restype = c_size_t
-    lib.hyq_vertical_select_workspace_size.argtypes = [c_int32, c_int32, c_int64]
+    lib.hyq_vertical_select_workspace_size.argtypes = [c_int32, c_int32, c_int64, c_int32]
     lib.hyq_vertical_select.restype = c_int
     lib.hyq_vertical_select.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32,
                                         c_void_p, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32,
@@ -124,8 +125,11 @@ def _declare(lib):
                                         c_int32, c_float, c_int32, c_void_p, c_int64, c_int64,
                                         c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p])
     lib.hyq_prefill_lists.restype = c_int
+    lib.hyq_prefill_lists_workspace_size.restype = c_size_t
+    lib.hyq_prefill_lists_workspace_size.argtypes = [c_int32, c_int32, c_int64, c_int64, c_int32]
     lib.hyq_prefill_lists.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int64, c_int64,
-                                      c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
+                                      c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                      c_void_p, c_size_t, c_void_p]
     lib.hyq_prefill_workspace_size.restype = c_size_t
     lib.hyq_prefill_workspace_size.argtypes = [c_int32, c_int32, c_int32, c_int64, c_int64, c_int32, c_int32]
     lib.hyq_prefill_hybrid.restype = c_int

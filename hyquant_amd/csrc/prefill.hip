@@ -70,8 +70,8 @@ constexpr float PF_M_INIT = -1.0e30f;
 constexpr float FP8_MAX = 448.0f;        // src/ops/sage_unified_fp8.py:44
 constexpr float S_FP8_OFFSET = 8.807f;   // vendor/sageattention/csrc/qattn/attn_utils.cuh:30 (log2 448)
 constexpr int LIST_THREADS = 1024;
-constexpr int MAX_T = 8192;              // vertical indices per head
-constexpr int64_t MAX_P = 131072;        // prefix positions N - W per head
+constexpr int64_t MAX_T = 1 << 26;        // vertical indices per head
+constexpr int64_t MAX_P = 1 << 26;        // prefix positions N - W per head
 constexpr int STAT_ROWS = 128;           // rows per kv_stats chunk
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -360,20 +360,24 @@ __device__ int block_exclusive_scan(int v, int* s_w) {
     return s_w[w] + x - v;
 }
 
-// grid (B*HQ), 1024 threads.  Dynamic LDS: sorted list [n2], bitmap [nw],
-// rest count before each word [nw], scan scratch [32].
+// grid (B*HQ), 1024 threads.  Per row: sorted list [n2], bitmap [nw], rest
+// count before each word [nw], in dynamic LDS, or (GL) in this row's slice
+// of a global scratch when they do not fit the LDS budget.
+template <bool GL>
 __global__ __launch_bounds__(LIST_THREADS) void lists_kernel(const int64_t* __restrict__ vidx, int64_t vi_b,
                                                              int64_t vi_h, int64_t vi_t, int HQ, int T, int n2,
                                                              int P, int nblk, int W, int32_t* __restrict__ vert,
                                                              int32_t* __restrict__ rest, int32_t* __restrict__ rcount,
-                                                             int32_t* __restrict__ nr, int32_t* __restrict__ nv) {
+                                                             int32_t* __restrict__ nr, int32_t* __restrict__ nv,
+                                                             int* __restrict__ gscratch) {
     extern __shared__ int s_lists[];
+    __shared__ int s_scan[LIST_THREADS / 64 + 1];
     const int nw = (P + 31) >> 5;
-    int* s_sort = s_lists;
-    uint32_t* s_bm = reinterpret_cast<uint32_t*>(s_lists + n2);
-    int* s_pre = s_lists + n2 + nw;
-    int* s_scan = s_pre + nw;
     const int bh = blockIdx.x, b = bh / HQ, h = bh % HQ;
+    int* const lbase = GL ? gscratch + static_cast<int64_t>(bh) * (n2 + 2 * static_cast<int64_t>(nw)) : s_lists;
+    int* s_sort = lbase;
+    uint32_t* s_bm = reinterpret_cast<uint32_t*>(lbase + n2);
+    int* s_pre = lbase + n2 + nw;
     const int tid = threadIdx.x;
     const int64_t* vrow = vidx + b * vi_b + h * vi_h;
     for (int i = tid; i < n2; i += LIST_THREADS) {
@@ -1098,8 +1102,37 @@ __global__ __launch_bounds__(256) void zero_counts_kernel(int32_t* __restrict__ 
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
+int next_pow2(int x) {
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+// LDS a workgroup may allocate dynamically on the current device
+size_t lds_budget() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
+    if (cache[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            v = 64 * 1024;
+        cache[dev] = v;
+    }
+    return static_cast<size_t>(cache[dev]) - 1024;   // the kernel's static LDS
+}
+
+// ints of one row's list scratch (sorted list, bitmap, per-word prefix)
+int64_t lists_row_ints(int64_t T, int64_t P) {
+    return next_pow2(static_cast<int>(std::max<int64_t>(T, 1))) + 2 * ((P + 31) / 32);
+}
+
+// do one row's list arrays fit the LDS budget?
+bool lists_in_lds(int64_t T, int64_t P) { return static_cast<size_t>(lists_row_ints(T, P)) * 4 <= lds_budget(); }
+
 struct PrefillLayout {
-    size_t kpart, vpart, km, vscale, k16, v16, v8, vert, rest, rcount, nr, nv, k8r, k8r_scale, vr, kv16, vv16, total;
+    size_t kpart, vpart, km, vscale, k16, v16, v8, vert, rest, rcount, nr, nv, k8r, k8r_scale, vr, kv16, vv16,
+        lscratch, total;
 };
 
 PrefillLayout prefill_layout(int B, int HQ, int HKV, int64_t N, int64_t T, int W, int pv_mode) {
@@ -1128,31 +1161,31 @@ PrefillLayout prefill_layout(int B, int HQ, int HKV, int64_t N, int64_t T, int W
     L.vr = take(BH * P * PD * (pv_mode ? 1 : 2));
     L.kv16 = take(BH * T * PD * 2);
     L.vv16 = take(BH * T * PD * 2);
+    L.lscratch = (P > 0 && !lists_in_lds(T, P)) ? take(BH * lists_row_ints(T, P) * 4) : 0;
     L.total = off;
     return L;
 }
 
-int next_pow2(int x) {
-    int p = 1;
-    while (p < x) p <<= 1;
-    return p;
-}
-
 int launch_lists(const int64_t* vidx, int64_t vi_b, int64_t vi_h, int64_t vi_t, int BH, int H, int T, int P,
                  int nblk, int W, int32_t* vert, int32_t* rest, int32_t* rcount, int32_t* nr, int32_t* nv,
-                 hipStream_t stream) {
+                 int* gscratch, hipStream_t stream) {
     static bool attr_set = false;
     const int n2 = next_pow2(std::max(T, 1));
-    const int nw = (P + 31) / 32;
-    const size_t lds = sizeof(int) * (static_cast<size_t>(n2) + 2 * nw + 32);
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(lists_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-            return fail(HYQ_EDEVICE, "prefill lists: cannot raise the LDS limit of lists_kernel");
-        attr_set = true;
+    if (lists_in_lds(T, P)) {
+        const size_t lds = sizeof(int) * static_cast<size_t>(lists_row_ints(T, P));
+        if (!attr_set && lds > 64 * 1024) {
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(&lists_kernel<false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_budget())) != hipSuccess)
+                return fail(HYQ_EDEVICE, "prefill lists: cannot raise the LDS limit of lists_kernel");
+            attr_set = true;
+        }
+        hipLaunchKernelGGL(lists_kernel<false>, dim3(BH), dim3(LIST_THREADS), lds, stream, vidx, vi_b, vi_h, vi_t, H, T,
+                           n2, P, nblk, W, vert, rest, rcount, nr, nv, nullptr);
+    } else {
+        if (!gscratch) return fail(HYQ_ENOSPC, "prefill lists: no scratch for lists larger than LDS");
+        hipLaunchKernelGGL(lists_kernel<true>, dim3(BH), dim3(LIST_THREADS), 0, stream, vidx, vi_b, vi_h, vi_t, H, T,
+                           n2, P, nblk, W, vert, rest, rcount, nr, nv, gscratch);
     }
-    hipLaunchKernelGGL(lists_kernel, dim3(BH), dim3(LIST_THREADS), lds, stream, vidx, vi_b, vi_h, vi_t, H, T, n2, P,
-                       nblk, W, vert, rest, rcount, nr, nv);
     return check_launch("lists_kernel");
 }
 
@@ -1189,14 +1222,22 @@ extern "C" int hyq_per_block_int8(const void* x, int32_t x_is_fp16, int64_t xs_b
     return check_launch("per_block_int8_kernel");
 }
 
+extern "C" size_t hyq_prefill_lists_workspace_size(int32_t b, int32_t h, int64_t n, int64_t t, int32_t window) {
+    if (b <= 0 || h <= 0 || n <= 0 || t < 0 || window < 0) return 0;
+    const int64_t P = std::max<int64_t>(0, n - window);
+    if (P == 0 || P > MAX_P || t > MAX_T || lists_in_lds(t, P)) return 0;
+    return static_cast<size_t>(b) * h * lists_row_ints(t, P) * 4;
+}
+
 extern "C" int hyq_prefill_lists(const int64_t* vidx, int64_t vi_b, int64_t vi_h, int64_t vi_t, int32_t b,
                                  int32_t h, int64_t n, int64_t t, int32_t window, int32_t* vert, int32_t* rest,
-                                 int32_t* rcount, int32_t* nr, int32_t* nv, void* stream) {
+                                 int32_t* rcount, int32_t* nr, int32_t* nv, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
     if (b < 0 || h < 0 || n < 0 || t < 0 || window < 0 || n > INT32_MAX / 2)
         return fail(HYQ_EINVAL, "hyq_prefill_lists: invalid sizes");
     const int64_t P = std::max<int64_t>(0, n - window);
-    if (P > MAX_P) return fail(HYQ_ENOTSUP, "hyq_prefill_lists: n - window exceeds 131072");
-    if (t > MAX_T) return fail(HYQ_ENOTSUP, "hyq_prefill_lists: more than 8192 indices per head");
+    if (P > MAX_P) return fail(HYQ_ENOTSUP, "hyq_prefill_lists: n - window exceeds 2^26");
+    if (t > MAX_T) return fail(HYQ_ENOTSUP, "hyq_prefill_lists: more than 2^26 indices per head");
     if (b == 0 || h == 0 || n == 0) return HYQ_OK;
     const int nblk = static_cast<int>((n + BM - 1) / BM);
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1208,8 +1249,11 @@ extern "C" int hyq_prefill_lists(const int64_t* vidx, int64_t vi_b, int64_t vi_h
     }
     if ((t > 0 && (!vidx || !vert)) || !rest || !rcount || !nr || !nv)
         return fail(HYQ_EINVAL, "hyq_prefill_lists: null pointer");
+    const size_t need = hyq_prefill_lists_workspace_size(b, h, n, t, window);
+    if (need > 0 && (!workspace || workspace_bytes < need || !aligned(workspace, 4)))
+        return fail(HYQ_ENOSPC, "hyq_prefill_lists: workspace too small (need " + std::to_string(need) + " bytes)");
     return launch_lists(vidx, vi_b, vi_h, vi_t, b * h, h, static_cast<int>(t), static_cast<int>(P), nblk, window, vert,
-                        rest, rcount, nr, nv, s);
+                        rest, rcount, nr, nv, need > 0 ? static_cast<int*>(workspace) : nullptr, s);
 }
 
 namespace hyq {
@@ -1226,8 +1270,8 @@ int prefill_run(const hyq_prefill_params* p, void* ws, size_t ws_bytes, hipStrea
     if (B <= 0 || HQ <= 0 || HKV <= 0 || HQ % HKV || N <= 0 || N > INT32_MAX / 2 || T < 0 || W < 0)
         return fail(HYQ_EINVAL, name + ": invalid sizes (need HQ % HKV == 0, N > 0)");
     const int64_t P = std::max<int64_t>(0, N - W);
-    if (P > MAX_P) return fail(HYQ_ENOTSUP, name + ": N - window exceeds 131072");
-    if (T > MAX_T) return fail(HYQ_ENOTSUP, name + ": more than 8192 vertical indices per head");
+    if (P > MAX_P) return fail(HYQ_ENOTSUP, name + ": N - window exceeds 2^26");
+    if (T > MAX_T) return fail(HYQ_ENOTSUP, name + ": more than 2^26 vertical indices per head");
     if (!p->q || !p->k || !p->v || !p->out || (P > 0 && T > 0 && !p->vidx))
         return fail(HYQ_EINVAL, name + ": null pointer");
     auto rows16 = [](const void* ptr, int64_t sb, int64_t sh, int64_t sn) {
@@ -1271,7 +1315,8 @@ int prefill_run(const hyq_prefill_params* p, void* ws, size_t ws_bytes, hipStrea
         if (int st = launch_lists(p->vidx, p->vi_stride_b, p->vi_stride_h, p->vi_stride_t, BH, HQ, Ti, Pi, nblk, W,
                                   static_cast<int32_t*>(at(L.vert)), static_cast<int32_t*>(at(L.rest)),
                                   static_cast<int32_t*>(at(L.rcount)), static_cast<int32_t*>(at(L.nr)),
-                                  static_cast<int32_t*>(at(L.nv)), stream))
+                                  static_cast<int32_t*>(at(L.nv)),
+                                  L.lscratch ? static_cast<int*>(at(L.lscratch)) : nullptr, stream))
             return st;
         const int nvb = (Ti + BN - 1) / BN;
         hipLaunchKernelGGL(gather_kernel, dim3(nsb + nvb, BH), dim3(256), 0, stream,

@@ -114,15 +114,22 @@ __global__ __launch_bounds__(256) void dequant_kernel(
     } else {
         lo = reinterpret_cast<const uint16_t*>(prow)[sub];
     }
-    const float sf = f16_bits_to_f32(scale[ib * ss_bh + in]);
+    // fp16(code * scale) as sign | fp16(|code| * |scale|): the product of the
+    // magnitudes is exact in fp32 and rounds like the signed one, and the
+    // sign is set explicitly because the compiler fuses the product and the
+    // fp16 rounding into one fma with a +0 addend, which turns a -0 product
+    // (negative code, zero scale) into +0
+    const uint16_t sbits = scale[ib * ss_bh + in];
+    const float smag = f16_bits_to_f32(static_cast<uint16_t>(sbits & 0x7fffu));
+    const uint32_t ssign = sbits & 0x8000u;
+    auto deq = [&](int c) -> uint32_t {
+        const _Float16 m = static_cast<_Float16>(static_cast<float>(c < 0 ? -c : c) * smag);
+        return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, m)) | ((c < 0 ? 0x8000u : 0u) ^ ssign);
+    };
     uint32_t o[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const _Float16 a = static_cast<_Float16>(static_cast<float>(code_at<NBITS>(lo, hi, 2 * j)) * sf);
-        const _Float16 b = static_cast<_Float16>(static_cast<float>(code_at<NBITS>(lo, hi, 2 * j + 1)) * sf);
-        o[j] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-               (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
-    }
+    for (int j = 0; j < 4; ++j)
+        o[j] = deq(code_at<NBITS>(lo, hi, 2 * j)) | (deq(code_at<NBITS>(lo, hi, 2 * j + 1)) << 16);
     reinterpret_cast<uint4*>(out + ib * os_bh + in * os_n)[sub] = make_uint4(o[0], o[1], o[2], o[3]);
 }
 

@@ -36,8 +36,8 @@ namespace hyq {
 namespace {
 
 constexpr int TOPK_THREADS = 512;
-constexpr int TOPK_MAX_T = 8192;           // bitonic sort buffer in LDS
-constexpr int64_t TOPK_MAX_P = 65536;      // 16-bit index in the composite
+constexpr int64_t TOPK_NARROW_P = 65536;   // rows up to this long use 32-bit composites (16-bit index)
+constexpr int64_t TOPK_MAX_P = 0x7fffffff; // 64-bit composites carry a 32-bit index
 
 
 __device__ __forceinline__ double bf16_bits_to_f64(uint16_t b) { return static_cast<double>(bf16_to_f32(b)); }
@@ -261,23 +261,51 @@ __device__ __forceinline__ void topk_find_bin(const uint32_t* hist, uint32_t nee
     }
 }
 
-// One workgroup per (b, ho) row.  "Score desc, index asc" is "composite
-// desc" for the unique composite (key << 16) | (0xffff - idx).  Two radix
-// passes over the 16-bit keys (one private histogram per wavefront) find the
-// threshold key K and how many of the entries equal to K are taken (the r of
-// lowest index: a prefix count over contiguous per-thread index ranges); the
-// T winners' composites are collected in LDS and each is written straight to
-// its output position, its rank among the winners (T <= TOPK_RANK_LIMIT), or
-// bitonic-sorted first (larger T).  Dynamic LDS: [hist][winners][keys].
+// The composite of one entry: (key << IDX_BITS) | (IDX_MASK - idx), unique,
+// and "score desc, index asc" is "composite desc".  32 bits (16-bit index)
+// while the row has at most 65536 positions, 64 bits (32-bit index) beyond.
+template <typename C>
+struct Comp {
+    static constexpr int IDX_BITS = sizeof(C) == 4 ? 16 : 32;
+    static constexpr C IDX_MASK = (static_cast<C>(1) << IDX_BITS) - 1;
+    __device__ static C make(uint32_t key, int64_t idx) {
+        return (static_cast<C>(key) << IDX_BITS) | (IDX_MASK - static_cast<C>(idx));
+    }
+    __device__ static int64_t index(C c) { return static_cast<int64_t>(IDX_MASK - (c & IDX_MASK)); }
+};
+
+// four composites starting at s[4j] (16-byte aligned groups)
+__device__ __forceinline__ void load4(const uint32_t* s, int j, uint32_t (&w)[4]) {
+    const uint4 v = reinterpret_cast<const uint4*>(s)[j];
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+}
+__device__ __forceinline__ void load4(const uint64_t* s, int j, uint64_t (&w)[4]) {
+    const ulonglong2 a = reinterpret_cast<const ulonglong2*>(s)[2 * j];
+    const ulonglong2 b = reinterpret_cast<const ulonglong2*>(s)[2 * j + 1];
+    w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y;
+}
+
+// One workgroup per (b, ho) row.  Two radix passes over the 16-bit keys (one
+// histogram per pair of wavefronts) find the threshold key K and how many of
+// the entries equal to K are taken (the r of lowest index: a prefix count
+// over contiguous per-thread index ranges); the T winners' composites are
+// collected and each is written straight to its output position, its rank
+// among the winners (T <= TOPK_RANK_LIMIT), or bitonic-sorted first (larger
+// T), in LDS or, when n2 composites do not fit the LDS budget (GSORT), in
+// this row's slice of a global buffer.  Dynamic LDS: [hist][winners][keys]
+// ([hist][keys] with GSORT).
+template <typename C, bool GSORT>
 __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __restrict__ keys, int64_t P, int T,
-                                                            int n2, int cached, int64_t* __restrict__ out) {
+                                                            int n2, int cached, C* __restrict__ gsel,
+                                                            int64_t* __restrict__ out) {
     extern __shared__ __align__(16) uint32_t tk_lds[];
     uint32_t* hist = tk_lds;                       // [TOPK_HIST][256]
-    uint32_t* sel = tk_lds + TOPK_HIST * 256;      // [n2]
-    uint16_t* s_keys = reinterpret_cast<uint16_t*>(sel + n2);
+    const int row = blockIdx.x;
+    C* sel = GSORT ? gsel + static_cast<int64_t>(row) * n2 : reinterpret_cast<C*>(tk_lds + TOPK_HIST * 256);
+    uint16_t* s_keys = GSORT ? reinterpret_cast<uint16_t*>(tk_lds + TOPK_HIST * 256)
+                             : reinterpret_cast<uint16_t*>(reinterpret_cast<C*>(tk_lds + TOPK_HIST * 256) + n2);
     __shared__ uint32_t s_bin, s_need, s_count;
     __shared__ uint32_t s_wsum[TOPK_WAVES];
-    const int row = blockIdx.x;
     const uint16_t* kr = keys + static_cast<int64_t>(row) * key_pitch(P);
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -325,12 +353,12 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __re
     // thread t scans indices [t*C, t*C + C) (C a multiple of 8, read 16 bytes
     // at a time): entries above kth are winners; the entries equal to kth are
     // numbered in index order by a prefix count over the threads
-    const int64_t C = (P + 8 * TOPK_THREADS - 1) / (8 * TOPK_THREADS) * 8;
-    const int64_t i0 = static_cast<int64_t>(tid) * C;
+    const int64_t CH = (P + 8 * TOPK_THREADS - 1) / (8 * TOPK_THREADS) * 8;
+    const int64_t i0 = static_cast<int64_t>(tid) * CH;
     const uint4* k4 = cached ? reinterpret_cast<const uint4*>(s_keys) : reinterpret_cast<const uint4*>(kr);
     if (tid == 0) s_count = 0;
     uint32_t eq = 0;
-    for (int64_t ib = i0; ib < i0 + C && ib < P; ib += 8) {
+    for (int64_t ib = i0; ib < i0 + CH && ib < P; ib += 8) {
         const uint4 w = k4[ib >> 3];
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -346,7 +374,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __re
     __syncthreads();
     uint32_t base = incl - eq;
     for (int w = 0; w < wave; ++w) base += s_wsum[w];
-    for (int64_t ib = i0; ib < i0 + C && ib < P; ib += 8) {
+    for (int64_t ib = i0; ib < i0 + CH && ib < P; ib += 8) {
         const uint4 w = k4[ib >> 3];
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -355,41 +383,43 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __re
             const uint32_t key = (ws[j >> 1] >> (16 * (j & 1))) & 0xffffu;
             bool take = i < P && key > kth;
             if (i < P && key == kth) take = base++ < r;
-            if (take) sel[atomicAdd(&s_count, 1u)] = (key << 16) | (0xffffu - static_cast<uint32_t>(i));
+            if (take) sel[atomicAdd(&s_count, 1u)] = Comp<C>::make(key, i);
         }
     }
     for (int i = T + tid; i < n2; i += TOPK_THREADS) sel[i] = 0;   // real composites are > 0
     __syncthreads();
     int64_t* orow = out + static_cast<int64_t>(row) * T;
-    if (T <= TOPK_RANK_LIMIT) {
+    if (!GSORT && T <= TOPK_RANK_LIMIT) {
         // rank = number of larger winners.  A thread ranks its (up to 4)
         // winners in one sweep; every lane of a wavefront reads the same four
         // composites per step (LDS broadcast)
         constexpr int E = TOPK_RANK_MAX / TOPK_THREADS;
-        uint32_t v[E], rank[E];
+        C v[E];
+        uint32_t rank[E];
 #pragma unroll
         for (int u = 0; u < E; ++u) {
-            v[u] = tid + u * TOPK_THREADS < T ? sel[tid + u * TOPK_THREADS] : 0u;
+            v[u] = tid + u * TOPK_THREADS < T ? sel[tid + u * TOPK_THREADS] : C(0);
             rank[u] = 0;
         }
-        const uint4* s4 = reinterpret_cast<const uint4*>(sel);
         const int ne = (T - tid + TOPK_THREADS - 1) / TOPK_THREADS;   // winners of this thread
         if (ne > 2) {
             for (int j = 0; j < n2 / 4; ++j) {
-                const uint4 w = s4[j];
+                C w[4];
+                load4(sel, j, w);
 #pragma unroll
-                for (int u = 0; u < E; ++u) rank[u] += (w.x > v[u]) + (w.y > v[u]) + (w.z > v[u]) + (w.w > v[u]);
+                for (int u = 0; u < E; ++u) rank[u] += (w[0] > v[u]) + (w[1] > v[u]) + (w[2] > v[u]) + (w[3] > v[u]);
             }
         } else if (ne > 0) {
             for (int j = 0; j < n2 / 4; ++j) {
-                const uint4 w = s4[j];
+                C w[4];
+                load4(sel, j, w);
 #pragma unroll
-                for (int u = 0; u < 2; ++u) rank[u] += (w.x > v[u]) + (w.y > v[u]) + (w.z > v[u]) + (w.w > v[u]);
+                for (int u = 0; u < 2; ++u) rank[u] += (w[0] > v[u]) + (w[1] > v[u]) + (w[2] > v[u]) + (w[3] > v[u]);
             }
         }
 #pragma unroll
         for (int u = 0; u < E; ++u)
-            if (u < ne) orow[rank[u]] = static_cast<int64_t>(0xffffu - (v[u] & 0xffffu));
+            if (u < ne) orow[rank[u]] = Comp<C>::index(v[u]);
         return;
     }
     // bitonic sort, descending
@@ -399,7 +429,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __re
                 const int lo = 2 * i - (i & (stride - 1));
                 const int hi = lo + stride;
                 const bool desc = ((lo & size) == 0);
-                const uint32_t x = sel[lo], y = sel[hi];
+                const C x = sel[lo], y = sel[hi];
                 if ((x < y) == desc) {
                     sel[lo] = y;
                     sel[hi] = x;
@@ -408,27 +438,48 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __re
             __syncthreads();
         }
     }
-    for (int i = tid; i < T; i += TOPK_THREADS) orow[i] = static_cast<int64_t>(0xffffu - (sel[i] & 0xffffu));
+    for (int i = tid; i < T; i += TOPK_THREADS) orow[i] = Comp<C>::index(sel[i]);
 }
 
-// LDS plan of topk_kernel for a row of P keys and T winners
+// Launch plan of topk_kernel for rows of P keys and T winners
 struct TopkPlan {
-    int n2, cached;
+    int n2, cached, wide, gsort;
     size_t lds;
+    size_t gbytes;               // global sort buffer bytes per row (gsort)
 };
-TopkPlan topk_plan(int64_t P, int T) {
-    TopkPlan t;
+TopkPlan topk_plan(int64_t P, int T, size_t lds_budget) {
+    TopkPlan t{};
+    t.wide = P > TOPK_NARROW_P;
+    const size_t cs = t.wide ? 8 : 4;
     if (T <= TOPK_RANK_LIMIT) {
         t.n2 = (T + 3) / 4 * 4;
     } else {
         t.n2 = 1;
         while (t.n2 < T) t.n2 <<= 1;
     }
-    const size_t fixed = (static_cast<size_t>(TOPK_HIST) * 256 + t.n2) * 4;
+    const size_t hist = static_cast<size_t>(TOPK_HIST) * 256 * 4;
+    const size_t sel = static_cast<size_t>(t.n2) * cs;
+    t.gsort = hist + sel > lds_budget;
+    const size_t fixed = hist + (t.gsort ? 0 : sel);
     const size_t with_keys = fixed + (static_cast<size_t>(P) * 2 + 15) / 16 * 16;
     t.cached = with_keys <= TOPK_LDS_MAX;
     t.lds = t.cached ? with_keys : fixed;
+    t.gbytes = t.gsort ? (sel + 255) / 256 * 256 : 0;
     return t;
+}
+
+// LDS a topk workgroup may use on the current device (cached per device)
+size_t topk_lds_budget() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
+    if (cache[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            v = 64 * 1024;
+        cache[dev] = v;
+    }
+    return static_cast<size_t>(cache[dev]) - 1024;   // room for the static LDS of the kernel
 }
 
 // ---------------------------------------------------------------------------
@@ -621,9 +672,18 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
 
 int padded_heads(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16; }
 
-size_t select_ws(int B, int H_out, int64_t P) {
-    const size_t qm = static_cast<size_t>(B) * H_out * 128 * sizeof(double) * 4;   // room for head padding
-    return ((qm + 255) / 256) * 256 + static_cast<size_t>(B) * H_out * key_pitch(P) * 2;
+// workspace: [query means][16-bit keys per row][global sort buffers (large top-k only)]
+struct SelectLayout {
+    size_t qm, keys, gsel, total;
+};
+SelectLayout select_layout(int B, int H_out, int64_t P, int T, const TopkPlan& tp) {
+    SelectLayout L;
+    L.qm = 0;
+    L.keys = ((static_cast<size_t>(B) * H_out * 128 * sizeof(double) * 4 + 255) / 256) * 256;   // room for head padding
+    L.gsel = L.keys + (static_cast<size_t>(B) * H_out * key_pitch(P) * 2 + 255) / 256 * 256;
+    L.total = L.gsel + (tp.gsort ? static_cast<size_t>(B) * H_out * tp.gbytes : 0);
+    (void)T;
+    return L;
 }
 
 }  // namespace
@@ -631,9 +691,10 @@ size_t select_ws(int B, int H_out, int64_t P) {
 
 using namespace hyq;
 
-extern "C" size_t hyq_vertical_select_workspace_size(int32_t b, int32_t h_out, int64_t p) {
-    if (b < 0 || h_out < 0 || p < 0) return 0;
-    return select_ws(b, h_out, p);
+extern "C" size_t hyq_vertical_select_workspace_size(int32_t b, int32_t h_out, int64_t p, int32_t top_k) {
+    if (b < 0 || h_out < 0 || p < 0 || top_k < 0 || p > TOPK_MAX_P) return 0;
+    const TopkPlan tp = topk_plan(p, top_k, topk_lds_budget());
+    return select_layout(b, h_out, p, top_k, tp).total;
 }
 
 extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, int32_t q_len,
@@ -648,19 +709,19 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
     if (G > 16) return fail(HYQ_ENOTSUP, "hyq_vertical_select: more than 16 query heads per key head");
     if (p <= 0 || top_k <= 0 || b == 0) return HYQ_OK;
     if (top_k > p) return fail(HYQ_EINVAL, "hyq_vertical_select: top_k > prefix length");
-    if (p > TOPK_MAX_P) return fail(HYQ_ENOTSUP, "hyq_vertical_select: prefix longer than 65536");
-    if (top_k > TOPK_MAX_T) return fail(HYQ_ENOTSUP, "hyq_vertical_select: top_k above 8192");
+    if (p > TOPK_MAX_P) return fail(HYQ_ENOTSUP, "hyq_vertical_select: prefix longer than 2^31 - 1");
     if (tail <= 0 || tail > q_len) return fail(HYQ_EINVAL, "hyq_vertical_select: bad query tail");
     if (!q || !k || !out_idx) return fail(HYQ_EINVAL, "hyq_vertical_select: null pointer");
     if (!aligned(k, 16) || ks_n % 8 || ks_h % 8 || ks_b % 8) return fail(HYQ_EINVAL, "hyq_vertical_select: keys must be 16-byte aligned rows");
     if (!aligned(q, 4) || qs_t % 2 || qs_h % 2 || qs_b % 2) return fail(HYQ_EINVAL, "hyq_vertical_select: query rows must be 4-byte aligned");
-    const size_t need = select_ws(b, h_out, p);
-    if (!workspace || ws_bytes < need || !aligned(workspace, 16))
+    const TopkPlan tp = topk_plan(p, top_k, topk_lds_budget());
+    const SelectLayout L = select_layout(b, h_out, p, top_k, tp);
+    if (!workspace || ws_bytes < L.total || !aligned(workspace, 16))
         return fail(HYQ_ENOSPC, "hyq_vertical_select: workspace too small or not 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
     double* qm = static_cast<double*>(workspace);
-    const size_t qm_bytes = ((static_cast<size_t>(b) * h_out * 128 * sizeof(double) * 4 + 255) / 256) * 256;
-    uint16_t* keys = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + qm_bytes);
+    uint16_t* keys = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + L.keys);
+    void* gsel = static_cast<char*>(workspace) + L.gsel;
     const int GP = padded_heads(G);
     qmean_kernel<<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(QM_THREADS), 0, s>>>(q, qs_b, qs_h, qs_t, q_len, tail,
                                                                                      group, hk, G, GP, qm);
@@ -676,9 +737,24 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
     }
     rc = check_launch("hyq_vertical_select (score)");
     if (rc) return rc;
-    const TopkPlan tp = topk_plan(p, top_k);
-    topk_kernel<<<dim3(static_cast<unsigned>(b * h_out)), dim3(TOPK_THREADS), tp.lds, s>>>(keys, p, top_k, tp.n2,
-                                                                                        tp.cached, out_idx);
+    const dim3 tgrid(static_cast<unsigned>(b * h_out)), tblock(TOPK_THREADS);
+    if (tp.lds > 64 * 1024) {
+        const void* fn = tp.wide ? (tp.gsort ? reinterpret_cast<const void*>(&topk_kernel<uint64_t, true>)
+                                             : reinterpret_cast<const void*>(&topk_kernel<uint64_t, false>))
+                                 : (tp.gsort ? reinterpret_cast<const void*>(&topk_kernel<uint32_t, true>)
+                                             : reinterpret_cast<const void*>(&topk_kernel<uint32_t, false>));
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(tp.lds)) != hipSuccess)
+            return fail(HYQ_EDEVICE, "hyq_vertical_select: cannot raise the LDS limit of the top-k kernel");
+    }
+    if (tp.wide) {
+        uint64_t* g = static_cast<uint64_t*>(gsel);
+        if (tp.gsort) topk_kernel<uint64_t, true><<<tgrid, tblock, tp.lds, s>>>(keys, p, top_k, tp.n2, tp.cached, g, out_idx);
+        else topk_kernel<uint64_t, false><<<tgrid, tblock, tp.lds, s>>>(keys, p, top_k, tp.n2, tp.cached, g, out_idx);
+    } else {
+        uint32_t* g = static_cast<uint32_t*>(gsel);
+        if (tp.gsort) topk_kernel<uint32_t, true><<<tgrid, tblock, tp.lds, s>>>(keys, p, top_k, tp.n2, tp.cached, g, out_idx);
+        else topk_kernel<uint32_t, false><<<tgrid, tblock, tp.lds, s>>>(keys, p, top_k, tp.n2, tp.cached, g, out_idx);
+    }
     return check_launch("hyq_vertical_select (topk)");
 }
 

@@ -127,10 +127,14 @@ def vertical_lists(vertical_indices: torch.Tensor, seq_len: int, window_size: in
                nv=torch.empty(B * H, nblk, dtype=torch.int32, device=dev))
     if P == 0:
         out["rcount"].zero_()
-    st = _lib.lib().hyq_prefill_lists(vidx.data_ptr(), vidx.stride(0), vidx.stride(1), vidx.stride(2), B, H,
-                                      seq_len, T, window_size, out["vert"].data_ptr(), out["rest"].data_ptr(),
-                                      out["rcount"].data_ptr(), out["nr"].data_ptr(), out["nv"].data_ptr(),
-                                      _stream(dev))
+    L = _lib.lib()
+    stream = _stream(dev)
+    need = L.hyq_prefill_lists_workspace_size(B, H, seq_len, T, window_size)
+    ws = _workspace(dev, stream, need) if need else None
+    st = L.hyq_prefill_lists(vidx.data_ptr(), vidx.stride(0), vidx.stride(1), vidx.stride(2), B, H,
+                             seq_len, T, window_size, out["vert"].data_ptr(), out["rest"].data_ptr(),
+                             out["rcount"].data_ptr(), out["nr"].data_ptr(), out["nv"].data_ptr(),
+                             None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream)
     _lib.check(st, "vertical_lists")
     return out
 

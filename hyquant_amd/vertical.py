@@ -54,7 +54,10 @@ def _select(q: torch.Tensor, group: int, k: torch.Tensor, prefix_len: int, tail:
         return out
     L = _lib.lib()
     stream = _stream(q.device)
-    ws = _scratch(q.device, stream, L.hyq_vertical_select_workspace_size(B, h_out, prefix_len))
+    need = L.hyq_vertical_select_workspace_size(B, h_out, prefix_len, top_k)
+    if need == 0:
+        raise ValueError(f"compute_vertical_indices: unsupported prefix length {prefix_len}")
+    ws = _scratch(q.device, stream, need)
     st = L.hyq_vertical_select(q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), QL, HQ, group,
                                k.data_ptr(), k.stride(0), k.stride(1), k.stride(2), HK, prefix_len, B, D,
                                tail, top_k, out.data_ptr(), ws.data_ptr(), ws.numel(), stream)

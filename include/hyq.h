@@ -146,10 +146,11 @@ int hyq_decode_bf16(const uint16_t* q, int64_t q_stride, uint16_t* out, int64_t 
  *   out  int64 [b, hq_in/group, top_k] (score desc, index asc)
  * qm = bf16(mean over the last `tail` queries [of bf16(mean over the group)]),
  * score = bf16(exact dot(qm, k)), top_k chosen by the caller
- * (reference: min(max(1, ceil(p * top_ratio)), p)).  d = 128, p <= 65536,
- * top_k <= 8192, at most 16 output heads per key head.
+ * (reference: min(max(1, ceil(p * top_ratio)), p)).  d = 128, p < 2^31,
+ * top_k <= p, at most 16 output heads per key head.  The workspace size
+ * depends on top_k: winner sets too large for LDS are sorted in it.
  */
-size_t hyq_vertical_select_workspace_size(int32_t b, int32_t h_out, int64_t p);
+size_t hyq_vertical_select_workspace_size(int32_t b, int32_t h_out, int64_t p, int32_t top_k);
 int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, int32_t q_len,
                         int32_t hq_in, int32_t group, const uint16_t* k, int64_t ks_b, int64_t ks_h,
                         int64_t ks_n, int32_t hk, int64_t p, int32_t b, int32_t d, int32_t tail,
@@ -216,12 +217,16 @@ int hyq_per_block_int8(const void* x, int32_t x_is_fp16, int64_t xs_b, int64_t x
  *   nr, nv int32 [b*h, ceil(n/128)]  entries of rest / vert below the window
  *                             start of each 128-row query block,
  *                             wla = floor64(max(0, 128 blk - (window - 1)))
- * vidx int64 [b, h, t] with strides (vi_b, vi_h, vi_t).  p <= 131072, t <= 8192.
+ * vidx int64 [b, h, t] with strides (vi_b, vi_h, vi_t).  p, t <= 2^26.
+ * Workspace: hyq_prefill_lists_workspace_size(b, h, n, t, window) bytes, zero
+ * (NULL allowed) while one head's lists fit the device's LDS, else a per-head
+ * scratch for them, 4-byte aligned.
  */
+size_t hyq_prefill_lists_workspace_size(int32_t b, int32_t h, int64_t n, int64_t t, int32_t window);
 int hyq_prefill_lists(const int64_t* vidx, int64_t vi_b, int64_t vi_h, int64_t vi_t,
                       int32_t b, int32_t h, int64_t n, int64_t t, int32_t window,
                       int32_t* vert, int32_t* rest, int32_t* rcount, int32_t* nr, int32_t* nv,
-                      void* stream);
+                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* Arguments of hyq_prefill_hybrid (strides in elements, channels contiguous). */
 typedef struct hyq_prefill_params {
@@ -248,7 +253,7 @@ typedef struct hyq_prefill_params {
  * (int8 Q . int8 K with per-block scales), vertical positions below wla and
  * the causal window wla <= j <= i (fp16 Q . fp16 K); one softmax; bf16 out.
  * Workspace: hyq_prefill_workspace_size(...) bytes, 256-byte aligned.
- * Limits: head_dim 128, N - window <= 131072, T <= 8192.
+ * Limits: head_dim 128, N - window <= 2^26, T <= 2^26.
  */
 size_t hyq_prefill_workspace_size(int32_t b, int32_t hq, int32_t hkv, int64_t n, int64_t t,
                                   int32_t window, int32_t pv_mode);

@@ -78,7 +78,9 @@ def test_per_block_int8_bit_exact(layout):
     assert np.array_equal(ks.cpu().numpy().view(np.uint32), eks.view(np.uint32))
 
 
-@pytest.mark.parametrize("N,W,T", [(700, 100, 40), (5000, 128, 300), (1000, 1, 999), (300, 64, 0), (100, 256, 5)])
+@pytest.mark.parametrize("N,W,T", [(700, 100, 40), (5000, 128, 300), (1000, 1, 999), (300, 64, 0), (100, 256, 5),
+                                   (150000, 128, 9000),     # past 131072 positions and 8192 indices, lists in LDS
+                                   (700000, 128, 5000)])    # lists larger than LDS: workspace
 def test_lists_bit_exact(N, W, T):
     from hyquant_amd.sage_unified import vertical_lists
     rng = np.random.default_rng(N + T)
@@ -344,3 +346,33 @@ def test_prefill_fp8_pv_tight_where_running_max_is_exact(cfg):
     l2 = float(np.linalg.norm(out - ref) / np.linalg.norm(ref))
     print(f"  relative L2 vs the fp8 oracle {l2:.3e}", flush=True)
     assert l2 < 2.0 ** -9
+
+
+def test_prefill_past_131072_positions():
+    """sage_vertical_attention_v2 at N = 140000 (the reference's
+    reorder_kv_for_vertical has no length limit, src/ops/sage_unified.py:499-547):
+    one query head against the float64 oracle on its first, a middle and its
+    last query blocks, every head against fp32 exact attention (MSE)."""
+    from hyquant_amd.sage_unified import sage_vertical_attention_v2
+    N, W = 140000, 128
+    print(f"prefill long N={N}", flush=True)
+    rng = np.random.default_rng(77)
+    q = _rand_bf16(rng, (1, 2, N, 128))
+    k = O.bf16_round(_rand_bf16(rng, (1, 1, N, 128), 1.5) + O.bf16_round(rng.standard_normal((1, 1, 1, 128)).astype(np.float32)))
+    v = _rand_bf16(rng, (1, 1, N, 128))
+    vidx = O.compute_vertical_indices(q, k, W, 0.05, kv_repeat=2)
+    assert vidx.shape[-1] > 6000
+    dev = torch.device("cuda")
+    qd, kd, vd = to_dev_bf16(q, dev), to_dev_bf16(k, dev), to_dev_bf16(v, dev)
+    out = sage_vertical_attention_v2(qd, kd, vd, torch.from_numpy(vidx).to(dev), window_size=W)
+    exact = _exact_attention_gpu(qd, kd, vd, chunk=2048)
+    mse = float(((out.float() - exact) ** 2).mean())
+    print(f"  N={N}: MSE vs exact fp32 attention {mse:.3e}", flush=True)
+    assert mse < 1e-6
+    nblk = (N + 127) // 128
+    blocks = [0, nblk // 2, nblk - 1]
+    ref = O.hybrid_prefill_fp64(q[:, :1], k, v, vidx[:, :1], W, blocks=blocks)
+    ref_abs = O.hybrid_prefill_fp64(q[:, :1], k, v, vidx[:, :1], W, blocks=blocks, abs_v=True)
+    rows = np.concatenate([np.arange(b * 128, min(N, (b + 1) * 128)) for b in blocks])
+    o = out[:, :1].float().cpu().numpy()
+    _check(f"N={N} head 0 blocks {blocks}", o[:, :, rows], ref[:, :, rows], ref_abs[:, :, rows])

@@ -28,6 +28,7 @@ EXPORTS = (
     "hyq_dequant",
     "hyq_decode_workspace_size",
     "hyq_decode_hybrid",
+    "hyq_decode_hybrid_noalloc",
     "hyq_decode_bf16_workspace_size",
     "hyq_decode_bf16",
     "hyq_vertical_select_workspace_size",
@@ -99,6 +100,8 @@ def _declare(lib):
     lib.hyq_decode_workspace_size.argtypes = [POINTER(DecodeParams)]
     lib.hyq_decode_hybrid.restype = c_int
     lib.hyq_decode_hybrid.argtypes = [POINTER(DecodeParams), c_void_p, c_size_t, c_void_p]
+    lib.hyq_decode_hybrid_noalloc.restype = c_int
+    lib.hyq_decode_hybrid_noalloc.argtypes = [POINTER(DecodeParams), c_void_p]
     lib.hyq_decode_bf16_workspace_size.restype = c_size_t
     lib.hyq_decode_bf16_workspace_size.argtypes = [c_int32, c_int32, c_int64, c_int32]
     lib.hyq_decode_bf16.restype = c_int

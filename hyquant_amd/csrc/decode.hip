@@ -60,6 +60,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <string>
 
 namespace hyq {
@@ -1044,17 +1045,13 @@ extern "C" size_t hyq_decode_workspace_size(const hyq_decode_params* p) {
     return layout(pl, p->bh_kv, p->kv_repeat).total;
 }
 
-extern "C" int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace, size_t ws_bytes, void* stream) {
-    int rc = validate(p);
-    if (rc != HYQ_OK) return rc;
-    if (p->bh_kv == 0) return HYQ_OK;
-    const Plan pl = plan_for(p);
-    if (pl.nwg == 0) return fail(HYQ_EINVAL, "decode with zero key tokens");
-    if (static_cast<int64_t>(pl.nwg) * p->kv_repeat > MAX_PARTIALS || pl.nwg > MAX_NWG)
-        return fail(HYQ_ENOTSUP, "too many pieces per head for the merge tables");
-    const Layout L = layout(pl, p->bh_kv, p->kv_repeat);
-    if (!workspace || ws_bytes < L.total || !aligned(workspace, 256))
-        return fail(HYQ_ENOSPC, "decode workspace too small or misaligned: need " + std::to_string(L.total) + " bytes");
+namespace hyq {
+namespace {
+
+// The launch of hyq_decode_hybrid once the workspace is settled (p validated,
+// the plan checked against the merge tables, the workspace L.total bytes,
+// 256-byte aligned, its counter area zero).
+int launch_decode(const hyq_decode_params* p, const Plan& pl, const Layout& L, void* workspace, void* stream) {
     DecArgs a{};
     a.q = p->q; a.q_stride = p->q_stride;
     a.out = p->out; a.out_stride = p->out_stride;
@@ -1099,6 +1096,85 @@ extern "C" int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace, si
         default: decode_kernel<8, 8><<<grid, block, lds, s>>>(a); break;
     }
     return check_launch("hyq_decode_hybrid");
+}
+
+// validation, plan and layout shared by both decode entry points
+int prepare(const hyq_decode_params* p, Plan& pl, Layout& L) {
+    int rc = validate(p);
+    if (rc != HYQ_OK) return rc;
+    if (p->bh_kv == 0) return HYQ_OK;
+    pl = plan_for(p);
+    if (pl.nwg == 0) return fail(HYQ_EINVAL, "decode with zero key tokens");
+    if (static_cast<int64_t>(pl.nwg) * p->kv_repeat > MAX_PARTIALS || pl.nwg > MAX_NWG)
+        return fail(HYQ_ENOTSUP, "too many pieces per head for the merge tables");
+    L = layout(pl, p->bh_kv, p->kv_repeat);
+    return HYQ_OK;
+}
+
+// ---------------------------------------------------------------------------
+// allocation-free variant: the workspace is a file-scope device array
+// ---------------------------------------------------------------------------
+constexpr size_t SCRATCH_BYTES = 16u << 20;     // counters (2 MiB) + (m, l) table and partials
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+__global__ void clear_words_kernel(uint32_t* __restrict__ p, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// This device's address of `scratch`, looked up once per device with that
+// device current; the first lookup also clears the counter area on `stream`
+// (a fill kernel, so that a captured first call records no memset node).
+// Every completed decode launch leaves the counters at zero again.
+int scratch_for_current_device(hipStream_t stream, void** out) {
+    static std::mutex mu;
+    static void* ptrs[64] = {nullptr};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return fail(HYQ_EDEVICE, "hyq_decode_hybrid_noalloc: no current HIP device");
+    std::lock_guard<std::mutex> lock(mu);
+    if (ptrs[dev] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr)
+            return fail(HYQ_EDEVICE, std::string("hyq_decode_hybrid_noalloc: hipGetSymbolAddress failed: ") +
+                                         hipGetErrorString(e));
+        const int64_t words = static_cast<int64_t>(CNT_CAP) * CNT_PAD;
+        clear_words_kernel<<<dim3(static_cast<unsigned>((words + 255) / 256)), dim3(256), 0, stream>>>(
+            static_cast<uint32_t*>(ptr), words);
+        if (int rc = check_launch("hyq_decode_hybrid_noalloc (clear)")) return rc;
+        ptrs[dev] = ptr;
+    }
+    *out = ptrs[dev];
+    return HYQ_OK;
+}
+
+}  // namespace
+}  // namespace hyq
+
+extern "C" int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace, size_t ws_bytes, void* stream) {
+    Plan pl{};
+    Layout L{};
+    int rc = prepare(p, pl, L);
+    if (rc != HYQ_OK || p->bh_kv == 0) return rc;
+    if (!workspace || ws_bytes < L.total || !aligned(workspace, 256))
+        return fail(HYQ_ENOSPC, "decode workspace too small or misaligned: need " + std::to_string(L.total) + " bytes");
+    return launch_decode(p, pl, L, workspace, stream);
+}
+
+extern "C" int hyq_decode_hybrid_noalloc(const hyq_decode_params* p, void* stream) {
+    Plan pl{};
+    Layout L{};
+    int rc = prepare(p, pl, L);
+    if (rc != HYQ_OK || p->bh_kv == 0) return rc;
+    if (L.total > SCRATCH_BYTES)
+        return fail(HYQ_ENOSPC, "hyq_decode_hybrid_noalloc: the call needs " + std::to_string(L.total) +
+                                    " bytes of workspace, above the " + std::to_string(SCRATCH_BYTES) +
+                                    "-byte scratch; use hyq_decode_hybrid");
+    void* ws = nullptr;
+    rc = scratch_for_current_device(static_cast<hipStream_t>(stream), &ws);
+    if (rc != HYQ_OK) return rc;
+    return launch_decode(p, pl, L, ws, stream);
 }
 
 extern "C" size_t hyq_decode_bf16_workspace_size(int32_t bh_kv, int32_t kv_repeat, int64_t n, int32_t d) {

@@ -214,6 +214,25 @@ def fused_d_stage_decode(
 
 def _decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk, k_staging, v_staging,
             k_window, v_window, k_bits, v_bits, kv_repeat, sm_scale, split_tokens, lens_q, lens_s0):
+    p, keep, out = decode_params(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk, k_staging,
+                                 v_staging, k_window, v_window, k_bits, v_bits, kv_repeat, sm_scale, split_tokens,
+                                 lens_q, lens_s0)
+    L = _lib.lib()
+    need = L.hyq_decode_workspace_size(p)
+    if need == 0:
+        _lib.check(L.hyq_decode_hybrid(p, None, 0, None), "fused_d_stage_decode")
+    stream = _stream(q.device)
+    ws = _workspace(q.device, stream, need)
+    st = L.hyq_decode_hybrid(p, ws.data_ptr(), ws.numel(), stream)
+    _lib.check(st, "fused_d_stage_decode")
+    return out
+
+
+def decode_params(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk, k_staging, v_staging,
+                  k_window, v_window, k_bits, v_bits, kv_repeat=1, sm_scale=None, split_tokens=0, lens_q=None,
+                  lens_s0=None):
+    """The hyq_decode_params of a fused_d_stage_decode call: returns (params,
+    tensors that must stay alive while the call runs, the output tensor)."""
     _require_gpu(q, "q")
     if q.dtype != torch.bfloat16:
         raise ValueError(f"fused_d_stage_decode expects bf16 q, got {q.dtype}")
@@ -252,15 +271,7 @@ def _decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk,
     if lens_q is not None:
         keep += [lens_q, lens_s0]
         p.seq_lens_quant, p.seq_lens_seg0 = lens_q.data_ptr(), lens_s0.data_ptr()
-    L = _lib.lib()
-    need = L.hyq_decode_workspace_size(p)
-    if need == 0:
-        _lib.check(L.hyq_decode_hybrid(p, None, 0, None), "fused_d_stage_decode")
-    stream = _stream(q.device)
-    ws = _workspace(q.device, stream, need)
-    st = L.hyq_decode_hybrid(p, ws.data_ptr(), ws.numel(), stream)
-    _lib.check(st, "fused_d_stage_decode")
-    return out
+    return p, keep, out
 
 
 # the reference's split-K entry point is the same operator here

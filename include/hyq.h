@@ -120,6 +120,21 @@ int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace,
                       size_t workspace_bytes, void* stream);
 
 /*
+ * hyq_decode_hybrid without a workspace argument and without any allocation.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The arrival counters, (m, l) table and partials live
+ * in a 16 MiB array of library device memory, one per GPU, held until the
+ * process ends; a call whose workspace (hyq_decode_workspace_size) exceeds
+ * 16 MiB returns HYQ_ENOSPC.  The first call on a device looks the array up
+ * and clears its counter area on `stream`.  Calls on one GPU share the array:
+ * calls that overlap in time on one GPU (different streams, or host threads)
+ * race and must be ordered by the caller; calls ordered on one stream are
+ * safe.  Results are bit-identical to hyq_decode_hybrid's.
+ */
+int hyq_decode_hybrid_noalloc(const hyq_decode_params* p, void* stream);
+
+/*
  * Full-precision bf16 decode attention over one contiguous KV per head, the
  * hand-written split-K comparator at the same shapes (no reference
  * counterpart on this path other than the FA2 baseline of README.md:62-71).

@@ -110,6 +110,19 @@ def test_decode_host_validation():
     assert b"16 * bits" in L.hyq_last_error()
 
 
+def test_decode_noalloc_host_validation():
+    """hyq_decode_hybrid_noalloc validates like hyq_decode_hybrid and refuses,
+    before touching the device, a call whose workspace exceeds its 16 MiB
+    scratch (16384 KV heads x 16 query heads: 128 MiB of partials)."""
+    _lib, L = _L()
+    assert L.hyq_decode_hybrid_noalloc(_params(_lib, k_bits=3), None) == _lib.HYQ_EINVAL
+    assert L.hyq_decode_hybrid_noalloc(_params(_lib, bh_kv=0), None) == _lib.HYQ_OK
+    p = _params(_lib, bh_kv=16384, kv_repeat=16)
+    assert L.hyq_decode_workspace_size(p) > 16 << 20
+    assert L.hyq_decode_hybrid_noalloc(p, None) == _lib.HYQ_ENOSPC
+    assert b"scratch" in L.hyq_last_error()
+
+
 def test_prefill_unified_host_validation():
     """hyq_prefill_unified takes no vertical indices: t != 0 is EINVAL
     before anything is launched."""

@@ -9,9 +9,10 @@ fused_d_stage_decode call over that cache.
 Timing: inputs are resident in HBM; R copies of the cache (R chosen so the
 copies exceed 1 GiB, i.e. four times the 256 MiB Infinity Cache) are used in
 rotation so every step streams its bytes from HBM.  W untimed steps, then the
-K timed steps are one replay of a HIP graph holding the K steps, bracketed by
-two HIP events on the stream the kernels run on (the same K steps issued as
-Python calls one by one are reported as eager_us_per_step).
+K timed steps are captured in a HIP graph; the graph is replayed five times,
+each replay bracketed by two HIP events on the stream the kernels run on and
+by synchronisations, and the median replay gives the per-step time (the same
+K steps issued as Python calls one by one are reported as eager_us_per_step).
 
 Output: one JSON line (rank 0), with the roofline of the decode kernel, the
 CPU baseline (the reference's bf16 eager decode math run by torch on the host
@@ -106,13 +107,17 @@ def run_decode(q, st, G):
                                    st["k_window"], st["v_window"], st["bits"][0], st["bits"][1], kv_repeat=G)
 
 
-def time_rotating(fn, states, warmup, steps):
+REPLAYS = 5
+
+
+def time_rotating(fn, states, warmup, steps, replays=REPLAYS):
     """ms per step over `steps` steps cycling through `states`.
 
-    The steps are captured once into a HIP graph and the timed region is one
-    replay of it (K steps, no host work between launches); returns
-    (graph_ms_per_step, eager_ms_per_step) where the eager figure times the
-    same K Python calls issued one by one."""
+    The steps are captured once into a HIP graph; the graph is replayed
+    `replays` times, each replay (K steps, no host work between launches)
+    bracketed by HIP events on the stream, and the median replay gives the
+    per-step time.  Returns (graph_ms_per_step, eager_ms_per_step) where the
+    eager figure times the same K Python calls issued one by one."""
     n = len(states)
     for i in range(warmup):
         fn(states[i % n])
@@ -131,13 +136,16 @@ def time_rotating(fn, states, warmup, steps):
             fn(states[i % n])
     g.replay()
     torch.cuda.synchronize()
-    e0.record()
-    g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    graph = e0.elapsed_time(e1) / steps
+    per = []
+    for _ in range(replays):
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) / steps)
+    per.sort()
     del g
-    return graph, eager
+    return per[len(per) // 2], eager
 
 
 def copies_for(nbytes, cap=512):
@@ -167,13 +175,30 @@ def bench_bf16(B, HQ, HKV, N, dev, warmup, steps, seed=0):
     return ms, nbytes, R, eager
 
 
-def cpu_baseline(N=8192, min_steps=20, budget_s=20.0):
+def cpu_threads():
+    """Threads for the CPU baseline: os.cpu_count(), capped by the CPUs this
+    process may run on and by OMP_NUM_THREADS when the environment sets it
+    (the GPU box gives one GPU's job a 16-CPU share and sets
+    OMP_NUM_THREADS=16; more threads than that share oversubscribe it)."""
+    n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except (AttributeError, OSError):
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_baseline(N=8192, S=64, min_steps=20, budget_s=20.0):
     """The reference's eager decode math (bf16 dequant + SDPA on torch CPU,
-    src/ops/d_stage_kv_cache.py:309-354) on config 1, timed on the host CPU."""
+    src/ops/d_stage_kv_cache.py:309-354) on config 1 (or config 0 with N=1024,
+    S=37), timed on the host CPU."""
     from oracle import hyq_oracle as O
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores = cpu_threads()
     torch.set_num_threads(cores)
-    inp = O.make_decode_inputs(B=1, HQ=32, HKV=8, N=N, W=128, S=64, seed=0)
+    inp = O.make_decode_inputs(B=1, HQ=32, HKV=8, N=N, W=128, S=S, seed=0)
     st = O.build_decode_state(inp)
     es = O.prepare_eager_state(st)
     q = torch.from_numpy(inp.q_dec)
@@ -197,9 +222,12 @@ def cpu_baseline(N=8192, min_steps=20, budget_s=20.0):
                     break
     except OSError:
         pass
+    name = "config 1" if N == 8192 else "config 0" if N == 1024 else f"prefix {N}"
     return {"value": round(med * 1e6, 1), "unit": "us/step", "cores": cores, "kind": "port",
-            "sample": f"config 1 (B=1, 32q/8kv, prefix 8192), median of {len(times)} steps of the "
-                      f"bf16 eager dequant+SDPA decode on torch CPU; host CPU: {model}"}
+            "sample": f"{name} (B=1, 32q/8kv, prefix {N}, {S} staging tokens), median of {len(times)} steps "
+                      f"of the bf16 eager dequant+SDPA decode on torch CPU, {cores} threads "
+                      f"(os.cpu_count() {os.cpu_count()}, capped by the process's CPU set and "
+                      f"OMP_NUM_THREADS); host CPU: {model}"}
 
 
 # MI355X dense peaks (TFLOP/s or TOP/s)
@@ -499,7 +527,8 @@ def main():
         "config": {"workload": "config1: fused hybrid decode, B=1, 32q/8kv, d128, prefix 8192",
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "prefix": N,
                    "n_quant": Nq, "n_topk": T, "n_staging": S, "n_window": W,
-                   "cache_copies_rotated": R, "timing": "one HIP-graph replay of K steps",
+                   "cache_copies_rotated": R,
+                   "timing": f"median of {REPLAYS} HIP-graph replays of K steps, HIP events on the kernel's stream",
                    "eager_us_per_step": round(eager * 1e3, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
@@ -516,7 +545,9 @@ def main():
         ms16, b16, _, _ = bench_bf16(B, HQ, HKV, N, dev, args.warmup, args.steps)
         res["bf16_comparator"] = {"us_per_step": round(ms16 * 1e3, 3),
                                   "gbs": round(b16 / (ms16 * 1e-3) / 1e9, 1),
-                                  "speedup_hybrid_vs_bf16": round(ms16 / ms, 3)}
+                                  "frac_peak": round(b16 / (ms16 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                  "speedup_hybrid_vs_bf16": round(ms16 / ms, 3),
+                                  "meets_3x": bool(ms16 / ms >= 3.0)}
     if not args.no_sweep:
         sweep = []
         for b in (1, 16):
@@ -528,7 +559,9 @@ def main():
                 if not args.no_bf16:
                     m16, nb16, _, _ = bench_bf16(b, HQ, HKV, n, dev, 5, 50)
                     row["bf16_us_per_step"] = round(m16 * 1e3, 3)
+                    row["bf16_frac_peak"] = round(nb16 / (m16 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
                     row["speedup_vs_bf16"] = round(m16 / m, 3)
+                    row["meets_3x"] = bool(m16 / m >= 3.0)
                 sweep.append(row)
                 print(f"# sweep {row}", file=sys.stderr, flush=True)
         res["sweep"] = sweep
@@ -539,6 +572,7 @@ def main():
         res["config4_prefill"] = bench_prefill(dev)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
+        res["cpu_baseline_config0"] = cpu_baseline(N=1024, S=37)
     print(json.dumps(res), flush=True)
 
 

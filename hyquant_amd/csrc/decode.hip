@@ -50,9 +50,11 @@
 //   The four lanes of a quad load the K and V scales of tokens 4kb..4kb+3 of a
 //   tile and quad-broadcast DPP moves hand every lane all four.
 // int4 -> MFMA operand conversion is done in registers without any lookup:
-//   K: nibble ^ 8 -> fp16(1024 + u) by OR-ing a magic exponent, then one
-//      packed fp16 add of -1032 gives the exact code (Q is fed as fp16,
-//      pre-scaled by a power of two so every bf16 query value is exact).
+//   K: u = nibble ^ 8 placed in the mantissa of an fp16 subnormal (value
+//      u * 2^-24, one shift and one bitop3 per pair of codes); Q is fed as
+//      fp16, pre-scaled by a power of two so every bf16 query value is
+//      exact, every product is exact in fp32, and the QK accumulators start
+//      at -2^-24 * 8 * sum(q) so that they end at 2^-24 * q . code.
 //   V: nibble ^ 8 -> bf16(128 + u); the constant 136 is removed after the
 //      product with a ninth MFMA against an all-ones operand, which yields
 //      sum_t P'[g][t] rounded exactly as the main product.
@@ -135,9 +137,6 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-__device__ __forceinline__ uint32_t f16x2_add(uint32_t a, f16x2 b) {
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, a) + b);
-}
 
 // NB: operand vectors are always assembled from scalars with a brace list;
 // element-wise stores into an ext_vector inside unrolled loops were
@@ -147,15 +146,6 @@ __device__ __forceinline__ uint32_t f16x2_add(uint32_t a, f16x2 b) {
 // exponent: ((x >> s) & 0x000f000f) ^ (0x00080008 | magic).
 __device__ __forceinline__ uint32_t nib2(uint32_t x, int s, uint32_t magic_xor) {
     return ((x >> s) & 0x000f000fu) ^ magic_xor;
-}
-
-// 8 int4 codes (one dword, nibble i = channel i, two's complement) -> 8 exact
-// fp16 values in slot order [c0,c4,c1,c5,c2,c6,c3,c7]: fp16(1024 + u) - 1032.
-__device__ __forceinline__ f16x8 int4_to_f16x8(uint32_t x) {
-    const f16x2 bias = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
-    const u32x4 o = {f16x2_add(nib2(x, 0, 0x64086408u), bias), f16x2_add(nib2(x, 4, 0x64086408u), bias),
-                     f16x2_add(nib2(x, 8, 0x64086408u), bias), f16x2_add(nib2(x, 12, 0x64086408u), bias)};
-    return __builtin_bit_cast(f16x8, o);
 }
 
 // v_exp_f32: 2^x without the denormal range fix-up of exp2f (results below
@@ -306,35 +296,51 @@ __device__ __forceinline__ void qload(QRaw<KB, VB>& r, const QCtx& x, int t0) {
     r.sv[1] = bld16(x.vs, x.slane + 32, ss);
 }
 
-// QK A operand of MFMA m (channels 32kb + 8m + [0..7]) as exact fp16 codes in
-// slot order [c0,c4,c1,c5,c2,c6,c3,c7], the order of the Q operands:
-//   4 bits: fp16(1024 + (nibble ^ 8)) - 1032             (int4_to_f16x8)
-//   8 bits: fp16(1024 + (byte ^ 0x80)) - 1152; byte j of the two dwords
-//           paired by one perm
-//   2 bits: fp16(1024 + (crumb ^ 2)) - 1026; the two bytes of the 16-bit
-//           half spread to the two fp16 halves by one perm
+// QK A operand of MFMA m (channels 32kb + 8m + [0..7]) in slot order
+// [c0,c4,c1,c5,c2,c6,c3,c7], the order of the Q operands, as fp16
+// subnormals whose bits are the offset-binary code u = code + 2^(KB-1):
+// the value is u * 2^-24 exactly, so every product with the fp16 query is
+// exact in fp32 and the MFMA yields 2^-24 (q . code + 2^(KB-1) sum(q)).  The
+// second term is the same for every token of a query column: the QK
+// accumulators start at minus that bias (kbias, one MFMA product per piece),
+// which leaves 2^-24 q . code.
+//   4 bits: (nibble ^ 8) pairs (s, s + 16) of one dword
+//   8 bits: byte j of the two dwords paired by one perm, ^ 0x80
+//   2 bits: the two bytes of the 16-bit half spread to the two fp16 halves by
+//           one perm, crumbs ^ 2
 template <int KB>
 __device__ __forceinline__ f16x8 k_operand(const uint32_t (&k)[KB], int m) {
     if constexpr (KB == 4) {
-        return int4_to_f16x8(k[m]);
+        const uint32_t x = k[m];
+        const u32x4 o = {nib2(x, 0, 0x00080008u), nib2(x, 4, 0x00080008u), nib2(x, 8, 0x00080008u),
+                         nib2(x, 12, 0x00080008u)};
+        return __builtin_bit_cast(f16x8, o);
     } else if constexpr (KB == 8) {
-        const f16x2 bias = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
         const uint32_t lo = k[2 * m], hi = k[2 * m + 1];
-        const u32x4 o = {f16x2_add(perm(hi, lo, 0x0c040c00u) ^ 0x64806480u, bias),
-                         f16x2_add(perm(hi, lo, 0x0c050c01u) ^ 0x64806480u, bias),
-                         f16x2_add(perm(hi, lo, 0x0c060c02u) ^ 0x64806480u, bias),
-                         f16x2_add(perm(hi, lo, 0x0c070c03u) ^ 0x64806480u, bias)};
+        const u32x4 o = {perm(hi, lo, 0x0c040c00u) ^ 0x00800080u, perm(hi, lo, 0x0c050c01u) ^ 0x00800080u,
+                         perm(hi, lo, 0x0c060c02u) ^ 0x00800080u, perm(hi, lo, 0x0c070c03u) ^ 0x00800080u};
         return __builtin_bit_cast(f16x8, o);
     } else {
-        const f16x2 bias = {static_cast<_Float16>(-1026.0f), static_cast<_Float16>(-1026.0f)};
         const uint32_t w = k[m >> 1];
         const uint32_t y = (m & 1) ? perm(w, w, 0x0c030c02u) : perm(w, w, 0x0c010c00u);
-        const u32x4 o = {f16x2_add(((y >> 0) & 0x00030003u) ^ 0x64026402u, bias),
-                         f16x2_add(((y >> 2) & 0x00030003u) ^ 0x64026402u, bias),
-                         f16x2_add(((y >> 4) & 0x00030003u) ^ 0x64026402u, bias),
-                         f16x2_add(((y >> 6) & 0x00030003u) ^ 0x64026402u, bias)};
+        const u32x4 o = {((y >> 0) & 0x00030003u) ^ 0x00020002u, ((y >> 2) & 0x00030003u) ^ 0x00020002u,
+                         ((y >> 4) & 0x00030003u) ^ 0x00020002u, ((y >> 6) & 0x00030003u) ^ 0x00020002u};
         return __builtin_bit_cast(f16x8, o);
     }
+}
+
+// Minus the K operand's offset term of each query column, -2^-24 2^(KB-1)
+// sum_d q_d, as the MFMA forms it: the product of an all-offset K tile (every
+// slot the subnormal 2^(KB-1) * 2^-24) with the Q operands.  Lane (c, kb)
+// gets column c in all four entries.
+template <int KB>
+__device__ __forceinline__ f32x4 k_bias(const f16x8 (&qop)[4]) {
+    constexpr uint32_t half = 1u << (KB - 1);
+    const u32x4 w = {half | half << 16, half | half << 16, half | half << 16, half | half << 16};
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc = mfma_f16(__builtin_bit_cast(f16x8, w), qop[m], acc);
+    return -acc;
 }
 
 // The constant the PV operands add to every V code (removed at the end with
@@ -344,31 +350,35 @@ __device__ __forceinline__ f16x8 k_operand(const uint32_t (&k)[KB], int m) {
 template <int VB>
 constexpr float v_offset() { return VB == 4 ? 136.0f : VB == 2 ? 130.0f : 2304.0f; }
 
-// The four lanes of a quad hold the scales of tokens 4kb..4kb+3 of a tile;
-// quad broadcasts give every lane all four.
-__device__ __forceinline__ void quad_scales(uint32_t v, float* out) {
-    out[0] = f16_bits_to_f32(static_cast<uint16_t>(dpp_mov<0x00>(v)));
-    out[1] = f16_bits_to_f32(static_cast<uint16_t>(dpp_mov<0x55>(v)));
-    out[2] = f16_bits_to_f32(static_cast<uint16_t>(dpp_mov<0xaa>(v)));
-    out[3] = f16_bits_to_f32(static_cast<uint16_t>(dpp_mov<0xff>(v)));
+// x of lane i of this lane's quad (a DPP quad broadcast, which the compiler
+// folds into the VOP2 instruction that consumes it)
+template <int I>
+__device__ __forceinline__ float quad_bcast(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), I * 0x55, 0xf, 0xf, true));
 }
 
 template <int KB, int VB>
-__device__ __forceinline__ void qcompute(WaveState& st, const QRaw<KB, VB>& r, const f16x8 (&qop)[4], int nv,
-                                         int lane, float qk) {
+__device__ __forceinline__ void qcompute(WaveState& st, const QRaw<KB, VB>& r, const f16x8 (&qop)[4],
+                                         const f32x4& kbias, int nv, int lane, float qk) {
     const int kb = lane >> 4;
-    float sk[8], sv[8];
-    quad_scales(r.sk[0], sk); quad_scales(r.sk[1], sk + 4);
-    quad_scales(r.sv[0], sv); quad_scales(r.sv[1], sv + 4);
+    // each lane converts the scales of its own token of each tile (the
+    // quad's four lanes hold tokens 4kb..4kb+3 of a tile); the scores and P'
+    // take them with quad broadcasts
+    const float skq[2] = {f16_bits_to_f32(static_cast<uint16_t>(r.sk[0])) * qk,
+                          f16_bits_to_f32(static_cast<uint16_t>(r.sk[1])) * qk};
+    const float svo[2] = {f16_bits_to_f32(static_cast<uint16_t>(r.sv[0])),
+                          f16_bits_to_f32(static_cast<uint16_t>(r.sv[1]))};
     // QK: S^T tile = K_tile . Q^T (exact fp16 codes x fp16 q)
     float s[8];
 #pragma unroll
     for (int tile = 0; tile < 2; ++tile) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        f32x4 acc = kbias;
 #pragma unroll
         for (int m = 0; m < 4; ++m) acc = mfma_f16(k_operand<KB>(r.k[tile], m), qop[m], acc);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s[4 * tile + i] = acc[i] * (sk[4 * tile + i] * qk);
+        s[4 * tile + 0] = acc[0] * quad_bcast<0>(skq[tile]);
+        s[4 * tile + 1] = acc[1] * quad_bcast<1>(skq[tile]);
+        s[4 * tile + 2] = acc[2] * quad_bcast<2>(skq[tile]);
+        s[4 * tile + 3] = acc[3] * quad_bcast<3>(skq[tile]);
     }
     if (nv < GROUP) {
 #pragma unroll
@@ -377,8 +387,10 @@ __device__ __forceinline__ void qcompute(WaveState& st, const QRaw<KB, VB>& r, c
     }
     softmax_step<8>(st, s, true);
     // P' = bf16(p * s_v): B operand of the PV MFMAs (slot e = token tau(kb, e))
-    const u32x4 pw = {pack_bf16x2(s[0] * sv[0], s[1] * sv[1]), pack_bf16x2(s[2] * sv[2], s[3] * sv[3]),
-                      pack_bf16x2(s[4] * sv[4], s[5] * sv[5]), pack_bf16x2(s[6] * sv[6], s[7] * sv[7])};
+    const u32x4 pw = {pack_bf16x2(s[0] * quad_bcast<0>(svo[0]), s[1] * quad_bcast<1>(svo[0])),
+                      pack_bf16x2(s[2] * quad_bcast<2>(svo[0]), s[3] * quad_bcast<3>(svo[0])),
+                      pack_bf16x2(s[4] * quad_bcast<0>(svo[1]), s[5] * quad_bcast<1>(svo[1])),
+                      pack_bf16x2(s[6] * quad_bcast<2>(svo[1]), s[7] * quad_bcast<3>(svo[1]))};
     const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
     // V^T operands (A of PV MFMA nb: channel 8c + nb of the 8 token slots),
     // token pairs (2pr, 2pr + 1) merged into one dword per operand register
@@ -710,17 +722,19 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
                              static_cast<_Float16>(f[3] * qscale), static_cast<_Float16>(f[7] * qscale)};
             qop[sidx] = v;
         }
-        const float qk = qk_scale * ldexpf(1.0f, ex);
+        // the K operands are u * 2^-24 (k_operand): 2^24 goes into the score scale
+        const float qk = qk_scale * ldexpf(1.0f, ex + 24);
+        const f32x4 kbias = k_bias<KB>(qop);
         for (int i = 0; i < nmine; i += 3) {
             const int t = t0 + i * STRIDE;
             qload(b2, x, t + 2 * STRIDE);
-            qcompute(st, b0, qop, ntok - t, lane, qk);
+            qcompute(st, b0, qop, kbias, ntok - t, lane, qk);
             if (i + 1 >= nmine) break;
             qload(b0, x, t + 3 * STRIDE);
-            qcompute(st, b1, qop, ntok - t - STRIDE, lane, qk);
+            qcompute(st, b1, qop, kbias, ntok - t - STRIDE, lane, qk);
             if (i + 2 >= nmine) break;
             qload(b1, x, t + 4 * STRIDE);
-            qcompute(st, b2, qop, ntok - t - 2 * STRIDE, lane, qk);
+            qcompute(st, b2, qop, kbias, ntok - t - 2 * STRIDE, lane, qk);
         }
         // remove the offset of the V operands: acc -= offset * sum_t P'
         const float corr = v_offset<VB>() * st.ones[0];

@@ -14,6 +14,13 @@ from ctypes import POINTER, Structure, c_float, c_int, c_int32, c_int64, c_size_
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libhyq.so")
 
+# the hyq_abi_version() these bindings (struct layouts, argument lists) match
+ABI_VERSION = 4
+
+HYQ_DT_Q_FP16 = 1
+HYQ_DT_SEG_FP16 = 2
+HYQ_DT_OUT_FP16 = 4
+
 HYQ_OK = 0
 HYQ_EINVAL = -22
 HYQ_ENOTSUP = -95
@@ -63,6 +70,7 @@ class DecodeParams(Structure):
         ("sm_scale", c_float),
         ("split_tokens", c_int32),
         ("seq_lens_quant", c_void_p), ("seq_lens_seg0", c_void_p),
+        ("dtype_flags", c_int32),
     ]
 
 
@@ -78,6 +86,7 @@ class PrefillParams(Structure):
         ("n", c_int64), ("t", c_int64),
         ("window", c_int32), ("smooth_k", c_int32), ("pv_mode", c_int32),
         ("sm_scale", c_double),
+        ("dtype_fp16", c_int32),
     ]
 
 
@@ -114,13 +123,13 @@ def _declare(lib):
     lib.hyq_vertical_select.restype = c_int
     lib.hyq_vertical_select.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32,
                                         c_void_p, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32,
-                                        c_int32, c_int32, c_int32, c_void_p, c_void_p, c_size_t, c_void_p]
+                                        c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_size_t, c_void_p]
     lib.hyq_freeze_workspace_size.restype = c_size_t
     lib.hyq_freeze_workspace_size.argtypes = [c_int32, c_int64]
     lib.hyq_freeze_reorganise.restype = c_int
     lib.hyq_freeze_reorganise.argtypes = (
         [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64,
-         c_int32, c_int32, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32]
+         c_int32, c_int32, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32, c_int32]
         + [c_void_p, c_int64, c_int64] * 2 + [c_void_p, c_int64] * 2 + [c_void_p, c_int64, c_int64] * 4
         + [c_void_p, c_size_t, c_void_p])
     lib.hyq_per_block_int8.restype = c_int
@@ -155,6 +164,10 @@ def lib():
                         "(there is no fallback implementation)")
                 l = ctypes.CDLL(LIB_PATH)
                 _declare(l)
+                if l.hyq_abi_version() != ABI_VERSION:
+                    raise RuntimeError(
+                        f"{LIB_PATH} reports ABI {l.hyq_abi_version()}, these bindings need {ABI_VERSION}: "
+                        "rebuild it with `python -m hyquant_amd.build`")
                 _lib = l
     return _lib
 

@@ -114,6 +114,7 @@ struct DecArgs {
     uint32_t* cnt;         // arrival counter of head h at cnt[h * CNT_PAD]
     const int32_t* len_q;  // optional per-head valid prefix tokens
     const int32_t* len_s0; // optional per-head valid tokens of segment 0
+    int32_t io;            // HYQ_DT_* flags: fp16 q / fp16 segments / fp16 out
 };
 
 struct WaveState {
@@ -452,6 +453,16 @@ struct Bf16Raw {
     u32x4 v[4];            // slot e: token 4kb+e, channels 8c..8c+7
 };
 
+__device__ __forceinline__ void f16_to_bf16(Bf16Raw& r) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r.k[i][j] = f16x2_to_bf16x2(r.k[i][j]);
+            r.v[i][j] = f16x2_to_bf16x2(r.v[i][j]);
+        }
+}
+
 // rk / rv cover this chunk's rows; tokens past the chunk read zeros
 __device__ __forceinline__ void bf16_load(Bf16Raw& r, Rsrc rk, Rsrc rv, int t0, int lane) {
     const int c = lane & 15, kb = lane >> 4;
@@ -536,6 +547,7 @@ struct MergeArgs {
     const float* ml;
     uint16_t* out;
     int64_t out_stride;
+    int out16;             // store fp16 instead of bf16
 };
 
 __device__ __forceinline__ void merge_head(const MergeArgs& a, int head, float* s_wt) {
@@ -598,10 +610,18 @@ __device__ __forceinline__ void merge_head(const MergeArgs& a, int head, float* 
             acc[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
         }
         if (h == 0) {
-            const u32x2 o = {static_cast<uint32_t>(f32_to_bf16_rne(den > 0.f ? acc[0] / den : 0.f)) |
-                                 (static_cast<uint32_t>(f32_to_bf16_rne(den > 0.f ? acc[1] / den : 0.f)) << 16),
-                             static_cast<uint32_t>(f32_to_bf16_rne(den > 0.f ? acc[2] / den : 0.f)) |
-                                 (static_cast<uint32_t>(f32_to_bf16_rne(den > 0.f ? acc[3] / den : 0.f)) << 16)};
+            float r[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[i] = den > 0.f ? acc[i] / den : 0.f;
+            // out.to(q.dtype) of the fp32 result: one rounding to bf16 or fp16
+            const u32x2 o = a.out16 ? u32x2{static_cast<uint32_t>(f32_to_f16_bits(r[0])) |
+                                                (static_cast<uint32_t>(f32_to_f16_bits(r[1])) << 16),
+                                            static_cast<uint32_t>(f32_to_f16_bits(r[2])) |
+                                                (static_cast<uint32_t>(f32_to_f16_bits(r[3])) << 16)}
+                                    : u32x2{static_cast<uint32_t>(f32_to_bf16_rne(r[0])) |
+                                                (static_cast<uint32_t>(f32_to_bf16_rne(r[1])) << 16),
+                                            static_cast<uint32_t>(f32_to_bf16_rne(r[2])) |
+                                                (static_cast<uint32_t>(f32_to_bf16_rne(r[3])) << 16)};
             *reinterpret_cast<u32x2*>(a.out + static_cast<int64_t>(head * G + g) * a.out_stride + 4 * q) = o;
         }
         wave_sync_lds();                             // the table is rewritten for the next g
@@ -635,7 +655,8 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
     const int sn0 = a.sn[0], sn1 = a.sn[1], sn2 = a.sn[2];
     const int su0 = a.segu[0], su1 = a.segu[1];
     const float qk_scale = a.qk_scale;
-    const MergeArgs ma{a.G, a.nwg, a.part, a.ml, a.out, a.out_stride};
+    const int io = a.io;
+    const MergeArgs ma{a.G, a.nwg, a.part, a.ml, a.out, a.out_stride, io & HYQ_DT_OUT_FP16};
     uint32_t* const cnt = a.cnt;
     asm volatile("" ::"s"(u0), "s"(u1), "s"(nqg), "s"(nquant), "s"(len_q), "s"(len_s0), "s"(kp), "s"(vp),
                  "s"(ksp), "s"(vsp), "s"(kp_bh), "s"(vp_bh), "s"(ks_bh), "s"(vs_bh));
@@ -667,6 +688,12 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         const uint32_t qo = static_cast<uint32_t>(c * a.q_stride * 2 + 64 * kb);
 #pragma unroll
         for (int i = 0; i < 4; ++i) qraw[i] = bld128(rq, qo + 16 * i);
+        if (io & HYQ_DT_Q_FP16) {   // q.to(bf16), as the reference's Q loads
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) qraw[i][j] = f16x2_to_bf16x2(qraw[i][j]);
+        }
     }
 
     if (u0 < nqg) {
@@ -747,6 +774,9 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         // during the other's loop)
         const bf16x8 qb[4] = {__builtin_bit_cast(bf16x8, qraw[0]), __builtin_bit_cast(bf16x8, qraw[1]),
                               __builtin_bit_cast(bf16x8, qraw[2]), __builtin_bit_cast(bf16x8, qraw[3])};
+        // fp16 segments (an fp16 model's cache) are rounded to bf16 after
+        // their loads, as the reference's .to(tl.bfloat16) of each tile
+        const bool seg16 = io & HYQ_DT_SEG_FP16;
         // segment bounds in units: [nqg, b1), [b1, b2), [b2, end of head)
         const int b1 = nqg + su0, b2 = b1 + su1;
         for (int seg = 0; seg < 3; ++seg) {
@@ -775,9 +805,11 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
             for (int i = 0; i < nmine; i += 2) {
                 const int t = t0 + i * TSTRIDE;
                 bf16_load(r1, rk, rv, t + TSTRIDE, lane);
+                if (seg16) f16_to_bf16(r0);
                 bf16_compute(st, r0, qb, n - t, lane, qk_scale);
                 if (i + 1 >= nmine) break;
                 bf16_load(r0, rk, rv, t + 2 * TSTRIDE, lane);
+                if (seg16) f16_to_bf16(r1);
                 bf16_compute(st, r1, qb, n - t - TSTRIDE, lane, qk_scale);
             }
         }
@@ -1012,6 +1044,8 @@ int validate(const hyq_decode_params* p) {
     if (p->bh_kv < 0) return fail(HYQ_EINVAL, "bh_kv < 0");
     if (p->bh_kv > CNT_CAP) return fail(HYQ_ENOTSUP, "bh_kv (batch * kv heads) above " + std::to_string(CNT_CAP));
     if (p->n_quant < 0 || p->n_quant > (1 << 24)) return fail(HYQ_EINVAL, "bad n_quant");
+    if (p->dtype_flags & ~(HYQ_DT_Q_FP16 | HYQ_DT_SEG_FP16 | HYQ_DT_OUT_FP16))
+        return fail(HYQ_EINVAL, "unknown dtype_flags bits " + std::to_string(p->dtype_flags));
     if (p->bh_kv == 0) return HYQ_OK;
     if (!p->q || !p->out) return fail(HYQ_EINVAL, "null q/out");
     if (!aligned(p->q, 16) || p->q_stride % 8 || p->q_stride < D)
@@ -1069,6 +1103,7 @@ int launch_decode(const hyq_decode_params* p, const Plan& pl, const Layout& L, v
     DecArgs a{};
     a.q = p->q; a.q_stride = p->q_stride;
     a.out = p->out; a.out_stride = p->out_stride;
+    a.io = p->dtype_flags;
     a.kp = reinterpret_cast<const uint8_t*>(p->k_packed); a.kp_bh = p->kp_stride_bh; a.kp_n = p->kp_stride_n;
     a.vp = reinterpret_cast<const uint8_t*>(p->v_packed); a.vp_bh = p->vp_stride_bh; a.vp_n = p->vp_stride_n;
     a.ks = p->k_scale; a.ks_bh = p->ks_stride_bh;

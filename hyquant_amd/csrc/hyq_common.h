@@ -41,14 +41,35 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// float64 -> bf16 with one correct RNE rounding: round to float32 toward zero
-// with a sticky bit (round-to-odd), then RNE to bf16.
-__device__ __forceinline__ uint16_t f64_to_bf16_rne(double x) {
+// packed fp16 pair -> packed bf16 pair, each value rounded to nearest even
+// (an fp16 value is exact in float, so this is the one rounding of
+// tensor.to(torch.bfloat16) / Triton's .to(tl.bfloat16))
+__device__ __forceinline__ uint32_t f16x2_to_bf16x2(uint32_t w) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t h = __builtin_bit_cast(f16x2_t, w);
+    return pack_bf16x2(static_cast<float>(h[0]), static_cast<float>(h[1]));
+}
+
+// float -> fp16 bits, round to nearest even (overflow to inf)
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// round a float64 to float32 toward zero with a sticky bit (round-to-odd):
+// a later RNE rounding of the result to any format of at most 22 significand
+// bits equals one RNE rounding of x
+__device__ __forceinline__ float f64_to_f32_odd(double x) {
     float f = __double2float_rz(x);
     uint32_t u = __float_as_uint(f);
     if (static_cast<double>(f) != x) u |= 1u;
-    return f32_to_bf16_rne(__uint_as_float(u));
+    return __uint_as_float(u);
 }
+
+// float64 -> bf16 with one correct RNE rounding
+__device__ __forceinline__ uint16_t f64_to_bf16_rne(double x) { return f32_to_bf16_rne(f64_to_f32_odd(x)); }
+
+// float64 -> fp16 with one correct RNE rounding
+__device__ __forceinline__ uint16_t f64_to_f16_rne(double x) { return f32_to_f16_bits(f64_to_f32_odd(x)); }
 
 // ---- wavefront helpers (wave64) ---------------------------------------------
 

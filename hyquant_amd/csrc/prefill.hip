@@ -161,6 +161,10 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 }
 
 __device__ __forceinline__ float bf16_round_f32(float x) { return bf16_to_f32(f32_to_bf16_rne(x)); }
+// a bf16 or (f16 != 0) fp16 element -> float (exact)
+__device__ __forceinline__ float half_to_f32(uint16_t h, int f16) {
+    return f16 ? f16_bits_to_f32(h) : bf16_to_f32(h);
+}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -216,7 +220,7 @@ __device__ __forceinline__ uint32_t pack_e4m3x4_raw(float a, float b, float c, f
 // order, so km does not depend on scheduling.
 __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restrict__ k, int64_t k_b, int64_t k_h,
                                                        int64_t k_n, const uint16_t* __restrict__ v, int64_t v_b,
-                                                       int64_t v_h, int64_t v_n, int HKV, int N, int nch,
+                                                       int64_t v_h, int64_t v_n, int HKV, int N, int nch, int f16,
                                                        double* __restrict__ kpart, float* __restrict__ vpart) {
     __shared__ double s_sum[4][PD];
     __shared__ float s_max[4][PD];
@@ -231,10 +235,10 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
     for (int r = chunk * STAT_ROWS + ph; r < r_end; r += 4) {
         const uint32_t kk = *reinterpret_cast<const uint32_t*>(kb + r * k_n);
         const uint32_t vv = *reinterpret_cast<const uint32_t*>(vb + r * v_n);
-        s0 += static_cast<double>(bf16_to_f32(static_cast<uint16_t>(kk)));
-        s1 += static_cast<double>(bf16_to_f32(static_cast<uint16_t>(kk >> 16)));
-        m0 = fmaxf(m0, fabsf(bf16_to_f32(static_cast<uint16_t>(vv))));
-        m1 = fmaxf(m1, fabsf(bf16_to_f32(static_cast<uint16_t>(vv >> 16))));
+        s0 += static_cast<double>(half_to_f32(static_cast<uint16_t>(kk), f16));
+        s1 += static_cast<double>(half_to_f32(static_cast<uint16_t>(kk >> 16), f16));
+        m0 = fmaxf(m0, fabsf(half_to_f32(static_cast<uint16_t>(vv), f16)));
+        m1 = fmaxf(m1, fabsf(half_to_f32(static_cast<uint16_t>(vv >> 16), f16)));
     }
     s_sum[ph][2 * cp] = s0;
     s_sum[ph][2 * cp + 1] = s1;
@@ -250,11 +254,11 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
     }
 }
 
-// grid (B*HKV), 128 threads: km = bf16(sum / N) (one rounding of the float64
-// quotient), fp8 V scale = max|v| / 448.
+// grid (B*HKV), 128 threads: km = the model dtype's rounding of sum / N (one
+// rounding of the float64 quotient), fp8 V scale = max|v| / 448.
 __global__ __launch_bounds__(128) void kv_final_kernel(const double* __restrict__ kpart,
                                                        const float* __restrict__ vpart, int nch, int N, int smooth,
-                                                       uint16_t* __restrict__ km, float* __restrict__ vscale) {
+                                                       int f16, uint16_t* __restrict__ km, float* __restrict__ vscale) {
     const int bhk = blockIdx.x, ch = threadIdx.x;
     const double* kp = kpart + static_cast<int64_t>(bhk) * nch * PD + ch;
     const float* vp = vpart + static_cast<int64_t>(bhk) * nch * PD + ch;
@@ -281,16 +285,19 @@ __global__ __launch_bounds__(128) void kv_final_kernel(const double* __restrict_
         s += kp[i * PD];
         m = fmaxf(m, vp[i * PD]);
     }
-    km[bhk * PD + ch] = smooth ? f64_to_bf16_rne(s / static_cast<double>(N)) : static_cast<uint16_t>(0);
+    const double mean = s / static_cast<double>(N);
+    km[bhk * PD + ch] = !smooth ? static_cast<uint16_t>(0) : f16 ? f64_to_f16_rne(mean) : f64_to_bf16_rne(mean);
     vscale[bhk * PD + ch] = m / FP8_MAX;
 }
 
 // grid (ceil(N*16 / 256), B*HKV): thread = 8 channels of one row.
-//   k16 = fp16(bf16(k - km)), v16 = fp16(v); fp8 PV: v8 = e4m3(v / vscale)
-//   and v16 = fp16(v / vscale)
+//   bf16 model: k16 = fp16(bf16(k - km)); fp16 model: k16 = fp16(k - km)
+//   (the difference in float32, rounded to the model dtype, then
+//   .to(float16)); v16 = fp16(v); fp8 PV: v8 = e4m3(v / vscale) and
+//   v16 = fp16(v / vscale)
 __global__ __launch_bounds__(256) void kv_convert_kernel(const uint16_t* __restrict__ k, int64_t k_b, int64_t k_h,
                                                          int64_t k_n, const uint16_t* __restrict__ v, int64_t v_b,
-                                                         int64_t v_h, int64_t v_n, int HKV, int N,
+                                                         int64_t v_h, int64_t v_n, int HKV, int N, int f16,
                                                          const uint16_t* __restrict__ km,
                                                          const float* __restrict__ vscale, uint16_t* __restrict__ k16,
                                                          uint16_t* __restrict__ v16, uint8_t* __restrict__ v8) {
@@ -305,9 +312,10 @@ __global__ __launch_bounds__(256) void kv_convert_kernel(const uint16_t* __restr
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const uint32_t kw = kk[e >> 1], vw = vv[e >> 1];
-        kf[e] = bf16_to_f32(static_cast<uint16_t>((e & 1) ? (kw >> 16) : kw));
-        vf[e] = bf16_to_f32(static_cast<uint16_t>((e & 1) ? (vw >> 16) : vw));
-        kf[e] = bf16_round_f32(kf[e] - bf16_to_f32(km[bhk * PD + 8 * co + e]));
+        kf[e] = half_to_f32(static_cast<uint16_t>((e & 1) ? (kw >> 16) : kw), f16);
+        vf[e] = half_to_f32(static_cast<uint16_t>((e & 1) ? (vw >> 16) : vw), f16);
+        const float d = kf[e] - half_to_f32(km[bhk * PD + 8 * co + e], f16);
+        kf[e] = f16 ? d : bf16_round_f32(d);     // pack_f16x2 below rounds to fp16
     }
     const int64_t o = (static_cast<int64_t>(bhk) * N + row) * PD + 8 * co;
     const u32x4 ko = {pack_f16x2(kf[0], kf[1]), pack_f16x2(kf[2], kf[3]), pack_f16x2(kf[4], kf[5]),
@@ -606,6 +614,7 @@ struct PfArgs {
     int total, per_xcd;
     const float* vscale;                                              // fp8 PV: [BHK][128] per-channel V scale
     int rest_causal;       // all keys int8 up to the diagonal (rest list = positions, causal mask, no window)
+    int f16;               // q and out are fp16 (an fp16 model), else bf16
 };
 
 __device__ __forceinline__ f32x4 mfma_f16(const f16x8& a, const f16x8& b, const f32x4& c) {
@@ -686,7 +695,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const uint32_t wd = (e < 8) ? lo[e >> 1] : hi[(e - 8) >> 1];
-                const float v = bf16_to_f32(static_cast<uint16_t>((e & 1) ? (wd >> 16) : wd)) * a.c;
+                const float v = half_to_f32(static_cast<uint16_t>((e & 1) ? (wd >> 16) : wd), a.f16) * a.c;
                 x[sb][cc][e] = v;
                 amax = fmaxf(amax, fabsf(v));
             }
@@ -717,10 +726,13 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
                 const float* z = xv + 8 * hf;
-                const u32x4 hv = {pack_f16x2(bf16_round_f32(z[0]), bf16_round_f32(z[1])),
-                                  pack_f16x2(bf16_round_f32(z[2]), bf16_round_f32(z[3])),
-                                  pack_f16x2(bf16_round_f32(z[4]), bf16_round_f32(z[5])),
-                                  pack_f16x2(bf16_round_f32(z[6]), bf16_round_f32(z[7]))};
+                // q_scaled = (q * c) in the model dtype, then .to(float16):
+                // a bf16 model rounds twice, an fp16 model once
+                float zr[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) zr[e] = a.f16 ? z[e] : bf16_round_f32(z[e]);
+                const u32x4 hv = {pack_f16x2(zr[0], zr[1]), pack_f16x2(zr[2], zr[3]), pack_f16x2(zr[4], zr[5]),
+                                  pack_f16x2(zr[6], zr[7])};
                 qh[sb][2 * cc + hf] = __builtin_bit_cast(f16x8, hv);
             }
         }
@@ -1082,7 +1094,8 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             for (int cb = 0; cb < 8; ++cb) {
                 f32x4 o4 = acc[sb][cb] * inv;
                 if (PV8) o4 *= *reinterpret_cast<const f32x4*>(a.vscale + bhk * PD + 16 * cb + 4 * g);
-                const u32x2 o = {pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3])};
+                const u32x2 o = a.f16 ? u32x2{pack_f16x2(o4[0], o4[1]), pack_f16x2(o4[2], o4[3])}
+                                      : u32x2{pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3])};
                 *reinterpret_cast<u32x2*>(orow + 16 * cb + 4 * g) = o;
             }
         }
@@ -1267,6 +1280,8 @@ int prefill_run(const hyq_prefill_params* p, void* ws, size_t ws_bytes, hipStrea
     const int64_t N = p->n, T = p->t;
     if (p->head_dim != PD) return fail(HYQ_ENOTSUP, name + ": head_dim must be 128");
     if (p->pv_mode != 0 && p->pv_mode != 1) return fail(HYQ_EINVAL, name + ": pv_mode must be 0 (fp16) or 1 (fp8)");
+    if (p->dtype_fp16 != 0 && p->dtype_fp16 != 1) return fail(HYQ_EINVAL, name + ": dtype_fp16 must be 0 or 1");
+    const int f16 = p->dtype_fp16;
     if (B <= 0 || HQ <= 0 || HKV <= 0 || HQ % HKV || N <= 0 || N > INT32_MAX / 2 || T < 0 || W < 0)
         return fail(HYQ_EINVAL, name + ": invalid sizes (need HQ % HKV == 0, N > 0)");
     const int64_t P = std::max<int64_t>(0, N - W);
@@ -1297,16 +1312,16 @@ int prefill_run(const hyq_prefill_params* p, void* ws, size_t ws_bytes, hipStrea
     const uint16_t* v = static_cast<const uint16_t*>(p->v);
 
     hipLaunchKernelGGL(kv_stats_kernel, dim3(nch, BHK), dim3(256), 0, stream, k, p->k_stride_b, p->k_stride_h,
-                       p->k_stride_n, v, p->v_stride_b, p->v_stride_h, p->v_stride_n, HKV, Ni, nch,
+                       p->k_stride_n, v, p->v_stride_b, p->v_stride_h, p->v_stride_n, HKV, Ni, nch, f16,
                        static_cast<double*>(at(L.kpart)), static_cast<float*>(at(L.vpart)));
     if (int st = check_launch("kv_stats_kernel")) return st;
     hipLaunchKernelGGL(kv_final_kernel, dim3(BHK), dim3(PD), 0, stream, static_cast<const double*>(at(L.kpart)),
-                       static_cast<const float*>(at(L.vpart)), nch, Ni, p->smooth_k ? 1 : 0,
+                       static_cast<const float*>(at(L.vpart)), nch, Ni, p->smooth_k ? 1 : 0, f16,
                        static_cast<uint16_t*>(at(L.km)), static_cast<float*>(at(L.vscale)));
     if (int st = check_launch("kv_final_kernel")) return st;
     const int cblocks = static_cast<int>((N * 16 + 255) / 256);
     hipLaunchKernelGGL(kv_convert_kernel, dim3(cblocks, BHK), dim3(256), 0, stream, k, p->k_stride_b,
-                       p->k_stride_h, p->k_stride_n, v, p->v_stride_b, p->v_stride_h, p->v_stride_n, HKV, Ni,
+                       p->k_stride_h, p->k_stride_n, v, p->v_stride_b, p->v_stride_h, p->v_stride_n, HKV, Ni, f16,
                        static_cast<const uint16_t*>(at(L.km)), static_cast<const float*>(at(L.vscale)),
                        static_cast<uint16_t*>(at(L.k16)), static_cast<uint16_t*>(at(L.v16)),
                        p->pv_mode ? static_cast<uint8_t*>(at(L.v8)) : nullptr);
@@ -1352,6 +1367,7 @@ int prefill_run(const hyq_prefill_params* p, void* ws, size_t ws_bytes, hipStrea
     a.per_xcd = (a.total + 7) / 8;
     a.vscale = static_cast<const float*>(at(L.vscale));
     a.rest_causal = rest_causal ? 1 : 0;
+    a.f16 = f16;
     if (qk_fp8)
         hipLaunchKernelGGL((prefill_main_kernel<false, true>), dim3(8 * a.per_xcd), dim3(PF_THREADS), 0, stream, a);
     else if (p->pv_mode)

@@ -9,6 +9,8 @@
 //                 each sum exact in float64 and each mean rounded once (RNE) to bf16;
 //   score[p]    = bf16( sum_d qm[d] * k[p, d] )  with the sum taken in d order in
 //                 float64 (bf16 x bf16 products are exact in float64);
+//   an fp16 model (is_fp16) rounds the means and scores to fp16 instead: the
+//                 reference computes them in the model dtype.
 //   top-T       = the T largest scores, ties broken by the lower index, returned
 //                 in (score desc, index asc) order (the lower-index rule fixes
 //                 the unspecified tie order of torch.topk, src/patch/_common.py:189).
@@ -31,6 +33,7 @@
 
 #include <algorithm>
 #include <string>
+#include <type_traits>
 
 namespace hyq {
 namespace {
@@ -42,7 +45,17 @@ constexpr int64_t TOPK_MAX_P = 0x7fffffff; // 64-bit composites carry a 32-bit i
 
 __device__ __forceinline__ double bf16_bits_to_f64(uint16_t b) { return static_cast<double>(bf16_to_f32(b)); }
 
-// monotone key of a bf16 value (-0 and +0 share a key)
+// an element of the model dtype (bf16, or fp16 when f16) as float64 (exact)
+__device__ __forceinline__ double half_bits_to_f64(uint16_t b, bool f16) {
+    return f16 ? static_cast<double>(f16_bits_to_f32(b)) : bf16_bits_to_f64(b);
+}
+// one RNE rounding of a float64 to the model dtype, as bits
+__device__ __forceinline__ uint16_t f64_to_half_rne(double x, bool f16) {
+    return f16 ? f64_to_f16_rne(x) : f64_to_bf16_rne(x);
+}
+
+// monotone key of a bf16 or fp16 value (-0 and +0 share a key); both formats
+// keep the sign in bit 15 above a biased exponent, so one mapping orders both
 __device__ __forceinline__ uint32_t orderable_key(uint16_t b) {
     uint32_t u = b;
     if (u == 0x8000u) u = 0;
@@ -60,7 +73,7 @@ constexpr int QM_SLICES = QM_THREADS / 64;
 
 __global__ __launch_bounds__(QM_THREADS) void qmean_kernel(const uint16_t* __restrict__ q, int64_t qs_b, int64_t qs_h,
                                                            int64_t qs_t, int QL, int tail, int R, int HK, int G,
-                                                           int GP, double* __restrict__ qm) {
+                                                           int GP, int f16, double* __restrict__ qm) {
     const int row = blockIdx.x;                    // (b, hk, g)
     const int g = row % GP;
     const int bhk = row / GP;
@@ -83,14 +96,14 @@ __global__ __launch_bounds__(QM_THREADS) void qmean_kernel(const uint16_t* __res
             for (int u = 0; u < 4; ++u) v[u] = base[static_cast<int64_t>(t + u * QM_SLICES) * st];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                lo += bf16_bits_to_f64(static_cast<uint16_t>(v[u]));
-                hi += bf16_bits_to_f64(static_cast<uint16_t>(v[u] >> 16));
+                lo += half_bits_to_f64(static_cast<uint16_t>(v[u]), f16);
+                hi += half_bits_to_f64(static_cast<uint16_t>(v[u] >> 16), f16);
             }
         }
         for (; t < tail; t += QM_SLICES) {
             const uint32_t v = base[static_cast<int64_t>(t) * st];
-            lo += bf16_bits_to_f64(static_cast<uint16_t>(v));
-            hi += bf16_bits_to_f64(static_cast<uint16_t>(v >> 16));
+            lo += half_bits_to_f64(static_cast<uint16_t>(v), f16);
+            hi += half_bits_to_f64(static_cast<uint16_t>(v >> 16), f16);
         }
     } else {
         // four tail rows at a time, so that 4 R loads are in flight per step
@@ -105,15 +118,15 @@ __global__ __launch_bounds__(QM_THREADS) void qmean_kernel(const uint16_t* __res
                 }
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    ilo[u] += bf16_bits_to_f64(static_cast<uint16_t>(v[u]));
-                    ihi[u] += bf16_bits_to_f64(static_cast<uint16_t>(v[u] >> 16));
+                    ilo[u] += half_bits_to_f64(static_cast<uint16_t>(v[u]), f16);
+                    ihi[u] += half_bits_to_f64(static_cast<uint16_t>(v[u] >> 16), f16);
                 }
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 if (t + u * QM_SLICES < tail) {
-                    lo += bf16_bits_to_f64(f64_to_bf16_rne(ilo[u] / R));
-                    hi += bf16_bits_to_f64(f64_to_bf16_rne(ihi[u] / R));
+                    lo += half_bits_to_f64(f64_to_half_rne(ilo[u] / R, f16), f16);
+                    hi += half_bits_to_f64(f64_to_half_rne(ihi[u] / R, f16), f16);
                 }
             }
         }
@@ -126,7 +139,7 @@ __global__ __launch_bounds__(QM_THREADS) void qmean_kernel(const uint16_t* __res
         double sum = 0.0;
 #pragma unroll
         for (int k = 0; k < QM_SLICES; ++k) sum += s_sum[k][threadIdx.x];
-        out[threadIdx.x] = bf16_bits_to_f64(f64_to_bf16_rne(sum / tail));
+        out[threadIdx.x] = half_bits_to_f64(f64_to_half_rne(sum / tail, f16), f16);
     }
 }
 
@@ -144,7 +157,7 @@ __host__ __device__ inline int64_t key_pitch(int64_t P) { return (P + 7) / 8 * 8
 constexpr int SC_ROWS = 64;                 // rows per wavefront
 constexpr int SC_PITCH = 144;               // LDS bytes per half-row (128 + 16)
 
-template <int GM>
+template <int GM, bool F16>
 __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__ k, int64_t ks_b, int64_t ks_h,
                                                     int64_t ks_n, int HK, int G, int64_t P, int64_t KP,
                                                     const double* __restrict__ qm, uint16_t* __restrict__ keys) {
@@ -188,7 +201,8 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
             double kv[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j)
-                kv[j] = static_cast<double>(__uint_as_float(j & 1 ? ww[j >> 1] & 0xffff0000u : ww[j >> 1] << 16));
+                kv[j] = F16 ? static_cast<double>(f16_bits_to_f32(static_cast<uint16_t>(ww[j >> 1] >> (16 * (j & 1)))))
+                            : static_cast<double>(__uint_as_float(j & 1 ? ww[j >> 1] & 0xffff0000u : ww[j >> 1] << 16));
             const int d0 = 64 * half + 8 * c;
 #pragma unroll
             for (int g = 0; g < GM; ++g) {
@@ -201,7 +215,9 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
     if (p < P) {
 #pragma unroll
         for (int g = 0; g < GM; ++g)
-            if (g < G) keys[(static_cast<int64_t>(bh) * G + g) * KP + p] = static_cast<uint16_t>(orderable_key(f64_to_bf16_rne(acc[g])));
+            if (g < G)
+                keys[(static_cast<int64_t>(bh) * G + g) * KP + p] =
+                    static_cast<uint16_t>(orderable_key(f64_to_half_rne(acc[g], F16)));
     }
 }
 
@@ -503,19 +519,19 @@ __global__ void mark_kernel(const int64_t* __restrict__ idx, int T, int64_t P, i
 constexpr int CQ_CHUNK = 256;               // prefix positions per workgroup
 constexpr int CQ_UNROLL = 4;                // tokens per 16-lane group per pass
 
-// 16 lanes quantise one bf16 row of 128 channels: lane `sub` holds channels
-// 8 sub .. 8 sub + 7 (`raw`).  All 16 lanes take part in the amax reduction;
-// only the stores depend on `store`.
+// 16 lanes quantise one bf16 (fp16 when f16) row of 128 channels: lane `sub`
+// holds channels 8 sub .. 8 sub + 7 (`raw`).  All 16 lanes take part in the
+// amax reduction; only the stores depend on `store`.
 template <int NBITS>
-__device__ __forceinline__ void quant_row_group(uint4 raw, int8_t* dst, uint16_t* scl, int sub, bool store) {
+__device__ __forceinline__ void quant_row_group(uint4 raw, int8_t* dst, uint16_t* scl, int sub, bool store, bool f16) {
     constexpr int QMAX = (1 << (NBITS - 1)) - 1;
     constexpr int QMIN = -(1 << (NBITS - 1));
     float v[8];
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        v[2 * i] = __uint_as_float(w[i] << 16);
-        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        v[2 * i] = f16 ? f16_bits_to_f32(static_cast<uint16_t>(w[i])) : __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = f16 ? f16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16)) : __uint_as_float(w[i] & 0xffff0000u);
     }
     float amax = 0.f;
 #pragma unroll
@@ -569,6 +585,7 @@ struct CompactArgs {
     uint16_t* ksc; uint16_t* vsc;
     int64_t ksc_bh, vsc_bh;
     int k_bits, v_bits;
+    int f16;                     // k / v are fp16 (else bf16)
 };
 
 template <int KB, int VB>
@@ -598,6 +615,7 @@ __global__ __launch_bounds__(256) void compact_quant_kernel(CompactArgs a) {
     }
     __syncthreads();
     const uint32_t base = s_base;
+    const bool f16 = a.f16;
     // 16 lanes per token; each 16-lane group takes CQ_UNROLL tokens per pass
     // and issues their K and V row loads together (selected rows are loaded
     // too and simply not stored, which keeps the loads unconditional)
@@ -627,8 +645,8 @@ __global__ __launch_bounds__(256) void compact_quant_kernel(CompactArgs a) {
             // the n_compact rows of the outputs when they are not
             const bool keep = p < a.P && !((word >> (p & 31)) & 1u) && slot < a.n_compact;
             const int64_t dst = keep ? slot : 0;
-            quant_row_group<KB>(kr[u], a.kp + bh * a.kp_bh + dst * a.kp_n, a.ksc + bh * a.ksc_bh + dst, sub, keep);
-            quant_row_group<VB>(vr[u], a.vp + bh * a.vp_bh + dst * a.vp_n, a.vsc + bh * a.vsc_bh + dst, sub, keep);
+            quant_row_group<KB>(kr[u], a.kp + bh * a.kp_bh + dst * a.kp_n, a.ksc + bh * a.ksc_bh + dst, sub, keep, f16);
+            quant_row_group<VB>(vr[u], a.vp + bh * a.vp_bh + dst * a.vp_n, a.vsc + bh * a.vsc_bh + dst, sub, keep, f16);
         }
     }
 }
@@ -700,8 +718,10 @@ extern "C" size_t hyq_vertical_select_workspace_size(int32_t b, int32_t h_out, i
 extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, int32_t q_len,
                                    int32_t hq_in, int32_t group, const uint16_t* k, int64_t ks_b, int64_t ks_h,
                                    int64_t ks_n, int32_t hk, int64_t p, int32_t b, int32_t d, int32_t tail,
-                                   int32_t top_k, int64_t* out_idx, void* workspace, size_t ws_bytes, void* stream) {
+                                   int32_t top_k, int32_t is_fp16, int64_t* out_idx, void* workspace, size_t ws_bytes,
+                                   void* stream) {
     if (d != 128) return fail(HYQ_ENOTSUP, "hyq_vertical_select: head_dim must be 128");
+    if (is_fp16 != 0 && is_fp16 != 1) return fail(HYQ_EINVAL, "hyq_vertical_select: is_fp16 must be 0 or 1");
     if (b < 0 || hq_in <= 0 || hk <= 0 || group <= 0 || hq_in % group) return fail(HYQ_EINVAL, "hyq_vertical_select: bad head counts");
     const int h_out = hq_in / group;
     if (h_out % hk) return fail(HYQ_EINVAL, "hyq_vertical_select: output heads must be a multiple of key heads");
@@ -724,17 +744,25 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
     void* gsel = static_cast<char*>(workspace) + L.gsel;
     const int GP = padded_heads(G);
     qmean_kernel<<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(QM_THREADS), 0, s>>>(q, qs_b, qs_h, qs_t, q_len, tail,
-                                                                                     group, hk, G, GP, qm);
+                                                                                     group, hk, G, GP, is_fp16, qm);
     int rc = check_launch("hyq_vertical_select (mean)");
     if (rc) return rc;
     const dim3 sgrid(static_cast<unsigned>((p + 255) / 256), static_cast<unsigned>(b * hk));
-    switch (GP) {
-        case 1: score_kernel<1><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys); break;
-        case 2: score_kernel<2><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys); break;
-        case 4: score_kernel<4><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys); break;
-        case 8: score_kernel<8><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys); break;
-        default: score_kernel<16><<<sgrid, dim3(256), 0, s>>>(k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys); break;
-    }
+    auto score = [&](auto gm, auto f16) {
+        score_kernel<decltype(gm)::value, decltype(f16)::value><<<sgrid, dim3(256), 0, s>>>(
+            k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys);
+    };
+    auto score_gm = [&](auto f16) {
+        switch (GP) {
+            case 1: score(std::integral_constant<int, 1>{}, f16); break;
+            case 2: score(std::integral_constant<int, 2>{}, f16); break;
+            case 4: score(std::integral_constant<int, 4>{}, f16); break;
+            case 8: score(std::integral_constant<int, 8>{}, f16); break;
+            default: score(std::integral_constant<int, 16>{}, f16); break;
+        }
+    };
+    if (is_fp16) score_gm(std::true_type{});
+    else score_gm(std::false_type{});
     rc = check_launch("hyq_vertical_select (score)");
     if (rc) return rc;
     const dim3 tgrid(static_cast<unsigned>(b * h_out)), tblock(TOPK_THREADS);
@@ -767,7 +795,7 @@ extern "C" int hyq_freeze_reorganise(const uint16_t* k, int64_t ks_b, int64_t ks
                                      const uint16_t* v, int64_t vs_b, int64_t vs_h, int64_t vs_n,
                                      int32_t b, int32_t hk, int64_t n, int32_t d, int32_t w,
                                      const int64_t* topk_idx, int32_t top_k, int32_t k_bits, int32_t v_bits,
-                                     int8_t* kp, int64_t kp_bh, int64_t kp_n, int8_t* vp, int64_t vp_bh, int64_t vp_n,
+                                     int32_t is_fp16, int8_t* kp, int64_t kp_bh, int64_t kp_n, int8_t* vp, int64_t vp_bh, int64_t vp_n,
                                      uint16_t* ksc, int64_t ksc_bh, uint16_t* vsc, int64_t vsc_bh,
                                      uint16_t* kt, int64_t kt_bh, int64_t kt_n, uint16_t* vt, int64_t vt_bh, int64_t vt_n,
                                      uint16_t* kw, int64_t kw_bh, int64_t kw_n, uint16_t* vw, int64_t vw_bh, int64_t vw_n,
@@ -775,6 +803,7 @@ extern "C" int hyq_freeze_reorganise(const uint16_t* k, int64_t ks_b, int64_t ks
     if (d != 128) return fail(HYQ_ENOTSUP, "hyq_freeze_reorganise: head_dim must be 128");
     auto okbits = [](int x) { return x == 2 || x == 4 || x == 8; };
     if (!okbits(k_bits) || !okbits(v_bits)) return fail(HYQ_EINVAL, "hyq_freeze_reorganise: bits must be 2, 4 or 8");
+    if (is_fp16 != 0 && is_fp16 != 1) return fail(HYQ_EINVAL, "hyq_freeze_reorganise: is_fp16 must be 0 or 1");
     if (b < 0 || hk <= 0 || n < 0 || w < 0 || w > n || top_k < 0) return fail(HYQ_EINVAL, "hyq_freeze_reorganise: bad shape");
     const int64_t P = n - w;
     if (top_k > P) return fail(HYQ_EINVAL, "hyq_freeze_reorganise: top_k > prefix length");
@@ -798,7 +827,7 @@ extern "C" int hyq_freeze_reorganise(const uint16_t* k, int64_t ks_b, int64_t ks
             if (rc) return rc;
         }
         CompactArgs a{k, v, ks_b, ks_h, ks_n, vs_b, vs_h, vs_n, hk, P, P - top_k, words, bits,
-                      kp, vp, kp_bh, kp_n, vp_bh, vp_n, ksc, vsc, ksc_bh, vsc_bh, k_bits, v_bits};
+                      kp, vp, kp_bh, kp_n, vp_bh, vp_n, ksc, vsc, ksc_bh, vsc_bh, k_bits, v_bits, is_fp16};
         dim3 grid(static_cast<unsigned>((P + CQ_CHUNK - 1) / CQ_CHUNK), static_cast<unsigned>(bh));
         switch (10 * k_bits + v_bits) {
             case 44: compact_quant_kernel<4, 4><<<grid, dim3(256), 0, s>>>(a); break;

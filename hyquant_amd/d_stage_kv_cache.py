@@ -177,7 +177,7 @@ class DStageLayerCache:
         vidx_flat = vidx.reshape(BH, T).contiguous()
         st = L.hyq_freeze_reorganise(
             k.data_ptr(), k.stride(0), k.stride(1), k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
-            B, H_KV, N, D, W, vidx_flat.data_ptr(), T, self.k_bits, self.v_bits,
+            B, H_KV, N, D, W, vidx_flat.data_ptr(), T, self.k_bits, self.v_bits, int(dtype == torch.float16),
             kp.data_ptr(), kp.stride(0), kp.stride(1), vp.data_ptr(), vp.stride(0), vp.stride(1),
             ks.data_ptr(), ks.stride(0), vs.data_ptr(), vs.stride(0),
             self.k_topk.data_ptr(), self.k_topk.stride(0), self.k_topk.stride(1),

@@ -207,7 +207,10 @@ def fused_d_stage_decode(
 ) -> torch.Tensor:
     """Fused four-segment decode: quantised prefix (K and V codes of 2, 4 or 8
     bits) + top-k + staging + window under one online softmax.  Returns a new
-    [BH_Q, D] tensor of q.dtype (bf16)."""
+    [BH_Q, D] tensor of q.dtype.  q and the segments may be bf16 or fp16
+    (one dtype for the segments): fp16 values are rounded to bf16 before the
+    products, as the reference's kernels do (src/ops/decode_d_stage.py:537-541),
+    and the fp32 result is rounded once to q.dtype (:866)."""
     return _decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk, k_staging, v_staging,
                    k_window, v_window, k_bits, v_bits, kv_repeat, sm_scale, split_tokens, None, None)
 
@@ -234,8 +237,20 @@ def decode_params(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v
     """The hyq_decode_params of a fused_d_stage_decode call: returns (params,
     tensors that must stay alive while the call runs, the output tensor)."""
     _require_gpu(q, "q")
-    if q.dtype != torch.bfloat16:
-        raise ValueError(f"fused_d_stage_decode expects bf16 q, got {q.dtype}")
+    if q.dtype not in _HALF:
+        raise ValueError(f"fused_d_stage_decode expects bf16 or fp16 q, got {q.dtype}")
+    segs = (k_topk, v_topk, k_staging, v_staging, k_window, v_window)
+    seg_dtypes = {t.dtype for t in segs if t.shape[1] > 0}
+    if not seg_dtypes <= set(_HALF) or len(seg_dtypes) > 1:
+        raise ValueError(f"the top-k / staging / window segments must share one dtype, bf16 or fp16; "
+                         f"got {sorted(str(d) for d in seg_dtypes)}")
+    # an fp16 model: q and the segments are rounded to bf16 inside the kernel
+    # (the reference's .to(tl.bfloat16) of its loads) and the result is fp16
+    flags = 0
+    if q.dtype == torch.float16:
+        flags |= _lib.HYQ_DT_Q_FP16 | _lib.HYQ_DT_OUT_FP16
+    if torch.float16 in seg_dtypes:
+        flags |= _lib.HYQ_DT_SEG_FP16
     if k_bits not in (2, 4, 8) or v_bits not in (2, 4, 8):
         raise ValueError(f"k_bits and v_bits must be 2, 4, or 8, got {k_bits}, {v_bits}")
     BH_Q, D = q.shape
@@ -268,6 +283,7 @@ def decode_params(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v
     p.k_bits, p.v_bits = k_bits, v_bits
     p.sm_scale = float(sm_scale)
     p.split_tokens = int(split_tokens)
+    p.dtype_flags = flags
     if lens_q is not None:
         keep += [lens_q, lens_s0]
         p.seq_lens_quant, p.seq_lens_seg0 = lens_q.data_ptr(), lens_s0.data_ptr()

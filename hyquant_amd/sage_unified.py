@@ -4,8 +4,10 @@ of `reorder_kv_for_vertical` (:499-547) and the vendored `per_block_int8`
 (src/ops/vendor/sageattention/triton/quant_per_block.py:49-101).
 
 Every call runs the HIP kernels of libhyq.so on the current HIP stream of
-the input's device; there is no CPU or Triton path.  Only bf16 attention
-inputs are supported (the reference's fp16 branch is not on the hybrid path).
+the input's device; there is no CPU or Triton path.  q, k and v are bf16 or
+fp16 (one dtype); an fp16 model takes the reference's fp16 branch
+(src/ops/sage_unified.py:565-580): the K mean, k - km and the scaled Q are
+rounded once to fp16, and the output is fp16.
 """
 
 from __future__ import annotations
@@ -175,8 +177,8 @@ def _prefill(entry: str, name: str, q: torch.Tensor, k: torch.Tensor, v: torch.T
              vertical_indices: Optional[torch.Tensor], window_size: int, sm_scale: Optional[float],
              smooth_k: bool, pv_mode: str) -> torch.Tensor:
     _require_gpu(q, "q")
-    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
-        raise ValueError(f"{name} expects bf16 q, k, v")
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"{name} expects q, k, v of one dtype, bf16 or fp16; got {q.dtype}, {k.dtype}, {v.dtype}")
     if pv_mode not in PV_MODES:
         raise ValueError(f"pv_mode must be one of {tuple(PV_MODES)}")
     B, H_q, N, D = q.shape
@@ -206,6 +208,7 @@ def _prefill(entry: str, name: str, q: torch.Tensor, k: torch.Tensor, v: torch.T
     p.n, p.t = N, T
     p.window, p.smooth_k, p.pv_mode = window_size, int(bool(smooth_k)), mode
     p.sm_scale = float(sm_scale)
+    p.dtype_fp16 = int(q.dtype == torch.float16)
     st = getattr(L, entry)(ctypes.byref(p), ws.data_ptr(), ws.numel(), stream)
     _lib.check(st, name)
     return out
@@ -216,8 +219,8 @@ def sage_vertical_attention_v2(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
                                pv_mode: str = "fp16") -> torch.Tensor:
     """Hybrid prefill (int8 QK on rest tiles, fp16 QK on vertical / window
     tiles, one online softmax, fp16 P.V).  q [B, H_q, N, D], k/v
-    [B, H_kv, N, D] bf16 (GQA-native), vertical_indices [B, H_q, T] -> bf16
-    [B, H_q, N, D].  pv_mode "fp8" runs P.V on the rest tiles in OCP e4m3
+    [B, H_kv, N, D] bf16 or fp16 (GQA-native), vertical_indices [B, H_q, T]
+    -> [B, H_q, N, D] of q.dtype.  pv_mode "fp8" runs P.V on the rest tiles in OCP e4m3
     with per-channel V scales."""
     _require_gpu(q, "q")
     if vertical_indices.dim() != 3 or vertical_indices.shape[:2] != q.shape[:2]:
@@ -233,7 +236,7 @@ def sage_unified_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     :112-231).  window_size > 0: int8 keys below the 64-aligned window start
     of each 128-row query block, fp16 causal window above it; window_size = 0:
     every key up to the diagonal in int8.  q [B, H_q, N, D], k/v
-    [B, H_kv, N, D] bf16 -> bf16 [B, H_q, N, D]."""
+    [B, H_kv, N, D] bf16 or fp16 -> [B, H_q, N, D] of q.dtype."""
     return _prefill("hyq_prefill_unified", "sage_unified_attention", q, k, v, None, window_size, sm_scale,
                     smooth_k, "fp16")
 

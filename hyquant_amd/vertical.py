@@ -44,8 +44,9 @@ def _rows_ok(t: torch.Tensor) -> torch.Tensor:
 def _select(q: torch.Tensor, group: int, k: torch.Tensor, prefix_len: int, tail: int, top_k: int) -> torch.Tensor:
     B, HQ, QL, D = q.shape
     HK = k.shape[1]
-    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
-        raise ValueError("compute_vertical_indices expects bf16 queries and keys")
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype:
+        raise ValueError(f"compute_vertical_indices expects bf16 or fp16 queries and keys of one dtype, "
+                         f"got {q.dtype} and {k.dtype}")
     q = q if q.stride(-1) == 1 else q.contiguous()
     k = _rows_ok(k)
     h_out = HQ // group
@@ -60,7 +61,8 @@ def _select(q: torch.Tensor, group: int, k: torch.Tensor, prefix_len: int, tail:
     ws = _scratch(q.device, stream, need)
     st = L.hyq_vertical_select(q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), QL, HQ, group,
                                k.data_ptr(), k.stride(0), k.stride(1), k.stride(2), HK, prefix_len, B, D,
-                               tail, top_k, out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+                               tail, top_k, int(q.dtype == torch.float16), out.data_ptr(), ws.data_ptr(),
+                               ws.numel(), stream)
     _lib.check(st, "compute_vertical_indices")
     return out
 

@@ -101,7 +101,17 @@ typedef struct hyq_decode_params {
      * (src/ops/decode_d_stage.py:1008-1129). */
     const int32_t* seq_lens_quant;
     const int32_t* seq_lens_seg0;
+    /* HYQ_DT_* bits for an fp16 model (0 = all bf16).  fused_d_stage_decode
+     * (src/ops/decode_d_stage.py:537-541, 240-263) rounds fp16 q and fp16
+     * segment tiles to bf16 before its products and writes out in q.dtype
+     * (:866, :782): HYQ_DT_Q_FP16 and HYQ_DT_SEG_FP16 apply that rounding
+     * to q and to the three segments, HYQ_DT_OUT_FP16 rounds the fp32 result
+     * to fp16 instead of bf16. */
+    int32_t dtype_flags;
 } hyq_decode_params;
+#define HYQ_DT_Q_FP16 1
+#define HYQ_DT_SEG_FP16 2
+#define HYQ_DT_OUT_FP16 4
 /* Alignment: q 16-byte aligned (row stride % 8 == 0), out 8-byte aligned (row
  * stride % 4 == 0), k_packed 16-byte aligned (8 for 2-bit K), v_packed aligned
  * to v_bits bytes, head strides likewise, bf16 segments 16-byte aligned. */
@@ -161,7 +171,9 @@ int hyq_decode_bf16(const uint16_t* q, int64_t q_stride, uint16_t* out, int64_t 
  *   out  int64 [b, hq_in/group, top_k] (score desc, index asc)
  * qm = bf16(mean over the last `tail` queries [of bf16(mean over the group)]),
  * score = bf16(exact dot(qm, k)), top_k chosen by the caller
- * (reference: min(max(1, ceil(p * top_ratio)), p)).  d = 128, p < 2^31,
+ * (reference: min(max(1, ceil(p * top_ratio)), p)).  is_fp16 = 1: q and k
+ * are an fp16 model's, and the means and scores are rounded to fp16 (the
+ * reference computes them in the model dtype).  d = 128, p < 2^31,
  * top_k <= p, at most 16 output heads per key head.  The workspace size
  * depends on top_k: winner sets too large for LDS are sorted in it.
  */
@@ -169,8 +181,8 @@ size_t hyq_vertical_select_workspace_size(int32_t b, int32_t h_out, int64_t p, i
 int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, int32_t q_len,
                         int32_t hq_in, int32_t group, const uint16_t* k, int64_t ks_b, int64_t ks_h,
                         int64_t ks_n, int32_t hk, int64_t p, int32_t b, int32_t d, int32_t tail,
-                        int32_t top_k, int64_t* out_idx, void* workspace, size_t workspace_bytes,
-                        void* stream);
+                        int32_t top_k, int32_t is_fp16, int64_t* out_idx, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /*
  * Prefill -> decode cache reorganisation.  Replaces the body of
@@ -183,6 +195,8 @@ int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h, int64_t q
  *                                     ascending position, quantised per token
  *                                     exactly as hyq_quant_pack (k_bits, v_bits),
  *                                     any of the nine pairs of 2, 4 and 8 bits.
+ * is_fp16 = 1: keys/values and the top-k / window copies are fp16 (an fp16
+ * model; the codes and scales are those of hyq_quant_pack on fp16 input).
  * Precondition: each row of topk_idx holds distinct positions in [0, n-w)
  * (the selector's output).  Violations cannot make the call touch memory
  * outside its arguments: an index outside [0, n-w) copies a zero row into
@@ -196,7 +210,7 @@ int hyq_freeze_reorganise(const uint16_t* k, int64_t ks_b, int64_t ks_h, int64_t
                           const uint16_t* v, int64_t vs_b, int64_t vs_h, int64_t vs_n,
                           int32_t b, int32_t hk, int64_t n, int32_t d, int32_t w,
                           const int64_t* topk_idx, int32_t top_k, int32_t k_bits, int32_t v_bits,
-                          int8_t* kp, int64_t kp_bh, int64_t kp_n, int8_t* vp, int64_t vp_bh, int64_t vp_n,
+                          int32_t is_fp16, int8_t* kp, int64_t kp_bh, int64_t kp_n, int8_t* vp, int64_t vp_bh, int64_t vp_n,
                           uint16_t* ksc, int64_t ksc_bh, uint16_t* vsc, int64_t vsc_bh,
                           uint16_t* kt, int64_t kt_bh, int64_t kt_n, uint16_t* vt, int64_t vt_bh, int64_t vt_n,
                           uint16_t* kw, int64_t kw_bh, int64_t kw_n, uint16_t* vw, int64_t vw_bh, int64_t vw_n,
@@ -256,6 +270,11 @@ typedef struct hyq_prefill_params {
     int32_t smooth_k;     /* subtract the per-channel K mean before quantising */
     int32_t pv_mode;      /* 0: fp16 P.V; 1: OCP e4m3 P.V on the rest tiles */
     double sm_scale;      /* <= 0: head_dim^-0.5 */
+    /* 1: q, k, v and out are fp16 (an fp16 model), 0: bf16.  The reference
+     * (src/ops/sage_unified.py:565-580) forms the K mean, k - km and
+     * q * sm_scale * log2e in the model dtype before .to(float16), and
+     * returns q.dtype: an fp16 model rounds each once to fp16. */
+    int32_t dtype_fp16;
 } hyq_prefill_params;
 
 /*

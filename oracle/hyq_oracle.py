@@ -187,6 +187,18 @@ def top_k_count(prefix_len: int, top_ratio: float) -> int:
     return min(t, prefix_len)
 
 
+def f16_round_f64(x: np.ndarray) -> np.ndarray:
+    """float64 -> nearest fp16 value (single correct RNE rounding), as float32."""
+    return f64_to_f32_round_odd(x).astype(np.float16).astype(np.float32)
+
+
+def mean_f16(x: np.ndarray, axis: int) -> np.ndarray:
+    """fp16 mean, as mean_bf16 with one RNE rounding to fp16."""
+    n = x.shape[axis]
+    s = np.asarray(x, dtype=np.float64).sum(axis=axis)
+    return f16_round_f64(s / np.float64(n))
+
+
 def mean_bf16(x: np.ndarray, axis: int) -> np.ndarray:
     """bf16 mean: exact float64 sum, one float64 division, one RNE rounding to
     bf16.  Equals torch's fp32-accumulated bf16 mean except where the fp32 sum
@@ -196,33 +208,43 @@ def mean_bf16(x: np.ndarray, axis: int) -> np.ndarray:
     return bf16_round_f64(s / np.float64(n))
 
 
-def dot_bf16_exact(qm: np.ndarray, k: np.ndarray) -> np.ndarray:
+def mean_half(x: np.ndarray, axis: int, fp16: bool = False) -> np.ndarray:
+    """The model dtype's mean: mean_f16 for an fp16 model, else mean_bf16."""
+    return mean_f16(x, axis) if fp16 else mean_bf16(x, axis)
+
+
+def dot_bf16_exact(qm: np.ndarray, k: np.ndarray, fp16: bool = False) -> np.ndarray:
     """scores[..., p] = bf16(sum_d qm[..., d] * k[..., p, d]) with the sum taken
     sequentially in d order in float64 (products of bf16 values are exact in
     float64; the running sum is exact unless the products span > 2^37 in
-    magnitude).  qm [..., D], k [..., P, D] -> [..., P]."""
+    magnitude).  fp16=True (fp16 operands, products exact in float64 too):
+    the sum is rounded to fp16 instead.  qm [..., D], k [..., P, D] -> [..., P]."""
     qm64 = np.asarray(qm, dtype=np.float64)
     k64 = np.asarray(k, dtype=np.float64)
     acc = np.zeros(k64.shape[:-1], dtype=np.float64)
     for d in range(k64.shape[-1]):
         acc = acc + qm64[..., d, None] * k64[..., d]
-    return bf16_round_f64(acc)
+    return f16_round_f64(acc) if fp16 else bf16_round_f64(acc)
 
 
-def orderable_bf16_key(scores_bf16: np.ndarray) -> np.ndarray:
-    """Monotone uint16 key of a bf16 value; -0 and +0 get the same key (torch
+def orderable_bf16_key(scores_bf16: np.ndarray, fp16: bool = False) -> np.ndarray:
+    """Monotone uint16 key of a bf16 value (fp16 when fp16=True: the same
+    sign / biased-exponent layout); -0 and +0 get the same key (torch
     compares them equal)."""
-    b = f32_to_bf16_bits(scores_bf16).astype(np.uint32)
+    if fp16:
+        b = np.asarray(scores_bf16, np.float32).astype(np.float16).view(np.uint16).astype(np.uint32)
+    else:
+        b = f32_to_bf16_bits(scores_bf16).astype(np.uint32)
     b = np.where(b == 0x8000, 0, b)
     neg = (b & 0x8000) != 0
     return np.where(neg, (~b) & 0xFFFF, b | 0x8000).astype(np.uint32)
 
 
-def topk_desc_index_asc(scores_bf16: np.ndarray, k: int) -> np.ndarray:
+def topk_desc_index_asc(scores_bf16: np.ndarray, k: int, fp16: bool = False) -> np.ndarray:
     """Top-k along the last axis ordered by score descending, ties broken by
     lower index first (the deterministic rule this build adopts for
     torch.topk(sorted=True), src/patch/_common.py:189)."""
-    key = orderable_bf16_key(scores_bf16).astype(np.int64)
+    key = orderable_bf16_key(scores_bf16, fp16).astype(np.int64)
     P = scores_bf16.shape[-1]
     idx = np.broadcast_to(np.arange(P, dtype=np.int64), key.shape)
     combo = key * (1 << 32) + (0xFFFFFFFF - idx)
@@ -232,11 +254,12 @@ def topk_desc_index_asc(scores_bf16: np.ndarray, k: int) -> np.ndarray:
 
 def compute_vertical_indices(query_states: np.ndarray, key_states: np.ndarray,
                              window_size: int, top_ratio: float,
-                             kv_repeat: int = 1) -> np.ndarray:
+                             kv_repeat: int = 1, fp16: bool = False) -> np.ndarray:
     """src/patch/_common.py:144-190.
 
     query_states [B, H_Q, Q, D] (bf16 values), key_states [B, H, K, D] with
-    H == H_Q or H == H_Q / kv_repeat.  Returns int64 [B, H_Q, top_k].
+    H == H_Q or H == H_Q / kv_repeat.  fp16=True: fp16 values, the mean and
+    the scores in fp16 (the model dtype).  Returns int64 [B, H_Q, top_k].
     """
     B, HQ, QL, D = query_states.shape
     KL = key_states.shape[2]
@@ -244,31 +267,31 @@ def compute_vertical_indices(query_states: np.ndarray, key_states: np.ndarray,
     if P == 0:
         return np.zeros((B, HQ, 0), dtype=np.int64)
     tail = min(window_size, QL)
-    qm = mean_bf16(query_states[:, :, QL - tail:, :], axis=2)          # [B, HQ, D]
+    qm = mean_half(query_states[:, :, QL - tail:, :], 2, fp16)          # [B, HQ, D]
     HK = key_states.shape[1]
     if kv_repeat <= 1 or HK == HQ:
         kp = key_states[:, :, :P, :]
-        scores = dot_bf16_exact(qm, kp)                                   # [B, HQ, P]
+        scores = dot_bf16_exact(qm, kp, fp16)                             # [B, HQ, P]
     else:
         assert HQ == HK * kv_repeat
         kp = np.repeat(key_states[:, :, :P, :], kv_repeat, axis=1)        # head h -> h // R
-        scores = dot_bf16_exact(qm, kp)
+        scores = dot_bf16_exact(qm, kp, fp16)
     k = top_k_count(P, top_ratio)
-    return topk_desc_index_asc(scores, k)
+    return topk_desc_index_asc(scores, k, fp16)
 
 
-def vertical_scores(query_states, key_states, window_size, kv_repeat=1):
-    """The bf16 score matrix the selector ranks (for tests)."""
+def vertical_scores(query_states, key_states, window_size, kv_repeat=1, fp16=False):
+    """The bf16 (fp16) score matrix the selector ranks (for tests)."""
     B, HQ, QL, D = query_states.shape
     KL = key_states.shape[2]
     P = max(0, KL - window_size)
     tail = min(window_size, QL)
-    qm = mean_bf16(query_states[:, :, QL - tail:, :], axis=2)
+    qm = mean_half(query_states[:, :, QL - tail:, :], 2, fp16)
     HK = key_states.shape[1]
     kp = key_states[:, :, :P, :]
     if HK != HQ:
         kp = np.repeat(kp, HQ // HK, axis=1)
-    return dot_bf16_exact(qm, kp)
+    return dot_bf16_exact(qm, kp, fp16)
 
 
 # ---------------------------------------------------------------------------
@@ -306,20 +329,22 @@ class DecodeState:
         return self.v_ring[:, :self.ring_ptr]
 
 
-def group_mean_query(query_tail: np.ndarray, h_kv: int) -> np.ndarray:
-    """[B, H_Q, W, D] -> bf16 mean over each KV group (src/ops/d_stage_kv_cache.py:131-133)."""
+def group_mean_query(query_tail: np.ndarray, h_kv: int, fp16: bool = False) -> np.ndarray:
+    """[B, H_Q, W, D] -> bf16 (fp16) mean over each KV group (src/ops/d_stage_kv_cache.py:131-133)."""
     B, HQ, W, D = query_tail.shape
     R = HQ // h_kv
-    return mean_bf16(query_tail.reshape(B, h_kv, R, W, D), axis=2)
+    return mean_half(query_tail.reshape(B, h_kv, R, W, D), 2, fp16)
 
 
 def freeze(keys: np.ndarray, values: np.ndarray, query_tail: Optional[np.ndarray],
            window_size: int, top_ratio: float, kv_repeat: int,
-           k_bits: int = 4, v_bits: int = 4, use_vert: bool = True) -> DecodeState:
+           k_bits: int = 4, v_bits: int = 4, use_vert: bool = True, fp16: bool = False) -> DecodeState:
     """Prefill -> decode reorganisation (src/ops/d_stage_kv_cache.py:106-189).
 
     keys/values [B, H_KV, N, D]; query_tail [B, H_Q, W', D] (the last
-    min(window_size, Q) prefill queries, :97-100).
+    min(window_size, Q) prefill queries, :97-100).  fp16=True: an fp16
+    model's values; the selector's means and scores are fp16 (quantisation
+    is the same formula on the fp16 values).
     """
     B, HKV, N, D = keys.shape
     BH = B * HKV
@@ -332,10 +357,10 @@ def freeze(keys: np.ndarray, values: np.ndarray, query_tail: Optional[np.ndarray
         kp = keys[:, :, :P, :]
         vp = values[:, :, :P, :]
         if use_vert and query_tail is not None and kv_repeat >= 1:
-            q_kv = group_mean_query(query_tail, HKV)                       # [B, HKV, W', D]
+            q_kv = group_mean_query(query_tail, HKV, fp16)                 # [B, HKV, W', D]
             # the selector again subtracts window_size from the already
             # window-free prefix (F3: vertical lines come from [0, N - 2W))
-            topk_idx = compute_vertical_indices(q_kv, kp, window_size, top_ratio)
+            topk_idx = compute_vertical_indices(q_kv, kp, window_size, top_ratio, fp16=fp16)
         T = topk_idx.shape[-1]
         sel = np.zeros((B, HKV, P), dtype=bool)
         bi, hi = np.meshgrid(np.arange(B), np.arange(HKV), indexing="ij")
@@ -600,12 +625,16 @@ def per_block_int8(x: np.ndarray, sm: float, blk: int) -> Tuple[np.ndarray, np.n
     return codes, scales
 
 
-def smooth_keys(k: np.ndarray, smooth: bool = True) -> Tuple[np.ndarray, np.ndarray]:
+def smooth_keys(k: np.ndarray, smooth: bool = True, fp16: bool = False) -> Tuple[np.ndarray, np.ndarray]:
     """K-smoothing (sage_unified.py:565-570): km = bf16 mean over the sequence
     (exact float64 sum, one RNE rounding), ks = bf16(fp32(k) - fp32(km)).
+    fp16=True (an fp16 model, k holding fp16 values): the same in fp16.
     Returns (km [..., 1, D], ks)."""
     if not smooth:
         return np.zeros(k.shape[:-2] + (1, k.shape[-1]), np.float32), np.asarray(k, np.float32)
+    if fp16:
+        km = mean_f16(k, axis=-2)[..., None, :]
+        return km, to_fp16((np.asarray(k, np.float32) - km).astype(np.float32))
     km = mean_bf16(k, axis=-2)[..., None, :]
     ks = bf16_round((np.asarray(k, np.float32) - km).astype(np.float32))
     return km, ks
@@ -643,18 +672,21 @@ def window_start(b: int, W: int) -> int:
     return max(0, PREFILL_BLOCK_M * b - (W - 1)) // PREFILL_BLOCK_N * PREFILL_BLOCK_N
 
 
-def prefill_operands(q, k, v, sm_scale: Optional[float] = None, smooth: bool = True):
+def prefill_operands(q, k, v, sm_scale: Optional[float] = None, smooth: bool = True, fp16: bool = False):
     """The wrapper's operand preparation (sage_unified.py:559-584):
     c = fp32(sm_scale * log2e); Q int8 per 128-row block of x = fp32(q) * c
     (codes, scales); q16 = fp16(bf16(fp32(q) * c)); km and the smoothed keys
-    ks = bf16(k - km) as fp16; v16 = fp16(v).  Returns a dict."""
+    ks = bf16(k - km) as fp16; v16 = fp16(v).  fp16=True (an fp16 model: q,
+    k, v hold fp16 values) takes the reference's fp16 branch (:569, :575-576):
+    q16 = fp16(fp32(q) * c), km and ks rounded to fp16.  Returns a dict."""
     D = q.shape[-1]
     if sm_scale is None:
         sm_scale = D ** -0.5
     c = np.float32(sm_scale * LOG2E)
     q8, qsc = per_block_int8(q, c, PREFILL_BLOCK_M)
-    q16 = to_fp16(bf16_round((np.asarray(q, np.float32) * c).astype(np.float32)))
-    km, ks = smooth_keys(k, smooth)
+    qc = (np.asarray(q, np.float32) * c).astype(np.float32)
+    q16 = to_fp16(qc if fp16 else bf16_round(qc))
+    km, ks = smooth_keys(k, smooth, fp16)
     return dict(c=c, q8=q8, q_scale=qsc, q16=q16, km=km, k16=to_fp16(ks), v16=to_fp16(v))
 
 
@@ -727,7 +759,7 @@ def _round_span(x: np.ndarray, rnd, rel: float) -> np.ndarray:
 
 def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None, smooth: bool = True,
                         int8_rest: bool = True, abs_v: bool = False, pv_mode: str = "fp16",
-                        qk_mode: str = "int8", blocks=None, fp8_detail: bool = False):
+                        qk_mode: str = "int8", blocks=None, fp8_detail: bool = False, fp16: bool = False):
     """float64 restatement of sage_vertical_attention_v2 (sage_unified.py:550-622,
     kernel :398-496).  q [B, HQ, N, D], k/v [B, HKV, N, D] (bf16 values),
     vidx [B, HQ, T].  For query row i of block b (128 rows):
@@ -752,7 +784,7 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
     s = (q8 . k8) * q_scale * k_scale, everything else unchanged.
 
     blocks: the 128-row query blocks to compute (default all); rows of other
-    blocks are left zero.
+    blocks are left zero.  fp16: q, k, v are an fp16 model's (prefill_operands).
 
     fp8_detail (pv_mode='fp8'): also return `slack` and `exact_rows`.
     slack [B, HQ, N, D] = sum over keys j of |V_j| vs / l times the step
@@ -771,7 +803,7 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
     B, HQ, N, D = q.shape
     HKV = k.shape[1]
     G = HQ // HKV
-    op = prefill_operands(q, k, v, sm_scale, smooth)
+    op = prefill_operands(q, k, v, sm_scale, smooth, fp16)
     q8, qsc, q16, k16, v16 = op["q8"], op["q_scale"], op["q16"], op["k16"], op["v16"]
     quant = per_block_int8
     if qk_mode == "fp8":
@@ -851,7 +883,7 @@ def hybrid_prefill_fp64(q, k, v, vidx, W: int, sm_scale: Optional[float] = None,
 
 
 def unified_prefill_fp64(q, k, v, W: int, sm_scale: Optional[float] = None, smooth: bool = True,
-                         int8: bool = True, abs_v: bool = False, blocks=None):
+                         int8: bool = True, abs_v: bool = False, blocks=None, fp16: bool = False):
     """float64 restatement of sage_unified_attention (sage_unified.py:234-313,
     kernel _attn_fwd_unified :112-231).  W > 0: int8 keys below wla(b), the
     fp16 causal window wla(b) <= j <= i; this is hybrid_prefill_fp64 with no
@@ -864,10 +896,10 @@ def unified_prefill_fp64(q, k, v, W: int, sm_scale: Optional[float] = None, smoo
     B, HQ, N, D = q.shape
     if W > 0:
         return hybrid_prefill_fp64(q, k, v, np.zeros((B, HQ, 0), np.int64), W, sm_scale, smooth,
-                                   int8_rest=int8, abs_v=abs_v, blocks=blocks)
+                                   int8_rest=int8, abs_v=abs_v, blocks=blocks, fp16=fp16)
     HKV = k.shape[1]
     G = HQ // HKV
-    op = prefill_operands(q, k, v, sm_scale, smooth)
+    op = prefill_operands(q, k, v, sm_scale, smooth, fp16)
     q8, qsc, q16, k16, v16 = op["q8"], op["q_scale"], op["q16"], op["k16"], op["v16"]
     if abs_v:
         v16 = np.abs(v16)

@@ -40,7 +40,7 @@ def _L():
 
 def test_abi_version_and_error_strings():
     _lib, L = _L()
-    assert L.hyq_abi_version() == 3
+    assert L.hyq_abi_version() == _lib.ABI_VERSION == 4
     st = L.hyq_quant_pack(None, 0, 1, 1, 128, 0, 0, 3, None, 0, 0, None, 0, None)
     assert st == _lib.HYQ_EINVAL
     assert b"nbits must be 2, 4, or 8" in L.hyq_last_error()
@@ -108,6 +108,29 @@ def test_decode_host_validation():
                 kp_stride_bh=512 * 64, kp_stride_n=64, vp_stride_bh=512 * 64, vp_stride_n=64)
     assert L.hyq_decode_hybrid(p, 4096, 1 << 30, None) == _lib.HYQ_EINVAL
     assert b"16 * bits" in L.hyq_last_error()
+
+
+def test_dtype_flags_host_validation():
+    """The fp16-model switches: unknown dtype_flags bits, and is_fp16 /
+    dtype_fp16 values other than 0 and 1, are EINVAL before any launch."""
+    _lib, L = _L()
+    ok = _lib.HYQ_DT_Q_FP16 | _lib.HYQ_DT_SEG_FP16 | _lib.HYQ_DT_OUT_FP16
+    assert L.hyq_decode_workspace_size(_params(_lib, dtype_flags=ok)) > 0
+    p = _params(_lib, dtype_flags=8)
+    assert L.hyq_decode_workspace_size(p) == 0
+    assert L.hyq_decode_hybrid(p, None, 0, None) == _lib.HYQ_EINVAL
+    assert b"dtype_flags" in L.hyq_last_error()
+    assert L.hyq_vertical_select(None, 0, 0, 0, 4, 2, 1, None, 0, 0, 0, 2, 10, 1, 128, 4, 3, 2,
+                                 None, None, 0, None) == _lib.HYQ_EINVAL
+    assert b"is_fp16" in L.hyq_last_error()
+    args = [None, 0, 0, 0, None, 0, 0, 0, 1, 1, 64, 128, 16, None, 0, 4, 4, 5] + [None, 0, 0] * 2 + \
+        [None, 0] * 2 + [None, 0, 0] * 4 + [None, 0, None]
+    assert L.hyq_freeze_reorganise(*args) == _lib.HYQ_EINVAL
+    assert b"is_fp16" in L.hyq_last_error()
+    pp = _lib.PrefillParams()
+    pp.batch, pp.hq, pp.hkv, pp.head_dim, pp.n, pp.t, pp.window, pp.dtype_fp16 = 1, 1, 1, 128, 64, 0, 16, 2
+    assert L.hyq_prefill_hybrid(ctypes.byref(pp), None, 0, None) == _lib.HYQ_EINVAL
+    assert b"dtype_fp16" in L.hyq_last_error()
 
 
 def test_decode_noalloc_host_validation():

@@ -264,3 +264,60 @@ def test_decode_batched_ragged_lengths(kb, vb):
         ref = O.decode_fp64(*args, k_bits=kb, v_bits=vb, kv_repeat=G)
         ref_abs = O.decode_fp64(*args, k_bits=kb, v_bits=vb, kv_repeat=G, abs_v=True)
         _check(f"batched seq {s} lens {nq}/{nb}", out[s * HKV * G:(s + 1) * HKV * G], ref, ref_abs=ref_abs)
+
+
+def _bf16_neighbours_ok(out16: np.ndarray, outb: np.ndarray) -> np.ndarray:
+    """out16 = fp16(r) and outb = bf16(r) of one float32 r: bf16(out16) equals
+    outb unless out16 sits exactly halfway between two bf16 values (then the
+    rounding of r decides), where outb must be one of those two.  Below 2^-14
+    fp16 is subnormal and coarser than bf16: there |outb - out16| <= 2^-24."""
+    x = out16.astype(np.float32)
+    rb = O.bf16_round(x)
+    lo = O.bf16_round(np.nextafter(x, np.float32(-np.inf)).astype(np.float32))
+    hi = O.bf16_round(np.nextafter(x, np.float32(np.inf)).astype(np.float32))
+    tiny = (np.abs(x) < 2.0 ** -14) & (np.abs(outb - x) <= 2.0 ** -24)
+    return (rb == outb) | ((lo != hi) & ((outb == lo) | (outb == hi))) | tiny
+
+
+@pytest.mark.parametrize("N,split", [(300, 0), (4096, 0), (4096, 256)])
+def test_decode_fp16_model(N, split):
+    """An fp16 model: fp16 q and fp16 top-k / staging / window segments.  The
+    reference rounds them to bf16 before its products
+    (src/ops/decode_d_stage.py:537-541, 240-263) and returns q.dtype (:866):
+    the fp16 result is within 2e-3 of the fp64 oracle on the bf16-rounded
+    state, and it is the same float32 result as a bf16 call on the
+    bf16-rounded inputs, rounded to fp16 instead of bf16 (checked exactly)."""
+    import hyquant_amd as hq
+    inp = O.make_decode_inputs(B=1, HQ=32, HKV=8, N=N, W=128, S=37, seed=5)
+    st = O.build_decode_state(inp)
+    G = 4
+    rng = np.random.default_rng(N + split)
+    # fp16 values with mantissa bits bf16 does not hold
+    f16 = lambda a: (a * (1 + rng.uniform(-2 ** -8, 2 ** -8, a.shape))).astype(np.float16)
+    names = ("k_topk", "v_topk", "k_staging", "v_staging", "k_window", "v_window")
+    seg16 = {n: f16(np.asarray(getattr(st, n), np.float32)) for n in names}
+    q16 = (inp.q_dec * rng.uniform(0.9, 1.1, inp.q_dec.shape)).astype(np.float16)
+    assert not np.array_equal(O.bf16_round(q16.astype(np.float32)), q16.astype(np.float32))
+    # the oracle state: the same values rounded to bf16
+    rb = lambda a: O.bf16_round(a.astype(np.float32))
+    st.k_topk, st.v_topk = rb(seg16["k_topk"]), rb(seg16["v_topk"])
+    st.k_window, st.v_window = rb(seg16["k_window"]), rb(seg16["v_window"])
+    st.k_ring[:, :st.ring_ptr] = rb(seg16["k_staging"])
+    st.v_ring[:, :st.ring_ptr] = rb(seg16["v_staging"])
+    qb = rb(q16)
+    dev = torch.device("cuda")
+    t = state_to_device(st, dev)
+    d16 = {n: torch.from_numpy(np.ascontiguousarray(seg16[n])).to(dev) for n in names}
+    print(f"decode fp16 model N={N} split={split}", flush=True)
+    out16 = hq.fused_d_stage_decode(torch.from_numpy(q16).to(dev), t["k_packed"], t["v_packed"], t["k_scale"],
+                                    t["v_scale"], *[d16[n] for n in names], 4, 4, kv_repeat=G,
+                                    split_tokens=split)
+    outb = hq.fused_d_stage_decode(to_dev_bf16(qb, dev), t["k_packed"], t["v_packed"], t["k_scale"],
+                                   t["v_scale"], *[t[n] for n in names], 4, 4, kv_repeat=G, split_tokens=split)
+    torch.cuda.synchronize()
+    assert out16.dtype == torch.float16 and outb.dtype == torch.bfloat16
+    o16 = out16.float().cpu().numpy()
+    ob = outb.float().cpu().numpy()
+    _check(f"fp16 model N={N}", o16, O.decode_fp64_state(qb, st, G))
+    ok = _bf16_neighbours_ok(o16, ob)
+    assert ok.all(), f"{int((~ok).sum())} outputs are not the fp16 rounding of the bf16 call's float32 result"

@@ -376,3 +376,63 @@ def test_prefill_past_131072_positions():
     rows = np.concatenate([np.arange(b * 128, min(N, (b + 1) * 128)) for b in blocks])
     o = out[:, :1].float().cpu().numpy()
     _check(f"N={N} head 0 blocks {blocks}", o[:, :, rows], ref[:, :, rows], ref_abs[:, :, rows])
+
+
+FP16_CASES = [
+    dict(entry="hybrid", B=2, HQ=8, HKV=2, N=1000, W=100, T=45, seed=61),
+    dict(entry="hybrid_fp8pv", B=1, HQ=4, HKV=1, N=640, W=128, T=30, seed=62),
+    dict(entry="unified", B=1, HQ=4, HKV=2, N=700, W=128, T=0, seed=63),
+    dict(entry="unified_w0", B=1, HQ=2, HKV=1, N=520, W=0, T=0, seed=64),
+    dict(entry="fp8qk", B=1, HQ=4, HKV=1, N=640, W=128, T=30, seed=65),
+]
+
+
+@pytest.mark.parametrize("cfg", FP16_CASES, ids=[c["entry"] for c in FP16_CASES])
+def test_prefill_fp16_model(cfg):
+    """An fp16 model's prefill (src/ops/sage_unified.py:565-580 and
+    sage_unified_fp8.py:344-351, the dtype == float16 branch): fp16 q, k, v in,
+    fp16 out, against the float64 restatement of that branch.  The kernel
+    must also be much closer to it than to the bf16 branch on the same
+    values (which rounds q * c and k - km to bf16 first), so a kernel that
+    took the wrong branch fails."""
+    from hyquant_amd import sage_unified as su
+    print(f"prefill fp16 {cfg}", flush=True)
+    rng = np.random.default_rng(cfg["seed"])
+    B, HQ, HKV, N, W, T = (cfg[x] for x in ("B", "HQ", "HKV", "N", "W", "T"))
+    f16 = lambda a: a.astype(np.float16).astype(np.float32)
+    q = f16(rng.standard_normal((B, HQ, N, 128)) * 1.3)
+    k = f16(rng.standard_normal((B, HKV, N, 128)) * 1.5 + rng.standard_normal((1, HKV, 1, 128)))
+    v = f16(rng.standard_normal((B, HKV, N, 128)))
+    P = max(0, N - W)
+    vidx = np.stack([np.stack([rng.permutation(P)[:T] if P else np.zeros(0, np.int64) for _ in range(HQ)])
+                     for _ in range(B)]).astype(np.int64).reshape(B, HQ, T)
+    dev = torch.device("cuda")
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(torch.float16).to(dev)
+    vi = torch.from_numpy(vidx).to(dev)
+    e = cfg["entry"]
+    if e.startswith("hybrid"):
+        pv = "fp8" if e == "hybrid_fp8pv" else "fp16"
+        out = su.sage_vertical_attention_v2(d(q), d(k), d(v), vi, window_size=W, pv_mode=pv)
+        oracle = lambda fp16, **kw: O.hybrid_prefill_fp64(q, k, v, vidx, W, pv_mode=pv, fp16=fp16, **kw)
+    elif e == "fp8qk":
+        out = su.sage_vertical_attention_v2_fp8(d(q), d(k), d(v), vi, window_size=W)
+        oracle = lambda fp16, **kw: O.hybrid_prefill_fp64(q, k, v, vidx, W, qk_mode="fp8", fp16=fp16, **kw)
+    else:
+        out = su.sage_unified_attention(d(q), d(k), d(v), window_size=W)
+        oracle = lambda fp16, **kw: O.unified_prefill_fp64(q, k, v, W, fp16=fp16, **kw)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16
+    out = out.float().cpu().numpy()
+    ref = oracle(True)
+    ref_abs = oracle(True, abs_v=True)
+    if e == "hybrid_fp8pv":
+        # e4m3 P' and V: the loose fp8 bound of test_prefill_fp8_pv_vs_oracle
+        diff = np.abs(out - ref)
+        assert np.all(diff <= ATOL + 2.0 ** -3 * ref_abs + 2.0 ** -8 * np.abs(ref)), float(diff.max())
+    else:
+        _check(f"fp16 {e}", out, ref, ref_abs)
+    mse16 = float(np.mean((out - ref) ** 2))
+    mse_b = float(np.mean((out - oracle(False)) ** 2))
+    print(f"  mse vs fp16 branch {mse16:.3e}, vs bf16 branch {mse_b:.3e}", flush=True)
+    if e != "hybrid_fp8pv":        # there the e4m3 rounding of P' hides the branch difference
+        assert mse16 * 4 < mse_b

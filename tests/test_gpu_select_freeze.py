@@ -213,7 +213,7 @@ def test_freeze_bad_indices_stay_inside_the_outputs():
     ws = torch.empty(max(L.hyq_freeze_workspace_size(HK, P), 256), dtype=torch.uint8, device=dev)
     st = L.hyq_freeze_reorganise(
         kd.data_ptr(), kd.stride(0), kd.stride(1), kd.stride(2), vd.data_ptr(), vd.stride(0), vd.stride(1),
-        vd.stride(2), 1, HK, N, 128, W, ti.data_ptr(), T, 4, 4,
+        vd.stride(2), 1, HK, N, 128, W, ti.data_ptr(), T, 4, 4, 0,
         kp.data_ptr(), kp.stride(0), kp.stride(1), vp.data_ptr(), vp.stride(0), vp.stride(1),
         ks.data_ptr(), ks.stride(0), vs.data_ptr(), vs.stride(0),
         kt.data_ptr(), kt.stride(0), kt.stride(1), vt.data_ptr(), vt.stride(0), vt.stride(1),
@@ -268,3 +268,57 @@ def test_freeze_long_prefix_bit_exact():
     st = O.freeze(inp.keys, inp.values, inp.query_tail, inp.W, inp.rho, 4)
     torch.cuda.synchronize()
     _check_state(layer, st)
+
+
+def test_fp16_model_selector_freeze_flush_decode():
+    """An fp16 model through the cache (src/ops/d_stage_kv_cache.py:82-217 with
+    fp16 K/V): the prefill-time and freeze-time selections bit-exact with the
+    oracle's fp16 branch (means and scores rounded to fp16), the frozen
+    segments and codes bit-exact, a flush of fp16 staging tokens bit-exact,
+    and the decode (fp16 q, fp16 segments, fp16 out) within 2e-3 of the
+    float64 oracle on the bf16-rounded segments the reference's kernel sees."""
+    from hyquant_amd.d_stage_kv_cache import DStageLayerCache
+    from hyquant_amd.vertical import compute_vertical_indices
+    inp = O.make_decode_inputs(B=1, HQ=32, HKV=8, N=2048, W=128, S=37, seed=17)
+    G = inp.HQ // inp.HKV
+    rng = np.random.default_rng(17)
+    f16 = lambda a: (a * (1 + rng.uniform(-2 ** -8, 2 ** -8, a.shape))).astype(np.float16).astype(np.float32)
+    keys, values, qt = f16(inp.keys), f16(inp.values), f16(inp.query_tail)
+    kn, vn, qd = f16(inp.k_new), f16(inp.v_new), f16(inp.q_dec)
+    dev = torch.device("cuda")
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(torch.float16).to(dev)
+    print("fp16 model cache", flush=True)
+    got_q = compute_vertical_indices(d(qt), d(keys), inp.W, inp.rho, kv_repeat=G)
+    exp_q = O.compute_vertical_indices(qt, keys, inp.W, inp.rho, kv_repeat=G, fp16=True)
+    assert np.array_equal(got_q.cpu().numpy(), exp_q)
+    layer = DStageLayerCache(0, k_bits=4, v_bits=4, window_size=inp.W, top_ratio=inp.rho)
+    layer.update_prefill(d(keys), d(values))
+    layer.save_query_tail(d(qt))
+    layer.freeze(kv_repeat=G)
+    st = O.freeze(keys, values, qt, inp.W, inp.rho, G, fp16=True)
+    torch.cuda.synchronize()
+    assert layer.k_topk.dtype == torch.float16
+    # the fp16 selection differs from the bf16 one on these inputs
+    st_b = O.freeze(keys, values, qt, inp.W, inp.rho, G)
+    print(f"  fp16 / bf16 top-k sets differ: {not np.array_equal(st.topk_idx, st_b.topk_idx)}", flush=True)
+    _check_state(layer, st)
+    layer.append_staging(d(kn), d(vn))
+    O.append_staging(st, kn, vn)
+    extra_k = f16(_rand_bf16(rng, (1, inp.HKV, 100, 128), 1.4))
+    extra_v = f16(_rand_bf16(rng, (1, inp.HKV, 100, 128)))
+    for i in range(100):
+        layer.append_staging(d(extra_k[:, :, i:i + 1]), d(extra_v[:, :, i:i + 1]))
+    O.append_staging(st, extra_k, extra_v)
+    torch.cuda.synchronize()
+    _check_state(layer, st)
+    out = layer.decode_attention(d(qd).reshape(1, inp.HQ, 1, 128), G)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16
+    out = out.reshape(-1, 128).float().cpu().numpy()
+    rb = O.bf16_round
+    st.k_topk, st.v_topk, st.k_window, st.v_window = rb(st.k_topk), rb(st.v_topk), rb(st.k_window), rb(st.v_window)
+    st.k_ring, st.v_ring = rb(st.k_ring), rb(st.v_ring)
+    ref = O.decode_fp64_state(rb(qd), st, G)
+    err = float(np.max(np.abs(out - ref)))
+    print(f"  fp16 cache decode max-abs {err:.3e}", flush=True)
+    assert err <= 2e-3

@@ -91,6 +91,41 @@ def test_operands_against_rationals():
             assert Fraction(float(op["k16"][0, 0, j, d])) == exp
 
 
+def test_operands_fp16_model_against_rationals_and_torch():
+    """The fp16 branch (sage_unified.py:569, :575-576): q16 = fp16(fp32(q) * c)
+    with one rounding, km = fp16(mean), k16 = fp16(fp32(k - km)); rederived
+    with exact rationals, and q16 / k16 (given km) equal to torch's own fp16
+    arithmetic on the same tensors."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(11)
+    q = (rng.standard_normal((1, 1, 3, 8)) * 3).astype(np.float16).astype(np.float32)
+    k = (rng.standard_normal((1, 1, 5, 8)) * 2 + 0.5).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((1, 1, 5, 8)).astype(np.float16).astype(np.float32)
+    assert not np.array_equal(O.bf16_round(q), q)         # fp16 values bf16 cannot hold
+    op = O.prefill_operands(q, k, v, sm_scale=8 ** -0.5, fp16=True)
+    c = Fraction(float(np.float32(8 ** -0.5 * O.LOG2E)))
+    for i in range(3):
+        for d in range(8):
+            exp = to_fp16(to_fp32(Fraction(float(q[0, 0, i, d])) * c))
+            assert Fraction(float(op["q16"][0, 0, i, d])) == exp
+    for d in range(8):
+        km = to_fp16(sum(Fraction(float(k[0, 0, j, d])) for j in range(5)) / 5)
+        assert Fraction(float(op["km"][0, 0, 0, d])) == km
+        for j in range(5):
+            exp = to_fp16(to_fp32(Fraction(float(k[0, 0, j, d])) - km))
+            assert Fraction(float(op["k16"][0, 0, j, d])) == exp
+    # torch's fp16 elementwise ops on the same values
+    qt = torch.from_numpy(q).to(torch.float16)
+    sm_l2e = 8 ** -0.5 * O.LOG2E
+    assert np.array_equal((qt * sm_l2e).float().numpy(), op["q16"])
+    kt = torch.from_numpy(k).to(torch.float16)
+    kmt = torch.from_numpy(op["km"]).to(torch.float16)
+    assert np.array_equal((kt - kmt).float().numpy(), op["k16"])
+    assert np.array_equal(O.to_fp16(v), v)
+    # the bf16 branch differs on these inputs (it rounds q * c to bf16 first)
+    assert not np.array_equal(O.prefill_operands(q, k, v, sm_scale=8 ** -0.5)["q16"], op["q16"])
+
+
 def test_lists_partition_and_duplicates():
     N, W = 700, 100
     vidx = np.array([5, 3, 590, 599, 3, 10_000, -4])           # duplicate, out of range both ways

@@ -10,15 +10,16 @@ import numpy as np
 import pytest
 
 from oracle import hyq_oracle as O
-from tests._exact import to_bf16
+from tests._exact import to_bf16, to_fp16
 
 
 def _rand_bf16(rng, shape, scale=1.0):
     return O.bf16_round((rng.standard_normal(shape) * scale).astype(np.float32))
 
 
-def _brute_select(q, k, W, rho, kv_repeat=1):
-    """Selector by exact rational arithmetic and a full Python sort."""
+def _brute_select(q, k, W, rho, kv_repeat=1, rnd=to_bf16):
+    """Selector by exact rational arithmetic and a full Python sort (rnd: the
+    model dtype's rounding)."""
     B, HQ, QL, D = q.shape
     P = max(0, k.shape[2] - W)
     tail = min(W, QL)
@@ -27,10 +28,10 @@ def _brute_select(q, k, W, rho, kv_repeat=1):
     for b in range(B):
         for h in range(HQ):
             hk = h // kv_repeat if k.shape[1] != HQ else h
-            qm = [to_bf16(sum(Fraction(float(q[b, h, QL - tail + i, d])) for i in range(tail)) / tail) for d in range(D)]
+            qm = [rnd(sum(Fraction(float(q[b, h, QL - tail + i, d])) for i in range(tail)) / tail) for d in range(D)]
             sc = []
             for p in range(P):
-                s = to_bf16(sum(qm[d] * Fraction(float(k[b, hk, p, d])) for d in range(D)))
+                s = rnd(sum(qm[d] * Fraction(float(k[b, hk, p, d])) for d in range(D)))
                 sc.append((-s, p))
             sc.sort()
             out[b, h] = [p for _, p in sc[:T]]
@@ -47,6 +48,41 @@ def test_selector_brute_force(kv_repeat):
     exp = _brute_select(q, k, 4, 0.2, kv_repeat)
     assert got.shape == (1, HQ, 6)
     assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("kv_repeat", [1, 2])
+def test_selector_fp16_model_brute_force(kv_repeat):
+    """An fp16 model's selector: fp16 means and scores (torch computes
+    query_tail.mean and the matmul in the model dtype), brute-forced with
+    exact rationals; scores are spread so that fp16 and bf16 rankings differ."""
+    rng = np.random.default_rng(20)
+    HQ = 2
+    q = (rng.standard_normal((1, HQ, 5, 8))).astype(np.float16).astype(np.float32)
+    k = (rng.standard_normal((1, HQ // kv_repeat, 40, 8)) * 2).astype(np.float16).astype(np.float32)
+    got = O.compute_vertical_indices(q, k, 4, 0.3, kv_repeat=kv_repeat, fp16=True)
+    exp = _brute_select(q, k, 4, 0.3, kv_repeat, rnd=to_fp16)
+    assert np.array_equal(got, exp)
+    # the group mean of the freeze-time call, in fp16
+    qt = (rng.standard_normal((1, 4, 3, 8)) * 3).astype(np.float16).astype(np.float32)
+    gm = O.group_mean_query(qt, 2, fp16=True)
+    for h in range(2):
+        for t in range(3):
+            for d in range(8):
+                exp_m = to_fp16((Fraction(float(qt[0, 2 * h, t, d])) + Fraction(float(qt[0, 2 * h + 1, t, d]))) / 2)
+                assert Fraction(float(gm[0, h, t, d])) == exp_m
+
+
+def test_selector_fp16_ties_and_signed_zero():
+    """Ties and -0 in fp16 keys: same rules as bf16."""
+    q = np.ones((1, 1, 1, 2), np.float32)
+    k = np.zeros((1, 1, 6, 2), np.float32)
+    k[0, 0, 0] = [1.0, -1.0]
+    k[0, 0, 2] = [-0.0, -0.0]
+    k[0, 0, 1] = [-1.0, 0.0]
+    k[0, 0, 3] = [1000.0, 1e-3]     # 1000.001 rounds to 1000 in fp16 (a tie with row 4)
+    k[0, 0, 4] = [1000.0, 0.0]
+    got = O.compute_vertical_indices(q, k, window_size=1, top_ratio=0.8, fp16=True)
+    assert got.tolist() == [[[3, 4, 0, 2]]]
 
 
 def test_selector_ties_lower_index_first():

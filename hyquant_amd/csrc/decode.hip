@@ -81,7 +81,6 @@ constexpr int MAX_PARTIALS = 1024;       // nwg * G bound
 constexpr int MAX_NWG = 256;             // chunks per head (merge weight table)
 constexpr int CNT_PAD = 32;              // arrival counters 128 bytes apart
 constexpr int CNT_CAP = 16384;           // counter slots at the head of every workspace (bh_kv bound)
-constexpr int MJ = 24;                   // partial float4 loads per lane per merge batch
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -115,6 +114,7 @@ struct DecArgs {
     const int32_t* len_q;  // optional per-head valid prefix tokens
     const int32_t* len_s0; // optional per-head valid tokens of segment 0
     int32_t io;            // HYQ_DT_* flags: fp16 q / fp16 segments / fp16 out
+    int32_t mj;            // merge batch: partial columns per merging thread and load batch
 };
 
 struct WaveState {
@@ -527,20 +527,29 @@ __device__ __forceinline__ float wave_sum64(float v) {
     return col_sum(v);
 }
 
-__device__ __forceinline__ void wave_sync_lds() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// One wavefront per query head g.  Lane (h, q) = (lane >> 5, lane & 31) sums
-// channels 4q..4q+3 over the partials w = 2j + h (a row swap adds the two
-// halves).  Lane w computes the weight exp2(m_w - M_g) of partial w (and
-// w + 64, ...); the wavefront max / sum give M_g and the denominator
-// sum_w exp2(m_w - M_g) l_w; the weights reach every lane through a
-// per-wavefront LDS table (same-address reads broadcast).  The first batch of
-// partial loads is issued before the (m, l) loads, so the merge is about one
-// memory round trip while nwg <= 2 * MJ.
+// The merge of a head's partials, by all THREADS threads of its last
+// workgroup.  The partials of query head g are rows of D floats, so the head
+// has NC = 32 G float4 columns.  For G <= 8 thread t owns column t % NC of
+// the partials s, s + TPC, ... (s = t / NC, TPC = THREADS / NC threads per
+// column); for G > 8 it owns columns t and t + THREADS of every partial.  A
+// thread's items alternate between two accumulators: item e goes to acc[e & 1]
+// (its two columns for G > 8, the even and odd partials of its column
+// otherwise).
+//   1. every (m, l) pair of the head is loaded (two float4 per thread), then
+//      the thread's first MJ items, all before any wait: the weights are
+//      built while the partial loads are in flight;
+//   2. (m, l) go to LDS; wavefront w takes query heads w, w + 4, ...: lane p
+//      holds partial p (p + 64, ...), the wavefront max / sum give M_g and
+//      den_g = sum_p exp2(m_p - M_g) l_p, and the weight exp2(m_p - M_g)
+//      replaces m_p in LDS;
+//   3. each thread sums weight * partial over its items in order (further
+//      batches of MJ loads when it owns more), the TPC threads of a column
+//      add their sums in subset order through LDS, and the column is divided
+//      by den_g and stored.
+// Items past a thread's share load from an offset outside the buffer range
+// (zeros) and take their weight from an LDS slot holding zero, so the loops
+// have no branches.  The summation order depends on nothing but (G, nwg):
+// every call gives the same result.
 struct MergeArgs {
     int G, nwg;
     const float* part;
@@ -550,82 +559,196 @@ struct MergeArgs {
     int out16;             // store fp16 instead of bf16
 };
 
-__device__ __forceinline__ void merge_head(const MergeArgs& a, int head, float* s_wt) {
-    const int G = a.G, nwg = a.nwg;
+constexpr int ML_LDS = 2 * MAX_PARTIALS;               // (m, l) per partial; the weights overwrite m
+constexpr int ZERO_SLOT = ML_LDS + 16;                  // holds 0.0f (weight of an empty item)
+constexpr int COMB_LDS = ML_LDS + 32;                   // one float4 per thread (column sums)
+constexpr int MERGE_LDS = COMB_LDS + 4 * THREADS;
+constexpr uint32_t OUT_OF_RANGE = 0xfffffff0u;          // a buffer offset past every range: reads zero
+
+// Column q (channels 4q..4q+3) of query head g: acc / den rounded once to
+// the output dtype (out.to(q.dtype) of the fp32 result), 0 when den == 0.
+__device__ __forceinline__ void store_out(const MergeArgs& a, int head, int g, int q, const f32x4& acc, float den) {
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = den > 0.f ? acc[i] / den : 0.f;
+    const u32x2 o = a.out16 ? u32x2{static_cast<uint32_t>(f32_to_f16_bits(r[0])) |
+                                        (static_cast<uint32_t>(f32_to_f16_bits(r[1])) << 16),
+                                    static_cast<uint32_t>(f32_to_f16_bits(r[2])) |
+                                        (static_cast<uint32_t>(f32_to_f16_bits(r[3])) << 16)}
+                            : u32x2{static_cast<uint32_t>(f32_to_bf16_rne(r[0])) |
+                                        (static_cast<uint32_t>(f32_to_bf16_rne(r[1])) << 16),
+                                    static_cast<uint32_t>(f32_to_bf16_rne(r[2])) |
+                                        (static_cast<uint32_t>(f32_to_bf16_rne(r[3])) << 16)};
+    *reinterpret_cast<u32x2*>(a.out + static_cast<int64_t>(head * a.G + g) * a.out_stride + 4 * q) = o;
+}
+
+// G <= 4: one wavefront per query head g, no workgroup barrier.  Lane
+// (h, q) = (lane >> 5, lane & 31) sums channels 4q..4q+3 of g over the
+// partials 2j + h; lane p holds (m, l) of partial p (p + 64, ...).  The (m, l)
+// loads go first, then the first MJ partial loads (MJ >= half the partials
+// when the host can pick it), so the weights are built while the partials
+// are in flight; they reach the lanes through a per-wavefront LDS table
+// (same-address reads broadcast), whose entries past nwg hold zero, and a
+// row swap adds the two halves.
+template <int MJ>
+__device__ __forceinline__ void merge_head_waves(const MergeArgs& a, int head, float* lds) {
+    const int G = a.G, P = a.nwg;
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (g >= G) return;
     const int h = lane >> 5, q = lane & 31;
-    const int npair = nwg * G;
+    const int npair = P * G;
     const Rsrc rp = make_rsrc(a.part + static_cast<int64_t>(head) * npair * D, static_cast<uint32_t>(npair) * D * 4);
     const Rsrc rm = make_rsrc(a.ml + static_cast<int64_t>(head) * npair * 2, static_cast<uint32_t>(npair) * 8);
-    float* wt = s_wt + wave * MAX_NWG;
-    const int npr = (nwg + 1) / 2;                   // partial pairs
+    float* wt = lds + g * MAX_NWG;
+    // (m, l) of partials lane, lane + 64, ... (past nwg: out of range, zeros)
+    u32x2 mlr[MAX_NWG / 64];
+#pragma unroll
+    for (int k = 0; k < MAX_NWG / 64; ++k) mlr[k] = ld2_dev(rm, static_cast<uint32_t>(((lane + 64 * k) * G + g) * 8));
+    const uint32_t pbase = static_cast<uint32_t>(((h * G + g) * D + 4 * q) * 4);
+    const uint32_t pstep = static_cast<uint32_t>(2 * G * D * 4);
+    f32x4 px[MJ];
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) px[j] = ld4_dev(rp, pbase + j * pstep);
+    float M = M_INIT;
+#pragma unroll
+    for (int k = 0; k < MAX_NWG / 64; ++k)
+        if (lane + 64 * k < P) M = fmaxf(M, __uint_as_float(mlr[k][0]));
+    M = wave_max64(M);
+    float den = 0.f;
+#pragma unroll
+    for (int k = 0; k < MAX_NWG / 64; ++k) {
+        const bool ok = lane + 64 * k < P;
+        const float w = ok ? fast_exp2(__uint_as_float(mlr[k][0]) - M) : 0.f;
+        den += ok ? w * __uint_as_float(mlr[k][1]) : 0.f;
+        wt[lane + 64 * k] = w;
+    }
+    den = wave_sum64(den);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    static_assert(2 * MJ <= MAX_NWG, "a batch lies inside the weight table");
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) acc += wt[2 * j + h] * px[j];
+    const int npr = (P + 1) / 2;                          // partial pairs
+    for (int j0 = MJ; j0 < npr; j0 += MJ) {              // more than MJ pairs: one round trip per batch
+#pragma unroll
+        for (int j = 0; j < MJ; ++j) px[j] = ld4_dev(rp, pbase + (j0 + j) * pstep);
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+            if (2 * (j0 + j) + h < P) acc += wt[2 * (j0 + j) + h] * px[j];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i]), false, false);
+        acc[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    if (h == 0) store_out(a, head, g, q, acc, den);
+}
+
+// MJ: items loaded per thread per batch (even; the host picks the smallest
+// instance that covers a thread's items, merge_batch)
+template <int MJ>
+__device__ __forceinline__ void merge_head_cols(const MergeArgs& a, int head, float* lds) {
+    static_assert(MJ % 2 == 0, "items come in (even, odd) pairs");
+    const int G = a.G, P = a.nwg;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int npair = P * G;
+    const Rsrc rp = make_rsrc(a.part + static_cast<int64_t>(head) * npair * D, static_cast<uint32_t>(npair) * D * 4);
+    const Rsrc rm = make_rsrc(a.ml + static_cast<int64_t>(head) * npair * 2, static_cast<uint32_t>(npair) * 8);
+    const int NC = G * (D / 4);
+    const bool two = NC > THREADS;                       // G > 8
+    const int TPC = two ? 1 : THREADS / NC;
+    const int s = two ? 0 : t / NC;                      // partial subset (s >= TPC: idle thread)
+    const int col0 = two ? t : t - s * NC;
+    // item e = 2k + b: partial pb[b] + pstep * k, column col[b]
+    const int pstep = two ? 1 : 2 * TPC;
+    int pb[2], vb[2], wb[2];
+    bool ok[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        pb[b] = two ? 0 : s + TPC * b;
+        const int col = two ? col0 + THREADS * b : col0;
+        ok[b] = col < NC && s < TPC;
+        vb[b] = (pb[b] * G * D + 4 * col) * 4;           // byte offset in the head's partials
+        wb[b] = (pb[b] * G + (col >> 5)) * 2;            // LDS index of the weight
+    }
+    const int vstep = pstep * G * D * 4, wstep = pstep * G * 2;
+    auto voff = [&](int e) -> uint32_t {
+        const int b = e & 1, k = e >> 1;
+        return ok[b] && pb[b] + pstep * k < P ? static_cast<uint32_t>(vb[b] + k * vstep) : OUT_OF_RANGE;
+    };
+    auto widx = [&](int e) -> int {
+        const int b = e & 1, k = e >> 1;
+        return ok[b] && pb[b] + pstep * k < P ? wb[b] + k * wstep : ZERO_SLOT;
+    };
+    // 1. (m, l) table, then the first batch of items
+    static_assert(2 * MAX_PARTIALS <= 2 * 4 * THREADS, "two float4 (m, l) loads per thread cover the table");
+    f32x4 mlv[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) mlv[k] = ld4_dev(rm, static_cast<uint32_t>((t + THREADS * k) * 16));
+    f32x4 px[MJ];
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) px[j] = ld4_dev(rp, voff(j));
+    // 2. weights
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int u = t + THREADS * k;                   // float4 unit: pairs 2u, 2u + 1
+        if (4 * u < 2 * npair) *reinterpret_cast<f32x4*>(lds + 4 * u) = mlv[k];
+    }
+    if (t == 0) lds[ZERO_SLOT] = 0.f;
+    __syncthreads();
     for (int g = wave; g < G; g += WAVES) {
-        const uint32_t pbase = static_cast<uint32_t>(((h * G + g) * D + 4 * q) * 4);
-        const uint32_t pstep = static_cast<uint32_t>(2 * G * D * 4);
-        f32x4 px[MJ];
-        // unconditional: partials past nwg fail the range check and read as zeros
-#pragma unroll
-        for (int j = 0; j < MJ; ++j) px[j] = ld4_dev(rp, pbase + j * pstep);
-        u32x2 mlr[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            if (64 * k < nwg) mlr[k] = ld2_dev(rm, static_cast<uint32_t>(((lane + 64 * k) * G + g) * 8));
         float M = M_INIT;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            if (64 * k < nwg && lane + 64 * k < nwg) M = fmaxf(M, __uint_as_float(mlr[k][0]));
+        for (int p = lane; p < P; p += 64) M = fmaxf(M, lds[(p * G + g) * 2]);
         M = wave_max64(M);
         float den = 0.f;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if (64 * k < nwg) {
-                const bool ok = lane + 64 * k < nwg;
-                const float w = ok ? fast_exp2(__uint_as_float(mlr[k][0]) - M) : 0.f;
-                den += ok ? w * __uint_as_float(mlr[k][1]) : 0.f;
-                wt[lane + 64 * k] = w;
-            }
+        for (int p = lane; p < P; p += 64) {
+            const float w = fast_exp2(lds[(p * G + g) * 2] - M);
+            den += w * lds[(p * G + g) * 2 + 1];
+            lds[(p * G + g) * 2] = w;
         }
         den = wave_sum64(den);
-        wave_sync_lds();
-        const int nj = (nwg + 1 - h) / 2;            // partials of this half
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        // table entries [nwg, 64) hold zero weights and their partials read as
-        // zeros, so the first batch needs no bounds: its 2 MJ table reads issue
-        // back to back instead of one per branch
-        static_assert(2 * MJ <= 64, "first merge batch must lie in the zero-filled table head");
-#pragma unroll
-        for (int j = 0; j < MJ; ++j) acc += wt[2 * j + h] * px[j];
-        for (int j0 = MJ; j0 < npr; j0 += MJ) {      // nwg > 2 * MJ: one more round trip per batch
-#pragma unroll
-            for (int j = 0; j < MJ; ++j)
-                if (j0 + j < npr) px[j] = ld4_dev(rp, pbase + (j0 + j) * pstep);
-#pragma unroll
-            for (int j = 0; j < MJ; ++j)
-                if (j0 + j < nj) acc += wt[2 * (j0 + j) + h] * px[j];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i]), false, false);
-            acc[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-        }
-        if (h == 0) {
-            float r[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) r[i] = den > 0.f ? acc[i] / den : 0.f;
-            // out.to(q.dtype) of the fp32 result: one rounding to bf16 or fp16
-            const u32x2 o = a.out16 ? u32x2{static_cast<uint32_t>(f32_to_f16_bits(r[0])) |
-                                                (static_cast<uint32_t>(f32_to_f16_bits(r[1])) << 16),
-                                            static_cast<uint32_t>(f32_to_f16_bits(r[2])) |
-                                                (static_cast<uint32_t>(f32_to_f16_bits(r[3])) << 16)}
-                                    : u32x2{static_cast<uint32_t>(f32_to_bf16_rne(r[0])) |
-                                                (static_cast<uint32_t>(f32_to_bf16_rne(r[1])) << 16),
-                                            static_cast<uint32_t>(f32_to_bf16_rne(r[2])) |
-                                                (static_cast<uint32_t>(f32_to_bf16_rne(r[3])) << 16)};
-            *reinterpret_cast<u32x2*>(a.out + static_cast<int64_t>(head * G + g) * a.out_stride + 4 * q) = o;
-        }
-        wave_sync_lds();                             // the table is rewritten for the next g
+        if (lane == 0) lds[ML_LDS + g] = den;
     }
+    __syncthreads();
+    // 3. weighted sums in item order
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) acc[j & 1] += lds[widx(j)] * px[j];
+    const int nitems = s < TPC ? (two ? 2 * P : (P - s + TPC - 1) / TPC) : 0;
+    for (int j0 = MJ; j0 < nitems; j0 += MJ) {           // a thread with more than MJ items
+#pragma unroll
+        for (int j = 0; j < MJ; ++j) px[j] = ld4_dev(rp, voff(j0 + j));
+#pragma unroll
+        for (int j = 0; j < MJ; ++j) acc[j & 1] += lds[widx(j0 + j)] * px[j];
+    }
+    if (!two) acc[0] += acc[1];
+    f32x4* comb = reinterpret_cast<f32x4*>(lds + COMB_LDS);
+    if (TPC > 1) {
+        if (s >= 1 && s < TPC) comb[t] = acc[0];
+        __syncthreads();
+        if (s == 0)
+            for (int k = 1; k < TPC; ++k) acc[0] += comb[t + k * NC];
+    }
+    if (s == 0) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int col = col0 + THREADS * b;
+            if ((b == 0 || two) && col < NC) {
+                store_out(a, head, col >> 5, col & 31, acc[b], lds[ML_LDS + (col >> 5)]);
+            }
+        }
+    }
+}
+
+// Largest number of items one merging thread loads (the host's choice of
+// the MJ instance).
+constexpr int merge_items(int G, int nwg) {
+    return 32 * G > THREADS ? 2 * nwg : (nwg + THREADS / (32 * G) - 1) / (THREADS / (32 * G));
 }
 
 // ---------------------------------------------------------------------------
@@ -656,13 +779,14 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
     const int su0 = a.segu[0], su1 = a.segu[1];
     const float qk_scale = a.qk_scale;
     const int io = a.io;
+    const int mj = a.mj;
     const MergeArgs ma{a.G, a.nwg, a.part, a.ml, a.out, a.out_stride, io & HYQ_DT_OUT_FP16};
     uint32_t* const cnt = a.cnt;
     asm volatile("" ::"s"(u0), "s"(u1), "s"(nqg), "s"(nquant), "s"(len_q), "s"(len_s0), "s"(kp), "s"(vp),
                  "s"(ksp), "s"(vsp), "s"(kp_bh), "s"(vp_bh), "s"(ks_bh), "s"(vs_bh));
     asm volatile("" ::"s"(sk0), "s"(sk1), "s"(sk2), "s"(sv0), "s"(sv1), "s"(sv2), "s"(skb0), "s"(skb1), "s"(skb2),
                  "s"(svb0), "s"(svb1), "s"(svb2), "s"(sn0), "s"(sn1), "s"(sn2), "s"(su0), "s"(su1), "s"(qk_scale));
-    asm volatile("" ::"s"(ma.nwg), "s"(ma.part), "s"(ma.ml), "s"(ma.out), "s"(ma.out_stride), "s"(cnt));
+    asm volatile("" ::"s"(ma.nwg), "s"(ma.part), "s"(ma.ml), "s"(ma.out), "s"(ma.out_stride), "s"(cnt), "s"(mj));
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, kb = lane >> 4;
@@ -871,7 +995,17 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
     __syncthreads();
     if (s_last) {
         if (threadIdx.x == 0) __hip_atomic_store(cnt + head * CNT_PAD, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        merge_head(ma, head, s_acc);
+        switch (mj) {      // G <= 4: merge_head_waves, pairs per lane; G > 4: merge_head_cols, items per thread
+            case 4: merge_head_waves<4>(ma, head, s_acc); break;
+            case 8: merge_head_waves<8>(ma, head, s_acc); break;
+            case 12: merge_head_waves<12>(ma, head, s_acc); break;
+            case 16: merge_head_waves<16>(ma, head, s_acc); break;
+            case 20: merge_head_waves<20>(ma, head, s_acc); break;
+            case 24: merge_head_waves<24>(ma, head, s_acc); break;
+            case 108: merge_head_cols<8>(ma, head, s_acc); break;
+            case 116: merge_head_cols<16>(ma, head, s_acc); break;
+            default: merge_head_cols<24>(ma, head, s_acc); break;
+        }
     }
 }
 
@@ -973,7 +1107,24 @@ Plan make_plan(int64_t n_quant, const int64_t seg_n[3], int bh_kv, int G, int re
 }
 
 size_t lds_bytes(int G) {
-    return std::max(static_cast<size_t>(WAVES) * G * (D + 1), static_cast<size_t>(WAVES) * MAX_NWG) * sizeof(float);
+    return std::max(static_cast<size_t>(WAVES) * G * (D + 1), static_cast<size_t>(MERGE_LDS)) * sizeof(float);
+}
+
+// The merge instance: for G <= 4 merge_head_waves with the smallest batch
+// covering a lane's partial pairs (else batches of 24); for G > 4
+// merge_head_cols (100 + batch) with the smallest batch covering a thread's
+// items (else batches of 24).
+int merge_batch(int G, int nwg) {
+    if (G <= WAVES) {
+        const int pairs = (nwg + 1) / 2;
+        for (int mj : {4, 8, 12, 16, 20})
+            if (pairs <= mj) return mj;
+        return 24;
+    }
+    const int items = merge_items(G, nwg);
+    for (int mj : {8, 16})
+        if (items <= mj) return 100 + mj;
+    return 124;
 }
 
 // Workgroups of one decode_kernel instance the device holds at once, cached
@@ -1120,6 +1271,7 @@ int launch_decode(const hyq_decode_params* p, const Plan& pl, const Layout& L, v
     a.bh_kv = p->bh_kv;
     a.qk_scale = p->sm_scale * LOG2E;
     a.nqg = pl.nqg; a.nwg = pl.nwg;
+    a.mj = merge_batch(p->kv_repeat, pl.nwg);
     for (int i = 0; i <= pl.nwg; ++i) a.bnd[i] = pl.bnd[i];
     char* ws = static_cast<char*>(workspace);
     a.cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);

@@ -36,19 +36,26 @@
 // device-scope loads.
 //
 // Per wavefront, lane l = 16*kb + c (c = l & 15, kb = l >> 4):
-//   QK  S^T[token][g] = K_tile . Q^T with v_mfma_f32_16x16x32_{f16,bf16}:
-//       A = 16 tokens x 32 channels (lane = token c, 8 channels), B = Q^T
-//       (lane = head c).  Output lane (g=c, r=kb) holds tokens 4r..4r+3.
 //   PV  O^T[channel][g] = V^T . P'^T with v_mfma_f32_16x16x32_bf16:
-//       A = 16 channels x 32 token slots, B = P'^T; the 32-token group is
-//       permuted so that slot e of lane-row kb is token
-//       tau(kb,e) = e<4 ? 4kb+e : 16+4kb+(e-4), exactly the tokens whose
-//       scores the QK output left in that lane: no cross-lane shuffle of P.
+//       A = 16 channels x 32 token slots, B = P'^T.  Slot e of lane-row kb
+//       is token 4e + kb of the 32-token group, so V load e of the wavefront
+//       reads four consecutive packed rows 4e..4e+3 (whole 128-byte lines).
+//   QK  S^T[token][g] = K_tile . Q^T with v_mfma_f32_16x16x32_{f16,bf16}:
+//       A = 16 tokens x 32 channels, B = Q^T (lane = head c).  Row i of tile
+//       t is token 16t + 4(i & 3) + (i >> 2), so output lane (g = c, kb),
+//       which holds rows 4kb..4kb+3, holds tokens 16t + 4i + kb: exactly the
+//       P' slots 4t + i of its lane-row.  No cross-lane shuffle of P.
 //   Channel 8*j+nb of V sits in row j of PV MFMA nb (lane j loads the dword /
 //   16 bytes holding channels 8j..8j+7).  bf16 tiles use the K=16 form
 //   (v_mfma_f32_16x16x16_bf16) whose slot e of lane-row kb is token 4kb+e.
-//   The four lanes of a quad load the K and V scales of tokens 4kb..4kb+3 of a
+//   Lane i of a quad loads the K and V scales of token 16t + 4i + kb of a
 //   tile and quad-broadcast DPP moves hand every lane all four.
+//   The quantised prefix's packed-row loads are non-temporal: with every
+//   row load instruction covering whole 128-byte lines this raised a
+//   loads-only copy of the schedule from 75% to 82% of HBM peak, and the
+//   kernel at B=16, 32K from 66% to 81%.  Loads that read a line in pieces
+//   from several instructions (the scales, the bf16 tiles' K rows) were
+//   slower non-temporal and keep the default policy.
 // int4 -> MFMA operand conversion is done in registers without any lookup:
 //   K: u = nibble ^ 8 placed in the mantissa of an fp16 subnormal (value
 //      u * 2^-24, one shift and one bitop3 per pair of codes); Q is fed as
@@ -174,7 +181,9 @@ __device__ __forceinline__ float col_sum(float v) {
 }
 
 // token slot e of lane-row kb within a 32-token group
-__device__ __forceinline__ constexpr int tau(int kb, int e) { return e < 4 ? 4 * kb + e : 16 + 4 * kb + (e - 4); }
+__device__ __forceinline__ constexpr int slot_token(int kb, int e) { return 4 * e + kb; }
+// token of row i of a 16-token QK tile (relative to the tile)
+__device__ __forceinline__ constexpr int krow_token(int i) { return 4 * (i & 3) + (i >> 2); }
 
 // Online-softmax update with this lane's N log2-domain scores; on return s
 // holds p = exp2(s - m) relative to the (possibly raised) running max.
@@ -217,18 +226,24 @@ __device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, RSRC_W3);
 }
 // voff: per-lane byte offset (constant across a loop), soff: wave-uniform
-// byte offset (the loop position, kept in an SGPR)
+// byte offset (the loop position, kept in an SGPR); POL: cache policy bits
+// (NT: non-temporal, for data read once)
+constexpr int NT = 2;
+template <int POL = 0>
 __device__ __forceinline__ u32x4 bld128(Rsrc r, uint32_t voff, uint32_t soff = 0) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POL));
 }
+template <int POL = 0>
 __device__ __forceinline__ uint32_t bld32(Rsrc r, uint32_t voff, uint32_t soff = 0) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, POL);
 }
+template <int POL = 0>
 __device__ __forceinline__ u32x2 bld64(Rsrc r, uint32_t voff, uint32_t soff = 0) {
-    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, POL));
 }
+template <int POL = 0>
 __device__ __forceinline__ uint32_t bld16(Rsrc r, uint32_t voff, uint32_t soff = 0) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, POL);
 }
 
 template <int CTRL>
@@ -238,10 +253,10 @@ __device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
 
 // Quantised prefix with KB-bit K codes and VB-bit V codes (2, 4 or 8; packed
 // rows of 16*bits bytes, src/ops/decode_d_stage.py:104-133).  Per lane:
-//   k[t][*]  tile t: token 16t + c, channels 32kb..32kb+31 (KB dwords)
-//   v[e][*]  slot e: token tau(kb, e), channels 8c..8c+7 (VB bytes; 2-byte
-//            loads are zero-extended)
-//   sk, sv   tile t: fp16 scale bits of token 16t + 4kb + (c & 3)
+//   k[t][*]  tile t: token 16t + krow_token(c), channels 32kb..32kb+31 (KB dwords)
+//   v[e][*]  slot e: token slot_token(kb, e) = 4e + kb, channels 8c..8c+7 (VB
+//            bytes; 2-byte loads are zero-extended)
+//   sk, sv   tile t: fp16 scale bits of token 16t + 4(c & 3) + kb
 template <int KB, int VB>
 struct QRaw {
     uint32_t k[2][KB];
@@ -254,9 +269,9 @@ constexpr int BROW = D;                   // bf16 row stride in elements
 
 struct QCtx {
     Rsrc k, v, ks, vs;     // this chunk's packed K / V rows and scales
-    uint32_t klane;        // lane offset of tile 0: c * prow(KB) + 4 KB kb
-    uint32_t vlane;        // lane offset of slot 0: 4kb * prow(VB) + VB c
-    uint32_t slane;        // lane offset of the scale of tile 0: (4kb + (c & 3)) * 2
+    uint32_t klane;        // lane offset of tile 0: krow_token(c) * prow(KB) + 4 KB kb
+    uint32_t vlane;        // lane offset of slot 0: kb * prow(VB) + VB c
+    uint32_t slane;        // lane offset of the scale of tile 0: (4 (c & 3) + kb) * 2
 };
 
 // t0 is wave-uniform: it only enters the scalar offsets
@@ -269,28 +284,30 @@ __device__ __forceinline__ void qload(QRaw<KB, VB>& r, const QCtx& x, int t0) {
     for (int t = 0; t < 2; ++t) {
         const uint32_t ko = x.klane + t * 16 * prow(KB);
         if constexpr (KB == 2) {
-            const u32x2 w = bld64(x.k, ko, sok);
+            const u32x2 w = bld64<NT>(x.k, ko, sok);
             r.k[t][0] = w[0]; r.k[t][1] = w[1];
         } else {
 #pragma unroll
             for (int h = 0; h < KB / 4; ++h) {
-                const u32x4 w = bld128(x.k, ko + 16 * h, sok);
+                const u32x4 w = bld128<NT>(x.k, ko + 16 * h, sok);
                 r.k[t][4 * h] = w[0]; r.k[t][4 * h + 1] = w[1]; r.k[t][4 * h + 2] = w[2]; r.k[t][4 * h + 3] = w[3];
             }
         }
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const uint32_t vo = x.vlane + tau(0, e) * prow(VB);
+        const uint32_t vo = x.vlane + slot_token(0, e) * prow(VB);
         if constexpr (VB == 2) {
-            r.v[e][0] = bld16(x.v, vo, sov);
+            r.v[e][0] = bld16<NT>(x.v, vo, sov);
         } else if constexpr (VB == 4) {
-            r.v[e][0] = bld32(x.v, vo, sov);
+            r.v[e][0] = bld32<NT>(x.v, vo, sov);
         } else {
-            const u32x2 w = bld64(x.v, vo, sov);
+            const u32x2 w = bld64<NT>(x.v, vo, sov);
             r.v[e][0] = w[0]; r.v[e][1] = w[1];
         }
     }
+    // scales: a 128-byte line of them is read by several instructions, so
+    // they keep the default cache policy
     r.sk[0] = bld16(x.ks, x.slane, ss);
     r.sk[1] = bld16(x.ks, x.slane + 32, ss);
     r.sv[0] = bld16(x.vs, x.slane, ss);
@@ -362,9 +379,9 @@ template <int KB, int VB>
 __device__ __forceinline__ void qcompute(WaveState& st, const QRaw<KB, VB>& r, const f16x8 (&qop)[4],
                                          const f32x4& kbias, int nv, int lane, float qk) {
     const int kb = lane >> 4;
-    // each lane converts the scales of its own token of each tile (the
-    // quad's four lanes hold tokens 4kb..4kb+3 of a tile); the scores and P'
-    // take them with quad broadcasts
+    // each lane converts the scales of its own token of each tile (lane i of
+    // a quad holds token 16t + 4i + kb, the token of score slot 4t + i); the
+    // scores and P' take them with quad broadcasts
     const float skq[2] = {f16_bits_to_f32(static_cast<uint16_t>(r.sk[0])) * qk,
                           f16_bits_to_f32(static_cast<uint16_t>(r.sk[1])) * qk};
     const float svo[2] = {f16_bits_to_f32(static_cast<uint16_t>(r.sv[0])),
@@ -384,10 +401,10 @@ __device__ __forceinline__ void qcompute(WaveState& st, const QRaw<KB, VB>& r, c
     if (nv < GROUP) {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-            if (tau(kb, e) >= nv) s[e] = -INFINITY;
+            if (slot_token(kb, e) >= nv) s[e] = -INFINITY;
     }
     softmax_step<8>(st, s, true);
-    // P' = bf16(p * s_v): B operand of the PV MFMAs (slot e = token tau(kb, e))
+    // P' = bf16(p * s_v): B operand of the PV MFMAs (slot e = token slot_token(kb, e))
     const u32x4 pw = {pack_bf16x2(s[0] * quad_bcast<0>(svo[0]), s[1] * quad_bcast<1>(svo[0])),
                       pack_bf16x2(s[2] * quad_bcast<2>(svo[0]), s[3] * quad_bcast<3>(svo[0])),
                       pack_bf16x2(s[4] * quad_bcast<0>(svo[1]), s[5] * quad_bcast<1>(svo[1])),
@@ -833,9 +850,9 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
                         static_cast<uint32_t>(ntok) * prow(VB));
         x.ks = make_rsrc(ksp + static_cast<int64_t>(head) * ks_bh + lo, static_cast<uint32_t>(ntok) * 2);
         x.vs = make_rsrc(vsp + static_cast<int64_t>(head) * vs_bh + lo, static_cast<uint32_t>(ntok) * 2);
-        x.klane = static_cast<uint32_t>(c * prow(KB) + 4 * KB * kb);
-        x.vlane = static_cast<uint32_t>(4 * kb * prow(VB) + VB * c);
-        x.slane = static_cast<uint32_t>((4 * kb + (c & 3)) * 2);
+        x.klane = static_cast<uint32_t>(krow_token(c) * prow(KB) + 4 * KB * kb);
+        x.vlane = static_cast<uint32_t>(kb * prow(VB) + VB * c);
+        x.slane = static_cast<uint32_t>((4 * (c & 3) + kb) * 2);
         // groups wave, wave+WAVES, ... of the piece through a three-deep
         // register ring: two groups' loads in flight while one is computed
         constexpr int STRIDE = WAVES * GROUP;

@@ -50,12 +50,13 @@
 //   (v_mfma_f32_16x16x16_bf16) whose slot e of lane-row kb is token 4kb+e.
 //   Lane i of a quad loads the K and V scales of token 16t + 4i + kb of a
 //   tile and quad-broadcast DPP moves hand every lane all four.
-//   The quantised prefix's packed-row loads are non-temporal: with every
-//   row load instruction covering whole 128-byte lines this raised a
-//   loads-only copy of the schedule from 75% to 82% of HBM peak, and the
-//   kernel at B=16, 32K from 66% to 81%.  Loads that read a line in pieces
-//   from several instructions (the scales, the bf16 tiles' K rows) were
-//   slower non-temporal and keep the default policy.
+//   Loads whose instructions cover whole 128-byte lines are non-temporal:
+//   the quantised prefix's packed rows and the bf16 tiles' V rows.  This
+//   raised a loads-only copy of the prefix schedule from 75% to 82% of HBM
+//   peak, the kernel at B=16, 32K from 66% to 81% and the bf16-only
+//   comparator from 72% to 80%.  Loads that read a line in pieces from
+//   several instructions (the scales, the bf16 tiles' K rows) were slower
+//   non-temporal and keep the default policy.
 // int4 -> MFMA operand conversion is done in registers without any lookup:
 //   K: u = nibble ^ 8 placed in the mantissa of an fp16 subnormal (value
 //      u * 2^-24, one shift and one bitop3 per pair of codes); Q is fed as
@@ -489,7 +490,7 @@ __device__ __forceinline__ void bf16_load(Bf16Raw& r, Rsrc rk, Rsrc rv, int t0, 
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.k[i] = bld128(rk, ko + 16 * i, so);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r.v[e] = bld128(rv, vo + e * (BROW * 2), so);
+    for (int e = 0; e < 4; ++e) r.v[e] = bld128<NT>(rv, vo + e * (BROW * 2), so);
 }
 
 __device__ __forceinline__ void bf16_compute(WaveState& st, const Bf16Raw& r, const bf16x8 (&qop)[4], int nv,

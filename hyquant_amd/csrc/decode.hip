@@ -1031,6 +1031,10 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
 // host side
 // ---------------------------------------------------------------------------
 
+struct Slots {
+    int slots, cus;        // workgroups resident at once, compute units (0: unknown)
+};
+
 struct Plan {
     int nwg;               // pieces per head
     int nqg, segu[3];      // schedule units: int4 groups, bf16 units per segment
@@ -1045,10 +1049,13 @@ size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 // short segment pieces fill the end of the grid.
 //   requested > 0: pieces of about that many int4 tokens' bytes.
 //   few KV heads (bh_kv < 32, a step of a few microseconds, bound by the
-//     per-piece round trips): int4 pieces of the smallest power-of-two
-//     token count >= 128 that gives at most 32 pieces (2048 at most), bf16
-//     pieces of 128 tokens (without a prefix, like the prefix: a power of
-//     two from 128 to 512).
+//     per-piece round trips), G <= 4: every segment cut into pieces of
+//     equal bytes, total / (0.8 CUs) (measured best at B=1 from 2K to 32K
+//     prefixes), at most 48 per head.
+//   few KV heads, G > 4 (each partial is G rows, so the merge weighs more):
+//     int4 pieces of the smallest power-of-two token count >= 128 that gives
+//     at most 32 pieces (2048 at most), bf16 pieces of 128 tokens (without
+//     a prefix, like the prefix: a power of two from 128 to 512).
 //   many KV heads: pieces of about total / (1.25 * slots) bytes, `slots`
 //     being the workgroups the device holds at once: the first round fills
 //     every slot and the remaining quarter, with the short segment pieces,
@@ -1057,7 +1064,8 @@ size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 // Each segment gets its bytes / target pieces (rounded, at least one); the
 // target grows until the pieces fit the merge tables.
 Plan make_plan(int64_t n_quant, const int64_t seg_n[3], int bh_kv, int G, int requested, int kb, int vb,
-               int slots) {
+               Slots sl_) {
+    const int slots = sl_.slots;
     Plan p{};
     p.nqg = static_cast<int>((n_quant + GROUP - 1) / GROUP);
     for (int s = 0; s < 3; ++s) p.segu[s] = static_cast<int>((seg_n[s] + BUNIT - 1) / BUNIT);
@@ -1089,6 +1097,15 @@ Plan make_plan(int64_t n_quant, const int64_t seg_n[3], int bh_kv, int G, int re
     int64_t target;
     if (requested > 0) {
         target = std::max<int64_t>(1, (requested + GROUP - 1) / GROUP) * cq;
+        total = counts_for(target);
+    } else if (bh_kv < 32 && G <= WAVES) {
+        // few heads, G <= 4: pieces of equal bytes, about 0.8 per CU (a
+        // workgroup per CU streams faster than two sharing one, and the
+        // merge grows with the piece count), at least 8 KiB and at most 48
+        // per head
+        const int64_t cus = sl_.cus > 0 ? sl_.cus : 256;
+        target = std::max<int64_t>(8 << 10, head_bytes * bh_kv * 5 / (4 * cus));
+        target = std::max<int64_t>(target, (head_bytes + 47) / 48);
         total = counts_for(target);
     } else if (bh_kv < 32) {
         int64_t split = 4 * GROUP, bsplit = 128;
@@ -1145,25 +1162,26 @@ int merge_batch(int G, int nwg) {
     return 124;
 }
 
-// Workgroups of one decode_kernel instance the device holds at once, cached
-// per device and GQA width (the LDS size).
+// Workgroups of one decode_kernel instance the device holds at once (and
+// the device's CU count), cached per device and GQA width (the LDS size).
 template <int KB, int VB>
-int resident_slots_of(int G) {
-    static std::atomic<int> cache[64][17];
+Slots resident_slots_of(int G) {
+    static std::atomic<int> cache[64][17][2];
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || G < 1 || G > 16) return 0;
-    const int known = cache[dev][G].load(std::memory_order_relaxed);
-    if (known > 0) return known;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || G < 1 || G > 16) return {0, 0};
+    const int known = cache[dev][G][0].load(std::memory_order_relaxed);
+    if (known > 0) return {known, cache[dev][G][1].load(std::memory_order_relaxed)};
     int per_cu = 0, cus = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&decode_kernel<KB, VB>),
                                                      THREADS, lds_bytes(G)) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return 0;
-    cache[dev][G].store(per_cu * cus, std::memory_order_relaxed);
-    return per_cu * cus;
+        return {0, 0};
+    cache[dev][G][1].store(cus, std::memory_order_relaxed);
+    cache[dev][G][0].store(per_cu * cus, std::memory_order_relaxed);
+    return {per_cu * cus, cus};
 }
 
-int resident_slots(int kb, int vb, int G) {
+Slots resident_slots(int kb, int vb, int G) {
     switch (10 * kb + vb) {
         case 44: return resident_slots_of<4, 4>(G);
         case 42: return resident_slots_of<4, 2>(G);

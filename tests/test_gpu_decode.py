@@ -179,6 +179,57 @@ def test_decode_workspace_reuse_interleaved():
     assert torch.equal(outs[0], outs[3]) and torch.equal(outs[1], outs[5]) and torch.equal(outs[2], outs[4])
 
 
+
+def test_decode_graph_replay_interleaved():
+    """The same interleaved calls captured in one HIP graph: every replay
+    (with eager decode calls on the same workspace between replays) must give
+    outputs bit-identical to the eager calls, so the arrival counters are
+    back at zero after every launch and no launch reads another's partials."""
+    import hyquant_amd as hq
+    dev = torch.device("cuda")
+    cfgs = {
+        "A": dict(B=1, HQ=32, HKV=8, N=8192, S=64, seed=17),
+        "B": dict(B=2, HQ=64, HKV=8, N=2048, S=64, seed=18),    # G = 8: column merge
+        "C": dict(B=8, HQ=32, HKV=8, N=4096, S=64, seed=19),    # 64 KV heads
+        "D": dict(B=1, HQ=32, HKV=2, N=4096, S=37, seed=20),    # G = 16
+    }
+    data = {}
+    for name, cfg in cfgs.items():
+        inp = O.make_decode_inputs(W=128, **cfg)
+        st = O.build_decode_state(inp)
+        data[name] = (state_to_device(st, dev), to_dev_bf16(inp.q_dec, dev), cfg["HQ"] // cfg["HKV"])
+
+    def call(name, **kw):
+        t, q, G = data[name]
+        return hq.fused_d_stage_decode(q, t["k_packed"], t["v_packed"], t["k_scale"], t["v_scale"],
+                                       t["k_topk"], t["v_topk"], t["k_staging"], t["v_staging"],
+                                       t["k_window"], t["v_window"], 4, 4, kv_repeat=G, **kw)
+
+    order = [("A", {}), ("B", {}), ("C", {}), ("D", {}), ("A", {"split_tokens": 128}), ("C", {}), ("B", {})]
+    eager = [call(n, **kw) for n, kw in order]        # also sizes the cached workspace before capture
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for n, kw in order:                            # warm-up on the capture stream (its own workspace)
+            call(n, **kw)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        outs = [call(n, **kw) for n, kw in order]
+    for rep in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        for i, ((n, _), o) in enumerate(zip(order, outs)):
+            assert torch.equal(o, eager[i]), f"replay {rep}, call {i} ({n}) differs from the eager call"
+        # eager calls between replays (on the capture stream's workspace as well)
+        with torch.cuda.stream(s):
+            mid = call("D")
+        torch.cuda.synchronize()
+        assert torch.equal(mid, eager[3])
+
+
 BIT_PAIRS = [(4, 4), (4, 2), (2, 4), (8, 8), (2, 2), (4, 8), (8, 4), (2, 8), (8, 2)]
 
 

@@ -542,10 +542,21 @@ __device__ __forceinline__ void quant_row_group(uint4 raw, int8_t* dst, uint16_t
     const float s32 = amax / static_cast<float>(QMAX);
     const _Float16 s16 = static_cast<_Float16>(s32);
     const float sf = static_cast<float>(s16);
+    // x / sf: the fma form for every finite scale, the IEEE division when the
+    // scale overflowed fp16 (sf = inf, where the residual would be inf * 0)
+    float q[8];
+    if (sf <= 65504.0f) {
+        const float inv = 1.0f / sf;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = quot_rn(v[i], sf, inv);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = v[i] / sf;
+    }
     int c[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        float r = rintf(v[i] / sf);
+        float r = rintf(q[i]);
         r = fminf(fmaxf(r, static_cast<float>(QMIN)), static_cast<float>(QMAX));
         c[i] = static_cast<int>(r);
     }

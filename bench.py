@@ -251,6 +251,33 @@ def time_calls(fn, warmup=2, iters=5):
     return e0.elapsed_time(e1) / iters
 
 
+def time_graph(fn, iters=50, replays=REPLAYS):
+    """ms per call of fn: iters calls captured in one HIP graph, the median of
+    `replays` replays bracketed by HIP events (no host launch cost inside the
+    timed region, for calls shorter than a launch)."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(iters):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    per = []
+    for _ in range(replays):
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) / iters)
+    per.sort()
+    del g
+    return per[len(per) // 2]
+
+
 def exact_attention_fp32(q, k, v, chunk=1024):
     """Causal softmax(q k^T / sqrt(D)) v in float32 on the GPU, chunked over
     queries, GQA by head index (the reference for the prefill error figures;
@@ -355,7 +382,8 @@ def bench_boundary(dev):
     """Config 3 boundary ops at B=32, prefix 16384 (Llama shape 32q/8kv):
     the prefill-time vertical-line selector (W=256, rho=5%), the freeze
     (freeze-time selector + reorganisation into the four segments) and a staging
-    flush (128 bf16 tokens of every KV head quantised to int4)."""
+    flush (128 bf16 tokens of every KV head quantised to int4; timed as 50
+    calls in a HIP graph, since one call is shorter than a host launch)."""
     from hyquant_amd.decode_d_stage import quantize_into
     from hyquant_amd.d_stage_kv_cache import DStageLayerCache
     from hyquant_amd.vertical import compute_vertical_indices
@@ -386,7 +414,7 @@ def bench_boundary(dev):
     x = torch.randn(B * HKV, 128, D, generator=g, device=dev).to(torch.bfloat16)
     packed = torch.empty(B * HKV, 128, D // 2, dtype=torch.int8, device=dev)
     scale = torch.empty(B * HKV, 128, dtype=torch.float16, device=dev)
-    ms = time_calls(lambda: quantize_into(x, 4, packed, scale), warmup=5, iters=50)
+    ms = time_graph(lambda: quantize_into(x, 4, packed, scale), iters=50)
     by = B * HKV * 128 * (D * 2 + D // 2 + 2)
     out["flush"] = {"us": round(ms * 1e3, 2), "gbs": round(by / (ms * 1e-3) / 1e9, 1), "algorithmic_bytes": by}
     print(f"# boundary {out}", file=sys.stderr, flush=True)

@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 #include <string>
 
@@ -20,6 +21,19 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
     return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// max over each aligned group of 16 lanes with DPP row operations (quad
+// swaps, then the half-row and row mirrors), no LDS permute
+__device__ __forceinline__ float max16_dpp(float v) {
+    auto dpp = [](float x, auto ctrl) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+    };
+    v = fmaxf(v, dpp(v, std::integral_constant<int, 0xb1>{}));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp(v, std::integral_constant<int, 0x4e>{}));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp(v, std::integral_constant<int, 0x141>{}));   // row_half_mirror
+    v = fmaxf(v, dpp(v, std::integral_constant<int, 0x140>{}));   // row_mirror
+    return v;
 }
 
 // The correctly rounded fp32 quotient v / sf of a quantiser (finite sf > 0,

@@ -51,7 +51,11 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    for (int m = 1; m < lpt; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    if (lpt == 16) {
+        amax = max16_dpp(amax);
+    } else {
+        for (int m = 1; m < lpt; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    }
     amax = fmaxf(amax, 1e-5f);
     const float s32 = amax / static_cast<float>(QMAX);
     const _Float16 s16 = static_cast<_Float16>(s32);

@@ -536,8 +536,7 @@ __device__ __forceinline__ void quant_row_group(uint4 raw, int8_t* dst, uint16_t
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    amax = max16_dpp(amax);
     amax = fmaxf(amax, 1e-5f);
     const float s32 = amax / static_cast<float>(QMAX);
     const _Float16 s16 = static_cast<_Float16>(s32);

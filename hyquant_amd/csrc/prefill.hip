@@ -54,6 +54,7 @@
 #include <algorithm>
 #include <cmath>
 #include <string>
+#include <utility>
 
 namespace hyq {
 namespace {
@@ -132,6 +133,31 @@ __device__ __forceinline__ u32x2 lds_tr8_i(const uint8_t* p) {
 }
 __device__ __forceinline__ void lds_wait(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>): loop bodies
+// whose index must be a compile-time constant (LDS read offsets are asm
+// immediates)
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+// 16-byte LDS reads in the same style (the K tile of the fp16 P.V loop)
+template <int OFF>
+__device__ __forceinline__ i32x4 lds_rd128(uint32_t addr) {
+    i32x4 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+    return r;
+}
+__device__ __forceinline__ void lds_wait4(i32x4& a, i32x4& b, i32x4& c, i32x4& d) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+__device__ __forceinline__ void lds_wait8(i32x4& a, i32x4& b, i32x4& c, i32x4& d, i32x4& e, i32x4& f, i32x4& g,
+                                          i32x4& h) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f), "+v"(g), "+v"(h));
 }
 
 
@@ -704,7 +730,10 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     amax = wave_max(amax);
     if (lane == 0) s_red[w] = amax;
     __syncthreads();
-    const float q_amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    // uniform over the workgroup: held in a scalar register, so that the score
+    // scale below and every test on it stay scalar (no per-lane branches)
+    const float q_amax = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int,
+        fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3])))));
     float q_scale = q_amax / (QF8 ? FP8_MAX : 127.0f);
     if (QF8 && !(q_scale > 0.0f)) q_scale = 1.0f;
     i32x4 q8[2][2];
@@ -838,24 +867,12 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
 #pragma unroll
         for (int cb = 0; cb < 8; ++cb) acc[sb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    TileDesc cur = describe(0);
-    issue_tile(cur, s_k0, s_v0);
+    TileDesc cur{};                // the next tile (fp8 P.V loop)
     // one tile: its DMAs (into kb / vb) were issued a tile earlier; the next
     // tile's go into knext / vnext
-    auto step = [&](int t, const uint8_t* kb, const uint8_t* vb, uint8_t* knext, uint8_t* vnext)
-                    __attribute__((always_inline)) {
-        // this wavefront's DMAs of tile t have landed; the barrier extends that
-        // to the workgroup and frees the other buffer (read by tile t - 1)
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        const TileDesc d = cur;
-        if (t + 1 < ntiles) {
-            cur = describe(t + 1);
-            issue_tile(cur, knext, vnext);
-        }
-
-        // ---- S^T = K . Q^T --------------------------------------------------
-        float s[2][4][4];
+    // S^T = K . Q^T of tile d from its K buffer kb; returns whether any score
+    // of the tile needs the mask
+    auto qk_tile = [&](const TileDesc& d, const uint8_t* kb, float (&s)[2][4][4]) __attribute__((always_inline)) {
         bool masked;
         if (d.kind == T_REST && QF8) {
 #pragma unroll
@@ -922,7 +939,12 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             else  // window: causal against this wavefront's first row, or past N
                 masked = d.idx0 + BN - 1 > BM * blk + 32 * w || d.idx0 + BN > d.valid;
         }
-        if (masked) {
+        return masked;
+    };
+
+    // -inf for the keys of tile d a row may not see
+    auto mask_tile = [&](const TileDesc& d, float (&s)[2][4][4]) __attribute__((always_inline)) {
+        {
 #pragma unroll
             for (int sb = 0; sb < 2; ++sb) {
                 const int row = BM * blk + 32 * w + 16 * sb + c16;
@@ -932,11 +954,31 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                     for (int r = 0; r < 4; ++r) {
                         const int e = d.idx0 + 16 * kbk + 4 * g + r;
                         const bool causal = d.kind == T_WIN || (d.kind == T_REST && a.rest_causal);
-                        const bool ok = causal ? (e < d.valid && e <= row) : (e < d.valid);
-                        if (!ok) s[sb][kbk][r] = -INFINITY;
+                        // bitwise: one select per score, no per-lane branches
+                        const bool ok = (e < d.valid) & (!causal | (e <= row));
+                        s[sb][kbk][r] = ok ? s[sb][kbk][r] : -INFINITY;
                     }
             }
         }
+
+    };
+
+    auto step = [&](int t, const uint8_t* kb, const uint8_t* vb, uint8_t* knext, uint8_t* vnext)
+                    __attribute__((always_inline)) {
+        // this wavefront's DMAs of tile t have landed; the barrier extends that
+        // to the workgroup and frees the other buffer (read by tile t - 1)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const TileDesc d = cur;
+        if (t + 1 < ntiles) {
+            cur = describe(t + 1);
+            issue_tile(cur, knext, vnext);
+        }
+
+        // ---- S^T = K . Q^T --------------------------------------------------
+        float s[2][4][4];
+        const bool masked = qk_tile(d, kb, s);
+        if (masked) mask_tile(d, s);
 
         // ---- online softmax (lazy max) and P -> fp16 (fp8 on PV8 rest tiles) ---
         // rest-tile scores stay integer-valued until the exponent:
@@ -1068,6 +1110,8 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         }
     };
     if constexpr (PV8) {
+        cur = describe(0);
+        issue_tile(cur, s_k0, s_v0);
         // one copy of the step (the register budget of this kernel has no room
         // for two); buffers chosen at run time
         for (int t = 0; t < ntiles; ++t) {
@@ -1075,11 +1119,313 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             step(t, odd ? s_k1 : s_k0, odd ? s_v1 : s_v0, odd ? s_k0 : s_k1, odd ? s_v0 : s_v1);
         }
     } else {
-        for (int t = 0; t < ntiles; t += 2) {  // unrolled by two: each step's buffers are fixed objects
-            step(t, s_k0, s_v0, s_k1, s_v1);
-            if (t + 1 >= ntiles) break;
-            step(t + 1, s_k1, s_v1, s_k0, s_v0);
+        // ---- fp16 P.V: the tiles as three runs, each its own loop -----------
+        // Tiles t < nrt are rest tiles, then nvt vertical tiles, then nwt
+        // window tiles.  A run fixes its kind at compile time and its K / V
+        // sources (buffer resources) before its loop, so a tile costs only its
+        // DMA offsets: no per-tile source selection, no reload of kernel
+        // arguments, no scalar-memory load whose wait would also drain the LDS
+        // reads (the rest tiles' k_scale arrives by a vector load a tile ahead,
+        // under the tile's DMA wait).  Tile t uses buffer pair t & 1 (chosen at
+        // run time: the K and V reads are inline asm, so the compiler does not
+        // order them after the other buffer's in-flight DMAs); the last tile of
+        // a run prefetches the next run's first tile.
+        const Rsrc rsc = pf_rsrc(ksc_row, static_cast<uint32_t>(nrt) * 4u);
+        auto sources = [&](auto KT, Rsrc& rk, Rsrc& rv) __attribute__((always_inline)) {
+            constexpr int KIND = decltype(KT)::value;
+            if constexpr (KIND == T_REST) {
+                rk = pf_rsrc(a.k8r + static_cast<int64_t>(bh) * a.P * PD, static_cast<uint32_t>(nr_b) * RS8);
+                rv = pf_rsrc(a.vr + static_cast<int64_t>(bh) * a.P * PD, static_cast<uint32_t>(nr_b) * RS16);
+            } else if constexpr (KIND == T_VERT) {
+                rk = pf_rsrc(a.kv16 + static_cast<int64_t>(bh) * a.T * PD, static_cast<uint32_t>(nv_b) * RS16);
+                rv = pf_rsrc(a.vv16 + static_cast<int64_t>(bh) * a.T * PD, static_cast<uint32_t>(nv_b) * RS16);
+            } else {
+                rk = pf_rsrc(a.k16 + bhk * a.N * PD, static_cast<uint32_t>(wend) * RS16);
+                rv = pf_rsrc(a.v16 + bhk * a.N * PD, static_cast<uint32_t>(wend) * RS16);
+            }
+        };
+        // first key (window) or list entry (rest, vertical) of tile t of run KIND
+        auto first_of = [&](auto KT, int t) __attribute__((always_inline)) {
+            constexpr int KIND = decltype(KT)::value;
+            if constexpr (KIND == T_REST) return BN * t;
+            else if constexpr (KIND == T_VERT) return BN * (t - nrt);
+            else return wla + BN * (t - nrt - nvt);
+        };
+        // the DMAs of one tile into buffer pair par
+        auto issue = [&](auto KT, const Rsrc& rk, const Rsrc& rv, int i0, int par) __attribute__((always_inline)) {
+            constexpr int KIND = decltype(KT)::value;
+            uint8_t* kd = par ? s_k1 : s_k0;
+            uint8_t* vd = par ? s_v1 : s_v0;
+            const uint32_t r0 = static_cast<uint32_t>(i0);
+            if constexpr (KIND == T_REST) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int q = 2 * w + i;
+                    pf_dma16(rk, kd + 1024 * q, dk8, r0 * RS8 + 1024 * q);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int q = 4 * w + i;
+                    const uint32_t vo = static_cast<uint32_t>((lane >> 4) * RS16 +
+                                                              16 * ((lane & 15) ^ ((4 * i + (lane >> 4)) & 15)));
+                    pf_dma16(rk, kd + 1024 * q, vo, r0 * RS16 + 1024 * q);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int q = 4 * w + i;
+                pf_dma16(rv, vd + 1024 * q, dv16, r0 * RS16 + 1024 * q);
+            }
+        };
+        // the first tile of the run after KIND (the rare cross-run prefetch)
+        auto issue_next_run = [&](auto KT, int t, int par) __attribute__((always_inline)) {
+            constexpr int KIND = decltype(KT)::value;
+            Rsrc rk, rv;
+            if constexpr (KIND == T_REST) {
+                if (t < nrt + nvt) {
+                    sources(std::integral_constant<int, T_VERT>{}, rk, rv);
+                    issue(std::integral_constant<int, T_VERT>{}, rk, rv, first_of(std::integral_constant<int, T_VERT>{}, t), par);
+                    return;
+                }
+            }
+            if constexpr (KIND != T_WIN) {
+                sources(std::integral_constant<int, T_WIN>{}, rk, rv);
+                issue(std::integral_constant<int, T_WIN>{}, rk, rv, first_of(std::integral_constant<int, T_WIN>{}, t), par);
+            }
+        };
+
+        // per-lane LDS byte offsets of the reads within a buffer
+        //   rest K (128-B rows):   chunk g and 4 + g of row 16 kb + c16
+        //   fp16 K (256-B rows):   chunk 8 (m >> 1) + 2g + (m & 1) of row 16 kb + c16
+        //   fp16 V (transposed):   the lds_tr16 addressing of channel block cb
+        const uint32_t ok8a = c16 * RS8 + 16 * (g ^ (c16 & 7));
+        const uint32_t ok8b = c16 * RS8 + 16 * ((4 + g) ^ (c16 & 7));
+        uint32_t ok16[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) ok16[m] = c16 * RS16 + 16 * ((8 * (m >> 1) + 2 * g + (m & 1)) ^ c16);
+        uint32_t ov[4];            // channel blocks cb and cb + 4 differ by a constant 128 bytes
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+            ov[cb] = (4 * g + (c16 >> 2)) * RS16 + 8 * (c16 & 1) +
+                     16 * ((2 * cb + ((c16 & 3) >> 1)) ^ (2 * ((c16 >> 2) & 3)));
+        const uint32_t kbase[2] = {lds_addr(s_k0), lds_addr(s_k1)};
+        const uint32_t vbase[2] = {lds_addr(s_v0), lds_addr(s_v1)};
+        const u32x4 onew = {0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};   // fp16 1.0
+
+        // S^T = K . Q^T of a rest tile (int8 or e4m3) from K at kb
+        auto qk_rest = [&](uint32_t kb, float (&s)[2][4][4]) __attribute__((always_inline)) {
+            i32x4 ka[4][2];
+            const uint32_t aa = kb + ok8a, ab = kb + ok8b;
+            ka[0][0] = lds_rd128<0 * 16 * RS8>(aa); ka[0][1] = lds_rd128<0 * 16 * RS8>(ab);
+            ka[1][0] = lds_rd128<1 * 16 * RS8>(aa); ka[1][1] = lds_rd128<1 * 16 * RS8>(ab);
+            ka[2][0] = lds_rd128<2 * 16 * RS8>(aa); ka[2][1] = lds_rd128<2 * 16 * RS8>(ab);
+            ka[3][0] = lds_rd128<3 * 16 * RS8>(aa); ka[3][1] = lds_rd128<3 * 16 * RS8>(ab);
+            lds_wait8(ka[0][0], ka[0][1], ka[1][0], ka[1][1], ka[2][0], ka[2][1], ka[3][0], ka[3][1]);
+#pragma unroll
+            for (int kbk = 0; kbk < 4; ++kbk) {
+                if constexpr (QF8) {
+                    const i32x8 av = {ka[kbk][0][0], ka[kbk][0][1], ka[kbk][0][2], ka[kbk][0][3],
+                                      ka[kbk][1][0], ka[kbk][1][1], ka[kbk][1][2], ka[kbk][1][3]};
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb) {
+                        const i32x8 bv = {q8[sb][0][0], q8[sb][0][1], q8[sb][0][2], q8[sb][0][3],
+                                          q8[sb][1][0], q8[sb][1][1], q8[sb][1][2], q8[sb][1][3]};
+                        const f32x4 sf = mfma_f8_k128(av, bv);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) s[sb][kbk][r] = sf[r];
+                    }
+                } else {
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb) {
+                        i32x4 si = mfma_i8(ka[kbk][0], q8[sb][0], i32x4{0, 0, 0, 0});
+                        si = mfma_i8(ka[kbk][1], q8[sb][1], si);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) s[sb][kbk][r] = static_cast<float>(si[r]);
+                    }
+                }
+            }
+        };
+        // S^T = K . Q^T of an fp16 tile (vertical, window) from K at kb; the
+        // reads of key block kbk + 1 in flight during the MFMAs of kbk
+        auto qk_f16 = [&](uint32_t kb, float (&s)[2][4][4]) __attribute__((always_inline)) {
+            f32x4 sf[2][4];
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk) sf[sb][kbk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            i32x4 kr[2][4];
+            const uint32_t ad[4] = {kb + ok16[0], kb + ok16[1], kb + ok16[2], kb + ok16[3]};
+            auto rd = [&](auto KBT, int st) __attribute__((always_inline)) {
+                constexpr int OFF = 16 * RS16 * decltype(KBT)::value;
+                kr[st][0] = lds_rd128<OFF>(ad[0]);
+                kr[st][1] = lds_rd128<OFF>(ad[1]);
+                kr[st][2] = lds_rd128<OFF>(ad[2]);
+                kr[st][3] = lds_rd128<OFF>(ad[3]);
+            };
+            rd(std::integral_constant<int, 0>{}, 0);
+            static_for<4>([&](auto KBT) __attribute__((always_inline)) {
+                constexpr int kbk = decltype(KBT)::value, st = kbk & 1;
+                lds_wait4(kr[st][0], kr[st][1], kr[st][2], kr[st][3]);
+                if constexpr (kbk + 1 < 4) rd(std::integral_constant<int, kbk + 1>{}, st ^ 1);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const f16x8 av = __builtin_bit_cast(f16x8, kr[st][m]);
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb) sf[sb][kbk] = mfma_f16(av, qh[sb][m], sf[sb][kbk]);
+                }
+            });
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s[sb][kbk][r] = sf[sb][kbk][r];
+        };
+        // -inf for the keys e of the tile a row may not see: e >= valid, and
+        // with `causal` e > row
+        auto mask_keys = [&](int i0, int valid, bool causal, float (&s)[2][4][4]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                const int row = BM * blk + 32 * w + 16 * sb + c16;
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int e = i0 + 16 * kbk + 4 * g + r;
+                        const bool ok = (e < valid) & (!causal | (e <= row));
+                        s[sb][kbk][r] = ok ? s[sb][kbk][r] : -INFINITY;
+                    }
+            }
+        };
+        // online softmax (lazy max) of one tile and P -> fp16 B operands;
+        // rest-tile scores stay integer-valued until the exponent (ssc =
+        // q_scale k_scale, or 1 for fp16 tiles and all-zero blocks)
+        auto softmax16 = [&](float ssc, float (&s)[2][4][4], u32x4 (&pw)[2][2]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                float mx = s[sb][0][0];
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[sb][kbk][r]);
+                mx = quad_max(mx) * ssc;
+                if (__builtin_amdgcn_ballot_w64(mx > m_run[sb] + PF_SLACK)) {
+                    const float mnew = fmaxf(m_run[sb], mx);
+                    const float alpha = __builtin_amdgcn_exp2f(m_run[sb] - mnew);
+                    lsum[sb] *= alpha;
+#pragma unroll
+                    for (int cb = 0; cb < 8; ++cb) acc[sb][cb] *= alpha;
+                    m_run[sb] = mnew;
+                }
+                float p[4][4];
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        p[kbk][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][kbk][r], ssc, -m_run[sb]));
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    pw[sb][j] = u32x4{pack_f16x2(p[2 * j][0], p[2 * j][1]), pack_f16x2(p[2 * j][2], p[2 * j][3]),
+                                      pack_f16x2(p[2 * j + 1][0], p[2 * j + 1][1]),
+                                      pack_f16x2(p[2 * j + 1][2], p[2 * j + 1][3])};
+            }
+        };
+        // O^T += V^T . P^T from V at vb, and the row sums of P; the reads of
+        // channel block cb + 1 in flight during the MFMAs of cb
+        auto pv16 = [&](uint32_t vb, const u32x4 (&pw)[2][2]) __attribute__((always_inline)) {
+            u32x2 v16[2][2][2];            // [stage][j][h]
+            const uint32_t ad[4] = {vb + ov[0], vb + ov[1], vb + ov[2], vb + ov[3]};
+            auto rd16 = [&](auto CBT, int st) __attribute__((always_inline)) {
+                constexpr int cb = decltype(CBT)::value, OFF = 128 * (cb >> 2);
+                v16[st][0][0] = lds_tr16<OFF>(ad[cb & 3]);
+                v16[st][0][1] = lds_tr16<OFF + 16 * RS16>(ad[cb & 3]);
+                v16[st][1][0] = lds_tr16<OFF + 32 * RS16>(ad[cb & 3]);
+                v16[st][1][1] = lds_tr16<OFF + 48 * RS16>(ad[cb & 3]);
+            };
+            rd16(std::integral_constant<int, 0>{}, 0);
+            static_for<8>([&](auto CBT) __attribute__((always_inline)) {
+                constexpr int cb = decltype(CBT)::value, st = cb & 1;
+                lds_wait(v16[st][0][0], v16[st][0][1], v16[st][1][0], v16[st][1][1]);
+                if constexpr (cb + 1 < 8) rd16(std::integral_constant<int, cb + 1>{}, st ^ 1);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const f16x8 av = __builtin_bit_cast(f16x8, u32x4{v16[st][j][0][0], v16[st][j][0][1],
+                                                                     v16[st][j][1][0], v16[st][j][1][1]});
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb)
+                        acc[sb][cb] = mfma_f16(av, __builtin_bit_cast(f16x8, pw[sb][j]), acc[sb][cb]);
+                }
+            });
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb)
+                    lsum[sb] = mfma_f16(__builtin_bit_cast(f16x8, onew), __builtin_bit_cast(f16x8, pw[sb][j]), lsum[sb]);
+        };
+
+        // one run: tiles [t0, t1) of kind KIND
+        float sc_next = 0.0f;      // k_scale of the next rest tile (vector load, a tile ahead)
+        auto run = [&](auto KT, int t0, int t1) __attribute__((always_inline)) {
+            constexpr int KIND = decltype(KT)::value;
+            if (t0 >= t1) return;
+            Rsrc rk, rv;
+            sources(KT, rk, rv);
+            const int valid = KIND == T_REST ? nr_b : KIND == T_VERT ? nv_b : wend;
+            const bool causal = KIND == T_WIN || (KIND == T_REST && a.rest_causal);
+            for (int t = t0; t < t1; ++t) {
+                // this wavefront's DMAs of tile t have landed; the barrier
+                // extends that to the workgroup and frees the other buffer pair
+                // (read by tile t - 1)
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+                const int par = t & 1;
+                const int i0 = first_of(KT, t);
+                float sc = 1.0f;
+                if constexpr (KIND == T_REST) {
+                    sc = sc_next;
+                    if (t + 1 < t1)
+                        sc_next = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, 0, 4 * (t + 1), 0));
+                }
+                if (t + 1 < t1) issue(KT, rk, rv, i0 + BN, par ^ 1);
+                else if (t + 1 < ntiles) issue_next_run(KT, t + 1, par ^ 1);
+
+                float s[2][4][4];
+                if constexpr (KIND == T_REST) qk_rest(kbase[par], s);
+                else qk_f16(kbase[par], s);
+                const int row0 = BM * blk + 32 * w;       // this wavefront's first row
+                if (i0 + BN > valid || (causal && i0 + BN - 1 > row0)) mask_keys(i0, valid, causal, s);
+                float ssc = 1.0f;
+                if constexpr (KIND == T_REST) {
+                    // a zero scale means all-zero codes on one side: every
+                    // score is 0 and the scale 1 gives the same result (and
+                    // keeps -inf * scale = -inf)
+                    const float qks = q_scale * sc;
+                    ssc = qks > 0.0f ? qks : 1.0f;
+                }
+                u32x4 pw[2][2];
+                softmax16(ssc, s, pw);
+                pv16(vbase[par], pw);
+            }
+        };
+        {
+            // tile 0's DMAs (and scale) before the first run
+            Rsrc rk, rv;
+            if (nrt > 0) {
+                sources(std::integral_constant<int, T_REST>{}, rk, rv);
+                issue(std::integral_constant<int, T_REST>{}, rk, rv, 0, 0);
+                sc_next = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, 0, 0, 0));
+            } else if (nvt > 0) {
+                sources(std::integral_constant<int, T_VERT>{}, rk, rv);
+                issue(std::integral_constant<int, T_VERT>{}, rk, rv, 0, 0);
+            } else if (nwt > 0) {
+                sources(std::integral_constant<int, T_WIN>{}, rk, rv);
+                issue(std::integral_constant<int, T_WIN>{}, rk, rv, wla, 0);
+            }
         }
+        run(std::integral_constant<int, T_REST>{}, 0, nrt);
+        run(std::integral_constant<int, T_VERT>{}, nrt, nrt + nvt);
+        run(std::integral_constant<int, T_WIN>{}, nrt + nvt, ntiles);
     }
 
     // ---- epilogue: O = acc / l (x vscale in fp8 mode) ------------------------------

@@ -78,6 +78,7 @@ constexpr int STAT_ROWS = 128;           // rows per kv_stats chunk
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -118,18 +119,11 @@ __device__ __forceinline__ u32x2 lds_tr16(uint32_t addr) {
     asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
     return r;
 }
-// The intrinsic forms, for the kernel with fp8 P.V: its register budget has
-// no room for the pipelined asm reads, and there the compiler's drain of the
-// next tile's DMAs costs less than spilling.
-typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 tr_f16x4;
-typedef __attribute__((__vector_size__(2 * sizeof(int)))) int tr_i32x2;
-__device__ __forceinline__ u32x2 lds_tr16_i(const uint8_t* p) {
-    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                                         (__attribute__((address_space(3))) tr_f16x4*)(p)));
-}
-__device__ __forceinline__ u32x2 lds_tr8_i(const uint8_t* p) {
-    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                                         (__attribute__((address_space(3))) tr_i32x2*)(p)));
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_tr8(uint32_t addr) {
+    u32x2 r;
+    asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+    return r;
 }
 __device__ __forceinline__ void lds_wait(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
@@ -660,13 +654,6 @@ __device__ __forceinline__ f32x4 mfma_fp8(const u32x2& a, const u32x2& b, const 
     return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0, 0, 0);
 }
 
-struct TileDesc {
-    int kind;
-    int idx0;      // first list entry (rest / vert) or first key (window)
-    int valid;     // rest / vert: entries of the list below wla; window: end key (exclusive)
-    float sc;      // rest: the 64-entry block's k_scale (times q_scale at use)
-};
-
 // PV8: fp8 PV on the rest tiles (P' = exp2(s - m + 8.807) as e4m3 against
 // e4m3(v / vscale)); the vertical and window tiles keep fp16 operands in the
 // same units (fp16(P'), fp16(v / vscale)); the epilogue multiplies by vscale.
@@ -782,18 +769,6 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     const int ntiles = nrt + nvt + nwt;
     const float* ksc_row = a.k8r_scale + static_cast<int64_t>(bh) * a.nsb;
 
-    auto describe = [&](int t) {
-        TileDesc d;
-        if (t < nrt) {
-            d.kind = T_REST; d.idx0 = BN * t; d.valid = nr_b; d.sc = ksc_row[t];    // used a tile later
-        } else if (t < nrt + nvt) {
-            d.kind = T_VERT; d.idx0 = BN * (t - nrt); d.valid = nv_b; d.sc = 1.0f;
-        } else {
-            d.kind = T_WIN; d.idx0 = wla + BN * (t - nrt - nvt); d.valid = wend; d.sc = 1.0f;
-        }
-        return d;
-    };
-
     // Tiles go from HBM straight into LDS (LDS DMA, no register staging).
     // Rows are stored whole, 128 B (int8 / e4m3) or 256 B (fp16), with
     // their 16-byte chunks XOR-swizzled by row so that the reads below hit
@@ -811,49 +786,6 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     const uint32_t dv16 = static_cast<uint32_t>((lane >> 4) * RS16 + 16 * ((lane & 15) ^ (2 * ((lane >> 4) & 3))));
     const uint32_t dv8 = static_cast<uint32_t>((lane >> 3) * RS8 +
                                                16 * ((lane & 7) ^ (((lane >> 3) & 3) | ((w & 1) << 2))));
-    auto issue_tile = [&](const TileDesc& d, uint8_t* kdst, uint8_t* vdst) {
-        const uint32_t i0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(d.idx0));
-        const uint32_t nvalid = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(d.valid));
-        if (d.kind == T_REST) {
-            const Rsrc rk = pf_rsrc(a.k8r + static_cast<int64_t>(bh) * a.P * PD, nvalid * RS8);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int q = 2 * w + i;
-                pf_dma16(rk, kdst + 1024 * q, dk8, i0 * RS8 + 1024 * q);
-            }
-        } else {
-            const uint16_t* kb = d.kind == T_VERT ? a.kv16 + static_cast<int64_t>(bh) * a.T * PD
-                                                  : a.k16 + bhk * a.N * PD;
-            const Rsrc rk = pf_rsrc(kb, nvalid * RS16);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int q = 4 * w + i;
-                const uint32_t vo = static_cast<uint32_t>((lane >> 4) * RS16 +
-                                                          16 * ((lane & 15) ^ ((4 * i + (lane >> 4)) & 15)));
-                pf_dma16(rk, kdst + 1024 * q, vo, i0 * RS16 + 1024 * q);
-            }
-        }
-        if (PV8 && d.kind == T_REST) {
-            const Rsrc rv = pf_rsrc(reinterpret_cast<const uint8_t*>(a.vr) + static_cast<int64_t>(bh) * a.P * PD,
-                                    nvalid * RS8);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int q = 2 * w + i;
-                pf_dma16(rv, vdst + 1024 * q, dv8, i0 * RS8 + 1024 * q);
-            }
-            return;
-        }
-        const uint16_t* vb = d.kind == T_REST ? a.vr + static_cast<int64_t>(bh) * a.P * PD
-                             : d.kind == T_VERT ? a.vv16 + static_cast<int64_t>(bh) * a.T * PD
-                                                : a.v16 + bhk * a.N * PD;
-        const Rsrc rv = pf_rsrc(vb, nvalid * RS16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int q = 4 * w + i;
-            pf_dma16(rv, vdst + 1024 * q, dv16, i0 * RS16 + 1024 * q);
-        }
-    };
-
     float m_run[2] = {PF_M_INIT, PF_M_INIT};
     // softmax denominators: PV8 sums P' on the VALU (l_run, per lane, summed
     // over the quad at the end); fp16 PV sums the fp16 P operands with one
@@ -861,265 +793,24 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     // column's full sum), which takes 32 adds per tile off the VALU
     float l_run[2] = {0.0f, 0.0f};
     f32x4 lsum[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+    // fp16 P.V: O^T in 16 x 16 blocks [sub-block][16 channels] (lane (c, g):
+    // row c of the sub-block, channels 16 cb + 4 g + 0..3)
     f32x4 acc[2][8];
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
         for (int cb = 0; cb < 8; ++cb) acc[sb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // fp8 P.V: O^T in 32 x 32 blocks of 32 channels (lane l: row l % 32 of
+    // the wavefront, channels 32 cbk + 8 (i >> 2) + 4 (l >> 5) + (i & 3) in
+    // register i), the layout of v_mfma_scale_f32_32x32x64_f8f6f4
+    f32x16 acc32[4];
+#pragma unroll
+    for (int cbk = 0; cbk < 4; ++cbk)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc32[cbk][i] = 0.0f;
 
-    TileDesc cur{};                // the next tile (fp8 P.V loop)
-    // one tile: its DMAs (into kb / vb) were issued a tile earlier; the next
-    // tile's go into knext / vnext
-    // S^T = K . Q^T of tile d from its K buffer kb; returns whether any score
-    // of the tile needs the mask
-    auto qk_tile = [&](const TileDesc& d, const uint8_t* kb, float (&s)[2][4][4]) __attribute__((always_inline)) {
-        bool masked;
-        if (d.kind == T_REST && QF8) {
-#pragma unroll
-            for (int kbk = 0; kbk < 4; ++kbk) {
-                const uint8_t* row = kb + (16 * kbk + c16) * RS8;
-                const i32x4 a0 = *reinterpret_cast<const i32x4*>(row + 16 * (g ^ (c16 & 7)));
-                const i32x4 a1 = *reinterpret_cast<const i32x4*>(row + 16 * ((4 + g) ^ (c16 & 7)));
-                const i32x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-#pragma unroll
-                for (int sb = 0; sb < 2; ++sb) {
-                    const i32x8 bv = {q8[sb][0][0], q8[sb][0][1], q8[sb][0][2], q8[sb][0][3],
-                                      q8[sb][1][0], q8[sb][1][1], q8[sb][1][2], q8[sb][1][3]};
-                    const f32x4 sf = mfma_f8_k128(av, bv);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) s[sb][kbk][r] = sf[r];
-                }
-            }
-            masked = d.idx0 + BN > d.valid || (a.rest_causal && d.idx0 + BN - 1 > BM * blk + 32 * w);
-        } else if (d.kind == T_REST) {
-            i32x4 si[2][4];
-#pragma unroll
-            for (int kbk = 0; kbk < 4; ++kbk) {
-                const uint8_t* row = kb + (16 * kbk + c16) * RS8;
-                const i32x4 a0 = *reinterpret_cast<const i32x4*>(row + 16 * (g ^ (c16 & 7)));
-                const i32x4 a1 = *reinterpret_cast<const i32x4*>(row + 16 * ((4 + g) ^ (c16 & 7)));
-#pragma unroll
-                for (int sb = 0; sb < 2; ++sb) {
-                    si[sb][kbk] = mfma_i8(a0, q8[sb][0], i32x4{0, 0, 0, 0});
-                    si[sb][kbk] = mfma_i8(a1, q8[sb][1], si[sb][kbk]);
-                }
-            }
-#pragma unroll
-            for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-                for (int kbk = 0; kbk < 4; ++kbk)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) s[sb][kbk][r] = static_cast<float>(si[sb][kbk][r]);
-            masked = d.idx0 + BN > d.valid || (a.rest_causal && d.idx0 + BN - 1 > BM * blk + 32 * w);
-        } else {
-            f32x4 sf[2][4];
-#pragma unroll
-            for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-                for (int kbk = 0; kbk < 4; ++kbk) sf[sb][kbk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int kbk = 0; kbk < 4; ++kbk) {
-                const uint8_t* row = kb + (16 * kbk + c16) * RS16;
-#pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    const int chunk = 8 * (m >> 1) + 2 * g + (m & 1);          // channels 8 chunk .. + 7
-                    const f16x8 av = *reinterpret_cast<const f16x8*>(row + 16 * (chunk ^ c16));
-#pragma unroll
-                    for (int sb = 0; sb < 2; ++sb) sf[sb][kbk] = mfma_f16(av, qh[sb][m], sf[sb][kbk]);
-                }
-            }
-#pragma unroll
-            for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-                for (int kbk = 0; kbk < 4; ++kbk)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) s[sb][kbk][r] = sf[sb][kbk][r];
-            if (d.kind == T_VERT)
-                masked = d.idx0 + BN > d.valid;
-            else  // window: causal against this wavefront's first row, or past N
-                masked = d.idx0 + BN - 1 > BM * blk + 32 * w || d.idx0 + BN > d.valid;
-        }
-        return masked;
-    };
-
-    // -inf for the keys of tile d a row may not see
-    auto mask_tile = [&](const TileDesc& d, float (&s)[2][4][4]) __attribute__((always_inline)) {
-        {
-#pragma unroll
-            for (int sb = 0; sb < 2; ++sb) {
-                const int row = BM * blk + 32 * w + 16 * sb + c16;
-#pragma unroll
-                for (int kbk = 0; kbk < 4; ++kbk)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int e = d.idx0 + 16 * kbk + 4 * g + r;
-                        const bool causal = d.kind == T_WIN || (d.kind == T_REST && a.rest_causal);
-                        // bitwise: one select per score, no per-lane branches
-                        const bool ok = (e < d.valid) & (!causal | (e <= row));
-                        s[sb][kbk][r] = ok ? s[sb][kbk][r] : -INFINITY;
-                    }
-            }
-        }
-
-    };
-
-    auto step = [&](int t, const uint8_t* kb, const uint8_t* vb, uint8_t* knext, uint8_t* vnext)
-                    __attribute__((always_inline)) {
-        // this wavefront's DMAs of tile t have landed; the barrier extends that
-        // to the workgroup and frees the other buffer (read by tile t - 1)
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        const TileDesc d = cur;
-        if (t + 1 < ntiles) {
-            cur = describe(t + 1);
-            issue_tile(cur, knext, vnext);
-        }
-
-        // ---- S^T = K . Q^T --------------------------------------------------
-        float s[2][4][4];
-        const bool masked = qk_tile(d, kb, s);
-        if (masked) mask_tile(d, s);
-
-        // ---- online softmax (lazy max) and P -> fp16 (fp8 on PV8 rest tiles) ---
-        // rest-tile scores stay integer-valued until the exponent:
-        // p = exp2(s_int * (q_scale k_scale) - m) in one fma.  A zero scale
-        // means all-zero codes on one side, so every such score is 0 and the
-        // scale 1 gives the same result (and keeps -inf * scale = -inf).
-        const float qks = q_scale * d.sc;
-        const float ssc = d.kind == T_REST && qks > 0.0f ? qks : 1.0f;
-        u32x4 pw[2][2];                    // P^T operands: fp16 x 8, or fp8 x 8 in .xy
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-            float mx = s[sb][0][0];
-#pragma unroll
-            for (int kbk = 0; kbk < 4; ++kbk)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[sb][kbk][r]);
-            mx = quad_max(mx) * ssc;
-            if (__builtin_amdgcn_ballot_w64(mx > m_run[sb] + (PV8 ? 0.0f : PF_SLACK))) {
-                const float mnew = fmaxf(m_run[sb], mx);
-                const float alpha = __builtin_amdgcn_exp2f(m_run[sb] - mnew);
-                if constexpr (PV8) l_run[sb] *= alpha;
-                else lsum[sb] *= alpha;
-#pragma unroll
-                for (int cb = 0; cb < 8; ++cb) acc[sb][cb] *= alpha;
-                m_run[sb] = mnew;
-            }
-            float p[4][4];
-            float ls = 0.0f;
-            // PV8: the rounding of mx, of the bias and of the fma can lift
-            // the largest exponent by ulp(m) + 1e-6 above 8.807; the bias gives
-            // that back so P' never passes 447.98 (no clamp before e4m3)
-            const float bias = PV8 ? S_FP8_OFFSET - m_run[sb] - (fabsf(m_run[sb]) * 2.4e-7f + 1e-6f) : -m_run[sb];
-#pragma unroll
-            for (int kbk = 0; kbk < 4; ++kbk)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    p[kbk][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][kbk][r], ssc, bias));
-                    if constexpr (PV8) ls += p[kbk][r];
-                }
-            if constexpr (PV8) l_run[sb] += ls;
-            if (PV8 && d.kind == T_REST) {
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    pw[sb][j] = u32x4{pack_e4m3x4_raw(p[2 * j][0], p[2 * j][1], p[2 * j][2], p[2 * j][3]),
-                                      pack_e4m3x4_raw(p[2 * j + 1][0], p[2 * j + 1][1], p[2 * j + 1][2], p[2 * j + 1][3]),
-                                      0u, 0u};
-            } else {
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    pw[sb][j] = u32x4{pack_f16x2(p[2 * j][0], p[2 * j][1]), pack_f16x2(p[2 * j][2], p[2 * j][3]),
-                                      pack_f16x2(p[2 * j + 1][0], p[2 * j + 1][1]),
-                                      pack_f16x2(p[2 * j + 1][2], p[2 * j + 1][3])};
-                }
-            }
-        }
-
-        // ---- O^T += V^T . P^T -------------------------------------------------
-        // Lane addressing of the transpose reads: fp8 slot e = c16 >> 1 of
-        // lane-row g is key 32j + 16 (e >> 2) + 4g + (e & 3), whose swizzle
-        // is e, bytes 16cb + 8 (c16 & 1) of its row; fp16 slots 4h .. 4h + 3
-        // are keys 32j + 16h + 4g + (0..3), this lane addressing key
-        // 32j + 16h + 4g + (c16 >> 2), channels 16cb + 4 (c16 & 3) .. + 3
-        // (chunk 2cb + ((c16 & 3) >> 1), swizzled by 2 ((c16 >> 2) & 3)).
-        if constexpr (PV8) {
-            if (d.kind == T_REST) {
-                const int e = c16 >> 1;
-                const uint8_t* b8 = vb + (16 * (e >> 2) + 4 * g + (e & 3)) * RS8 + 8 * (c16 & 1);
-#pragma unroll
-                for (int cb = 0; cb < 8; ++cb) {
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const u32x2 av = lds_tr8_i(b8 + 32 * j * RS8 + 16 * (cb ^ e));
-#pragma unroll
-                        for (int sb = 0; sb < 2; ++sb)
-                            acc[sb][cb] = mfma_fp8(av, u32x2{pw[sb][j][0], pw[sb][j][1]}, acc[sb][cb]);
-                    }
-                }
-            } else {
-                const uint8_t* b16 = vb + (4 * g + (c16 >> 2)) * RS16 + 8 * (c16 & 1);
-#pragma unroll
-                for (int cb = 0; cb < 8; ++cb) {
-                    const int chunk = (2 * cb + ((c16 & 3) >> 1)) ^ (2 * ((c16 >> 2) & 3));
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const uint8_t* p0 = b16 + 32 * j * RS16 + 16 * chunk;
-                        const u32x2 lo = lds_tr16_i(p0), hi = lds_tr16_i(p0 + 16 * RS16);
-                        const f16x8 av = __builtin_bit_cast(f16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-#pragma unroll
-                        for (int sb = 0; sb < 2; ++sb)
-                            acc[sb][cb] = mfma_f16(av, __builtin_bit_cast(f16x8, pw[sb][j]), acc[sb][cb]);
-                    }
-                }
-            }
-        } else {
-            // asm reads, the reads of channel block cb + 1 in flight during the
-            // MFMAs of cb
-            const uint32_t a16 = lds_addr(vb + (4 * g + (c16 >> 2)) * RS16 + 8 * (c16 & 1));
-            u32x2 v16[2][2][2];            // [stage][j][h]
-            auto rd16 = [&](int cb, int st) {
-                const uint32_t ad = a16 + 16 * ((2 * cb + ((c16 & 3) >> 1)) ^ (2 * ((c16 >> 2) & 3)));
-                v16[st][0][0] = lds_tr16<0>(ad);
-                v16[st][0][1] = lds_tr16<16 * RS16>(ad);
-                v16[st][1][0] = lds_tr16<32 * RS16>(ad);
-                v16[st][1][1] = lds_tr16<48 * RS16>(ad);
-            };
-            rd16(0, 0);
-#pragma unroll
-            for (int cb = 0; cb < 8; ++cb) {
-                const int st = cb & 1;
-                lds_wait(v16[st][0][0], v16[st][0][1], v16[st][1][0], v16[st][1][1]);
-                if (cb + 1 < 8) rd16(cb + 1, st ^ 1);
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const f16x8 av = __builtin_bit_cast(f16x8, u32x4{v16[st][j][0][0], v16[st][j][0][1],
-                                                                     v16[st][j][1][0], v16[st][j][1][1]});
-#pragma unroll
-                    for (int sb = 0; sb < 2; ++sb)
-                        acc[sb][cb] = mfma_f16(av, __builtin_bit_cast(f16x8, pw[sb][j]), acc[sb][cb]);
-                }
-            }
-        }
-        if constexpr (!PV8) {
-            const u32x4 onew = {0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};   // fp16 1.0
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int sb = 0; sb < 2; ++sb)
-                    lsum[sb] = mfma_f16(__builtin_bit_cast(f16x8, onew), __builtin_bit_cast(f16x8, pw[sb][j]), lsum[sb]);
-        }
-    };
-    if constexpr (PV8) {
-        cur = describe(0);
-        issue_tile(cur, s_k0, s_v0);
-        // one copy of the step (the register budget of this kernel has no room
-        // for two); buffers chosen at run time
-        for (int t = 0; t < ntiles; ++t) {
-            const bool odd = t & 1;
-            step(t, odd ? s_k1 : s_k0, odd ? s_v1 : s_v0, odd ? s_k0 : s_k1, odd ? s_v0 : s_v1);
-        }
-    } else {
-        // ---- fp16 P.V: the tiles as three runs, each its own loop -----------
+    {
+        // ---- the tiles as three runs, each its own loop ---------------------
         // Tiles t < nrt are rest tiles, then nvt vertical tiles, then nwt
         // window tiles.  A run fixes its kind at compile time and its K / V
         // sources (buffer resources) before its loop, so a tile costs only its
@@ -1135,7 +826,11 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             constexpr int KIND = decltype(KT)::value;
             if constexpr (KIND == T_REST) {
                 rk = pf_rsrc(a.k8r + static_cast<int64_t>(bh) * a.P * PD, static_cast<uint32_t>(nr_b) * RS8);
-                rv = pf_rsrc(a.vr + static_cast<int64_t>(bh) * a.P * PD, static_cast<uint32_t>(nr_b) * RS16);
+                if constexpr (PV8)     // e4m3 V rows of 128 bytes
+                    rv = pf_rsrc(reinterpret_cast<const uint8_t*>(a.vr) + static_cast<int64_t>(bh) * a.P * PD,
+                                 static_cast<uint32_t>(nr_b) * RS8);
+                else
+                    rv = pf_rsrc(a.vr + static_cast<int64_t>(bh) * a.P * PD, static_cast<uint32_t>(nr_b) * RS16);
             } else if constexpr (KIND == T_VERT) {
                 rk = pf_rsrc(a.kv16 + static_cast<int64_t>(bh) * a.T * PD, static_cast<uint32_t>(nv_b) * RS16);
                 rv = pf_rsrc(a.vv16 + static_cast<int64_t>(bh) * a.T * PD, static_cast<uint32_t>(nv_b) * RS16);
@@ -1172,10 +867,18 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                     pf_dma16(rk, kd + 1024 * q, vo, r0 * RS16 + 1024 * q);
                 }
             }
+            if constexpr (PV8 && KIND == T_REST) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int q = 4 * w + i;
-                pf_dma16(rv, vd + 1024 * q, dv16, r0 * RS16 + 1024 * q);
+                for (int i = 0; i < 2; ++i) {
+                    const int q = 2 * w + i;
+                    pf_dma16(rv, vd + 1024 * q, dv8, r0 * RS8 + 1024 * q);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int q = 4 * w + i;
+                    pf_dma16(rv, vd + 1024 * q, dv16, r0 * RS16 + 1024 * q);
+                }
             }
         };
         // the first tile of the run after KIND (the rare cross-run prefetch)
@@ -1209,6 +912,34 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         for (int cb = 0; cb < 4; ++cb)
             ov[cb] = (4 * g + (c16 >> 2)) * RS16 + 8 * (c16 & 1) +
                      16 * ((2 * cb + ((c16 & 3) >> 1)) ^ (2 * ((c16 >> 2) & 3)));
+        // fp8 P.V kernel, vertical / window tiles: the V^T operand of
+        // v_mfma_f32_32x32x16_f16 (32 channels x 16 keys): lane l = 16 G + j
+        // receives channel 32 cbk + 16 (G & 1) + j of keys 16 kb + 8 (G >> 1) +
+        // 4 rd + e (e = 0..3) from read rd; as the addressing lane a = j it
+        // names row 16 kb + 8 (G >> 1) + 4 rd + (a >> 2), channels 32 cbk +
+        // 16 (G & 1) + 4 (a & 3) .. + 3, in chunk 4 cbk + 2 (G & 1) + ((a & 3) >> 1)
+        // stored at chunk ^ 2 (row & 3).  Blocks cbk and cbk + 2 differ by a
+        // constant 128 bytes, kb and rd by whole rows.
+        uint32_t ovh[2];
+#pragma unroll
+        for (int cbk = 0; cbk < 2; ++cbk)
+            ovh[cbk] = (8 * (g >> 1) + (c16 >> 2)) * RS16 + 8 * (c16 & 1) +
+                       16 * ((4 * cbk + 2 * (g & 1) + ((c16 & 3) >> 1)) ^ (2 * (c16 >> 2)));
+        // fp8 P.V kernel, rest tiles: the V^T operand of
+        // v_mfma_scale_f32_32x32x64_f8f6f4 (32 channels x 64 keys, e4m3): byte
+        // i of lane l holds channel 32 cbk + l % 32 of key kp(i) + 8 (l >> 5),
+        // kp(i) = 16 (i >> 2) + (i & 3) for i < 16 and 16 ((i - 16) >> 2) + 4 +
+        // (i & 3) above (the key order of P after the row swap below).  Read rd
+        // (ds_read_b64_tr_b8) fills bytes 8 rd .. 8 rd + 7: the addressing lane
+        // a = j of group G names key kb0(rd) + 16 (a >> 3) + ((a >> 1) & 3) +
+        // 8 (G >> 1), kb0 = 0, 32, 4, 36, channels 32 cbk + 16 (G & 1) + 8 (a & 1)
+        // .. + 7: chunk 2 cbk + (G & 1), stored at chunk ^ (a >> 1) (the e4m3 V
+        // swizzle: (row & 3) | 4 ((row >> 4) & 1) is a >> 1 for these rows).
+        uint32_t ov8[4];
+#pragma unroll
+        for (int cbk = 0; cbk < 4; ++cbk)
+            ov8[cbk] = (16 * (c16 >> 3) + ((c16 >> 1) & 3) + 8 * (g >> 1)) * RS8 + 8 * (c16 & 1) +
+                       16 * ((2 * cbk + (g & 1)) ^ (c16 >> 1));
         const uint32_t kbase[2] = {lds_addr(s_k0), lds_addr(s_k1)};
         const uint32_t vbase[2] = {lds_addr(s_v0), lds_addr(s_v1)};
         const u32x4 onew = {0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};   // fp16 1.0
@@ -1364,6 +1095,142 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                     lsum[sb] = mfma_f16(__builtin_bit_cast(f16x8, onew), __builtin_bit_cast(f16x8, pw[sb][j]), lsum[sb]);
         };
 
+        // fp8 P.V kernel: exact running max (P' = exp2(s - m + 8.807) stays at
+        // or below 448, the e4m3 range), the row sums of P' on the VALU
+        // (l_run); rest tiles pack P' as e4m3 (pk8[sb][kb]: keys 16 kb + 4 g +
+        // 0..3), vertical and window tiles as fp16 (pw, as softmax16)
+        auto softmax8 = [&](auto KT, float ssc, float (&s)[2][4][4], uint32_t (&pk8)[2][4], u32x4 (&pw)[2][2])
+                            __attribute__((always_inline)) {
+            constexpr int KIND = decltype(KT)::value;
+            float alpha[2] = {1.0f, 1.0f};
+            bool resc = false;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                float mx = s[sb][0][0];
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[sb][kbk][r]);
+                mx = quad_max(mx) * ssc;
+                if (__builtin_amdgcn_ballot_w64(mx > m_run[sb])) {
+                    const float mnew = fmaxf(m_run[sb], mx);
+                    alpha[sb] = __builtin_amdgcn_exp2f(m_run[sb] - mnew);
+                    l_run[sb] *= alpha[sb];
+                    m_run[sb] = mnew;
+                    resc = true;
+                }
+            }
+            if (resc) {                // acc32 lane l holds row l % 32: sub-block (l >> 4) & 1
+                const float al = ((lane >> 4) & 1) ? alpha[1] : alpha[0];
+#pragma unroll
+                for (int cbk = 0; cbk < 4; ++cbk) acc32[cbk] *= al;
+            }
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                // the rounding of mx, of the bias and of the fma can lift the
+                // largest exponent by ulp(m) + 1e-6 above 8.807; the bias gives
+                // that back so P' never passes 447.98 (no clamp before e4m3)
+                const float bias = S_FP8_OFFSET - m_run[sb] - (fabsf(m_run[sb]) * 2.4e-7f + 1e-6f);
+                float p[4][4];
+                float ls = 0.0f;
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        p[kbk][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][kbk][r], ssc, bias));
+                        ls += p[kbk][r];
+                    }
+                l_run[sb] += ls;
+                if constexpr (KIND == T_REST) {
+#pragma unroll
+                    for (int kbk = 0; kbk < 4; ++kbk)
+                        pk8[sb][kbk] = pack_e4m3x4_raw(p[kbk][0], p[kbk][1], p[kbk][2], p[kbk][3]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        pw[sb][j] = u32x4{pack_f16x2(p[2 * j][0], p[2 * j][1]), pack_f16x2(p[2 * j][2], p[2 * j][3]),
+                                          pack_f16x2(p[2 * j + 1][0], p[2 * j + 1][1]),
+                                          pack_f16x2(p[2 * j + 1][2], p[2 * j + 1][3])};
+                }
+            }
+        };
+        // fp8 P.V kernel: P arrives in the score layout (lane (c, g): keys
+        // 16 kb + 4 g + r of rows c (sub-block 0) and 16 + c (sub-block 1));
+        // v_permlane16_swap of the two sub-blocks' registers leaves lane l with
+        // row l % 32: its own keys then those of lane l ^ 16, i.e. keys
+        // 16 kb + 8 (l >> 5) + 0..7 for fp16 P and the kp order above for e4m3 P.
+        // O^T += V^T . P^T of a vertical / window tile (fp16 V at vb) with
+        // v_mfma_f32_32x32x16_f16 per 16 keys and 32 channels
+        auto pvh32 = [&](uint32_t vb, u32x4 (&pw)[2][2]) __attribute__((always_inline)) {
+            u32x4 pb[4];               // B operand of key block kb
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const int j = kb >> 1, e0 = 2 * (kb & 1);
+                const auto r0 = __builtin_amdgcn_permlane16_swap(pw[0][j][e0], pw[1][j][e0], false, false);
+                const auto r1 = __builtin_amdgcn_permlane16_swap(pw[0][j][e0 + 1], pw[1][j][e0 + 1], false, false);
+                pb[kb] = u32x4{r0[0], r1[0], r0[1], r1[1]};
+            }
+            const uint32_t ad[2] = {vb + ovh[0], vb + ovh[1]};
+            u32x2 va[2][4][2];         // [stage][cbk][rd]: the 8 reads of key block kb
+            auto rd = [&](auto KBT, int st) __attribute__((always_inline)) {
+                constexpr int kb = decltype(KBT)::value;
+                static_for<4>([&](auto CBT) __attribute__((always_inline)) {
+                    constexpr int cbk = decltype(CBT)::value, OFF = (16 * kb) * RS16 + 128 * (cbk >> 1);
+                    va[st][cbk][0] = lds_tr16<OFF>(ad[cbk & 1]);
+                    va[st][cbk][1] = lds_tr16<OFF + 4 * RS16>(ad[cbk & 1]);
+                });
+            };
+            rd(std::integral_constant<int, 0>{}, 0);
+            static_for<4>([&](auto KBT) __attribute__((always_inline)) {
+                constexpr int kb = decltype(KBT)::value, st = kb & 1;
+                lds_wait(va[st][0][0], va[st][0][1], va[st][1][0], va[st][1][1]);
+                lds_wait(va[st][2][0], va[st][2][1], va[st][3][0], va[st][3][1]);
+                if constexpr (kb + 1 < 4) rd(std::integral_constant<int, kb + 1>{}, st ^ 1);
+#pragma unroll
+                for (int cbk = 0; cbk < 4; ++cbk) {
+                    const f16x8 av = __builtin_bit_cast(f16x8, u32x4{va[st][cbk][0][0], va[st][cbk][0][1],
+                                                                     va[st][cbk][1][0], va[st][cbk][1][1]});
+                    acc32[cbk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, __builtin_bit_cast(f16x8, pb[kb]),
+                                                                        acc32[cbk], 0, 0, 0);
+                }
+            });
+        };
+        // O^T += V^T . P'^T of a rest tile (e4m3 V at vb): one
+        // v_mfma_scale_f32_32x32x64_f8f6f4 per 32 channels over all 64 keys
+        // (unit block scales), the reads of block cbk + 1 in flight during the
+        // MFMA of cbk
+        auto pv8x = [&](uint32_t vb, uint32_t (&pk8)[2][4]) __attribute__((always_inline)) {
+            uint32_t ba[4], bb[4];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const auto r = __builtin_amdgcn_permlane16_swap(pk8[0][kb], pk8[1][kb], false, false);
+                ba[kb] = r[0];
+                bb[kb] = r[1];
+            }
+            const i32x8 bop = {static_cast<int>(ba[0]), static_cast<int>(ba[1]), static_cast<int>(ba[2]),
+                               static_cast<int>(ba[3]), static_cast<int>(bb[0]), static_cast<int>(bb[1]),
+                               static_cast<int>(bb[2]), static_cast<int>(bb[3])};
+            u32x2 va[2][4];            // [stage][rd]
+            auto rd = [&](auto CBT, int st) __attribute__((always_inline)) {
+                const uint32_t ad = vb + ov8[decltype(CBT)::value];
+                va[st][0] = lds_tr8<0>(ad);
+                va[st][1] = lds_tr8<32 * RS8>(ad);
+                va[st][2] = lds_tr8<4 * RS8>(ad);
+                va[st][3] = lds_tr8<36 * RS8>(ad);
+            };
+            rd(std::integral_constant<int, 0>{}, 0);
+            static_for<4>([&](auto CBT) __attribute__((always_inline)) {
+                constexpr int cbk = decltype(CBT)::value, st = cbk & 1;
+                lds_wait(va[st][0], va[st][1], va[st][2], va[st][3]);
+                if constexpr (cbk + 1 < 4) rd(std::integral_constant<int, cbk + 1>{}, st ^ 1);
+                const i32x8 aop = {static_cast<int>(va[st][0][0]), static_cast<int>(va[st][0][1]),
+                                   static_cast<int>(va[st][1][0]), static_cast<int>(va[st][1][1]),
+                                   static_cast<int>(va[st][2][0]), static_cast<int>(va[st][2][1]),
+                                   static_cast<int>(va[st][3][0]), static_cast<int>(va[st][3][1])};
+                acc32[cbk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, bop, acc32[cbk], 0, 0, 0, 127, 0, 127);
+            });
+        };
+
         // one run: tiles [t0, t1) of kind KIND
         float sc_next = 0.0f;      // k_scale of the next rest tile (vector load, a tile ahead)
         auto run = [&](auto KT, int t0, int t1) __attribute__((always_inline)) {
@@ -1404,8 +1271,15 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                     ssc = qks > 0.0f ? qks : 1.0f;
                 }
                 u32x4 pw[2][2];
-                softmax16(ssc, s, pw);
-                pv16(vbase[par], pw);
+                if constexpr (PV8) {
+                    uint32_t pk8[2][4];
+                    softmax8(KT, ssc, s, pk8, pw);
+                    if constexpr (KIND == T_REST) pv8x(vbase[par], pk8);
+                    else pvh32(vbase[par], pw);
+                } else {
+                    softmax16(ssc, s, pw);
+                    pv16(vbase[par], pw);
+                }
             }
         };
         {
@@ -1428,21 +1302,43 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         run(std::integral_constant<int, T_WIN>{}, nrt + nvt, ntiles);
     }
 
+
     // ---- epilogue: O = acc / l (x vscale in fp8 mode) ------------------------------
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-        const float l = PV8 ? quad_sum(l_run[sb]) : lsum[sb][0];
-        const float inv = 1.0f / l;
-        const int row = BM * blk + 32 * w + 16 * sb + c16;
+    if constexpr (PV8) {
+        // lane l: row l % 32 of the wavefront (row c of sub-block (l >> 4) & 1),
+        // channels 32 cbk + 8 i4 + 4 (l >> 5) + 0..3
+        const float l0 = quad_sum(l_run[0]), l1 = quad_sum(l_run[1]);
+        const float inv = 1.0f / (((lane >> 4) & 1) ? l1 : l0);
+        const int row = BM * blk + 32 * w + (lane & 31);
         if (row < a.N) {
             uint16_t* orow = a.out + b * a.o_b + h * a.o_h + static_cast<int64_t>(row) * a.o_n;
 #pragma unroll
-            for (int cb = 0; cb < 8; ++cb) {
-                f32x4 o4 = acc[sb][cb] * inv;
-                if (PV8) o4 *= *reinterpret_cast<const f32x4*>(a.vscale + bhk * PD + 16 * cb + 4 * g);
-                const u32x2 o = a.f16 ? u32x2{pack_f16x2(o4[0], o4[1]), pack_f16x2(o4[2], o4[3])}
-                                      : u32x2{pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3])};
-                *reinterpret_cast<u32x2*>(orow + 16 * cb + 4 * g) = o;
+            for (int cbk = 0; cbk < 4; ++cbk)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const int ch = 32 * cbk + 8 * i4 + 4 * (lane >> 5);
+                    const f32x4 vs = *reinterpret_cast<const f32x4*>(a.vscale + bhk * PD + ch);
+                    f32x4 o4 = {acc32[cbk][4 * i4], acc32[cbk][4 * i4 + 1], acc32[cbk][4 * i4 + 2], acc32[cbk][4 * i4 + 3]};
+                    o4 = o4 * inv * vs;
+                    const u32x2 o = a.f16 ? u32x2{pack_f16x2(o4[0], o4[1]), pack_f16x2(o4[2], o4[3])}
+                                          : u32x2{pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3])};
+                    *reinterpret_cast<u32x2*>(orow + ch) = o;
+                }
+        }
+    } else {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            const float inv = 1.0f / lsum[sb][0];
+            const int row = BM * blk + 32 * w + 16 * sb + c16;
+            if (row < a.N) {
+                uint16_t* orow = a.out + b * a.o_b + h * a.o_h + static_cast<int64_t>(row) * a.o_n;
+#pragma unroll
+                for (int cb = 0; cb < 8; ++cb) {
+                    const f32x4 o4 = acc[sb][cb] * inv;
+                    const u32x2 o = a.f16 ? u32x2{pack_f16x2(o4[0], o4[1]), pack_f16x2(o4[2], o4[3])}
+                                          : u32x2{pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3])};
+                    *reinterpret_cast<u32x2*>(orow + 16 * cb + 4 * g) = o;
+                }
             }
         }
     }

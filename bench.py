@@ -452,7 +452,8 @@ def pmc_workload(dev):
     """Fixed workload for rocprofv3 --pmc passes: a 256 MiB device copy (the
     FETCH_SIZE / WRITE_SIZE calibration: it reads and writes 256 MiB), then 20
     eager config-1 decode steps, each over its own cache copy, then three
-    config-4 hybrid prefill calls at N = 32768 (int8 QK, fp16 P.V)."""
+    config-4 hybrid prefill calls at N = 32768 (int8 QK, fp16 P.V), two with
+    fp8 P.V and two with fp8 QK."""
     src_t = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst_t = torch.empty_like(src_t)
     for _ in range(3):
@@ -465,7 +466,7 @@ def pmc_workload(dev):
         run_decode(q, st, 4)
     torch.cuda.synchronize()
     del states
-    from hyquant_amd.sage_unified import sage_vertical_attention_v2
+    from hyquant_amd.sage_unified import sage_vertical_attention_v2, sage_vertical_attention_v2_fp8
     from hyquant_amd.vertical import compute_vertical_indices
     g = torch.Generator(device=dev).manual_seed(4)
     N, HQ, HKV, W = 32768, 32, 8, 128
@@ -476,6 +477,10 @@ def pmc_workload(dev):
     vidx = compute_vertical_indices(q, k, W, 0.05, kv_repeat=HQ // HKV)
     for _ in range(3):
         sage_vertical_attention_v2(q, k, v, vidx, window_size=W)
+    for _ in range(2):
+        sage_vertical_attention_v2(q, k, v, vidx, window_size=W, pv_mode="fp8")
+    for _ in range(2):
+        sage_vertical_attention_v2_fp8(q, k, v, vidx, window_size=W)
     torch.cuda.synchronize()
 
 

@@ -206,6 +206,35 @@ __device__ __forceinline__ float quad_sum(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Score maxima as plain v_max3_f32 / v_max_f32: fmaxf must quiet signalling
+// NaNs, so the compiler puts a v_max_f32 x, x in front of every operand it
+// cannot prove canonical (MFMA results, masked selects).  The scores are
+// finite or -inf, never NaN.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float vmax2(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+// max of one sub-block's 16 scores of a tile (a tree of depth 3)
+__device__ __forceinline__ float tile_max16(const float (&v)[4][4]) {
+    const float a = vmax3(v[0][0], v[0][1], v[0][2]), b = vmax3(v[0][3], v[1][0], v[1][1]);
+    const float c = vmax3(v[1][2], v[1][3], v[2][0]), d = vmax3(v[2][1], v[2][2], v[2][3]);
+    const float e = vmax3(v[3][0], v[3][1], v[3][2]);
+    return vmax2(vmax3(a, b, c), vmax3(d, e, v[3][3]));
+}
+// max over the four lanes c, c+16, c+32, c+48 with the same plain maxima
+__device__ __forceinline__ float quad_max_raw(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = vmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return vmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // OCP e4m3 (gfx950 conversion, RNE), saturated to +-448 first
 __device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d) {
     auto cl = [](float x) { return fminf(fmaxf(x, -FP8_MAX), FP8_MAX); };
@@ -1035,12 +1064,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         auto softmax16 = [&](float ssc, float (&s)[2][4][4], u32x4 (&pw)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
             for (int sb = 0; sb < 2; ++sb) {
-                float mx = s[sb][0][0];
-#pragma unroll
-                for (int kbk = 0; kbk < 4; ++kbk)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[sb][kbk][r]);
-                mx = quad_max(mx) * ssc;
+                const float mx = quad_max_raw(tile_max16(s[sb])) * ssc;
                 if (__builtin_amdgcn_ballot_w64(mx > m_run[sb] + PF_SLACK)) {
                     const float mnew = fmaxf(m_run[sb], mx);
                     const float alpha = __builtin_amdgcn_exp2f(m_run[sb] - mnew);
@@ -1106,12 +1130,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             bool resc = false;
 #pragma unroll
             for (int sb = 0; sb < 2; ++sb) {
-                float mx = s[sb][0][0];
-#pragma unroll
-                for (int kbk = 0; kbk < 4; ++kbk)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[sb][kbk][r]);
-                mx = quad_max(mx) * ssc;
+                const float mx = quad_max_raw(tile_max16(s[sb])) * ssc;
                 if (__builtin_amdgcn_ballot_w64(mx > m_run[sb])) {
                     const float mnew = fmaxf(m_run[sb], mx);
                     alpha[sb] = __builtin_amdgcn_exp2f(m_run[sb] - mnew);

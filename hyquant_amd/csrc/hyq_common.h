@@ -49,6 +49,45 @@ __device__ __forceinline__ float quot_rn(float v, float sf, float inv) {
     return __builtin_fmaf(r, inv, q);
 }
 
+// Scale and codes of one row of the K/V quantisers (bit-exact contract:
+// s16 = fp16(amax / qmax), sf = fp32(s16), code = clamp(RNE(x / sf),
+// -qmax - 1, qmax), amax already clamped at 1e-5), without IEEE divisions:
+//   - fp16(amax * RN(1 / qmax)) equals fp16(amax / qmax) for every 16-bit amax
+//     (all positive bf16 and fp16 patterns, clamped at 1e-5) and qmax = 7, 127
+//     (checked exhaustively on the GPU; qmax = 1 is exact);
+//   - RN(1 / sf) is v_rcp_f32(sf) with one Newton step for every finite fp16
+//     sf (checked exhaustively on the GPU; the raw v_rcp_f32 differs for 2746
+//     of the 31743 scales);
+//   - x / sf by quot_rn, and the IEEE division where sf overflowed fp16;
+//   - RNE(q) is the integer in the low mantissa bits of q + 1.5 * 2^23 (exact
+//     for |q| < 2^22; here |q| <= 128), clamped as that bit pattern, whose
+//     low NBITS bits are the two's-complement code.
+// pat[i] holds code i in its low NBITS bits.
+template <int NBITS>
+__device__ __forceinline__ void quant_row_codes(const float (&v)[8], float amax, _Float16& s16, uint32_t (&pat)[8]) {
+    constexpr int QMAX = (1 << (NBITS - 1)) - 1;
+    constexpr int QMIN = -(1 << (NBITS - 1));
+    constexpr float RQ = 1.0f / static_cast<float>(QMAX);     // RN(1 / qmax), folded at compile time
+    constexpr int MAGIC = 0x4B400000;                          // bits of 1.5 * 2^23
+    s16 = static_cast<_Float16>(amax * RQ);
+    const float sf = static_cast<float>(s16);
+    float q[8];
+    if (sf <= 65504.0f) {
+        const float r0 = __builtin_amdgcn_rcpf(sf);
+        const float inv = __builtin_fmaf(__builtin_fmaf(-sf, r0, 1.0f), r0, r0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = quot_rn(v[i], sf, inv);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = v[i] / sf;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int t = __float_as_int(q[i] + 12582912.0f);
+        pat[i] = static_cast<uint32_t>(min(max(t, MAGIC + QMIN), MAGIC + QMAX));
+    }
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }

@@ -23,8 +23,6 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(
     const uint16_t* __restrict__ x, int64_t n, int64_t total, int lpt_log2,
     int64_t xs_bh, int64_t xs_n, int8_t* __restrict__ packed, int64_t ps_bh, int64_t ps_n,
     uint16_t* __restrict__ scale, int64_t ss_bh) {
-    constexpr int QMAX = (1 << (NBITS - 1)) - 1;
-    constexpr int QMIN = -(1 << (NBITS - 1));
     const int lpt = 1 << lpt_log2;                 // lanes per token
     const int lane = threadIdx.x & 63;
     const int sub = lane & (lpt - 1);              // lane within its token group
@@ -57,27 +55,9 @@ __global__ __launch_bounds__(256) void quant_pack_kernel(
         for (int m = 1; m < lpt; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
     }
     amax = fmaxf(amax, 1e-5f);
-    const float s32 = amax / static_cast<float>(QMAX);
-    const _Float16 s16 = static_cast<_Float16>(s32);
-    const float sf = static_cast<float>(s16);
-    // x / sf: the fma form for every finite scale, the IEEE division when the
-    // scale overflowed fp16 (sf = inf, where the residual would be inf * 0)
-    float q[8];
-    if (sf <= 65504.0f) {
-        const float inv = 1.0f / sf;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = quot_rn(v[i], sf, inv);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = v[i] / sf;
-    }
-    int c[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        float r = rintf(q[i]);
-        r = fminf(fmaxf(r, static_cast<float>(QMIN)), static_cast<float>(QMAX));
-        c[i] = static_cast<int>(r);
-    }
+    _Float16 s16;
+    uint32_t c[8];                                  // code i in the low NBITS bits
+    quant_row_codes<NBITS>(v, amax, s16, c);
     if (!valid) return;
     int8_t* prow = packed + ib * ps_bh + in * ps_n;
     if (NBITS == 4) {

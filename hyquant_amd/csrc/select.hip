@@ -524,8 +524,6 @@ constexpr int CQ_UNROLL = 4;                // tokens per 16-lane group per pass
 // amax reduction; only the stores depend on `store`.
 template <int NBITS>
 __device__ __forceinline__ void quant_row_group(uint4 raw, int8_t* dst, uint16_t* scl, int sub, bool store, bool f16) {
-    constexpr int QMAX = (1 << (NBITS - 1)) - 1;
-    constexpr int QMIN = -(1 << (NBITS - 1));
     float v[8];
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
@@ -538,27 +536,9 @@ __device__ __forceinline__ void quant_row_group(uint4 raw, int8_t* dst, uint16_t
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
     amax = max16_dpp(amax);
     amax = fmaxf(amax, 1e-5f);
-    const float s32 = amax / static_cast<float>(QMAX);
-    const _Float16 s16 = static_cast<_Float16>(s32);
-    const float sf = static_cast<float>(s16);
-    // x / sf: the fma form for every finite scale, the IEEE division when the
-    // scale overflowed fp16 (sf = inf, where the residual would be inf * 0)
-    float q[8];
-    if (sf <= 65504.0f) {
-        const float inv = 1.0f / sf;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = quot_rn(v[i], sf, inv);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = v[i] / sf;
-    }
-    int c[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        float r = rintf(q[i]);
-        r = fminf(fmaxf(r, static_cast<float>(QMIN)), static_cast<float>(QMAX));
-        c[i] = static_cast<int>(r);
-    }
+    _Float16 s16;
+    uint32_t c[8];                                  // code i in the low NBITS bits
+    quant_row_codes<NBITS>(v, amax, s16, c);
     if (!store) return;
     if (NBITS == 4) {
         uint32_t word = 0;

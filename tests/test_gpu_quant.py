@@ -103,6 +103,40 @@ def test_quant_every_bf16_value_bit_exact(nbits):
 
 
 @pytest.mark.parametrize("nbits", [4, 2, 8])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_quant_every_amax_bit_exact(nbits, dtype):
+    """One token per positive finite 16-bit value a (every bf16, or every
+    fp16 including subnormals), whose largest magnitude is a: the scale
+    fp16(amax / qmax) and its reciprocal are formed without IEEE divisions
+    in the kernel (a product with RN(1 / qmax), v_rcp_f32 with a Newton
+    step), so every reachable amax and scale is compared with the oracle's
+    IEEE arithmetic, codes included (the other channels are random values
+    in [-a, a])."""
+    rng = np.random.default_rng(500 + nbits + (dtype == "fp16"))
+    D = 128
+    if dtype == "bf16":
+        a = (np.arange(1, 0x7F80, dtype=np.uint32) << 16).view(np.float32)
+    else:
+        a = np.arange(1, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    x = rng.uniform(-1.0, 1.0, (len(a), D)).astype(np.float32) * a[:, None]
+    x[:, rng.integers(0, D)] = a
+    x[::2, 0] = -a[::2]                                # negative amax on half of the tokens
+    if dtype == "bf16":
+        x = O.bf16_round(x)
+        xd = to_dev_bf16(x[None], "cuda")
+    else:
+        x = x.astype(np.float16).astype(np.float32)
+        xd = torch.from_numpy(x[None].astype(np.float16)).cuda()
+    print(f"quant every amax nbits={nbits} {dtype} tokens={len(a)}", flush=True)
+    import hyquant_amd as hq
+    packed, scale = hq.quantize_per_token(xd, nbits)
+    torch.cuda.synchronize()
+    rp, rs = O.quantize_per_token(x[None], nbits)
+    assert np.array_equal(scale.cpu().numpy().view(np.uint16), rs.view(np.uint16))
+    assert np.array_equal(packed.cpu().numpy(), rp)
+
+
+@pytest.mark.parametrize("nbits", [4, 2, 8])
 def test_quant_pack_fp16_input_bit_exact(nbits):
     """quantize_per_token on fp16 tokens (src/ops/decode_d_stage.py:50-77
     takes bf16 or fp16: x.float() is exact for both): codes, bytes and scales

@@ -81,10 +81,16 @@ __device__ __forceinline__ void quant_row_codes(const float (&v)[8], float amax,
 #pragma unroll
         for (int i = 0; i < 8; ++i) q[i] = v[i] / sf;
     }
+    // The clamp only binds for 8 bits.  With qmax = 7 or 1, |x| <= amax and
+    // amax >= 1e-5, sf is at most 2.1% below amax / qmax (fp16 subnormal
+    // steps of 2^-24 against amax / qmax >= 1.43e-6, or 2^-11 relative for
+    // normal scales; an overflowing scale gives q = 0), so |q| < 7.15 (int4)
+    // or < 1.01 (int2) and RNE(q) is already within [qmin, qmax].  With
+    // qmax = 127 a subnormal sf can leave q near 168.
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int t = __float_as_int(q[i] + 12582912.0f);
-        pat[i] = static_cast<uint32_t>(min(max(t, MAGIC + QMIN), MAGIC + QMAX));
+        pat[i] = static_cast<uint32_t>(NBITS == 8 ? min(max(t, MAGIC + QMIN), MAGIC + QMAX) : t);
     }
 }
 

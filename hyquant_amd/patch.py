@@ -134,6 +134,23 @@ def handle_d_stage_cache(layer_idx: int, past_key_values: Any, query_states: tor
     return key_states, value_states
 
 
+def resolve_attention_interface(config: Any, eager_fn, *, output_attentions: bool = False):
+    """The HF attention backend the dense path calls (src/patch/_common.py:102-121):
+    the model's `_attn_implementation` looked up in transformers' registry of
+    attention functions, falling back to the family's eager forward when the
+    implementation is eager, unknown or unavailable, or when attention
+    weights are requested from sdpa (some transformers versions cannot
+    return them)."""
+    impl = getattr(config, "_attn_implementation", None) or "eager"
+    if impl == "eager" or (impl == "sdpa" and output_attentions):
+        return eager_fn
+    try:
+        from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    except Exception:
+        return eager_fn
+    return ALL_ATTENTION_FUNCTIONS.get(impl, eager_fn)
+
+
 def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
     """Exact causal attention, q [B, H_q, N, D], k/v [B, H_kv, N, D] (GQA-native):
     the hybrid kernel with every key inside the window (fp16 QK and P.V)."""
@@ -221,7 +238,9 @@ def build_attention_forward(family: str, *, mode: str, window_size: int, top_rat
         if mode == "dense" or (q_len == 1 and not d_mode):
             if attention_mask is not None and attention_mask.ndim == 4:
                 attention_mask = attention_mask[:, :, :, : k.shape[-2]]
-            out, attn_weights = eager_attention_forward(
+            attend = resolve_attention_interface(getattr(self, "config", None), eager_attention_forward,
+                                                 output_attentions=output_attentions)
+            out, attn_weights = attend(
                 self, q, k, v, attention_mask, dropout=0.0, scaling=getattr(self, "scaling", q.shape[-1] ** -0.5),
                 sliding_window=getattr(self, "sliding_window", None), **kwargs)
         else:

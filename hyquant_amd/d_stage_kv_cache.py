@@ -237,8 +237,22 @@ class DStageLayerCache:
         return self._seq_len
 
 
+def _per_layer(spec, layer_idx: int) -> int:
+    """A bit width given as one int for every layer or as a function of the layer index."""
+    return int(spec(layer_idx)) if callable(spec) else int(spec)
+
+
 class DStageKVCache(_HF_Cache):
-    """HF-compatible cache with D-stage quantisation (src/ops/d_stage_kv_cache.py:360-491)."""
+    """HF `Cache` of D-stage layers, the drop-in for src/ops/d_stage_kv_cache.py:360-491.
+
+    Each layer is a `DStageLayerCache`: bf16 K/V while the prompt is
+    prefilled, then (after its `freeze`) the four decode segments, with
+    decode-step tokens appended to the bf16 staging segment.  The HF
+    protocol surface is what `generate()` touches: `update`,
+    `get_seq_length`, `get_mask_sizes`, `get_max_cache_shape`, `reset`,
+    indexing and iteration per layer.  Beam search is not supported (its
+    batch re-indexing methods raise), and `crop` leaves the cache as it is:
+    the quantised segments are never shortened."""
 
     is_compileable = False
 
@@ -246,51 +260,80 @@ class DStageKVCache(_HF_Cache):
                  window_size: int = 256, top_ratio: float = 0.05, use_vert: bool = True):
         # transformers 5.x wants an explicit (here empty) layer list; 4.x takes
         # no arguments; without transformers the base is `object`
-        try:
-            super().__init__(layers=[])
-        except TypeError:
+        for kwargs in ({"layers": []}, {}):
             try:
-                super().__init__()
+                super().__init__(**kwargs)
+                break
             except TypeError:
-                pass
+                continue
         self.num_layers = num_layers
         self.window_size = window_size
         self.top_ratio = top_ratio
         self.use_vert = use_vert
-        k_bits_fn = k_bits if callable(k_bits) else (lambda i, _kb=k_bits: _kb)
-        self._layers = [DStageLayerCache(i, k_bits_fn(i), v_bits_fn(i), window_size, top_ratio, use_vert)
-                        for i in range(num_layers)]
+        self._bits = [(_per_layer(k_bits, i), _per_layer(v_bits_fn, i)) for i in range(num_layers)]
+        self._layers = [self._new_layer(i) for i in range(num_layers)]
         self._seen_tokens = 0
+
+    def _new_layer(self, i: int) -> DStageLayerCache:
+        kb, vb = self._bits[i]
+        return DStageLayerCache(i, kb, vb, self.window_size, self.top_ratio, self.use_vert)
+
+    # -- HF Cache protocol ---------------------------------------------------
 
     def update(self, key_states, value_states, layer_idx: int, cache_kwargs: Optional[dict[str, Any]] = None):
         layer = self._layers[layer_idx]
         if layer.phase == "prefill":
-            result = layer.update_prefill(key_states, value_states)
-            if layer_idx == 0:
-                self._seen_tokens = layer.get_seq_length()
-            return result
-        layer.append_staging(key_states, value_states)
-        if layer_idx == 0:
+            out = layer.update_prefill(key_states, value_states)
+        else:                           # a decode step: the token joins the bf16 staging segment
+            layer.append_staging(key_states, value_states)
+            out = (key_states, value_states)
+        if layer_idx == 0:              # HF reads the running token count from layer 0
             self._seen_tokens = layer.get_seq_length()
-        return key_states, value_states
+        return out
 
     def get_seq_length(self, layer_idx: int = 0) -> int:
-        return self._layers[layer_idx].get_seq_length() if layer_idx < len(self._layers) else 0
+        if 0 <= layer_idx < len(self._layers):
+            return self._layers[layer_idx].get_seq_length()
+        return 0
 
     def get_max_cache_shape(self) -> int:
-        return -1
-
-    def reset(self):
-        for layer in self._layers:
-            layer.__init__(layer.layer_idx, layer.k_bits, layer.v_bits, layer.window_size, layer.top_ratio,
-                           layer.use_vert)
-        self._seen_tokens = 0
+        return -1                       # no fixed capacity
 
     def get_mask_sizes(self, query_length: int, layer_idx: int = 0) -> Tuple[int, int]:
-        kv_length = self.get_seq_length(layer_idx)
-        if kv_length == 0:
-            return query_length, 0
-        return kv_length, max(0, kv_length - query_length)
+        """(kv_length, kv_offset) for HF's causal-mask construction."""
+        kv = self.get_seq_length(layer_idx)
+        return (query_length, 0) if kv == 0 else (kv, max(0, kv - query_length))
+
+    def reset(self):
+        self._layers = [self._new_layer(i) for i in range(self.num_layers)]
+        self._seen_tokens = 0
+
+    def crop(self, max_length: int):
+        pass
+
+    def batch_repeat_interleave(self, repeats: int):
+        raise NotImplementedError("beam search is not supported by DStageKVCache")
+
+    def batch_select_indices(self, indices: torch.Tensor):
+        raise NotImplementedError("beam search is not supported by DStageKVCache")
+
+    def __len__(self) -> int:
+        return self.num_layers
+
+    def __getitem__(self, idx: int):
+        """The bf16 prompt K/V of a layer still in prefill, else (None, None)."""
+        layer = self._layers[idx]
+        if layer.phase == "prefill" and layer._keys is not None:
+            return layer._keys, layer._values
+        return None, None
+
+    def __iter__(self):
+        return (self[i] for i in range(len(self._layers)))
+
+    def __bool__(self) -> bool:
+        return True                     # an empty cache is still a cache to generate()
+
+    # -- this implementation -------------------------------------------------
 
     def get_layer(self, layer_idx: int) -> DStageLayerCache:
         return self._layers[layer_idx]
@@ -310,31 +353,6 @@ class DStageKVCache(_HF_Cache):
         """Read a file written by save() onto `device` (default: the current GPU)."""
         from .cache_io import load_cache
         return load_cache(path, device)
-
-    def batch_repeat_interleave(self, repeats: int):
-        raise NotImplementedError("DStageKVCache does not support beam search yet.")
-
-    def batch_select_indices(self, indices: torch.Tensor):
-        raise NotImplementedError("DStageKVCache does not support beam search yet.")
-
-    def crop(self, max_length: int):
-        pass
-
-    def __len__(self) -> int:
-        return self.num_layers
-
-    def __getitem__(self, idx: int):
-        layer = self._layers[idx]
-        if layer.phase == "prefill" and layer._keys is not None:
-            return layer._keys, layer._values
-        return None, None
-
-    def __iter__(self):
-        for i in range(len(self._layers)):
-            yield self[i]
-
-    def __bool__(self) -> bool:
-        return True
 
 
 QuantizedKVCache = DStageKVCache

@@ -719,18 +719,26 @@ __device__ __forceinline__ void merge_head_cols(const MergeArgs& a, int head, fl
     }
     if (t == 0) lds[ZERO_SLOT] = 0.f;
     __syncthreads();
-    for (int g = wave; g < G; g += WAVES) {
+    // one 16-lane row per query head (heads 4 w .. 4 w + 3 on wavefront w,
+    // then 16 more per pass), lane j of the row taking partials j, j + 16, ...:
+    // every head's max and denominator at once, by 16-lane DPP reductions
+    const int seg = lane >> 4, jl = lane & 15;
+    for (int g0 = 4 * wave; g0 < G; g0 += 4 * WAVES) {
+        const int g = g0 + seg;
+        const bool gv = g < G;
         float M = M_INIT;
-        for (int p = lane; p < P; p += 64) M = fmaxf(M, lds[(p * G + g) * 2]);
-        M = wave_max64(M);
+        if (gv)
+            for (int p = jl; p < P; p += 16) M = fmaxf(M, lds[(p * G + g) * 2]);
+        M = max16_dpp(M);
         float den = 0.f;
-        for (int p = lane; p < P; p += 64) {
-            const float w = fast_exp2(lds[(p * G + g) * 2] - M);
-            den += w * lds[(p * G + g) * 2 + 1];
-            lds[(p * G + g) * 2] = w;
-        }
-        den = wave_sum64(den);
-        if (lane == 0) lds[ML_LDS + g] = den;
+        if (gv)
+            for (int p = jl; p < P; p += 16) {
+                const float w = fast_exp2(lds[(p * G + g) * 2] - M);
+                den += w * lds[(p * G + g) * 2 + 1];
+                lds[(p * G + g) * 2] = w;
+            }
+        den = sum16_dpp(den);
+        if (gv && jl == 0) lds[ML_LDS + g] = den;
     }
     __syncthreads();
     // 3. weighted sums in item order

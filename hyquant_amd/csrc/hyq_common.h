@@ -36,6 +36,20 @@ __device__ __forceinline__ float max16_dpp(float v) {
     return v;
 }
 
+// sum over each aligned group of 16 lanes, the same four steps (each adds
+// the value of a disjoint lane set: the pair, the other pair of the quad,
+// the other quad of the half-row, the other half-row)
+__device__ __forceinline__ float sum16_dpp(float v) {
+    auto dpp = [](float x, auto ctrl) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+    };
+    v += dpp(v, std::integral_constant<int, 0xb1>{});
+    v += dpp(v, std::integral_constant<int, 0x4e>{});
+    v += dpp(v, std::integral_constant<int, 0x141>{});
+    v += dpp(v, std::integral_constant<int, 0x140>{});
+    return v;
+}
+
 // The correctly rounded fp32 quotient v / sf of a quantiser (finite sf > 0,
 // |v| <= 128 sf) from inv = RN(1 / sf) computed once per row: q = RN(v inv),
 // the residual r = v - q sf (exact by fma) and one fma correction

@@ -1064,8 +1064,13 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         auto softmax16 = [&](float ssc, float (&s)[2][4][4], u32x4 (&pw)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
             for (int sb = 0; sb < 2; ++sb) {
-                const float mx = quad_max_raw(tile_max16(s[sb])) * ssc;
-                if (__builtin_amdgcn_ballot_w64(mx > m_run[sb] + PF_SLACK)) {
+                // the test needs no cross-lane max: m_run is the same on the
+                // four lanes of a row and ssc > 0, so some lane's own max
+                // passes it exactly when the row max does; the row max is
+                // formed only when the running max moves
+                const float lmx = tile_max16(s[sb]) * ssc;
+                if (__builtin_amdgcn_ballot_w64(lmx > m_run[sb] + PF_SLACK)) {
+                    const float mx = quad_max_raw(lmx);
                     const float mnew = fmaxf(m_run[sb], mx);
                     const float alpha = __builtin_amdgcn_exp2f(m_run[sb] - mnew);
                     lsum[sb] *= alpha;
@@ -1130,8 +1135,9 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             bool resc = false;
 #pragma unroll
             for (int sb = 0; sb < 2; ++sb) {
-                const float mx = quad_max_raw(tile_max16(s[sb])) * ssc;
-                if (__builtin_amdgcn_ballot_w64(mx > m_run[sb])) {
+                const float lmx = tile_max16(s[sb]) * ssc;        // as in softmax16
+                if (__builtin_amdgcn_ballot_w64(lmx > m_run[sb])) {
+                    const float mx = quad_max_raw(lmx);
                     const float mnew = fmaxf(m_run[sb], mx);
                     alpha[sb] = __builtin_amdgcn_exp2f(m_run[sb] - mnew);
                     l_run[sb] *= alpha[sb];

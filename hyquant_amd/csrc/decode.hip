@@ -190,12 +190,17 @@ __device__ __forceinline__ constexpr int krow_token(int i) { return 4 * (i & 3) 
 // holds p = exp2(s - m) relative to the (possibly raised) running max.
 template <int N>
 __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[N], bool has_ones) {
+    // this lane's max (plain v_max3 steps), tested against the running max
+    // on its own: st.m is the same on the four lanes of a column, so some
+    // lane passes exactly when the column max does, and the column max (two
+    // row swaps) is formed only when the running max moves
     float mx = s[0];
+    int e = 1;
 #pragma unroll
-    for (int e = 1; e < N; ++e) mx = fmaxf(mx, s[e]);
-    mx = col_max(mx);
-    const bool need = mx > st.m + RESCALE_SLACK;
-    if (__builtin_amdgcn_ballot_w64(need)) {             // rare after the first group
+    for (; e + 1 < N; e += 2) mx = vmax3(mx, s[e], s[e + 1]);
+    if (e < N) mx = vmax2(mx, s[e]);
+    if (__builtin_amdgcn_ballot_w64(mx > st.m + RESCALE_SLACK)) {   // rare after the first group
+        mx = col_max(mx);
         const float mnew = fmaxf(st.m, mx);
         const float alpha = fast_exp2(st.m - mnew);
         st.l *= alpha;

@@ -36,6 +36,21 @@ __device__ __forceinline__ float max16_dpp(float v) {
     return v;
 }
 
+// Score maxima as plain v_max3_f32 / v_max_f32: fmaxf must quiet signalling
+// NaNs, so the compiler puts a v_max_f32 x, x in front of every operand it
+// cannot prove canonical (MFMA results, masked selects).  Attention scores
+// are finite or -inf, never NaN.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float vmax2(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // sum over each aligned group of 16 lanes, the same four steps (each adds
 // the value of a disjoint lane set: the pair, the other pair of the quad,
 // the other quad of the half-row, the other half-row)

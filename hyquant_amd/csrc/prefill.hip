@@ -206,20 +206,6 @@ __device__ __forceinline__ float quad_sum(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Score maxima as plain v_max3_f32 / v_max_f32: fmaxf must quiet signalling
-// NaNs, so the compiler puts a v_max_f32 x, x in front of every operand it
-// cannot prove canonical (MFMA results, masked selects).  The scores are
-// finite or -inf, never NaN.
-__device__ __forceinline__ float vmax3(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-__device__ __forceinline__ float vmax2(float a, float b) {
-    float r;
-    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
 // max of one sub-block's 16 scores of a tile (a tree of depth 3)
 __device__ __forceinline__ float tile_max16(const float (&v)[4][4]) {
     const float a = vmax3(v[0][0], v[0][1], v[0][2]), b = vmax3(v[0][3], v[1][0], v[1][1]);

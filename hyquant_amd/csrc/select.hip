@@ -146,54 +146,90 @@ __global__ __launch_bounds__(QM_THREADS) void qmean_kernel(const uint16_t* __res
 // keys of one output row start 16-byte aligned
 __host__ __device__ inline int64_t key_pitch(int64_t P) { return (P + 7) / 8 * 8; }
 
-// One workgroup per 256 key rows of one (b, hk).  The query means (float64,
-// [GM][128]) sit in LDS and are read with same-address (broadcast) loads.
-// Each wavefront stages half-rows (64 channels) of its 64 rows through LDS
-// with coalesced 1 KB loads (pitch 144 B: the per-row reads hit every bank
-// once per 16 lanes), then lane r accumulates the GM dot products of row r
-// sequentially in channel order in float64.  GM is G rounded up to 1, 2, 4,
-// 8 or 16; the means are stored with zero rows past G, so the FMA loop has no
-// branches and only the key store skips heads g >= G.
-constexpr int SC_ROWS = 64;                 // rows per wavefront
+// Buffer descriptor over `bytes` bytes at `base`: loads past the range read
+// zeros without touching memory, so the score kernel's loads need no branch
+// (a branch around a load makes the compiler drain every load at the join).
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+constexpr int POL_NT = 2;                   // non-temporal: the K prefix is read once
+
+// One workgroup per SC_WG_ROWS key rows of one (b, hk); wavefront w takes the
+// 64-row blocks w, w + 4, ... of them.  The query means (float64, [GM][128])
+// are the same for every lane: they are read by scalar loads and enter each
+// FMA as an SGPR pair (read from LDS, every broadcast read moves 1 KB to the
+// registers, and the GM = 4 kernel was bound by LDS bandwidth).  A block is
+// streamed as two half-rows (64 channels, one 128-byte line per row): 8
+// lanes per row, 16 bytes each, one 1 KB non-temporal load per 8 rows, into
+// two register stages that are copied to the wavefront's LDS rows (pitch
+// 144 B: the per-row reads hit every bank once per 16 lanes) and reloaded at
+// once, so two half-blocks are in flight while lane r accumulates the GM dot products
+// of row r sequentially in channel order in float64.  GM is G rounded up to
+// 1, 2, 4, 8 or 16; the means are stored with zero rows past G, so the FMA
+// loop has no branches and only the key store skips heads g >= G.  Rows past
+// the prefix read zeros through the descriptor and are not stored.
+constexpr int SC_ROWS = 64;                 // rows per block
 constexpr int SC_PITCH = 144;               // LDS bytes per half-row (128 + 16)
+constexpr int SC_BLOCKS = 4;                // blocks per wavefront
+constexpr int SC_WG_ROWS = 4 * SC_BLOCKS * SC_ROWS;
 
 template <int GM, bool F16>
 __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__ k, int64_t ks_b, int64_t ks_h,
                                                     int64_t ks_n, int HK, int G, int64_t P, int64_t KP,
                                                     const double* __restrict__ qm, uint16_t* __restrict__ keys) {
-    __shared__ __align__(16) double s_q[GM * 128];
     __shared__ __align__(16) uint8_t s_rows[4][SC_ROWS * SC_PITCH];
     const int bh = blockIdx.y;                     // b * HK + hk
     const int b = bh / HK, hk = bh % HK;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const double* qg = qm + static_cast<int64_t>(bh) * GM * 128;
-    for (int i = threadIdx.x; i < GM * 128; i += 256) s_q[i] = qg[i];
-    const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 256 + wave * SC_ROWS;
-    const uint16_t* kb = k + b * ks_b + hk * ks_h;
-    uint8_t* lds = s_rows[wave];
-    // lane l loads 16-byte chunk (l & 7) of half-row `half` of rows p0 + 8i + (l >> 3)
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * SC_WG_ROWS;
+    const int nrows = static_cast<int>(min<int64_t>(SC_WG_ROWS, P - r0));
+    const uint32_t rowb = static_cast<uint32_t>(ks_n) * 2;          // bytes between rows (host: < 2^20)
+    const Rsrc rk = make_rsrc(k + b * ks_b + hk * ks_h + r0 * ks_n, static_cast<uint32_t>(nrows) * rowb);
+    // blocks of this wavefront that hold rows: wave, wave + 4, ... below nrows
+    const int nblk = (nrows + SC_ROWS - 1) / SC_ROWS;
+    const int mine = nblk > wave ? (nblk - wave + 3) / 4 : 0;
+    const int nst = 2 * mine;                      // half-block stages
+    // lane l loads 16-byte chunk (l & 7) of rows 8i + (l >> 3) of a half-block
     const int sub = lane & 7, rq = lane >> 3;
+    uint32_t vo[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vo[i] = static_cast<uint32_t>(8 * i + rq) * rowb + 16 * sub;
+    // stage s: block wave + 4 (s >> 1), half s & 1
+    auto soff = [&](int s) -> uint32_t {
+        return static_cast<uint32_t>((wave + 4 * (s >> 1)) * SC_ROWS) * rowb + 128u * (s & 1);
+    };
+    auto load = [&](uint4 (&r)[8], int s) {
+        const uint32_t so = soff(s);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, vo[i], so, POL_NT));
+        // keep the stages in issue order: the wait for a stage counts the
+        // loads issued after it, so interleaved stages would wait for each other
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    const double* qg = qm + static_cast<int64_t>(bh) * GM * 128;
+    if (nst == 0) return;                          // (nst is even: both first stages hold rows)
+    uint4 ra[8], rb[8];
+    load(ra, 0);
+    load(rb, 1);
+    uint8_t* lds = s_rows[wave];
     double acc[GM];
 #pragma unroll
     for (int g = 0; g < GM; ++g) acc[g] = 0.0;
-    __syncthreads();
-#pragma unroll 1
-    for (int half = 0; half < 2; ++half) {
-        uint4 raw[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int64_t p = min(p0 + 8 * i + rq, P - 1);
-            raw[i] = *reinterpret_cast<const uint4*>(kb + p * ks_n + 64 * half + 8 * sub);
-        }
-        // One wavefront writes and reads its own LDS rows; its LDS accesses
-        // execute in program order, so the writes of this half follow every
-        // read of the previous one and precede the reads below.
+    // One wavefront writes and reads its own LDS rows; its LDS accesses
+    // execute in program order, so a stage's writes follow every read of the
+    // previous stage and precede the reads of its own.
+    auto stage = [&](const uint4 (&r)[8]) {
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(lds + (8 * i + rq) * SC_PITCH + 16 * sub) = raw[i];
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(lds + (8 * i + rq) * SC_PITCH + 16 * sub) = r[i];
         __builtin_amdgcn_wave_barrier();
+    };
+    auto compute = [&](int s) {
         const uint8_t* row = lds + lane * SC_PITCH;
+        const int half = s & 1;
 #pragma unroll 1
         for (int c = 0; c < 8; ++c) {
             const uint4 w = *reinterpret_cast<const uint4*>(row + 16 * c);
@@ -207,18 +243,36 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
 #pragma unroll
             for (int g = 0; g < GM; ++g) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[g] = fma(s_q[g * 128 + d0 + j], kv[j], acc[g]);
+                for (int j = 0; j < 8; ++j) acc[g] = fma(qg[g * 128 + d0 + j], kv[j], acc[g]);
             }
         }
-    }
-    const int64_t p = p0 + lane;
-    if (p < P) {
+        if (half) {
+            const int64_t p = r0 + (wave + 4 * (s >> 1)) * SC_ROWS + lane;
+            if (p < P) {
 #pragma unroll
-        for (int g = 0; g < GM; ++g)
-            if (g < G)
-                keys[(static_cast<int64_t>(bh) * G + g) * KP + p] =
-                    static_cast<uint16_t>(orderable_key(f64_to_half_rne(acc[g], F16)));
+                for (int g = 0; g < GM; ++g)
+                    if (g < G)
+                        keys[(static_cast<int64_t>(bh) * G + g) * KP + p] =
+                            static_cast<uint16_t>(orderable_key(f64_to_half_rne(acc[g], F16)));
+            }
+#pragma unroll
+            for (int g = 0; g < GM; ++g) acc[g] = 0.0;
+        }
+    };
+    // Two register stages and the LDS rows: a stage's registers are reloaded
+    // as soon as they are copied to LDS, so the loads of the next two stages
+    // are in flight while one is computed (stages past nst lie past the
+    // descriptor's range: no memory access).  nst is even: no exit mid-loop,
+    // which keeps the compiler's wait counts exact.
+    for (int s = 0; s < nst; s += 2) {
+        stage(ra);
+        load(ra, s + 2);
+        compute(s);
+        stage(rb);
+        load(rb, s + 3);
+        compute(s + 1);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last (empty) loads retire before the wave ends
 }
 
 constexpr int TOPK_WAVES = TOPK_THREADS / 64;
@@ -723,6 +777,7 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
     if (tail <= 0 || tail > q_len) return fail(HYQ_EINVAL, "hyq_vertical_select: bad query tail");
     if (!q || !k || !out_idx) return fail(HYQ_EINVAL, "hyq_vertical_select: null pointer");
     if (!aligned(k, 16) || ks_n % 8 || ks_h % 8 || ks_b % 8) return fail(HYQ_EINVAL, "hyq_vertical_select: keys must be 16-byte aligned rows");
+    if (ks_n < 128 || ks_n > (1 << 20)) return fail(HYQ_ENOTSUP, "hyq_vertical_select: key row stride must be in [128, 2^20] elements");
     if (!aligned(q, 4) || qs_t % 2 || qs_h % 2 || qs_b % 2) return fail(HYQ_EINVAL, "hyq_vertical_select: query rows must be 4-byte aligned");
     const TopkPlan tp = topk_plan(p, top_k, topk_lds_budget());
     const SelectLayout L = select_layout(b, h_out, p, top_k, tp);
@@ -737,7 +792,7 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
                                                                                      group, hk, G, GP, is_fp16, qm);
     int rc = check_launch("hyq_vertical_select (mean)");
     if (rc) return rc;
-    const dim3 sgrid(static_cast<unsigned>((p + 255) / 256), static_cast<unsigned>(b * hk));
+    const dim3 sgrid(static_cast<unsigned>((p + SC_WG_ROWS - 1) / SC_WG_ROWS), static_cast<unsigned>(b * hk));
     auto score = [&](auto gm, auto f16) {
         score_kernel<decltype(gm)::value, decltype(f16)::value><<<sgrid, dim3(256), 0, s>>>(
             k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys);

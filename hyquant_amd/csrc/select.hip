@@ -15,7 +15,9 @@
 //                 in (score desc, index asc) order (the lower-index rule fixes
 //                 the unspecified tie order of torch.topk, src/patch/_common.py:189).
 // Kernels:
-//   qmean_kernel      one workgroup per (b, ho): channel pairs x tail slices.
+//   qmean16_kernel    one workgroup per (b, ho): 16-byte row chunks x tail slots
+//                     (qmean_kernel, channel pairs x tail slices, for query
+//                     rows that are not 16-byte aligned).
 //   score_kernel      one thread per key row, G output heads sharing the row
 //                     (GQA-native, the K prefix is read once); writes the
 //                     monotone 16-bit key of each bf16 score.
@@ -140,6 +142,91 @@ __global__ __launch_bounds__(QM_THREADS) void qmean_kernel(const uint16_t* __res
 #pragma unroll
         for (int k = 0; k < QM_SLICES; ++k) sum += s_sum[k][threadIdx.x];
         out[threadIdx.x] = half_bits_to_f64(f64_to_half_rne(sum / tail, f16), f16);
+    }
+}
+
+// The same means from 16-byte loads, for query rows that are 16-byte aligned
+// (every contiguous query tensor): 16 lanes hold one row (8 channels each),
+// THREADS / 16 rows per pass of the workgroup, so each load instruction reads
+// four whole rows.  The four row slots of a wavefront are added by lane
+// shuffles, the wavefronts' sums in LDS; as above, every partial sum is exact
+// in float64, so the result equals qmean_kernel's.  256 threads for the
+// per-query-head means (one workgroup per output head), 1024 for the group
+// means (a quarter as many workgroups, R heads read per row).
+
+__device__ __forceinline__ void add8_f64(double (&acc)[8], uint4 v, bool f16) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += half_bits_to_f64(static_cast<uint16_t>(w[i]), f16);
+        acc[2 * i + 1] += half_bits_to_f64(static_cast<uint16_t>(w[i] >> 16), f16);
+    }
+}
+
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void qmean16_kernel(const uint16_t* __restrict__ q, int64_t qs_b, int64_t qs_h,
+                                                            int64_t qs_t, int QL, int tail, int R, int HK, int G,
+                                                            int GP, int f16, double* __restrict__ qm) {
+    const int row = blockIdx.x;                    // (b, hk, g)
+    const int g = row % GP;
+    const int bhk = row / GP;
+    const int tid = threadIdx.x;
+    double* out = qm + static_cast<int64_t>(row) * 128;
+    if (g >= G) {
+        if (tid < 128) out[tid] = 0.0;
+        return;
+    }
+    constexpr int QV_SLOTS = THREADS / 16;
+    const int b = bhk / HK, ho = (bhk % HK) * G + g;
+    const int sub = tid & 15, slot = tid >> 4;
+    const uint16_t* base = q + b * qs_b + static_cast<int64_t>(ho * R) * qs_h + static_cast<int64_t>(QL - tail) * qs_t + 8 * sub;
+    auto ld = [&](int r, int t) { return *reinterpret_cast<const uint4*>(base + r * qs_h + static_cast<int64_t>(t) * qs_t); };
+    double acc[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+    if (R == 1) {
+        int t = slot;
+        for (; t + 3 * QV_SLOTS < tail; t += 4 * QV_SLOTS) {
+            uint4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = ld(0, t + u * QV_SLOTS);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) add8_f64(acc, v[u], f16);
+        }
+        for (; t < tail; t += QV_SLOTS) add8_f64(acc, ld(0, t), f16);
+    } else {
+        // the R heads of a row are averaged (one rounding to the model
+        // dtype), then the row means summed; two rows per pass
+        for (int t = slot; t < tail; t += 2 * QV_SLOTS) {
+            const int t1 = min(t + QV_SLOTS, tail - 1);
+            double g0[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0}, g1[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+            for (int r = 0; r < R; ++r) {
+                const uint4 v0 = ld(r, t), v1 = ld(r, t1);
+                add8_f64(g0, v0, f16);
+                add8_f64(g1, v1, f16);
+            }
+            const bool has1 = t + QV_SLOTS < tail;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                acc[i] += half_bits_to_f64(f64_to_half_rne(g0[i] / R, f16), f16);
+                if (has1) acc[i] += half_bits_to_f64(f64_to_half_rne(g1[i] / R, f16), f16);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        acc[i] += __shfl_xor(acc[i], 16, 64);
+        acc[i] += __shfl_xor(acc[i], 32, 64);
+    }
+    __shared__ double s_sum[THREADS / 64][128];
+    if ((tid & 63) < 16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s_sum[tid >> 6][8 * sub + i] = acc[i];
+    }
+    __syncthreads();
+    if (tid < 128) {
+        double sum = 0.0;
+#pragma unroll
+        for (int k = 0; k < THREADS / 64; ++k) sum += s_sum[k][tid];
+        out[tid] = half_bits_to_f64(f64_to_half_rne(sum / tail, f16), f16);
     }
 }
 
@@ -674,6 +761,8 @@ __global__ __launch_bounds__(256) void compact_quant_kernel(CompactArgs a) {
             const int64_t p = p0 + j0 + 16 * u;
             pp[u] = p;
             const int64_t pc = p < a.P ? p : a.P - 1;
+            // default cache policy: with non-temporal loads here the gather of
+            // the top-k and window rows that follows ran 1.7x slower
             kr[u] = *reinterpret_cast<const uint4*>(kbase + pc * a.ks_n);
             vr[u] = *reinterpret_cast<const uint4*>(vbase + pc * a.vs_n);
         }
@@ -788,8 +877,16 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
     uint16_t* keys = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + L.keys);
     void* gsel = static_cast<char*>(workspace) + L.gsel;
     const int GP = padded_heads(G);
-    qmean_kernel<<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(QM_THREADS), 0, s>>>(q, qs_b, qs_h, qs_t, q_len, tail,
-                                                                                     group, hk, G, GP, is_fp16, qm);
+    if (aligned(q, 16) && qs_t % 8 == 0 && qs_h % 8 == 0 && qs_b % 8 == 0) {
+        if (group == 1)
+            qmean16_kernel<256><<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(256), 0, s>>>(
+                q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm);
+        else
+            qmean16_kernel<1024><<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(1024), 0, s>>>(
+                q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm);
+    } else
+        qmean_kernel<<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(QM_THREADS), 0, s>>>(
+            q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm);
     int rc = check_launch("hyq_vertical_select (mean)");
     if (rc) return rc;
     const dim3 sgrid(static_cast<unsigned>((p + SC_WG_ROWS - 1) / SC_WG_ROWS), static_cast<unsigned>(b * hk));

@@ -37,6 +37,36 @@ def test_selector_prefill_variant_bit_exact(B, HQ, HK, QL, KL, W, rho):
     assert np.array_equal(got.cpu().numpy(), exp)
 
 
+@pytest.mark.parametrize("R", [1, 4])
+def test_selector_query_rows_not_16_byte_aligned(R):
+    """Query views whose rows are 4- but not 16-byte aligned take the
+    channel-pair mean kernel (qmean_kernel), contiguous ones the 16-byte one
+    (qmean16_kernel): both against the oracle, for the per-query-head (R = 1)
+    and the group-mean (R = kv_repeat) selector."""
+    from hyquant_amd.vertical import compute_vertical_indices, freeze_vertical_indices
+    rng = np.random.default_rng(11 + R)
+    B, HK, QL, P, W = 2, 2, 48, 700, 32
+    HQ = HK * (R if R > 1 else 4)
+    q = _rand_bf16(rng, (B, HQ, QL, 128))
+    k = _rand_bf16(rng, (B, HK, P, 128), 2.0)
+    wide = np.zeros((B, HQ, QL, 130), np.float32)
+    wide[..., 2:] = q
+    qv = to_dev_bf16(wide, "cuda")[..., 2:]           # row stride 130, base 4 bytes past 16-byte alignment
+    assert qv.data_ptr() % 16 != 0 and qv.stride(2) % 8 != 0
+    kd = to_dev_bf16(k, "cuda")
+    if R == 1:
+        exp = O.compute_vertical_indices(q, k, W, 0.1, kv_repeat=HQ // HK)
+        got_v = compute_vertical_indices(qv, kd, W, 0.1, kv_repeat=HQ // HK)
+        got_c = compute_vertical_indices(to_dev_bf16(q, "cuda"), kd, W, 0.1, kv_repeat=HQ // HK)
+    else:
+        tail = q[:, :, -W:]
+        exp = O.compute_vertical_indices(O.group_mean_query(tail, HK), k, W, 0.1)
+        got_v = freeze_vertical_indices(qv[:, :, -W:], kd, W, 0.1, R)
+        got_c = freeze_vertical_indices(to_dev_bf16(tail, "cuda"), kd, W, 0.1, R)
+    assert np.array_equal(got_v.cpu().numpy(), exp)
+    assert np.array_equal(got_c.cpu().numpy(), exp)
+
+
 def test_selector_ties_and_negative_zero():
     from hyquant_amd.vertical import compute_vertical_indices
     rng = np.random.default_rng(5)

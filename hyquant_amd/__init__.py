@@ -19,6 +19,13 @@ from .sage_unified import (  # noqa: F401
     sage_vertical_attention_v2_fp8,
 )
 from .vertical import compute_vertical_indices  # noqa: F401
+from .d_stage_cache import (  # noqa: F401
+    d_stage_decode_attention,
+    fused_decode_attention_k4v4,
+    legacy_dequantize,
+    splitk_decode_attention_k4v4,
+    splitk_decode_attention_k4v4_mma,
+)
 from .cache_io import load_cache, save_cache  # noqa: F401
 
 __all__ = [
@@ -35,4 +42,9 @@ __all__ = [
     "sage_vertical_attention_v2_fp8",
     "save_cache",
     "load_cache",
+    "legacy_dequantize",
+    "fused_decode_attention_k4v4",
+    "splitk_decode_attention_k4v4",
+    "splitk_decode_attention_k4v4_mma",
+    "d_stage_decode_attention",
 ]

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libhyq.so")
 
 # the hyq_abi_version() these bindings (struct layouts, argument lists) match
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 HYQ_DT_Q_FP16 = 1
 HYQ_DT_SEG_FP16 = 2
@@ -33,6 +33,7 @@ EXPORTS = (
     "hyq_abi_version",
     "hyq_quant_pack",
     "hyq_dequant",
+    "hyq_legacy_dequant",
     "hyq_decode_workspace_size",
     "hyq_decode_hybrid",
     "hyq_decode_hybrid_noalloc",
@@ -105,6 +106,9 @@ def _declare(lib):
     lib.hyq_dequant.restype = c_int
     lib.hyq_dequant.argtypes = [c_void_p, c_int64, c_int64, c_int32, c_int64, c_int64, c_int32,
                                 c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p]
+    lib.hyq_legacy_dequant.restype = c_int
+    lib.hyq_legacy_dequant.argtypes = [c_void_p, c_int64, c_int64, c_int32, c_int64, c_int64, c_int32,
+                                       c_void_p, c_int64, c_int64, c_int32, c_void_p, c_int64, c_int64, c_void_p]
     lib.hyq_decode_workspace_size.restype = c_size_t
     lib.hyq_decode_workspace_size.argtypes = [POINTER(DecodeParams)]
     lib.hyq_decode_hybrid.restype = c_int

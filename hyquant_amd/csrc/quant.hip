@@ -128,6 +128,65 @@ __global__ __launch_bounds__(256) void dequant_kernel(
     reinterpret_cast<uint4*>(out + ib * os_bh + in * os_n)[sub] = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// Dequantisation of the legacy decode format of src/ops/d_stage_cache.py
+// (the layout its fused / split-K kernels read, :281-373, :1019-1087):
+// offset-encoded unsigned codes, int4 with the even channel in the HIGH
+// nibble (value u - 8), int2 with channel 4k + i in bits 7-2i..6-2i (value
+// u - 1.5), and one fp16 scale per (group of `group` tokens, channel),
+// [bh, n / group, d].  out = bf16(fp32(u - offset) * fp32(scale)), RNE, as the
+// reference's (K_int * sk).to(tl.bfloat16) (:1041-1045); the product is exact
+// in fp32, and its sign is set explicitly (see dequant_kernel).  A lane owns
+// 8 channels of one token: the scale row's 16 bytes and the packed bytes in
+// one load each, 16 output bytes in one store.
+template <int NBITS>
+__global__ __launch_bounds__(256) void legacy_dequant_kernel(
+    const uint8_t* __restrict__ packed, int64_t n, int64_t total, int lpt_log2, int64_t ps_bh, int64_t ps_n,
+    const uint16_t* __restrict__ scale, int64_t ss_bh, int64_t ss_g, int group, uint16_t* __restrict__ out,
+    int64_t os_bh, int64_t os_n) {
+    const int lpt = 1 << lpt_log2;
+    const int sub = threadIdx.x & (lpt - 1);
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * (256 >> lpt_log2) + (threadIdx.x >> lpt_log2);
+    if (t >= total) return;
+    const int64_t ib = t / n, in = t - ib * n;
+    const uint8_t* prow = packed + ib * ps_bh + in * ps_n;
+    const uint4 sraw = reinterpret_cast<const uint4*>(scale + ib * ss_bh + (in / group) * ss_g)[sub];
+    const uint32_t sw[4] = {sraw.x, sraw.y, sraw.z, sraw.w};
+    // twice the signed value of channel 8 sub + c: 2u - 16 (int4) or 2u - 3 (int2)
+    int twice[8];
+    if constexpr (NBITS == 4) {
+        const uint32_t w = reinterpret_cast<const uint32_t*>(prow)[sub];   // channels 8sub .. 8sub+7
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t b = (w >> (8 * i)) & 0xffu;
+            twice[2 * i] = 2 * static_cast<int>(b >> 4) - 16;
+            twice[2 * i + 1] = 2 * static_cast<int>(b & 15u) - 16;
+        }
+    } else {
+        const uint32_t w = reinterpret_cast<const uint16_t*>(prow)[sub];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t b = (w >> (8 * i)) & 0xffu;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) twice[4 * i + j] = 2 * static_cast<int>((b >> (6 - 2 * j)) & 3u) - 3;
+        }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t h[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int c = 2 * j + e;
+            const uint32_t sb = (sw[j] >> (16 * e)) & 0xffffu;
+            const float mag = 0.5f * static_cast<float>(twice[c] < 0 ? -twice[c] : twice[c]) *
+                              f16_bits_to_f32(static_cast<uint16_t>(sb & 0x7fffu));
+            h[e] = f32_to_bf16_rne(mag) | ((twice[c] < 0 ? 0x8000u : 0u) ^ (sb & 0x8000u));
+        }
+        o[j] = h[0] | (h[1] << 16);
+    }
+    reinterpret_cast<uint4*>(out + ib * os_bh + in * os_n)[sub] = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 int lanes_log2(int d) {
     int l = 0;
     while ((1 << l) < d / 8) ++l;
@@ -212,4 +271,37 @@ extern "C" int hyq_dequant(const int8_t* packed, int64_t bh, int64_t n, int32_t 
         dequant_kernel<2><<<grid, block, 0, s>>>(packed, n, total, lpt_log2, p_stride_bh, p_stride_n, scale, s_stride_bh,
                                                  out, o_stride_bh, o_stride_n);
     return check_launch("hyq_dequant");
+}
+
+extern "C" int hyq_legacy_dequant(const uint8_t* packed, int64_t bh, int64_t n, int32_t d, int64_t p_stride_bh,
+                                  int64_t p_stride_n, int32_t nbits, const uint16_t* scale, int64_t s_stride_bh,
+                                  int64_t s_stride_g, int32_t group, uint16_t* out, int64_t o_stride_bh,
+                                  int64_t o_stride_n, void* stream) {
+    if (bh < 0 || n < 0) return fail(HYQ_EINVAL, "hyq_legacy_dequant: negative shape");
+    if (nbits != 2 && nbits != 4) return fail(HYQ_EINVAL, "hyq_legacy_dequant: nbits must be 2 or 4, got " + std::to_string(nbits));
+    if (!ok_dim(d)) return fail(HYQ_ENOTSUP, "hyq_legacy_dequant: head dim must be 8*2^k <= 512, got " + std::to_string(d));
+    if (group <= 0) return fail(HYQ_EINVAL, "hyq_legacy_dequant: group must be positive");
+    if (bh == 0 || n == 0) return HYQ_OK;
+    if (!packed || !scale || !out) return fail(HYQ_EINVAL, "hyq_legacy_dequant: null pointer");
+    const int pbytes = nbits;  // packed bytes per lane (8 channels)
+    if (!aligned(packed, pbytes) || p_stride_n % pbytes || p_stride_bh % pbytes)
+        return fail(HYQ_EINVAL, "hyq_legacy_dequant: packed input misaligned");
+    if (!aligned(scale, 16) || s_stride_g % 8 || s_stride_bh % 8)
+        return fail(HYQ_EINVAL, "hyq_legacy_dequant: scale rows must be 16-byte aligned with strides divisible by 8");
+    if (!aligned(out, 16) || o_stride_n % 8 || o_stride_bh % 8)
+        return fail(HYQ_EINVAL, "hyq_legacy_dequant: out must be 16-byte aligned with strides divisible by 8");
+    const int lpt_log2 = lanes_log2(d);
+    const int64_t total = bh * n;
+    const int64_t tpb = 256 >> lpt_log2;
+    const int64_t blocks = (total + tpb - 1) / tpb;
+    if (blocks > 0x7fffffffLL) return fail(HYQ_ENOTSUP, "hyq_legacy_dequant: too many tokens");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    dim3 grid(static_cast<unsigned>(blocks)), block(256);
+    if (nbits == 4)
+        legacy_dequant_kernel<4><<<grid, block, 0, s>>>(packed, n, total, lpt_log2, p_stride_bh, p_stride_n, scale,
+                                                        s_stride_bh, s_stride_g, group, out, o_stride_bh, o_stride_n);
+    else
+        legacy_dequant_kernel<2><<<grid, block, 0, s>>>(packed, n, total, lpt_log2, p_stride_bh, p_stride_n, scale,
+                                                        s_stride_bh, s_stride_g, group, out, o_stride_bh, o_stride_n);
+    return check_launch("hyq_legacy_dequant");
 }

@@ -68,6 +68,24 @@ int hyq_dequant(const int8_t* packed, int64_t bh, int64_t n, int32_t d,
                 uint16_t* out, int64_t o_stride_bh, int64_t o_stride_n, void* stream);
 
 /*
+ * Dequantisation of the legacy decode format: the [bh, n, d*nbits/8] uint8
+ * prefix and [bh, G, d] fp16 per-group-per-channel scales read by
+ * fused_decode_attention_k4v4 / splitk_decode_attention_k4v4(_mma)
+ * (src/ops/d_stage_cache.py:281-373, :955-1087; their unpack and scale
+ * loads).  Codes are offset-encoded: int4 even channel in the HIGH nibble,
+ * value u - 8; int2 channel 4k+i in bits (7-2i, 6-2i) of byte k, value u - 1.5.
+ *   packed uint8 [bh, n, d*nbits/8] strides (p_stride_bh, p_stride_n)
+ *   scale  fp16  [bh, ceil(n/group), d] strides (s_stride_bh, s_stride_g, 1), rows 16-byte aligned
+ *   out    bf16  [bh, n, d]         strides (o_stride_bh, o_stride_n), rows 16-byte aligned
+ * out = bf16(fp32(value) * fp32(scale[token / group][channel])) (RNE);
+ * nbits in {2,4}; d = 8 * 2^k <= 512.
+ */
+int hyq_legacy_dequant(const uint8_t* packed, int64_t bh, int64_t n, int32_t d,
+                       int64_t p_stride_bh, int64_t p_stride_n, int32_t nbits,
+                       const uint16_t* scale, int64_t s_stride_bh, int64_t s_stride_g, int32_t group,
+                       uint16_t* out, int64_t o_stride_bh, int64_t o_stride_n, void* stream);
+
+/*
  * Four-segment hybrid decode attention for one query token per head.
  * Replaces fused_d_stage_decode (src/ops/decode_d_stage.py:916-1005) and its
  * split-K path fused_d_stage_decode_splitk (:823-913) with kernels

@@ -30,6 +30,11 @@ its own formulas):
   hybrid_prefill_fp64(pv_mode='fp8')  -> with V, P exactly representable in
       e4m3 (powers of two) it equals the fp16 mode; per-channel V scale
       invariance; fp8 error against exact attention within the e4m3 bound.
+  legacy_unpack / legacy_values       -> hand-decoded bytes (nibble and crumb
+      order, offsets 8 and 1.5), every byte value against per-bit Python
+      arithmetic, group boundaries of the [G, D] scales.
+  legacy_decode_fp64                  -> with unit scales and no bf16 segments
+      it equals decode_fp64 over the same values re-expressed per token.
 """
 
 from __future__ import annotations
@@ -441,6 +446,82 @@ def decode_fp64(q: np.ndarray, k_packed, v_packed, k_scale, v_scale,
     if abs_v:   # sum_t p_t |v_t| / l: the scale of rounding errors in P and in the output
         V = np.abs(V)
     qg = q.astype(np.float64).reshape(BHK, kv_repeat, D)            # head h -> KV head h // R
+    s = np.einsum("hrd,hnd->hrn", qg, K) * sm_scale
+    s -= s.max(axis=2, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=2, keepdims=True)
+    return np.einsum("hrn,hnd->hrd", p, V).reshape(BHQ, D)
+
+
+# ---------------------------------------------------------------------------
+# legacy decode format (src/ops/d_stage_cache.py)
+# ---------------------------------------------------------------------------
+
+
+def legacy_unpack(packed: np.ndarray, nbits: int) -> np.ndarray:
+    """Offset-encoded codes of the legacy format -> float32 values.
+    int4 (src/ops/d_stage_cache.py:1020-1028): byte j holds channel 2j in the
+    HIGH nibble and 2j+1 in the low nibble, value u - 8.  int2 (:1074-1087):
+    byte k holds channel 4k+i in bits (7-2i, 6-2i), value u - 1.5.
+    packed uint8 [..., D*nbits/8] -> [..., D]."""
+    b = np.asarray(packed).astype(np.uint8).astype(np.int32)
+    if nbits == 4:
+        parts = [(b >> 4) - 8, (b & 15) - 8]
+        return np.stack(parts, axis=-1).reshape(*b.shape[:-1], 2 * b.shape[-1]).astype(np.float32)
+    if nbits == 2:
+        parts = [((b >> (6 - 2 * i)) & 3).astype(np.float32) - 1.5 for i in range(4)]
+        return np.stack(parts, axis=-1).reshape(*b.shape[:-1], 4 * b.shape[-1]).astype(np.float32)
+    raise ValueError(f"legacy format bits must be 2 or 4, got {nbits}")
+
+
+def legacy_values(packed: np.ndarray, scale: np.ndarray, nbits: int, group: int = GROUP_SIZE) -> np.ndarray:
+    """Exact float64 values (code value) * scale[token // group][channel]:
+    packed [BH, N, D*nbits/8], scale fp16 [BH, G, D] -> [BH, N, D]
+    (the K_int * sk / V_int * sv products of src/ops/d_stage_cache.py:1041-1044,
+    :1088-1092)."""
+    v = legacy_unpack(packed, nbits).astype(np.float64)
+    N = v.shape[1]
+    g = np.arange(N) // group
+    return v * scale.astype(np.float64)[:, g, :]
+
+
+def legacy_dequant_bf16(packed: np.ndarray, scale: np.ndarray, nbits: int, group: int = GROUP_SIZE) -> np.ndarray:
+    """(K_int * sk).to(bfloat16) (src/ops/d_stage_cache.py:1045): the exact
+    product rounded once to bf16, as bf16 bits [BH, N, D] (uint16)."""
+    x = legacy_values(packed, scale, nbits, group)
+    return f32_to_bf16_bits(x.astype(np.float32))     # the product is exact in float32
+
+
+def legacy_decode_fp64(q: np.ndarray, k_packed, v_packed, k_scale, v_scale,
+                       k_topk, v_topk, k_staging, v_staging, k_window, v_window,
+                       k_bits: int = 4, v_bits: int = 4, kv_repeat: int = 1,
+                       sm_scale: Optional[float] = None, group: int = GROUP_SIZE,
+                       abs_v: bool = False, bf16_operands: bool = False) -> np.ndarray:
+    """Float64 restatement of the legacy four-segment decode
+    (fused_decode_attention_k4v4 / splitk_decode_attention_k4v4(_mma),
+    src/ops/d_stage_cache.py:396-502, :595-822, :955-1245): softmax over
+    [prefix | topk | staging | window] of q . k * sm_scale with the prefix
+    values of legacy_values; q [BH_Q, D], KV head of query head h = h // R.
+    bf16_operands=True rounds the prefix values to bf16 first, as the MMA
+    variant's K_deq / V_deq (:1045, :1092).  Returns [BH_Q, D] float64."""
+    BHQ, D = q.shape
+    BHK = BHQ // kv_repeat
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    if k_packed.shape[1] > 0:
+        kq = legacy_values(k_packed, k_scale, k_bits, group)
+        vq = legacy_values(v_packed, v_scale, v_bits, group)
+        if bf16_operands:
+            kq = bf16_round(kq.astype(np.float32)).astype(np.float64)
+            vq = bf16_round(vq.astype(np.float32)).astype(np.float64)
+    else:
+        kq = np.zeros((BHK, 0, D))
+        vq = np.zeros((BHK, 0, D))
+    K = np.concatenate([kq, k_topk, k_staging, k_window], axis=1).astype(np.float64)
+    V = np.concatenate([vq, v_topk, v_staging, v_window], axis=1).astype(np.float64)
+    if abs_v:
+        V = np.abs(V)
+    qg = q.astype(np.float64).reshape(BHK, kv_repeat, D)
     s = np.einsum("hrd,hnd->hrn", qg, K) * sm_scale
     s -= s.max(axis=2, keepdims=True)
     p = np.exp(s)

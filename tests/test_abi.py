@@ -40,7 +40,7 @@ def _L():
 
 def test_abi_version_and_error_strings():
     _lib, L = _L()
-    assert L.hyq_abi_version() == _lib.ABI_VERSION == 4
+    assert L.hyq_abi_version() == _lib.ABI_VERSION == 5
     st = L.hyq_quant_pack(None, 0, 1, 1, 128, 0, 0, 3, None, 0, 0, None, 0, None)
     assert st == _lib.HYQ_EINVAL
     assert b"nbits must be 2, 4, or 8" in L.hyq_last_error()
@@ -66,6 +66,18 @@ def test_dequant_host_validation():
     assert L.hyq_dequant(None, 0, 7, 128, 0, 0, 4, None, 0, None, 0, 0, None) == _lib.HYQ_OK
     # misaligned fp16 output rows (8 is not 16-byte aligned)
     assert L.hyq_dequant(16, 1, 1, 128, 64, 64, 4, 16, 1, 8, 128, 128, None) == _lib.HYQ_EINVAL
+
+
+def test_legacy_dequant_host_validation():
+    _lib, L = _L()
+    # 8 bits is not a legacy format width; head dim 100 is unsupported
+    assert L.hyq_legacy_dequant(None, 1, 1, 128, 0, 0, 8, None, 0, 0, 128, None, 0, 0, None) == _lib.HYQ_EINVAL
+    assert L.hyq_legacy_dequant(None, 1, 1, 100, 0, 0, 4, None, 0, 0, 128, None, 0, 0, None) == _lib.HYQ_ENOTSUP
+    assert L.hyq_legacy_dequant(None, 1, 1, 128, 0, 0, 4, None, 0, 0, 0, None, 0, 0, None) == _lib.HYQ_EINVAL
+    # empty input is a no-op
+    assert L.hyq_legacy_dequant(None, 0, 7, 128, 0, 0, 4, None, 0, 0, 128, None, 0, 0, None) == _lib.HYQ_OK
+    # scale rows must be 16-byte aligned (8 is not)
+    assert L.hyq_legacy_dequant(16, 1, 1, 128, 64, 64, 4, 8, 128, 128, 128, 256, 128, 128, None) == _lib.HYQ_EINVAL
 
 
 def _params(_lib, **kw):

@@ -1,0 +1,156 @@
+"""GPU parity of the legacy decode format (src/ops/d_stage_cache.py) against
+the CPU oracle: the prefix dequantisation bit-exact (hyq_legacy_dequant), the
+four legacy decode entry points within the decode tolerance of the float64
+restatement."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import hyq_oracle as O
+from tests.gpu_util import to_dev_bf16
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+
+
+def _legacy_inputs(rng, BHK, N, D, bits, group=128, neg=True):
+    packed = rng.integers(0, 256, (BHK, N, D * bits // 8), dtype=np.uint8)
+    G = (N + group - 1) // group
+    lo = -0.12 if neg else 0.02
+    scale = rng.uniform(lo, 0.12, (BHK, G, D)).astype(np.float16)
+    return packed, scale
+
+
+@pytest.mark.parametrize("bits,N", [(4, 300), (4, 128), (2, 257), (2, 1)])
+def test_legacy_dequant_bit_exact(bits, N):
+    from hyquant_amd.d_stage_cache import legacy_dequantize
+    print(f"legacy dequant bits={bits} N={N}", flush=True)
+    rng = np.random.default_rng(bits * 100 + N)
+    BHK, D = 3, 128
+    packed, scale = _legacy_inputs(rng, BHK, N, D, bits)
+    scale[0, 0, :4] = 0.0                                     # zero scales: signed zeros
+    exp = O.legacy_dequant_bf16(packed, scale, bits)
+    got = legacy_dequantize(torch.from_numpy(packed).cuda(), torch.from_numpy(scale).cuda(), D, bits)
+    got_bits = got.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got_bits, exp)
+    # a scale view with a padded group stride and an output view inside a larger buffer
+    wide = torch.zeros(BHK, scale.shape[1], 2 * D, dtype=torch.float16, device="cuda")
+    wide[:, :, :D] = torch.from_numpy(scale).cuda()
+    buf = torch.full((BHK, N + 7, D), 7.0, dtype=torch.bfloat16, device="cuda")
+    legacy_dequantize(torch.from_numpy(packed).cuda(), wide[:, :, :D], D, bits, out=buf[:, 3:3 + N])
+    assert np.array_equal(buf[:, 3:3 + N].contiguous().view(torch.int16).cpu().numpy().view(np.uint16), exp)
+    assert bool((buf[:, :3] == 7.0).all()) and bool((buf[:, 3 + N:] == 7.0).all())
+
+
+def _check(name, out, ref, ref_abs):
+    out = out.float().cpu().numpy().reshape(ref.shape)
+    diff = np.abs(out - ref)
+    bound = ATOL + 2.0 ** -9 * ref_abs + 2.0 ** -8 * np.abs(ref)
+    print(f"{name}: max-abs {diff.max():.3e}, max diff/bound {(diff / bound).max():.3f}", flush=True)
+    assert (diff <= bound).all(), name
+
+
+@pytest.mark.parametrize("entry,kb,vb,R", [
+    ("fused", 4, 4, 4), ("splitk", 4, 4, 4), ("mma", 4, 4, 4), ("mma", 4, 2, 8), ("mma", 2, 4, 1), ("mma", 2, 2, 4),
+])
+def test_legacy_decode_vs_oracle(entry, kb, vb, R):
+    import hyquant_amd.d_stage_cache as L
+    print(f"legacy decode {entry} K{kb}V{vb} R={R}", flush=True)
+    rng = np.random.default_rng(kb * 10 + vb + R)
+    B, HKV, N, D, T, S, W = 2, 2, 700, 128, 37, 5, 64
+    BHK = B * HKV
+    kp, ks = _legacy_inputs(rng, BHK, N, D, kb)
+    vp, vs = _legacy_inputs(rng, BHK, N, D, vb)
+    f = lambda n, s=1.0: O.bf16_round((rng.standard_normal((BHK, n, D)) * s).astype(np.float32))
+    kt, vt, kst, vst, kw, vw = f(T), f(T), f(S), f(S), f(W), f(W)
+    q = O.bf16_round(rng.standard_normal((B * HKV * R, D)).astype(np.float32))
+    d = lambda a: to_dev_bf16(a, "cuda")
+    u = lambda a: torch.from_numpy(a).cuda()
+    qd = d(q).view(B, HKV * R, 1, D)
+    args = (qd, u(kp), u(vp), u(ks), u(vs), d(kt), d(vt), d(kst), d(vst), d(kw), d(vw))
+    if entry == "fused":
+        out = L.fused_decode_attention_k4v4(*args, kv_repeat=R)
+    elif entry == "splitk":
+        out = L.splitk_decode_attention_k4v4(*args, kv_repeat=R, split_size=512)
+    else:
+        out = L.splitk_decode_attention_k4v4_mma(*args, kv_repeat=R, k_bits=kb, v_bits=vb)
+    assert out.shape == (B, HKV * R, 1, D) and out.dtype == torch.bfloat16
+    oargs = (q, kp, vp, ks, vs, kt, vt, kst, vst, kw, vw)
+    ref = O.legacy_decode_fp64(*oargs, k_bits=kb, v_bits=vb, kv_repeat=R, bf16_operands=True)
+    ref_abs = O.legacy_decode_fp64(*oargs, k_bits=kb, v_bits=vb, kv_repeat=R, bf16_operands=True, abs_v=True)
+    _check(f"{entry} K{kb}V{vb}", out, ref, ref_abs)
+    # and close to the unrounded legacy math (the FFMA variants' fp32 operands)
+    exact = O.legacy_decode_fp64(*oargs, k_bits=kb, v_bits=vb, kv_repeat=R)
+    assert np.abs(out.float().cpu().numpy().reshape(exact.shape) - exact).max() <= 4 * ATOL
+
+
+def test_legacy_decode_empty_segments_and_no_prefix():
+    import hyquant_amd.d_stage_cache as L
+    rng = np.random.default_rng(5)
+    BHK, R, D, W = 2, 4, 128, 32
+    q = O.bf16_round(rng.standard_normal((BHK * R, D)).astype(np.float32))
+    kw = O.bf16_round(rng.standard_normal((BHK, W, D)).astype(np.float32))
+    vw = O.bf16_round(rng.standard_normal((BHK, W, D)).astype(np.float32))
+    e8 = torch.empty(BHK, 0, D // 2, dtype=torch.uint8, device="cuda")
+    es = torch.empty(BHK, 0, D, dtype=torch.float16, device="cuda")
+    eb = torch.empty(BHK, 0, D, dtype=torch.bfloat16, device="cuda")
+    d = lambda a: to_dev_bf16(a, "cuda")
+    out = L.fused_decode_attention_k4v4(d(q).view(1, BHK * R, 1, D), e8, e8, es, es, eb, eb, eb, eb, d(kw), d(vw),
+                                        kv_repeat=R)
+    z8 = np.zeros((BHK, 0, D // 2), np.uint8)
+    zs = np.zeros((BHK, 0, D), np.float16)
+    zb = np.zeros((BHK, 0, D), np.float32)
+    ref = O.legacy_decode_fp64(q, z8, z8, zs, zs, zb, zb, zb, zb, kw, vw, kv_repeat=R)
+    ref_abs = O.legacy_decode_fp64(q, z8, z8, zs, zs, zb, zb, zb, zb, kw, vw, kv_repeat=R, abs_v=True)
+    _check("window only", out, ref, ref_abs)
+
+
+def test_d_stage_decode_attention_per_token_format():
+    """Legacy path A: per-token int4 K (and int4 / int2 V) prefix dequantised
+    to fp16 then bf16, one KV head per query head, [B, H, W, D] window."""
+    from hyquant_amd.d_stage_cache import d_stage_decode_attention, decode_4seg_attention
+    assert decode_4seg_attention is d_stage_decode_attention
+    rng = np.random.default_rng(9)
+    B, H, N, D, T, S, W = 2, 3, 400, 128, 20, 6, 48
+    BH = B * H
+    for vb in (4, 2):
+        k = O.bf16_round(rng.standard_normal((BH, N, D)).astype(np.float32))
+        v = O.bf16_round(rng.standard_normal((BH, N, D)).astype(np.float32))
+        kp, ks = O.quantize_per_token(k, 4)
+        vp, vs = O.quantize_per_token(v, vb)
+        f = lambda n: O.bf16_round(rng.standard_normal((BH, n, D)).astype(np.float32))
+        kt, vt, kst, vst, kw, vw = f(T), f(T), f(S), f(S), f(W), f(W)
+        q = O.bf16_round(rng.standard_normal((BH, D)).astype(np.float32))
+        d = lambda a: to_dev_bf16(a, "cuda")
+        u = lambda a: torch.from_numpy(a).cuda()
+        out = d_stage_decode_attention(d(q).view(B, H, 1, D), u(kp), u(vp), u(ks), u(vs), d(kt), d(vt), d(kst),
+                                       d(vst), d(kw).view(B, H, W, D), d(vw).view(B, H, W, D), v_bits=vb)
+        assert out.shape == (B, H, 1, D)
+        # dequantize_k_int4_channel(...).to(bf16): fp16(code * scale) rounded to bf16
+        kd = O.bf16_round(O.dequantize_per_token(kp, ks, 4).astype(np.float32))
+        vd = O.bf16_round(O.dequantize_per_token(vp, vs, vb).astype(np.float32))
+        e8 = np.zeros((BH, 0, D // 2), np.int8)
+        e16 = np.zeros((BH, 0), np.float16)
+        Kb = np.concatenate([kd, kt], 1)
+        Vb = np.concatenate([vd, vt], 1)
+        ref = O.decode_fp64(q, e8, e8, e16, e16, Kb, Vb, kst, vst, kw, vw)
+        ref_abs = O.decode_fp64(q, e8, e8, e16, e16, Kb, Vb, kst, vst, kw, vw, abs_v=True)
+        _check(f"d_stage_decode_attention V{vb}", out, ref, ref_abs)
+
+
+def test_legacy_entry_points_reject_bad_arguments():
+    import hyquant_amd.d_stage_cache as L
+    D = 128
+    q = torch.zeros(1, 4, 1, D, dtype=torch.bfloat16, device="cuda")
+    kp = torch.zeros(1, 10, D // 2, dtype=torch.uint8, device="cuda")
+    ks = torch.zeros(1, 1, D, dtype=torch.float16, device="cuda")
+    eb = torch.zeros(1, 0, D, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(1, 4, D, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        L.fused_decode_attention_k4v4(q.half(), kp, kp, ks, ks, eb, eb, eb, eb, w, w, kv_repeat=4)
+    with pytest.raises(AssertionError):
+        L.splitk_decode_attention_k4v4_mma(q, kp, kp, ks, ks, eb, eb, eb, eb, w, w, kv_repeat=4, k_bits=8)
+    with pytest.raises(ValueError):       # too few scale groups for the prefix
+        L.legacy_dequantize(torch.zeros(1, 200, D // 2, dtype=torch.uint8, device="cuda"), ks, D, 4)

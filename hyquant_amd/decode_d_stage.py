@@ -24,7 +24,14 @@ _LOG2_E = 1.44269504
 # ---------------------------------------------------------------------------
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device) -> int:
+    """The current HIP stream of `device` as a pointer value (torch's raw
+    accessor when it has one: the Stream object costs microseconds a call)."""
+    if _raw_stream is not None and device.index is not None:
+        return _raw_stream(device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -37,9 +44,11 @@ def _inner_contig(t: torch.Tensor) -> torch.Tensor:
     """The kernels take any head stride (a multiple of 16 bytes) but need each
     head's rows packed back to back (token stride = row length) and 16-byte
     aligned; anything else gets a contiguous copy."""
+    es = t.element_size()
+    if t.is_contiguous() and t.data_ptr() % 16 == 0 and (t.shape[-1] * es) % 16 == 0:
+        return t                       # the common case, decided in three calls
     if t.numel() == 0:
         return t
-    es = t.element_size()
     ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and (t.dim() < 3 or t.stride(-2) == t.shape[-1])
           and all((s * es) % 16 == 0 for s in t.stride()[:-1]))
     return t if ok else t.contiguous()

@@ -86,6 +86,31 @@ def test_legacy_decode_vs_oracle(entry, kb, vb, R):
     assert np.abs(out.float().cpu().numpy().reshape(exact.shape) - exact).max() <= 4 * ATOL
 
 
+def test_legacy_decode_config1_shape():
+    """Config-1 shape (B=1, 32q/8kv, 8K prefix) through the legacy entry point."""
+    import hyquant_amd.d_stage_cache as L
+    print("legacy decode config-1 shape", flush=True)
+    rng = np.random.default_rng(77)
+    HKV, R, N, D, T, S, W = 8, 4, 7667, 128, 397, 64, 128
+    kp, ks = _legacy_inputs(rng, HKV, N, D, 4)
+    vp, vs = _legacy_inputs(rng, HKV, N, D, 4)
+    f = lambda n: O.bf16_round(rng.standard_normal((HKV, n, D)).astype(np.float32))
+    kt, vt, kst, vst, kw, vw = f(T), f(T), f(S), f(S), f(W), f(W)
+    q = O.bf16_round(rng.standard_normal((HKV * R, D)).astype(np.float32))
+    d = lambda a: to_dev_bf16(a, "cuda")
+    u = lambda a: torch.from_numpy(a).cuda()
+    out = L.fused_decode_attention_k4v4(d(q).view(1, HKV * R, 1, D), u(kp), u(vp), u(ks), u(vs), d(kt), d(vt),
+                                        d(kst), d(vst), d(kw), d(vw), kv_repeat=R)
+    oargs = (q, kp, vp, ks, vs, kt, vt, kst, vst, kw, vw)
+    ref = O.legacy_decode_fp64(*oargs, kv_repeat=R, bf16_operands=True)
+    ref_abs = O.legacy_decode_fp64(*oargs, kv_repeat=R, bf16_operands=True, abs_v=True)
+    _check("config-1 shape", out, ref, ref_abs)
+    # a second call gives the same bits
+    out2 = L.fused_decode_attention_k4v4(d(q).view(1, HKV * R, 1, D), u(kp), u(vp), u(ks), u(vs), d(kt), d(vt),
+                                         d(kst), d(vst), d(kw), d(vw), kv_repeat=R)
+    assert torch.equal(out, out2)
+
+
 def test_legacy_decode_empty_segments_and_no_prefix():
     import hyquant_amd.d_stage_cache as L
     rng = np.random.default_rng(5)

@@ -657,8 +657,12 @@ __global__ void mark_kernel(const int64_t* __restrict__ idx, int T, int64_t P, i
     atomicOr(bits + bh * words + (p >> 5), 1u << (p & 31));
 }
 
-constexpr int CQ_CHUNK = 256;               // prefix positions per workgroup
-constexpr int CQ_UNROLL = 4;                // tokens per 16-lane group per pass
+// prefix positions per workgroup: 16 KiB of K and V rows read per workgroup.
+// Streams of this read:write mix ran faster the fewer bytes each workgroup
+// covers, down to about 8 KiB; at 16 positions the per-workgroup set-up
+// (the bitmap prefix count and two barriers) costs more than that gains
+constexpr int CQ_CHUNK = 32;
+constexpr int CQ_UNROLL = 2;                // tokens per 16-lane group per pass (one pass)
 
 // 16 lanes quantise one bf16 (fp16 when f16) row of 128 channels: lane `sub`
 // holds channels 8 sub .. 8 sub + 7 (`raw`).  All 16 lanes take part in the

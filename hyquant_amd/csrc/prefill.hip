@@ -267,13 +267,30 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
     double s0 = 0.0, s1 = 0.0;
     float m0 = 0.0f, m1 = 0.0f;
     const int r_end = min(N, (chunk + 1) * STAT_ROWS);
-    for (int r = chunk * STAT_ROWS + ph; r < r_end; r += 4) {
-        const uint32_t kk = *reinterpret_cast<const uint32_t*>(kb + r * k_n);
-        const uint32_t vv = *reinterpret_cast<const uint32_t*>(vb + r * v_n);
+    const int r0 = chunk * STAT_ROWS + ph;
+    const int nr = r_end > r0 ? (r_end - r0 + 3) / 4 : 0;     // rows r0, r0 + 4, ...
+    auto add = [&](uint32_t kk, uint32_t vv) {
         s0 += static_cast<double>(half_to_f32(static_cast<uint16_t>(kk), f16));
         s1 += static_cast<double>(half_to_f32(static_cast<uint16_t>(kk >> 16), f16));
         m0 = fmaxf(m0, fabsf(half_to_f32(static_cast<uint16_t>(vv), f16)));
         m1 = fmaxf(m1, fabsf(half_to_f32(static_cast<uint16_t>(vv >> 16), f16)));
+    };
+    // sixteen rows' loads in flight before their adds, which stay in row order
+    int i = 0;
+    for (; i + 16 <= nr; i += 16) {
+        uint32_t kk[16], vv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int64_t r = r0 + 4 * (i + j);
+            kk[j] = *reinterpret_cast<const uint32_t*>(kb + r * k_n);
+            vv[j] = *reinterpret_cast<const uint32_t*>(vb + r * v_n);
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) add(kk[j], vv[j]);
+    }
+    for (; i < nr; ++i) {
+        const int64_t r = r0 + 4 * i;
+        add(*reinterpret_cast<const uint32_t*>(kb + r * k_n), *reinterpret_cast<const uint32_t*>(vb + r * v_n));
     }
     s_sum[ph][2 * cp] = s0;
     s_sum[ph][2 * cp + 1] = s1;
@@ -343,13 +360,15 @@ __global__ __launch_bounds__(256) void kv_convert_kernel(const uint16_t* __restr
     if (row >= N) return;
     const u32x4 kk = *reinterpret_cast<const u32x4*>(k + b * k_b + hk * k_h + row * k_n + 8 * co);
     const u32x4 vv = *reinterpret_cast<const u32x4*>(v + b * v_b + hk * v_h + row * v_n + 8 * co);
+    // the 8 channel means in one 16-byte load (km rows are 256-byte aligned)
+    const u32x4 mm = *reinterpret_cast<const u32x4*>(km + bhk * PD + 8 * co);
     float kf[8], vf[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const uint32_t kw = kk[e >> 1], vw = vv[e >> 1];
+        const uint32_t kw = kk[e >> 1], vw = vv[e >> 1], mw = mm[e >> 1];
         kf[e] = half_to_f32(static_cast<uint16_t>((e & 1) ? (kw >> 16) : kw), f16);
         vf[e] = half_to_f32(static_cast<uint16_t>((e & 1) ? (vw >> 16) : vw), f16);
-        const float d = kf[e] - half_to_f32(km[bhk * PD + 8 * co + e], f16);
+        const float d = kf[e] - half_to_f32(static_cast<uint16_t>((e & 1) ? (mw >> 16) : mw), f16);
         kf[e] = f16 ? d : bf16_round_f32(d);     // pack_f16x2 below rounds to fp16
     }
     const int64_t o = (static_cast<int64_t>(bhk) * N + row) * PD + 8 * co;
@@ -362,9 +381,11 @@ __global__ __launch_bounds__(256) void kv_convert_kernel(const uint16_t* __restr
         // fp8 PV: e4m3(v / vscale) for the rest keys and fp16(v / vscale) for
         // the vertical and window keys, so that all tiles accumulate in one unit
         float q[8];
+        const f32x4 vs0 = *reinterpret_cast<const f32x4*>(vscale + bhk * PD + 8 * co);
+        const f32x4 vs1 = *reinterpret_cast<const f32x4*>(vscale + bhk * PD + 8 * co + 4);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float s = vscale[bhk * PD + 8 * co + e];
+            const float s = e < 4 ? vs0[e] : vs1[e - 4];
             q[e] = s > 0.0f ? vf[e] / s : 0.0f;
         }
         const u32x2 p = {pack_e4m3x4(q[0], q[1], q[2], q[3]), pack_e4m3x4(q[4], q[5], q[6], q[7])};

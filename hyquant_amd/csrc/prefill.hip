@@ -548,16 +548,18 @@ __global__ __launch_bounds__(256) void gather_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) kk[i] = reinterpret_cast<const u32x4*>(src)[i];
             const int64_t dst = (static_cast<int64_t>(bh) * P + base + r) * PD;
+            // V rows are plain copies: 16-byte chunk qq + 4 i of the row, so
+            // the four lanes of a row cover 64 contiguous bytes per instruction
             if (v8 != nullptr) {
-                const u32x4* vs = reinterpret_cast<const u32x4*>(v8 + (bhk * N + pos) * PD + 32 * qq);
-                u32x4* vd = reinterpret_cast<u32x4*>(vr + dst + 32 * qq);
-                vd[0] = vs[0];
-                vd[1] = vs[1];
+                const u32x4* vs = reinterpret_cast<const u32x4*>(v8 + (bhk * N + pos) * PD);
+                u32x4* vd = reinterpret_cast<u32x4*>(vr + dst);
+                vd[qq] = vs[qq];
+                vd[qq + 4] = vs[qq + 4];
             } else {
-                const u32x4* vs = reinterpret_cast<const u32x4*>(v16 + (bhk * N + pos) * PD + 32 * qq);
-                u32x4* vd = reinterpret_cast<u32x4*>(vr + 2 * (dst + 32 * qq));
+                const u32x4* vs = reinterpret_cast<const u32x4*>(v16 + (bhk * N + pos) * PD);
+                u32x4* vd = reinterpret_cast<u32x4*>(vr + 2 * dst);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) vd[i] = vs[i];
+                for (int i = 0; i < 4; ++i) vd[qq + 4 * i] = vs[qq + 4 * i];
             }
         }
         float x[32];
@@ -592,15 +594,15 @@ __global__ __launch_bounds__(256) void gather_kernel(
         const int base = (blockIdx.x - nsb) * BN;
         if (base + r >= T) return;
         const int pos = vert[static_cast<int64_t>(bh) * T + base + r];
-        const u32x4* ks = reinterpret_cast<const u32x4*>(k16 + (bhk * N + pos) * PD + 32 * qq);
-        const u32x4* vs = reinterpret_cast<const u32x4*>(v16 + (bhk * N + pos) * PD + 32 * qq);
-        const int64_t dst = (static_cast<int64_t>(bh) * T + base + r) * PD + 32 * qq;
+        const u32x4* ks = reinterpret_cast<const u32x4*>(k16 + (bhk * N + pos) * PD);
+        const u32x4* vs = reinterpret_cast<const u32x4*>(v16 + (bhk * N + pos) * PD);
+        const int64_t dst = (static_cast<int64_t>(bh) * T + base + r) * PD;
         u32x4* kd = reinterpret_cast<u32x4*>(kv16 + dst);
         u32x4* vd = reinterpret_cast<u32x4*>(vv16 + dst);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            kd[i] = ks[i];
-            vd[i] = vs[i];
+            kd[qq + 4 * i] = ks[qq + 4 * i];
+            vd[qq + 4 * i] = vs[qq + 4 * i];
         }
     }
 }

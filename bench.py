@@ -8,11 +8,13 @@ fused_d_stage_decode call over that cache.
 
 Timing: inputs are resident in HBM; R copies of the cache (R chosen so the
 copies exceed 1 GiB, i.e. four times the 256 MiB Infinity Cache) are used in
-rotation so every step streams its bytes from HBM.  W untimed steps, then the
-K timed steps are captured in a HIP graph; the graph is replayed five times,
-each replay bracketed by two HIP events on the stream the kernels run on and
-by synchronisations, and the median replay gives the per-step time (the same
-K steps issued as Python calls one by one are reported as eager_us_per_step).
+rotation so every step streams its bytes from HBM.  W untimed steps, then
+the steps are captured in ceil(R / K) HIP graphs of K steps, graph j over
+copies jK .. jK + K - 1, replayed in turn so that a copy comes back only after
+all R were streamed (whatever K is); each replay is bracketed by two HIP
+events on the stream the kernels run on and by synchronisations, and the
+median of five replays gives the per-step time (the same K steps issued as
+Python calls one by one are reported as eager_us_per_step).
 
 Output: one JSON line (rank 0), with the roofline of the decode kernel, the
 CPU baseline (the reference's bf16 eager decode math run by torch on the host
@@ -113,11 +115,15 @@ REPLAYS = 5
 def time_rotating(fn, states, warmup, steps, replays=REPLAYS):
     """ms per step over `steps` steps cycling through `states`.
 
-    The steps are captured once into a HIP graph; the graph is replayed
-    `replays` times, each replay (K steps, no host work between launches)
-    bracketed by HIP events on the stream, and the median replay gives the
-    per-step time.  Returns (graph_ms_per_step, eager_ms_per_step) where the
-    eager figure times the same K Python calls issued one by one."""
+    The steps are captured into ceil(R / K) HIP graphs of K steps each, graph
+    j covering copies jK .. jK + K - 1 (mod R), and the graphs are replayed in
+    turn, so a copy is streamed again only after every other copy was: R
+    copies of >= 1 GiB together (four times the 256 MiB Infinity Cache) put
+    at least that much traffic between two uses of a copy whatever K is.
+    Each replay (K steps, no host work between launches) is bracketed by HIP
+    events on the stream, and the median replay gives the per-step time.
+    Returns (graph_ms_per_step, eager_ms_per_step) where the eager figure
+    times K Python calls issued one by one."""
     n = len(states)
     for i in range(warmup):
         fn(states[i % n])
@@ -130,31 +136,36 @@ def time_rotating(fn, states, warmup, steps, replays=REPLAYS):
     e1.record()
     torch.cuda.synchronize()
     eager = e0.elapsed_time(e1) / steps
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for i in range(steps):
-            fn(states[i % n])
-    g.replay()
+    graphs = []
+    for j in range(max(1, -(-n // steps))):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                fn(states[(j * steps + i) % n])
+        graphs.append(g)
+    for g in graphs:
+        g.replay()
     torch.cuda.synchronize()
     per = []
-    for _ in range(replays):
+    for r in range(replays):
         e0.record()
-        g.replay()
+        graphs[r % len(graphs)].replay()
         e1.record()
         torch.cuda.synchronize()
         per.append(e0.elapsed_time(e1) / steps)
     per.sort()
-    del g
+    del graphs
     return per[len(per) // 2], eager
 
 
-def copies_for(nbytes, cap=512):
+def copies_for(nbytes, cap=2048):
     return int(max(1, min(cap, math.ceil((1 << 30) / max(nbytes, 1)))))
 
 
 def bench_hybrid(B, HQ, HKV, N, dev, warmup, steps, seed=0, kb=4, vb=4):
     nbytes = algorithmic_bytes(B, HQ, HKV, N, kb=kb, vb=vb)
     R = copies_for(nbytes)
+    assert R * nbytes >= (1 << 30), "the rotated copies must cover 1 GiB"
     states = [make_state(B, HQ, HKV, N, dev, seed + r, kb=kb, vb=vb) for r in range(R)]
     G = HQ // HKV
     ms, eager = time_rotating(lambda s: run_decode(s[0], s[1], G), states, warmup, steps)
@@ -500,6 +511,87 @@ def pmc_decode_shapes_workload(dev):
         torch.cuda.empty_cache()
 
 
+PHASES = ("entry", "arguments", "Q", "first K/V", "stream done", "LDS merge", "partial acked",
+          "counter", "merge (m,l) in", "merge summed", "merge stored", "merge entered",
+          "merge loads issued")
+
+
+def phase_trace(dev, steps=100):
+    """Per-phase timeline of the config-1 decode step under HIP-graph replay,
+    from the phase-trace build (libhyq_trace.so: s_memrealtime stamps of every
+    wavefront, 100 MHz).  Two workloads: the bench's rotation over >= 1 GiB
+    of cache copies, and one cache copy replayed (translations and caches
+    warm).  For each of the last launches of a replay: the launch start t0 is
+    the earliest wavefront entry; every phase is reported as the median and
+    the maximum over wavefronts of (stamp - t0) in microseconds (the merge
+    phases over the merging wavefronts only); `end` is the last merge store
+    acknowledged, `gap` the time from a launch's end to the next launch's t0,
+    `wave_spread` the median over workgroups of the spread of their four
+    wavefronts' stream-done stamps."""
+    import ctypes
+    import numpy as np
+    from hyquant_amd import _lib
+    L = _lib.lib()
+    if not hasattr(L, "hyq_phase_trace_read"):
+        raise RuntimeError("phase trace needs the trace build: python -m hyquant_amd.build --trace, "
+                           "then HYQ_LIBRARY=hyquant_amd/libhyq_trace.so")
+    slots, maxw, nph = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    L.hyq_phase_trace_geometry(ctypes.byref(slots), ctypes.byref(maxw), ctypes.byref(nph))
+    S, MW, NP = slots.value, maxw.value, nph.value
+    B, HQ, HKV, N = 1, 32, 8, 8192
+    G = HQ // HKV
+    out = {}
+    for mode in ("rotated", "one_copy"):
+        nb = algorithmic_bytes(B, HQ, HKV, N)
+        R = copies_for(nb) if mode == "rotated" else 1
+        states = [make_state(B, HQ, HKV, N, dev, r) for r in range(R)]
+        ms, _ = time_rotating(lambda s: run_decode(s[0], s[1], G), states, 10, steps)
+        buf = np.zeros(S * MW * NP, dtype=np.uint64)
+        nl = ctypes.c_uint32()
+        rc = L.hyq_phase_trace_read(buf.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(buf.nbytes), ctypes.byref(nl))
+        if rc != 0:
+            raise RuntimeError("hyq_phase_trace_read failed")
+        tr = buf.reshape(S, MW, NP).astype(np.int64)
+        launches = []
+        for s in range(S):
+            idx = np.nonzero(tr[s][:, 0] > 0)[0]
+            if len(idx) == 0:
+                continue
+            launches.append((int(tr[s][idx[0], NP - 1]), tr[s][: idx.max() + 1]))
+        launches.sort(key=lambda x: x[0])
+        launches = launches[-min(len(launches), steps, S):]
+        med, mx, gaps, ends, spread = [], [], [], [], []
+        for i, (_, w) in enumerate(launches):
+            t0 = w[:, 0].min()
+            nt = NP - 1                                       # the last field is the launch index
+            rel = (w[:, :nt] - t0) * 0.01                     # 100 MHz ticks -> us
+            m_row, x_row = np.zeros(nt), np.zeros(nt)
+            for k in range(nt):
+                col = rel[:, k][w[:, k] > 0]
+                m_row[k], x_row[k] = (np.median(col), col.max()) if len(col) else (np.nan, np.nan)
+            med.append(m_row)
+            mx.append(x_row)
+            end = max(w[:, 10].max(), w[:, 7].max())
+            ends.append((end - t0) * 0.01)
+            sd = w[:, 4].reshape(-1, 4)
+            spread.append(np.median(sd.max(axis=1) - sd.min(axis=1)) * 0.01)
+            if i + 1 < len(launches):
+                gaps.append((launches[i + 1][1][:, 0].min() - end) * 0.01)
+        med = np.nanmedian(np.stack(med), axis=0)
+        mx = np.nanmedian(np.stack(mx), axis=0)
+        out[mode] = {"us_per_step": round(ms * 1e3, 3), "launches": len(launches),
+                     "wavefronts": int((launches[-1][1][:, 0] > 0).sum()),
+                     "phases_us": {PHASES[k]: {"median": round(float(med[k]), 2), "max": round(float(mx[k]), 2)}
+                                   for k in range(len(med))},
+                     "end_us": round(float(np.median(ends)), 2),
+                     "gap_us": round(float(np.median(gaps)), 2) if gaps else None,
+                     "wave_spread_us": round(float(np.median(spread)), 2)}
+        del states
+        torch.cuda.empty_cache()
+        print(f"# phase-trace {mode} {out[mode]}", file=sys.stderr, flush=True)
+    return out
+
+
 def traffic_record():
     """HBM bytes per decode launch measured by the FETCH_SIZE / WRITE_SIZE
     passes over pmc_workload (profiles/decode_config1_traffic.json), or None."""
@@ -523,14 +615,21 @@ def main():
     ap.add_argument("--pmc", action="store_true", help="run the counter-pass workload only")
     ap.add_argument("--pmc-decode-shapes", action="store_true",
                     help="run the decode counter workload over three shapes only")
+    ap.add_argument("--phase-trace", action="store_true",
+                    help="print the config-1 decode phase timeline from the trace build (libhyq_trace.so)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(--gpus must be 1)", file=sys.stderr)
         sys.exit(2)
+    if args.phase_trace:
+        os.environ["HYQ_LIBRARY"] = os.path.join(ROOT, "hyquant_amd", "libhyq_trace.so")
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     import hyquant_amd  # noqa: F401  (fails loudly if libhyq.so is missing)
+    if args.phase_trace:
+        print(json.dumps({"phase_trace": phase_trace(dev, args.steps)}), flush=True)
+        return
     if args.pmc_decode_shapes:
         pmc_decode_shapes_workload(dev)
         return
@@ -561,7 +660,8 @@ def main():
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "prefix": N,
                    "n_quant": Nq, "n_topk": T, "n_staging": S, "n_window": W,
                    "cache_copies_rotated": R,
-                   "timing": f"median of {REPLAYS} HIP-graph replays of K steps, HIP events on the kernel's stream",
+                   "timing": f"median of {REPLAYS} HIP-graph replays of K steps, the graphs rotating over the "
+                             f"{R} copies (>= 1 GiB between two uses of a copy), HIP events on the kernel's stream",
                    "eager_us_per_step": round(eager * 1e3, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,

@@ -12,7 +12,9 @@ import threading
 from ctypes import POINTER, Structure, c_float, c_int, c_int32, c_int64, c_size_t, c_uint16, c_void_p, c_int8, c_char_p, c_double
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libhyq.so")
+# HYQ_LIBRARY names another build of the same sources (the phase-trace
+# build, libhyq_trace.so); the default is the product library
+LIB_PATH = os.environ.get("HYQ_LIBRARY") or os.path.join(HERE, "libhyq.so")
 
 # the hyq_abi_version() these bindings (struct layouts, argument lists) match
 ABI_VERSION = 5

@@ -35,10 +35,16 @@ def hipcc() -> str:
     return os.path.join(rocm, "bin", "hipcc")
 
 
-def build(verbose: bool = False) -> str:
+# the phase-trace build of the decode kernel (s_memrealtime stamps per
+# workgroup, read back with hyq_phase_trace_read; see bench.py --phase-trace)
+TRACE_LIB = os.path.join(HERE, "libhyq_trace.so")
+
+
+def build(verbose: bool = False, trace: bool = False) -> str:
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *srcs]
+    out = TRACE_LIB if trace else LIB
+    tmp = out + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, *(["-DHYQ_PHASE_TRACE"] if trace else []), "-o", tmp, *srcs]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
@@ -46,9 +52,9 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{' '.join(cmd)}\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, trace="--trace" in sys.argv[1:]))

@@ -30,7 +30,7 @@
 // one partial with device-scope stores (write-through to the device coherence
 // point), waits for them, and counts itself in on its head's arrival counter.
 // The workgroup that arrives last merges the head's partials (one wavefront
-// per query head; see merge_head) and resets the counter to zero, so the
+// per query head; see merge_head_waves) and resets the counter to zero, so the
 // counters are zero again when the launch ends.  No fence is needed: the
 // partials never sit dirty in a per-XCD L2, and the merge reads them with
 // device-scope loads.
@@ -98,32 +98,132 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
+// Kernel arguments.  The first PRO_DWORDS dwords are everything the
+// prologue needs before its first loads; decode_kernel reads them, with its
+// piece's two entries of bnd, in one batch of scalar loads (kernel_args), so
+// their layout is fixed: pointers on 8-byte boundaries, the rest 32-bit (row
+// and head strides fit 31 bits, checked on the host).
 struct DecArgs {
-    const uint16_t* q; int64_t q_stride;
-    uint16_t* out; int64_t out_stride;
-    const uint8_t* kp; int64_t kp_bh, kp_n;
-    const uint8_t* vp; int64_t vp_bh, vp_n;
-    const uint16_t* ks; int64_t ks_bh;
-    const uint16_t* vs; int64_t vs_bh;
-    int32_t n_quant;
-    const uint16_t* sk[3]; const uint16_t* sv[3];
-    int64_t sk_bh[3], sk_n[3], sv_bh[3], sv_n[3];
-    int32_t sn[3];
-    int32_t G;
-    int32_t bh_kv;
-    float qk_scale;        // sm_scale * log2(e)
-    int32_t nqg;           // int4 schedule units (GROUP tokens) per head
-    int32_t segu[3];       // bf16 schedule units (BUNIT tokens) per segment
-    int32_t nwg;           // pieces (workgroups) per head
+    const uint16_t* q;     // dwords 0-1
+    const uint8_t* kp;     // 2-3
+    const uint8_t* vp;     // 4-5
+    const uint16_t* ks;    // 6-7
+    const uint16_t* vs;    // 8-9
+    const uint16_t* sk[3]; // 10-15
+    const uint16_t* sv[3]; // 16-21
+    const int32_t* len_q;  // 22-23  optional per-head valid prefix tokens
+    const int32_t* len_s0; // 24-25  optional per-head valid tokens of segment 0
+    int32_t q_stride;      // 26
+    int32_t kp_bh, vp_bh, ks_bh, vs_bh;   // 27-30
+    int32_t sk_bh[3];      // 31-33
+    int32_t sv_bh[3];      // 34-36
+    int32_t n_quant;       // 37
+    int32_t sn[3];         // 38-40
+    int32_t G;             // 41
+    int32_t nqg;           // 42     int4 schedule units (GROUP tokens) per head
+    int32_t segu[2];       // 43-44  bf16 schedule units (BUNIT tokens) of segments 0 and 1
+    float qk_scale;        // 45     sm_scale * log2(e)
+    int32_t io;            // 46     HYQ_DT_* flags: fp16 q / fp16 segments / fp16 out
+    int32_t pad0;          // 47
+    // used once the stream is done (loaded with the prologue block, waited
+    // for after the stream)
+    uint16_t* out;         // 48-49
+    float* part;           // 50-51  [bh_kv][nwg][G][D] partial numerators
+    float* ml;             // 52-53  [bh_kv][nwg][G][2] = (m, l)
+    uint32_t* cnt;         // 54-55  arrival counter of head h at cnt[h * CNT_PAD]
+    int32_t out_stride;    // 56
+    int32_t nwg;           // 57     pieces (workgroups) per head
+    int32_t mj;            // 58     merge batch: partial columns per merging thread and load batch
+    int32_t bh_kv;         // 59
     int32_t bnd[MAX_NWG + 1];  // piece p: schedule units [bnd[p], bnd[p+1]) of its head
-    float* part;           // [bh_kv][nwg][G][D] partial numerators
-    float* ml;             // [bh_kv][nwg][G][2] = (m, l)
-    uint32_t* cnt;         // arrival counter of head h at cnt[h * CNT_PAD]
-    const int32_t* len_q;  // optional per-head valid prefix tokens
-    const int32_t* len_s0; // optional per-head valid tokens of segment 0
-    int32_t io;            // HYQ_DT_* flags: fp16 q / fp16 segments / fp16 out
-    int32_t mj;            // merge batch: partial columns per merging thread and load batch
 };
+constexpr int PRO_DWORDS = 48;
+static_assert(offsetof(DecArgs, pad0) == 4 * (PRO_DWORDS - 1), "prologue block layout");
+static_assert(offsetof(DecArgs, bh_kv) == 4 * 59, "epilogue block layout");
+
+typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+
+// The prologue block of the kernel arguments and this piece's bounds
+// (bnd[wg], bnd[wg + 1]) in one batch of scalar loads with one wait: left to
+// the compiler, they came in two batches (two round trips) before the first
+// vector load.  The epilogue block's loads are issued right after, into
+// registers of their own, and waited for by epilogue_args once the stream is
+// done (the compiler does not see these loads: its own lgkmcnt waits only
+// over-wait for them).
+struct KArgs {
+    u32x16 a, b, c;
+    u32x2 bnd;
+    u32x8 e0;              // dwords 48-55
+    u32x4 e1;              // dwords 56-59
+};
+__device__ __forceinline__ KArgs kernel_args(int wg) {
+    const char* const base = (const char*)__builtin_amdgcn_kernarg_segment_ptr();
+    const char* const bp = base + offsetof(DecArgs, bnd) + 4 * wg;
+    KArgs k;
+    asm volatile(
+        "s_load_dwordx16 %0, %4, 0x0\n\t"
+        "s_load_dwordx16 %1, %4, 0x40\n\t"
+        "s_load_dwordx16 %2, %4, 0x80\n\t"
+        "s_load_dwordx2 %3, %5, 0x0\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(k.a), "=&s"(k.b), "=&s"(k.c), "=&s"(k.bnd)
+        : "s"(base), "s"(bp)
+        : "memory");
+    asm volatile(
+        "s_load_dwordx8 %0, %2, 0xc0\n\t"
+        "s_load_dwordx4 %1, %2, 0xe0"
+        : "=&s"(k.e0), "=&s"(k.e1)
+        : "s"(base));
+    return k;
+}
+__device__ __forceinline__ void epilogue_args(KArgs& k) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(k.e0), "+s"(k.e1)::"memory");
+}
+// dword i of the prologue block
+__device__ __forceinline__ uint32_t kdw(const KArgs& k, int i) {
+    return i < 16 ? k.a[i] : i < 32 ? k.b[i - 16] : k.c[i - 32];
+}
+template <typename T>
+__device__ __forceinline__ T* kptr(const KArgs& k, int i) {
+    return reinterpret_cast<T*>(static_cast<uintptr_t>(kdw(k, i)) | (static_cast<uintptr_t>(kdw(k, i + 1)) << 32));
+}
+template <typename T>
+__device__ __forceinline__ T* eptr(const KArgs& k, int i) {
+    return reinterpret_cast<T*>(static_cast<uintptr_t>(k.e0[i]) | (static_cast<uintptr_t>(k.e0[i + 1]) << 32));
+}
+
+// ---------------------------------------------------------------------------
+// Phase trace (built only with -DHYQ_PHASE_TRACE, into a separate library:
+// `python -m hyquant_amd.build --trace`).  Every wavefront reads
+// s_memrealtime (a 100 MHz clock common to every XCD) at the phase points
+// below, keeps the stamps in SGPRs and stores them once at its end, into a
+// ring of the last TRACE_SLOTS launches (one record per wavefront).  The
+// workgroup that finishes a launch last advances the ring.
+// ---------------------------------------------------------------------------
+#ifdef HYQ_PHASE_TRACE
+constexpr int TRACE_SLOTS = 32;
+constexpr int TRACE_MAX_WG = 4096;
+constexpr int TRACE_PH = 14;
+//  0 entry                       7 arrival counter returned
+//  1 kernel arguments loaded
+//  2 Q arrived                   8 merge: (m, l) arrived       (merging
+//  3 first K/V group arrived     9 merge: partials summed       wavefronts of
+//  4 own stream done            10 merge: output acked          G <= 4 heads;
+//  5 all four wavefronts in LDS 11 merge: entered               else 0)
+//  6 partial stored, acknowledged 12 merge: loads issued
+//                               13 launch index (not a time)
+__device__ uint64_t g_trace[TRACE_SLOTS][TRACE_MAX_WG * 4][TRACE_PH];
+__device__ uint32_t g_trace_launch;
+__device__ uint32_t g_trace_done;
+#define HYQ_STAMP(i) (ph[i] = __builtin_amdgcn_s_memrealtime())
+#define TRACE_PARAM , uint64_t (&ph)[TRACE_PH]
+#define TRACE_ARG , ph
+#else
+#define HYQ_STAMP(i) ((void)0)
+#define TRACE_PARAM
+#define TRACE_ARG
+#endif
 
 struct WaveState {
     float m;               // running reference max of column g (same in the 4 lanes of g)
@@ -174,6 +274,31 @@ __device__ __forceinline__ float xor32_pair_max(float v) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float col_max(float v) { return xor32_pair_max(xor16_pair_max(v)); }
+
+// q.to(bf16) of an fp16 query (mask all ones) or the bf16 query unchanged
+// (mask zero), without a branch: a branch here made the compiler wait for the
+// Q loads at its join, before the first K/V loads were issued, which put the
+// whole Q round trip in front of the K/V stream.  Called after those loads;
+// the empty asm statements keep the compiler from hoisting the conversion
+// (and so the wait for Q) above them.
+__device__ __forceinline__ void q_to_bf16(u32x4 (&q)[4], uint32_t mask) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t w[4] = {q[i][0], q[i][1], q[i][2], q[i][3]};
+        asm volatile("" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]));
+        q[i] = u32x4{(f16x2_to_bf16x2(w[0]) & mask) | (w[0] & ~mask), (f16x2_to_bf16x2(w[1]) & mask) | (w[1] & ~mask),
+                     (f16x2_to_bf16x2(w[2]) & mask) | (w[2] & ~mask), (f16x2_to_bf16x2(w[3]) & mask) | (w[3] & ~mask)};
+    }
+}
+
+// One int32 through the scalar cache (a wave-uniform address written before
+// the launch): a vector load there would be waited for with vmcnt(0), which
+// also waits for the Q loads already in flight.
+__device__ __forceinline__ int sload_i32(const int32_t* p) {
+    int v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return v;
+}
 __device__ __forceinline__ float col_sum(float v) {
     auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
@@ -300,6 +425,13 @@ __device__ __forceinline__ void qload(QRaw<KB, VB>& r, const QCtx& x, int t0) {
             }
         }
     }
+    // scales (in the order qcompute uses them: after the K tiles, before the
+    // V rows): a 128-byte line of them is read by several instructions, so
+    // they keep the default cache policy
+    r.sk[0] = bld16(x.ks, x.slane, ss);
+    r.sk[1] = bld16(x.ks, x.slane + 32, ss);
+    r.sv[0] = bld16(x.vs, x.slane, ss);
+    r.sv[1] = bld16(x.vs, x.slane + 32, ss);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const uint32_t vo = x.vlane + slot_token(0, e) * prow(VB);
@@ -312,12 +444,6 @@ __device__ __forceinline__ void qload(QRaw<KB, VB>& r, const QCtx& x, int t0) {
             r.v[e][0] = w[0]; r.v[e][1] = w[1];
         }
     }
-    // scales: a 128-byte line of them is read by several instructions, so
-    // they keep the default cache policy
-    r.sk[0] = bld16(x.ks, x.slane, ss);
-    r.sk[1] = bld16(x.ks, x.slane + 32, ss);
-    r.sv[0] = bld16(x.vs, x.slane, ss);
-    r.sv[1] = bld16(x.vs, x.slane + 32, ss);
 }
 
 // QK A operand of MFMA m (channels 32kb + 8m + [0..7]) in slot order
@@ -614,38 +740,47 @@ __device__ __forceinline__ void store_out(const MergeArgs& a, int head, int g, i
 // (same-address reads broadcast), whose entries past nwg hold zero, and a
 // row swap adds the two halves.
 template <int MJ>
-__device__ __forceinline__ void merge_head_waves(const MergeArgs& a, int head, float* lds) {
+__device__ __forceinline__ void merge_head_waves(const MergeArgs& a, int head, float* lds TRACE_PARAM) {
     const int G = a.G, P = a.nwg;
     const int lane = threadIdx.x & 63;
     const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (g >= G) return;
+    HYQ_STAMP(11);
     const int h = lane >> 5, q = lane & 31;
     const int npair = P * G;
     const Rsrc rp = make_rsrc(a.part + static_cast<int64_t>(head) * npair * D, static_cast<uint32_t>(npair) * D * 4);
     const Rsrc rm = make_rsrc(a.ml + static_cast<int64_t>(head) * npair * 2, static_cast<uint32_t>(npair) * 8);
     float* wt = lds + g * MAX_NWG;
-    // (m, l) of partials lane, lane + 64, ... (past nwg: out of range, zeros)
-    u32x2 mlr[MAX_NWG / 64];
+    // (m, l) of partials lane, lane + 64, ... (past nwg: out of range, zeros);
+    // the host's choice of MJ covers every partial in one batch when nwg <=
+    // 48, so only the blocks of 64 that 2 MJ partials reach are loaded (a load
+    // past the range still takes the CU's address path, which bounds the merge)
+    constexpr int NML = MJ < 24 ? (2 * MJ + 63) / 64 : MAX_NWG / 64;
+    u32x2 mlr[NML];
 #pragma unroll
-    for (int k = 0; k < MAX_NWG / 64; ++k) mlr[k] = ld2_dev(rm, static_cast<uint32_t>(((lane + 64 * k) * G + g) * 8));
+    for (int k = 0; k < NML; ++k) mlr[k] = ld2_dev(rm, static_cast<uint32_t>(((lane + 64 * k) * G + g) * 8));
     const uint32_t pbase = static_cast<uint32_t>(((h * G + g) * D + 4 * q) * 4);
     const uint32_t pstep = static_cast<uint32_t>(2 * G * D * 4);
     f32x4 px[MJ];
 #pragma unroll
     for (int j = 0; j < MJ; ++j) px[j] = ld4_dev(rp, pbase + j * pstep);
+    HYQ_STAMP(12);
     float M = M_INIT;
 #pragma unroll
-    for (int k = 0; k < MAX_NWG / 64; ++k)
+    for (int k = 0; k < NML; ++k)
         if (lane + 64 * k < P) M = fmaxf(M, __uint_as_float(mlr[k][0]));
     M = wave_max64(M);
+    HYQ_STAMP(8);
     float den = 0.f;
 #pragma unroll
-    for (int k = 0; k < MAX_NWG / 64; ++k) {
+    for (int k = 0; k < NML; ++k) {
         const bool ok = lane + 64 * k < P;
         const float w = ok ? fast_exp2(__uint_as_float(mlr[k][0]) - M) : 0.f;
         den += ok ? w * __uint_as_float(mlr[k][1]) : 0.f;
         wt[lane + 64 * k] = w;
     }
+#pragma unroll
+    for (int k = NML; k < MAX_NWG / 64; ++k) wt[lane + 64 * k] = 0.f;
     den = wave_sum64(den);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -667,7 +802,12 @@ __device__ __forceinline__ void merge_head_waves(const MergeArgs& a, int head, f
         const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i]), false, false);
         acc[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
+    HYQ_STAMP(9);
     if (h == 0) store_out(a, head, g, q, acc, den);
+#ifdef HYQ_PHASE_TRACE
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    HYQ_STAMP(10);
+#endif
 }
 
 // MJ: items loaded per thread per batch (even; the host picks the smallest
@@ -787,41 +927,46 @@ constexpr int merge_items(int G, int nwg) {
 // ---------------------------------------------------------------------------
 template <int KB, int VB>
 __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
+#ifdef HYQ_PHASE_TRACE
+    uint64_t ph[TRACE_PH] = {};
+    HYQ_STAMP(0);
+    const uint32_t launch = __hip_atomic_load(&g_trace_launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#endif
     const int head = blockIdx.x;
     const int wg = blockIdx.y;                       // piece of the head
-    const int u0 = a.bnd[wg], u1 = a.bnd[wg + 1];    // its schedule units
-    // The kernel arguments the prologue branches on and the int4 and bf16
-    // addresses, read in one batch: left to the compiler, each load trails
-    // the branch that first uses it, one scalar round trip apiece.
-    const int nqg = a.nqg, nquant = a.n_quant;
-    const int32_t* const len_q = a.len_q;
-    const int32_t* const len_s0 = a.len_s0;
-    const uint8_t* const kp = a.kp; const uint8_t* const vp = a.vp;
-    const uint16_t* const ksp = a.ks; const uint16_t* const vsp = a.vs;
+    KArgs K = kernel_args(wg);
+    const int u0 = static_cast<int>(K.bnd[0]), u1 = static_cast<int>(K.bnd[1]);   // its schedule units
+    const uint16_t* const qp = kptr<const uint16_t>(K, 0);
+    const uint8_t* const kp = kptr<const uint8_t>(K, 2);
+    const uint8_t* const vp = kptr<const uint8_t>(K, 4);
+    const uint16_t* const ksp = kptr<const uint16_t>(K, 6);
+    const uint16_t* const vsp = kptr<const uint16_t>(K, 8);
+    const uint16_t* const sk0 = kptr<const uint16_t>(K, 10);
+    const uint16_t* const sk1 = kptr<const uint16_t>(K, 12);
+    const uint16_t* const sk2 = kptr<const uint16_t>(K, 14);
+    const uint16_t* const sv0 = kptr<const uint16_t>(K, 16);
+    const uint16_t* const sv1 = kptr<const uint16_t>(K, 18);
+    const uint16_t* const sv2 = kptr<const uint16_t>(K, 20);
+    const int32_t* const len_q = kptr<const int32_t>(K, 22);
+    const int32_t* const len_s0 = kptr<const int32_t>(K, 24);
+    const int32_t q_stride = static_cast<int32_t>(kdw(K, 26));
     // head strides fit 32 bits (the host checks); products are formed in 64
-    const int32_t kp_bh = static_cast<int32_t>(a.kp_bh), vp_bh = static_cast<int32_t>(a.vp_bh);
-    const int32_t ks_bh = static_cast<int32_t>(a.ks_bh), vs_bh = static_cast<int32_t>(a.vs_bh);
-    const uint16_t* const sk0 = a.sk[0]; const uint16_t* const sk1 = a.sk[1]; const uint16_t* const sk2 = a.sk[2];
-    const uint16_t* const sv0 = a.sv[0]; const uint16_t* const sv1 = a.sv[1]; const uint16_t* const sv2 = a.sv[2];
-    const int32_t skb0 = static_cast<int32_t>(a.sk_bh[0]), skb1 = static_cast<int32_t>(a.sk_bh[1]);
-    const int32_t skb2 = static_cast<int32_t>(a.sk_bh[2]), svb0 = static_cast<int32_t>(a.sv_bh[0]);
-    const int32_t svb1 = static_cast<int32_t>(a.sv_bh[1]), svb2 = static_cast<int32_t>(a.sv_bh[2]);
-    const int sn0 = a.sn[0], sn1 = a.sn[1], sn2 = a.sn[2];
-    const int su0 = a.segu[0], su1 = a.segu[1];
-    const float qk_scale = a.qk_scale;
-    const int io = a.io;
-    const int mj = a.mj;
-    const MergeArgs ma{a.G, a.nwg, a.part, a.ml, a.out, a.out_stride, io & HYQ_DT_OUT_FP16};
-    uint32_t* const cnt = a.cnt;
-    asm volatile("" ::"s"(u0), "s"(u1), "s"(nqg), "s"(nquant), "s"(len_q), "s"(len_s0), "s"(kp), "s"(vp),
-                 "s"(ksp), "s"(vsp), "s"(kp_bh), "s"(vp_bh), "s"(ks_bh), "s"(vs_bh));
-    asm volatile("" ::"s"(sk0), "s"(sk1), "s"(sk2), "s"(sv0), "s"(sv1), "s"(sv2), "s"(skb0), "s"(skb1), "s"(skb2),
-                 "s"(svb0), "s"(svb1), "s"(svb2), "s"(sn0), "s"(sn1), "s"(sn2), "s"(su0), "s"(su1), "s"(qk_scale));
-    asm volatile("" ::"s"(ma.nwg), "s"(ma.part), "s"(ma.ml), "s"(ma.out), "s"(ma.out_stride), "s"(cnt), "s"(mj));
+    const int32_t kp_bh = static_cast<int32_t>(kdw(K, 27)), vp_bh = static_cast<int32_t>(kdw(K, 28));
+    const int32_t ks_bh = static_cast<int32_t>(kdw(K, 29)), vs_bh = static_cast<int32_t>(kdw(K, 30));
+    const int32_t skb0 = static_cast<int32_t>(kdw(K, 31)), skb1 = static_cast<int32_t>(kdw(K, 32));
+    const int32_t skb2 = static_cast<int32_t>(kdw(K, 33)), svb0 = static_cast<int32_t>(kdw(K, 34));
+    const int32_t svb1 = static_cast<int32_t>(kdw(K, 35)), svb2 = static_cast<int32_t>(kdw(K, 36));
+    const int nquant = static_cast<int>(kdw(K, 37));
+    const int sn0 = static_cast<int>(kdw(K, 38)), sn1 = static_cast<int>(kdw(K, 39)), sn2 = static_cast<int>(kdw(K, 40));
+    const int G = static_cast<int>(kdw(K, 41));
+    const int nqg = static_cast<int>(kdw(K, 42));
+    const int su0 = static_cast<int>(kdw(K, 43)), su1 = static_cast<int>(kdw(K, 44));
+    const float qk_scale = __uint_as_float(kdw(K, 45));
+    const int io = static_cast<int>(kdw(K, 46));
+    HYQ_STAMP(1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, kb = lane >> 4;
-    const int G = a.G;
 
     extern __shared__ float s_acc[];               // [WAVES][G][D+1]; later the merge weights
     __shared__ float s_m[WAVES][16];
@@ -838,24 +983,22 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
     // Q row of head c (zero for padding columns c >= G): channels 32kb..32kb+31
     u32x4 qraw[4];
     {
-        const Rsrc rq = make_rsrc(a.q + static_cast<int64_t>(head) * G * a.q_stride,
-                                  static_cast<uint32_t>(G * a.q_stride * 2));
-        const uint32_t qo = static_cast<uint32_t>(c * a.q_stride * 2 + 64 * kb);
+        const Rsrc rq = make_rsrc(qp + static_cast<int64_t>(head) * G * q_stride,
+                                  static_cast<uint32_t>(G * q_stride * 2));
+        const uint32_t qo = static_cast<uint32_t>(c * q_stride * 2 + 64 * kb);
 #pragma unroll
         for (int i = 0; i < 4; ++i) qraw[i] = bld128(rq, qo + 16 * i);
-        if (io & HYQ_DT_Q_FP16) {   // q.to(bf16), as the reference's Q loads
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) qraw[i][j] = f16x2_to_bf16x2(qraw[i][j]);
-        }
     }
+    // an fp16 query is rounded to bf16 (as the reference's Q loads) once the
+    // first K/V loads are in flight
+    uint32_t q16 = (io & HYQ_DT_Q_FP16) ? ~0u : 0u;
+    asm volatile("" : "+s"(q16));
 
     if (u0 < nqg) {
         // ---------------- int4 part: groups wave, wave+WAVES, ... ----------------
         const int lo = u0 * GROUP;
         int nq = nquant;
-        if (len_q != nullptr) nq = min(nq, max(0, len_q[head]));
+        if (len_q != nullptr) nq = min(nq, max(0, sload_i32(len_q + head)));
         const int ntok = max(0, min((min(u1, nqg) - u0) * GROUP, nq - lo));   // 0: past a ragged head's end
         QCtx x;
         x.k = make_rsrc(kp + static_cast<int64_t>(head) * kp_bh + static_cast<int64_t>(lo) * prow(KB),
@@ -874,8 +1017,21 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         const int nmine = ngrp > wave ? (ngrp - wave + WAVES - 1) / WAVES : 0;
         const int t0 = wave * GROUP;
         QRaw<KB, VB> b0, b1, b2;
+        // in issue order (the scheduler would otherwise group the three
+        // groups' loads by kind, which puts the first group's last load near
+        // the end and its wait near a full drain)
         qload(b0, x, t0);
+        __builtin_amdgcn_sched_barrier(0);
         qload(b1, x, t0 + STRIDE);
+        __builtin_amdgcn_sched_barrier(0);
+        qload(b2, x, t0 + 2 * STRIDE);
+        __builtin_amdgcn_sched_barrier(0);
+        q_to_bf16(qraw, q16);
+        HYQ_STAMP(2);
+#ifdef HYQ_PHASE_TRACE
+        asm volatile("" ::"v"(b0.sv[1]));   // the last load of the first group
+        HYQ_STAMP(3);
+#endif
 
         // Q -> fp16 in int4 slot order, pre-scaled by 2^-ex so |q| < 2^15
         float qf[32];
@@ -907,17 +1063,33 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         // the K operands are u * 2^-24 (k_operand): 2^24 goes into the score scale
         const float qk = qk_scale * ldexpf(1.0f, ex + 24);
         const f32x4 kbias = k_bias<KB>(qop);
-        for (int i = 0; i < nmine; i += 3) {
-            const int t = t0 + i * STRIDE;
-            qload(b2, x, t + 2 * STRIDE);
-            qcompute(st, b0, qop, kbias, ntok - t, lane, qk);
-            if (i + 1 >= nmine) break;
-            qload(b0, x, t + 3 * STRIDE);
-            qcompute(st, b1, qop, kbias, ntok - t - STRIDE, lane, qk);
-            if (i + 2 >= nmine) break;
-            qload(b1, x, t + 4 * STRIDE);
-            qcompute(st, b2, qop, kbias, ntok - t - 2 * STRIDE, lane, qk);
-        }
+        // First round peeled (its three groups' loads were all issued before
+        // the wait for Q; straight-line code keeps the compiler's waits exact),
+        // then the ring: each round issues a group's loads before computing
+        // the oldest, two groups in flight while one is computed.
+        do {
+            qcompute(st, b0, qop, kbias, ntok - t0, lane, qk);
+            if (nmine <= 1) break;
+            qload(b0, x, t0 + 3 * STRIDE);
+            qcompute(st, b1, qop, kbias, ntok - t0 - STRIDE, lane, qk);
+            if (nmine <= 2) break;
+            qload(b1, x, t0 + 4 * STRIDE);
+            qcompute(st, b2, qop, kbias, ntok - t0 - 2 * STRIDE, lane, qk);
+            for (int i = 3; i < nmine; i += 3) {
+                const int t = t0 + i * STRIDE;
+                qload(b2, x, t + 2 * STRIDE);
+                __builtin_amdgcn_sched_barrier(0);
+                qcompute(st, b0, qop, kbias, ntok - t, lane, qk);
+                if (i + 1 >= nmine) break;
+                qload(b0, x, t + 3 * STRIDE);
+                __builtin_amdgcn_sched_barrier(0);
+                qcompute(st, b1, qop, kbias, ntok - t - STRIDE, lane, qk);
+                if (i + 2 >= nmine) break;
+                qload(b1, x, t + 4 * STRIDE);
+                __builtin_amdgcn_sched_barrier(0);
+                qcompute(st, b2, qop, kbias, ntok - t - 2 * STRIDE, lane, qk);
+            }
+        } while (false);
         // remove the offset of the V operands: acc -= offset * sum_t P'
         const float corr = v_offset<VB>() * st.ones[0];
 #pragma unroll
@@ -927,8 +1099,6 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
         // (a piece never holds both int4 and bf16 tokens: make_plan cuts at
         // the segment boundaries, so the Q copies of one part are dead
         // during the other's loop)
-        const bf16x8 qb[4] = {__builtin_bit_cast(bf16x8, qraw[0]), __builtin_bit_cast(bf16x8, qraw[1]),
-                              __builtin_bit_cast(bf16x8, qraw[2]), __builtin_bit_cast(bf16x8, qraw[3])};
         // fp16 segments (an fp16 model's cache) are rounded to bf16 after
         // their loads, as the reference's .to(tl.bfloat16) of each tile
         const bool seg16 = io & HYQ_DT_SEG_FP16;
@@ -940,7 +1110,7 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
             if (ua >= ub) continue;
             const int lo = (ua - sb) * BUNIT;
             int seg_len = seg == 0 ? sn0 : seg == 1 ? sn1 : sn2;
-            if (seg == 0 && len_s0 != nullptr) seg_len = min(seg_len, max(0, len_s0[head]));
+            if (seg == 0 && len_s0 != nullptr) seg_len = min(seg_len, max(0, sload_i32(len_s0 + head)));
             const int n = max(0, min((ub - ua) * BUNIT, seg_len - lo));     // 0: past a ragged head's end
             const uint16_t* const skp = seg == 0 ? sk0 : seg == 1 ? sk1 : sk2;
             const uint16_t* const svp = seg == 0 ? sv0 : seg == 1 ? sv1 : sv2;
@@ -957,20 +1127,45 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
             const int t0 = wave * TILE;
             Bf16Raw r0, r1;
             bf16_load(r0, rk, rv, t0, lane);
+            bf16_load(r1, rk, rv, t0 + TSTRIDE, lane);
+            u32x4 qs[4] = {qraw[0], qraw[1], qraw[2], qraw[3]};
+            q_to_bf16(qs, q16);
+#ifdef HYQ_PHASE_TRACE
+            if (ph[2] == 0) {
+                HYQ_STAMP(2);
+                asm volatile("" ::"v"(r0.v[3][3]));   // the last load of the first tile
+                HYQ_STAMP(3);
+            }
+#endif
+            const bf16x8 qb[4] = {__builtin_bit_cast(bf16x8, qs[0]), __builtin_bit_cast(bf16x8, qs[1]),
+                                  __builtin_bit_cast(bf16x8, qs[2]), __builtin_bit_cast(bf16x8, qs[3])};
+            // the ring: the tile two ahead is loaded into the slot just computed
             for (int i = 0; i < nmine; i += 2) {
                 const int t = t0 + i * TSTRIDE;
-                bf16_load(r1, rk, rv, t + TSTRIDE, lane);
                 if (seg16) f16_to_bf16(r0);
                 bf16_compute(st, r0, qb, n - t, lane, qk_scale);
                 if (i + 1 >= nmine) break;
                 bf16_load(r0, rk, rv, t + 2 * TSTRIDE, lane);
                 if (seg16) f16_to_bf16(r1);
                 bf16_compute(st, r1, qb, n - t - TSTRIDE, lane, qk_scale);
+                if (i + 2 >= nmine) break;
+                bf16_load(r1, rk, rv, t + 3 * TSTRIDE, lane);
             }
         }
     }
 
     // ---- wave -> LDS ----------------------------------------------------------
+    HYQ_STAMP(4);
+    epilogue_args(K);
+    const int mj = static_cast<int>(K.e1[2]);
+    const MergeArgs ma{G, static_cast<int>(K.e1[1]), eptr<const float>(K, 2), eptr<const float>(K, 4),
+                       eptr<uint16_t>(K, 0), static_cast<int64_t>(static_cast<int32_t>(K.e1[0])),
+                       io & HYQ_DT_OUT_FP16};
+    uint32_t* const cnt = eptr<uint32_t>(K, 6);
+    // The rings' last loads (past the piece's end: zeros, no memory access)
+    // are drained here, with a wait the compiler sees, so that it has no
+    // stale loads to wait for among the stores below.
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
     st.l = col_sum(st.l);
     if (kb == 0) {
         s_m[wave][c] = st.m;
@@ -984,6 +1179,7 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
             for (int i = 0; i < 4; ++i) row[32 * kb + 8 * i + nb] = st.acc[nb][i];
     }
     __syncthreads();
+    HYQ_STAMP(5);
 
     // ---- workgroup merge -> partial acc[G][D] and (m, l)[G] ----------------------
     const int64_t slot = static_cast<int64_t>(head) * ma.nwg + wg;
@@ -1019,25 +1215,43 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
     // every store of this workgroup acknowledged before its arrival is counted
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    HYQ_STAMP(6);
     if (threadIdx.x == 0) {
         const uint32_t old = __hip_atomic_fetch_add(cnt + head * CNT_PAD, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = (old == static_cast<uint32_t>(ma.nwg - 1));
     }
     __syncthreads();
+    HYQ_STAMP(7);
     if (s_last) {
         if (threadIdx.x == 0) __hip_atomic_store(cnt + head * CNT_PAD, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         switch (mj) {      // G <= 4: merge_head_waves, pairs per lane; G > 4: merge_head_cols, items per thread
-            case 4: merge_head_waves<4>(ma, head, s_acc); break;
-            case 8: merge_head_waves<8>(ma, head, s_acc); break;
-            case 12: merge_head_waves<12>(ma, head, s_acc); break;
-            case 16: merge_head_waves<16>(ma, head, s_acc); break;
-            case 20: merge_head_waves<20>(ma, head, s_acc); break;
-            case 24: merge_head_waves<24>(ma, head, s_acc); break;
+            case 4: merge_head_waves<4>(ma, head, s_acc TRACE_ARG); break;
+            case 8: merge_head_waves<8>(ma, head, s_acc TRACE_ARG); break;
+            case 12: merge_head_waves<12>(ma, head, s_acc TRACE_ARG); break;
+            case 16: merge_head_waves<16>(ma, head, s_acc TRACE_ARG); break;
+            case 20: merge_head_waves<20>(ma, head, s_acc TRACE_ARG); break;
+            case 24: merge_head_waves<24>(ma, head, s_acc TRACE_ARG); break;
             case 108: merge_head_cols<8>(ma, head, s_acc); break;
             case 116: merge_head_cols<16>(ma, head, s_acc); break;
             default: merge_head_cols<24>(ma, head, s_acc); break;
         }
     }
+#ifdef HYQ_PHASE_TRACE
+    const uint32_t lwg = blockIdx.y * gridDim.x + blockIdx.x;
+    if (lane == 0 && lwg < TRACE_MAX_WG) {
+        ph[13] = launch;
+        uint64_t* dst = g_trace[launch % TRACE_SLOTS][lwg * 4 + wave];
+        for (int i = 0; i < TRACE_PH; ++i) dst[i] = ph[i];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t total = gridDim.x * gridDim.y;
+        if (__hip_atomic_fetch_add(&g_trace_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1) {
+            __hip_atomic_store(&g_trace_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(&g_trace_launch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -1253,6 +1467,7 @@ int validate(const hyq_decode_params* p) {
     if (static_cast<int64_t>(p->kv_repeat) * p->q_stride * 2 > 0x7fffffffLL) return fail(HYQ_ENOTSUP, "q row stride too large");
     if (!aligned(p->out, 8) || p->out_stride % 4 || p->out_stride < D)
         return fail(HYQ_EINVAL, "out must be 8-byte aligned with row stride % 4 == 0 and >= head_dim");
+    if (!fits31(p->out_stride)) return fail(HYQ_ENOTSUP, "out row stride must lie in [0, 2^31)");
     if (p->n_quant > 0) {
         if (!p->k_packed || !p->v_packed || !p->k_scale || !p->v_scale) return fail(HYQ_EINVAL, "null prefix tensor");
         if (p->kp_stride_n != prow(p->k_bits) || p->vp_stride_n != prow(p->v_bits))
@@ -1301,21 +1516,21 @@ namespace {
 // 256-byte aligned, its counter area zero).
 int launch_decode(const hyq_decode_params* p, const Plan& pl, const Layout& L, void* workspace, void* stream) {
     DecArgs a{};
-    a.q = p->q; a.q_stride = p->q_stride;
-    a.out = p->out; a.out_stride = p->out_stride;
+    a.q = p->q; a.q_stride = static_cast<int32_t>(p->q_stride);
+    a.out = p->out; a.out_stride = static_cast<int32_t>(p->out_stride);
     a.io = p->dtype_flags;
-    a.kp = reinterpret_cast<const uint8_t*>(p->k_packed); a.kp_bh = p->kp_stride_bh; a.kp_n = p->kp_stride_n;
-    a.vp = reinterpret_cast<const uint8_t*>(p->v_packed); a.vp_bh = p->vp_stride_bh; a.vp_n = p->vp_stride_n;
-    a.ks = p->k_scale; a.ks_bh = p->ks_stride_bh;
-    a.vs = p->v_scale; a.vs_bh = p->vs_stride_bh;
+    a.kp = reinterpret_cast<const uint8_t*>(p->k_packed); a.kp_bh = static_cast<int32_t>(p->kp_stride_bh);
+    a.vp = reinterpret_cast<const uint8_t*>(p->v_packed); a.vp_bh = static_cast<int32_t>(p->vp_stride_bh);
+    a.ks = p->k_scale; a.ks_bh = static_cast<int32_t>(p->ks_stride_bh);
+    a.vs = p->v_scale; a.vs_bh = static_cast<int32_t>(p->vs_stride_bh);
     a.n_quant = static_cast<int32_t>(p->n_quant);
     for (int s = 0; s < 3; ++s) {
         a.sk[s] = p->seg_k[s]; a.sv[s] = p->seg_v[s];
-        a.sk_bh[s] = p->seg_k_stride_bh[s]; a.sk_n[s] = p->seg_k_stride_n[s];
-        a.sv_bh[s] = p->seg_v_stride_bh[s]; a.sv_n[s] = p->seg_v_stride_n[s];
+        a.sk_bh[s] = static_cast<int32_t>(p->seg_k_stride_bh[s]);
+        a.sv_bh[s] = static_cast<int32_t>(p->seg_v_stride_bh[s]);
         a.sn[s] = static_cast<int32_t>(p->seg_n[s]);
-        a.segu[s] = pl.segu[s];
     }
+    a.segu[0] = pl.segu[0]; a.segu[1] = pl.segu[1];
     a.G = p->kv_repeat;
     a.bh_kv = p->bh_kv;
     a.qk_scale = p->sm_scale * LOG2E;
@@ -1426,6 +1641,24 @@ extern "C" int hyq_decode_hybrid_noalloc(const hyq_decode_params* p, void* strea
     if (rc != HYQ_OK) return rc;
     return launch_decode(p, pl, L, ws, stream);
 }
+
+#ifdef HYQ_PHASE_TRACE
+// Copies the trace ring (TRACE_SLOTS x 4 TRACE_MAX_WG x TRACE_PH uint64) and
+// the number of launches recorded to the host; trace build only.
+extern "C" int hyq_phase_trace_read(uint64_t* dst, size_t bytes, uint32_t* launches) {
+    const size_t need = sizeof(uint64_t) * TRACE_SLOTS * TRACE_MAX_WG * 4 * TRACE_PH;
+    if (bytes < need) return fail(HYQ_ENOSPC, "phase trace buffer too small");
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_trace), need) != hipSuccess ||
+        hipMemcpyFromSymbol(launches, HIP_SYMBOL(g_trace_launch), sizeof(uint32_t)) != hipSuccess)
+        return fail(HYQ_EDEVICE, "phase trace copy failed");
+    return HYQ_OK;
+}
+extern "C" int hyq_phase_trace_geometry(int32_t* slots, int32_t* max_wg, int32_t* phases) {
+    *slots = TRACE_SLOTS; *max_wg = TRACE_MAX_WG * 4; *phases = TRACE_PH;
+    return HYQ_OK;
+}
+#endif
 
 extern "C" size_t hyq_decode_bf16_workspace_size(int32_t bh_kv, int32_t kv_repeat, int64_t n, int32_t d) {
     if (bh_kv < 0 || kv_repeat < 1 || kv_repeat > 16 || d != D || n < 0) return 0;

@@ -71,8 +71,12 @@ constexpr float PF_M_INIT = -1.0e30f;
 constexpr float FP8_MAX = 448.0f;        // src/ops/sage_unified_fp8.py:44
 constexpr float S_FP8_OFFSET = 8.807f;   // vendor/sageattention/csrc/qattn/attn_utils.cuh:30 (log2 448)
 constexpr int LIST_THREADS = 1024;
-constexpr int64_t MAX_T = 1 << 26;        // vertical indices per head
-constexpr int64_t MAX_P = 1 << 26;        // prefix positions N - W per head
+// The main kernel's buffer descriptors take 32-bit byte sizes and offsets:
+// fp16 rows of 256 bytes (rest V, vertical rows, the window) stay below 2^32
+// bytes per head up to 2^24 rows, so a head has at most 2^24 positions.
+constexpr int64_t MAX_N = 1 << 24;        // sequence length per head
+constexpr int64_t MAX_T = 1 << 24;        // vertical indices per head
+constexpr int64_t MAX_P = 1 << 24;        // prefix positions N - W per head
 constexpr int STAT_ROWS = 128;           // rows per kv_stats chunk
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -1525,8 +1529,8 @@ extern "C" int hyq_prefill_lists(const int64_t* vidx, int64_t vi_b, int64_t vi_h
     if (b < 0 || h < 0 || n < 0 || t < 0 || window < 0 || n > INT32_MAX / 2)
         return fail(HYQ_EINVAL, "hyq_prefill_lists: invalid sizes");
     const int64_t P = std::max<int64_t>(0, n - window);
-    if (P > MAX_P) return fail(HYQ_ENOTSUP, "hyq_prefill_lists: n - window exceeds 2^26");
-    if (t > MAX_T) return fail(HYQ_ENOTSUP, "hyq_prefill_lists: more than 2^26 indices per head");
+    if (P > MAX_P) return fail(HYQ_ENOTSUP, "hyq_prefill_lists: n - window exceeds 2^24");
+    if (t > MAX_T) return fail(HYQ_ENOTSUP, "hyq_prefill_lists: more than 2^24 indices per head");
     if (b == 0 || h == 0 || n == 0) return HYQ_OK;
     const int nblk = static_cast<int>((n + BM - 1) / BM);
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1561,8 +1565,9 @@ int prefill_run(const hyq_prefill_params* p, void* ws, size_t ws_bytes, hipStrea
     if (B <= 0 || HQ <= 0 || HKV <= 0 || HQ % HKV || N <= 0 || N > INT32_MAX / 2 || T < 0 || W < 0)
         return fail(HYQ_EINVAL, name + ": invalid sizes (need HQ % HKV == 0, N > 0)");
     const int64_t P = std::max<int64_t>(0, N - W);
-    if (P > MAX_P) return fail(HYQ_ENOTSUP, name + ": N - window exceeds 2^26");
-    if (T > MAX_T) return fail(HYQ_ENOTSUP, name + ": more than 2^26 vertical indices per head");
+    if (N > MAX_N) return fail(HYQ_ENOTSUP, name + ": sequence length exceeds 2^24");
+    if (P > MAX_P) return fail(HYQ_ENOTSUP, name + ": N - window exceeds 2^24");
+    if (T > MAX_T) return fail(HYQ_ENOTSUP, name + ": more than 2^24 vertical indices per head");
     if (!p->q || !p->k || !p->v || !p->out || (P > 0 && T > 0 && !p->vidx))
         return fail(HYQ_EINVAL, name + ": null pointer");
     auto rows16 = [](const void* ptr, int64_t sb, int64_t sh, int64_t sn) {

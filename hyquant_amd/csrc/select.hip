@@ -43,6 +43,7 @@ namespace {
 constexpr int TOPK_THREADS = 512;
 constexpr int64_t TOPK_NARROW_P = 65536;   // rows up to this long use 32-bit composites (16-bit index)
 constexpr int64_t TOPK_MAX_P = 0x7fffffff; // 64-bit composites carry a 32-bit index
+constexpr int TOPK_MAX_T = 1 << 30;         // the sort's power-of-two size n2 stays an int
 
 
 __device__ __forceinline__ double bf16_bits_to_f64(uint16_t b) { return static_cast<double>(bf16_to_f32(b)); }
@@ -847,7 +848,7 @@ SelectLayout select_layout(int B, int H_out, int64_t P, int T, const TopkPlan& t
 using namespace hyq;
 
 extern "C" size_t hyq_vertical_select_workspace_size(int32_t b, int32_t h_out, int64_t p, int32_t top_k) {
-    if (b < 0 || h_out < 0 || p < 0 || top_k < 0 || p > TOPK_MAX_P) return 0;
+    if (b < 0 || h_out < 0 || p < 0 || top_k < 0 || p > TOPK_MAX_P || top_k > TOPK_MAX_T) return 0;
     const TopkPlan tp = topk_plan(p, top_k, topk_lds_budget());
     return select_layout(b, h_out, p, top_k, tp).total;
 }
@@ -867,6 +868,7 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
     if (p <= 0 || top_k <= 0 || b == 0) return HYQ_OK;
     if (top_k > p) return fail(HYQ_EINVAL, "hyq_vertical_select: top_k > prefix length");
     if (p > TOPK_MAX_P) return fail(HYQ_ENOTSUP, "hyq_vertical_select: prefix longer than 2^31 - 1");
+    if (top_k > TOPK_MAX_T) return fail(HYQ_ENOTSUP, "hyq_vertical_select: top_k above 2^30");
     if (tail <= 0 || tail > q_len) return fail(HYQ_EINVAL, "hyq_vertical_select: bad query tail");
     if (!q || !k || !out_idx) return fail(HYQ_EINVAL, "hyq_vertical_select: null pointer");
     if (!aligned(k, 16) || ks_n % 8 || ks_h % 8 || ks_b % 8) return fail(HYQ_EINVAL, "hyq_vertical_select: keys must be 16-byte aligned rows");

@@ -8,7 +8,9 @@ kernels of libhyq.so on the current HIP stream of the input's device.
 
 from __future__ import annotations
 
+import ctypes
 import math
+import struct
 import threading
 from typing import Optional, Tuple
 
@@ -220,8 +222,133 @@ def fused_d_stage_decode(
     (one dtype for the segments): fp16 values are rounded to bf16 before the
     products, as the reference's kernels do (src/ops/decode_d_stage.py:537-541),
     and the fp32 result is rounded once to q.dtype (:866)."""
+    out = _fast_decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk, k_staging, v_staging,
+                       k_window, v_window, k_bits, v_bits, kv_repeat, sm_scale, split_tokens)
+    if out is not None:
+        return out
     return _decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk, k_staging, v_staging,
                    k_window, v_window, k_bits, v_bits, kv_repeat, sm_scale, split_tokens, None, None)
+
+
+# ---------------------------------------------------------------------------
+# the per-call host path
+# ---------------------------------------------------------------------------
+# A decode call is a few microseconds of GPU time, so the host side of an
+# eager call matters (once per layer per token in HF generate()).  The fast
+# path reads each tensor's data pointer, stride tuple and shape once, packs
+# every field of hyq_decode_params with one precompiled struct.pack_into into
+# a per-thread parameter block, and makes one library call, which validates
+# (alignment, strides, sizes) and launches.  Whatever the fast path does not
+# take (a non-unit channel stride, mixed segment dtypes, a bad argument the
+# library rejects with EINVAL) goes through the checked path (_decode), which
+# copies, or raises the reference's errors; a rejected call launches nothing.
+
+
+def _params_struct() -> struct.Struct:
+    """struct.Struct of hyq_decode_params in field order, built from the
+    ctypes mirror's offsets (little-endian, explicit padding)."""
+    codes = {ctypes.c_void_p: "Q", ctypes.c_int64: "q", ctypes.c_int32: "i", ctypes.c_float: "f"}
+    fmt, pos = "<", 0
+    for name, ctype in _lib.DecodeParams._fields_:
+        off = getattr(_lib.DecodeParams, name).offset
+        if off > pos:
+            fmt += f"{off - pos}x"
+        base, count = (ctype._type_, ctype._length_) if hasattr(ctype, "_length_") else (ctype, 1)
+        fmt += (str(count) if count > 1 else "") + codes[base]
+        pos = off + ctypes.sizeof(ctype)
+    size = ctypes.sizeof(_lib.DecodeParams)
+    if size > pos:
+        fmt += f"{size - pos}x"
+    st = struct.Struct(fmt)
+    assert st.size == size, (st.size, size)
+    return st
+
+
+_PSTRUCT = None
+_HYB = None
+_tls = threading.local()
+_BF16, _FP16 = torch.bfloat16, torch.float16
+
+
+def _seg(k, v):
+    """(k pointer, k head stride, k token stride, v pointer, v head stride,
+    v token stride, tokens, dtype) of one bf16 segment, or None when the
+    segment needs the checked path (channels not contiguous, K and V of
+    different lengths or dtypes)."""
+    n = k.shape[1]
+    if n == 0:
+        return (0, 0, 0, 0, 0, 0, 0, None)
+    a, b = k.stride(), v.stride()
+    d = k.dtype
+    if a[2] != 1 or b[2] != 1 or v.shape[1] != n or v.dtype is not d or (d is not _BF16 and d is not _FP16):
+        return None
+    return (k.data_ptr(), a[0], a[1], v.data_ptr(), b[0], b[1], n, d)
+
+
+def _fast_decode(q, kp, vp, ks, vs, kt, vt, kst, vst, kw, vw, k_bits, v_bits, kv_repeat, sm_scale, split_tokens):
+    """The eager fast path of fused_d_stage_decode; None when the call must
+    take the checked path (nothing was launched then).  Tensors of the wrong
+    rank fail an index or unpacking here and take the checked path too."""
+    global _PSTRUCT, _HYB
+    try:
+        qdt = q.dtype
+        if qdt is _BF16:
+            flags = 0
+        elif qdt is _FP16:
+            flags = 5                                  # HYQ_DT_Q_FP16 | HYQ_DT_OUT_FP16
+        else:
+            return None
+        BH_Q, D = q.shape
+        qs = q.stride()
+        if qs[1] != 1 or kv_repeat < 1 or BH_Q % kv_repeat or not q.is_cuda:
+            return None
+        s0, s1, s2 = _seg(kt, vt), _seg(kst, vst), _seg(kw, vw)
+        if s0 is None or s1 is None or s2 is None:
+            return None
+        dts = {s0[7], s1[7], s2[7]}
+        dts.discard(None)
+        if len(dts) > 1:
+            return None
+        if _FP16 in dts:
+            flags |= 2                                 # HYQ_DT_SEG_FP16
+        nq = kp.shape[1]
+        if nq > 0:
+            a, b, c, e = kp.stride(), vp.stride(), ks.stride(), vs.stride()
+            if a[2] != 1 or b[2] != 1 or c[1] != 1 or e[1] != 1:
+                return None
+            kpp, vpp, ksp, vsp = kp.data_ptr(), vp.data_ptr(), ks.data_ptr(), vs.data_ptr()
+        else:
+            a = b = c = e = (0, 0, 0)
+            kpp = vpp = ksp = vsp = 0
+    except (IndexError, ValueError, TypeError, AttributeError):
+        return None
+    out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    t = _tls
+    p = getattr(t, "p", None)
+    if p is None:
+        if _PSTRUCT is None:
+            _PSTRUCT = _params_struct()
+            _HYB = _lib.lib().hyq_decode_hybrid
+        p = t.p = _lib.DecodeParams()
+        t.ref = ctypes.byref(p)
+    _PSTRUCT.pack_into(
+        p, 0, q.data_ptr(), qs[0], out.data_ptr(), D, kpp, a[0], a[1], vpp, b[0], b[1], ksp, c[0], vsp, e[0], nq,
+        s0[0], s1[0], s2[0], s0[1], s1[1], s2[1], s0[2], s1[2], s2[2],
+        s0[3], s1[3], s2[3], s0[4], s1[4], s2[4], s0[5], s1[5], s2[5],
+        s0[6], s1[6], s2[6], BH_Q // kv_repeat, kv_repeat, D, k_bits, v_bits,
+        D ** -0.5 if sm_scale is None else float(sm_scale), int(split_tokens), 0, 0, flags)
+    dev = q.get_device()
+    stream = _raw_stream(dev) if _raw_stream is not None else torch.cuda.current_stream(dev).cuda_stream
+    ws = _ws_cache.get((dev, stream))
+    st = _HYB(t.ref, ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, stream)
+    if st == _lib.HYQ_ENOSPC:
+        L = _lib.lib()
+        ws = _workspace(q.device, stream, L.hyq_decode_workspace_size(t.ref))
+        st = _HYB(t.ref, ws.data_ptr(), ws.numel(), stream)
+    if st == _lib.HYQ_EINVAL:
+        return None
+    _lib.check(st, "fused_d_stage_decode")
+    return out
 
 
 def _decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk, k_staging, v_staging,

@@ -191,7 +191,7 @@ int hyq_decode_bf16(const uint16_t* q, int64_t q_stride, uint16_t* out, int64_t 
  * score = bf16(exact dot(qm, k)), top_k chosen by the caller
  * (reference: min(max(1, ceil(p * top_ratio)), p)).  is_fp16 = 1: q and k
  * are an fp16 model's, and the means and scores are rounded to fp16 (the
- * reference computes them in the model dtype).  d = 128, p < 2^31,
+ * reference computes them in the model dtype).  d = 128, p < 2^31, top_k <= 2^30,
  * top_k <= p, at most 16 output heads per key head.  The workspace size
  * depends on top_k: winner sets too large for LDS are sorted in it.
  */
@@ -264,7 +264,7 @@ int hyq_per_block_int8(const void* x, int32_t x_is_fp16, int64_t xs_b, int64_t x
  *   nr, nv int32 [b*h, ceil(n/128)]  entries of rest / vert below the window
  *                             start of each 128-row query block,
  *                             wla = floor64(max(0, 128 blk - (window - 1)))
- * vidx int64 [b, h, t] with strides (vi_b, vi_h, vi_t).  p, t <= 2^26.
+ * vidx int64 [b, h, t] with strides (vi_b, vi_h, vi_t).  p, t <= 2^24.
  * Workspace: hyq_prefill_lists_workspace_size(b, h, n, t, window) bytes, zero
  * (NULL allowed) while one head's lists fit the device's LDS, else a per-head
  * scratch for them, 4-byte aligned.
@@ -305,7 +305,8 @@ typedef struct hyq_prefill_params {
  * (int8 Q . int8 K with per-block scales), vertical positions below wla and
  * the causal window wla <= j <= i (fp16 Q . fp16 K); one softmax; bf16 out.
  * Workspace: hyq_prefill_workspace_size(...) bytes, 256-byte aligned.
- * Limits: head_dim 128, N - window <= 2^26, T <= 2^26.
+ * Limits: head_dim 128, N <= 2^24 (32-bit byte offsets of 256-byte rows per
+ * head), N - window <= 2^24, T <= 2^24.
  */
 size_t hyq_prefill_workspace_size(int32_t b, int32_t hq, int32_t hkv, int64_t n, int64_t t,
                                   int32_t window, int32_t pv_mode);

@@ -171,6 +171,40 @@ def test_prefill_unified_host_validation():
     assert L.hyq_prefill_unified(ctypes.byref(p), None, 0, None) == _lib.HYQ_EINVAL    # null tensors
 
 
+def test_prefill_length_limit():
+    """The prefill kernels address a head's 256-byte fp16 rows with 32-bit
+    byte offsets: a sequence longer than 2^24 (or that many prefix positions
+    or vertical indices) is ENOTSUP before anything is launched; 2^24 itself
+    passes the size checks and fails later on the null tensors."""
+    from hyquant_amd import _lib
+    L = _lib.lib()
+    for fn in (L.hyq_prefill_hybrid, L.hyq_prefill_hybrid_fp8qk):
+        p = _lib.PrefillParams()
+        p.batch, p.hq, p.hkv, p.head_dim, p.n, p.t, p.window = 1, 1, 1, 128, (1 << 24) + 1, 8, 128
+        assert fn(ctypes.byref(p), None, 0, None) == _lib.HYQ_ENOTSUP
+        assert b"2^24" in L.hyq_last_error()
+        p.n = 1 << 24
+        assert fn(ctypes.byref(p), None, 0, None) == _lib.HYQ_EINVAL
+        p.n, p.t = 4096, (1 << 24) + 1
+        assert fn(ctypes.byref(p), None, 0, None) == _lib.HYQ_ENOTSUP
+    p = _lib.PrefillParams()
+    p.batch, p.hq, p.hkv, p.head_dim, p.n, p.t, p.window = 1, 1, 1, 128, (1 << 24) + 1, 0, 0
+    assert L.hyq_prefill_unified(ctypes.byref(p), None, 0, None) == _lib.HYQ_ENOTSUP
+    assert L.hyq_prefill_lists(None, 0, 0, 0, 1, 1, (1 << 24) + 1, 8, 0, None, None, None, None, None,
+                               None, 0, None) == _lib.HYQ_ENOTSUP
+
+
+def test_select_top_k_limit():
+    """The selector's sort size is the power of two above top_k, kept in an
+    int: top_k above 2^30 is ENOTSUP before anything is launched."""
+    _lib, L = _L()
+    st = L.hyq_vertical_select(16, 0, 0, 128, 1, 1, 1, 16, 0, 0, 128, 1, (1 << 31) - 1, 1, 128, 1,
+                               (1 << 30) + 1, 0, 16, None, 0, None)
+    assert st == _lib.HYQ_ENOTSUP
+    assert b"2^30" in L.hyq_last_error()
+    assert L.hyq_vertical_select_workspace_size(1, 1, (1 << 31) - 1, (1 << 30) + 1) == 0
+
+
 def test_bf16_workspace_size():
     _lib, L = _L()
     assert L.hyq_decode_bf16_workspace_size(8, 4, 8192, 128) > 8 * 4 * 128 * 4

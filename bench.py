@@ -123,19 +123,21 @@ def time_rotating(fn, states, warmup, steps, replays=REPLAYS):
     Each replay (K steps, no host work between launches) is bracketed by HIP
     events on the stream, and the median replay gives the per-step time.
     Returns (graph_ms_per_step, eager_ms_per_step) where the eager figure
-    times K Python calls issued one by one."""
+    times max(K, 200) Python calls issued one by one (steady state: a short
+    burst after an idle GPU also times the clocks ramping up)."""
     n = len(states)
-    for i in range(warmup):
+    for i in range(max(warmup, 20)):
         fn(states[i % n])
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
+    ne = max(steps, 200)
     e0.record()
-    for i in range(steps):
+    for i in range(ne):
         fn(states[i % n])
     e1.record()
     torch.cuda.synchronize()
-    eager = e0.elapsed_time(e1) / steps
+    eager = e0.elapsed_time(e1) / ne
     graphs = []
     for j in range(max(1, -(-n // steps))):
         g = torch.cuda.CUDAGraph()

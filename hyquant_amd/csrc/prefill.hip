@@ -150,6 +150,16 @@ __device__ __forceinline__ i32x4 lds_rd128(uint32_t addr) {
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
     return r;
 }
+// a copy the compiler cannot see through: per-lane offsets derived from it
+// at their point of use are recomputed there rather than hoisted and held
+// in registers through loops that do not need them
+__device__ __forceinline__ uint32_t opaque_v(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+__device__ __forceinline__ void lds_wait2(i32x4& a, i32x4& b) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b));
+}
 __device__ __forceinline__ void lds_wait4(i32x4& a, i32x4& b, i32x4& c, i32x4& d) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
 }
@@ -733,29 +743,49 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     const int c16 = lane & 15, g = lane >> 4;
 
     // ---- Q block: load, quantise (int8 per block scale), fp16 copy --------
+    // q * c of sub-block sb, channels 64 cc + 16 g .. + 15 of row c16 (zeros
+    // past the last row)
+    auto q_chunk = [&](const uint16_t* qbase, int cr, int gr, int sb, int cc, float (&xv)[16])
+                       __attribute__((always_inline)) {
+        const int row = BM * blk + 32 * w + 16 * sb + cr;
+        const bool ok = row < a.N;
+        const uint16_t* qrow = qbase + b * a.q_b + h * a.q_h + static_cast<int64_t>(ok ? row : 0) * a.q_n;
+        u32x4 lo = {}, hi = {};
+        if (ok) {
+            lo = *reinterpret_cast<const u32x4*>(qrow + 64 * cc + 16 * gr);
+            hi = *reinterpret_cast<const u32x4*>(qrow + 64 * cc + 16 * gr + 8);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t wd = (e < 8) ? lo[e >> 1] : hi[(e - 8) >> 1];
+            xv[e] = half_to_f32(static_cast<uint16_t>((e & 1) ? (wd >> 16) : wd), a.f16) * a.c;
+        }
+    };
+    // the fp16 operand of the fp16 tiles: q_scaled = (q * c) in the model
+    // dtype, then .to(float16) (a bf16 model rounds twice, an fp16 model once)
+    f16x8 qh[2][4];
+    auto make_qh = [&](int sb, int cc, const float (&xv)[16]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const float* z = xv + 8 * hf;
+            float zr[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) zr[e] = a.f16 ? z[e] : bf16_round_f32(z[e]);
+            const u32x4 hv = {pack_f16x2(zr[0], zr[1]), pack_f16x2(zr[2], zr[3]), pack_f16x2(zr[4], zr[5]),
+                              pack_f16x2(zr[6], zr[7])};
+            qh[sb][2 * cc + hf] = __builtin_bit_cast(f16x8, hv);
+        }
+    };
     float x[2][2][16];
     float amax = 0.0f;
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-        const int row = BM * blk + 32 * w + 16 * sb + c16;
-        const bool ok = row < a.N;
-        const uint16_t* qrow = a.q + b * a.q_b + h * a.q_h + static_cast<int64_t>(ok ? row : 0) * a.q_n;
+    for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-            u32x4 lo = {}, hi = {};
-            if (ok) {
-                lo = *reinterpret_cast<const u32x4*>(qrow + 64 * cc + 16 * g);
-                hi = *reinterpret_cast<const u32x4*>(qrow + 64 * cc + 16 * g + 8);
-            }
+            q_chunk(a.q, c16, g, sb, cc, x[sb][cc]);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const uint32_t wd = (e < 8) ? lo[e >> 1] : hi[(e - 8) >> 1];
-                const float v = half_to_f32(static_cast<uint16_t>((e & 1) ? (wd >> 16) : wd), a.f16) * a.c;
-                x[sb][cc][e] = v;
-                amax = fmaxf(amax, fabsf(v));
-            }
+            for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(x[sb][cc][e]));
         }
-    }
     amax = wave_max(amax);
     if (lane == 0) s_red[w] = amax;
     __syncthreads();
@@ -766,7 +796,6 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     float q_scale = q_amax / (QF8 ? FP8_MAX : 127.0f);
     if (QF8 && !(q_scale > 0.0f)) q_scale = 1.0f;
     i32x4 q8[2][2];
-    f16x8 qh[2][4];
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
 #pragma unroll
@@ -781,18 +810,9 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                                        pb_code(xv[4 * i + 2], q_scale), pb_code(xv[4 * i + 3], q_scale));
             q8[sb][cc] = i32x4{static_cast<int>(wd[0]), static_cast<int>(wd[1]), static_cast<int>(wd[2]),
                                static_cast<int>(wd[3])};
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                const float* z = xv + 8 * hf;
-                // q_scaled = (q * c) in the model dtype, then .to(float16):
-                // a bf16 model rounds twice, an fp16 model once
-                float zr[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) zr[e] = a.f16 ? z[e] : bf16_round_f32(z[e]);
-                const u32x4 hv = {pack_f16x2(zr[0], zr[1]), pack_f16x2(zr[2], zr[3]), pack_f16x2(zr[4], zr[5]),
-                                  pack_f16x2(zr[6], zr[7])};
-                qh[sb][2 * cc + hf] = __builtin_bit_cast(f16x8, hv);
-            }
+            // the fp16 P.V kernels build this copy after the rest tiles (it
+            // is not held in registers through them)
+            if constexpr (PV8) make_qh(sb, cc, x[sb][cc]);
         }
     }
 
@@ -818,13 +838,19 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
     // picks the global chunk that belongs at its LDS position):
     //   K int8 / e4m3   position = chunk ^ (row & 7)
     //   K fp16          position = chunk ^ (row & 15)
-    //   V fp16          position = chunk ^ 2 (row & 3)
+    //   V fp16          position = chunk ^ 2 (row & 7)   (fp16 P.V kernels)
+    //                   position = chunk ^ 2 (row & 3)   (fp8 P.V kernel)
     //   V e4m3          position = chunk ^ ((row & 3) | 4 ((row >> 4) & 1))
     // One DMA writes 1 KiB: 8 rows of 128 B or 4 rows of 256 B; wavefront w
     // issues DMAs q = 2w, 2w + 1 (128-B rows) or q = 4w .. 4w + 3 (256-B
     // rows).  Rows past a source's valid rows read zeros (their scores are
     // masked and their P is zero).
     const uint32_t dk8 = static_cast<uint32_t>((lane >> 3) * RS8 + 16 * ((lane & 7) ^ (lane >> 3)));
+    const uint32_t dk16 = static_cast<uint32_t>((lane >> 4) * RS16 + 16 * ((lane & 15) ^ (lane >> 4)));
+    // (fp16 V with fp16 P.V: the 8 rows a 32-lane half of each transpose read
+    // touches sit on 8 distinct bank groups; DMA q writes rows 4q .. 4q + 3,
+    // so row & 7 is 4 (q & 1) + (lane >> 4) and the odd DMAs take this
+    // offset with 128 XOR-ed in)
     const uint32_t dv16 = static_cast<uint32_t>((lane >> 4) * RS16 + 16 * ((lane & 15) ^ (2 * ((lane >> 4) & 3))));
     const uint32_t dv8 = static_cast<uint32_t>((lane >> 3) * RS8 +
                                                16 * ((lane & 7) ^ (((lane >> 3) & 3) | ((w & 1) << 2))));
@@ -888,11 +914,10 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
             else if constexpr (KIND == T_VERT) return BN * (t - nrt);
             else return wla + BN * (t - nrt - nvt);
         };
-        // the DMAs of one tile into buffer pair par
-        auto issue = [&](auto KT, const Rsrc& rk, const Rsrc& rv, int i0, int par) __attribute__((always_inline)) {
+        // the K DMAs and the V DMAs of one tile into buffer par
+        auto issue_k = [&](auto KT, const Rsrc& rk, int i0, int par) __attribute__((always_inline)) {
             constexpr int KIND = decltype(KT)::value;
             uint8_t* kd = par ? s_k1 : s_k0;
-            uint8_t* vd = par ? s_v1 : s_v0;
             const uint32_t r0 = static_cast<uint32_t>(i0);
             if constexpr (KIND == T_REST) {
 #pragma unroll
@@ -901,14 +926,22 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                     pf_dma16(rk, kd + 1024 * q, dk8, r0 * RS8 + 1024 * q);
                 }
             } else {
+                // DMA q = 4 w + i writes rows 4 q + (lane >> 4), whose row & 15
+                // is 4 i + (lane >> 4): the source chunk is (lane & 15) ^
+                // (lane >> 4) ^ 4 i, i.e. the offset of i = 0 with 64 i
+                // XOR-ed in (recomputed here, not held through other runs)
+                const uint32_t vo0 = opaque_v(dk16);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int q = 4 * w + i;
-                    const uint32_t vo = static_cast<uint32_t>((lane >> 4) * RS16 +
-                                                              16 * ((lane & 15) ^ ((4 * i + (lane >> 4)) & 15)));
-                    pf_dma16(rk, kd + 1024 * q, vo, r0 * RS16 + 1024 * q);
+                    pf_dma16(rk, kd + 1024 * q, vo0 ^ (64u * i), r0 * RS16 + 1024 * q);
                 }
             }
+        };
+        auto issue_v = [&](auto KT, const Rsrc& rv, int i0, int par) __attribute__((always_inline)) {
+            constexpr int KIND = decltype(KT)::value;
+            uint8_t* vd = par ? s_v1 : s_v0;
+            const uint32_t r0 = static_cast<uint32_t>(i0);
             if constexpr (PV8 && KIND == T_REST) {
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
@@ -919,9 +952,13 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int q = 4 * w + i;
-                    pf_dma16(rv, vd + 1024 * q, dv16, r0 * RS16 + 1024 * q);
+                    pf_dma16(rv, vd + 1024 * q, (!PV8 && (i & 1)) ? (dv16 ^ 128u) : dv16, r0 * RS16 + 1024 * q);
                 }
             }
+        };
+        auto issue = [&](auto KT, const Rsrc& rk, const Rsrc& rv, int i0, int par) __attribute__((always_inline)) {
+            issue_k(KT, rk, i0, par);
+            issue_v(KT, rv, i0, par);
         };
         // the first tile of the run after KIND (the rare cross-run prefetch)
         auto issue_next_run = [&](auto KT, int t, int par) __attribute__((always_inline)) {
@@ -945,15 +982,13 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         //   fp16 K (256-B rows):   chunk 8 (m >> 1) + 2g + (m & 1) of row 16 kb + c16
         //   fp16 V (transposed):   the lds_tr16 addressing of channel block cb
         const uint32_t ok8a = c16 * RS8 + 16 * (g ^ (c16 & 7));
-        const uint32_t ok8b = c16 * RS8 + 16 * ((4 + g) ^ (c16 & 7));
-        uint32_t ok16[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) ok16[m] = c16 * RS16 + 16 * ((8 * (m >> 1) + 2 * g + (m & 1)) ^ c16);
-        uint32_t ov[4];            // channel blocks cb and cb + 4 differ by a constant 128 bytes
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
-            ov[cb] = (4 * g + (c16 >> 2)) * RS16 + 8 * (c16 & 1) +
-                     16 * ((2 * cb + ((c16 & 3) >> 1)) ^ (2 * ((c16 >> 2) & 3)));
+        // (ok16 of chunk 8 (m >> 1) + 2g + (m & 1) is that of m = 0 with
+        // 16 (m & 1) + 128 (m >> 1) XOR-ed in)
+        const uint32_t ok16 = c16 * RS16 + 16 * ((2 * g) ^ c16);
+        // (row 4 g + (c16 >> 2) + 16 k: chunk 2 cb + ((c16 & 3) >> 1) stored at
+        // chunk ^ 2 (row & 7); block cb is block 0 with 32 cb XOR-ed in)
+        const uint32_t ov0 = (4 * g + (c16 >> 2)) * RS16 + 8 * (c16 & 1) +
+                             16 * (((c16 & 3) >> 1) ^ (2 * ((4 * g + (c16 >> 2)) & 7)));
         // fp8 P.V kernel, vertical / window tiles: the V^T operand of
         // v_mfma_f32_32x32x16_f16 (32 channels x 16 keys): lane l = 16 G + j
         // receives channel 32 cbk + 16 (G & 1) + j of keys 16 kb + 8 (G >> 1) +
@@ -986,20 +1021,17 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         const uint32_t vbase[2] = {lds_addr(s_v0), lds_addr(s_v1)};
         const u32x4 onew = {0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};   // fp16 1.0
 
-        // S^T = K . Q^T of a rest tile (int8 or e4m3) from K at kb
-        auto qk_rest = [&](uint32_t kb, float (&s)[2][4][4]) __attribute__((always_inline)) {
-            i32x4 ka[4][2];
-            const uint32_t aa = kb + ok8a, ab = kb + ok8b;
-            ka[0][0] = lds_rd128<0 * 16 * RS8>(aa); ka[0][1] = lds_rd128<0 * 16 * RS8>(ab);
-            ka[1][0] = lds_rd128<1 * 16 * RS8>(aa); ka[1][1] = lds_rd128<1 * 16 * RS8>(ab);
-            ka[2][0] = lds_rd128<2 * 16 * RS8>(aa); ka[2][1] = lds_rd128<2 * 16 * RS8>(ab);
-            ka[3][0] = lds_rd128<3 * 16 * RS8>(aa); ka[3][1] = lds_rd128<3 * 16 * RS8>(ab);
-            lds_wait8(ka[0][0], ka[0][1], ka[1][0], ka[1][1], ka[2][0], ka[2][1], ka[3][0], ka[3][1]);
-#pragma unroll
-            for (int kbk = 0; kbk < 4; ++kbk) {
+        // S^T = K . Q^T of a rest tile (int8 or e4m3) from K at kb; the fp8
+        // P.V kernel reads the whole K block at once, the fp16 P.V kernels
+        // (whose pipelined steps hold two score tiles) key block kbk + 1
+        // during the MFMAs of kbk
+        // (RT: int8 scores stay raw int32 bits in s, converted by the caller)
+        auto qk_rest_t = [&](auto RT, uint32_t kb, float (&s)[2][4][4]) __attribute__((always_inline)) {
+            // (chunk 4 + g is chunk g with 64 bytes XOR-ed in)
+            const uint32_t aa = kb + ok8a, ab = kb + (opaque_v(ok8a) ^ 64u);
+            auto mm = [&](int kbk, const i32x4& k0, const i32x4& k1) __attribute__((always_inline)) {
                 if constexpr (QF8) {
-                    const i32x8 av = {ka[kbk][0][0], ka[kbk][0][1], ka[kbk][0][2], ka[kbk][0][3],
-                                      ka[kbk][1][0], ka[kbk][1][1], ka[kbk][1][2], ka[kbk][1][3]};
+                    const i32x8 av = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
 #pragma unroll
                     for (int sb = 0; sb < 2; ++sb) {
                         const i32x8 bv = {q8[sb][0][0], q8[sb][0][1], q8[sb][0][2], q8[sb][0][3],
@@ -1011,13 +1043,45 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                 } else {
 #pragma unroll
                     for (int sb = 0; sb < 2; ++sb) {
-                        i32x4 si = mfma_i8(ka[kbk][0], q8[sb][0], i32x4{0, 0, 0, 0});
-                        si = mfma_i8(ka[kbk][1], q8[sb][1], si);
+                        i32x4 si = mfma_i8(k0, q8[sb][0], i32x4{0, 0, 0, 0});
+                        si = mfma_i8(k1, q8[sb][1], si);
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) s[sb][kbk][r] = static_cast<float>(si[r]);
+                        for (int r = 0; r < 4; ++r) {
+                            // (the element is copied out first: a bit cast of a
+                            // vector element in place reads element 0)
+                            const int sr = si[r];
+                            s[sb][kbk][r] = decltype(RT)::value ? __builtin_bit_cast(float, sr) : static_cast<float>(sr);
+                        }
                     }
                 }
+            };
+            if constexpr (PV8) {
+                i32x4 ka[4][2];
+                ka[0][0] = lds_rd128<0 * 16 * RS8>(aa); ka[0][1] = lds_rd128<0 * 16 * RS8>(ab);
+                ka[1][0] = lds_rd128<1 * 16 * RS8>(aa); ka[1][1] = lds_rd128<1 * 16 * RS8>(ab);
+                ka[2][0] = lds_rd128<2 * 16 * RS8>(aa); ka[2][1] = lds_rd128<2 * 16 * RS8>(ab);
+                ka[3][0] = lds_rd128<3 * 16 * RS8>(aa); ka[3][1] = lds_rd128<3 * 16 * RS8>(ab);
+                lds_wait8(ka[0][0], ka[0][1], ka[1][0], ka[1][1], ka[2][0], ka[2][1], ka[3][0], ka[3][1]);
+#pragma unroll
+                for (int kbk = 0; kbk < 4; ++kbk) mm(kbk, ka[kbk][0], ka[kbk][1]);
+            } else {
+                i32x4 ka[2][2];        // [stage][half]
+                auto rd = [&](auto KBT, int st) __attribute__((always_inline)) {
+                    constexpr int OFF = 16 * RS8 * decltype(KBT)::value;
+                    ka[st][0] = lds_rd128<OFF>(aa);
+                    ka[st][1] = lds_rd128<OFF>(ab);
+                };
+                rd(std::integral_constant<int, 0>{}, 0);
+                static_for<4>([&](auto KBT) __attribute__((always_inline)) {
+                    constexpr int kbk = decltype(KBT)::value, st = kbk & 1;
+                    lds_wait2(ka[st][0], ka[st][1]);
+                    if constexpr (kbk + 1 < 4) rd(std::integral_constant<int, kbk + 1>{}, st ^ 1);
+                    mm(kbk, ka[st][0], ka[st][1]);
+                });
             }
+        };
+        auto qk_rest = [&](uint32_t kb, float (&s)[2][4][4]) __attribute__((always_inline)) {
+            qk_rest_t(std::false_type{}, kb, s);
         };
         // S^T = K . Q^T of an fp16 tile (vertical, window) from K at kb; the
         // reads of key block kbk + 1 in flight during the MFMAs of kbk
@@ -1028,7 +1092,8 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
 #pragma unroll
                 for (int kbk = 0; kbk < 4; ++kbk) sf[sb][kbk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             i32x4 kr[2][4];
-            const uint32_t ad[4] = {kb + ok16[0], kb + ok16[1], kb + ok16[2], kb + ok16[3]};
+            const uint32_t o0 = opaque_v(ok16);
+            const uint32_t ad[4] = {kb + o0, kb + (o0 ^ 16u), kb + (o0 ^ 128u), kb + (o0 ^ 144u)};
             auto rd = [&](auto KBT, int st) __attribute__((always_inline)) {
                 constexpr int OFF = 16 * RS16 * decltype(KBT)::value;
                 kr[st][0] = lds_rd128<OFF>(ad[0]);
@@ -1108,13 +1173,14 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
         // channel block cb + 1 in flight during the MFMAs of cb
         auto pv16 = [&](uint32_t vb, const u32x4 (&pw)[2][2]) __attribute__((always_inline)) {
             u32x2 v16[2][2][2];            // [stage][j][h]
-            const uint32_t ad[4] = {vb + ov[0], vb + ov[1], vb + ov[2], vb + ov[3]};
+            const uint32_t o0 = opaque_v(ov0);
             auto rd16 = [&](auto CBT, int st) __attribute__((always_inline)) {
-                constexpr int cb = decltype(CBT)::value, OFF = 128 * (cb >> 2);
-                v16[st][0][0] = lds_tr16<OFF>(ad[cb & 3]);
-                v16[st][0][1] = lds_tr16<OFF + 16 * RS16>(ad[cb & 3]);
-                v16[st][1][0] = lds_tr16<OFF + 32 * RS16>(ad[cb & 3]);
-                v16[st][1][1] = lds_tr16<OFF + 48 * RS16>(ad[cb & 3]);
+                constexpr uint32_t cb = decltype(CBT)::value;
+                const uint32_t ad = vb + (o0 ^ (32u * cb));
+                v16[st][0][0] = lds_tr16<0>(ad);
+                v16[st][0][1] = lds_tr16<16 * RS16>(ad);
+                v16[st][1][0] = lds_tr16<32 * RS16>(ad);
+                v16[st][1][1] = lds_tr16<48 * RS16>(ad);
             };
             rd16(std::integral_constant<int, 0>{}, 0);
             static_for<8>([&](auto CBT) __attribute__((always_inline)) {
@@ -1320,24 +1386,299 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                 }
             }
         };
-        {
-            // tile 0's DMAs (and scale) before the first run
-            Rsrc rk, rv;
-            if (nrt > 0) {
-                sources(std::integral_constant<int, T_REST>{}, rk, rv);
-                issue(std::integral_constant<int, T_REST>{}, rk, rv, 0, 0);
-                sc_next = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, 0, 0, 0));
-            } else if (nvt > 0) {
-                sources(std::integral_constant<int, T_VERT>{}, rk, rv);
-                issue(std::integral_constant<int, T_VERT>{}, rk, rv, 0, 0);
-            } else if (nwt > 0) {
-                sources(std::integral_constant<int, T_WIN>{}, rk, rv);
-                issue(std::integral_constant<int, T_WIN>{}, rk, rv, wla, 0);
+        if constexpr (PV8) {
+            {
+                // tile 0's DMAs (and scale) before the first run
+                Rsrc rk, rv;
+                if (nrt > 0) {
+                    sources(std::integral_constant<int, T_REST>{}, rk, rv);
+                    issue(std::integral_constant<int, T_REST>{}, rk, rv, 0, 0);
+                    sc_next = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, 0, 0, 0));
+                } else if (nvt > 0) {
+                    sources(std::integral_constant<int, T_VERT>{}, rk, rv);
+                    issue(std::integral_constant<int, T_VERT>{}, rk, rv, 0, 0);
+                } else if (nwt > 0) {
+                    sources(std::integral_constant<int, T_WIN>{}, rk, rv);
+                    issue(std::integral_constant<int, T_WIN>{}, rk, rv, wla, 0);
+                }
             }
+            run(std::integral_constant<int, T_REST>{}, 0, nrt);
+            run(std::integral_constant<int, T_VERT>{}, nrt, nrt + nvt);
+            run(std::integral_constant<int, T_WIN>{}, nrt + nvt, ntiles);
+        } else {
+            // ---- fp16 P.V: software-pipelined runs -----------------------------
+            // Step t exponentiates tile t's scores and multiplies P into O
+            // while it forms the scores of tile t + 1: the QK MFMAs of tile
+            // t + 1 share one instruction stream with the exponentials of tile
+            // t, and the P.V MFMAs of tile t with the conversion, masking and
+            // row maxima of tile t + 1, so that a wavefront keeps its matrix
+            // core and its VALU busy together.  K runs one tile ahead of V:
+            // entering step t the buffers hold K(t + 1) and V(t); the step
+            // issues K(t + 2) into the buffer of K(t) (read by step t - 1) and
+            // V(t + 1) into that of V(t - 1), so one barrier per step covers
+            // both, across the runs too (the DMAs name any tile's kind).  Each
+            // run starts with its first tile's scores alone and ends with its
+            // last tile's P.V alone.  The arithmetic is the tile-at-a-time
+            // order's: tile t + 1's maximum moves m (and rescales O) after
+            // P(t) has been added to O.
+            using KR = std::integral_constant<int, T_REST>;
+            using KV = std::integral_constant<int, T_VERT>;
+            using KW = std::integral_constant<int, T_WIN>;
+            // the K (V) DMAs of tile t, whatever its kind (uniform branches)
+            auto issue_k_any = [&](int t, int par) __attribute__((always_inline)) {
+                Rsrc rk, rv;
+                if (t < nrt) {
+                    sources(KR{}, rk, rv);
+                    issue_k(KR{}, rk, first_of(KR{}, t), par);
+                } else if (t < nrt + nvt) {
+                    sources(KV{}, rk, rv);
+                    issue_k(KV{}, rk, first_of(KV{}, t), par);
+                } else {
+                    sources(KW{}, rk, rv);
+                    issue_k(KW{}, rk, first_of(KW{}, t), par);
+                }
+            };
+            auto issue_v_any = [&](int t, int par) __attribute__((always_inline)) {
+                Rsrc rk, rv;
+                if (t < nrt) {
+                    sources(KR{}, rk, rv);
+                    issue_v(KR{}, rv, first_of(KR{}, t), par);
+                } else if (t < nrt + nvt) {
+                    sources(KV{}, rk, rv);
+                    issue_v(KV{}, rv, first_of(KV{}, t), par);
+                } else {
+                    sources(KW{}, rk, rv);
+                    issue_v(KW{}, rv, first_of(KW{}, t), par);
+                }
+            };
+            const int row0 = BM * blk + 32 * w;           // this wavefront's first row
+            auto rfl = [](float x) __attribute__((always_inline)) {
+                return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+            };
+            // the row maxima of a tile's scores move m (and rescale O and the
+            // row sums) when they pass it by more than the slack
+            auto rescale = [&](const float (&lmx)[2]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    if (__builtin_amdgcn_ballot_w64(lmx[sb] > m_run[sb] + PF_SLACK)) {
+                        const float mx = quad_max_raw(lmx[sb]);
+                        const float mnew = fmaxf(m_run[sb], mx);
+                        const float alpha = __builtin_amdgcn_exp2f(m_run[sb] - mnew);
+                        lsum[sb] *= alpha;
+#pragma unroll
+                        for (int cb = 0; cb < 8; ++cb) acc[sb][cb] *= alpha;
+                        m_run[sb] = mnew;
+                    }
+                }
+            };
+            // P = exp2(s ssc - m) as fp16 B operands
+            auto exp_pack = [&](float ssc, const float (&s)[2][4][4], u32x4 (&pw)[2][2]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    float p[4][4];
+#pragma unroll
+                    for (int kbk = 0; kbk < 4; ++kbk)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            p[kbk][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][kbk][r], ssc, -m_run[sb]));
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        pw[sb][j] = u32x4{pack_f16x2(p[2 * j][0], p[2 * j][1]), pack_f16x2(p[2 * j][2], p[2 * j][3]),
+                                          pack_f16x2(p[2 * j + 1][0], p[2 * j + 1][1]),
+                                          pack_f16x2(p[2 * j + 1][2], p[2 * j + 1][3])};
+                }
+            };
+            float ks_pend = 0.0f;          // k_scale of tile t + 2, loaded during step t
+            // one run: tiles [t0, t1) of kind KIND
+            auto prun = [&](auto KT, int t0, int t1) __attribute__((always_inline)) {
+                constexpr int KIND = decltype(KT)::value;
+                if (t0 >= t1) return;
+                const int valid = KIND == T_REST ? nr_b : KIND == T_VERT ? nv_b : wend;
+                const bool causal = KIND == T_WIN || (KIND == T_REST && a.rest_causal);
+                auto needs_mask = [&](int i0) __attribute__((always_inline)) {
+                    return i0 + BN > valid || (causal && i0 + BN - 1 > row0);
+                };
+                // the scores of tile t (K in buffer t & 1), -inf masked
+                auto scores = [&](auto MT, int t, float (&s)[2][4][4]) __attribute__((always_inline)) {
+                    if constexpr (KIND == T_REST) qk_rest(kbase[t & 1], s);
+                    else qk_f16(kbase[t & 1], s);
+                    if constexpr (decltype(MT)::value) mask_keys(first_of(KT, t), valid, causal, s);
+                };
+                auto scale_of = [&](float ks) __attribute__((always_inline)) {
+                    if constexpr (KIND == T_REST) {
+                        const float qks = q_scale * ks;
+                        return qks > 0.0f ? qks : 1.0f;
+                    } else {
+                        return 1.0f;
+                    }
+                };
+                // int8 rest tiles hand their scores on as raw int32 bits
+                constexpr bool RAW = KIND == T_REST && !QF8;
+                // one piece of a next tile's P: scores (sb, kbk, 2 hf .. 2 hf +
+                // 1) converted, masked, exponentiated with the current m and
+                // packed; their maximum joins mx[sb]
+                auto piece = [&](auto MT, auto PI, const float (&sn)[2][4][4], float ssc, int i0,
+                                 u32x4 (&pn)[2][2], float (&mx)[2]) __attribute__((always_inline)) {
+                    constexpr int pi = decltype(PI)::value, sb = pi >> 3, kbk = (pi >> 1) & 3, hf = pi & 1;
+                    float v[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int r = 2 * hf + e;
+                        float x = sn[sb][kbk][r];
+                        if constexpr (RAW) x = static_cast<float>(__builtin_bit_cast(int, x));
+                        if constexpr (decltype(MT)::value) {
+                            const int row = BM * blk + 32 * w + 16 * sb + c16;
+                            const int key = i0 + 16 * kbk + 4 * g + r;
+                            const bool ok = (key < valid) & (!causal | (key <= row));
+                            x = ok ? x : -INFINITY;
+                        }
+                        v[e] = x;
+                    }
+                    mx[sb] = (kbk == 0 && hf == 0) ? vmax2(v[0], v[1]) : vmax3(mx[sb], v[0], v[1]);
+                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(v[0], ssc, -m_run[sb]));
+                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(v[1], ssc, -m_run[sb]));
+                    pn[sb][kbk >> 1][2 * (kbk & 1) + hf] = pack_f16x2(p0, p1);
+                };
+                // P.V of tile t (P = pc, V at vb) with the next tile's scores
+                // turned into its P (pn) in between: after every second P.V
+                // MFMA one piece (8 VALU instructions, two of them
+                // exponentials); scheduling fences keep that interleave
+                auto pv_fused = [&](auto MT, uint32_t vb, const u32x4 (&pc)[2][2], const float (&sn)[2][4][4],
+                                    float ssc, int i0, u32x4 (&pn)[2][2], float (&lmx)[2]) __attribute__((always_inline)) {
+                    float mx[2];
+                    u32x2 v16[2][2][2];        // [stage][j][h]
+                    const uint32_t o0 = opaque_v(ov0);
+                    auto rd16 = [&](auto CBT, int st) __attribute__((always_inline)) {
+                        constexpr uint32_t cb = decltype(CBT)::value;
+                        const uint32_t ad = vb + (o0 ^ (32u * cb));
+                        v16[st][0][0] = lds_tr16<0>(ad);
+                        v16[st][0][1] = lds_tr16<16 * RS16>(ad);
+                        v16[st][1][0] = lds_tr16<32 * RS16>(ad);
+                        v16[st][1][1] = lds_tr16<48 * RS16>(ad);
+                    };
+                    rd16(std::integral_constant<int, 0>{}, 0);
+                    static_for<8>([&](auto CBT) __attribute__((always_inline)) {
+                        constexpr int cb = decltype(CBT)::value, st = cb & 1;
+                        lds_wait(v16[st][0][0], v16[st][0][1], v16[st][1][0], v16[st][1][1]);
+                        if constexpr (cb + 1 < 8) rd16(std::integral_constant<int, cb + 1>{}, st ^ 1);
+                        static_for<2>([&](auto JT) __attribute__((always_inline)) {
+                            constexpr int j = decltype(JT)::value;
+                            const f16x8 av = __builtin_bit_cast(f16x8, u32x4{v16[st][j][0][0], v16[st][j][0][1],
+                                                                             v16[st][j][1][0], v16[st][j][1][1]});
+#pragma unroll
+                            for (int sb = 0; sb < 2; ++sb)
+                                acc[sb][cb] = mfma_f16(av, __builtin_bit_cast(f16x8, pc[sb][j]), acc[sb][cb]);
+                            piece(MT, std::integral_constant<int, 2 * cb + j>{}, sn, ssc, i0, pn, mx);
+                            __builtin_amdgcn_sched_barrier(0);
+                        });
+                    });
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int sb = 0; sb < 2; ++sb)
+                            lsum[sb] = mfma_f16(__builtin_bit_cast(f16x8, onew), __builtin_bit_cast(f16x8, pc[sb][j]), lsum[sb]);
+                    lmx[0] = mx[0] * ssc;
+                    lmx[1] = mx[1] * ssc;
+                    // P is used here (not only on the branch that keeps it), so
+                    // that it is formed in its pieces rather than sunk past
+                    // the slack test
+                    asm volatile("" : "+v"(pn[0][0]), "+v"(pn[0][1]), "+v"(pn[1][0]), "+v"(pn[1][1]));
+                };
+                // one step with a next tile: its P is formed with the current m
+                // while P(t) goes into O; when one of its row maxima passes m
+                // by more than the slack (rare), O is rescaled after P(t) and
+                // its scores and P are formed again with the new m
+                auto body = [&](auto MT, int t, const u32x4 (&pc)[2][2], float ssc_n, u32x4 (&pn)[2][2])
+                                __attribute__((always_inline)) {
+                    float sn[2][4][4];
+                    if constexpr (KIND == T_REST) qk_rest_t(std::integral_constant<bool, RAW>{}, kbase[(t + 1) & 1], sn);
+                    else qk_f16(kbase[(t + 1) & 1], sn);
+                    const int i0 = first_of(KT, t + 1);
+                    float lmx[2];
+                    pv_fused(MT, vbase[t & 1], pc, sn, ssc_n, i0, pn, lmx);
+                    if (__builtin_amdgcn_ballot_w64(lmx[0] > m_run[0] + PF_SLACK) |
+                        __builtin_amdgcn_ballot_w64(lmx[1] > m_run[1] + PF_SLACK)) {
+                        rescale(lmx);
+                        // the scores again from K(t + 1), still in LDS (not
+                        // held through the step)
+                        float sr[2][4][4];
+                        if constexpr (KIND == T_REST) qk_rest_t(std::integral_constant<bool, RAW>{}, kbase[(t + 1) & 1], sr);
+                        else qk_f16(kbase[(t + 1) & 1], sr);
+                        float mx[2];
+                        static_for<16>([&](auto PI) __attribute__((always_inline)) {
+                            piece(MT, PI, sr, ssc_n, i0, pn, mx);
+                        });
+                    }
+                };
+                auto step = [&](int t, const u32x4 (&pc)[2][2], u32x4 (&pn)[2][2]) __attribute__((always_inline)) {
+                    // own DMAs of K(t + 1) and V(t) landed; the barrier extends
+                    // that to the workgroup and frees the buffers of K(t) and
+                    // V(t - 1)
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                    __syncthreads();
+                    const float ks1 = rfl(ks_pend);
+                    if (t + 2 < nrt)
+                        ks_pend = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, 0, 4 * (t + 2), 0));
+                    if (t + 2 < ntiles) issue_k_any(t + 2, t & 1);
+                    if (t + 1 < ntiles) issue_v_any(t + 1, (t + 1) & 1);
+                    if (t + 1 < t1) {
+                        const float ssc_n = scale_of(ks1);
+                        if (needs_mask(first_of(KT, t + 1))) body(std::true_type{}, t, pc, ssc_n, pn);
+                        else body(std::false_type{}, t, pc, ssc_n, pn);
+                    } else {
+                        pv16(vbase[t & 1], pc);
+                    }
+                };
+                // the run's first tile (K(t0) has landed for the workgroup: a
+                // step's or the prologue's barrier): exact maxima, then P
+                u32x4 pX[2][2], pY[2][2];
+                {
+                    float s0[2][4][4];
+                    if (needs_mask(first_of(KT, t0))) scores(std::true_type{}, t0, s0);
+                    else scores(std::false_type{}, t0, s0);
+                    float ssc0 = 1.0f;
+                    if constexpr (KIND == T_REST) ssc0 = scale_of(rfl(sc_next));
+                    const float lmx[2] = {tile_max16(s0[0]) * ssc0, tile_max16(s0[1]) * ssc0};
+                    rescale(lmx);
+                    exp_pack(ssc0, s0, pX);
+                }
+                // unrolled by two so that the two P sets keep their registers
+                for (int t = t0; t < t1; t += 2) {
+                    step(t, pX, pY);
+                    if (t + 1 < t1) step(t + 1, pY, pX);
+                }
+            };
+            if (ntiles > 0) {
+                // prologue: K(0), V(0), K(1) and the first two k_scales
+                issue_k_any(0, 0);
+                issue_v_any(0, 0);
+                if (ntiles > 1) issue_k_any(1, 1);
+                if (nrt > 0) sc_next = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, 0, 0, 0));
+                if (nrt > 1) ks_pend = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, 0, 4, 0));
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+            }
+            prun(KR{}, 0, nrt);
+            // the fp16 tiles' Q operand, from Q again (through a pointer and
+            // lane coordinates the compiler cannot match with the first
+            // loads: it would otherwise hold those values, or addresses, in
+            // registers through the rest tiles)
+            {
+                const uint16_t* qagain = a.q;
+                asm volatile("" : "+s"(qagain));
+                const int cr = static_cast<int>(opaque_v(c16)), gr = static_cast<int>(opaque_v(g));
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                    for (int cc = 0; cc < 2; ++cc) {
+                        float xv[16];
+                        q_chunk(qagain, cr, gr, sb, cc, xv);
+                        make_qh(sb, cc, xv);
+                    }
+            }
+            prun(KV{}, nrt, nrt + nvt);
+            prun(KW{}, nrt + nvt, ntiles);
         }
-        run(std::integral_constant<int, T_REST>{}, 0, nrt);
-        run(std::integral_constant<int, T_VERT>{}, nrt, nrt + nvt);
-        run(std::integral_constant<int, T_WIN>{}, nrt + nvt, ntiles);
     }
 
 
@@ -1364,10 +1705,12 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                 }
         }
     } else {
+        // lane coordinates formed here (not hoisted into the tile loops)
+        const int cr = static_cast<int>(opaque_v(c16)), gr = static_cast<int>(opaque_v(g));
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
             const float inv = 1.0f / lsum[sb][0];
-            const int row = BM * blk + 32 * w + 16 * sb + c16;
+            const int row = BM * blk + 32 * w + 16 * sb + cr;
             if (row < a.N) {
                 uint16_t* orow = a.out + b * a.o_b + h * a.o_h + static_cast<int64_t>(row) * a.o_n;
 #pragma unroll
@@ -1375,7 +1718,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_main_kernel(PfArgs a) {
                     const f32x4 o4 = acc[sb][cb] * inv;
                     const u32x2 o = a.f16 ? u32x2{pack_f16x2(o4[0], o4[1]), pack_f16x2(o4[2], o4[3])}
                                           : u32x2{pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3])};
-                    *reinterpret_cast<u32x2*>(orow + 16 * cb + 4 * g) = o;
+                    *reinterpret_cast<u32x2*>(orow + 16 * cb + 4 * gr) = o;
                 }
             }
         }

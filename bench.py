@@ -342,6 +342,17 @@ def decode_error(dev):
     return e
 
 
+PREFILL_NS = (8192, 16384, 32768)
+# (name, kernel kind, QK operand, P.V operand, QK peak, P.V peak)
+PREFILL_VARIANTS = (
+    ("hybrid int8/fp16", "hybrid", "int8", "fp16", PEAK_INT8, PEAK_FP16),
+    ("hybrid int8/fp8", "hybrid", "int8", "fp8", PEAK_INT8, PEAK_FP8),
+    ("hybrid fp8/fp16", "hybrid", "fp8", "fp16", PEAK_FP8, PEAK_FP16),
+    ("window_only int8/fp16", "window_only", "int8", "fp16", PEAK_INT8, PEAK_FP16),
+)
+PREFILL_CALLS = 14          # per variant and N: 3 warm-up, 10 timed, 1 for the error figures
+
+
 def bench_prefill(dev):
     """Config 4: hybrid prefill, B=1, 32q/8kv, d128, causal, W=128, rho=5%,
     with int8 or e4m3 QK on the rest tiles and fp16 or e4m3 P.V, and the
@@ -355,7 +366,7 @@ def bench_prefill(dev):
     from hyquant_amd.vertical import compute_vertical_indices
     g = torch.Generator(device=dev).manual_seed(4)
     rows = []
-    for N in (8192, 16384, 32768):
+    for N in PREFILL_NS:
         B, HQ, HKV, W = 1, 32, 8, 128
         q = torch.randn(B, HQ, N, D, generator=g, device=dev).to(torch.bfloat16)
         k = (torch.randn(B, HKV, N, D, generator=g, device=dev) +
@@ -364,18 +375,15 @@ def bench_prefill(dev):
         vidx = compute_vertical_indices(q, k, W, 0.05, kv_repeat=HQ // HKV)
         exact = exact_attention_fp32(q, k, v)
         flops = 2.0 * B * HQ * N * N * D
-        variants = (
-            ("hybrid", "int8", "fp16", PEAK_INT8, PEAK_FP16,
-             lambda: sage_vertical_attention_v2(q, k, v, vidx, window_size=W)),
-            ("hybrid", "int8", "fp8", PEAK_INT8, PEAK_FP8,
-             lambda: sage_vertical_attention_v2(q, k, v, vidx, window_size=W, pv_mode="fp8")),
-            ("hybrid", "fp8", "fp16", PEAK_FP8, PEAK_FP16,
-             lambda: sage_vertical_attention_v2_fp8(q, k, v, vidx, window_size=W)),
-            ("window_only", "int8", "fp16", PEAK_INT8, PEAK_FP16,
-             lambda: sage_unified_attention(q, k, v, window_size=W)),
-        )
-        for kind, qk, pv, qk_peak, pv_peak, fn in variants:
-            ms = time_calls(fn)
+        fns = {
+            "hybrid int8/fp16": lambda: sage_vertical_attention_v2(q, k, v, vidx, window_size=W),
+            "hybrid int8/fp8": lambda: sage_vertical_attention_v2(q, k, v, vidx, window_size=W, pv_mode="fp8"),
+            "hybrid fp8/fp16": lambda: sage_vertical_attention_v2_fp8(q, k, v, vidx, window_size=W),
+            "window_only int8/fp16": lambda: sage_unified_attention(q, k, v, window_size=W),
+        }
+        for name, kind, qk, pv, qk_peak, pv_peak in PREFILL_VARIANTS:
+            fn = fns[name]
+            ms = time_calls(fn, warmup=PREFILL_CALLS - 11, iters=10)
             tf = flops / (ms * 1e-3) / 1e12
             peak = 2.0 / (1.0 / qk_peak + 1.0 / pv_peak)
             err = error_vs(fn(), exact)
@@ -497,20 +505,182 @@ def pmc_workload(dev):
     torch.cuda.synchronize()
 
 
+# decode counter shapes: the 12 config-2 sweep points (Llama-3.1-8B,
+# 32q/8kv), then the config-3 Qwen3-32B and GLM-4-9B shapes
+PMC_SHAPES = tuple((b, 32, 8, n) for b in (1, 16) for n in (1024, 2048, 4096, 8192, 16384, 32768)) + \
+    ((32, 64, 8, 16384), (32, 32, 2, 16384))
+
+
+def pmc_copies(B, HQ, HKV, N):
+    """Cache copies (one eager decode step each) per counter shape: enough
+    to span more than the 256 MiB last-level cache, at most 64."""
+    return int(max(4, min(64, math.ceil((384 << 20) / algorithmic_bytes(B, HQ, HKV, N)))))
+
+
 def pmc_decode_shapes_workload(dev):
-    """Fixed workload for SQ counter passes over the decode kernel at three
-    shapes: Llama-3.1-8B B=16 prefix 32768, and the config-3 Qwen3-32B and
-    GLM-4-9B shapes at B=32 prefix 16384; four eager steps each over two
-    cache copies."""
-    for (B, HQ, HKV, N) in ((16, 32, 8, 32768), (32, 64, 8, 16384), (32, 32, 2, 16384)):
-        states = [make_state(B, HQ, HKV, N, dev, s) for s in range(2)]
+    """Fixed workload for counter passes over the decode kernel: a 256 MiB
+    device copy (the FETCH_SIZE / WRITE_SIZE calibration) three times, then
+    for each shape of PMC_SHAPES one eager step over each of pmc_copies()
+    cache copies, in that order (a summary maps the decode_kernel dispatches
+    back to the shapes by their order)."""
+    src_t = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst_t = torch.empty_like(src_t)
+    for _ in range(3):
+        dst_t.copy_(src_t)
+    torch.cuda.synchronize()
+    del src_t, dst_t
+    for (B, HQ, HKV, N) in PMC_SHAPES:
+        R = pmc_copies(B, HQ, HKV, N)
+        states = [make_state(B, HQ, HKV, N, dev, s) for s in range(R)]
         torch.cuda.synchronize()
-        for i in range(4):
-            q, st = states[i % 2]
+        for q, st in states:
             run_decode(q, st, HQ // HKV)
         torch.cuda.synchronize()
+        print(f"# pmc shape B={B} {HQ}q/{HKV}kv N={N}: {R} decode steps", file=sys.stderr, flush=True)
         del states
         torch.cuda.empty_cache()
+
+
+def _counter_rows(path, counter):
+    """(kernel name, dispatch id, value) of one counter from a rocprofv3
+    counter_collection.csv, in dispatch order (values summed over the
+    counter's instances)."""
+    import csv
+    vals = {}
+    for r in csv.DictReader(open(path)):
+        if r["Counter_Name"] != counter:
+            continue
+        key = int(r["Dispatch_Id"])
+        name, v = vals.get(key, (r["Kernel_Name"], 0.0))
+        vals[key] = (name, v + float(r["Counter_Value"]))
+    return [(vals[k][0], k, vals[k][1]) for k in sorted(vals)]
+
+
+def pmc_decode_summary(fetch_csv, write_csv, sq_csv=None):
+    """Per-shape HBM bytes per decode launch from the FETCH_SIZE and
+    WRITE_SIZE passes over --pmc-decode-shapes: the copy kernel's counters
+    give the calibration (it reads and writes 256 MiB), the decode_kernel
+    dispatches are mapped to PMC_SHAPES by order, and each shape reports the
+    median over its launches.  An optional third pass (SQ / GRBM counters)
+    adds each counter's per-shape median and the derived busy and wait
+    fractions (GRBM_GUI_ACTIVE summed over 8 XCDs, 1024 SIMDs, VALU issue
+    counted as 4 cycles per wave64 instruction)."""
+    import numpy as np
+    out = {"workload": "bench.py --pmc-decode-shapes", "shapes": []}
+    cal = {}
+    per = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = _counter_rows(path, counter)
+        copy = [v for (n, _, v) in rows if "copyBuffer" in n][:3]
+        dec = [v for (n, _, v) in rows if "decode_kernel" in n]
+        if not copy or not dec:
+            raise RuntimeError(f"{path}: no copy or decode_kernel dispatches for {counter}")
+        raw = float(np.median(copy))
+        scale = (256 << 10) / raw
+        cal[counter] = {"copy_kib_raw": round(raw, 2), "scale": round(scale, 4)}
+        per[counter] = (dec, scale)
+    i = {"FETCH_SIZE": 0, "WRITE_SIZE": 0}
+    for (B, HQ, HKV, N) in PMC_SHAPES:
+        R = pmc_copies(B, HQ, HKV, N)
+        row = {"batch": B, "q_heads": HQ, "kv_heads": HKV, "prefix": N, "launches": R,
+               "algorithmic_bytes_per_launch": algorithmic_bytes(B, HQ, HKV, N)}
+        for counter, key in (("FETCH_SIZE", "fetch_bytes_per_launch"), ("WRITE_SIZE", "write_bytes_per_launch")):
+            dec, scale = per[counter]
+            vals = dec[i[counter]: i[counter] + R]
+            if len(vals) != R:
+                raise RuntimeError(f"{counter}: {len(dec)} decode dispatches, fewer than the workload's")
+            i[counter] += R
+            row[key] = int(round(float(np.median(vals)) * 1024 * scale))
+        row["traffic_bytes_per_launch"] = row["fetch_bytes_per_launch"] + row["write_bytes_per_launch"]
+        row["traffic_over_algorithmic"] = round(row["traffic_bytes_per_launch"] / row["algorithmic_bytes_per_launch"], 4)
+        out["shapes"].append(row)
+    if sq_csv:
+        import csv
+        per_disp = {}
+        for r in csv.DictReader(open(sq_csv)):
+            if "decode_kernel" not in r["Kernel_Name"]:
+                continue
+            d = per_disp.setdefault(int(r["Dispatch_Id"]), {})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        disp = [per_disp[k] for k in sorted(per_disp)]
+        j = 0
+        for row in out["shapes"]:
+            cs = disp[j: j + row["launches"]]
+            j += row["launches"]
+            if len(cs) != row["launches"]:
+                raise RuntimeError(f"{sq_csv}: fewer decode dispatches than the workload's")
+            med = {c: float(np.median([d.get(c, 0.0) for d in cs])) for c in sorted({c for d in cs for c in d})}
+            row["sq"] = {c: float("%.4g" % v) for c, v in med.items()}
+            cyc = med.get("GRBM_GUI_ACTIVE", 0.0) / 8
+            der = {}
+            if cyc > 0 and "SQ_ACTIVE_INST_VALU" in med:
+                der["valu_busy"] = round(4 * med["SQ_ACTIVE_INST_VALU"] / 1024 / cyc, 3)
+            if cyc > 0 and "SQ_VALU_MFMA_BUSY_CYCLES" in med:
+                der["mfma_busy"] = round(med["SQ_VALU_MFMA_BUSY_CYCLES"] / 1024 / cyc, 3)
+            if med.get("SQ_WAVE_CYCLES"):
+                for c, key in (("SQ_WAIT_ANY", "wave_time_waiting_on_counters"),
+                               ("SQ_WAIT_INST_ANY", "wave_time_waiting_to_issue")):
+                    if c in med:
+                        der[key] = round(med[c] / med["SQ_WAVE_CYCLES"], 3)
+            if med.get("SQ_INSTS_VMEM_RD"):
+                der["fetch_bytes_per_vmem_read"] = round(row["fetch_bytes_per_launch"] / med["SQ_INSTS_VMEM_RD"], 1)
+            if med.get("SQ_INSTS_MFMA") and "SQ_INSTS_VALU" in med:
+                der["valu_per_mfma"] = round((med["SQ_INSTS_VALU"] - med["SQ_INSTS_MFMA"]) / med["SQ_INSTS_MFMA"], 2)
+            row["derived"] = der
+    out["calibration"] = cal
+    return out
+
+
+def sweep_traffic_record():
+    """{(batch, prefix): traffic bytes per launch} of the 32q/8kv decode
+    shapes from profiles/decode_sweep_traffic.json, or {}."""
+    path = os.path.join(ROOT, "profiles", "decode_sweep_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return {}
+    return {(r["batch"], r["prefix"]): r["traffic_bytes_per_launch"] for r in rec.get("shapes", [])
+            if r.get("q_heads") == 32 and r.get("kv_heads") == 8}
+
+
+def prefill_trace_summary(trace_csv):
+    """Per-kernel durations of `bench.py --prefill-only` from a rocprofv3
+    kernel trace (run_kernel_trace.csv): the calls are told apart by their
+    prefill_main_kernel dispatch (one per call; the auxiliary kernels of a
+    call precede it) and mapped to (N, variant) by order: for each N of
+    bench_prefill, for each variant, 3 warm-up + 10 timed calls + 1 error
+    call.  Reports the median over the 14 calls, in microseconds."""
+    import csv
+    import numpy as np
+    rows = list(csv.DictReader(open(trace_csv)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    calls, cur = [], {}
+    short = lambda n: n.replace("void ", "").replace("hyq::(anonymous namespace)::", "").split("(")[0]
+    ours = ("prefill_main_kernel", "kv_stats_kernel", "kv_final_kernel", "kv_convert_kernel", "gather_kernel",
+            "per_block_int8_kernel", "zero_counts_kernel", "lists_kernel")
+    for r in rows:
+        n = short(r["Kernel_Name"])
+        if not any(o in n for o in ours):
+            continue
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        cur[n] = cur.get(n, 0.0) + d
+        if "prefill_main_kernel" in n:
+            calls.append(cur)
+            cur = {}
+    variants = [v[0] for v in PREFILL_VARIANTS]
+    per = len(variants) * PREFILL_CALLS
+    if len(calls) != len(PREFILL_NS) * per:
+        raise RuntimeError(f"{len(calls)} prefill calls in the trace, expected {len(PREFILL_NS) * per}")
+    table = []
+    for ni, N in enumerate(PREFILL_NS):
+        for vi, v in enumerate(variants):
+            cs = calls[ni * per + vi * PREFILL_CALLS: ni * per + (vi + 1) * PREFILL_CALLS]
+            names = sorted({k for c in cs for k in c})
+            med = {k: round(float(np.median([c.get(k, 0.0) for c in cs])), 1) for k in names}
+            table.append({"seq_len": N, "variant": v, "kernels_us": med,
+                          "total_us": round(float(np.median([sum(c.values()) for c in cs])), 1)})
+    return table
 
 
 PHASES = ("entry", "arguments", "Q", "first K/V", "stream done", "LDS merge", "partial acked",
@@ -616,10 +786,22 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the config 3 / config 4 sections")
     ap.add_argument("--pmc", action="store_true", help="run the counter-pass workload only")
     ap.add_argument("--pmc-decode-shapes", action="store_true",
-                    help="run the decode counter workload over three shapes only")
+                    help="run the decode counter workload (12 config-2 and 2 config-3 shapes) only")
     ap.add_argument("--phase-trace", action="store_true",
                     help="print the config-1 decode phase timeline from the trace build (libhyq_trace.so)")
+    ap.add_argument("--prefill-only", action="store_true", help="run the config-4 prefill section only")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
+                    help="summarise the FETCH_SIZE, WRITE_SIZE (and optional SQ) passes over "
+                         "--pmc-decode-shapes: FETCH_CSV WRITE_CSV [SQ_CSV] (no GPU)")
+    ap.add_argument("--prefill-trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="per-kernel table of a kernel trace of --prefill-only (no GPU)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(json.dumps(pmc_decode_summary(*args.pmc_summary), indent=1))
+        return
+    if args.prefill_trace_summary:
+        print(json.dumps(prefill_trace_summary(args.prefill_trace_summary), indent=1))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(--gpus must be 1)", file=sys.stderr)
@@ -637,6 +819,9 @@ def main():
         return
     if args.pmc:
         pmc_workload(dev)
+        return
+    if args.prefill_only:
+        print(json.dumps({"config4_prefill": bench_prefill(dev)}), flush=True)
         return
 
     B, HQ, HKV, N = 1, 32, 8, 8192
@@ -684,6 +869,7 @@ def main():
                                   "speedup_hybrid_vs_bf16": round(ms16 / ms, 3),
                                   "meets_3x": bool(ms16 / ms >= 3.0)}
     if not args.no_sweep:
+        traffic = sweep_traffic_record()
         sweep = []
         for b in (1, 16):
             for n in (1024, 2048, 4096, 8192, 16384, 32768):
@@ -691,6 +877,12 @@ def main():
                 row = {"batch": b, "prefix": n, "us_per_step": round(m * 1e3, 3),
                        "gbs": round(nb / (m * 1e-3) / 1e9, 1),
                        "frac_peak": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                if (b, n) in traffic:
+                    # HBM bytes per launch from the FETCH_SIZE + WRITE_SIZE
+                    # passes (profiles/decode_sweep_traffic.json) over this
+                    # row's step time
+                    row["counter_traffic_bytes"] = traffic[(b, n)]
+                    row["counter_gbs"] = round(traffic[(b, n)] / (m * 1e-3) / 1e9, 1)
                 if not args.no_bf16:
                     m16, nb16, _, _ = bench_bf16(b, HQ, HKV, n, dev, 5, 50)
                     row["bf16_us_per_step"] = round(m16 * 1e3, 3)

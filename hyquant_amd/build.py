@@ -40,6 +40,34 @@ def hipcc() -> str:
 TRACE_LIB = os.path.join(HERE, "libhyq_trace.so")
 
 
+# the eager fast path of fused_d_stage_decode: a host-only Python extension
+# (g++ against torch's headers; it calls libhyq.so through an address the
+# Python side hands it, so it has no link dependency on the library)
+FAST_EXT = os.path.join(HERE, "_hyq_fast.so")
+
+
+def build_fast_ext(verbose: bool = False) -> str:
+    import sysconfig
+
+    import torch.utils.cpp_extension as ce
+    inc = ce.include_paths() + [sysconfig.get_paths()["include"]]
+    libs = ce.library_paths()
+    import torch
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
+    tmp = FAST_EXT + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-DTORCH_EXTENSION_NAME=_hyq_fast",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", f"-D_GLIBCXX_USE_CXX11_ABI={abi}", *[f"-I{i}" for i in inc],
+           os.path.join(CSRC, "fastpath.cpp"), *[f"-L{d}" for d in libs], *[f"-Wl,-rpath,{d}" for d in libs],
+           "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-o", tmp]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"g++ failed ({proc.returncode}):\n{' '.join(cmd)}\n{proc.stderr}")
+    if verbose and proc.stderr.strip():
+        print(proc.stderr, file=sys.stderr)
+    os.replace(tmp, FAST_EXT)
+    return FAST_EXT
+
+
 def build(verbose: bool = False, trace: bool = False) -> str:
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
     out = TRACE_LIB if trace else LIB
@@ -58,3 +86,5 @@ def build(verbose: bool = False, trace: bool = False) -> str:
 
 if __name__ == "__main__":
     print(build(verbose=True, trace="--trace" in sys.argv[1:]))
+    if "--trace" not in sys.argv[1:]:
+        print(build_fast_ext(verbose=True))

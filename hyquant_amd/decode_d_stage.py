@@ -58,6 +58,7 @@ def _inner_contig(t: torch.Tensor) -> torch.Tensor:
 
 _ws_lock = threading.Lock()
 _ws_cache: dict = {}
+_ws_raw: dict = {}          # (device, stream) -> (pointer, bytes) of the cached workspace
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
@@ -73,6 +74,7 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
         if buf is None or buf.numel() < nbytes:
             buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
             _ws_cache[key] = buf
+            _ws_raw[key] = (buf.data_ptr(), buf.numel())
         return buf
 
 
@@ -222,6 +224,20 @@ def fused_d_stage_decode(
     (one dtype for the segments): fp16 values are rounded to bf16 before the
     products, as the reference's kernels do (src/ops/decode_d_stage.py:537-541),
     and the fp32 result is rounded once to q.dtype (:866)."""
+    fx = _FX if _FX is not None else _load_fast_ext()
+    if fx:
+        dev = q.get_device() if isinstance(q, torch.Tensor) else -1
+        if dev >= 0:
+            stream = _raw_stream(dev) if _raw_stream is not None else torch.cuda.current_stream(dev).cuda_stream
+            w = _ws_raw.get((dev, stream), _NO_WS)
+            try:
+                st, out = fx.decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk, k_staging,
+                                    v_staging, k_window, v_window, k_bits, v_bits, kv_repeat,
+                                    _NAN if sm_scale is None else sm_scale, split_tokens, stream, w[0], w[1])
+            except TypeError:
+                st = -1
+            if st == 0:
+                return out
     out = _fast_decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, v_topk, k_staging, v_staging,
                        k_window, v_window, k_bits, v_bits, kv_repeat, sm_scale, split_tokens)
     if out is not None:
@@ -266,6 +282,34 @@ def _params_struct() -> struct.Struct:
 
 _PSTRUCT = None
 _HYB = None
+# The C++ form of the fast path (hyquant_amd/_hyq_fast.so, built by
+# build.build_fast_ext): the same checks and the same parameter block, with
+# the tensors' metadata read natively (about 3 us less host time per call).
+# A status other than 0 (not taken, workspace missing or too small, a
+# rejected argument) falls through to the Python fast path and then to the
+# checked path, which handle each case.  None: not loaded yet; False: absent
+# or built for a different parameter layout.
+_FX = None
+_NAN = float("nan")
+_NO_WS = (0, 0)
+
+
+def _load_fast_ext():
+    global _FX
+    import importlib.util
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_hyq_fast.so")
+    mod = False
+    if os.path.exists(path):
+        spec = importlib.util.spec_from_file_location("hyquant_amd._hyq_fast", path)
+        m = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(m)
+        P = _lib.DecodeParams
+        if m.layout() == (ctypes.sizeof(P), P.seg_n.offset, P.dtype_flags.offset):
+            m.set_entry(ctypes.cast(_lib.lib().hyq_decode_hybrid, ctypes.c_void_p).value)
+            mod = m
+    _FX = mod
+    return mod
 _tls = threading.local()
 _BF16, _FP16 = torch.bfloat16, torch.float16
 

@@ -128,6 +128,41 @@ def test_decode_strided_staging_view_and_sm_scale():
     _check("strided staging, sm_scale=0.05", out.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("fp16", [False, True])
+def test_decode_host_paths_bit_identical(fp16):
+    """The three host paths of fused_d_stage_decode (the C++ extension, the
+    Python fast path, the checked path) fill the same parameters: their
+    outputs are bit-identical, with the default and an explicit sm_scale and
+    a strided staging view."""
+    import hyquant_amd as hq
+    from hyquant_amd import decode_d_stage as dd
+    fx = dd._load_fast_ext()
+    if not fx:
+        pytest.skip("hyquant_amd/_hyq_fast.so not built")
+    inp = O.make_decode_inputs(B=1, HQ=32, HKV=8, N=2048, W=128, S=37, seed=9)
+    st = O.build_decode_state(inp)
+    dev = torch.device("cuda")
+    t = state_to_device(st, dev)
+    dt = torch.float16 if fp16 else torch.bfloat16
+    cv = (lambda x: x.to(dt)) if fp16 else (lambda x: x)
+    ring_k, ring_v = cv(to_dev_bf16(st.k_ring, dev)), cv(to_dev_bf16(st.v_ring, dev))
+    q = cv(to_dev_bf16(inp.q_dec, dev))
+    segs = [cv(t["k_topk"]), cv(t["v_topk"]), ring_k[:, :37], ring_v[:, :37], cv(t["k_window"]), cv(t["v_window"])]
+    for sm in (None, 0.05):
+        args = [q, t["k_packed"], t["v_packed"], t["k_scale"], t["v_scale"], *segs, 4, 4, 4, sm, 0]
+        ref = hq.fused_d_stage_decode(*args[:13], kv_repeat=4, sm_scale=sm)        # allocates the workspace
+        py = dd._fast_decode(*args)
+        chk = dd._decode(*args, None, None)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        w = dd._ws_raw[(dev.index if dev.index is not None else 0, stream)]
+        status, ext = fx.decode(*args[:14], float("nan") if sm is None else sm, 0, stream, w[0], w[1])
+        torch.cuda.synchronize()
+        assert status == 0
+        assert ext.dtype == dt and ext.shape == q.shape
+        for name, o in (("python fast path", py), ("checked path", chk), ("extension", ext)):
+            assert torch.equal(o.view(torch.int16), ref.view(torch.int16)), (name, sm)
+
+
 @pytest.mark.parametrize("n,G", [(1000, 4), (8192, 4), (333, 16)])
 def test_bf16_comparator(n, G):
     import hyquant_amd as hq

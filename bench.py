@@ -688,8 +688,9 @@ PHASES = ("entry", "arguments", "Q", "first K/V", "stream done", "LDS merge", "p
           "merge loads issued")
 
 
-def phase_trace(dev, steps=100):
-    """Per-phase timeline of the config-1 decode step under HIP-graph replay,
+def phase_trace(dev, steps=100, shape=(1, 32, 8, 8192)):
+    """Per-phase timeline of a decode step (config 1 unless `shape` = (B, HQ,
+    HKV, N) says otherwise) under HIP-graph replay,
     from the phase-trace build (libhyq_trace.so: s_memrealtime stamps of every
     wavefront, 100 MHz).  Two workloads: the bench's rotation over >= 1 GiB
     of cache copies, and one cache copy replayed (translations and caches
@@ -699,7 +700,11 @@ def phase_trace(dev, steps=100):
     phases over the merging wavefronts only); `end` is the last merge store
     acknowledged, `gap` the time from a launch's end to the next launch's t0,
     `wave_spread` the median over workgroups of the spread of their four
-    wavefronts' stream-done stamps."""
+    wavefronts' stream-done stamps; `entry_pct` and `stream_done_pct` the
+    10/50/90/100th percentiles over wavefronts of their entry and stream-done
+    stamps, `stream_us_pct` those of each wavefront's own stream (first K/V
+    to stream done) — for shapes with more workgroups than slots these show
+    the rounds and the tail."""
     import ctypes
     import numpy as np
     from hyquant_amd import _lib
@@ -710,9 +715,9 @@ def phase_trace(dev, steps=100):
     slots, maxw, nph = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     L.hyq_phase_trace_geometry(ctypes.byref(slots), ctypes.byref(maxw), ctypes.byref(nph))
     S, MW, NP = slots.value, maxw.value, nph.value
-    B, HQ, HKV, N = 1, 32, 8, 8192
+    B, HQ, HKV, N = shape
     G = HQ // HKV
-    out = {}
+    out = {"shape": {"batch": B, "q_heads": HQ, "kv_heads": HKV, "prefix": N}}
     for mode in ("rotated", "one_copy"):
         nb = algorithmic_bytes(B, HQ, HKV, N)
         R = copies_for(nb) if mode == "rotated" else 1
@@ -733,6 +738,7 @@ def phase_trace(dev, steps=100):
         launches.sort(key=lambda x: x[0])
         launches = launches[-min(len(launches), steps, S):]
         med, mx, gaps, ends, spread = [], [], [], [], []
+        pct = {"entry": [], "stream_done": [], "stream": []}
         for i, (_, w) in enumerate(launches):
             t0 = w[:, 0].min()
             nt = NP - 1                                       # the last field is the launch index
@@ -747,6 +753,11 @@ def phase_trace(dev, steps=100):
             ends.append((end - t0) * 0.01)
             sd = w[:, 4].reshape(-1, 4)
             spread.append(np.median(sd.max(axis=1) - sd.min(axis=1)) * 0.01)
+            live = w[:, 0] > 0
+            for key, col in (("entry", rel[:, 0][live]), ("stream_done", rel[:, 4][live]),
+                             ("stream", (rel[:, 4] - rel[:, 3])[live & (w[:, 3] > 0)])):
+                if len(col):
+                    pct[key].append(np.percentile(col, [10, 50, 90, 100]))
             if i + 1 < len(launches):
                 gaps.append((launches[i + 1][1][:, 0].min() - end) * 0.01)
         med = np.nanmedian(np.stack(med), axis=0)
@@ -757,7 +768,10 @@ def phase_trace(dev, steps=100):
                                    for k in range(len(med))},
                      "end_us": round(float(np.median(ends)), 2),
                      "gap_us": round(float(np.median(gaps)), 2) if gaps else None,
-                     "wave_spread_us": round(float(np.median(spread)), 2)}
+                     "wave_spread_us": round(float(np.median(spread)), 2),
+                     "entry_pct_us": [round(float(x), 2) for x in np.median(np.stack(pct["entry"]), axis=0)],
+                     "stream_done_pct_us": [round(float(x), 2) for x in np.median(np.stack(pct["stream_done"]), axis=0)],
+                     "stream_us_pct": [round(float(x), 2) for x in np.median(np.stack(pct["stream"]), axis=0)]}
         del states
         torch.cuda.empty_cache()
         print(f"# phase-trace {mode} {out[mode]}", file=sys.stderr, flush=True)
@@ -789,6 +803,8 @@ def main():
                     help="run the decode counter workload (12 config-2 and 2 config-3 shapes) only")
     ap.add_argument("--phase-trace", action="store_true",
                     help="print the config-1 decode phase timeline from the trace build (libhyq_trace.so)")
+    ap.add_argument("--phase-trace-shape", metavar="B,HQ,HKV,N",
+                    help="with --phase-trace: the decode shape (default 1,32,8,8192)")
     ap.add_argument("--prefill-only", action="store_true", help="run the config-4 prefill section only")
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
                     help="summarise the FETCH_SIZE, WRITE_SIZE (and optional SQ) passes over "
@@ -812,7 +828,8 @@ def main():
     torch.cuda.set_device(dev)
     import hyquant_amd  # noqa: F401  (fails loudly if libhyq.so is missing)
     if args.phase_trace:
-        print(json.dumps({"phase_trace": phase_trace(dev, args.steps)}), flush=True)
+        shp = tuple(int(x) for x in args.phase_trace_shape.split(",")) if args.phase_trace_shape else (1, 32, 8, 8192)
+        print(json.dumps({"phase_trace": phase_trace(dev, args.steps, shp)}), flush=True)
         return
     if args.pmc_decode_shapes:
         pmc_decode_shapes_workload(dev)

@@ -76,16 +76,20 @@ constexpr int QM_SLICES = QM_THREADS / 64;
 
 __global__ __launch_bounds__(QM_THREADS) void qmean_kernel(const uint16_t* __restrict__ q, int64_t qs_b, int64_t qs_h,
                                                            int64_t qs_t, int QL, int tail, int R, int HK, int G,
-                                                           int GP, int f16, double* __restrict__ qm) {
+                                                           int GP, int f16, double* __restrict__ qm,
+                                                           uint16_t* __restrict__ qb, uint32_t* __restrict__ hist) {
     const int row = blockIdx.x;                    // (b, hk, g)
     const int g = row % GP;
     const int bhk = row / GP;
     const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
     double* out = qm + static_cast<int64_t>(row) * 128;
+    uint16_t* outb = qb + static_cast<int64_t>(row) * 128;
     if (g >= G) {
         out[threadIdx.x & 127] = 0.0;
+        outb[threadIdx.x & 127] = 0;
         return;
     }
+    if (threadIdx.x < 256) hist[(static_cast<int64_t>(bhk) * G + g) * 256 + threadIdx.x] = 0;
     const int b = bhk / HK, ho = (bhk % HK) * G + g;
     const uint32_t* base = reinterpret_cast<const uint32_t*>(
         q + b * qs_b + static_cast<int64_t>(ho * R) * qs_h + static_cast<int64_t>(QL - tail) * qs_t) + lane;
@@ -142,7 +146,9 @@ __global__ __launch_bounds__(QM_THREADS) void qmean_kernel(const uint16_t* __res
         double sum = 0.0;
 #pragma unroll
         for (int k = 0; k < QM_SLICES; ++k) sum += s_sum[k][threadIdx.x];
-        out[threadIdx.x] = half_bits_to_f64(f64_to_half_rne(sum / tail, f16), f16);
+        const uint16_t m = f64_to_half_rne(sum / tail, f16);
+        out[threadIdx.x] = half_bits_to_f64(m, f16);
+        outb[threadIdx.x] = m;
     }
 }
 
@@ -167,16 +173,22 @@ __device__ __forceinline__ void add8_f64(double (&acc)[8], uint4 v, bool f16) {
 template <int THREADS>
 __global__ __launch_bounds__(THREADS) void qmean16_kernel(const uint16_t* __restrict__ q, int64_t qs_b, int64_t qs_h,
                                                             int64_t qs_t, int QL, int tail, int R, int HK, int G,
-                                                            int GP, int f16, double* __restrict__ qm) {
+                                                            int GP, int f16, double* __restrict__ qm,
+                                                            uint16_t* __restrict__ qb, uint32_t* __restrict__ hist) {
     const int row = blockIdx.x;                    // (b, hk, g)
     const int g = row % GP;
     const int bhk = row / GP;
     const int tid = threadIdx.x;
     double* out = qm + static_cast<int64_t>(row) * 128;
+    uint16_t* outb = qb + static_cast<int64_t>(row) * 128;
     if (g >= G) {
-        if (tid < 128) out[tid] = 0.0;
+        if (tid < 128) {
+            out[tid] = 0.0;
+            outb[tid] = 0;
+        }
         return;
     }
+    if (tid < 256) hist[(static_cast<int64_t>(bhk) * G + g) * 256 + tid] = 0;
     constexpr int QV_SLOTS = THREADS / 16;
     const int b = bhk / HK, ho = (bhk % HK) * G + g;
     const int sub = tid & 15, slot = tid >> 4;
@@ -227,12 +239,16 @@ __global__ __launch_bounds__(THREADS) void qmean16_kernel(const uint16_t* __rest
         double sum = 0.0;
 #pragma unroll
         for (int k = 0; k < THREADS / 64; ++k) sum += s_sum[k][tid];
-        out[tid] = half_bits_to_f64(f64_to_half_rne(sum / tail, f16), f16);
+        const uint16_t m = f64_to_half_rne(sum / tail, f16);
+        out[tid] = half_bits_to_f64(m, f16);
+        outb[tid] = m;
     }
 }
 
 // keys of one output row start 16-byte aligned
 __host__ __device__ inline int64_t key_pitch(int64_t P) { return (P + 7) / 8 * 8; }
+// words of the uncertain bitmap per output row
+__host__ __device__ inline int64_t unc_words(int64_t P) { return (P + 31) / 32; }
 
 // Buffer descriptor over `bytes` bytes at `base`: loads past the range read
 // zeros without touching memory, so the score kernel's loads need no branch
@@ -265,8 +281,12 @@ constexpr int SC_WG_ROWS = 4 * SC_BLOCKS * SC_ROWS;
 template <int GM, bool F16>
 __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__ k, int64_t ks_b, int64_t ks_h,
                                                     int64_t ks_n, int HK, int G, int64_t P, int64_t KP,
-                                                    const double* __restrict__ qm, uint16_t* __restrict__ keys) {
+                                                    const double* __restrict__ qm, uint16_t* __restrict__ keys,
+                                                    uint32_t* __restrict__ unc, uint32_t* __restrict__ hist) {
     __shared__ __align__(16) uint8_t s_rows[4][SC_ROWS * SC_PITCH];
+    __shared__ uint32_t s_hist[GM][256];           // certified (here: all) keys by high byte
+    for (int i = threadIdx.x; i < GM * 256; i += 256) (&s_hist[0][0])[i] = 0;
+    __syncthreads();
     const int bh = blockIdx.y;                     // b * HK + hk
     const int b = bh / HK, hk = bh % HK;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -298,8 +318,9 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
         __builtin_amdgcn_sched_barrier(0);
     };
     const double* qg = qm + static_cast<int64_t>(bh) * GM * 128;
-    if (nst == 0) return;                          // (nst is even: both first stages hold rows)
+    const int64_t UW = unc_words(P);
     uint4 ra[8], rb[8];
+    if (nst > 0) {                                 // (nst is even: both first stages hold rows)
     load(ra, 0);
     load(rb, 1);
     uint8_t* lds = s_rows[wave];
@@ -335,14 +356,20 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
             }
         }
         if (half) {
-            const int64_t p = r0 + (wave + 4 * (s >> 1)) * SC_ROWS + lane;
+            const int64_t pb = r0 + (wave + 4 * (s >> 1)) * SC_ROWS;
+            const int64_t p = pb + lane;
             if (p < P) {
 #pragma unroll
                 for (int g = 0; g < GM; ++g)
-                    if (g < G)
-                        keys[(static_cast<int64_t>(bh) * G + g) * KP + p] =
-                            static_cast<uint16_t>(orderable_key(f64_to_half_rne(acc[g], F16)));
+                    if (g < G) {
+                        const uint32_t key = orderable_key(f64_to_half_rne(acc[g], F16));
+                        keys[(static_cast<int64_t>(bh) * G + g) * KP + p] = static_cast<uint16_t>(key);
+                        atomicAdd(&s_hist[g][key >> 8], 1u);
+                    }
             }
+            // every key here is exact: the block's uncertain words are zero
+            if (lane < 2 * G && pb + 32 * (lane & 1) < P)
+                unc[(static_cast<int64_t>(bh) * G + (lane >> 1)) * UW + pb / 32 + (lane & 1)] = 0u;
 #pragma unroll
             for (int g = 0; g < GM; ++g) acc[g] = 0.0;
         }
@@ -361,6 +388,282 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
         compute(s + 1);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last (empty) loads retire before the wave ends
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * 256; i += 256) {
+        const uint32_t c = (&s_hist[0][0])[i];
+        if (c) atomicAdd(hist + (static_cast<int64_t>(bh) * G + i / 256) * 256 + (i & 255), c);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 scores on the matrix cores, with certified keys
+// ---------------------------------------------------------------------------
+// The score is bf16(R), R the float64 sequential sum of the exact products
+// qm[g, d] * k[p, d] (score_kernel).  Here v_mfma_f32_16x16x32_bf16 takes 16
+// key rows (M) by 32 channels (K) against the query means (N): each 32-channel
+// chunk c of a row gives an fp32 partial D_c in an accumulator of its own,
+// s = (D_0 + D_1) + (D_2 + D_3), and MFMAs over |k| and |qm| give
+// A' = sum_c A'_c >= (1 - 2^-17) A, A = sum_d |qm_d k_d|.
+//
+// Error bound.  Model of the MFMA: the products of bf16 values are exact; the
+// result differs from the exact sum of the products and the accumulator input
+// by at most 32 * 2^-23 times the sum of their magnitudes, whatever the order
+// and rounding of its additions, and equals the accumulator input when every
+// product is zero; subnormal inputs, products and results may be flushed to
+// zero.  Then
+//   |D_c - S_c| <= 2^-18 A_c + 2^-120      (S_c the chunk's exact sum),
+//   the three fp32 additions add at most 2^-23 A,
+//   R lies within 127 * 2^-53 A of the exact sum,
+//   flushed subnormal key elements lose at most 2^-126 sum_d |qm_d| <= 2^-59
+//   when every nonzero |qm_d| lies in [2^-60, 2^60],
+// so |s - R| <= 1.04 * 2^-18 A' + 2^-58.9.  With E = 2^-17 A' + 2^-56 the fp32
+// ends lo = s - E and hi = s + E (rounded: below 2^-24 (|s| + E) each) still
+// enclose R.  RNE to bf16 is monotone, so when bf16(lo) and bf16(hi) are one
+// value, its key is the key of R: the score is certified.  Otherwise the pass
+// stores the key of bf16(hi), an upper bound of the exact key, and sets the
+// position's bit in the uncertain bitmap; A' above 2^100 (overflow, an
+// infinite or NaN input) stores the largest key.  The top-k recomputes, in
+// float64, the uncertain positions that can still be selected.  When a query
+// mean has a NaN, an infinity or a nonzero |qm_d| outside [2^-60, 2^60], the
+// pass computes that key head's scores in float64 instead (exact keys).
+//
+// The pass also counts each output row's certified keys by their high byte
+// (hist, zeroed by the query-mean kernel); the top-k starts from that count.
+//
+// One workgroup per SM_WG_ROWS rows of one (b, hk); wavefront w takes the
+// 32-row stages w, w + 4, ...  A stage is 8 KB: eight 1 KB non-temporal loads
+// (lane l: row 4i + l / 16, bytes 16 (l % 16) of it, so each instruction reads
+// four whole rows) into one of two register stages, copied to the wavefront's
+// LDS rows (pitch 272 B) and read back in the MFMA layout: lane l holds row
+// l % 16, channels 32c + 8 (l / 16) .. + 7.
+//
+// Packing: with GM heads, TPK = 16 / GM row tiles share one accumulator.  The
+// B operand of tile j is the query means in columns GM j .. GM j + GM - 1 and
+// zero elsewhere, so column n ends up with head n % GM of tile n / GM, and
+// every lane's four results (rows 4 (l / 16) + v of its column) are scores:
+// the certification work is spread over all 64 lanes.  Tile j of a packed
+// group of stages sits in stage j / 2 of the group, rows 16 (j % 2).
+constexpr int SM_ROWS = 32;                 // rows per stage
+constexpr int SM_PITCH = 272;               // LDS bytes per row (256 + 16)
+constexpr int SM_STAGES = 8;                // stages per wavefront
+constexpr int SM_WG_ROWS = 4 * SM_STAGES * SM_ROWS;
+
+typedef __bf16 sel_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float sel_f32x4 __attribute__((ext_vector_type(4)));
+
+// the exact (float64, d order) key of one bf16 row held in LDS, as score_kernel
+__device__ __forceinline__ uint32_t exact_key_lds(const uint8_t* row, const double* q) {
+    double acc = 0.0;
+#pragma unroll 4
+    for (int c = 0; c < 16; ++c) {
+        const uint4 w = *reinterpret_cast<const uint4*>(row + 16 * c);
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float kv = __uint_as_float(j & 1 ? ww[j >> 1] & 0xffff0000u : ww[j >> 1] << 16);
+            acc = fma(q[8 * c + j], static_cast<double>(kv), acc);
+        }
+    }
+    return orderable_key(f64_to_bf16_rne(acc));
+}
+
+template <int GM>
+__global__ __launch_bounds__(256) void score_mfma_kernel(const uint16_t* __restrict__ k, int64_t ks_b, int64_t ks_h,
+                                                         int64_t ks_n, int HK, int G, int64_t P, int64_t KP,
+                                                         const double* __restrict__ qm, const uint16_t* __restrict__ qb,
+                                                         uint16_t* __restrict__ keys, uint32_t* __restrict__ unc,
+                                                         uint32_t* __restrict__ hist) {
+    constexpr int TPK = 16 / GM;                   // tiles per packed accumulator
+    constexpr int SPK = TPK >= 2 ? TPK / 2 : 1;    // stages per packed group
+    constexpr int SGRP = SPK >= 2 ? SPK : 2;       // stages per loop pass (two register stages)
+    __shared__ __align__(16) uint8_t s_rows[4][SM_ROWS * SM_PITCH];
+    __shared__ uint32_t s_hist[GM][256];
+    const int bh = blockIdx.y;                     // b * HK + hk
+    const int b = bh / HK, hk = bh % HK;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * SM_WG_ROWS;
+    const int nrows = static_cast<int>(min<int64_t>(SM_WG_ROWS, P - r0));
+    const uint32_t rowb = static_cast<uint32_t>(ks_n) * 2;          // bytes between rows (host: < 2^21)
+    const Rsrc rk = make_rsrc(k + b * ks_b + hk * ks_h + r0 * ks_n, static_cast<uint32_t>(nrows) * rowb);
+    const int nblk = (nrows + SM_ROWS - 1) / SM_ROWS;
+    const int mine = nblk > wave ? (nblk - wave + 3) / 4 : 0;
+    const int n = lane & 15, kg = lane >> 4;
+    const int h = n % GM, jt = n / GM;             // head and tile of this lane's column
+    // B operand of head h (bf16 bits of the means), and whether the means of
+    // the key head's query heads are fit for the bound
+    uint4 qw[4];
+    bool bad = false;
+    const uint16_t* qbrow = qb + (static_cast<int64_t>(bh) * GM + h) * 128;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        qw[c] = *reinterpret_cast<const uint4*>(qbrow + 32 * c + 8 * kg);
+        const uint32_t ww[4] = {qw[c].x, qw[c].y, qw[c].z, qw[c].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t e = (ww[j >> 1] >> (16 * (j & 1))) & 0x7fffu;
+            // zero, or |x| in [2^-60, 2^60]: biased exponent in [67, 187]
+            bad |= !(e == 0 || (e >= (67u << 7) && e < (188u << 7)));
+        }
+    }
+    const bool exact = __ballot(bad && h < G) != 0;   // the same in every workgroup of bh
+    for (int i = threadIdx.x; i < GM * 256; i += 256) (&s_hist[0][0])[i] = 0;
+    __syncthreads();
+    uint8_t* lds = s_rows[wave];
+    const int sub = lane & 15, rq = lane >> 4;
+    const uint32_t vo0 = static_cast<uint32_t>(rq) * rowb + 16 * sub;
+    // the whole offset in the lane offset, which the descriptor's range check
+    // covers: stages past the rows read zeros without touching memory
+    auto load = [&](uint4 (&r)[8], int st) {
+        const uint32_t so = static_cast<uint32_t>((wave + 4 * st) * SM_ROWS) * rowb;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, vo0 + so + 4 * i * rowb, 0, POL_NT));
+        // keep the stages in issue order: a stage's wait counts the loads issued after it
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // One wavefront writes and reads its own LDS rows, and its LDS accesses
+    // execute in program order
+    auto stage = [&](const uint4 (&r)[8]) {
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(lds + (4 * i + rq) * SM_PITCH + 16 * sub) = r[i];
+        __builtin_amdgcn_wave_barrier();
+    };
+    const int64_t UW = unc_words(P);
+    sel_f32x4 d[4], a[4];
+    auto zero_acc = [&]() {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            d[c] = sel_f32x4{0.f, 0.f, 0.f, 0.f};
+            a[c] = sel_f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    // tile tj of the packed accumulator from LDS rows 16 t .. 16 t + 15
+    auto mfma_tile = [&](int tj, int t) {
+        uint32_t msk = jt == tj ? 0xffffffffu : 0u;
+        asm volatile("" : "+v"(msk));              // per tile: hoisted, the masked operands would take 128 VGPRs
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint4 w = *reinterpret_cast<const uint4*>(lds + (16 * t + n) * SM_PITCH + 64 * c + 16 * kg);
+            const uint4 wa = {w.x & 0x7fff7fffu, w.y & 0x7fff7fffu, w.z & 0x7fff7fffu, w.w & 0x7fff7fffu};
+            const uint4 qv = {qw[c].x & msk, qw[c].y & msk, qw[c].z & msk, qw[c].w & msk};
+            const uint4 qa = {qv.x & 0x7fff7fffu, qv.y & 0x7fff7fffu, qv.z & 0x7fff7fffu, qv.w & 0x7fff7fffu};
+            d[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(sel_bf16x8, w),
+                                                          __builtin_bit_cast(sel_bf16x8, qv), d[c], 0, 0, 0);
+            a[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(sel_bf16x8, wa),
+                                                          __builtin_bit_cast(sel_bf16x8, qa), a[c], 0, 0, 0);
+        }
+    };
+    // Keys, histogram counts and uncertain bits of the packed accumulator of
+    // the group starting at stage sfirst (GM <= 8), or of tile t1 of stage
+    // sfirst (GM = 16).  Returns this lane's bits of its stage's word, OR-ed
+    // over the lanes that share the word.
+    auto epilogue = [&](int sfirst, int t1) -> uint32_t {
+        const int st = TPK >= 2 ? sfirst + jt / 2 : sfirst;
+        const int tin = TPK >= 2 ? (jt & 1) : t1;
+        const int blk = wave + 4 * st;
+        const int rt = blk * SM_ROWS + 16 * tin + 4 * kg;   // first of this lane's four rows
+        uint32_t kv[4], nib = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float sv = (d[0][v] + d[1][v]) + (d[2][v] + d[3][v]);
+            const float av = (a[0][v] + a[1][v]) + (a[2][v] + a[3][v]);
+            const float e = fmaf(av, 0x1p-17f, 0x1p-56f);
+            const uint32_t lo = __float_as_uint(sv - e), hi = __float_as_uint(sv + e);
+            const uint32_t blo = (lo + 0x7fffu + ((lo >> 16) & 1u)) >> 16;   // RNE to bf16 (finite values)
+            const uint32_t bhi = (hi + 0x7fffu + ((hi >> 16) & 1u)) >> 16;
+            const bool fin = av <= 0x1p100f;                                  // false for NaN
+            const bool cert = fin && blo == bhi;
+            const uint32_t key = orderable_key(static_cast<uint16_t>(bhi));
+            kv[v] = fin ? key : 0xffffu;
+            if (cert && rt + v < nrows && h < G) atomicAdd(&s_hist[h][key >> 8], 1u);
+            nib |= (cert ? 0u : 1u) << v;
+        }
+        if (h < G && rt < nrows) {
+            uint16_t* kr = keys + (static_cast<int64_t>(bh) * G + h) * KP + r0 + rt;
+            if (rt + 3 < nrows) {
+                *reinterpret_cast<uint2*>(kr) = uint2{kv[0] | (kv[1] << 16), kv[2] | (kv[3] << 16)};
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (rt + v < nrows) kr[v] = static_cast<uint16_t>(kv[v]);
+            }
+        }
+        const int nv = min(4, max(0, nrows - rt));     // rows past the workgroup's end are not uncertain
+        uint32_t word = (nib & ((1u << nv) - 1u)) << (16 * tin + 4 * kg);
+        word |= __shfl_xor(word, 16, 64);
+        word |= __shfl_xor(word, 32, 64);
+        if (TPK >= 2) {
+            word |= __shfl_xor(word, GM, 64);          // the stage's other tile
+            if (kg == 0 && (jt & 1) == 0 && h < G && blk < nblk)
+                unc[(static_cast<int64_t>(bh) * G + h) * UW + r0 / 32 + blk] = word;
+        }
+        return word;
+    };
+    // float64 keys of one stage (rows of lanes 0 .. 31), every head
+    auto exact_stage = [&](int blk) {
+        const int rbase = blk * SM_ROWS;
+        if (lane < SM_ROWS && rbase + lane < nrows) {
+            for (int g = 0; g < G; ++g) {
+                const uint32_t key = exact_key_lds(lds + lane * SM_PITCH, qm + (static_cast<int64_t>(bh) * GM + g) * 128);
+                keys[(static_cast<int64_t>(bh) * G + g) * KP + r0 + rbase + lane] = static_cast<uint16_t>(key);
+                atomicAdd(&s_hist[g][key >> 8], 1u);
+            }
+        }
+        if (lane < G) unc[(static_cast<int64_t>(bh) * G + lane) * UW + r0 / 32 + blk] = 0u;
+    };
+    // stage st, already in LDS (sg: its place in the packed group): MFMAs,
+    // or the float64 keys
+    auto compute = [&](int st, int sg) {
+        const int blk = wave + 4 * st;
+        if (exact) {
+            if (blk < nblk) exact_stage(blk);
+            return;
+        }
+        if (TPK >= 2) {
+            if (sg == 0) zero_acc();
+            mfma_tile(2 * sg, 0);
+            mfma_tile(2 * sg + 1, 1);
+            if (sg == SPK - 1) epilogue(st - SPK + 1, 0);
+        } else {
+            zero_acc();
+            mfma_tile(0, 0);
+            uint32_t w = epilogue(st, 0);
+            zero_acc();
+            mfma_tile(0, 1);
+            w |= epilogue(st, 1);
+            if (kg == 0 && h < G && blk < nblk) unc[(static_cast<int64_t>(bh) * G + h) * UW + r0 / 32 + blk] = w;
+        }
+    };
+    // Stages past `mine` lie past the descriptor's range (zeros, nothing
+    // stored).  The loop runs whole packed groups of stages and whole pairs
+    // of register stages; a register stage is reloaded as soon as it is
+    // copied to LDS, so two stages' loads are in flight while one is computed.
+    const int nst = (mine + SGRP - 1) / SGRP * SGRP;
+    if (nst > 0) {
+        uint4 ra[8], rb[8];
+        load(ra, 0);
+        load(rb, 1);
+        for (int s0 = 0; s0 < nst; s0 += SGRP) {
+#pragma unroll
+            for (int u = 0; u < SGRP; u += 2) {
+                stage(ra);
+                load(ra, s0 + u + 2);
+                compute(s0 + u, u % SPK);
+                stage(rb);
+                load(rb, s0 + u + 3);
+                compute(s0 + u + 1, (u + 1) % SPK);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last (empty) loads retire before the wave ends
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * 256; i += 256) {
+        const uint32_t c = (&s_hist[0][0])[i];
+        if (c) atomicAdd(hist + (static_cast<int64_t>(bh) * G + i / 256) * 256 + (i & 255), c);
+    }
 }
 
 constexpr int TOPK_WAVES = TOPK_THREADS / 64;
@@ -373,6 +676,8 @@ constexpr int TOPK_RANK_MAX = 2048;        // winners the rank path's per-thread
 // sorted (log2(n2) (log2(n2) + 1) / 2 barrier-separated stages), which costs
 // less vector work from about 512 winners up
 constexpr int TOPK_RANK_LIMIT = 512;
+// key offsets above the candidate bound that the counting rank covers
+constexpr int TOPK_SPAN = 2048;
 constexpr size_t TOPK_LDS_MAX = 64 * 1024; // keys are cached in LDS while the row fits this budget
 
 // Wavefront 0: the bin holding the need-th largest entry of a 256-bin
@@ -443,46 +748,129 @@ __device__ __forceinline__ void load4(const uint64_t* s, int j, uint64_t (&w)[4]
     w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y;
 }
 
-// One workgroup per (b, ho) row.  Two radix passes over the 16-bit keys (one
-// histogram per pair of wavefronts) find the threshold key K and how many of
-// the entries equal to K are taken (the r of lowest index: a prefix count
-// over contiguous per-thread index ranges); the T winners' composites are
-// collected and each is written straight to its output position, its rank
-// among the winners (T <= TOPK_RANK_LIMIT), or bitonic-sorted first (larger
-// T), in LDS or, when n2 composites do not fit the LDS budget (GSORT), in
-// this row's slice of a global buffer.  Dynamic LDS: [hist][winners][keys]
-// ([hist][keys] with GSORT).
-template <typename C, bool GSORT>
-__global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __restrict__ keys, int64_t P, int T,
-                                                            int n2, int cached, C* __restrict__ gsel,
-                                                            int64_t* __restrict__ out) {
-    extern __shared__ __align__(16) uint32_t tk_lds[];
-    uint32_t* hist = tk_lds;                       // [TOPK_HIST][256]
-    const int row = blockIdx.x;
-    C* sel = GSORT ? gsel + static_cast<int64_t>(row) * n2 : reinterpret_cast<C*>(tk_lds + TOPK_HIST * 256);
-    uint16_t* s_keys = GSORT ? reinterpret_cast<uint16_t*>(tk_lds + TOPK_HIST * 256)
-                             : reinterpret_cast<uint16_t*>(reinterpret_cast<C*>(tk_lds + TOPK_HIST * 256) + n2);
-    __shared__ uint32_t s_bin, s_need, s_count;
-    __shared__ uint32_t s_wsum[TOPK_WAVES];
-    const uint16_t* kr = keys + static_cast<int64_t>(row) * key_pitch(P);
+// Writes the indices of the T composites in sel (unique, zero-padded to n2)
+// in descending order: each at its rank among them (rank_ok: T <= TOPK_RANK_LIMIT
+// and sel in LDS; a thread ranks its up to four winners in one sweep, every
+// lane of a wavefront reading the same four composites per step), or after
+// a bitonic sort of the n2 entries.  Ends with the workgroup's threads done.
+template <typename C>
+__device__ void topk_sort_out(C* sel, int T, int n2, bool rank_ok, int64_t* __restrict__ orow) {
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    if (cached) {
-        // 16-byte copies, all of a thread's loads issued before its LDS writes
-        const int64_t n8 = (P + 7) / 8;
-        const uint4* src = reinterpret_cast<const uint4*>(kr);
-        uint4* dst = reinterpret_cast<uint4*>(s_keys);
-        for (int64_t i0 = tid; i0 < n8; i0 += 4 * TOPK_THREADS) {
-            uint4 v[4];
+    if (rank_ok) {
+        constexpr int E = TOPK_RANK_MAX / TOPK_THREADS;
+        C v[E];
+        uint32_t rank[E];
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (i0 + u * TOPK_THREADS < n8) v[u] = src[i0 + u * TOPK_THREADS];
+        for (int u = 0; u < E; ++u) {
+            v[u] = tid + u * TOPK_THREADS < T ? sel[tid + u * TOPK_THREADS] : C(0);
+            rank[u] = 0;
+        }
+        const int ne = (T - tid + TOPK_THREADS - 1) / TOPK_THREADS;   // winners of this thread
+        if (ne > 2) {
+            for (int j = 0; j < n2 / 4; ++j) {
+                C w[4];
+                load4(sel, j, w);
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (i0 + u * TOPK_THREADS < n8) dst[i0 + u * TOPK_THREADS] = v[u];
+                for (int u = 0; u < E; ++u) rank[u] += (w[0] > v[u]) + (w[1] > v[u]) + (w[2] > v[u]) + (w[3] > v[u]);
+            }
+        } else if (ne > 0) {
+            for (int j = 0; j < n2 / 4; ++j) {
+                C w[4];
+                load4(sel, j, w);
+#pragma unroll
+                for (int u = 0; u < 2; ++u) rank[u] += (w[0] > v[u]) + (w[1] > v[u]) + (w[2] > v[u]) + (w[3] > v[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < E; ++u)
+            if (u < ne) orow[rank[u]] = Comp<C>::index(v[u]);
+        return;
+    }
+    if (n2 == 2 * TOPK_THREADS) {
+        // 1024 entries in registers, two per thread: entry 128 w + 64 r + l
+        // sits in register r of lane l of wavefront w.  Compare-exchanges
+        // with partners in the same wavefront use the other register
+        // (stride 64) or a lane shuffle; strides of 128 and more go through
+        // sel with a barrier on each side.
+        const int wv = tid >> 6, ln = tid & 63;
+        C v[2] = {sel[128 * wv + ln], sel[128 * wv + 64 + ln]};
+        auto keep = [](C mine, C other, bool take_max) { return take_max ? (mine > other ? mine : other)
+                                                                        : (mine < other ? mine : other); };
+        for (int size = 2; size <= n2; size <<= 1) {
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                if (stride >= 128) {
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) sel[128 * wv + 64 * r + ln] = v[r];
+                    __syncthreads();
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        const int i = 128 * wv + 64 * r + ln;
+                        v[r] = keep(v[r], sel[i ^ stride], ((i & stride) == 0) == ((i & size) == 0));
+                    }
+                    __syncthreads();
+                } else if (stride == 64) {
+                    const int i0 = 128 * wv + ln;              // the lower entry of the pair is register 0
+                    const bool desc = (i0 & size) == 0;
+                    const C hi = v[0] > v[1] ? v[0] : v[1], lo = v[0] > v[1] ? v[1] : v[0];
+                    v[0] = desc ? hi : lo;
+                    v[1] = desc ? lo : hi;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        const int i = 128 * wv + 64 * r + ln;
+                        C o;
+                        if constexpr (sizeof(C) == 4) {
+                            o = static_cast<C>(__shfl_xor(static_cast<int>(v[r]), stride, 64));
+                        } else {
+                            const int lo32 = __shfl_xor(static_cast<int>(static_cast<uint32_t>(v[r])), stride, 64);
+                            const int hi32 = __shfl_xor(static_cast<int>(static_cast<uint32_t>(v[r] >> 32)), stride, 64);
+                            o = (static_cast<C>(static_cast<uint32_t>(hi32)) << 32) | static_cast<uint32_t>(lo32);
+                        }
+                        v[r] = keep(v[r], o, ((i & stride) == 0) == ((i & size) == 0));
+                    }
+                }
+            }
+        }
+        for (int r = 0; r < 2; ++r) {
+            const int i = 128 * wv + 64 * r + ln;
+            if (i < T) orow[i] = Comp<C>::index(v[r]);
+        }
+        return;
+    }
+    // bitonic sort, descending
+    for (int size = 2; size <= n2; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < n2 / 2; i += TOPK_THREADS) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool desc = ((lo & size) == 0);
+                const C x = sel[lo], y = sel[hi];
+                if ((x < y) == desc) {
+                    sel[lo] = y;
+                    sel[hi] = x;
+                }
+            }
+            __syncthreads();
         }
     }
-    auto key_at = [&](int64_t i) -> uint32_t { return cached ? s_keys[i] : kr[i]; };
+    for (int i = tid; i < T; i += TOPK_THREADS) orow[i] = Comp<C>::index(sel[i]);
+}
+
+// The top T of one row of exact 16-bit keys kr (global; s_keys: a copy in
+// LDS, or null).  Two radix passes over the keys (one histogram per pair of
+// wavefronts) find the threshold key K and how many of the entries equal to
+// K are taken (the r of lowest index: a prefix count over contiguous
+// per-thread index ranges); the T winners' composites are collected in sel
+// (n2 entries, LDS or this row's slice of a global buffer) and placed by
+// topk_sort_out.
+template <typename C>
+__device__ void topk_exact_row(const uint16_t* __restrict__ kr, const uint16_t* s_keys, int64_t P, int T, int n2,
+                               bool rank_ok, C* sel, uint32_t* hist, int64_t* __restrict__ orow) {
+    __shared__ uint32_t s_bin, s_need, s_count;
+    __shared__ uint32_t s_wsum[TOPK_WAVES];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    auto key_at = [&](int64_t i) -> uint32_t { return s_keys ? s_keys[i] : kr[i]; };
     uint32_t need = static_cast<uint32_t>(T);
     uint32_t khi = 0;
     for (int pass = 0; pass < 2; ++pass) {
@@ -513,7 +901,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __re
     // numbered in index order by a prefix count over the threads
     const int64_t CH = (P + 8 * TOPK_THREADS - 1) / (8 * TOPK_THREADS) * 8;
     const int64_t i0 = static_cast<int64_t>(tid) * CH;
-    const uint4* k4 = cached ? reinterpret_cast<const uint4*>(s_keys) : reinterpret_cast<const uint4*>(kr);
+    const uint4* k4 = s_keys ? reinterpret_cast<const uint4*>(s_keys) : reinterpret_cast<const uint4*>(kr);
     if (tid == 0) s_count = 0;
     uint32_t eq = 0;
     for (int64_t ib = i0; ib < i0 + CH && ib < P; ib += 8) {
@@ -546,62 +934,349 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(const uint16_t* __re
     }
     for (int i = T + tid; i < n2; i += TOPK_THREADS) sel[i] = 0;   // real composites are > 0
     __syncthreads();
-    int64_t* orow = out + static_cast<int64_t>(row) * T;
-    if (!GSORT && T <= TOPK_RANK_LIMIT) {
-        // rank = number of larger winners.  A thread ranks its (up to 4)
-        // winners in one sweep; every lane of a wavefront reads the same four
-        // composites per step (LDS broadcast)
-        constexpr int E = TOPK_RANK_MAX / TOPK_THREADS;
-        C v[E];
-        uint32_t rank[E];
+    topk_sort_out(sel, T, n2, rank_ok, orow);
+}
+
+// The exact key (float64, d order, one rounding to the model dtype: the
+// score kernels' arithmetic) of the key row at krow; q: the query mean in LDS
+template <bool F16>
+__device__ __forceinline__ uint32_t exact_key_row_t(const uint16_t* __restrict__ krow, const double* q) {
+    uint4 w[16];
 #pragma unroll
-        for (int u = 0; u < E; ++u) {
-            v[u] = tid + u * TOPK_THREADS < T ? sel[tid + u * TOPK_THREADS] : C(0);
-            rank[u] = 0;
-        }
-        const int ne = (T - tid + TOPK_THREADS - 1) / TOPK_THREADS;   // winners of this thread
-        if (ne > 2) {
-            for (int j = 0; j < n2 / 4; ++j) {
-                C w[4];
-                load4(sel, j, w);
+    for (int c = 0; c < 16; ++c) w[c] = reinterpret_cast<const uint4*>(krow)[c];
+    // an offset the compiler cannot see through: the mean's 128 loads stay
+    // in the loop body instead of 256 VGPRs hoisted out of it
+    int z = 0;
+    asm volatile("" : "+v"(z));
+    double acc = 0.0;
 #pragma unroll
-                for (int u = 0; u < E; ++u) rank[u] += (w[0] > v[u]) + (w[1] > v[u]) + (w[2] > v[u]) + (w[3] > v[u]);
-            }
-        } else if (ne > 0) {
-            for (int j = 0; j < n2 / 4; ++j) {
-                C w[4];
-                load4(sel, j, w);
+    for (int c = 0; c < 16; ++c) {
+        const uint32_t ww[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
 #pragma unroll
-                for (int u = 0; u < 2; ++u) rank[u] += (w[0] > v[u]) + (w[1] > v[u]) + (w[2] > v[u]) + (w[3] > v[u]);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < E; ++u)
-            if (u < ne) orow[rank[u]] = Comp<C>::index(v[u]);
-        return;
+        for (int j = 0; j < 8; ++j)
+            acc = fma(q[z + 8 * c + j], half_bits_to_f64(static_cast<uint16_t>(ww[j >> 1] >> (16 * (j & 1))), F16), acc);
     }
-    // bitonic sort, descending
-    for (int size = 2; size <= n2; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < n2 / 2; i += TOPK_THREADS) {
-                const int lo = 2 * i - (i & (stride - 1));
-                const int hi = lo + stride;
-                const bool desc = ((lo & size) == 0);
-                const C x = sel[lo], y = sel[hi];
-                if ((x < y) == desc) {
-                    sel[lo] = y;
-                    sel[hi] = x;
-                }
-            }
+    return orderable_key(f64_to_half_rne(acc, F16));
+}
+// (the model dtype chosen once: a run-time dtype inside the unrolled loop
+// kept both conversions of all 128 elements live)
+__device__ __forceinline__ uint32_t exact_key_row(const uint16_t* __restrict__ krow, const double* q, bool f16) {
+    return f16 ? exact_key_row_t<true>(krow, q) : exact_key_row_t<false>(krow, q);
+}
+
+struct TopkArgs {
+    uint16_t* keys;                  // [rows][KP] keys (exact, or upper bounds where uncertain)
+    const uint32_t* unc;             // [rows][UW] uncertain bits
+    const uint32_t* hist;            // [rows][256] certified keys by high byte
+    int64_t P, KP, UW;
+    int T, n2, cap;                  // winners, sort size, candidate list capacity
+    int fast;                        // the candidate path fits the LDS (else every row takes the exact path)
+    int gsort;                       // the exact path sorts in gsel (n2 composites per row)
+    void* gsel;
+    const uint16_t* k;               // key rows of the uncertain positions' recomputation
+    int64_t ks_b, ks_h, ks_n;
+    int HK, G, GP, f16;
+    const double* qm;                // [b * HK][GP][128] query means
+    int64_t* out;                    // [rows][T]
+};
+
+// One workgroup per (b, ho) row.
+// Candidate path: the certified histogram gives the high byte b of the T-th
+// largest certified key.  One pass over the row lists every position whose
+// stored key (exact, or an upper bound) is >= b << 8 and counts the certified
+// keys of bin b by low byte, which gives L, the T-th largest certified key.
+// The certified keys are exact and at least T of them are >= L, so the T-th
+// largest exact key K is >= L, and the list holds every position whose exact
+// key is >= L: the row's top T (were the list over its capacity, a second
+// pass lists the keys >= L only).  The uncertain entries whose stored key is
+// >= L get their exact keys in float64 (the others are below L, so below K,
+// whatever their exact key), four (six) byte passes of a radix select over
+// the unique composites (key << IDX_BITS) | (IDX_MASK - idx) find the T-th
+// largest, and the T composites at or above it are placed by topk_sort_out.
+// Exact path (fewer than T certified keys, or a list over its capacity): the
+// row's uncertain keys are recomputed in place in the keys array, then
+// topk_exact_row runs on the exact keys.
+// Dynamic LDS: [hist][list (cap C)][sel (n2 C)][uncertain flags (cap bytes)];
+// the exact path uses [hist][sel] (gsort: the global buffer).
+template <typename C>
+__global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
+    extern __shared__ __align__(16) uint32_t tk_lds[];
+    uint32_t* hist = tk_lds;                       // [TOPK_HIST][256]
+    C* list = reinterpret_cast<C*>(tk_lds + TOPK_HIST * 256);
+    C* sel_f = list + a.cap;
+    uint8_t* flags = reinterpret_cast<uint8_t*>(sel_f + a.n2);   // uncertain entries of the list
+    uint32_t* brk = reinterpret_cast<uint32_t*>(flags + (a.cap + 15) / 16 * 16);   // buckets: counts, starts
+    C* brank_tmp = reinterpret_cast<C*>(brk + 2 * TOPK_SPAN);      // entries >= L in bucket order
+    __shared__ uint32_t s_bin, s_need, s_count, s_total, s_ovf;
+    __shared__ uint32_t s_wtot[TOPK_WAVES];
+    __shared__ double s_q[128];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    uint16_t* kr = a.keys + static_cast<int64_t>(row) * a.KP;
+    const uint32_t* ur = a.unc + static_cast<int64_t>(row) * a.UW;
+    int64_t* orow = a.out + static_cast<int64_t>(row) * a.T;
+    // key rows and query means of this output row
+    const int H_out = a.HK * a.G;
+    const int b = row / H_out, ho = row % H_out, hk = ho / a.G, g = ho % a.G;
+    const uint16_t* kbase = a.k + b * a.ks_b + hk * a.ks_h;
+    if (tid < 128) s_q[tid] = a.qm[(static_cast<int64_t>(b * a.HK + hk) * a.GP + g) * 128 + tid];
+    const double* q = s_q;                         // (read after the first barrier below)
+    constexpr int NB = sizeof(C) == 4 ? 4 : 6;     // significant bytes of a composite
+    bool exact_path = !a.fast;
+    if (a.fast) {
+        if (tid < 256) hist[tid] = a.hist[static_cast<int64_t>(row) * 256 + tid];
+        if (tid == 0) s_count = 0;
+        __syncthreads();
+        if (wave == 0) {
+            uint32_t t = hist[4 * lane] + hist[4 * lane + 1] + hist[4 * lane + 2] + hist[4 * lane + 3];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off, 64);
+            if (lane == 0) s_total = t;
+            topk_find_bin(hist, static_cast<uint32_t>(a.T), lane, &s_bin, &s_need);
+        }
+        __syncthreads();
+        exact_path = s_total < static_cast<uint32_t>(a.T);
+        if (!exact_path) {
+            const uint32_t bsel = s_bin, need_lo = s_need;
+            uint32_t* lohist = hist + 256;          // certified keys of bin bsel by low byte
+            if (tid < 256) lohist[tid] = 0;
             __syncthreads();
+            // One pass over the row, 4 x 8 keys (16-byte loads) and their
+            // uncertain bits per thread at a time: every key >= bsel << 8
+            // joins the list (one LDS atomic per wavefront and step), and the
+            // certified keys of bin bsel are counted by low byte.  L, the
+            // T-th largest certified key, is then the bound; list entries
+            // below it are harmless (their exact keys are below L <= K).
+            auto collect = [&](uint32_t lim, bool count_lo) {
+                // (the trip count is the wavefront's: the shuffles below need every lane)
+                for (int64_t i0 = 8 * static_cast<int64_t>(tid); i0 - 8 * lane < a.P; i0 += 32 * TOPK_THREADS) {
+                    uint4 w[4];
+                    uint32_t ub[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int64_t ib = i0 + u * 8 * TOPK_THREADS;
+                        w[u] = ib < a.P ? *reinterpret_cast<const uint4*>(kr + ib) : uint4{0, 0, 0, 0};
+                        ub[u] = ib < a.P ? (ur[ib >> 5] >> (ib & 31)) & 0xffu : 0u;
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int64_t ib = i0 + u * 8 * TOPK_THREADS;
+                        const uint32_t ws[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+                        uint32_t take = 0;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const uint32_t key = (ws[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+                            const bool in = ib + j < a.P;
+                            take |= static_cast<uint32_t>(in && key >= lim) << j;
+                            if (count_lo && in && !((ub[u] >> j) & 1u) && (key >> 8) == bsel)
+                                atomicAdd(&lohist[key & 0xffu], 1u);
+                        }
+                        // wavefront-aggregated slots
+                        const uint32_t c = __popc(take);
+                        uint32_t incl = c;
+#pragma unroll
+                        for (int off = 1; off < 64; off <<= 1) {
+                            const uint32_t o = __shfl_up(incl, off, 64);
+                            if (lane >= off) incl += o;
+                        }
+                        uint32_t base = 0;
+                        if (lane == 63 && incl) base = atomicAdd(&s_count, incl);
+                        base = __shfl(base, 63, 64) + incl - c;
+                        while (take) {
+                            const int j = __ffs(static_cast<int>(take)) - 1;
+                            take &= take - 1;
+                            if (base < static_cast<uint32_t>(a.cap)) {
+                                const uint32_t key = (ws[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+                                list[base] = Comp<C>::make(key, ib + j);
+                                flags[base] = static_cast<uint8_t>((ub[u] >> j) & 1u);
+                            }
+                            ++base;
+                        }
+                    }
+                }
+            };
+            collect(bsel << 8, true);
+            __syncthreads();
+            if (wave == 0) topk_find_bin(lohist, need_lo, lane, &s_bin, &s_need);
+            __syncthreads();
+            const uint32_t L = (bsel << 8) | s_bin;
+            if (s_count > static_cast<uint32_t>(a.cap)) {
+                // over the capacity: collect again from the bound itself
+                __syncthreads();
+                if (tid == 0) s_count = 0;
+                __syncthreads();
+                collect(L, false);
+                __syncthreads();
+            }
+            const uint32_t cnt = s_count;
+            exact_path = cnt > static_cast<uint32_t>(a.cap);
+            if (!exact_path) {
+                // exact keys of the uncertain entries that can reach the bound:
+                // their slots are gathered first (in sel_f, free until the
+                // winners are collected), so that a thread recomputes one row
+                uint32_t* uslot = reinterpret_cast<uint32_t*>(sel_f);
+                const uint32_t ucap = static_cast<uint32_t>(a.n2) * sizeof(C) / 4;
+                if (tid == 0) s_total = 0;
+                __syncthreads();
+                for (uint32_t i0 = tid; i0 - lane < cnt; i0 += TOPK_THREADS) {
+                    const bool u = i0 < cnt && flags[i0] &&
+                                   static_cast<uint32_t>(list[i0] >> Comp<C>::IDX_BITS) >= L;
+                    const uint64_t m = __ballot(u);
+                    uint32_t base = 0;
+                    if (lane == 0 && m) base = atomicAdd(&s_total, static_cast<uint32_t>(__popcll(m)));
+                    base = __shfl(base, 0, 64) + static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)));
+                    if (u && base < ucap) uslot[base] = i0;
+                }
+                __syncthreads();
+                const uint32_t ucnt = s_total;
+                if (ucnt <= ucap) {
+                    for (uint32_t u = tid; u < ucnt; u += TOPK_THREADS) {
+                        const uint32_t i = uslot[u];
+                        const int64_t idx = Comp<C>::index(list[i]);
+                        list[i] = Comp<C>::make(exact_key_row(kbase + idx * a.ks_n, q, a.f16 != 0), idx);
+                    }
+                } else {
+                    for (uint32_t i = tid; i < cnt; i += TOPK_THREADS) {
+                        if (!flags[i]) continue;
+                        const C c = list[i];
+                        if (static_cast<uint32_t>(c >> Comp<C>::IDX_BITS) < L) continue;
+                        const int64_t idx = Comp<C>::index(c);
+                        list[i] = Comp<C>::make(exact_key_row(kbase + idx * a.ks_n, q, a.f16 != 0), idx);
+                    }
+                }
+                __syncthreads();
+                // Ranks by counting, while every entry at or above L has a
+                // key within TOPK_SPAN of L: each such entry is counted in
+                // its key's bucket, a bucket's first rank is the number of
+                // entries with larger keys, and inside a bucket the larger
+                // composite (the lower index) comes first.  The entries ranked
+                // below T are the winners, each written at its rank.
+                {
+                    uint32_t* bcnt = brk;                   // bucket counts (then fill counters)
+                    uint32_t* bstart = brk + TOPK_SPAN;     // first rank of each bucket
+                    for (int i = tid; i < TOPK_SPAN; i += TOPK_THREADS) bcnt[i] = 0;
+                    if (tid == 0) s_ovf = 0;
+                    __syncthreads();
+                    for (uint32_t i = tid; i < cnt; i += TOPK_THREADS) {
+                        const uint32_t key = static_cast<uint32_t>(list[i] >> Comp<C>::IDX_BITS);
+                        if (key >= L) {
+                            if (key - L < static_cast<uint32_t>(TOPK_SPAN)) atomicAdd(&bcnt[key - L], 1u);
+                            else s_ovf = 1;
+                        }
+                    }
+                    __syncthreads();
+                    if (!s_ovf) {
+                        // exclusive prefix over the buckets in descending key order
+                        // (thread t: buckets SPAN - 1 - BPT t - u, u < BPT)
+                        constexpr int BPT = TOPK_SPAN / TOPK_THREADS;
+                        uint32_t cu[BPT], sum = 0;
+#pragma unroll
+                        for (int u = 0; u < BPT; ++u) {
+                            cu[u] = bcnt[TOPK_SPAN - 1 - BPT * tid - u];
+                            sum += cu[u];
+                        }
+                        uint32_t incl = sum;
+#pragma unroll
+                        for (int off = 1; off < 64; off <<= 1) {
+                            const uint32_t o = __shfl_up(incl, off, 64);
+                            if (lane >= off) incl += o;
+                        }
+                        if (lane == 63) s_wtot[wave] = incl;
+                        __syncthreads();
+                        uint32_t excl = incl - sum;
+                        for (int w = 0; w < wave; ++w) excl += s_wtot[w];
+#pragma unroll
+                        for (int u = 0; u < BPT; ++u) {
+                            bstart[TOPK_SPAN - 1 - BPT * tid - u] = excl;
+                            bcnt[TOPK_SPAN - 1 - BPT * tid - u] = 0;
+                            excl += cu[u];
+                        }
+                        __syncthreads();
+                        for (uint32_t i = tid; i < cnt; i += TOPK_THREADS) {
+                            const C c = list[i];
+                            const uint32_t key = static_cast<uint32_t>(c >> Comp<C>::IDX_BITS);
+                            if (key >= L) brank_tmp[bstart[key - L] + atomicAdd(&bcnt[key - L], 1u)] = c;
+                        }
+                        __syncthreads();
+                        // the entries at or above L, bucket by bucket (the fill counters are the counts again)
+                        const uint32_t tot = bstart[0] + bcnt[0];
+                        for (uint32_t pos = tid; pos < tot; pos += TOPK_THREADS) {
+                            const C c = brank_tmp[pos];
+                            const uint32_t off = static_cast<uint32_t>(c >> Comp<C>::IDX_BITS) - L;
+                            const uint32_t s0 = bstart[off], n = bcnt[off];
+                            if (s0 >= static_cast<uint32_t>(a.T)) continue;
+                            uint32_t rin = 0;
+                            for (uint32_t j = 0; j < n; ++j) rin += brank_tmp[s0 + j] > c;
+                            if (s0 + rin < static_cast<uint32_t>(a.T)) orow[s0 + rin] = Comp<C>::index(c);
+                        }
+                        return;
+                    }
+                }
+                // radix select of the T-th largest composite, a byte at a time
+                C prefix = 0, pmask = 0;
+                uint32_t need = static_cast<uint32_t>(a.T);
+                for (int pass = 0; pass < NB; ++pass) {
+                    const int shift = 8 * (NB - 1 - pass);
+                    for (int i = tid; i < TOPK_HIST * 256; i += TOPK_THREADS) hist[i] = 0;
+                    __syncthreads();
+                    for (uint32_t i = tid; i < cnt; i += TOPK_THREADS) {
+                        const C c = list[i];
+                        // (entries below L are not winners)
+                        if ((c & pmask) == prefix && static_cast<uint32_t>(c >> Comp<C>::IDX_BITS) >= L)
+                            atomicAdd(&hist[(wave >> 1) * 256 + static_cast<uint32_t>((c >> shift) & 0xffu)], 1u);
+                    }
+                    __syncthreads();
+                    if (tid < 256) {
+                        uint32_t sum = 0;
+#pragma unroll
+                        for (int w = 0; w < TOPK_HIST; ++w) sum += hist[w * 256 + tid];
+                        hist[tid] = sum;
+                    }
+                    __syncthreads();
+                    if (wave == 0) topk_find_bin(hist, need, lane, &s_bin, &s_need);
+                    __syncthreads();
+                    prefix |= static_cast<C>(s_bin) << shift;
+                    pmask |= static_cast<C>(0xffu) << shift;
+                    need = s_need;
+                }
+                // the T composites >= the T-th largest
+                if (tid == 0) s_count = 0;
+                __syncthreads();
+                for (uint32_t i = tid; i < cnt; i += TOPK_THREADS) {
+                    const C c = list[i];
+                    if (c >= prefix) {
+                        const uint32_t slot = atomicAdd(&s_count, 1u);
+                        if (slot < static_cast<uint32_t>(a.n2)) sel_f[slot] = c;
+                    }
+                }
+                for (int i = a.T + tid; i < a.n2; i += TOPK_THREADS) sel_f[i] = 0;   // real composites are > 0
+                __syncthreads();
+                topk_sort_out(sel_f, a.T, a.n2, a.T <= TOPK_RANK_LIMIT, orow);
+                return;
+            }
         }
     }
-    for (int i = tid; i < T; i += TOPK_THREADS) orow[i] = Comp<C>::index(sel[i]);
+    // exact path: recompute the row's uncertain keys in place
+    __syncthreads();                               // (s_q written)
+    for (int64_t wi = tid; wi < a.UW; wi += TOPK_THREADS) {
+        uint32_t bits = ur[wi];
+        while (bits) {
+            const int j = __ffs(static_cast<int>(bits)) - 1;
+            bits &= bits - 1;
+            const int64_t p = wi * 32 + j;
+            if (p < a.P) kr[p] = static_cast<uint16_t>(exact_key_row(kbase + p * a.ks_n, q, a.f16 != 0));
+        }
+    }
+    __syncthreads();                               // the keys written above are visible to the workgroup
+    C* sel = a.gsort ? static_cast<C*>(a.gsel) + static_cast<int64_t>(row) * a.n2 : list;
+    topk_exact_row(kr, static_cast<const uint16_t*>(nullptr), a.P, a.T, a.n2,
+                   !a.gsort && a.T <= TOPK_RANK_LIMIT, sel, hist, orow);
 }
 
 // Launch plan of topk_kernel for rows of P keys and T winners
 struct TopkPlan {
-    int n2, cached, wide, gsort;
+    int n2, wide, gsort, fast, cap;
     size_t lds;
     size_t gbytes;               // global sort buffer bytes per row (gsort)
 };
@@ -615,13 +1290,22 @@ TopkPlan topk_plan(int64_t P, int T, size_t lds_budget) {
         t.n2 = 1;
         while (t.n2 < T) t.n2 <<= 1;
     }
+    const size_t budget = std::min<size_t>(lds_budget, TOPK_LDS_MAX);
     const size_t hist = static_cast<size_t>(TOPK_HIST) * 256 * 4;
     const size_t sel = static_cast<size_t>(t.n2) * cs;
-    t.gsort = hist + sel > lds_budget;
-    const size_t fixed = hist + (t.gsort ? 0 : sel);
-    const size_t with_keys = fixed + (static_cast<size_t>(P) * 2 + 15) / 16 * 16;
-    t.cached = with_keys <= TOPK_LDS_MAX;
-    t.lds = t.cached ? with_keys : fixed;
+    t.gsort = hist + sel > budget;
+    // candidate path: list (cap composites) + sel + uncertain flags (cap
+    // bytes) + the counting rank's buckets and cap composites
+    const size_t buckets = static_cast<size_t>(2 * TOPK_SPAN) * 4;
+    if (hist + sel + buckets + 16 < budget) {
+        const int64_t room = static_cast<int64_t>((budget - hist - sel - buckets - 16) / (2 * cs + 1)) / 16 * 16;
+        const int64_t want = std::min<int64_t>(std::max<int64_t>(2 * static_cast<int64_t>(T), 4096), (P + 7) / 8 * 8);
+        t.cap = static_cast<int>(std::min<int64_t>({want, room, 65536}));
+        t.fast = t.cap >= T;
+    }
+    t.lds = hist + (t.fast ? static_cast<size_t>(t.cap) * (2 * cs + 1) + 16 + buckets + sel
+                           : (t.gsort ? 0 : sel));
+    t.lds = (t.lds + 15) / 16 * 16;
     t.gbytes = t.gsort ? (sel + 255) / 256 * 256 : 0;
     return t;
 }
@@ -828,16 +1512,22 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
 
 int padded_heads(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16; }
 
-// workspace: [query means][16-bit keys per row][global sort buffers (large top-k only)]
+// workspace: [query means, float64][query means, bf16 bits][keys per row]
+// [uncertain bitmaps][certified-key histograms][global sort buffers (large top-k only)]
 struct SelectLayout {
-    size_t qm, keys, gsel, total;
+    size_t qm, qb, keys, unc, hist, gsel, total;
 };
 SelectLayout select_layout(int B, int H_out, int64_t P, int T, const TopkPlan& tp) {
+    auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+    const size_t rows = static_cast<size_t>(B) * H_out;
     SelectLayout L;
     L.qm = 0;
-    L.keys = ((static_cast<size_t>(B) * H_out * 128 * sizeof(double) * 4 + 255) / 256) * 256;   // room for head padding
-    L.gsel = L.keys + (static_cast<size_t>(B) * H_out * key_pitch(P) * 2 + 255) / 256 * 256;
-    L.total = L.gsel + (tp.gsort ? static_cast<size_t>(B) * H_out * tp.gbytes : 0);
+    L.qb = up(rows * 128 * sizeof(double) * 4);    // room for head padding
+    L.keys = L.qb + up(rows * 128 * 2 * 4);
+    L.unc = L.keys + up(rows * key_pitch(P) * 2);
+    L.hist = L.unc + up(rows * unc_words(P) * 4);
+    L.gsel = L.hist + up(rows * 256 * 4);
+    L.total = L.gsel + (tp.gsort ? rows * tp.gbytes : 0);
     (void)T;
     return L;
 }
@@ -879,58 +1569,63 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
     if (!workspace || ws_bytes < L.total || !aligned(workspace, 16))
         return fail(HYQ_ENOSPC, "hyq_vertical_select: workspace too small or not 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    double* qm = static_cast<double*>(workspace);
-    uint16_t* keys = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + L.keys);
-    void* gsel = static_cast<char*>(workspace) + L.gsel;
+    char* ws = static_cast<char*>(workspace);
+    double* qm = reinterpret_cast<double*>(ws + L.qm);
+    uint16_t* qb = reinterpret_cast<uint16_t*>(ws + L.qb);
+    uint16_t* keys = reinterpret_cast<uint16_t*>(ws + L.keys);
+    uint32_t* unc = reinterpret_cast<uint32_t*>(ws + L.unc);
+    uint32_t* hist = reinterpret_cast<uint32_t*>(ws + L.hist);
+    void* gsel = ws + L.gsel;
     const int GP = padded_heads(G);
     if (aligned(q, 16) && qs_t % 8 == 0 && qs_h % 8 == 0 && qs_b % 8 == 0) {
         if (group == 1)
             qmean16_kernel<256><<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(256), 0, s>>>(
-                q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm);
+                q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm, qb, hist);
         else
             qmean16_kernel<1024><<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(1024), 0, s>>>(
-                q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm);
+                q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm, qb, hist);
     } else
         qmean_kernel<<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(QM_THREADS), 0, s>>>(
-            q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm);
+            q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm, qb, hist);
     int rc = check_launch("hyq_vertical_select (mean)");
     if (rc) return rc;
-    const dim3 sgrid(static_cast<unsigned>((p + SC_WG_ROWS - 1) / SC_WG_ROWS), static_cast<unsigned>(b * hk));
-    auto score = [&](auto gm, auto f16) {
-        score_kernel<decltype(gm)::value, decltype(f16)::value><<<sgrid, dim3(256), 0, s>>>(
-            k, ks_b, ks_h, ks_n, hk, G, p, key_pitch(p), qm, keys);
+    const int64_t KP = key_pitch(p);
+    // bf16 models: scores on the matrix cores with certified keys; fp16
+    // models: float64 scores (exact keys)
+    auto score_f64 = [&](auto gm) {
+        const dim3 grid(static_cast<unsigned>((p + SC_WG_ROWS - 1) / SC_WG_ROWS), static_cast<unsigned>(b * hk));
+        score_kernel<decltype(gm)::value, true><<<grid, dim3(256), 0, s>>>(
+            k, ks_b, ks_h, ks_n, hk, G, p, KP, qm, keys, unc, hist);
     };
-    auto score_gm = [&](auto f16) {
+    auto score_mfma = [&](auto gm) {
+        const dim3 grid(static_cast<unsigned>((p + SM_WG_ROWS - 1) / SM_WG_ROWS), static_cast<unsigned>(b * hk));
+        score_mfma_kernel<decltype(gm)::value><<<grid, dim3(256), 0, s>>>(
+            k, ks_b, ks_h, ks_n, hk, G, p, KP, qm, qb, keys, unc, hist);
+    };
+    auto score_gm = [&](auto fn) {
         switch (GP) {
-            case 1: score(std::integral_constant<int, 1>{}, f16); break;
-            case 2: score(std::integral_constant<int, 2>{}, f16); break;
-            case 4: score(std::integral_constant<int, 4>{}, f16); break;
-            case 8: score(std::integral_constant<int, 8>{}, f16); break;
-            default: score(std::integral_constant<int, 16>{}, f16); break;
+            case 1: fn(std::integral_constant<int, 1>{}); break;
+            case 2: fn(std::integral_constant<int, 2>{}); break;
+            case 4: fn(std::integral_constant<int, 4>{}); break;
+            case 8: fn(std::integral_constant<int, 8>{}); break;
+            default: fn(std::integral_constant<int, 16>{}); break;
         }
     };
-    if (is_fp16) score_gm(std::true_type{});
-    else score_gm(std::false_type{});
+    if (is_fp16) score_gm(score_f64);
+    else score_gm(score_mfma);
     rc = check_launch("hyq_vertical_select (score)");
     if (rc) return rc;
+    TopkArgs ta{keys, unc, hist, p, KP, unc_words(p), top_k, tp.n2, tp.cap, tp.fast, tp.gsort, gsel,
+                k, ks_b, ks_h, ks_n, hk, G, GP, is_fp16, qm, out_idx};
     const dim3 tgrid(static_cast<unsigned>(b * h_out)), tblock(TOPK_THREADS);
     if (tp.lds > 64 * 1024) {
-        const void* fn = tp.wide ? (tp.gsort ? reinterpret_cast<const void*>(&topk_kernel<uint64_t, true>)
-                                             : reinterpret_cast<const void*>(&topk_kernel<uint64_t, false>))
-                                 : (tp.gsort ? reinterpret_cast<const void*>(&topk_kernel<uint32_t, true>)
-                                             : reinterpret_cast<const void*>(&topk_kernel<uint32_t, false>));
+        const void* fn = tp.wide ? reinterpret_cast<const void*>(&topk_kernel<uint64_t>)
+                                 : reinterpret_cast<const void*>(&topk_kernel<uint32_t>);
         if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(tp.lds)) != hipSuccess)
             return fail(HYQ_EDEVICE, "hyq_vertical_select: cannot raise the LDS limit of the top-k kernel");
     }
-    if (tp.wide) {
-        uint64_t* g = static_cast<uint64_t*>(gsel);
-        if (tp.gsort) topk_kernel<uint64_t, true><<<tgrid, tblock, tp.lds, s>>>(keys, p, top_k, tp.n2, tp.cached, g, out_idx);
-        else topk_kernel<uint64_t, false><<<tgrid, tblock, tp.lds, s>>>(keys, p, top_k, tp.n2, tp.cached, g, out_idx);
-    } else {
-        uint32_t* g = static_cast<uint32_t*>(gsel);
-        if (tp.gsort) topk_kernel<uint32_t, true><<<tgrid, tblock, tp.lds, s>>>(keys, p, top_k, tp.n2, tp.cached, g, out_idx);
-        else topk_kernel<uint32_t, false><<<tgrid, tblock, tp.lds, s>>>(keys, p, top_k, tp.n2, tp.cached, g, out_idx);
-    }
+    if (tp.wide) topk_kernel<uint64_t><<<tgrid, tblock, tp.lds, s>>>(ta);
+    else topk_kernel<uint32_t><<<tgrid, tblock, tp.lds, s>>>(ta);
     return check_launch("hyq_vertical_select (topk)");
 }
 

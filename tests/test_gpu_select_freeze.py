@@ -84,6 +84,49 @@ def test_selector_ties_and_negative_zero():
     assert list(first) == sorted(first)
 
 
+@pytest.mark.parametrize("case", ["large_query_mean", "small_query_mean", "overflowing_rows",
+                                  "wide_key_spread", "top_k_above_certified", "wide_spread_many_winners"])
+def test_selector_certification_paths(case):
+    """bf16 models score on the matrix cores with a certified error bound and
+    recompute uncertain keys that can be selected.  Inputs that take the
+    other paths, each bit-exact against the oracle (prefill-time call with
+    GQA 4, and the freeze-time group-mean call):
+      large / small query mean: a key head whose mean has entries above 2^60
+        or nonzero ones below 2^-60 is scored in float64;
+      overflowing rows: key rows of magnitude 2^100 leave the bound's range
+        (largest key stored, recomputed when a candidate);
+      wide key spread: rows scaled by 2^-30 .. 2^30, so the winners' keys span
+        more than the counting rank covers (radix select and sort);
+      top_k above certified: rho = 0.97, more winners than certified keys
+        (every uncertain key recomputed, then the exact selection);
+      wide spread, many winners: both of the last two."""
+    from hyquant_amd.vertical import compute_vertical_indices, freeze_vertical_indices
+    print(f"certification path {case}", flush=True)
+    rng = np.random.default_rng(sum(map(ord, case)))
+    B, HQ, HK, QL, W = 1, 8, 2, 64, 64
+    KL = 4096 + W
+    rho = 0.97 if case in ("top_k_above_certified", "wide_spread_many_winners") else 0.05
+    q = rng.standard_normal((B, HQ, QL, 128)).astype(np.float32)
+    k = (rng.standard_normal((B, HK, KL, 128)) + 1.5 * rng.standard_normal((1, HK, 1, 128))).astype(np.float32)
+    if case == "large_query_mean":
+        q[0, 1] *= 2.0 ** 70
+    elif case == "small_query_mean":
+        q[0, 5] *= 2.0 ** -70
+    elif case == "overflowing_rows":
+        k[0, 0, rng.choice(KL - W, 40, replace=False)] *= 2.0 ** 100
+    elif case in ("wide_key_spread", "wide_spread_many_winners"):
+        k *= 2.0 ** rng.integers(-30, 31, size=(B, HK, KL, 1))
+    q, k = O.bf16_round(q), O.bf16_round(k)
+    qd, kd = to_dev_bf16(q, "cuda"), to_dev_bf16(k, "cuda")
+    got = compute_vertical_indices(qd, kd, W, rho, kv_repeat=HQ // HK)
+    exp = O.compute_vertical_indices(q, k, W, rho, kv_repeat=HQ // HK)
+    assert np.array_equal(got.cpu().numpy(), exp)
+    P = KL - W
+    got_f = freeze_vertical_indices(qd[:, :, -W:], kd[:, :, :P], W, rho, HQ // HK)
+    exp_f = O.compute_vertical_indices(O.group_mean_query(q[:, :, -W:], HK), k[:, :, :P], W, rho)
+    assert np.array_equal(got_f.cpu().numpy(), exp_f)
+
+
 @pytest.mark.parametrize("cfg", [dict(B=1, HQ=32, HKV=8, N=1024), dict(B=2, HQ=32, HKV=8, N=8192),
                                  dict(B=2, HQ=64, HKV=8, N=4096), dict(B=1, HQ=32, HKV=2, N=16384)])
 def test_selector_freeze_variant_and_prefill_on_config_inputs(cfg):

@@ -17,15 +17,24 @@
 // Kernels:
 //   qmean16_kernel    one workgroup per (b, ho): 16-byte row chunks x tail slots
 //                     (qmean_kernel, channel pairs x tail slices, for query
-//                     rows that are not 16-byte aligned).
-//   score_kernel      one thread per key row, G output heads sharing the row
-//                     (GQA-native, the K prefix is read once); writes the
-//                     monotone 16-bit key of each bf16 score.
-//   topk_kernel       one workgroup per (b, ho) row: 2-pass radix select of
-//                     the threshold key, ties at the threshold taken in index
-//                     order, winners placed by their rank under the unique
-//                     composite (key << 16) | (0xffff - idx) ("score desc,
-//                     index asc" is "composite desc").
+//                     rows that are not 16-byte aligned); writes the means in
+//                     float64 and as model-dtype bits, and zeroes the row's
+//                     certified-key histogram.
+//   score_mfma_kernel bf16 models: the scores on the matrix cores with a
+//                     worst-case bound of their error; a key is stored exact
+//                     where the bound certifies it, else as an upper bound
+//                     with the position flagged uncertain; certified keys are
+//                     counted per output row (HIST_BINS bins of the key).
+//   score_kernel      fp16 models: one thread per key row in float64, G output
+//                     heads sharing the row (exact keys, the same outputs).
+//   topk_kernel       one workgroup per (b, ho) row: a candidate list of the
+//                     positions whose stored key reaches the T-th largest
+//                     certified key, float64 keys for its uncertain entries,
+//                     then a counting rank (or a radix select and sort); the
+//                     exact two-pass radix selection over the whole row when
+//                     the list does not apply.  Output order "score desc,
+//                     index asc" ("composite desc" for the unique composite
+//                     (key << IDX_BITS) | (IDX_MASK - idx)).
 //   mark_kernel / compact_quant_kernel / gather_rows_kernel  the freeze: a
 //                     bitmap of selected prefix positions, quantisation of the
 //                     unselected prefix rows straight into their compact slots
@@ -40,10 +49,30 @@
 namespace hyq {
 namespace {
 
-constexpr int TOPK_THREADS = 512;
+constexpr int TOPK_THREADS = 512;            // threads of a top-k workgroup (at most; 256 when rows are many)
 constexpr int64_t TOPK_NARROW_P = 65536;   // rows up to this long use 32-bit composites (16-bit index)
 constexpr int64_t TOPK_MAX_P = 0x7fffffff; // 64-bit composites carry a 32-bit index
 constexpr int TOPK_MAX_T = 1 << 30;         // the sort's power-of-two size n2 stays an int
+
+// Certified keys per output row are counted in HIST_BINS bins of key >> HIST_SHIFT
+// (half a bf16 binade each).  Inside a score workgroup the counts are 16-bit
+// halves of LDS words (a workgroup counts at most 1024 rows per head).
+constexpr int HIST_BINS = 1024;
+constexpr int HIST_SHIFT = 6;
+__device__ __forceinline__ void hist_add16(uint32_t* h, uint32_t key) {
+    const uint32_t bin = key >> HIST_SHIFT;
+    atomicAdd(&h[bin >> 1], 1u << (16 * (bin & 1)));
+}
+// adds a workgroup's packed counts of heads g < G to the rows' histograms
+__device__ __forceinline__ void hist_flush16(const uint32_t* h, int G, uint32_t* __restrict__ hist, int64_t row0) {
+    for (int i = threadIdx.x; i < G * (HIST_BINS / 2); i += blockDim.x) {
+        const uint32_t c = h[i];
+        if (!c) continue;
+        uint32_t* r = hist + (row0 + i / (HIST_BINS / 2)) * HIST_BINS + 2 * (i % (HIST_BINS / 2));
+        if (c & 0xffffu) atomicAdd(r, c & 0xffffu);
+        if (c >> 16) atomicAdd(r + 1, c >> 16);
+    }
+}
 
 
 __device__ __forceinline__ double bf16_bits_to_f64(uint16_t b) { return static_cast<double>(bf16_to_f32(b)); }
@@ -89,7 +118,7 @@ __global__ __launch_bounds__(QM_THREADS) void qmean_kernel(const uint16_t* __res
         outb[threadIdx.x & 127] = 0;
         return;
     }
-    if (threadIdx.x < 256) hist[(static_cast<int64_t>(bhk) * G + g) * 256 + threadIdx.x] = 0;
+    if (threadIdx.x < HIST_BINS) hist[(static_cast<int64_t>(bhk) * G + g) * HIST_BINS + threadIdx.x] = 0;
     const int b = bhk / HK, ho = (bhk % HK) * G + g;
     const uint32_t* base = reinterpret_cast<const uint32_t*>(
         q + b * qs_b + static_cast<int64_t>(ho * R) * qs_h + static_cast<int64_t>(QL - tail) * qs_t) + lane;
@@ -188,7 +217,7 @@ __global__ __launch_bounds__(THREADS) void qmean16_kernel(const uint16_t* __rest
         }
         return;
     }
-    if (tid < 256) hist[(static_cast<int64_t>(bhk) * G + g) * 256 + tid] = 0;
+    for (int i = tid; i < HIST_BINS; i += THREADS) hist[(static_cast<int64_t>(bhk) * G + g) * HIST_BINS + i] = 0;
     constexpr int QV_SLOTS = THREADS / 16;
     const int b = bhk / HK, ho = (bhk % HK) * G + g;
     const int sub = tid & 15, slot = tid >> 4;
@@ -284,8 +313,8 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
                                                     const double* __restrict__ qm, uint16_t* __restrict__ keys,
                                                     uint32_t* __restrict__ unc, uint32_t* __restrict__ hist) {
     __shared__ __align__(16) uint8_t s_rows[4][SC_ROWS * SC_PITCH];
-    __shared__ uint32_t s_hist[GM][256];           // certified (here: all) keys by high byte
-    for (int i = threadIdx.x; i < GM * 256; i += 256) (&s_hist[0][0])[i] = 0;
+    __shared__ uint32_t s_hist[GM][HIST_BINS / 2];  // certified (here: all) keys, packed 16-bit counts
+    for (int i = threadIdx.x; i < GM * (HIST_BINS / 2); i += 256) (&s_hist[0][0])[i] = 0;
     __syncthreads();
     const int bh = blockIdx.y;                     // b * HK + hk
     const int b = bh / HK, hk = bh % HK;
@@ -364,7 +393,7 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
                     if (g < G) {
                         const uint32_t key = orderable_key(f64_to_half_rne(acc[g], F16));
                         keys[(static_cast<int64_t>(bh) * G + g) * KP + p] = static_cast<uint16_t>(key);
-                        atomicAdd(&s_hist[g][key >> 8], 1u);
+                        hist_add16(s_hist[g], key);
                     }
             }
             // every key here is exact: the block's uncertain words are zero
@@ -390,10 +419,7 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last (empty) loads retire before the wave ends
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < G * 256; i += 256) {
-        const uint32_t c = (&s_hist[0][0])[i];
-        if (c) atomicAdd(hist + (static_cast<int64_t>(bh) * G + i / 256) * 256 + (i & 255), c);
-    }
+    hist_flush16(&s_hist[0][0], G, hist, static_cast<int64_t>(bh) * G);
 }
 
 // ---------------------------------------------------------------------------
@@ -428,7 +454,7 @@ __global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__
 // mean has a NaN, an infinity or a nonzero |qm_d| outside [2^-60, 2^60], the
 // pass computes that key head's scores in float64 instead (exact keys).
 //
-// The pass also counts each output row's certified keys by their high byte
+// The pass also counts each output row's certified keys in HIST_BINS bins
 // (hist, zeroed by the query-mean kernel); the top-k starts from that count.
 //
 // One workgroup per SM_WG_ROWS rows of one (b, hk); wavefront w takes the
@@ -478,7 +504,7 @@ __global__ __launch_bounds__(256) void score_mfma_kernel(const uint16_t* __restr
     constexpr int SPK = TPK >= 2 ? TPK / 2 : 1;    // stages per packed group
     constexpr int SGRP = SPK >= 2 ? SPK : 2;       // stages per loop pass (two register stages)
     __shared__ __align__(16) uint8_t s_rows[4][SM_ROWS * SM_PITCH];
-    __shared__ uint32_t s_hist[GM][256];
+    __shared__ uint32_t s_hist[GM][HIST_BINS / 2];  // certified keys, packed 16-bit counts
     const int bh = blockIdx.y;                     // b * HK + hk
     const int b = bh / HK, hk = bh % HK;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -508,7 +534,7 @@ __global__ __launch_bounds__(256) void score_mfma_kernel(const uint16_t* __restr
         }
     }
     const bool exact = __ballot(bad && h < G) != 0;   // the same in every workgroup of bh
-    for (int i = threadIdx.x; i < GM * 256; i += 256) (&s_hist[0][0])[i] = 0;
+    for (int i = threadIdx.x; i < GM * (HIST_BINS / 2); i += 256) (&s_hist[0][0])[i] = 0;
     __syncthreads();
     uint8_t* lds = s_rows[wave];
     const int sub = lane & 15, rq = lane >> 4;
@@ -578,7 +604,7 @@ __global__ __launch_bounds__(256) void score_mfma_kernel(const uint16_t* __restr
             const bool cert = fin && blo == bhi;
             const uint32_t key = orderable_key(static_cast<uint16_t>(bhi));
             kv[v] = fin ? key : 0xffffu;
-            if (cert && rt + v < nrows && h < G) atomicAdd(&s_hist[h][key >> 8], 1u);
+            if (cert && rt + v < nrows && h < G) hist_add16(s_hist[h], key);
             nib |= (cert ? 0u : 1u) << v;
         }
         if (h < G && rt < nrows) {
@@ -609,7 +635,7 @@ __global__ __launch_bounds__(256) void score_mfma_kernel(const uint16_t* __restr
             for (int g = 0; g < G; ++g) {
                 const uint32_t key = exact_key_lds(lds + lane * SM_PITCH, qm + (static_cast<int64_t>(bh) * GM + g) * 128);
                 keys[(static_cast<int64_t>(bh) * G + g) * KP + r0 + rbase + lane] = static_cast<uint16_t>(key);
-                atomicAdd(&s_hist[g][key >> 8], 1u);
+                hist_add16(s_hist[g], key);
             }
         }
         if (lane < G) unc[(static_cast<int64_t>(bh) * G + lane) * UW + r0 / 32 + blk] = 0u;
@@ -660,16 +686,16 @@ __global__ __launch_bounds__(256) void score_mfma_kernel(const uint16_t* __restr
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last (empty) loads retire before the wave ends
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < G * 256; i += 256) {
-        const uint32_t c = (&s_hist[0][0])[i];
-        if (c) atomicAdd(hist + (static_cast<int64_t>(bh) * G + i / 256) * 256 + (i & 255), c);
-    }
+    hist_flush16(&s_hist[0][0], G, hist, static_cast<int64_t>(bh) * G);
 }
 
 constexpr int TOPK_WAVES = TOPK_THREADS / 64;
 // histogram copies: one per pair of wavefronts, which keeps a 16K-key row's
 // LDS (keys, histograms, winners) under 40 KiB, four workgroups per CU
 constexpr int TOPK_HIST = TOPK_WAVES / 2;
+// the LDS histogram area: the copies above, or the certified-key histogram
+constexpr int TOPK_HIST_AREA = TOPK_HIST * 256 > HIST_BINS ? TOPK_HIST * 256 : HIST_BINS;
+static_assert(TOPK_HIST_AREA == HIST_BINS, "both block sizes share one LDS layout");
 constexpr int TOPK_RANK_MAX = 2048;        // winners the rank path's per-thread arrays can hold
 // rows with up to this many winners are placed by rank (each winner compared
 // with every other: T / 4 LDS steps per thread); larger rows are bitonic
@@ -677,19 +703,21 @@ constexpr int TOPK_RANK_MAX = 2048;        // winners the rank path's per-thread
 // less vector work from about 512 winners up
 constexpr int TOPK_RANK_LIMIT = 512;
 // key offsets above the candidate bound that the counting rank covers
-constexpr int TOPK_SPAN = 2048;
+constexpr int TOPK_SPAN = 1024;
 constexpr size_t TOPK_LDS_MAX = 64 * 1024; // keys are cached in LDS while the row fits this budget
 
-// Wavefront 0: the bin holding the need-th largest entry of a 256-bin
+// Wavefront 0: the bin holding the need-th largest entry of an NBINS-bin
 // histogram, scanning from the top.  Writes the bin and the entries still
 // needed inside it.
-__device__ __forceinline__ void topk_find_bin(const uint32_t* hist, uint32_t need, int lane, uint32_t* s_bin,
-                                              uint32_t* s_need) {
-    uint32_t c[4];
+template <int NBINS>
+__device__ __forceinline__ void topk_find_bin_n(const uint32_t* hist, uint32_t need, int lane, uint32_t* s_bin,
+                                                uint32_t* s_need) {
+    constexpr int PER = NBINS / 64;               // bins per lane, from the top
+    uint32_t c[PER];
     uint32_t mine = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        c[j] = hist[255 - (4 * lane + j)];
+    for (int j = 0; j < PER; ++j) {
+        c[j] = hist[NBINS - 1 - (PER * lane + j)];
         mine += c[j];
     }
     uint32_t incl = mine;                          // inclusive prefix over lanes (bins from the top)
@@ -702,9 +730,9 @@ __device__ __forceinline__ void topk_find_bin(const uint32_t* hist, uint32_t nee
     int found = -1;
     uint32_t before = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < PER; ++j) {
         if (found < 0 && acc + c[j] >= need) {
-            found = 255 - (4 * lane + j);
+            found = NBINS - 1 - (PER * lane + j);
             before = acc;
         }
         acc += c[j];
@@ -717,11 +745,15 @@ __device__ __forceinline__ void topk_find_bin(const uint32_t* hist, uint32_t nee
     if (lane == first) {
         if (found < 0) {
             found = 0;
-            before = acc - c[3];
+            before = acc - c[PER - 1];
         }
         *s_bin = static_cast<uint32_t>(found);
         *s_need = need - before;
     }
+}
+__device__ __forceinline__ void topk_find_bin(const uint32_t* hist, uint32_t need, int lane, uint32_t* s_bin,
+                                              uint32_t* s_need) {
+    topk_find_bin_n<256>(hist, need, lane, s_bin, s_need);
 }
 
 // The composite of one entry: (key << IDX_BITS) | (IDX_MASK - idx), unique,
@@ -753,19 +785,19 @@ __device__ __forceinline__ void load4(const uint64_t* s, int j, uint64_t (&w)[4]
 // and sel in LDS; a thread ranks its up to four winners in one sweep, every
 // lane of a wavefront reading the same four composites per step), or after
 // a bitonic sort of the n2 entries.  Ends with the workgroup's threads done.
-template <typename C>
+template <typename C, int NT>
 __device__ void topk_sort_out(C* sel, int T, int n2, bool rank_ok, int64_t* __restrict__ orow) {
     const int tid = threadIdx.x;
     if (rank_ok) {
-        constexpr int E = TOPK_RANK_MAX / TOPK_THREADS;
+        constexpr int E = TOPK_RANK_MAX / NT;
         C v[E];
         uint32_t rank[E];
 #pragma unroll
         for (int u = 0; u < E; ++u) {
-            v[u] = tid + u * TOPK_THREADS < T ? sel[tid + u * TOPK_THREADS] : C(0);
+            v[u] = tid + u * NT < T ? sel[tid + u * NT] : C(0);
             rank[u] = 0;
         }
-        const int ne = (T - tid + TOPK_THREADS - 1) / TOPK_THREADS;   // winners of this thread
+        const int ne = (T - tid + NT - 1) / NT;   // winners of this thread
         if (ne > 2) {
             for (int j = 0; j < n2 / 4; ++j) {
                 C w[4];
@@ -786,7 +818,7 @@ __device__ void topk_sort_out(C* sel, int T, int n2, bool rank_ok, int64_t* __re
             if (u < ne) orow[rank[u]] = Comp<C>::index(v[u]);
         return;
     }
-    if (n2 == 2 * TOPK_THREADS) {
+    if (n2 == 2 * NT) {
         // 1024 entries in registers, two per thread: entry 128 w + 64 r + l
         // sits in register r of lane l of wavefront w.  Compare-exchanges
         // with partners in the same wavefront use the other register
@@ -840,7 +872,7 @@ __device__ void topk_sort_out(C* sel, int T, int n2, bool rank_ok, int64_t* __re
     // bitonic sort, descending
     for (int size = 2; size <= n2; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < n2 / 2; i += TOPK_THREADS) {
+            for (int i = tid; i < n2 / 2; i += NT) {
                 const int lo = 2 * i - (i & (stride - 1));
                 const int hi = lo + stride;
                 const bool desc = ((lo & size) == 0);
@@ -853,7 +885,7 @@ __device__ void topk_sort_out(C* sel, int T, int n2, bool rank_ok, int64_t* __re
             __syncthreads();
         }
     }
-    for (int i = tid; i < T; i += TOPK_THREADS) orow[i] = Comp<C>::index(sel[i]);
+    for (int i = tid; i < T; i += NT) orow[i] = Comp<C>::index(sel[i]);
 }
 
 // The top T of one row of exact 16-bit keys kr (global; s_keys: a copy in
@@ -863,20 +895,20 @@ __device__ void topk_sort_out(C* sel, int T, int n2, bool rank_ok, int64_t* __re
 // per-thread index ranges); the T winners' composites are collected in sel
 // (n2 entries, LDS or this row's slice of a global buffer) and placed by
 // topk_sort_out.
-template <typename C>
+template <typename C, int NT>
 __device__ void topk_exact_row(const uint16_t* __restrict__ kr, const uint16_t* s_keys, int64_t P, int T, int n2,
                                bool rank_ok, C* sel, uint32_t* hist, int64_t* __restrict__ orow) {
     __shared__ uint32_t s_bin, s_need, s_count;
-    __shared__ uint32_t s_wsum[TOPK_WAVES];
+    __shared__ uint32_t s_wsum[(NT / 64)];
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     auto key_at = [&](int64_t i) -> uint32_t { return s_keys ? s_keys[i] : kr[i]; };
     uint32_t need = static_cast<uint32_t>(T);
     uint32_t khi = 0;
     for (int pass = 0; pass < 2; ++pass) {
-        for (int i = tid; i < TOPK_HIST * 256; i += TOPK_THREADS) hist[i] = 0;
+        for (int i = tid; i < (NT / 128) * 256; i += NT) hist[i] = 0;
         __syncthreads();
-        for (int64_t i = tid; i < P; i += TOPK_THREADS) {
+        for (int64_t i = tid; i < P; i += NT) {
             const uint32_t key = key_at(i);
             if (pass == 0) atomicAdd(&hist[(wave >> 1) * 256 + (key >> 8)], 1u);
             else if ((key >> 8) == khi) atomicAdd(&hist[(wave >> 1) * 256 + (key & 0xffu)], 1u);
@@ -885,7 +917,7 @@ __device__ void topk_exact_row(const uint16_t* __restrict__ kr, const uint16_t* 
         if (tid < 256) {
             uint32_t sum = 0;
 #pragma unroll
-            for (int w = 0; w < TOPK_HIST; ++w) sum += hist[w * 256 + tid];
+            for (int w = 0; w < (NT / 128); ++w) sum += hist[w * 256 + tid];
             hist[tid] = sum;
         }
         __syncthreads();
@@ -899,7 +931,7 @@ __device__ void topk_exact_row(const uint16_t* __restrict__ kr, const uint16_t* 
     // thread t scans indices [t*C, t*C + C) (C a multiple of 8, read 16 bytes
     // at a time): entries above kth are winners; the entries equal to kth are
     // numbered in index order by a prefix count over the threads
-    const int64_t CH = (P + 8 * TOPK_THREADS - 1) / (8 * TOPK_THREADS) * 8;
+    const int64_t CH = (P + 8 * NT - 1) / (8 * NT) * 8;
     const int64_t i0 = static_cast<int64_t>(tid) * CH;
     const uint4* k4 = s_keys ? reinterpret_cast<const uint4*>(s_keys) : reinterpret_cast<const uint4*>(kr);
     if (tid == 0) s_count = 0;
@@ -932,9 +964,9 @@ __device__ void topk_exact_row(const uint16_t* __restrict__ kr, const uint16_t* 
             if (take) sel[atomicAdd(&s_count, 1u)] = Comp<C>::make(key, i);
         }
     }
-    for (int i = T + tid; i < n2; i += TOPK_THREADS) sel[i] = 0;   // real composites are > 0
+    for (int i = T + tid; i < n2; i += NT) sel[i] = 0;   // real composites are > 0
     __syncthreads();
-    topk_sort_out(sel, T, n2, rank_ok, orow);
+    topk_sort_out<C, NT>(sel, T, n2, rank_ok, orow);
 }
 
 // The exact key (float64, d order, one rounding to the model dtype: the
@@ -967,7 +999,7 @@ __device__ __forceinline__ uint32_t exact_key_row(const uint16_t* __restrict__ k
 struct TopkArgs {
     uint16_t* keys;                  // [rows][KP] keys (exact, or upper bounds where uncertain)
     const uint32_t* unc;             // [rows][UW] uncertain bits
-    const uint32_t* hist;            // [rows][256] certified keys by high byte
+    const uint32_t* hist;            // [rows][HIST_BINS] certified keys by key >> HIST_SHIFT
     int64_t P, KP, UW;
     int T, n2, cap;                  // winners, sort size, candidate list capacity
     int fast;                        // the candidate path fits the LDS (else every row takes the exact path)
@@ -981,10 +1013,11 @@ struct TopkArgs {
 };
 
 // One workgroup per (b, ho) row.
-// Candidate path: the certified histogram gives the high byte b of the T-th
-// largest certified key.  One pass over the row lists every position whose
-// stored key (exact, or an upper bound) is >= b << 8 and counts the certified
-// keys of bin b by low byte, which gives L, the T-th largest certified key.
+// Candidate path: the certified histogram (bins of key >> HIST_SHIFT) gives
+// the bin b of the T-th largest certified key.  One pass over the row lists
+// every position whose stored key (exact, or an upper bound) is >= the bin's
+// first key and counts the certified keys of bin b by their low bits, which
+// gives L, the T-th largest certified key.
 // The certified keys are exact and at least T of them are >= L, so the T-th
 // largest exact key K is >= L, and the list holds every position whose exact
 // key is >= L: the row's top T (were the list over its capacity, a second
@@ -998,17 +1031,18 @@ struct TopkArgs {
 // topk_exact_row runs on the exact keys.
 // Dynamic LDS: [hist][list (cap C)][sel (n2 C)][uncertain flags (cap bytes)];
 // the exact path uses [hist][sel] (gsort: the global buffer).
-template <typename C>
-__global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
+template <typename C, int NT>
+__global__ __launch_bounds__(NT) void topk_kernel(TopkArgs a) {
     extern __shared__ __align__(16) uint32_t tk_lds[];
-    uint32_t* hist = tk_lds;                       // [TOPK_HIST][256]
-    C* list = reinterpret_cast<C*>(tk_lds + TOPK_HIST * 256);
+    uint32_t* hist = tk_lds;                       // [TOPK_HIST_AREA]
+    C* list = reinterpret_cast<C*>(tk_lds + TOPK_HIST_AREA);
     C* sel_f = list + a.cap;
     uint8_t* flags = reinterpret_cast<uint8_t*>(sel_f + a.n2);   // uncertain entries of the list
     uint32_t* brk = reinterpret_cast<uint32_t*>(flags + (a.cap + 15) / 16 * 16);   // buckets: counts, starts
     C* brank_tmp = reinterpret_cast<C*>(brk + 2 * TOPK_SPAN);      // entries >= L in bucket order
     __shared__ uint32_t s_bin, s_need, s_count, s_total, s_ovf;
-    __shared__ uint32_t s_wtot[TOPK_WAVES];
+    __shared__ uint32_t s_wtot[(NT / 64)];
+    __shared__ uint32_t s_lohist[64];
     __shared__ double s_q[128];
     const int row = blockIdx.x;
     const int tid = threadIdx.x;
@@ -1025,43 +1059,46 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
     constexpr int NB = sizeof(C) == 4 ? 4 : 6;     // significant bytes of a composite
     bool exact_path = !a.fast;
     if (a.fast) {
-        if (tid < 256) hist[tid] = a.hist[static_cast<int64_t>(row) * 256 + tid];
+        for (int i = tid; i < HIST_BINS; i += NT) hist[i] = a.hist[static_cast<int64_t>(row) * HIST_BINS + i];
         if (tid == 0) s_count = 0;
         __syncthreads();
         if (wave == 0) {
-            uint32_t t = hist[4 * lane] + hist[4 * lane + 1] + hist[4 * lane + 2] + hist[4 * lane + 3];
+            uint32_t t = 0;
+#pragma unroll
+            for (int j = 0; j < HIST_BINS / 64; ++j) t += hist[(HIST_BINS / 64) * lane + j];
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off, 64);
             if (lane == 0) s_total = t;
-            topk_find_bin(hist, static_cast<uint32_t>(a.T), lane, &s_bin, &s_need);
+            topk_find_bin_n<HIST_BINS>(hist, static_cast<uint32_t>(a.T), lane, &s_bin, &s_need);
         }
         __syncthreads();
         exact_path = s_total < static_cast<uint32_t>(a.T);
         if (!exact_path) {
+            constexpr uint32_t LOW = (1u << HIST_SHIFT) - 1u;
             const uint32_t bsel = s_bin, need_lo = s_need;
-            uint32_t* lohist = hist + 256;          // certified keys of bin bsel by low byte
-            if (tid < 256) lohist[tid] = 0;
+            uint32_t* lohist = s_lohist;            // certified keys of bin bsel by their low bits
+            if (tid < 64) lohist[tid] = 0;
             __syncthreads();
             // One pass over the row, 4 x 8 keys (16-byte loads) and their
-            // uncertain bits per thread at a time: every key >= bsel << 8
-            // joins the list (one LDS atomic per wavefront and step), and the
-            // certified keys of bin bsel are counted by low byte.  L, the
+            // uncertain bits per thread at a time: every key >= the first key
+            // of bin bsel joins the list (one LDS atomic per wavefront and step), and the
+            // certified keys of bin bsel are counted by their low bits.  L, the
             // T-th largest certified key, is then the bound; list entries
             // below it are harmless (their exact keys are below L <= K).
             auto collect = [&](uint32_t lim, bool count_lo) {
                 // (the trip count is the wavefront's: the shuffles below need every lane)
-                for (int64_t i0 = 8 * static_cast<int64_t>(tid); i0 - 8 * lane < a.P; i0 += 32 * TOPK_THREADS) {
+                for (int64_t i0 = 8 * static_cast<int64_t>(tid); i0 - 8 * lane < a.P; i0 += 32 * NT) {
                     uint4 w[4];
                     uint32_t ub[4];
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
-                        const int64_t ib = i0 + u * 8 * TOPK_THREADS;
+                        const int64_t ib = i0 + u * 8 * NT;
                         w[u] = ib < a.P ? *reinterpret_cast<const uint4*>(kr + ib) : uint4{0, 0, 0, 0};
                         ub[u] = ib < a.P ? (ur[ib >> 5] >> (ib & 31)) & 0xffu : 0u;
                     }
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
-                        const int64_t ib = i0 + u * 8 * TOPK_THREADS;
+                        const int64_t ib = i0 + u * 8 * NT;
                         const uint32_t ws[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
                         uint32_t take = 0;
 #pragma unroll
@@ -1069,8 +1106,8 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
                             const uint32_t key = (ws[j >> 1] >> (16 * (j & 1))) & 0xffffu;
                             const bool in = ib + j < a.P;
                             take |= static_cast<uint32_t>(in && key >= lim) << j;
-                            if (count_lo && in && !((ub[u] >> j) & 1u) && (key >> 8) == bsel)
-                                atomicAdd(&lohist[key & 0xffu], 1u);
+                            if (count_lo && in && !((ub[u] >> j) & 1u) && (key >> HIST_SHIFT) == bsel)
+                                atomicAdd(&lohist[key & LOW], 1u);
                         }
                         // wavefront-aggregated slots
                         const uint32_t c = __popc(take);
@@ -1096,11 +1133,11 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
                     }
                 }
             };
-            collect(bsel << 8, true);
+            collect(bsel << HIST_SHIFT, true);
             __syncthreads();
-            if (wave == 0) topk_find_bin(lohist, need_lo, lane, &s_bin, &s_need);
+            if (wave == 0) topk_find_bin_n<(1 << HIST_SHIFT)>(lohist, need_lo, lane, &s_bin, &s_need);
             __syncthreads();
-            const uint32_t L = (bsel << 8) | s_bin;
+            const uint32_t L = (bsel << HIST_SHIFT) | s_bin;
             if (s_count > static_cast<uint32_t>(a.cap)) {
                 // over the capacity: collect again from the bound itself
                 __syncthreads();
@@ -1119,7 +1156,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
                 const uint32_t ucap = static_cast<uint32_t>(a.n2) * sizeof(C) / 4;
                 if (tid == 0) s_total = 0;
                 __syncthreads();
-                for (uint32_t i0 = tid; i0 - lane < cnt; i0 += TOPK_THREADS) {
+                for (uint32_t i0 = tid; i0 - lane < cnt; i0 += NT) {
                     const bool u = i0 < cnt && flags[i0] &&
                                    static_cast<uint32_t>(list[i0] >> Comp<C>::IDX_BITS) >= L;
                     const uint64_t m = __ballot(u);
@@ -1131,13 +1168,13 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
                 __syncthreads();
                 const uint32_t ucnt = s_total;
                 if (ucnt <= ucap) {
-                    for (uint32_t u = tid; u < ucnt; u += TOPK_THREADS) {
+                    for (uint32_t u = tid; u < ucnt; u += NT) {
                         const uint32_t i = uslot[u];
                         const int64_t idx = Comp<C>::index(list[i]);
                         list[i] = Comp<C>::make(exact_key_row(kbase + idx * a.ks_n, q, a.f16 != 0), idx);
                     }
                 } else {
-                    for (uint32_t i = tid; i < cnt; i += TOPK_THREADS) {
+                    for (uint32_t i = tid; i < cnt; i += NT) {
                         if (!flags[i]) continue;
                         const C c = list[i];
                         if (static_cast<uint32_t>(c >> Comp<C>::IDX_BITS) < L) continue;
@@ -1155,10 +1192,10 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
                 {
                     uint32_t* bcnt = brk;                   // bucket counts (then fill counters)
                     uint32_t* bstart = brk + TOPK_SPAN;     // first rank of each bucket
-                    for (int i = tid; i < TOPK_SPAN; i += TOPK_THREADS) bcnt[i] = 0;
+                    for (int i = tid; i < TOPK_SPAN; i += NT) bcnt[i] = 0;
                     if (tid == 0) s_ovf = 0;
                     __syncthreads();
-                    for (uint32_t i = tid; i < cnt; i += TOPK_THREADS) {
+                    for (uint32_t i = tid; i < cnt; i += NT) {
                         const uint32_t key = static_cast<uint32_t>(list[i] >> Comp<C>::IDX_BITS);
                         if (key >= L) {
                             if (key - L < static_cast<uint32_t>(TOPK_SPAN)) atomicAdd(&bcnt[key - L], 1u);
@@ -1169,7 +1206,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
                     if (!s_ovf) {
                         // exclusive prefix over the buckets in descending key order
                         // (thread t: buckets SPAN - 1 - BPT t - u, u < BPT)
-                        constexpr int BPT = TOPK_SPAN / TOPK_THREADS;
+                        constexpr int BPT = TOPK_SPAN / NT;
                         uint32_t cu[BPT], sum = 0;
 #pragma unroll
                         for (int u = 0; u < BPT; ++u) {
@@ -1193,7 +1230,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
                             excl += cu[u];
                         }
                         __syncthreads();
-                        for (uint32_t i = tid; i < cnt; i += TOPK_THREADS) {
+                        for (uint32_t i = tid; i < cnt; i += NT) {
                             const C c = list[i];
                             const uint32_t key = static_cast<uint32_t>(c >> Comp<C>::IDX_BITS);
                             if (key >= L) brank_tmp[bstart[key - L] + atomicAdd(&bcnt[key - L], 1u)] = c;
@@ -1201,7 +1238,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
                         __syncthreads();
                         // the entries at or above L, bucket by bucket (the fill counters are the counts again)
                         const uint32_t tot = bstart[0] + bcnt[0];
-                        for (uint32_t pos = tid; pos < tot; pos += TOPK_THREADS) {
+                        for (uint32_t pos = tid; pos < tot; pos += NT) {
                             const C c = brank_tmp[pos];
                             const uint32_t off = static_cast<uint32_t>(c >> Comp<C>::IDX_BITS) - L;
                             const uint32_t s0 = bstart[off], n = bcnt[off];
@@ -1218,9 +1255,9 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
                 uint32_t need = static_cast<uint32_t>(a.T);
                 for (int pass = 0; pass < NB; ++pass) {
                     const int shift = 8 * (NB - 1 - pass);
-                    for (int i = tid; i < TOPK_HIST * 256; i += TOPK_THREADS) hist[i] = 0;
+                    for (int i = tid; i < (NT / 128) * 256; i += NT) hist[i] = 0;
                     __syncthreads();
-                    for (uint32_t i = tid; i < cnt; i += TOPK_THREADS) {
+                    for (uint32_t i = tid; i < cnt; i += NT) {
                         const C c = list[i];
                         // (entries below L are not winners)
                         if ((c & pmask) == prefix && static_cast<uint32_t>(c >> Comp<C>::IDX_BITS) >= L)
@@ -1230,7 +1267,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
                     if (tid < 256) {
                         uint32_t sum = 0;
 #pragma unroll
-                        for (int w = 0; w < TOPK_HIST; ++w) sum += hist[w * 256 + tid];
+                        for (int w = 0; w < (NT / 128); ++w) sum += hist[w * 256 + tid];
                         hist[tid] = sum;
                     }
                     __syncthreads();
@@ -1243,23 +1280,23 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
                 // the T composites >= the T-th largest
                 if (tid == 0) s_count = 0;
                 __syncthreads();
-                for (uint32_t i = tid; i < cnt; i += TOPK_THREADS) {
+                for (uint32_t i = tid; i < cnt; i += NT) {
                     const C c = list[i];
                     if (c >= prefix) {
                         const uint32_t slot = atomicAdd(&s_count, 1u);
                         if (slot < static_cast<uint32_t>(a.n2)) sel_f[slot] = c;
                     }
                 }
-                for (int i = a.T + tid; i < a.n2; i += TOPK_THREADS) sel_f[i] = 0;   // real composites are > 0
+                for (int i = a.T + tid; i < a.n2; i += NT) sel_f[i] = 0;   // real composites are > 0
                 __syncthreads();
-                topk_sort_out(sel_f, a.T, a.n2, a.T <= TOPK_RANK_LIMIT, orow);
+                topk_sort_out<C, NT>(sel_f, a.T, a.n2, a.T <= TOPK_RANK_LIMIT, orow);
                 return;
             }
         }
     }
     // exact path: recompute the row's uncertain keys in place
     __syncthreads();                               // (s_q written)
-    for (int64_t wi = tid; wi < a.UW; wi += TOPK_THREADS) {
+    for (int64_t wi = tid; wi < a.UW; wi += NT) {
         uint32_t bits = ur[wi];
         while (bits) {
             const int j = __ffs(static_cast<int>(bits)) - 1;
@@ -1270,7 +1307,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_kernel(TopkArgs a) {
     }
     __syncthreads();                               // the keys written above are visible to the workgroup
     C* sel = a.gsort ? static_cast<C*>(a.gsel) + static_cast<int64_t>(row) * a.n2 : list;
-    topk_exact_row(kr, static_cast<const uint16_t*>(nullptr), a.P, a.T, a.n2,
+    topk_exact_row<C, NT>(kr, static_cast<const uint16_t*>(nullptr), a.P, a.T, a.n2,
                    !a.gsort && a.T <= TOPK_RANK_LIMIT, sel, hist, orow);
 }
 
@@ -1291,7 +1328,7 @@ TopkPlan topk_plan(int64_t P, int T, size_t lds_budget) {
         while (t.n2 < T) t.n2 <<= 1;
     }
     const size_t budget = std::min<size_t>(lds_budget, TOPK_LDS_MAX);
-    const size_t hist = static_cast<size_t>(TOPK_HIST) * 256 * 4;
+    const size_t hist = static_cast<size_t>(TOPK_HIST_AREA) * 4;
     const size_t sel = static_cast<size_t>(t.n2) * cs;
     t.gsort = hist + sel > budget;
     // candidate path: list (cap composites) + sel + uncertain flags (cap
@@ -1299,7 +1336,9 @@ TopkPlan topk_plan(int64_t P, int T, size_t lds_budget) {
     const size_t buckets = static_cast<size_t>(2 * TOPK_SPAN) * 4;
     if (hist + sel + buckets + 16 < budget) {
         const int64_t room = static_cast<int64_t>((budget - hist - sel - buckets - 16) / (2 * cs + 1)) / 16 * 16;
-        const int64_t want = std::min<int64_t>(std::max<int64_t>(2 * static_cast<int64_t>(T), 4096), (P + 7) / 8 * 8);
+        // (about 34 KB at T ~ 800: four rows' workgroups share a CU)
+        const int64_t want = std::min<int64_t>((std::max<int64_t>(2 * static_cast<int64_t>(T), 2048) + 15) / 16 * 16,
+                                               (P + 15) / 16 * 16);
         t.cap = static_cast<int>(std::min<int64_t>({want, room, 65536}));
         t.fast = t.cap >= T;
     }
@@ -1308,6 +1347,19 @@ TopkPlan topk_plan(int64_t P, int T, size_t lds_budget) {
     t.lds = (t.lds + 15) / 16 * 16;
     t.gbytes = t.gsort ? (sel + 255) / 256 * 256 : 0;
     return t;
+}
+
+// compute units of the current device (cached per device)
+int device_cus() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cache[dev] = v;
+    }
+    return cache[dev];
 }
 
 // LDS a topk workgroup may use on the current device (cached per device)
@@ -1526,7 +1578,7 @@ SelectLayout select_layout(int B, int H_out, int64_t P, int T, const TopkPlan& t
     L.keys = L.qb + up(rows * 128 * 2 * 4);
     L.unc = L.keys + up(rows * key_pitch(P) * 2);
     L.hist = L.unc + up(rows * unc_words(P) * 4);
-    L.gsel = L.hist + up(rows * 256 * 4);
+    L.gsel = L.hist + up(rows * HIST_BINS * 4);
     L.total = L.gsel + (tp.gsort ? rows * tp.gbytes : 0);
     (void)T;
     return L;
@@ -1617,15 +1669,17 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
     if (rc) return rc;
     TopkArgs ta{keys, unc, hist, p, KP, unc_words(p), top_k, tp.n2, tp.cap, tp.fast, tp.gsort, gsel,
                 k, ks_b, ks_h, ks_n, hk, G, GP, is_fp16, qm, out_idx};
-    const dim3 tgrid(static_cast<unsigned>(b * h_out)), tblock(TOPK_THREADS);
-    if (tp.lds > 64 * 1024) {
-        const void* fn = tp.wide ? reinterpret_cast<const void*>(&topk_kernel<uint64_t>)
-                                 : reinterpret_cast<const void*>(&topk_kernel<uint32_t>);
-        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(tp.lds)) != hipSuccess)
-            return fail(HYQ_EDEVICE, "hyq_vertical_select: cannot raise the LDS limit of the top-k kernel");
+    // 256-thread workgroups (four rows per CU) when the rows are many, 512
+    // (a row's phases shorter) when a CU has at most a row or two
+    const dim3 tgrid(static_cast<unsigned>(b * h_out));
+    const bool many = static_cast<int64_t>(b) * h_out >= 2 * static_cast<int64_t>(device_cus());
+    if (tp.wide) {
+        if (many) topk_kernel<uint64_t, 256><<<tgrid, dim3(256), tp.lds, s>>>(ta);
+        else topk_kernel<uint64_t, 512><<<tgrid, dim3(512), tp.lds, s>>>(ta);
+    } else {
+        if (many) topk_kernel<uint32_t, 256><<<tgrid, dim3(256), tp.lds, s>>>(ta);
+        else topk_kernel<uint32_t, 512><<<tgrid, dim3(512), tp.lds, s>>>(ta);
     }
-    if (tp.wide) topk_kernel<uint64_t><<<tgrid, tblock, tp.lds, s>>>(ta);
-    else topk_kernel<uint32_t><<<tgrid, tblock, tp.lds, s>>>(ta);
     return check_launch("hyq_vertical_select (topk)");
 }
 

@@ -683,6 +683,24 @@ def prefill_trace_summary(trace_csv):
     return table
 
 
+def kernel_trace_summary(trace_csv):
+    """Median duration per kernel (name without its argument list) and grid
+    size over every dispatch of a rocprofv3 kernel trace (run_kernel_trace.csv),
+    this library's kernels only, in microseconds."""
+    import csv
+    import numpy as np
+    d = {}
+    for r in csv.DictReader(open(trace_csv)):
+        n = r["Kernel_Name"].replace("void ", "").replace("hyq::(anonymous namespace)::", "")
+        if not n.startswith(("score", "topk", "qmean", "mark", "zero_words", "compact_quant", "gather_rows",
+                             "quant_pack", "decode_kernel", "dequant", "prefill", "kv_", "lists", "per_block")):
+            continue
+        grid = r.get("Grid_Size_X", r.get("Grid_Size", ""))
+        d.setdefault((n.split("(")[0], grid), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    return [{"kernel": k, "grid": g, "dispatches": len(v), "median_us": round(float(np.median(v)), 1)}
+            for (k, g), v in sorted(d.items())]
+
+
 PHASES = ("entry", "arguments", "Q", "first K/V", "stream done", "LDS merge", "partial acked",
           "counter", "merge (m,l) in", "merge summed", "merge stored", "merge entered",
           "merge loads issued")
@@ -811,12 +829,20 @@ def main():
                          "--pmc-decode-shapes: FETCH_CSV WRITE_CSV [SQ_CSV] (no GPU)")
     ap.add_argument("--prefill-trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="per-kernel table of a kernel trace of --prefill-only (no GPU)")
+    ap.add_argument("--boundary-only", action="store_true",
+                    help="run the config-3 boundary section (select, freeze, flush) only")
+    ap.add_argument("--kernel-trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="median duration per kernel and grid of a kernel trace (no GPU)")
     args = ap.parse_args()
     if args.pmc_summary:
         print(json.dumps(pmc_decode_summary(*args.pmc_summary), indent=1))
         return
     if args.prefill_trace_summary:
         print(json.dumps(prefill_trace_summary(args.prefill_trace_summary), indent=1))
+        return
+    if args.kernel_trace_summary:
+        for r in kernel_trace_summary(args.kernel_trace_summary):
+            print(json.dumps(r))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -839,6 +865,9 @@ def main():
         return
     if args.prefill_only:
         print(json.dumps({"config4_prefill": bench_prefill(dev)}), flush=True)
+        return
+    if args.boundary_only:
+        print(json.dumps({"config3_boundary": bench_boundary(dev)}), flush=True)
         return
 
     B, HQ, HKV, N = 1, 32, 8, 8192

@@ -303,7 +303,12 @@ def _load_fast_ext():
     if os.path.exists(path):
         spec = importlib.util.spec_from_file_location("hyquant_amd._hyq_fast", path)
         m = importlib.util.module_from_spec(spec)
-        spec.loader.exec_module(m)
+        try:
+            spec.loader.exec_module(m)
+        except (ImportError, OSError):
+            # built against another torch: the Python paths take every call
+            _FX = False
+            return False
         P = _lib.DecodeParams
         if m.layout() == (ctypes.sizeof(P), P.seg_n.offset, P.dtype_flags.offset):
             m.set_entry(ctypes.cast(_lib.lib().hyq_decode_hybrid, ctypes.c_void_p).value)

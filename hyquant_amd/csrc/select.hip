@@ -199,10 +199,10 @@ __device__ __forceinline__ void add8_f64(double (&acc)[8], uint4 v, bool f16) {
     }
 }
 
-template <int THREADS>
+template <int THREADS, bool F16>
 __global__ __launch_bounds__(THREADS) void qmean16_kernel(const uint16_t* __restrict__ q, int64_t qs_b, int64_t qs_h,
                                                             int64_t qs_t, int QL, int tail, int R, int HK, int G,
-                                                            int GP, int f16, double* __restrict__ qm,
+                                                            int GP, double* __restrict__ qm,
                                                             uint16_t* __restrict__ qb, uint32_t* __restrict__ hist) {
     const int row = blockIdx.x;                    // (b, hk, g)
     const int g = row % GP;
@@ -224,23 +224,44 @@ __global__ __launch_bounds__(THREADS) void qmean16_kernel(const uint16_t* __rest
     const uint16_t* base = q + b * qs_b + static_cast<int64_t>(ho * R) * qs_h + static_cast<int64_t>(QL - tail) * qs_t + 8 * sub;
     auto ld = [&](int r, int t) { return *reinterpret_cast<const uint4*>(base + r * qs_h + static_cast<int64_t>(t) * qs_t); };
     double acc[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+    const bool f16 = F16;
     if (R == 1) {
+        // eight rows' loads in flight per thread (the kernel is bound by
+        // their latency), added in row order
         int t = slot;
-        for (; t + 3 * QV_SLOTS < tail; t += 4 * QV_SLOTS) {
-            uint4 v[4];
+        for (; t + 7 * QV_SLOTS < tail; t += 8 * QV_SLOTS) {
+            uint4 v[8];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = ld(0, t + u * QV_SLOTS);
+            for (int u = 0; u < 8; ++u) v[u] = ld(0, t + u * QV_SLOTS);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) add8_f64(acc, v[u], f16);
+            for (int u = 0; u < 8; ++u) add8_f64(acc, v[u], f16);
         }
         for (; t < tail; t += QV_SLOTS) add8_f64(acc, ld(0, t), f16);
     } else {
         // the R heads of a row are averaged (one rounding to the model
-        // dtype), then the row means summed; two rows per pass
+        // dtype), then the row means summed; two rows per pass, two heads'
+        // loads of both in flight at a time.  x / R is x * (1 / R), exact,
+        // when R is a power of two.
+        const bool pow2 = (R & (R - 1)) == 0;
+        const double rinv = 1.0 / R;
         for (int t = slot; t < tail; t += 2 * QV_SLOTS) {
             const int t1 = min(t + QV_SLOTS, tail - 1);
             double g0[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0}, g1[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
-            for (int r = 0; r < R; ++r) {
+            int r = 0;
+            for (; r + 1 < R; r += 2) {
+                uint4 v0[2], v1[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    v0[u] = ld(r + u, t);
+                    v1[u] = ld(r + u, t1);
+                }
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    add8_f64(g0, v0[u], f16);
+                    add8_f64(g1, v1[u], f16);
+                }
+            }
+            for (; r < R; ++r) {
                 const uint4 v0 = ld(r, t), v1 = ld(r, t1);
                 add8_f64(g0, v0, f16);
                 add8_f64(g1, v1, f16);
@@ -248,8 +269,10 @@ __global__ __launch_bounds__(THREADS) void qmean16_kernel(const uint16_t* __rest
             const bool has1 = t + QV_SLOTS < tail;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                acc[i] += half_bits_to_f64(f64_to_half_rne(g0[i] / R, f16), f16);
-                if (has1) acc[i] += half_bits_to_f64(f64_to_half_rne(g1[i] / R, f16), f16);
+                const double m0 = pow2 ? g0[i] * rinv : g0[i] / R;
+                const double m1 = pow2 ? g1[i] * rinv : g1[i] / R;
+                acc[i] += half_bits_to_f64(f64_to_half_rne(m0, f16), f16);
+                if (has1) acc[i] += half_bits_to_f64(f64_to_half_rne(m1, f16), f16);
             }
         }
     }
@@ -268,8 +291,8 @@ __global__ __launch_bounds__(THREADS) void qmean16_kernel(const uint16_t* __rest
         double sum = 0.0;
 #pragma unroll
         for (int k = 0; k < THREADS / 64; ++k) sum += s_sum[k][tid];
-        const uint16_t m = f64_to_half_rne(sum / tail, f16);
-        out[tid] = half_bits_to_f64(m, f16);
+        const uint16_t m = f64_to_half_rne(sum / tail, F16);
+        out[tid] = half_bits_to_f64(m, F16);
         outb[tid] = m;
     }
 }
@@ -1404,14 +1427,14 @@ constexpr int CQ_UNROLL = 2;                // tokens per 16-lane group per pass
 // 16 lanes quantise one bf16 (fp16 when f16) row of 128 channels: lane `sub`
 // holds channels 8 sub .. 8 sub + 7 (`raw`).  All 16 lanes take part in the
 // amax reduction; only the stores depend on `store`.
-template <int NBITS>
-__device__ __forceinline__ void quant_row_group(uint4 raw, int8_t* dst, uint16_t* scl, int sub, bool store, bool f16) {
+template <int NBITS, bool F16>
+__device__ __forceinline__ void quant_row_group(uint4 raw, int8_t* dst, uint16_t* scl, int sub, bool store) {
     float v[8];
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        v[2 * i] = f16 ? f16_bits_to_f32(static_cast<uint16_t>(w[i])) : __uint_as_float(w[i] << 16);
-        v[2 * i + 1] = f16 ? f16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16)) : __uint_as_float(w[i] & 0xffff0000u);
+        v[2 * i] = F16 ? f16_bits_to_f32(static_cast<uint16_t>(w[i])) : __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = F16 ? f16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16)) : __uint_as_float(w[i] & 0xffff0000u);
     }
     float amax = 0.f;
 #pragma unroll
@@ -1460,7 +1483,9 @@ struct CompactArgs {
     int f16;                     // k / v are fp16 (else bf16)
 };
 
-template <int KB, int VB>
+// (the element type is a template parameter: chosen at run time inside the
+// unrolled conversions, both conversions of every element were issued)
+template <int KB, int VB, bool F16>
 __global__ __launch_bounds__(256) void compact_quant_kernel(CompactArgs a) {
     __shared__ uint32_t s_base;
     __shared__ uint32_t s_wpre[CQ_CHUNK / 32 + 1];
@@ -1487,7 +1512,6 @@ __global__ __launch_bounds__(256) void compact_quant_kernel(CompactArgs a) {
     }
     __syncthreads();
     const uint32_t base = s_base;
-    const bool f16 = a.f16;
     // 16 lanes per token; each 16-lane group takes CQ_UNROLL tokens per pass
     // and issues their K and V row loads together (selected rows are loaded
     // too and simply not stored, which keeps the loads unconditional)
@@ -1519,8 +1543,8 @@ __global__ __launch_bounds__(256) void compact_quant_kernel(CompactArgs a) {
             // the n_compact rows of the outputs when they are not
             const bool keep = p < a.P && !((word >> (p & 31)) & 1u) && slot < a.n_compact;
             const int64_t dst = keep ? slot : 0;
-            quant_row_group<KB>(kr[u], a.kp + bh * a.kp_bh + dst * a.kp_n, a.ksc + bh * a.ksc_bh + dst, sub, keep, f16);
-            quant_row_group<VB>(vr[u], a.vp + bh * a.vp_bh + dst * a.vp_n, a.vsc + bh * a.vsc_bh + dst, sub, keep, f16);
+            quant_row_group<KB, F16>(kr[u], a.kp + bh * a.kp_bh + dst * a.kp_n, a.ksc + bh * a.ksc_bh + dst, sub, keep);
+            quant_row_group<VB, F16>(vr[u], a.vp + bh * a.vp_bh + dst * a.vp_n, a.vsc + bh * a.vsc_bh + dst, sub, keep);
         }
     }
 }
@@ -1630,12 +1654,17 @@ extern "C" int hyq_vertical_select(const uint16_t* q, int64_t qs_b, int64_t qs_h
     void* gsel = ws + L.gsel;
     const int GP = padded_heads(G);
     if (aligned(q, 16) && qs_t % 8 == 0 && qs_h % 8 == 0 && qs_b % 8 == 0) {
-        if (group == 1)
-            qmean16_kernel<256><<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(256), 0, s>>>(
-                q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm, qb, hist);
-        else
-            qmean16_kernel<1024><<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(1024), 0, s>>>(
-                q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm, qb, hist);
+        auto mean16 = [&](auto f16) {
+            constexpr bool F = decltype(f16)::value;
+            if (group == 1)
+                qmean16_kernel<256, F><<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(256), 0, s>>>(
+                    q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, qm, qb, hist);
+            else
+                qmean16_kernel<1024, F><<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(1024), 0, s>>>(
+                    q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, qm, qb, hist);
+        };
+        if (is_fp16) mean16(std::true_type{});
+        else mean16(std::false_type{});
     } else
         qmean_kernel<<<dim3(static_cast<unsigned>(b * hk * GP)), dim3(QM_THREADS), 0, s>>>(
             q, qs_b, qs_h, qs_t, q_len, tail, group, hk, G, GP, is_fp16, qm, qb, hist);
@@ -1726,17 +1755,22 @@ extern "C" int hyq_freeze_reorganise(const uint16_t* k, int64_t ks_b, int64_t ks
         CompactArgs a{k, v, ks_b, ks_h, ks_n, vs_b, vs_h, vs_n, hk, P, P - top_k, words, bits,
                       kp, vp, kp_bh, kp_n, vp_bh, vp_n, ksc, vsc, ksc_bh, vsc_bh, k_bits, v_bits, is_fp16};
         dim3 grid(static_cast<unsigned>((P + CQ_CHUNK - 1) / CQ_CHUNK), static_cast<unsigned>(bh));
-        switch (10 * k_bits + v_bits) {
-            case 44: compact_quant_kernel<4, 4><<<grid, dim3(256), 0, s>>>(a); break;
-            case 42: compact_quant_kernel<4, 2><<<grid, dim3(256), 0, s>>>(a); break;
-            case 48: compact_quant_kernel<4, 8><<<grid, dim3(256), 0, s>>>(a); break;
-            case 24: compact_quant_kernel<2, 4><<<grid, dim3(256), 0, s>>>(a); break;
-            case 22: compact_quant_kernel<2, 2><<<grid, dim3(256), 0, s>>>(a); break;
-            case 28: compact_quant_kernel<2, 8><<<grid, dim3(256), 0, s>>>(a); break;
-            case 84: compact_quant_kernel<8, 4><<<grid, dim3(256), 0, s>>>(a); break;
-            case 82: compact_quant_kernel<8, 2><<<grid, dim3(256), 0, s>>>(a); break;
-            default: compact_quant_kernel<8, 8><<<grid, dim3(256), 0, s>>>(a); break;
-        }
+        auto launch = [&](auto f16) {
+            constexpr bool F = decltype(f16)::value;
+            switch (10 * k_bits + v_bits) {
+                case 44: compact_quant_kernel<4, 4, F><<<grid, dim3(256), 0, s>>>(a); break;
+                case 42: compact_quant_kernel<4, 2, F><<<grid, dim3(256), 0, s>>>(a); break;
+                case 48: compact_quant_kernel<4, 8, F><<<grid, dim3(256), 0, s>>>(a); break;
+                case 24: compact_quant_kernel<2, 4, F><<<grid, dim3(256), 0, s>>>(a); break;
+                case 22: compact_quant_kernel<2, 2, F><<<grid, dim3(256), 0, s>>>(a); break;
+                case 28: compact_quant_kernel<2, 8, F><<<grid, dim3(256), 0, s>>>(a); break;
+                case 84: compact_quant_kernel<8, 4, F><<<grid, dim3(256), 0, s>>>(a); break;
+                case 82: compact_quant_kernel<8, 2, F><<<grid, dim3(256), 0, s>>>(a); break;
+                default: compact_quant_kernel<8, 8, F><<<grid, dim3(256), 0, s>>>(a); break;
+            }
+        };
+        if (is_fp16) launch(std::true_type{});
+        else launch(std::false_type{});
         int rc = check_launch("hyq_freeze_reorganise (compact)");
         if (rc) return rc;
     }

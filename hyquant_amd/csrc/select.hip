@@ -1102,50 +1102,58 @@ __global__ __launch_bounds__(NT) void topk_kernel(TopkArgs a) {
             uint32_t* lohist = s_lohist;            // certified keys of bin bsel by their low bits
             if (tid < 64) lohist[tid] = 0;
             __syncthreads();
-            // One pass over the row, 4 x 8 keys (16-byte loads) and their
+            // One pass over the row, CU x 8 keys (16-byte loads) and their
             // uncertain bits per thread at a time: every key >= the first key
             // of bin bsel joins the list (one LDS atomic per wavefront and step), and the
             // certified keys of bin bsel are counted by their low bits.  L, the
             // T-th largest certified key, is then the bound; list entries
             // below it are harmless (their exact keys are below L <= K).
+            constexpr int CU = NT == 256 ? 8 : 4;   // 16-byte key loads in flight per thread
             auto collect = [&](uint32_t lim, bool count_lo) {
                 // (the trip count is the wavefront's: the shuffles below need every lane)
-                for (int64_t i0 = 8 * static_cast<int64_t>(tid); i0 - 8 * lane < a.P; i0 += 32 * NT) {
-                    uint4 w[4];
-                    uint32_t ub[4];
+                for (int64_t i0 = 8 * static_cast<int64_t>(tid); i0 - 8 * lane < a.P; i0 += 8 * CU * NT) {
+                    uint4 w[CU];
+                    uint32_t ub[CU];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
+                    for (int u = 0; u < CU; ++u) {
                         const int64_t ib = i0 + u * 8 * NT;
                         w[u] = ib < a.P ? *reinterpret_cast<const uint4*>(kr + ib) : uint4{0, 0, 0, 0};
                         ub[u] = ib < a.P ? (ur[ib >> 5] >> (ib & 31)) & 0xffu : 0u;
                     }
+                    uint32_t take[CU], c = 0;
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
+                    for (int u = 0; u < CU; ++u) {
                         const int64_t ib = i0 + u * 8 * NT;
                         const uint32_t ws[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-                        uint32_t take = 0;
+                        take[u] = 0;
 #pragma unroll
                         for (int j = 0; j < 8; ++j) {
                             const uint32_t key = (ws[j >> 1] >> (16 * (j & 1))) & 0xffffu;
                             const bool in = ib + j < a.P;
-                            take |= static_cast<uint32_t>(in && key >= lim) << j;
+                            take[u] |= static_cast<uint32_t>(in && key >= lim) << j;
                             if (count_lo && in && !((ub[u] >> j) & 1u) && (key >> HIST_SHIFT) == bsel)
                                 atomicAdd(&lohist[key & LOW], 1u);
                         }
-                        // wavefront-aggregated slots
-                        const uint32_t c = __popc(take);
-                        uint32_t incl = c;
+                        c += __popc(take[u]);
+                    }
+                    // one wavefront-aggregated block of slots for the whole step
+                    uint32_t incl = c;
 #pragma unroll
-                        for (int off = 1; off < 64; off <<= 1) {
-                            const uint32_t o = __shfl_up(incl, off, 64);
-                            if (lane >= off) incl += o;
-                        }
-                        uint32_t base = 0;
-                        if (lane == 63 && incl) base = atomicAdd(&s_count, incl);
-                        base = __shfl(base, 63, 64) + incl - c;
-                        while (take) {
-                            const int j = __ffs(static_cast<int>(take)) - 1;
-                            take &= take - 1;
+                    for (int off = 1; off < 64; off <<= 1) {
+                        const uint32_t o = __shfl_up(incl, off, 64);
+                        if (lane >= off) incl += o;
+                    }
+                    uint32_t base = 0;
+                    if (lane == 63 && incl) base = atomicAdd(&s_count, incl);
+                    base = __shfl(base, 63, 64) + incl - c;
+#pragma unroll
+                    for (int u = 0; u < CU; ++u) {
+                        const int64_t ib = i0 + u * 8 * NT;
+                        const uint32_t ws[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+                        uint32_t t = take[u];
+                        while (t) {
+                            const int j = __ffs(static_cast<int>(t)) - 1;
+                            t &= t - 1;
                             if (base < static_cast<uint32_t>(a.cap)) {
                                 const uint32_t key = (ws[j >> 1] >> (16 * (j & 1))) & 0xffffu;
                                 list[base] = Comp<C>::make(key, ib + j);

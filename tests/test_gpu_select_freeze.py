@@ -24,6 +24,9 @@ def _rand_bf16(rng, shape, scale=1.0):
     (3, 2, 2, 64, 129, 128, 1.0),     # prefix of one token, rho = 1
     (1, 2, 2, 8, 16064, 64, 0.1),     # 1600 winners: several ranked per thread, keys cached in LDS
     (1, 2, 1, 16, 30064, 64, 0.1),    # 3000 winners: bitonic order, keys read from memory
+    (2, 4, 2, 32, 5000, 64, 0.05),    # GQA 2 (two heads per packed column group)
+    (1, 6, 2, 32, 5000, 64, 0.05),    # GQA 3 (padded to four: a padding column per group)
+    (1, 16, 2, 32, 3000, 64, 0.05),   # GQA 8
 ])
 def test_selector_prefill_variant_bit_exact(B, HQ, HK, QL, KL, W, rho):
     from hyquant_amd.vertical import compute_vertical_indices

@@ -500,6 +500,8 @@ constexpr int SM_WG_ROWS = 4 * SM_STAGES * SM_ROWS;
 
 typedef __bf16 sel_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float sel_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));   // (non-temporal stores take clang vectors)
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // the exact (float64, d order) key of one bf16 row held in LDS, as score_kernel
 __device__ __forceinline__ uint32_t exact_key_lds(const uint8_t* row, const double* q) {
@@ -526,8 +528,14 @@ __global__ __launch_bounds__(256) void score_mfma_kernel(const uint16_t* __restr
     constexpr int TPK = 16 / GM;                   // tiles per packed accumulator
     constexpr int SPK = TPK >= 2 ? TPK / 2 : 1;    // stages per packed group
     constexpr int SGRP = SPK >= 2 ? SPK : 2;       // stages per loop pass (two register stages)
+    // GM <= 8: the workgroup's keys and uncertain words wait in LDS and are
+    // written after its stream (GM = 16 would need 32 KB more LDS, one
+    // workgroup per CU: its epilogues store directly)
+    constexpr bool DEFER = GM <= 8;
     __shared__ __align__(16) uint8_t s_rows[4][SM_ROWS * SM_PITCH];
     __shared__ uint32_t s_hist[GM][HIST_BINS / 2];  // certified keys, packed 16-bit counts
+    __shared__ __align__(16) uint16_t s_keys[DEFER ? GM : 1][DEFER ? SM_WG_ROWS : 8];
+    __shared__ uint32_t s_unc[DEFER ? GM : 1][DEFER ? SM_WG_ROWS / 32 : 1];
     const int bh = blockIdx.y;                     // b * HK + hk
     const int b = bh / HK, hk = bh % HK;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -630,10 +638,14 @@ __global__ __launch_bounds__(256) void score_mfma_kernel(const uint16_t* __restr
             if (cert && rt + v < nrows && h < G) hist_add16(s_hist[h], key);
             nib |= (cert ? 0u : 1u) << v;
         }
-        if (h < G && rt < nrows) {
+        const u32x2_t kpair = {kv[0] | (kv[1] << 16), kv[2] | (kv[3] << 16)};
+        if (DEFER) {
+            // rt + 3 < SM_WG_ROWS: rt is a multiple of 4 below the workgroup's rows
+            if (h < G && rt < SM_WG_ROWS) *reinterpret_cast<u32x2_t*>(&s_keys[DEFER ? h : 0][rt]) = kpair;
+        } else if (h < G && rt < nrows) {
             uint16_t* kr = keys + (static_cast<int64_t>(bh) * G + h) * KP + r0 + rt;
             if (rt + 3 < nrows) {
-                *reinterpret_cast<uint2*>(kr) = uint2{kv[0] | (kv[1] << 16), kv[2] | (kv[3] << 16)};
+                __builtin_nontemporal_store(kpair, reinterpret_cast<u32x2_t*>(kr));
             } else {
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
@@ -644,10 +656,9 @@ __global__ __launch_bounds__(256) void score_mfma_kernel(const uint16_t* __restr
         uint32_t word = (nib & ((1u << nv) - 1u)) << (16 * tin + 4 * kg);
         word |= __shfl_xor(word, 16, 64);
         word |= __shfl_xor(word, 32, 64);
-        if (TPK >= 2) {
+        if (TPK >= 2) {                                // (DEFER)
             word |= __shfl_xor(word, GM, 64);          // the stage's other tile
-            if (kg == 0 && (jt & 1) == 0 && h < G && blk < nblk)
-                unc[(static_cast<int64_t>(bh) * G + h) * UW + r0 / 32 + blk] = word;
+            if (kg == 0 && (jt & 1) == 0 && h < G && blk < nblk) s_unc[DEFER ? h : 0][DEFER ? blk : 0] = word;
         }
         return word;
     };
@@ -709,6 +720,27 @@ __global__ __launch_bounds__(256) void score_mfma_kernel(const uint16_t* __restr
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last (empty) loads retire before the wave ends
     }
     __syncthreads();
+    if (DEFER && !exact) {
+        // The keys and uncertain words of the workgroup's rows.  Stores mixed
+        // into the K stream cost about as much as 20 us of reading per 32 MB
+        // written on MI355X's HBM wherever they fall; written here, in whole
+        // 16-byte pieces and non-temporal, they cost the least measured.
+        for (int i = threadIdx.x; i < G * (SM_WG_ROWS / 8); i += 256) {
+            const int hh = i / (SM_WG_ROWS / 8), row = 8 * (i % (SM_WG_ROWS / 8));
+            if (row >= nrows) continue;
+            uint16_t* kr = keys + (static_cast<int64_t>(bh) * G + hh) * KP + r0 + row;
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&s_keys[DEFER ? hh : 0][DEFER ? row : 0]);
+            if (row + 8 <= nrows) {
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(kr));   // KP and r0: multiples of 8
+            } else {
+                for (int j = 0; j < nrows - row; ++j) kr[j] = static_cast<uint16_t>(v[j >> 1] >> (16 * (j & 1)));
+            }
+        }
+        for (int i = threadIdx.x; i < G * (SM_WG_ROWS / 32); i += 256) {
+            const int hh = i / (SM_WG_ROWS / 32), blk = i % (SM_WG_ROWS / 32);
+            if (blk < nblk) unc[(static_cast<int64_t>(bh) * G + hh) * UW + r0 / 32 + blk] = s_unc[DEFER ? hh : 0][DEFER ? blk : 0];
+        }
+    }
     hist_flush16(&s_hist[0][0], G, hist, static_cast<int64_t>(bh) * G);
 }
 

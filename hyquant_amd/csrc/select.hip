@@ -35,7 +35,7 @@
 //                     the list does not apply.  Output order "score desc,
 //                     index asc" ("composite desc" for the unique composite
 //                     (key << IDX_BITS) | (IDX_MASK - idx)).
-//   mark_kernel / compact_quant_kernel / gather_rows_kernel  the freeze: a
+//   mark_row_kernel (mark_kernel) / compact_quant_kernel / gather_rows_kernel  the freeze: a
 //                     bitmap of selected prefix positions, quantisation of the
 //                     unselected prefix rows straight into their compact slots
 //                     (ascending position, F6), and the bf16 copies of the
@@ -1457,6 +1457,25 @@ __global__ void mark_kernel(const int64_t* __restrict__ idx, int T, int64_t P, i
     atomicOr(bits + bh * words + (p >> 5), 1u << (p & 31));
 }
 
+// One workgroup per row, rows of up to MARK_ROW_WORDS words: the row's bitmap
+// is built in LDS and written whole (one launch in place of zero_words_kernel
+// and mark_kernel).  Indices outside [0, P) are ignored, as in mark_kernel.
+constexpr int MARK_ROW_WORDS = 8192;       // 32 KiB of LDS: P <= 262144
+__global__ __launch_bounds__(1024) void mark_row_kernel(const int64_t* __restrict__ idx, int T, int64_t P, int64_t words,
+                                                        uint32_t* __restrict__ bits) {
+    __shared__ uint32_t s_w[MARK_ROW_WORDS];
+    const int64_t bh = blockIdx.x;
+    const int nw = static_cast<int>(words);    // <= MARK_ROW_WORDS (host)
+    for (int i = threadIdx.x; i < nw; i += blockDim.x) s_w[i] = 0;
+    __syncthreads();
+    for (int t = threadIdx.x; t < T; t += blockDim.x) {
+        const int64_t p = idx[bh * T + t];
+        if (p >= 0 && p < P) atomicOr(&s_w[p >> 5], 1u << (p & 31));
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nw; i += blockDim.x) bits[bh * words + i] = s_w[i];
+}
+
 // prefix positions per workgroup: 16 KiB of K and V rows read per workgroup.
 // Streams of this read:write mix ran faster the fewer bytes each workgroup
 // covers, down to about 8 KiB; at 16 positions the per-workgroup set-up
@@ -1784,13 +1803,18 @@ extern "C" int hyq_freeze_reorganise(const uint16_t* k, int64_t ks_b, int64_t ks
             return fail(HYQ_ENOSPC, "hyq_freeze_reorganise: workspace too small");
         uint32_t* bits = static_cast<uint32_t*>(workspace);
         const int64_t nw = static_cast<int64_t>(bh) * words;
-        zero_words_kernel<<<dim3(static_cast<unsigned>((nw + 255) / 256)), dim3(256), 0, s>>>(bits, nw);
-        if (int rc0 = check_launch("hyq_freeze_reorganise (zero)")) return rc0;
-        if (top_k > 0) {
-            mark_kernel<<<dim3(static_cast<unsigned>((top_k + 255) / 256), static_cast<unsigned>(bh)), dim3(256), 0, s>>>(
-                topk_idx, top_k, P, words, bits);
-            int rc = check_launch("hyq_freeze_reorganise (mark)");
-            if (rc) return rc;
+        if (words <= MARK_ROW_WORDS) {
+            mark_row_kernel<<<dim3(static_cast<unsigned>(bh)), dim3(1024), 0, s>>>(topk_idx, top_k, P, words, bits);
+            if (int rc0 = check_launch("hyq_freeze_reorganise (mark)")) return rc0;
+        } else {
+            zero_words_kernel<<<dim3(static_cast<unsigned>((nw + 255) / 256)), dim3(256), 0, s>>>(bits, nw);
+            if (int rc0 = check_launch("hyq_freeze_reorganise (zero)")) return rc0;
+            if (top_k > 0) {
+                mark_kernel<<<dim3(static_cast<unsigned>((top_k + 255) / 256), static_cast<unsigned>(bh)), dim3(256), 0, s>>>(
+                    topk_idx, top_k, P, words, bits);
+                int rc = check_launch("hyq_freeze_reorganise (mark)");
+                if (rc) return rc;
+            }
         }
         CompactArgs a{k, v, ks_b, ks_h, ks_n, vs_b, vs_h, vs_n, hk, P, P - top_k, words, bits,
                       kp, vp, kp_bh, kp_n, vp_bh, vp_n, ksc, vsc, ksc_bh, vsc_bh, k_bits, v_bits, is_fp16};

@@ -257,14 +257,18 @@ def test_cache_save_load_resumes_bit_identically(tmp_path, kv):
     assert back.get_seq_length(0) == cache.get_seq_length(0) == inp.N + 37 + 100
 
 
-def test_freeze_bad_indices_stay_inside_the_outputs():
+@pytest.mark.parametrize("N", [600, 263208])
+def test_freeze_bad_indices_stay_inside_the_outputs(N):
     """hyq_freeze_reorganise with repeated and out-of-range top-k indices (an
     ABI precondition violation): an index outside [0, n - w) yields a zero
     row, nothing is written past the n - w - top_k compact rows, and the
-    rows that are written are the right ones (ascending unselected positions)."""
+    rows that are written are the right ones (ascending unselected positions).
+    N = 263208: a prefix of 263144 positions, past the rows whose bitmap is
+    built in one workgroup's LDS (262144)."""
     from hyquant_amd import _lib
+    print(f"freeze bad indices N={N}", flush=True)
     rng = np.random.default_rng(17)
-    HK, N, W, T = 2, 600, 64, 20
+    HK, W, T = 2, 64, 20
     P = N - W
     k = _rand_bf16(rng, (1, HK, N, 128))
     v = _rand_bf16(rng, (1, HK, N, 128))

@@ -1287,7 +1287,12 @@ size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 //     being the workgroups the device holds at once: the first round fills
 //     every slot and the remaining quarter, with the short segment pieces,
 //     evens out the workgroups that ran slow.  Pieces stay >= 96 KiB: below
-//     that the per-piece round trips cost more than the balance gains.
+//     that the per-piece round trips cost more than the balance gains.  From
+//     a 384 KiB target the bf16 segments (the top-k rows above all, which
+//     run in the last round) are cut at half the target: B=16, 32K went
+//     from 100.9 to 98.2 us and B=8, 32K from 54.4 to 52.7 us (same box),
+//     while with smaller targets the extra partials cost more than the
+//     shorter round gains (GLM-4-9B shape, 248 KiB: 37.4 -> 40.1 us).
 // Each segment gets its bytes / target pieces (rounded, at least one); the
 // target grows until the pieces fit the merge tables.
 Plan make_plan(int64_t n_quant, const int64_t seg_n[3], int bh_kv, int G, int requested, int kb, int vb,
@@ -1310,11 +1315,13 @@ Plan make_plan(int64_t n_quant, const int64_t seg_n[3], int bh_kv, int G, int re
     if (nonempty == 0) return p;
     const int kmax = std::max(nonempty, std::min(MAX_NWG, MAX_PARTIALS / G));
     int ks[4];
+    int bdiv = 1;                      // the bf16 segments' pieces: target / bdiv bytes
     auto counts_for = [&](int64_t target) {
         int total = 0;
         for (int s = 0; s < 4; ++s) {
+            const int64_t tg = s == 0 ? target : std::max<int64_t>(1, target / bdiv);
             ks[s] = su[s] > 0 ? static_cast<int>(std::min<int64_t>(
-                                    su[s], std::max<int64_t>(1, (su[s] * sc[s] + target / 2) / target)))
+                                    su[s], std::max<int64_t>(1, (su[s] * sc[s] + tg / 2) / tg)))
                               : 0;
             total += ks[s];
         }
@@ -1353,6 +1360,7 @@ Plan make_plan(int64_t n_quant, const int64_t seg_n[3], int bh_kv, int G, int re
     } else {
         const int64_t sl = slots > 0 ? slots : 512;
         target = std::max<int64_t>(96 << 10, head_bytes * bh_kv * 4 / (5 * sl));
+        bdiv = target >= (384 << 10) ? 2 : 1;
         total = counts_for(target);
     }
     while (total > kmax) {

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("HYQ_LIBRARY") or os.path.join(HERE, "libhyq.so")
 
 # the hyq_abi_version() these bindings (struct layouts, argument lists) match
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 HYQ_DT_Q_FP16 = 1
 HYQ_DT_SEG_FP16 = 2
@@ -41,6 +41,8 @@ EXPORTS = (
     "hyq_decode_hybrid_noalloc",
     "hyq_decode_bf16_workspace_size",
     "hyq_decode_bf16",
+    "hyq_decode_legacy4_workspace_size",
+    "hyq_decode_legacy4",
     "hyq_vertical_select_workspace_size",
     "hyq_vertical_select",
     "hyq_freeze_workspace_size",
@@ -74,6 +76,25 @@ class DecodeParams(Structure):
         ("split_tokens", c_int32),
         ("seq_lens_quant", c_void_p), ("seq_lens_seg0", c_void_p),
         ("dtype_flags", c_int32),
+    ]
+
+
+class Legacy4Params(Structure):
+    """Mirror of `hyq_legacy4_params` (include/hyq.h)."""
+    _fields_ = [
+        ("q", c_void_p), ("q_stride", c_int64),
+        ("out", c_void_p), ("out_stride", c_int64),
+        ("k_codes", c_void_p), ("kc_stride_bh", c_int64), ("kc_stride_n", c_int64),
+        ("v_codes", c_void_p), ("vc_stride_bh", c_int64), ("vc_stride_n", c_int64),
+        ("k_scale", c_void_p), ("ks_stride_bh", c_int64), ("ks_stride_g", c_int64),
+        ("v_scale", c_void_p), ("vs_stride_bh", c_int64), ("vs_stride_g", c_int64),
+        ("n", c_int64),
+        ("group", c_int32),
+        ("seg_k", c_void_p * 3), ("seg_k_stride_bh", c_int64 * 3),
+        ("seg_v", c_void_p * 3), ("seg_v_stride_bh", c_int64 * 3),
+        ("seg_n", c_int64 * 3),
+        ("bh_kv", c_int32), ("kv_repeat", c_int32), ("head_dim", c_int32),
+        ("sm_scale", c_float),
     ]
 
 
@@ -124,6 +145,10 @@ def _declare(lib):
                                     c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64,
                                     c_int64, c_int32, c_int32, c_int32, c_float,
                                     c_void_p, c_size_t, c_void_p]
+    lib.hyq_decode_legacy4_workspace_size.restype = c_size_t
+    lib.hyq_decode_legacy4_workspace_size.argtypes = [POINTER(Legacy4Params)]
+    lib.hyq_decode_legacy4.restype = c_int
+    lib.hyq_decode_legacy4.argtypes = [POINTER(Legacy4Params), c_void_p, c_size_t, c_void_p]
     lib.hyq_vertical_select_workspace_size.restype = c_size_t
     lib.hyq_vertical_select_workspace_size.argtypes = [c_int32, c_int32, c_int64, c_int32]
     lib.hyq_vertical_select.restype = c_int

@@ -1255,6 +1255,275 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// legacy-format decode
+// ---------------------------------------------------------------------------
+// The legacy decode format of src/ops/d_stage_cache.py (fused_decode_
+// attention_k4v4 :504-591, splitk_decode_attention_k4v4 :825-951 and its MMA
+// variant :1247-1366): an int4 prefix of offset-encoded codes (channel 2j in
+// the high nibble of byte j, value u - 8) with one fp16 scale per (group of
+// tokens, channel), then the top-k, staging and window bf16 rows.  The
+// prefix tiles are dequantised in registers to the bf16 values of
+// legacy_dequant_kernel (legacy_twice_to_bf16) and computed by the bf16 tile
+// path (bf16_compute): the result of dequantising the prefix and decoding
+// bf16 rows, without the bf16 copy in HBM.  One workgroup per piece
+// (LEG_PIECE prefix tokens or BF_PIECE rows of one segment, doubled for long
+// caches until the pieces fit the merge tables), merged by the head's last
+// arriving workgroup with decode_kernel's protocol and merge.
+constexpr int LEG_PIECE = 512;
+constexpr int BF_PIECE = 128;
+
+struct LegArgs {
+    const uint16_t* q;
+    int64_t q_stride;
+    const uint8_t* kc;             // prefix codes [bh][n][64] (byte strides)
+    const uint8_t* vc;
+    int64_t kc_bh, kc_n, vc_bh, vc_n;
+    const uint16_t* ks;            // prefix scales [bh][groups][D] (element strides)
+    const uint16_t* vs;
+    int64_t ks_bh, ks_g, vs_bh, vs_g;
+    int64_t ks_rows, vs_rows;      // scale rows per head (the descriptors' ranges)
+    int n_leg, group;
+    const uint16_t* sk[3];         // top-k, staging, window rows [bh][n][D]
+    const uint16_t* sv[3];
+    int64_t sk_bh[3], sv_bh[3];
+    int sn[3];
+    int G;
+    float qk_scale;                // sm_scale * log2(e)
+    float* part;
+    float* ml;
+    uint32_t* cnt;
+    uint16_t* out;
+    int64_t out_stride;
+    int nwg, mj;
+    int pfirst[5];                 // pieces of segment s (0: the prefix): [pfirst[s], pfirst[s + 1])
+    int plen[4];                   // tokens per piece of segment s
+};
+
+// the raw loads of one 16-token prefix tile, for the layout of Bf16Raw (the
+// group is a multiple of 16 and pieces start on group boundaries, so the
+// tile's tokens share one scale row)
+struct LegRaw {
+    u32x4 kc;                      // token c: codes of channels 32kb .. 32kb + 31 (byte j: 2j high, 2j + 1 low)
+    u32x4 ksc[4];                  // their fp16 scales, 8 channels per vector
+    uint32_t vc[4];                // slot e (token 4kb + e): codes of channels 8c .. 8c + 7
+    u32x4 vsc;                     // their fp16 scales
+};
+
+// Loads of the tile at token t of a piece starting at prefix token lo: the
+// lane's offsets (kco: token c, vco: token 4kb) are fixed, the tile's
+// position goes in the scalar offsets.  The code descriptors cover the piece
+// and the scale descriptors the head's scale rows (the range check covers
+// the scalar offset too): tokens past either read zeros.
+__device__ __forceinline__ void legacy_fetch(LegRaw& r, const LegArgs& a, Rsrc rkc, Rsrc rvc, Rsrc rks, Rsrc rvs,
+                                             uint32_t kco, uint32_t vco, int lo, int t, int lane) {
+    const int c = lane & 15, kb = lane >> 4;
+    // wave-uniform scalar offsets (left to the compiler, some became vector
+    // values and their loads were wrapped in waterfall loops)
+    const int tu = __builtin_amdgcn_readfirstlane(t);
+    const int g = (lo + tu) / a.group;                     // the tile's scale row
+    const uint32_t skc = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tu * a.kc_n));
+    const uint32_t sks = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(g * a.ks_g * 2));
+    const uint32_t svc = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tu * a.vc_n));
+    const uint32_t svs = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(g * a.vs_g * 2));
+    r.kc = bld128(rkc, kco, skc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.ksc[i] = bld128(rks, static_cast<uint32_t>(64 * kb + 16 * i), sks);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r.vc[e] = bld32(rvc, vco + static_cast<uint32_t>(e * a.vc_n), svc);
+    r.vsc = bld128(rvs, static_cast<uint32_t>(16 * c), svs);
+}
+
+// Byte d of wx (four code bytes with every nibble XOR 8, so a nibble read as a
+// signed 4-bit field is u - 8; channel 2j in the high nibble, 2j + 1 in the
+// low) and the pair's fp16 scales -> bf16 pair.  The float of u - 8 times the
+// scale is exact in fp32 and is rounded once by the packed conversion: for
+// every finite scale these are the bits of legacy_twice_to_bf16 (round to
+// nearest even is symmetric and the product's zeros carry the same signs;
+// checked for every code and every finite fp16 scale), in 3 operations per
+// element instead of about 14.
+// (__builtin_amdgcn_sbfe's result type is unsigned: it is cast to int before
+// the conversion, else the conversion is the unsigned one)
+__device__ __forceinline__ uint32_t leg4_pair(uint32_t wx, int d, uint32_t sw) {
+    const int hi = static_cast<int>(__builtin_amdgcn_sbfe(wx, 8 * d + 4, 4));
+    const int lo = static_cast<int>(__builtin_amdgcn_sbfe(wx, 8 * d, 4));
+    const float a = static_cast<float>(hi) * f16_bits_to_f32(static_cast<uint16_t>(sw));
+    const float b = static_cast<float>(lo) * f16_bits_to_f32(static_cast<uint16_t>(sw >> 16));
+    return pack_bf16x2(a, b);
+}
+
+__device__ __forceinline__ void legacy_dequant(Bf16Raw& b, const LegRaw& r) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t w = r.kc[i] ^ 0x88888888u;
+        b.k[i] = u32x4{leg4_pair(w, 0, r.ksc[i][0]), leg4_pair(w, 1, r.ksc[i][1]), leg4_pair(w, 2, r.ksc[i][2]),
+                       leg4_pair(w, 3, r.ksc[i][3])};
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t w = r.vc[e] ^ 0x88888888u;
+        b.v[e] = u32x4{leg4_pair(w, 0, r.vsc[0]), leg4_pair(w, 1, r.vsc[1]), leg4_pair(w, 2, r.vsc[2]),
+                       leg4_pair(w, 3, r.vsc[3])};
+    }
+}
+
+__global__ __launch_bounds__(THREADS, 2) void legacy_decode_kernel(LegArgs a) {
+#ifdef HYQ_PHASE_TRACE
+    uint64_t ph[TRACE_PH] = {};    // (the merge stamps; not stored by this kernel)
+#endif
+    const int head = blockIdx.x;
+    const int wg = blockIdx.y;
+    const int G = a.G;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 15, kb = lane >> 4;
+
+    extern __shared__ float s_acc[];               // [WAVES][G][D+1]; later the merge weights
+    __shared__ float s_m[WAVES][16];
+    __shared__ float s_l[WAVES][16];
+    __shared__ int s_last;
+
+    WaveState st;
+    st.m = M_INIT;
+    st.l = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) st.acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.ones = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Q row of head c (zero for c >= G): channels 32kb..32kb+31
+    u32x4 qs[4];
+    {
+        const Rsrc rq = make_rsrc(a.q + static_cast<int64_t>(head) * G * a.q_stride,
+                                  static_cast<uint32_t>(G * a.q_stride * 2));
+        const uint32_t qo = static_cast<uint32_t>(c * a.q_stride * 2 + 64 * kb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qs[i] = bld128(rq, qo + 16 * i);
+    }
+    const bf16x8 qb[4] = {__builtin_bit_cast(bf16x8, qs[0]), __builtin_bit_cast(bf16x8, qs[1]),
+                          __builtin_bit_cast(bf16x8, qs[2]), __builtin_bit_cast(bf16x8, qs[3])};
+
+    // this piece: segment sg (0: the prefix), tokens [lo, lo + n) of it
+    int sg = 0;
+    while (sg < 3 && wg >= a.pfirst[sg + 1]) ++sg;
+    const int lo = (wg - a.pfirst[sg]) * a.plen[sg];
+    const int seg_n = sg == 0 ? a.n_leg : a.sn[sg - 1];
+    const int n = max(0, min(a.plen[sg], seg_n - lo));
+    constexpr int TSTRIDE = WAVES * TILE;
+    const int ntile = (n + TILE - 1) / TILE;
+    const int nmine = ntile > wave ? (ntile - wave + WAVES - 1) / WAVES : 0;
+    const int t0 = wave * TILE;
+    if (sg == 0) {
+        const Rsrc rkc = make_rsrc(a.kc + head * a.kc_bh + lo * a.kc_n, static_cast<uint32_t>(n * a.kc_n));
+        const Rsrc rvc = make_rsrc(a.vc + head * a.vc_bh + lo * a.vc_n, static_cast<uint32_t>(n * a.vc_n));
+        const Rsrc rks = make_rsrc(a.ks + head * a.ks_bh, static_cast<uint32_t>(a.ks_rows * a.ks_g * 2));
+        const Rsrc rvs = make_rsrc(a.vs + head * a.vs_bh, static_cast<uint32_t>(a.vs_rows * a.vs_g * 2));
+        // tiles wave, wave+WAVES, ... through a two-deep register ring
+        const uint32_t kco = static_cast<uint32_t>(c * a.kc_n + 16 * kb);
+        const uint32_t vco = static_cast<uint32_t>(4 * kb * a.vc_n + 4 * c);
+        LegRaw r0, r1;
+        Bf16Raw b;
+        legacy_fetch(r0, a, rkc, rvc, rks, rvs, kco, vco, lo, t0, lane);
+        legacy_fetch(r1, a, rkc, rvc, rks, rvs, kco, vco, lo, t0 + TSTRIDE, lane);
+        for (int i = 0; i < nmine; i += 2) {
+            const int t = t0 + i * TSTRIDE;
+            legacy_dequant(b, r0);
+            bf16_compute(st, b, qb, n - t, lane, a.qk_scale);
+            if (i + 1 >= nmine) break;
+            legacy_fetch(r0, a, rkc, rvc, rks, rvs, kco, vco, lo, t + 2 * TSTRIDE, lane);
+            legacy_dequant(b, r1);
+            bf16_compute(st, b, qb, n - t - TSTRIDE, lane, a.qk_scale);
+            if (i + 2 >= nmine) break;
+            legacy_fetch(r1, a, rkc, rvc, rks, rvs, kco, vco, lo, t + 3 * TSTRIDE, lane);
+        }
+    } else {
+        const int s3 = sg - 1;
+        const uint16_t* kbase = a.sk[s3] + head * a.sk_bh[s3] + static_cast<int64_t>(lo) * BROW;
+        const uint16_t* vbase = a.sv[s3] + head * a.sv_bh[s3] + static_cast<int64_t>(lo) * BROW;
+        const uint32_t nbytes = static_cast<uint32_t>(n) * (BROW * 2);
+        const Rsrc rk = make_rsrc(kbase, nbytes), rv = make_rsrc(vbase, nbytes);
+        Bf16Raw r0, r1;
+        bf16_load(r0, rk, rv, t0, lane);
+        bf16_load(r1, rk, rv, t0 + TSTRIDE, lane);
+        for (int i = 0; i < nmine; i += 2) {
+            const int t = t0 + i * TSTRIDE;
+            bf16_compute(st, r0, qb, n - t, lane, a.qk_scale);
+            if (i + 1 >= nmine) break;
+            bf16_load(r0, rk, rv, t + 2 * TSTRIDE, lane);
+            bf16_compute(st, r1, qb, n - t - TSTRIDE, lane, a.qk_scale);
+            if (i + 2 >= nmine) break;
+            bf16_load(r1, rk, rv, t + 3 * TSTRIDE, lane);
+        }
+    }
+
+    // ---- wave -> LDS -> this piece's partial, then decode_kernel's arrival protocol ----
+    const MergeArgs ma{G, a.nwg, a.part, a.ml, a.out, a.out_stride, 0};
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): the rings' last (empty) loads
+    st.l = col_sum(st.l);
+    if (kb == 0) {
+        s_m[wave][c] = st.m;
+        s_l[wave][c] = st.l;
+    }
+    if (c < G) {
+        float* row = s_acc + (wave * G + c) * (D + 1);
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) row[32 * kb + 8 * i + nb] = st.acc[nb][i];
+    }
+    __syncthreads();
+    const int64_t slot = static_cast<int64_t>(head) * ma.nwg + wg;
+    {
+        const Rsrc rpart = make_rsrc(ma.part + slot * G * D, static_cast<uint32_t>(G * D * 4));
+        for (int o = threadIdx.x; o < G * (D / 4); o += THREADS) {
+            const int g = o / (D / 4), ch = 4 * (o % (D / 4));
+            float M = s_m[0][g];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_m[w][g]);
+            f32x4 accv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+                const float wt = fast_exp2(s_m[w][g] - M);
+                const float* row = s_acc + (w * G + g) * (D + 1) + ch;
+                accv += wt * f32x4{row[0], row[1], row[2], row[3]};
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, accv), rpart, o * 16, 0, 16);   // sc1
+        }
+    }
+    if (threadIdx.x < G) {
+        const int g = threadIdx.x;
+        float M = s_m[0][g];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_m[w][g]);
+        float lv = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) lv += fast_exp2(s_m[w][g] - M) * s_l[w][g];
+        __hip_atomic_store(a.ml + (slot * G + g) * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.ml + (slot * G + g) * 2 + 1, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // every store of this workgroup acknowledged before its arrival is counted
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(a.cnt + head * CNT_PAD, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old == static_cast<uint32_t>(ma.nwg - 1));
+    }
+    __syncthreads();
+    if (s_last) {
+        if (threadIdx.x == 0) __hip_atomic_store(a.cnt + head * CNT_PAD, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        switch (a.mj) {
+            case 4: merge_head_waves<4>(ma, head, s_acc TRACE_ARG); break;
+            case 8: merge_head_waves<8>(ma, head, s_acc TRACE_ARG); break;
+            case 12: merge_head_waves<12>(ma, head, s_acc TRACE_ARG); break;
+            case 16: merge_head_waves<16>(ma, head, s_acc TRACE_ARG); break;
+            case 20: merge_head_waves<20>(ma, head, s_acc TRACE_ARG); break;
+            case 24: merge_head_waves<24>(ma, head, s_acc TRACE_ARG); break;
+            case 108: merge_head_cols<8>(ma, head, s_acc); break;
+            case 116: merge_head_cols<16>(ma, head, s_acc); break;
+            default: merge_head_cols<24>(ma, head, s_acc); break;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
@@ -1505,6 +1774,104 @@ int validate(const hyq_decode_params* p) {
     return HYQ_OK;
 }
 
+// ---- legacy-format decode: plan and checks ----
+struct LegPlan {
+    int nwg = 0;
+    int pfirst[5] = {0, 0, 0, 0, 0};
+    int plen[4] = {LEG_PIECE, BF_PIECE, BF_PIECE, BF_PIECE};
+};
+LegPlan legacy_plan(const hyq_legacy4_params* p) {
+    LegPlan pl;
+    const int64_t n[4] = {p->n, p->seg_n[0], p->seg_n[1], p->seg_n[2]};
+    for (;;) {
+        int64_t total = 0;
+        for (int s = 0; s < 4; ++s) total += (n[s] + pl.plen[s] - 1) / pl.plen[s];
+        if (total <= MAX_NWG && total * p->kv_repeat <= MAX_PARTIALS) break;
+        for (int s = 0; s < 4; ++s) pl.plen[s] *= 2;
+    }
+    for (int s = 0; s < 4; ++s)
+        pl.pfirst[s + 1] = pl.pfirst[s] + static_cast<int>((n[s] + pl.plen[s] - 1) / pl.plen[s]);
+    pl.nwg = pl.pfirst[4];
+    return pl;
+}
+
+int validate_legacy(const hyq_legacy4_params* p) {
+    const char* w = "hyq_decode_legacy4: ";
+    if (!p) return fail(HYQ_EINVAL, std::string(w) + "null params");
+    if (p->head_dim != D) return fail(HYQ_ENOTSUP, std::string(w) + "head_dim must be 128");
+    if (p->kv_repeat < 1 || p->kv_repeat > 16) return fail(HYQ_ENOTSUP, std::string(w) + "kv_repeat must be in [1, 16]");
+    if (p->bh_kv < 0 || p->bh_kv > CNT_CAP) return fail(HYQ_ENOTSUP, std::string(w) + "bh_kv out of range");
+    if (p->bh_kv == 0) return HYQ_OK;
+    constexpr int64_t NMAX = int64_t{1} << 24;
+    if (p->n < 0 || p->n > NMAX) return fail(HYQ_ENOTSUP, std::string(w) + "prefix length out of [0, 2^24]");
+    int64_t total = p->n;
+    for (int s = 0; s < 3; ++s) {
+        if (p->seg_n[s] < 0 || p->seg_n[s] > NMAX) return fail(HYQ_ENOTSUP, std::string(w) + "segment length out of [0, 2^24]");
+        total += p->seg_n[s];
+        if (p->seg_n[s] == 0) continue;
+        if (!p->seg_k[s] || !p->seg_v[s]) return fail(HYQ_EINVAL, std::string(w) + "null segment");
+        if (!aligned(p->seg_k[s], 16) || !aligned(p->seg_v[s], 16) || p->seg_k_stride_bh[s] % 8 ||
+            p->seg_v_stride_bh[s] % 8 || p->seg_k_stride_bh[s] < 0 || p->seg_v_stride_bh[s] < 0)
+            return fail(HYQ_EINVAL, std::string(w) + "segments must be 16-byte aligned (head strides % 8 == 0)");
+    }
+    if (total == 0) return fail(HYQ_EINVAL, std::string(w) + "decode with zero key tokens");
+    if (!p->q || !p->out) return fail(HYQ_EINVAL, std::string(w) + "null q or out");
+    if (!aligned(p->q, 16) || p->q_stride % 8 || p->q_stride < D || p->q_stride > NMAX)
+        return fail(HYQ_EINVAL, std::string(w) + "q rows must be 16-byte aligned, stride in [128, 2^24]");
+    if (!aligned(p->out, 8) || p->out_stride % 4 || p->out_stride < D)
+        return fail(HYQ_EINVAL, std::string(w) + "out rows must be 8-byte aligned");
+    if (p->n > 0) {
+        if (p->group <= 0 || p->group % 16) return fail(HYQ_EINVAL, std::string(w) + "group must be a positive multiple of 16");
+        if (!p->k_codes || !p->v_codes || !p->k_scale || !p->v_scale) return fail(HYQ_EINVAL, std::string(w) + "null prefix");
+        if (!aligned(p->k_codes, 16) || p->kc_stride_n % 16 || p->kc_stride_bh % 16 || p->kc_stride_n < 64 ||
+            p->kc_stride_n > 4096 || p->kc_stride_bh < 0)
+            return fail(HYQ_EINVAL, std::string(w) + "k_codes rows must be 16-byte aligned, row stride in [64, 4096]");
+        if (!aligned(p->v_codes, 4) || p->vc_stride_n % 4 || p->vc_stride_bh % 4 || p->vc_stride_n < 64 ||
+            p->vc_stride_n > 4096 || p->vc_stride_bh < 0)
+            return fail(HYQ_EINVAL, std::string(w) + "v_codes rows must be 4-byte aligned, row stride in [64, 4096]");
+        if (!aligned(p->k_scale, 16) || !aligned(p->v_scale, 16) || p->ks_stride_g % 8 || p->vs_stride_g % 8 ||
+            p->ks_stride_bh % 8 || p->vs_stride_bh % 8 || p->ks_stride_g < D || p->vs_stride_g < D ||
+            p->ks_stride_bh < 0 || p->vs_stride_bh < 0)
+            return fail(HYQ_EINVAL, std::string(w) + "scale rows must be 16-byte aligned (strides % 8 == 0)");
+        const int64_t rows = (p->n + p->group - 1) / p->group;
+        if (rows * std::max(p->ks_stride_g, p->vs_stride_g) * 2 > 0xffffffffLL)
+            return fail(HYQ_ENOTSUP, std::string(w) + "a head's scale rows span 4 GiB or more");
+    }
+    return HYQ_OK;
+}
+
+int launch_legacy(const hyq_legacy4_params* p, const LegPlan& pl, const Layout& L, void* workspace, void* stream) {
+    LegArgs a{};
+    a.q = p->q; a.q_stride = p->q_stride;
+    a.kc = p->k_codes; a.vc = p->v_codes;
+    a.kc_bh = p->kc_stride_bh; a.kc_n = p->kc_stride_n; a.vc_bh = p->vc_stride_bh; a.vc_n = p->vc_stride_n;
+    a.ks = p->k_scale; a.vs = p->v_scale;
+    a.ks_bh = p->ks_stride_bh; a.ks_g = p->ks_stride_g; a.vs_bh = p->vs_stride_bh; a.vs_g = p->vs_stride_g;
+    a.group = p->n > 0 ? p->group : 1;
+    a.ks_rows = a.vs_rows = (p->n + a.group - 1) / a.group;
+    a.n_leg = static_cast<int>(p->n);
+    for (int s = 0; s < 3; ++s) {
+        a.sk[s] = p->seg_k[s]; a.sv[s] = p->seg_v[s];
+        a.sk_bh[s] = p->seg_k_stride_bh[s]; a.sv_bh[s] = p->seg_v_stride_bh[s];
+        a.sn[s] = static_cast<int>(p->seg_n[s]);
+    }
+    a.G = p->kv_repeat;
+    a.qk_scale = p->sm_scale * LOG2E;
+    char* ws = static_cast<char*>(workspace);
+    a.cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
+    a.ml = reinterpret_cast<float*>(ws + L.ml);
+    a.part = reinterpret_cast<float*>(ws + L.part);
+    a.out = p->out; a.out_stride = p->out_stride;
+    a.nwg = pl.nwg;
+    a.mj = merge_batch(a.G, pl.nwg);
+    for (int s = 0; s < 5; ++s) a.pfirst[s] = pl.pfirst[s];
+    for (int s = 0; s < 4; ++s) a.plen[s] = pl.plen[s];
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    legacy_decode_kernel<<<dim3(static_cast<unsigned>(p->bh_kv), static_cast<unsigned>(pl.nwg)), dim3(THREADS),
+                           lds_bytes(a.G), st>>>(a);
+    return check_launch("hyq_decode_legacy4");
+}
+
 }  // namespace
 }  // namespace hyq
 
@@ -1688,4 +2055,23 @@ extern "C" int hyq_decode_bf16(const uint16_t* q, int64_t q_stride, uint16_t* ou
     p.bh_kv = bh_kv; p.kv_repeat = kv_repeat; p.head_dim = d; p.k_bits = 4; p.v_bits = 4;
     p.sm_scale = sm_scale;
     return hyq_decode_hybrid(&p, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t hyq_decode_legacy4_workspace_size(const hyq_legacy4_params* p) {
+    if (validate_legacy(p) != HYQ_OK || p->bh_kv == 0) return 0;
+    Plan dp{};
+    dp.nwg = legacy_plan(p).nwg;
+    return layout(dp, p->bh_kv, p->kv_repeat).total;
+}
+
+extern "C" int hyq_decode_legacy4(const hyq_legacy4_params* p, void* workspace, size_t ws_bytes, void* stream) {
+    int rc = validate_legacy(p);
+    if (rc != HYQ_OK || p->bh_kv == 0) return rc;
+    const LegPlan pl = legacy_plan(p);
+    Plan dp{};
+    dp.nwg = pl.nwg;
+    const Layout L = layout(dp, p->bh_kv, p->kv_repeat);
+    if (!workspace || ws_bytes < L.total || !aligned(workspace, 256))
+        return fail(HYQ_ENOSPC, "hyq_decode_legacy4: workspace too small or misaligned: need " + std::to_string(L.total) + " bytes");
+    return launch_legacy(p, pl, L, workspace, stream);
 }

@@ -135,6 +135,17 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return static_cast<uint16_t>(u >> 16);
 }
 
+// One element of the legacy decode format (src/ops/d_stage_cache.py:1019-1045,
+// :1063-1092) as bf16 bits: `twice` is twice the signed code value (2u - 16
+// for int4, 2u - 3 for int2), `sb` the fp16 bits of its scale.  The product
+// is formed in magnitude (exact in fp32), rounded once, and given the sign of
+// the code times the scale, so a zero code with a negative scale is -0.
+__device__ __forceinline__ uint32_t legacy_twice_to_bf16(int twice, uint32_t sb) {
+    const float mag = 0.5f * static_cast<float>(twice < 0 ? -twice : twice) *
+                      f16_bits_to_f32(static_cast<uint16_t>(sb & 0x7fffu));
+    return f32_to_bf16_rne(mag) | ((twice < 0 ? 0x8000u : 0u) ^ (sb & 0x8000u));
+}
+
 // two floats -> packed bf16 pair (RNE), low half = a
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));

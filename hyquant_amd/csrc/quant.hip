@@ -175,13 +175,7 @@ __global__ __launch_bounds__(256) void legacy_dequant_kernel(
     for (int j = 0; j < 4; ++j) {
         uint32_t h[2];
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int c = 2 * j + e;
-            const uint32_t sb = (sw[j] >> (16 * e)) & 0xffffu;
-            const float mag = 0.5f * static_cast<float>(twice[c] < 0 ? -twice[c] : twice[c]) *
-                              f16_bits_to_f32(static_cast<uint16_t>(sb & 0x7fffu));
-            h[e] = f32_to_bf16_rne(mag) | ((twice[c] < 0 ? 0x8000u : 0u) ^ (sb & 0x8000u));
-        }
+        for (int e = 0; e < 2; ++e) h[e] = legacy_twice_to_bf16(twice[2 * j + e], (sw[j] >> (16 * e)) & 0xffffu);
         o[j] = h[0] | (h[1] << 16);
     }
     reinterpret_cast<uint4*>(out + ib * os_bh + in * os_n)[sub] = make_uint4(o[0], o[1], o[2], o[3]);

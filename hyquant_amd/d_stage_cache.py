@@ -14,26 +14,31 @@ Drop-in for its entry points:
   per-token format, dequantised to the model dtype first, with one KV head
   per query head and a `[B, H, W, D]` window.
 
-All of them run here as the reference's legacy path A does
-(:1-8): the prefix is dequantised to bf16 by `hyq_legacy_dequant` (or
-`hyq_dequant` for the per-token format) into a buffer followed by the
-top-k rows, and the four segments go through the bf16 path of the fused
-decode kernel (`hyq_decode_hybrid` with no int4 prefix).  The operand
-roundings are those of the reference's MMA variant: K and V of the prefix
-rounded to bf16, P rounded to bf16 for the P.V product, fp32 accumulation.
+With 4-bit K and V codes, `hyq_decode_legacy4` reads the legacy prefix
+directly: each tile's codes and group scales are dequantised in registers to
+the bf16 values of `legacy_dequantize`, and the prefix and the three bf16
+segments go through one softmax.  With 2-bit codes, and for the per-token
+format, the prefix is dequantised to bf16 first (`hyq_legacy_dequant`, or
+`hyq_dequant`), as the reference's legacy path A does (:1-8), into a buffer
+followed by the top-k rows, and the segments go through the bf16 path of the
+fused decode kernel (`hyq_decode_hybrid` with no int4 prefix).  Either way the
+operand roundings are those of the reference's MMA variant: K and V of the
+prefix rounded to bf16, P rounded to bf16 for the P.V product, fp32
+accumulation.
 `split_size` / `block_kv` are the reference's tuning knobs and do not change
 the result; they are accepted and ignored.  The model dtype must be bf16.
 """
 
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
 
 from . import _lib
 from .decode_d_stage import (GROUP_SIZE, _decode, _inner_contig, _packed_dim, _require_gpu, _stream,
-                             dequantize_per_token)
+                             _workspace, dequantize_per_token)
 
 __all__ = [
     "legacy_dequantize",
@@ -105,7 +110,11 @@ def _legacy_decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, 
     if N_q > 0:
         assert k_quant_packed.shape[0] == BH_KV, f"K_packed[0]={k_quant_packed.shape[0]} vs BH_KV={BH_KV} mismatch"
     T = k_topk.shape[1] if _nonempty(k_topk) else 0
-    # [dequantised prefix | top-k rows] as the first bf16 segment
+    if k_bits == 4 and v_bits == 4 and D == 128:
+        return _legacy4_direct(q, k_quant_packed, v_quant_packed, k_scale, v_scale, N_q, BH_KV,
+                               [(k_topk, v_topk), (k_staging, v_staging), (k_window, v_window)],
+                               kv_repeat, sm_scale, what)
+    # 2-bit codes: [dequantised prefix | top-k rows] as the first bf16 segment
     kf = torch.empty(BH_KV, N_q + T, D, dtype=torch.bfloat16, device=q.device)
     vf = torch.empty_like(kf)
     if N_q > 0:
@@ -123,6 +132,58 @@ def _legacy_decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, 
     none16 = torch.empty(BH_KV, 0, dtype=torch.float16, device=q.device)
     out = _decode(q.reshape(B * H_Q, D), none8, none8, none16, none16, kf, vf, ks, vs, kw, vw,
                   4, 4, kv_repeat, sm_scale, 0, None, None)
+    return out.view(B, H_Q, 1, D)
+
+
+def _legacy4_direct(q, kp, vp, ks, vs, N_q, BH_KV, segs, kv_repeat, sm_scale, what):
+    """4-bit K and V: hyq_decode_legacy4 reads the legacy codes and their
+    group scales directly (dequantised in registers to the bf16 values of
+    legacy_dequantize) together with the three bf16 segments, one softmax."""
+    B, H_Q, _, D = q.shape
+    L = _lib.lib()
+    qf = _inner_contig(q.reshape(B * H_Q, D))
+    out = torch.empty(B * H_Q, D, dtype=torch.bfloat16, device=q.device)
+    p = _lib.Legacy4Params()
+    p.q, p.q_stride = qf.data_ptr(), qf.stride(0)
+    p.out, p.out_stride = out.data_ptr(), out.stride(0)
+    keep = [qf]
+    if N_q > 0:
+        if kp.dtype not in (torch.uint8, torch.int8) or vp.dtype not in (torch.uint8, torch.int8):
+            raise ValueError(f"{what}: the packed prefix must be uint8 codes")
+        if ks.dtype != torch.float16 or vs.dtype != torch.float16:
+            raise ValueError(f"{what}: the prefix scales must be fp16")
+        if kp.shape[2] != D // 2 or vp.shape[2] != D // 2 or vp.shape[:2] != kp.shape[:2]:
+            raise ValueError(f"{what}: packed K and V must be [BH_KV, N_q, {D // 2}]")
+        groups = -(-N_q // GROUP_SIZE)
+        for name, sc in (("k_scale", ks), ("v_scale", vs)):
+            if sc.dim() != 3 or sc.shape[0] != BH_KV or sc.shape[2] != D or sc.shape[1] < groups:
+                raise ValueError(f"{what}: {name} must be [{BH_KV}, >= {groups}, {D}], got {tuple(sc.shape)}")
+        kp, vp, ks, vs = (_inner_contig(t) for t in (kp, vp, ks, vs))
+        keep += [kp, vp, ks, vs]
+        p.k_codes, p.kc_stride_bh, p.kc_stride_n = kp.data_ptr(), kp.stride(0), kp.stride(1)
+        p.v_codes, p.vc_stride_bh, p.vc_stride_n = vp.data_ptr(), vp.stride(0), vp.stride(1)
+        p.k_scale, p.ks_stride_bh, p.ks_stride_g = ks.data_ptr(), ks.stride(0), ks.stride(1)
+        p.v_scale, p.vs_stride_bh, p.vs_stride_g = vs.data_ptr(), vs.stride(0), vs.stride(1)
+        p.n, p.group = N_q, GROUP_SIZE
+    for i, (sk, sv) in enumerate(segs):
+        if not _nonempty(sk):
+            continue
+        if sk.dtype != torch.bfloat16 or sv.dtype != torch.bfloat16 or sk.shape != sv.shape:
+            raise ValueError(f"{what}: segment {i} must be bf16 K and V of one shape")
+        if sk.shape[0] != BH_KV or sk.shape[2] != D:
+            raise ValueError(f"{what}: segment {i} must be [{BH_KV}, n, {D}], got {tuple(sk.shape)}")
+        sk, sv = _inner_contig(sk), _inner_contig(sv)
+        keep += [sk, sv]
+        p.seg_k[i], p.seg_k_stride_bh[i] = sk.data_ptr(), sk.stride(0)
+        p.seg_v[i], p.seg_v_stride_bh[i] = sv.data_ptr(), sv.stride(0)
+        p.seg_n[i] = sk.shape[1]
+    p.bh_kv, p.kv_repeat, p.head_dim = BH_KV, kv_repeat, D
+    p.sm_scale = D ** -0.5 if sm_scale is None else float(sm_scale)
+    stream = _stream(q.device)
+    need = L.hyq_decode_legacy4_workspace_size(ctypes.byref(p))
+    ws = _workspace(q.device, stream, max(need, 1))
+    st = L.hyq_decode_legacy4(ctypes.byref(p), ws.data_ptr(), ws.numel(), stream)
+    _lib.check(st, what)
     return out.view(B, H_Q, 1, D)
 
 

@@ -54,6 +54,7 @@ def _check(name, out, ref, ref_abs):
 
 @pytest.mark.parametrize("entry,kb,vb,R", [
     ("fused", 4, 4, 4), ("splitk", 4, 4, 4), ("mma", 4, 4, 4), ("mma", 4, 2, 8), ("mma", 2, 4, 1), ("mma", 2, 2, 4),
+    ("fused", 4, 4, 1), ("mma", 4, 4, 8), ("mma", 4, 4, 16),
 ])
 def test_legacy_decode_vs_oracle(entry, kb, vb, R):
     import hyquant_amd.d_stage_cache as L
@@ -84,6 +85,63 @@ def test_legacy_decode_vs_oracle(entry, kb, vb, R):
     # and close to the unrounded legacy math (the FFMA variants' fp32 operands)
     exact = O.legacy_decode_fp64(*oargs, k_bits=kb, v_bits=vb, kv_repeat=R)
     assert np.abs(out.float().cpu().numpy().reshape(exact.shape) - exact).max() <= 4 * ATOL
+
+
+def test_legacy4_direct_long_prefix():
+    """A 140000-token legacy prefix through the direct 4-bit path (the codes
+    read in the decode, no bf16 copy): the pieces are doubled until they fit
+    the merge tables, and the result stays within the bound of the fp64
+    restatement."""
+    import hyquant_amd.d_stage_cache as L
+    print("legacy direct long prefix", flush=True)
+    rng = np.random.default_rng(140)
+    BHK, R, N, D, T, S, W = 1, 4, 140000, 128, 300, 17, 64
+    kp, ks = _legacy_inputs(rng, BHK, N, D, 4)
+    vp, vs = _legacy_inputs(rng, BHK, N, D, 4)
+    f = lambda n: O.bf16_round(rng.standard_normal((BHK, n, D)).astype(np.float32))
+    kt, vt, kst, vst, kw, vw = f(T), f(T), f(S), f(S), f(W), f(W)
+    q = O.bf16_round(rng.standard_normal((BHK * R, D)).astype(np.float32))
+    d = lambda a: to_dev_bf16(a, "cuda")
+    u = lambda a: torch.from_numpy(a).cuda()
+    out = L.fused_decode_attention_k4v4(d(q).view(1, BHK * R, 1, D), u(kp), u(vp), u(ks), u(vs), d(kt), d(vt),
+                                        d(kst), d(vst), d(kw), d(vw), kv_repeat=R)
+    oargs = (q, kp, vp, ks, vs, kt, vt, kst, vst, kw, vw)
+    ref = O.legacy_decode_fp64(*oargs, kv_repeat=R, bf16_operands=True)
+    ref_abs = O.legacy_decode_fp64(*oargs, kv_repeat=R, bf16_operands=True, abs_v=True)
+    _check("direct long prefix", out, ref, ref_abs)
+
+
+def test_legacy4_direct_matches_dequantise_first():
+    """The direct 4-bit path dequantises each tile in registers to the bf16
+    values legacy_dequantize writes; decoding those bf16 rows through the
+    hybrid kernel's bf16 path gives the same attention up to the order of the
+    split-K sums (here within 2^-10 of the output scale)."""
+    import hyquant_amd.d_stage_cache as L
+    from hyquant_amd.decode_d_stage import _decode
+    print("legacy direct vs dequantise-first", flush=True)
+    rng = np.random.default_rng(404)
+    BHK, R, N, D, T, S, W = 4, 4, 3000, 128, 150, 9, 64
+    kp, ks = _legacy_inputs(rng, BHK, N, D, 4)
+    vp, vs = _legacy_inputs(rng, BHK, N, D, 4)
+    f = lambda n: O.bf16_round(rng.standard_normal((BHK, n, D)).astype(np.float32))
+    kt, vt, kst, vst, kw, vw = f(T), f(T), f(S), f(S), f(W), f(W)
+    q = O.bf16_round(rng.standard_normal((BHK * R, D)).astype(np.float32))
+    d = lambda a: to_dev_bf16(a, "cuda")
+    u = lambda a: torch.from_numpy(a).cuda()
+    direct = L.fused_decode_attention_k4v4(d(q).view(1, BHK * R, 1, D), u(kp), u(vp), u(ks), u(vs), d(kt), d(vt),
+                                           d(kst), d(vst), d(kw), d(vw), kv_repeat=R)
+    kf = torch.empty(BHK, N + T, D, dtype=torch.bfloat16, device="cuda")
+    vf = torch.empty_like(kf)
+    L.legacy_dequantize(u(kp), u(ks), D, 4, out=kf[:, :N])
+    L.legacy_dequantize(u(vp), u(vs), D, 4, out=vf[:, :N])
+    kf[:, N:].copy_(d(kt))
+    vf[:, N:].copy_(d(vt))
+    none8 = torch.empty(BHK, 0, D // 2, dtype=torch.int8, device="cuda")
+    none16 = torch.empty(BHK, 0, dtype=torch.float16, device="cuda")
+    first = _decode(d(q), none8, none8, none16, none16, kf, vf, d(kst), d(vst), d(kw), d(vw), 4, 4, R, None, 0,
+                    None, None)
+    a, b = direct.float().reshape(BHK * R, D), first.float()
+    assert (a - b).abs().max().item() <= 2.0 ** -10 * max(1.0, b.abs().max().item())
 
 
 def test_legacy_decode_config1_shape():

@@ -237,3 +237,33 @@ def test_legacy_entry_points_reject_bad_arguments():
         L.splitk_decode_attention_k4v4_mma(q, kp, kp, ks, ks, eb, eb, eb, eb, w, w, kv_repeat=4, k_bits=8)
     with pytest.raises(ValueError):       # too few scale groups for the prefix
         L.legacy_dequantize(torch.zeros(1, 200, D // 2, dtype=torch.uint8, device="cuda"), ks, D, 4)
+
+
+def test_legacy4_direct_every_code_and_scale():
+    """The direct path's in-register dequantisation against the oracle for
+    every 4-bit code with every finite fp16 scale.  Each head holds a one-token
+    prefix and no bf16 rows, so its softmax weight is exactly 1 and its output
+    row is the dequantised V row: 7936 heads x 128 channels carry the 16 x
+    63488 (code, scale) pairs.  Zeros are compared without their sign (the
+    product with P = 1 accumulates onto +0)."""
+    import hyquant_amd.d_stage_cache as L
+    print("legacy direct: every code and finite fp16 scale", flush=True)
+    D = 128
+    b = np.arange(65536, dtype=np.uint32)
+    fin = b[((b >> 10) & 0x1F) != 0x1F].astype(np.uint16)          # 63488 finite fp16
+    BHK = fin.size * 16 // D
+    p = np.arange(BHK * D).reshape(BHK, D)
+    code = (p % 16).astype(np.uint8)
+    vs = fin[p // 16].reshape(BHK, 1, D).view(np.float16)
+    vp = ((code[:, 0::2] << 4) | code[:, 1::2]).reshape(BHK, 1, D // 2)
+    rng = np.random.default_rng(9)
+    kp = rng.integers(0, 256, (BHK, 1, D // 2), dtype=np.uint8)
+    ks = np.ones((BHK, 1, D), np.float16)
+    q = O.bf16_round(rng.standard_normal((BHK, D)).astype(np.float32))
+    eb = torch.empty(BHK, 0, D, dtype=torch.bfloat16, device="cuda")
+    u = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    out = L.fused_decode_attention_k4v4(to_dev_bf16(q, "cuda").view(1, BHK, 1, D), u(kp), u(vp), u(ks), u(vs),
+                                        eb, eb, eb, eb, eb, eb, kv_repeat=1)
+    got = out.view(BHK, D).view(torch.int16).cpu().numpy().view(np.uint16)
+    exp = O.legacy_dequant_bf16(vp, vs, 4)[:, 0, :]
+    assert np.array_equal(np.where(got == 0x8000, 0, got), np.where(exp == 0x8000, 0, exp))

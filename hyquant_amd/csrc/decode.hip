@@ -1266,10 +1266,13 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
 // legacy_dequant_kernel (legacy_twice_to_bf16) and computed by the bf16 tile
 // path (bf16_compute): the result of dequantising the prefix and decoding
 // bf16 rows, without the bf16 copy in HBM.  One workgroup per piece
-// (LEG_PIECE prefix tokens or BF_PIECE rows of one segment, doubled for long
-// caches until the pieces fit the merge tables), merged by the head's last
-// arriving workgroup with decode_kernel's protocol and merge.
+// (LEG_PIECE prefix tokens or BF_PIECE rows of one segment, the same number
+// of bytes; doubled together while the prefix still gives every resident
+// workgroup slot a piece, up to LEG_PIECE_MAX tokens, and for long caches
+// until the pieces fit the merge tables), merged by the head's last arriving
+// workgroup with decode_kernel's protocol and merge.
 constexpr int LEG_PIECE = 512;
+constexpr int LEG_PIECE_MAX = 4096;
 constexpr int BF_PIECE = 128;
 
 struct LegArgs {
@@ -1333,36 +1336,73 @@ __device__ __forceinline__ void legacy_fetch(LegRaw& r, const LegArgs& a, Rsrc r
     r.vsc = bld128(rvs, static_cast<uint32_t>(16 * c), svs);
 }
 
-// Byte d of wx (four code bytes with every nibble XOR 8, so a nibble read as a
-// signed 4-bit field is u - 8; channel 2j in the high nibble, 2j + 1 in the
-// low) and the pair's fp16 scales -> bf16 pair.  The float of u - 8 times the
-// scale is exact in fp32 and is rounded once by the packed conversion: for
-// every finite scale these are the bits of legacy_twice_to_bf16 (round to
-// nearest even is symmetric and the product's zeros carry the same signs;
-// checked for every code and every finite fp16 scale), in 3 operations per
-// element instead of about 14.
-// (__builtin_amdgcn_sbfe's result type is unsigned: it is cast to int before
-// the conversion, else the conversion is the unsigned one)
-__device__ __forceinline__ uint32_t leg4_pair(uint32_t wx, int d, uint32_t sw) {
-    const int hi = static_cast<int>(__builtin_amdgcn_sbfe(wx, 8 * d + 4, 4));
-    const int lo = static_cast<int>(__builtin_amdgcn_sbfe(wx, 8 * d, 4));
-    const float a = static_cast<float>(hi) * f16_bits_to_f32(static_cast<uint16_t>(sw));
-    const float b = static_cast<float>(lo) * f16_bits_to_f32(static_cast<uint16_t>(sw >> 16));
-    return pack_bf16x2(a, b);
+// Codes -> bf16 operands at 1/16 of the dequantised values.  The code word
+// w has every nibble XOR 8, so a nibble read as a signed 4-bit field is
+// u - 8; channel 2j sits in the high nibble of byte j, 2j + 1 in the low one.
+// v_cvt_off_f32_i4 turns the low 4 bits of its operand (here byte B, picked
+// by SDWA, of w for the odd channel and of w >> 4 for the even one) into the
+// signed field divided by 16, so one instruction replaces a bit-field extract
+// and a conversion.  (u - 8) / 16 times an fp16 scale is exact in fp32 and is
+// rounded once by the packed bf16 conversion, which gives exactly 1/16 of
+// legacy_twice_to_bf16's bits (every such product is a normal float or zero,
+// so the power-of-two factor commutes with the rounding; the zeros keep their
+// signs).  The kernel multiplies the score scale by 16 for the prefix and its
+// P.V accumulators by 16 after it, both exact.
+template <int B>
+__device__ __forceinline__ float off4_byte(uint32_t w) {
+    float r;
+    if constexpr (B == 0)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+    else if constexpr (B == 1)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+    else if constexpr (B == 2)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+    else
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+    return r;
+}
+// x times the fp16 in the low (HI = false) or high half of sw, converted
+// inside v_fma_mix_f32; the addend is neg(0) = -0 so that x * s + a is the
+// product itself, zeros with their signs
+template <bool HI>
+__device__ __forceinline__ float mul_f16_half(float x, uint32_t sw) {
+    float r;
+    if constexpr (HI)
+        asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(x), "v"(sw));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel:[0,0,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(x), "v"(sw));
+    return r;
+}
+// K: byte B's two channels, each with its own fp16 scale (the halves of sw)
+template <int B>
+__device__ __forceinline__ uint32_t leg4_pair_k(uint32_t w, uint32_t wsh, uint32_t sw) {
+    return pack_bf16x2(mul_f16_half<false>(off4_byte<B>(wsh), sw), mul_f16_half<true>(off4_byte<B>(w), sw));
+}
+// V: the lane's eight channel scales are shared by its four code words, so
+// they are converted once and multiplied in fp32
+template <int B>
+__device__ __forceinline__ uint32_t leg4_pair_v(uint32_t w, uint32_t wsh, const float (&s)[8]) {
+    return pack_bf16x2(off4_byte<B>(wsh) * s[2 * B], off4_byte<B>(w) * s[2 * B + 1]);
 }
 
 __device__ __forceinline__ void legacy_dequant(Bf16Raw& b, const LegRaw& r) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t w = r.kc[i] ^ 0x88888888u;
-        b.k[i] = u32x4{leg4_pair(w, 0, r.ksc[i][0]), leg4_pair(w, 1, r.ksc[i][1]), leg4_pair(w, 2, r.ksc[i][2]),
-                       leg4_pair(w, 3, r.ksc[i][3])};
+        const uint32_t w = r.kc[i] ^ 0x88888888u, wsh = w >> 4;
+        b.k[i] = u32x4{leg4_pair_k<0>(w, wsh, r.ksc[i][0]), leg4_pair_k<1>(w, wsh, r.ksc[i][1]),
+                       leg4_pair_k<2>(w, wsh, r.ksc[i][2]), leg4_pair_k<3>(w, wsh, r.ksc[i][3])};
+    }
+    float vs[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        vs[2 * j] = f16_bits_to_f32(static_cast<uint16_t>(r.vsc[j]));
+        vs[2 * j + 1] = f16_bits_to_f32(static_cast<uint16_t>(r.vsc[j] >> 16));
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const uint32_t w = r.vc[e] ^ 0x88888888u;
-        b.v[e] = u32x4{leg4_pair(w, 0, r.vsc[0]), leg4_pair(w, 1, r.vsc[1]), leg4_pair(w, 2, r.vsc[2]),
-                       leg4_pair(w, 3, r.vsc[3])};
+        const uint32_t w = r.vc[e] ^ 0x88888888u, wsh = w >> 4;
+        b.v[e] = u32x4{leg4_pair_v<0>(w, wsh, vs), leg4_pair_v<1>(w, wsh, vs), leg4_pair_v<2>(w, wsh, vs),
+                       leg4_pair_v<3>(w, wsh, vs)};
     }
 }
 
@@ -1421,19 +1461,22 @@ __global__ __launch_bounds__(THREADS, 2) void legacy_decode_kernel(LegArgs a) {
         const uint32_t vco = static_cast<uint32_t>(4 * kb * a.vc_n + 4 * c);
         LegRaw r0, r1;
         Bf16Raw b;
+        const float qk16 = 16.f * a.qk_scale;       // the operands are 1/16 of the values
         legacy_fetch(r0, a, rkc, rvc, rks, rvs, kco, vco, lo, t0, lane);
         legacy_fetch(r1, a, rkc, rvc, rks, rvs, kco, vco, lo, t0 + TSTRIDE, lane);
         for (int i = 0; i < nmine; i += 2) {
             const int t = t0 + i * TSTRIDE;
             legacy_dequant(b, r0);
-            bf16_compute(st, b, qb, n - t, lane, a.qk_scale);
+            bf16_compute(st, b, qb, n - t, lane, qk16);
             if (i + 1 >= nmine) break;
             legacy_fetch(r0, a, rkc, rvc, rks, rvs, kco, vco, lo, t + 2 * TSTRIDE, lane);
             legacy_dequant(b, r1);
-            bf16_compute(st, b, qb, n - t - TSTRIDE, lane, a.qk_scale);
+            bf16_compute(st, b, qb, n - t - TSTRIDE, lane, qk16);
             if (i + 2 >= nmine) break;
             legacy_fetch(r1, a, rkc, rvc, rks, rvs, kco, vco, lo, t + 3 * TSTRIDE, lane);
         }
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) st.acc[nb] *= 16.f;
     } else {
         const int s3 = sg - 1;
         const uint16_t* kbase = a.sk[s3] + head * a.sk_bh[s3] + static_cast<int64_t>(lo) * BROW;
@@ -1780,9 +1823,38 @@ struct LegPlan {
     int pfirst[5] = {0, 0, 0, 0, 0};
     int plen[4] = {LEG_PIECE, BF_PIECE, BF_PIECE, BF_PIECE};
 };
+// Workgroups of legacy_decode_kernel the device holds at once (0: unknown),
+// cached per device and GQA width (the LDS size).
+int legacy_slots(int G) {
+    static std::atomic<int> cache[64][17];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || G < 1 || G > 16) return 0;
+    const int known = cache[dev][G].load(std::memory_order_relaxed);
+    if (known > 0) return known;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&legacy_decode_kernel),
+                                                     THREADS, lds_bytes(G)) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    cache[dev][G].store(per_cu * cus, std::memory_order_relaxed);
+    return per_cu * cus;
+}
+
+// Pieces grow while the prefix alone would still hand every resident slot a
+// piece after the doubling: a piece carries a fixed cost (the Q load, the
+// partial store, the arrival and merge), and a 512-token piece is only four
+// two-tile iterations per wave.  Measured on one MI355X (128 key heads,
+// 31000 tokens): 209 us with 512-token pieces, 187 us with 1024, 176 us with
+// 2048; with 8 key heads 2048-token pieces left most CUs idle (33 us against
+// 23 us).
 LegPlan legacy_plan(const hyq_legacy4_params* p) {
     LegPlan pl;
     const int64_t n[4] = {p->n, p->seg_n[0], p->seg_n[1], p->seg_n[2]};
+    const int sl = legacy_slots(p->kv_repeat);
+    const int64_t slots = sl > 0 ? sl : 512;
+    while (pl.plen[0] < LEG_PIECE_MAX &&
+           static_cast<int64_t>(p->bh_kv) * ((n[0] + 2 * pl.plen[0] - 1) / (2 * pl.plen[0])) >= slots)
+        for (int s = 0; s < 4; ++s) pl.plen[s] *= 2;
     for (;;) {
         int64_t total = 0;
         for (int s = 0; s < 4; ++s) total += (n[s] + pl.plen[s] - 1) / pl.plen[s];

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("HYQ_LIBRARY") or os.path.join(HERE, "libhyq.so")
 
 # the hyq_abi_version() these bindings (struct layouts, argument lists) match
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 HYQ_DT_Q_FP16 = 1
 HYQ_DT_SEG_FP16 = 2
@@ -41,8 +41,8 @@ EXPORTS = (
     "hyq_decode_hybrid_noalloc",
     "hyq_decode_bf16_workspace_size",
     "hyq_decode_bf16",
-    "hyq_decode_legacy4_workspace_size",
-    "hyq_decode_legacy4",
+    "hyq_decode_legacy_workspace_size",
+    "hyq_decode_legacy",
     "hyq_vertical_select_workspace_size",
     "hyq_vertical_select",
     "hyq_freeze_workspace_size",
@@ -79,8 +79,8 @@ class DecodeParams(Structure):
     ]
 
 
-class Legacy4Params(Structure):
-    """Mirror of `hyq_legacy4_params` (include/hyq.h)."""
+class LegacyParams(Structure):
+    """Mirror of `hyq_legacy_params` (include/hyq.h)."""
     _fields_ = [
         ("q", c_void_p), ("q_stride", c_int64),
         ("out", c_void_p), ("out_stride", c_int64),
@@ -90,6 +90,7 @@ class Legacy4Params(Structure):
         ("v_scale", c_void_p), ("vs_stride_bh", c_int64), ("vs_stride_g", c_int64),
         ("n", c_int64),
         ("group", c_int32),
+        ("k_bits", c_int32), ("v_bits", c_int32),
         ("seg_k", c_void_p * 3), ("seg_k_stride_bh", c_int64 * 3),
         ("seg_v", c_void_p * 3), ("seg_v_stride_bh", c_int64 * 3),
         ("seg_n", c_int64 * 3),
@@ -145,10 +146,10 @@ def _declare(lib):
                                     c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64,
                                     c_int64, c_int32, c_int32, c_int32, c_float,
                                     c_void_p, c_size_t, c_void_p]
-    lib.hyq_decode_legacy4_workspace_size.restype = c_size_t
-    lib.hyq_decode_legacy4_workspace_size.argtypes = [POINTER(Legacy4Params)]
-    lib.hyq_decode_legacy4.restype = c_int
-    lib.hyq_decode_legacy4.argtypes = [POINTER(Legacy4Params), c_void_p, c_size_t, c_void_p]
+    lib.hyq_decode_legacy_workspace_size.restype = c_size_t
+    lib.hyq_decode_legacy_workspace_size.argtypes = [POINTER(LegacyParams)]
+    lib.hyq_decode_legacy.restype = c_int
+    lib.hyq_decode_legacy.argtypes = [POINTER(LegacyParams), c_void_p, c_size_t, c_void_p]
     lib.hyq_vertical_select_workspace_size.restype = c_size_t
     lib.hyq_vertical_select_workspace_size.argtypes = [c_int32, c_int32, c_int64, c_int32]
     lib.hyq_vertical_select.restype = c_int

@@ -1259,13 +1259,15 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
 // ---------------------------------------------------------------------------
 // The legacy decode format of src/ops/d_stage_cache.py (fused_decode_
 // attention_k4v4 :504-591, splitk_decode_attention_k4v4 :825-951 and its MMA
-// variant :1247-1366): an int4 prefix of offset-encoded codes (channel 2j in
-// the high nibble of byte j, value u - 8) with one fp16 scale per (group of
-// tokens, channel), then the top-k, staging and window bf16 rows.  The
-// prefix tiles are dequantised in registers to the bf16 values of
-// legacy_dequant_kernel (legacy_twice_to_bf16) and computed by the bf16 tile
-// path (bf16_compute): the result of dequantising the prefix and decoding
-// bf16 rows, without the bf16 copy in HBM.  One workgroup per piece
+// variant :1247-1366 with K_BITS / V_BITS of 4 or 2, :977-1092): a prefix of
+// offset-encoded codes (int4: channel 2j in the high nibble of byte j, value
+// u - 8; int2: channel 4j + i in bits 7-2i..6-2i of byte j, value u - 1.5)
+// with one fp16 scale per (group of tokens, channel), then the top-k,
+// staging and window bf16 rows.  The prefix tiles are dequantised in
+// registers to the bf16 values of legacy_dequant_kernel (legacy_twice_to_bf16)
+// scaled by an exact power of two, and computed by the bf16 tile path
+// (bf16_compute): the result of dequantising the prefix and decoding bf16
+// rows, without the bf16 copy in HBM.  One workgroup per piece
 // (LEG_PIECE prefix tokens or BF_PIECE rows of one segment, the same number
 // of bytes; doubled together while the prefix still gives every resident
 // workgroup slot a piece, up to LEG_PIECE_MAX tokens, and for long caches
@@ -1278,7 +1280,7 @@ constexpr int BF_PIECE = 128;
 struct LegArgs {
     const uint16_t* q;
     int64_t q_stride;
-    const uint8_t* kc;             // prefix codes [bh][n][64] (byte strides)
+    const uint8_t* kc;             // prefix codes [bh][n][16 * bits] (byte strides)
     const uint8_t* vc;
     int64_t kc_bh, kc_n, vc_bh, vc_n;
     const uint16_t* ks;            // prefix scales [bh][groups][D] (element strides)
@@ -1305,10 +1307,11 @@ struct LegArgs {
 // the raw loads of one 16-token prefix tile, for the layout of Bf16Raw (the
 // group is a multiple of 16 and pieces start on group boundaries, so the
 // tile's tokens share one scale row)
+template <int KB, int VB>
 struct LegRaw {
-    u32x4 kc;                      // token c: codes of channels 32kb .. 32kb + 31 (byte j: 2j high, 2j + 1 low)
+    uint32_t kc[KB];               // token c: codes of channels 32kb .. 32kb + 31 (4 KB bytes)
     u32x4 ksc[4];                  // their fp16 scales, 8 channels per vector
-    uint32_t vc[4];                // slot e (token 4kb + e): codes of channels 8c .. 8c + 7
+    uint32_t vc[4];                // slot e (token 4kb + e): codes of channels 8c .. 8c + 7 (VB bytes, zero-extended)
     u32x4 vsc;                     // their fp16 scales
 };
 
@@ -1317,8 +1320,9 @@ struct LegRaw {
 // position goes in the scalar offsets.  The code descriptors cover the piece
 // and the scale descriptors the head's scale rows (the range check covers
 // the scalar offset too): tokens past either read zeros.
-__device__ __forceinline__ void legacy_fetch(LegRaw& r, const LegArgs& a, Rsrc rkc, Rsrc rvc, Rsrc rks, Rsrc rvs,
-                                             uint32_t kco, uint32_t vco, int lo, int t, int lane) {
+template <int KB, int VB>
+__device__ __forceinline__ void legacy_fetch(LegRaw<KB, VB>& r, const LegArgs& a, Rsrc rkc, Rsrc rvc, Rsrc rks,
+                                             Rsrc rvs, uint32_t kco, uint32_t vco, int lo, int t, int lane) {
     const int c = lane & 15, kb = lane >> 4;
     // wave-uniform scalar offsets (left to the compiler, some became vector
     // values and their loads were wrapped in waterfall loops)
@@ -1328,26 +1332,38 @@ __device__ __forceinline__ void legacy_fetch(LegRaw& r, const LegArgs& a, Rsrc r
     const uint32_t sks = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(g * a.ks_g * 2));
     const uint32_t svc = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tu * a.vc_n));
     const uint32_t svs = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(g * a.vs_g * 2));
-    r.kc = bld128(rkc, kco, skc);
+    if constexpr (KB == 4) {
+        const u32x4 w = bld128(rkc, kco, skc);
+        r.kc[0] = w[0]; r.kc[1] = w[1]; r.kc[2] = w[2]; r.kc[3] = w[3];
+    } else {
+        const u32x2 w = bld64(rkc, kco, skc);
+        r.kc[0] = w[0]; r.kc[1] = w[1];
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.ksc[i] = bld128(rks, static_cast<uint32_t>(64 * kb + 16 * i), sks);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r.vc[e] = bld32(rvc, vco + static_cast<uint32_t>(e * a.vc_n), svc);
+    for (int e = 0; e < 4; ++e)
+        r.vc[e] = VB == 4 ? bld32(rvc, vco + static_cast<uint32_t>(e * a.vc_n), svc)
+                          : bld16(rvc, vco + static_cast<uint32_t>(e * a.vc_n), svc);
     r.vsc = bld128(rvs, static_cast<uint32_t>(16 * c), svs);
 }
 
-// Codes -> bf16 operands at 1/16 of the dequantised values.  The code word
-// w has every nibble XOR 8, so a nibble read as a signed 4-bit field is
-// u - 8; channel 2j sits in the high nibble of byte j, 2j + 1 in the low one.
-// v_cvt_off_f32_i4 turns the low 4 bits of its operand (here byte B, picked
-// by SDWA, of w for the odd channel and of w >> 4 for the even one) into the
-// signed field divided by 16, so one instruction replaces a bit-field extract
-// and a conversion.  (u - 8) / 16 times an fp16 scale is exact in fp32 and is
-// rounded once by the packed bf16 conversion, which gives exactly 1/16 of
+// Codes -> bf16 operands at a power-of-two fraction of the dequantised
+// values.  v_cvt_off_f32_i4 turns the low 4 bits of its operand (byte B of
+// the word, picked by SDWA) into that signed 4-bit field divided by 16, so
+// one instruction replaces a bit-field extract and a conversion.
+//   int4: the code word w has every nibble XOR 8, so a nibble read as a
+//     signed field is u - 8; channel 2j sits in the high nibble of byte j
+//     (read from w >> 4), 2j + 1 in the low one (read from w): (u - 8) / 16.
+//   int2: crumb m of every byte (bits 7-2m..6-2m, channel 4j + m) goes to
+//     the low bits of its byte, and 2u + 13 makes a nibble whose signed value
+//     is 2u - 3: (u - 1.5) / 8.
+// The value times an fp16 scale is exact in fp32 and is rounded once by the
+// packed bf16 conversion, which gives exactly 1/16 (int4) or 1/8 (int2) of
 // legacy_twice_to_bf16's bits (every such product is a normal float or zero,
 // so the power-of-two factor commutes with the rounding; the zeros keep their
-// signs).  The kernel multiplies the score scale by 16 for the prefix and its
-// P.V accumulators by 16 after it, both exact.
+// signs).  The kernel multiplies the score scale by 16 (8) for the prefix and
+// its P.V accumulators by 16 (8) after it, both exact.
 template <int B>
 __device__ __forceinline__ float off4_byte(uint32_t w) {
     float r;
@@ -1385,12 +1401,45 @@ __device__ __forceinline__ uint32_t leg4_pair_v(uint32_t w, uint32_t wsh, const 
     return pack_bf16x2(off4_byte<B>(wsh) * s[2 * B], off4_byte<B>(w) * s[2 * B + 1]);
 }
 
-__device__ __forceinline__ void legacy_dequant(Bf16Raw& b, const LegRaw& r) {
+// int2: crumb m of every byte of w as a nibble of value 2u - 3 in its byte
+template <int M>
+__device__ __forceinline__ uint32_t crumb_nibbles(uint32_t w) {
+    return (((w >> (6 - 2 * M)) & 0x03030303u) << 1) + 0x0d0d0d0du;
+}
+// K, int2: the pair (channels 4j + M, 4j + M + 1) of byte J, with the two
+// halves of the scale word sw
+template <int J, int M>
+__device__ __forceinline__ uint32_t leg2_pair_k(const uint32_t (&n)[4], uint32_t sw) {
+    return pack_bf16x2(mul_f16_half<false>(off4_byte<J>(n[M]), sw), mul_f16_half<true>(off4_byte<J>(n[M + 1]), sw));
+}
+template <int J, int M>
+__device__ __forceinline__ uint32_t leg2_pair_v(const uint32_t (&n)[4], const float (&s)[8]) {
+    return pack_bf16x2(off4_byte<J>(n[M]) * s[4 * J + M], off4_byte<J>(n[M + 1]) * s[4 * J + M + 1]);
+}
+
+template <int KB, int VB>
+__device__ __forceinline__ void legacy_dequant(Bf16Raw& b, const LegRaw<KB, VB>& r) {
+    if constexpr (KB == 4) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t w = r.kc[i] ^ 0x88888888u, wsh = w >> 4;
-        b.k[i] = u32x4{leg4_pair_k<0>(w, wsh, r.ksc[i][0]), leg4_pair_k<1>(w, wsh, r.ksc[i][1]),
-                       leg4_pair_k<2>(w, wsh, r.ksc[i][2]), leg4_pair_k<3>(w, wsh, r.ksc[i][3])};
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w = r.kc[i] ^ 0x88888888u, wsh = w >> 4;
+            b.k[i] = u32x4{leg4_pair_k<0>(w, wsh, r.ksc[i][0]), leg4_pair_k<1>(w, wsh, r.ksc[i][1]),
+                           leg4_pair_k<2>(w, wsh, r.ksc[i][2]), leg4_pair_k<3>(w, wsh, r.ksc[i][3])};
+        }
+    } else {
+        // word h holds channels 32kb + 16h .. + 15: operand 2h + 0 takes its
+        // bytes 0 and 1, operand 2h + 1 its bytes 2 and 3
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t n[4] = {crumb_nibbles<0>(r.kc[h]), crumb_nibbles<1>(r.kc[h]), crumb_nibbles<2>(r.kc[h]),
+                                   crumb_nibbles<3>(r.kc[h])};
+            const u32x4& s0 = r.ksc[2 * h];
+            const u32x4& s1 = r.ksc[2 * h + 1];
+            b.k[2 * h] = u32x4{leg2_pair_k<0, 0>(n, s0[0]), leg2_pair_k<0, 2>(n, s0[1]), leg2_pair_k<1, 0>(n, s0[2]),
+                               leg2_pair_k<1, 2>(n, s0[3])};
+            b.k[2 * h + 1] = u32x4{leg2_pair_k<2, 0>(n, s1[0]), leg2_pair_k<2, 2>(n, s1[1]),
+                                   leg2_pair_k<3, 0>(n, s1[2]), leg2_pair_k<3, 2>(n, s1[3])};
+        }
     }
     float vs[8];
 #pragma unroll
@@ -1400,12 +1449,20 @@ __device__ __forceinline__ void legacy_dequant(Bf16Raw& b, const LegRaw& r) {
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const uint32_t w = r.vc[e] ^ 0x88888888u, wsh = w >> 4;
-        b.v[e] = u32x4{leg4_pair_v<0>(w, wsh, vs), leg4_pair_v<1>(w, wsh, vs), leg4_pair_v<2>(w, wsh, vs),
-                       leg4_pair_v<3>(w, wsh, vs)};
+        if constexpr (VB == 4) {
+            const uint32_t w = r.vc[e] ^ 0x88888888u, wsh = w >> 4;
+            b.v[e] = u32x4{leg4_pair_v<0>(w, wsh, vs), leg4_pair_v<1>(w, wsh, vs), leg4_pair_v<2>(w, wsh, vs),
+                           leg4_pair_v<3>(w, wsh, vs)};
+        } else {
+            const uint32_t n[4] = {crumb_nibbles<0>(r.vc[e]), crumb_nibbles<1>(r.vc[e]), crumb_nibbles<2>(r.vc[e]),
+                                   crumb_nibbles<3>(r.vc[e])};
+            b.v[e] = u32x4{leg2_pair_v<0, 0>(n, vs), leg2_pair_v<0, 2>(n, vs), leg2_pair_v<1, 0>(n, vs),
+                           leg2_pair_v<1, 2>(n, vs)};
+        }
     }
 }
 
+template <int KB, int VB>
 __global__ __launch_bounds__(THREADS, 2) void legacy_decode_kernel(LegArgs a) {
 #ifdef HYQ_PHASE_TRACE
     uint64_t ph[TRACE_PH] = {};    // (the merge stamps; not stored by this kernel)
@@ -1457,11 +1514,12 @@ __global__ __launch_bounds__(THREADS, 2) void legacy_decode_kernel(LegArgs a) {
         const Rsrc rks = make_rsrc(a.ks + head * a.ks_bh, static_cast<uint32_t>(a.ks_rows * a.ks_g * 2));
         const Rsrc rvs = make_rsrc(a.vs + head * a.vs_bh, static_cast<uint32_t>(a.vs_rows * a.vs_g * 2));
         // tiles wave, wave+WAVES, ... through a two-deep register ring
-        const uint32_t kco = static_cast<uint32_t>(c * a.kc_n + 16 * kb);
-        const uint32_t vco = static_cast<uint32_t>(4 * kb * a.vc_n + 4 * c);
-        LegRaw r0, r1;
+        const uint32_t kco = static_cast<uint32_t>(c * a.kc_n + 4 * KB * kb);
+        const uint32_t vco = static_cast<uint32_t>(4 * kb * a.vc_n + VB * c);
+        LegRaw<KB, VB> r0, r1;
         Bf16Raw b;
-        const float qk16 = 16.f * a.qk_scale;       // the operands are 1/16 of the values
+        constexpr float KF = KB == 4 ? 16.f : 8.f, VF = VB == 4 ? 16.f : 8.f;   // the operands are 1/KF, 1/VF of the values
+        const float qk16 = KF * a.qk_scale;
         legacy_fetch(r0, a, rkc, rvc, rks, rvs, kco, vco, lo, t0, lane);
         legacy_fetch(r1, a, rkc, rvc, rks, rvs, kco, vco, lo, t0 + TSTRIDE, lane);
         for (int i = 0; i < nmine; i += 2) {
@@ -1476,7 +1534,7 @@ __global__ __launch_bounds__(THREADS, 2) void legacy_decode_kernel(LegArgs a) {
             legacy_fetch(r1, a, rkc, rvc, rks, rvs, kco, vco, lo, t + 3 * TSTRIDE, lane);
         }
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) st.acc[nb] *= 16.f;
+        for (int nb = 0; nb < 8; ++nb) st.acc[nb] *= VF;
     } else {
         const int s3 = sg - 1;
         const uint16_t* kbase = a.sk[s3] + head * a.sk_bh[s3] + static_cast<int64_t>(lo) * BROW;
@@ -1823,21 +1881,30 @@ struct LegPlan {
     int pfirst[5] = {0, 0, 0, 0, 0};
     int plen[4] = {LEG_PIECE, BF_PIECE, BF_PIECE, BF_PIECE};
 };
-// Workgroups of legacy_decode_kernel the device holds at once (0: unknown),
-// cached per device and GQA width (the LDS size).
-int legacy_slots(int G) {
+// Workgroups of legacy_decode_kernel<KB, VB> the device holds at once (0:
+// unknown), cached per device, variant and GQA width (the LDS size).
+template <int KB, int VB>
+int legacy_slots_of(int G) {
     static std::atomic<int> cache[64][17];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || G < 1 || G > 16) return 0;
     const int known = cache[dev][G].load(std::memory_order_relaxed);
     if (known > 0) return known;
     int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&legacy_decode_kernel),
-                                                     THREADS, lds_bytes(G)) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&legacy_decode_kernel<KB, VB>), THREADS, lds_bytes(G)) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return 0;
     cache[dev][G].store(per_cu * cus, std::memory_order_relaxed);
     return per_cu * cus;
+}
+int legacy_slots(int kb, int vb, int G) {
+    switch (10 * kb + vb) {
+        case 44: return legacy_slots_of<4, 4>(G);
+        case 42: return legacy_slots_of<4, 2>(G);
+        case 24: return legacy_slots_of<2, 4>(G);
+        default: return legacy_slots_of<2, 2>(G);
+    }
 }
 
 // Pieces grow while the prefix alone would still hand every resident slot a
@@ -1847,10 +1914,10 @@ int legacy_slots(int G) {
 // 31000 tokens): 209 us with 512-token pieces, 187 us with 1024, 176 us with
 // 2048; with 8 key heads 2048-token pieces left most CUs idle (33 us against
 // 23 us).
-LegPlan legacy_plan(const hyq_legacy4_params* p) {
+LegPlan legacy_plan(const hyq_legacy_params* p) {
     LegPlan pl;
     const int64_t n[4] = {p->n, p->seg_n[0], p->seg_n[1], p->seg_n[2]};
-    const int sl = legacy_slots(p->kv_repeat);
+    const int sl = legacy_slots(p->k_bits, p->v_bits, p->kv_repeat);
     const int64_t slots = sl > 0 ? sl : 512;
     while (pl.plen[0] < LEG_PIECE_MAX &&
            static_cast<int64_t>(p->bh_kv) * ((n[0] + 2 * pl.plen[0] - 1) / (2 * pl.plen[0])) >= slots)
@@ -1867,10 +1934,12 @@ LegPlan legacy_plan(const hyq_legacy4_params* p) {
     return pl;
 }
 
-int validate_legacy(const hyq_legacy4_params* p) {
-    const char* w = "hyq_decode_legacy4: ";
+int validate_legacy(const hyq_legacy_params* p) {
+    const char* w = "hyq_decode_legacy: ";
     if (!p) return fail(HYQ_EINVAL, std::string(w) + "null params");
     if (p->head_dim != D) return fail(HYQ_ENOTSUP, std::string(w) + "head_dim must be 128");
+    if ((p->k_bits != 2 && p->k_bits != 4) || (p->v_bits != 2 && p->v_bits != 4))
+        return fail(HYQ_ENOTSUP, std::string(w) + "k_bits and v_bits must be 2 or 4");
     if (p->kv_repeat < 1 || p->kv_repeat > 16) return fail(HYQ_ENOTSUP, std::string(w) + "kv_repeat must be in [1, 16]");
     if (p->bh_kv < 0 || p->bh_kv > CNT_CAP) return fail(HYQ_ENOTSUP, std::string(w) + "bh_kv out of range");
     if (p->bh_kv == 0) return HYQ_OK;
@@ -1895,12 +1964,17 @@ int validate_legacy(const hyq_legacy4_params* p) {
     if (p->n > 0) {
         if (p->group <= 0 || p->group % 16) return fail(HYQ_EINVAL, std::string(w) + "group must be a positive multiple of 16");
         if (!p->k_codes || !p->v_codes || !p->k_scale || !p->v_scale) return fail(HYQ_EINVAL, std::string(w) + "null prefix");
-        if (!aligned(p->k_codes, 16) || p->kc_stride_n % 16 || p->kc_stride_bh % 16 || p->kc_stride_n < 64 ||
+        // a K row is read as one 4*k_bits-byte load per lane, a V row as
+        // v_bits-byte loads: rows aligned to those sizes, at least 16*bits bytes
+        const int ka = 4 * p->k_bits, va = p->v_bits, krow = 16 * p->k_bits, vrow = 16 * p->v_bits;
+        if (!aligned(p->k_codes, ka) || p->kc_stride_n % ka || p->kc_stride_bh % ka || p->kc_stride_n < krow ||
             p->kc_stride_n > 4096 || p->kc_stride_bh < 0)
-            return fail(HYQ_EINVAL, std::string(w) + "k_codes rows must be 16-byte aligned, row stride in [64, 4096]");
-        if (!aligned(p->v_codes, 4) || p->vc_stride_n % 4 || p->vc_stride_bh % 4 || p->vc_stride_n < 64 ||
+            return fail(HYQ_EINVAL, std::string(w) + "k_codes rows must be " + std::to_string(ka) +
+                                        "-byte aligned, row stride in [" + std::to_string(krow) + ", 4096]");
+        if (!aligned(p->v_codes, va) || p->vc_stride_n % va || p->vc_stride_bh % va || p->vc_stride_n < vrow ||
             p->vc_stride_n > 4096 || p->vc_stride_bh < 0)
-            return fail(HYQ_EINVAL, std::string(w) + "v_codes rows must be 4-byte aligned, row stride in [64, 4096]");
+            return fail(HYQ_EINVAL, std::string(w) + "v_codes rows must be " + std::to_string(va) +
+                                        "-byte aligned, row stride in [" + std::to_string(vrow) + ", 4096]");
         if (!aligned(p->k_scale, 16) || !aligned(p->v_scale, 16) || p->ks_stride_g % 8 || p->vs_stride_g % 8 ||
             p->ks_stride_bh % 8 || p->vs_stride_bh % 8 || p->ks_stride_g < D || p->vs_stride_g < D ||
             p->ks_stride_bh < 0 || p->vs_stride_bh < 0)
@@ -1912,7 +1986,7 @@ int validate_legacy(const hyq_legacy4_params* p) {
     return HYQ_OK;
 }
 
-int launch_legacy(const hyq_legacy4_params* p, const LegPlan& pl, const Layout& L, void* workspace, void* stream) {
+int launch_legacy(const hyq_legacy_params* p, const LegPlan& pl, const Layout& L, void* workspace, void* stream) {
     LegArgs a{};
     a.q = p->q; a.q_stride = p->q_stride;
     a.kc = p->k_codes; a.vc = p->v_codes;
@@ -1939,9 +2013,15 @@ int launch_legacy(const hyq_legacy4_params* p, const LegPlan& pl, const Layout& 
     for (int s = 0; s < 5; ++s) a.pfirst[s] = pl.pfirst[s];
     for (int s = 0; s < 4; ++s) a.plen[s] = pl.plen[s];
     hipStream_t st = static_cast<hipStream_t>(stream);
-    legacy_decode_kernel<<<dim3(static_cast<unsigned>(p->bh_kv), static_cast<unsigned>(pl.nwg)), dim3(THREADS),
-                           lds_bytes(a.G), st>>>(a);
-    return check_launch("hyq_decode_legacy4");
+    const dim3 grid(static_cast<unsigned>(p->bh_kv), static_cast<unsigned>(pl.nwg));
+    const size_t lds = lds_bytes(a.G);
+    switch (10 * p->k_bits + p->v_bits) {
+        case 44: legacy_decode_kernel<4, 4><<<grid, dim3(THREADS), lds, st>>>(a); break;
+        case 42: legacy_decode_kernel<4, 2><<<grid, dim3(THREADS), lds, st>>>(a); break;
+        case 24: legacy_decode_kernel<2, 4><<<grid, dim3(THREADS), lds, st>>>(a); break;
+        default: legacy_decode_kernel<2, 2><<<grid, dim3(THREADS), lds, st>>>(a); break;
+    }
+    return check_launch("hyq_decode_legacy");
 }
 
 }  // namespace
@@ -2129,14 +2209,14 @@ extern "C" int hyq_decode_bf16(const uint16_t* q, int64_t q_stride, uint16_t* ou
     return hyq_decode_hybrid(&p, workspace, workspace_bytes, stream);
 }
 
-extern "C" size_t hyq_decode_legacy4_workspace_size(const hyq_legacy4_params* p) {
+extern "C" size_t hyq_decode_legacy_workspace_size(const hyq_legacy_params* p) {
     if (validate_legacy(p) != HYQ_OK || p->bh_kv == 0) return 0;
     Plan dp{};
     dp.nwg = legacy_plan(p).nwg;
     return layout(dp, p->bh_kv, p->kv_repeat).total;
 }
 
-extern "C" int hyq_decode_legacy4(const hyq_legacy4_params* p, void* workspace, size_t ws_bytes, void* stream) {
+extern "C" int hyq_decode_legacy(const hyq_legacy_params* p, void* workspace, size_t ws_bytes, void* stream) {
     int rc = validate_legacy(p);
     if (rc != HYQ_OK || p->bh_kv == 0) return rc;
     const LegPlan pl = legacy_plan(p);
@@ -2144,6 +2224,6 @@ extern "C" int hyq_decode_legacy4(const hyq_legacy4_params* p, void* workspace, 
     dp.nwg = pl.nwg;
     const Layout L = layout(dp, p->bh_kv, p->kv_repeat);
     if (!workspace || ws_bytes < L.total || !aligned(workspace, 256))
-        return fail(HYQ_ENOSPC, "hyq_decode_legacy4: workspace too small or misaligned: need " + std::to_string(L.total) + " bytes");
+        return fail(HYQ_ENOSPC, "hyq_decode_legacy: workspace too small or misaligned: need " + std::to_string(L.total) + " bytes");
     return launch_legacy(p, pl, L, workspace, stream);
 }

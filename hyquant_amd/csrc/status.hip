@@ -23,4 +23,4 @@ const char* last_error_cstr() { return g_last_error.c_str(); }
 }  // namespace hyq
 
 extern "C" const char* hyq_last_error(void) { return hyq::last_error_cstr(); }
-extern "C" int hyq_abi_version(void) { return 6; }
+extern "C" int hyq_abi_version(void) { return 7; }

@@ -14,17 +14,15 @@ Drop-in for its entry points:
   per-token format, dequantised to the model dtype first, with one KV head
   per query head and a `[B, H, W, D]` window.
 
-With 4-bit K and V codes, `hyq_decode_legacy4` reads the legacy prefix
-directly: each tile's codes and group scales are dequantised in registers to
-the bf16 values of `legacy_dequantize`, and the prefix and the three bf16
-segments go through one softmax.  With 2-bit codes, and for the per-token
-format, the prefix is dequantised to bf16 first (`hyq_legacy_dequant`, or
-`hyq_dequant`), as the reference's legacy path A does (:1-8), into a buffer
-followed by the top-k rows, and the segments go through the bf16 path of the
-fused decode kernel (`hyq_decode_hybrid` with no int4 prefix).  Either way the
-operand roundings are those of the reference's MMA variant: K and V of the
-prefix rounded to bf16, P rounded to bf16 for the P.V product, fp32
-accumulation.
+`hyq_decode_legacy` reads the legacy prefix directly (K and V of 4 or 2
+bits, as the reference's MMA variant takes them, :977-1092): each tile's
+codes and group scales are dequantised in registers to the bf16 values of
+`legacy_dequantize`, and the prefix and the three bf16 segments go through
+one softmax.  For the per-token format the prefix is dequantised to the
+model dtype first (`hyq_dequant`), as the reference's legacy path A does
+(:1-8).  The operand roundings are those of the reference's MMA variant: K
+and V of the prefix rounded to bf16, P rounded to bf16 for the P.V product,
+fp32 accumulation.
 `split_size` / `block_kv` are the reference's tuning knobs and do not change
 the result; they are accepted and ignored.  The model dtype must be bf16.
 """
@@ -109,41 +107,24 @@ def _legacy_decode(q, k_quant_packed, v_quant_packed, k_scale, v_scale, k_topk, 
     N_q = k_quant_packed.shape[1] if k_quant_packed.numel() > 0 else 0
     if N_q > 0:
         assert k_quant_packed.shape[0] == BH_KV, f"K_packed[0]={k_quant_packed.shape[0]} vs BH_KV={BH_KV} mismatch"
-    T = k_topk.shape[1] if _nonempty(k_topk) else 0
-    if k_bits == 4 and v_bits == 4 and D == 128:
-        return _legacy4_direct(q, k_quant_packed, v_quant_packed, k_scale, v_scale, N_q, BH_KV,
-                               [(k_topk, v_topk), (k_staging, v_staging), (k_window, v_window)],
-                               kv_repeat, sm_scale, what)
-    # 2-bit codes: [dequantised prefix | top-k rows] as the first bf16 segment
-    kf = torch.empty(BH_KV, N_q + T, D, dtype=torch.bfloat16, device=q.device)
-    vf = torch.empty_like(kf)
-    if N_q > 0:
-        legacy_dequantize(k_quant_packed, k_scale, D, k_bits, out=kf[:, :N_q])
-        legacy_dequantize(v_quant_packed, v_scale, D, v_bits, out=vf[:, :N_q])
-    if T > 0:
-        kf[:, N_q:].copy_(k_topk)
-        vf[:, N_q:].copy_(v_topk)
-    e = _bf16_rows(BH_KV, D, q)
-    ks = k_staging if _nonempty(k_staging) else e
-    vs = v_staging if _nonempty(v_staging) else e
-    kw = k_window if _nonempty(k_window) else e
-    vw = v_window if _nonempty(v_window) else e
-    none8 = torch.empty(BH_KV, 0, D // 2, dtype=torch.int8, device=q.device)
-    none16 = torch.empty(BH_KV, 0, dtype=torch.float16, device=q.device)
-    out = _decode(q.reshape(B * H_Q, D), none8, none8, none16, none16, kf, vf, ks, vs, kw, vw,
-                  4, 4, kv_repeat, sm_scale, 0, None, None)
-    return out.view(B, H_Q, 1, D)
+    return _legacy_direct(q, k_quant_packed, v_quant_packed, k_scale, v_scale, N_q, BH_KV,
+                          [(k_topk, v_topk), (k_staging, v_staging), (k_window, v_window)],
+                          kv_repeat, k_bits, v_bits, sm_scale, what)
 
 
-def _legacy4_direct(q, kp, vp, ks, vs, N_q, BH_KV, segs, kv_repeat, sm_scale, what):
-    """4-bit K and V: hyq_decode_legacy4 reads the legacy codes and their
-    group scales directly (dequantised in registers to the bf16 values of
-    legacy_dequantize) together with the three bf16 segments, one softmax."""
+def _legacy_direct(q, kp, vp, ks, vs, N_q, BH_KV, segs, kv_repeat, k_bits, v_bits, sm_scale, what):
+    """hyq_decode_legacy reads the legacy codes (K and V of 4 or 2 bits) and
+    their group scales directly (dequantised in registers to the bf16 values
+    of legacy_dequantize) together with the three bf16 segments, one
+    softmax."""
     B, H_Q, _, D = q.shape
     L = _lib.lib()
     qf = _inner_contig(q.reshape(B * H_Q, D))
     out = torch.empty(B * H_Q, D, dtype=torch.bfloat16, device=q.device)
-    p = _lib.Legacy4Params()
+    if k_bits not in (2, 4) or v_bits not in (2, 4):
+        raise ValueError(f"{what}: k_bits and v_bits must be 2 or 4, got {k_bits}, {v_bits}")
+    p = _lib.LegacyParams()
+    p.k_bits, p.v_bits = k_bits, v_bits
     p.q, p.q_stride = qf.data_ptr(), qf.stride(0)
     p.out, p.out_stride = out.data_ptr(), out.stride(0)
     keep = [qf]
@@ -152,8 +133,9 @@ def _legacy4_direct(q, kp, vp, ks, vs, N_q, BH_KV, segs, kv_repeat, sm_scale, wh
             raise ValueError(f"{what}: the packed prefix must be uint8 codes")
         if ks.dtype != torch.float16 or vs.dtype != torch.float16:
             raise ValueError(f"{what}: the prefix scales must be fp16")
-        if kp.shape[2] != D // 2 or vp.shape[2] != D // 2 or vp.shape[:2] != kp.shape[:2]:
-            raise ValueError(f"{what}: packed K and V must be [BH_KV, N_q, {D // 2}]")
+        if kp.shape[2] != D * k_bits // 8 or vp.shape[2] != D * v_bits // 8 or vp.shape[:2] != kp.shape[:2]:
+            raise ValueError(f"{what}: packed K and V must be [BH_KV, N_q, D * bits / 8] "
+                             f"({D * k_bits // 8} and {D * v_bits // 8} bytes)")
         groups = -(-N_q // GROUP_SIZE)
         for name, sc in (("k_scale", ks), ("v_scale", vs)):
             if sc.dim() != 3 or sc.shape[0] != BH_KV or sc.shape[2] != D or sc.shape[1] < groups:
@@ -180,9 +162,9 @@ def _legacy4_direct(q, kp, vp, ks, vs, N_q, BH_KV, segs, kv_repeat, sm_scale, wh
     p.bh_kv, p.kv_repeat, p.head_dim = BH_KV, kv_repeat, D
     p.sm_scale = D ** -0.5 if sm_scale is None else float(sm_scale)
     stream = _stream(q.device)
-    need = L.hyq_decode_legacy4_workspace_size(ctypes.byref(p))
+    need = L.hyq_decode_legacy_workspace_size(ctypes.byref(p))
     ws = _workspace(q.device, stream, max(need, 1))
-    st = L.hyq_decode_legacy4(ctypes.byref(p), ws.data_ptr(), ws.numel(), stream)
+    st = L.hyq_decode_legacy(ctypes.byref(p), ws.data_ptr(), ws.numel(), stream)
     _lib.check(st, what)
     return out.view(B, H_Q, 1, D)
 

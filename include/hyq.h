@@ -163,24 +163,29 @@ int hyq_decode_hybrid(const hyq_decode_params* p, void* workspace,
 int hyq_decode_hybrid_noalloc(const hyq_decode_params* p, void* stream);
 
 /*
- * Decode over the legacy int4 format, reading the codes directly.  Replaces
+ * Decode over the legacy format, reading the codes directly.  Replaces
  * fused_decode_attention_k4v4 (src/ops/d_stage_cache.py:504-591),
  * splitk_decode_attention_k4v4 (:825-951) and
- * splitk_decode_attention_k4v4_mma (:1247-1366) for 4-bit K and V: the
- * prefix codes (offset-encoded, even channel in the HIGH nibble, value
- * u - 8) and their per-(group, channel) fp16 scales are dequantised in
- * registers to the bf16 values of hyq_legacy_dequant, and attention runs with
- * bf16 K/V and P operands and fp32 accumulation, over the prefix and three
- * bf16 segments (top-k, staging, window), one softmax.
+ * splitk_decode_attention_k4v4_mma (:1247-1366, K_BITS / V_BITS of 4 or 2):
+ * the prefix codes and their per-(group, channel) fp16 scales are
+ * dequantised in registers to the bf16 values of hyq_legacy_dequant (up to
+ * an exact power of two that the kernel compensates), and attention runs
+ * with bf16 K/V and P operands and fp32 accumulation, over the prefix and
+ * three bf16 segments (top-k, staging, window), one softmax.  Codes are
+ * offset-encoded: int4 has channel 2j in the HIGH nibble of byte j, value
+ * u - 8; int2 has channel 4j + i in bits 7-2i..6-2i of byte j, value u - 1.5.
  *   q, out    bf16 [bh_kv * kv_repeat, 128] (row strides)
- *   k_codes   uint8 [bh_kv, n, 64] strides (kc_stride_bh, kc_stride_n), rows 16-byte aligned
- *   v_codes   uint8 [bh_kv, n, 64] strides (vc_stride_bh, vc_stride_n), rows 4-byte aligned
+ *   k_codes   uint8 [bh_kv, n, 16 * k_bits] strides (kc_stride_bh, kc_stride_n),
+ *             rows 4 * k_bits-byte aligned
+ *   v_codes   uint8 [bh_kv, n, 16 * v_bits] strides (vc_stride_bh, vc_stride_n),
+ *             rows v_bits-byte aligned
  *   k_scale, v_scale fp16 [bh_kv, ceil(n / group), 128] strides (bh, g, 1), rows 16-byte aligned
  *   seg_k, seg_v bf16 [bh_kv, seg_n, 128] with contiguous 128-element rows
  *     (head strides seg_*_stride_bh), 16-byte aligned
- * Limits: head_dim 128, kv_repeat 1..16, n and each seg_n <= 2^24, code row
- * strides <= 4096 bytes, each head's scale rows under 4 GiB.  Workspace rules
- * as for hyq_decode_hybrid (size from hyq_decode_legacy4_workspace_size).
+ * Limits: head_dim 128, k_bits and v_bits 2 or 4, kv_repeat 1..16, n and
+ * each seg_n <= 2^24, code row strides <= 4096 bytes, group a positive
+ * multiple of 16, each head's scale rows under 4 GiB.  Workspace rules as for
+ * hyq_decode_hybrid (size from hyq_decode_legacy_workspace_size).
  */
 typedef struct {
     const uint16_t* q; int64_t q_stride;
@@ -191,15 +196,16 @@ typedef struct {
     const uint16_t* v_scale; int64_t vs_stride_bh, vs_stride_g;
     int64_t n;            /* prefix tokens                                       */
     int32_t group;        /* tokens per scale row (the reference's 128)          */
+    int32_t k_bits, v_bits; /* code widths: 2 or 4                               */
     const uint16_t* seg_k[3]; int64_t seg_k_stride_bh[3];
     const uint16_t* seg_v[3]; int64_t seg_v_stride_bh[3];
     int64_t seg_n[3];
     int32_t bh_kv, kv_repeat, head_dim;
     float sm_scale;
-} hyq_legacy4_params;
+} hyq_legacy_params;
 
-size_t hyq_decode_legacy4_workspace_size(const hyq_legacy4_params* p);
-int hyq_decode_legacy4(const hyq_legacy4_params* p, void* workspace, size_t workspace_bytes, void* stream);
+size_t hyq_decode_legacy_workspace_size(const hyq_legacy_params* p);
+int hyq_decode_legacy(const hyq_legacy_params* p, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Full-precision bf16 decode attention over one contiguous KV per head, the

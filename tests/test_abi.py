@@ -40,7 +40,7 @@ def _L():
 
 def test_abi_version_and_error_strings():
     _lib, L = _L()
-    assert L.hyq_abi_version() == _lib.ABI_VERSION == 6
+    assert L.hyq_abi_version() == _lib.ABI_VERSION == 7
     st = L.hyq_quant_pack(None, 0, 1, 1, 128, 0, 0, 3, None, 0, 0, None, 0, None)
     assert st == _lib.HYQ_EINVAL
     assert b"nbits must be 2, 4, or 8" in L.hyq_last_error()
@@ -220,14 +220,15 @@ def test_python_layer_rejects_cpu_tensors():
         hq.quantize_per_token(torch.zeros(1, 1, 128, dtype=torch.bfloat16), 5)
 
 
-def _legacy4_params(_lib, **kw):
-    p = _lib.Legacy4Params()
+def _legacy_params(_lib, **kw):
+    p = _lib.LegacyParams()
     p.q, p.q_stride, p.out, p.out_stride = 256, 128, 512, 128
     p.k_codes, p.kc_stride_bh, p.kc_stride_n = 4096, 1000 * 64, 64
     p.v_codes, p.vc_stride_bh, p.vc_stride_n = 8192, 1000 * 64, 64
     p.k_scale, p.ks_stride_bh, p.ks_stride_g = 16384, 8 * 128, 128
     p.v_scale, p.vs_stride_bh, p.vs_stride_g = 32768, 8 * 128, 128
     p.n, p.group = 1000, 128
+    p.k_bits = p.v_bits = 4
     p.seg_n[0] = 37
     p.seg_k[0], p.seg_v[0] = 65536, 131072
     p.seg_k_stride_bh[0] = p.seg_v_stride_bh[0] = 37 * 128
@@ -238,26 +239,39 @@ def _legacy4_params(_lib, **kw):
     return p
 
 
-def test_legacy4_host_validation():
-    """hyq_decode_legacy4's checks run on the host before any launch: a valid
+def test_legacy_host_validation():
+    """hyq_decode_legacy's checks run on the host before any launch: a valid
     parameter block gets a workspace size (arrival counters, then the (m, l)
     table and partials of 2 + 1 pieces per head); each invalid one gets size 0
-    and its status, and a valid call without a workspace is refused."""
+    and its status, and a valid call without a workspace is refused.  Code
+    rows are checked against the loads of their bit width: a 4*k_bits-byte K
+    load and v_bits-byte V loads per lane, rows of at least 16*bits bytes."""
     _lib, L = _L()
-    p = _legacy4_params(_lib)
-    need = L.hyq_decode_legacy4_workspace_size(p)
+    p = _legacy_params(_lib)
+    need = L.hyq_decode_legacy_workspace_size(p)
     assert need > 2 << 20
-    assert L.hyq_decode_legacy4(p, None, 0, None) == _lib.HYQ_ENOSPC
+    assert L.hyq_decode_legacy(p, None, 0, None) == _lib.HYQ_ENOSPC
+    # 2-bit rows: 32-byte strides, K rows 8-byte and V rows 2-byte aligned
+    for kw in (dict(k_bits=2, kc_stride_n=32, k_codes=4104), dict(v_bits=2, vc_stride_n=32, v_codes=8194),
+               dict(k_bits=2, v_bits=2, kc_stride_n=40, vc_stride_n=34)):
+        p = _legacy_params(_lib, **kw)
+        assert L.hyq_decode_legacy_workspace_size(p) > 0, kw
+        assert L.hyq_decode_legacy(p, None, 0, None) == _lib.HYQ_ENOSPC, kw
     bad = ((dict(head_dim=64), _lib.HYQ_ENOTSUP), (dict(kv_repeat=17), _lib.HYQ_ENOTSUP),
+           (dict(k_bits=3), _lib.HYQ_ENOTSUP), (dict(v_bits=8), _lib.HYQ_ENOTSUP),
            (dict(group=100), _lib.HYQ_EINVAL), (dict(kc_stride_n=48), _lib.HYQ_EINVAL),
            (dict(k_codes=4100), _lib.HYQ_EINVAL), (dict(v_codes=8194), _lib.HYQ_EINVAL),
+           (dict(k_bits=2, kc_stride_n=32, k_codes=4100), _lib.HYQ_EINVAL),
+           (dict(k_bits=2, kc_stride_n=24), _lib.HYQ_EINVAL),
+           (dict(v_bits=2, vc_stride_n=32, v_codes=8193), _lib.HYQ_EINVAL),
+           (dict(v_bits=2, vc_stride_n=30), _lib.HYQ_EINVAL),
            (dict(ks_stride_g=120), _lib.HYQ_EINVAL), (dict(q=258), _lib.HYQ_EINVAL),
            (dict(n=(1 << 24) + 1), _lib.HYQ_ENOTSUP), (dict(bh_kv=16385), _lib.HYQ_ENOTSUP))
     for kw, code in bad:
-        p = _legacy4_params(_lib, **kw)
-        assert L.hyq_decode_legacy4_workspace_size(p) == 0, kw
-        assert L.hyq_decode_legacy4(p, None, 0, None) == code, kw
-    p = _legacy4_params(_lib, n=0)
+        p = _legacy_params(_lib, **kw)
+        assert L.hyq_decode_legacy_workspace_size(p) == 0, kw
+        assert L.hyq_decode_legacy(p, None, 0, None) == code, kw
+    p = _legacy_params(_lib, n=0)
     p.seg_n[0] = 0
-    assert L.hyq_decode_legacy4(p, None, 0, None) == _lib.HYQ_EINVAL
+    assert L.hyq_decode_legacy(p, None, 0, None) == _lib.HYQ_EINVAL
     assert b"zero key tokens" in L.hyq_last_error()

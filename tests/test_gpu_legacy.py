@@ -87,53 +87,56 @@ def test_legacy_decode_vs_oracle(entry, kb, vb, R):
     assert np.abs(out.float().cpu().numpy().reshape(exact.shape) - exact).max() <= 4 * ATOL
 
 
-def test_legacy4_direct_long_prefix():
-    """A 140000-token legacy prefix through the direct 4-bit path (the codes
-    read in the decode, no bf16 copy): the pieces are doubled until they fit
-    the merge tables, and the result stays within the bound of the fp64
+@pytest.mark.parametrize("kb,vb", [(4, 4), (2, 2)])
+def test_legacy_direct_long_prefix(kb, vb):
+    """A 140000-token legacy prefix through the direct path (the codes read
+    in the decode, no bf16 copy): the pieces are doubled until they fit the
+    merge tables, and the result stays within the bound of the fp64
     restatement."""
     import hyquant_amd.d_stage_cache as L
-    print("legacy direct long prefix", flush=True)
-    rng = np.random.default_rng(140)
+    print(f"legacy direct long prefix K{kb}V{vb}", flush=True)
+    rng = np.random.default_rng(140 + kb + vb)
     BHK, R, N, D, T, S, W = 1, 4, 140000, 128, 300, 17, 64
-    kp, ks = _legacy_inputs(rng, BHK, N, D, 4)
-    vp, vs = _legacy_inputs(rng, BHK, N, D, 4)
+    kp, ks = _legacy_inputs(rng, BHK, N, D, kb)
+    vp, vs = _legacy_inputs(rng, BHK, N, D, vb)
     f = lambda n: O.bf16_round(rng.standard_normal((BHK, n, D)).astype(np.float32))
     kt, vt, kst, vst, kw, vw = f(T), f(T), f(S), f(S), f(W), f(W)
     q = O.bf16_round(rng.standard_normal((BHK * R, D)).astype(np.float32))
     d = lambda a: to_dev_bf16(a, "cuda")
     u = lambda a: torch.from_numpy(a).cuda()
-    out = L.fused_decode_attention_k4v4(d(q).view(1, BHK * R, 1, D), u(kp), u(vp), u(ks), u(vs), d(kt), d(vt),
-                                        d(kst), d(vst), d(kw), d(vw), kv_repeat=R)
+    out = L.splitk_decode_attention_k4v4_mma(d(q).view(1, BHK * R, 1, D), u(kp), u(vp), u(ks), u(vs), d(kt),
+                                             d(vt), d(kst), d(vst), d(kw), d(vw), kv_repeat=R, k_bits=kb, v_bits=vb)
     oargs = (q, kp, vp, ks, vs, kt, vt, kst, vst, kw, vw)
-    ref = O.legacy_decode_fp64(*oargs, kv_repeat=R, bf16_operands=True)
-    ref_abs = O.legacy_decode_fp64(*oargs, kv_repeat=R, bf16_operands=True, abs_v=True)
-    _check("direct long prefix", out, ref, ref_abs)
+    ref = O.legacy_decode_fp64(*oargs, k_bits=kb, v_bits=vb, kv_repeat=R, bf16_operands=True)
+    ref_abs = O.legacy_decode_fp64(*oargs, k_bits=kb, v_bits=vb, kv_repeat=R, bf16_operands=True, abs_v=True)
+    _check(f"direct long prefix K{kb}V{vb}", out, ref, ref_abs)
 
 
-def test_legacy4_direct_matches_dequantise_first():
-    """The direct 4-bit path dequantises each tile in registers to the bf16
-    values legacy_dequantize writes; decoding those bf16 rows through the
-    hybrid kernel's bf16 path gives the same attention up to the order of the
-    split-K sums (here within 2^-10 of the output scale)."""
+@pytest.mark.parametrize("kb,vb", [(4, 4), (4, 2), (2, 4), (2, 2)])
+def test_legacy_direct_matches_dequantise_first(kb, vb):
+    """The direct path dequantises each tile in registers to the bf16 values
+    legacy_dequantize writes (up to an exact power of two); decoding those
+    bf16 rows through the hybrid kernel's bf16 path gives the same attention
+    up to the order of the split-K sums (here within 2^-10 of the output
+    scale)."""
     import hyquant_amd.d_stage_cache as L
     from hyquant_amd.decode_d_stage import _decode
-    print("legacy direct vs dequantise-first", flush=True)
-    rng = np.random.default_rng(404)
+    print(f"legacy direct vs dequantise-first K{kb}V{vb}", flush=True)
+    rng = np.random.default_rng(404 + 10 * kb + vb)
     BHK, R, N, D, T, S, W = 4, 4, 3000, 128, 150, 9, 64
-    kp, ks = _legacy_inputs(rng, BHK, N, D, 4)
-    vp, vs = _legacy_inputs(rng, BHK, N, D, 4)
+    kp, ks = _legacy_inputs(rng, BHK, N, D, kb)
+    vp, vs = _legacy_inputs(rng, BHK, N, D, vb)
     f = lambda n: O.bf16_round(rng.standard_normal((BHK, n, D)).astype(np.float32))
     kt, vt, kst, vst, kw, vw = f(T), f(T), f(S), f(S), f(W), f(W)
     q = O.bf16_round(rng.standard_normal((BHK * R, D)).astype(np.float32))
     d = lambda a: to_dev_bf16(a, "cuda")
     u = lambda a: torch.from_numpy(a).cuda()
-    direct = L.fused_decode_attention_k4v4(d(q).view(1, BHK * R, 1, D), u(kp), u(vp), u(ks), u(vs), d(kt), d(vt),
-                                           d(kst), d(vst), d(kw), d(vw), kv_repeat=R)
+    direct = L.splitk_decode_attention_k4v4_mma(d(q).view(1, BHK * R, 1, D), u(kp), u(vp), u(ks), u(vs), d(kt),
+                                                d(vt), d(kst), d(vst), d(kw), d(vw), kv_repeat=R, k_bits=kb, v_bits=vb)
     kf = torch.empty(BHK, N + T, D, dtype=torch.bfloat16, device="cuda")
     vf = torch.empty_like(kf)
-    L.legacy_dequantize(u(kp), u(ks), D, 4, out=kf[:, :N])
-    L.legacy_dequantize(u(vp), u(vs), D, 4, out=vf[:, :N])
+    L.legacy_dequantize(u(kp), u(ks), D, kb, out=kf[:, :N])
+    L.legacy_dequantize(u(vp), u(vs), D, vb, out=vf[:, :N])
     kf[:, N:].copy_(d(kt))
     vf[:, N:].copy_(d(vt))
     none8 = torch.empty(BHK, 0, D // 2, dtype=torch.int8, device="cuda")
@@ -239,31 +242,37 @@ def test_legacy_entry_points_reject_bad_arguments():
         L.legacy_dequantize(torch.zeros(1, 200, D // 2, dtype=torch.uint8, device="cuda"), ks, D, 4)
 
 
-def test_legacy4_direct_every_code_and_scale():
+@pytest.mark.parametrize("vb", [4, 2])
+def test_legacy_direct_every_code_and_scale(vb):
     """The direct path's in-register dequantisation against the oracle for
-    every 4-bit code with every finite fp16 scale.  Each head holds a one-token
-    prefix and no bf16 rows, so its softmax weight is exactly 1 and its output
-    row is the dequantised V row: 7936 heads x 128 channels carry the 16 x
-    63488 (code, scale) pairs.  Zeros are compared without their sign (the
-    product with P = 1 accumulates onto +0)."""
+    every V code (16 int4 or 4 int2 values) with every finite fp16 scale.
+    Each head holds a one-token prefix and no bf16 rows, so its softmax
+    weight is exactly 1 and its output row is the dequantised V row: heads x
+    128 channels carry the codes x 63488 (code, scale) pairs.  Zeros are
+    compared without their sign (the product with P = 1 accumulates onto
+    +0).  K of the same width shares the code conversion."""
     import hyquant_amd.d_stage_cache as L
-    print("legacy direct: every code and finite fp16 scale", flush=True)
+    print(f"legacy direct: every int{vb} code and finite fp16 scale", flush=True)
     D = 128
+    ncode = 1 << vb
     b = np.arange(65536, dtype=np.uint32)
     fin = b[((b >> 10) & 0x1F) != 0x1F].astype(np.uint16)          # 63488 finite fp16
-    BHK = fin.size * 16 // D
+    BHK = fin.size * ncode // D
     p = np.arange(BHK * D).reshape(BHK, D)
-    code = (p % 16).astype(np.uint8)
-    vs = fin[p // 16].reshape(BHK, 1, D).view(np.float16)
-    vp = ((code[:, 0::2] << 4) | code[:, 1::2]).reshape(BHK, 1, D // 2)
+    code = (p % ncode).astype(np.uint8)
+    vs = fin[p // ncode].reshape(BHK, 1, D).view(np.float16)
+    if vb == 4:
+        vp = ((code[:, 0::2] << 4) | code[:, 1::2]).reshape(BHK, 1, D // 2)
+    else:      # channel 4j + i in bits 7-2i..6-2i of byte j
+        vp = ((code[:, 0::4] << 6) | (code[:, 1::4] << 4) | (code[:, 2::4] << 2) | code[:, 3::4]).reshape(BHK, 1, D // 4)
     rng = np.random.default_rng(9)
     kp = rng.integers(0, 256, (BHK, 1, D // 2), dtype=np.uint8)
     ks = np.ones((BHK, 1, D), np.float16)
     q = O.bf16_round(rng.standard_normal((BHK, D)).astype(np.float32))
     eb = torch.empty(BHK, 0, D, dtype=torch.bfloat16, device="cuda")
     u = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
-    out = L.fused_decode_attention_k4v4(to_dev_bf16(q, "cuda").view(1, BHK, 1, D), u(kp), u(vp), u(ks), u(vs),
-                                        eb, eb, eb, eb, eb, eb, kv_repeat=1)
+    out = L.splitk_decode_attention_k4v4_mma(to_dev_bf16(q, "cuda").view(1, BHK, 1, D), u(kp), u(vp), u(ks), u(vs),
+                                             eb, eb, eb, eb, eb, eb, kv_repeat=1, k_bits=4, v_bits=vb)
     got = out.view(BHK, D).view(torch.int16).cpu().numpy().view(np.uint16)
-    exp = O.legacy_dequant_bf16(vp, vs, 4)[:, 0, :]
+    exp = O.legacy_dequant_bf16(vp, vs, vb)[:, 0, :]
     assert np.array_equal(np.where(got == 0x8000, 0, got), np.where(exp == 0x8000, 0, exp))

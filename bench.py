@@ -683,19 +683,86 @@ def prefill_trace_summary(trace_csv):
     return table
 
 
+def bench_legacy(dev):
+    """The legacy decode format (src/ops/d_stage_cache.py): the direct path
+    (hyq_decode_legacy: codes and [G, D] group scales read in the decode)
+    against the dequantise-first route (legacy_dequantize into bf16 rows, then
+    the fused decode's bf16 path), eager calls, kv_repeat 4, bf16 top-k N/20,
+    staging 64, window 128.  Time: best of three runs of 50 calls after 5
+    warm-up calls, events around each run.  Bytes: 16*(k_bits + v_bits) + 4
+    per prefix token and key head (codes and group scales) plus 512 per bf16
+    row."""
+    import hyquant_amd.d_stage_cache as L
+    from hyquant_amd.decode_d_stage import GROUP_SIZE, _decode
+    def timed(fn, n):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(n):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) / n * 1e3)
+        return best
+    rows = []
+    shapes = [(4, 4, 8, 7667), (4, 4, 32, 31000), (4, 4, 128, 31000), (4, 4, 128, 62000),
+              (4, 2, 128, 31000), (2, 4, 128, 31000), (2, 2, 128, 31000)]
+    for kb, vb, BHK, N in shapes:
+        R, T, S, W, D = 4, N // 20, 64, 128, 128
+        g = torch.Generator(device="cpu").manual_seed(0)
+        kp = torch.randint(0, 256, (BHK, N, 16 * kb), generator=g, dtype=torch.uint8).to(dev)
+        vp = torch.randint(0, 256, (BHK, N, 16 * vb), generator=g, dtype=torch.uint8).to(dev)
+        G = -(-N // GROUP_SIZE)
+        ks = (torch.rand(BHK, G, D, generator=g) * 0.24 - 0.12).half().to(dev)
+        vs = (torch.rand(BHK, G, D, generator=g) * 0.24 - 0.12).half().to(dev)
+        seg = [torch.randn(BHK, n, D, generator=g).bfloat16().to(dev) for n in (T, T, S, S, W, W)]
+        q = torch.randn(1, BHK * R, 1, D, generator=g).bfloat16().to(dev)
+        direct = lambda: L.splitk_decode_attention_k4v4_mma(q, kp, vp, ks, vs, *seg, kv_repeat=R,
+                                                            k_bits=kb, v_bits=vb)
+        kf = torch.empty(BHK, N + T, D, dtype=torch.bfloat16, device=dev)
+        vf = torch.empty_like(kf)
+        n8 = torch.empty(BHK, 0, D // 2, dtype=torch.int8, device=dev)
+        n16 = torch.empty(BHK, 0, dtype=torch.float16, device=dev)
+        def first():
+            L.legacy_dequantize(kp, ks, D, kb, out=kf[:, :N])
+            L.legacy_dequantize(vp, vs, D, vb, out=vf[:, :N])
+            kf[:, N:].copy_(seg[0])
+            vf[:, N:].copy_(seg[1])
+            return _decode(q.reshape(BHK * R, D), n8, n8, n16, n16, kf, vf, seg[2], seg[3], seg[4], seg[5],
+                           4, 4, R, None, 0, None, None)
+        diff = (direct().float().reshape(BHK * R, D) - first().float()).abs().max().item()
+        td, tf = timed(direct, 50), timed(first, 20)
+        nb = BHK * N * (16 * (kb + vb) + 4) + BHK * (T + S + W) * 512
+        rows.append({"k_bits": kb, "v_bits": vb, "kv_heads": BHK, "prefix": N, "direct_us": round(td, 1),
+                     "direct_gbs": round(nb / (td * 1e-6) / 1e9, 1), "dequantise_first_us": round(tf, 1),
+                     "max_abs_diff": float(f"{diff:.3g}")})
+        print(f"# legacy {rows[-1]}", file=sys.stderr, flush=True)
+        del kp, vp, ks, vs, seg, q, kf, vf
+        torch.cuda.empty_cache()
+    return rows
+
+
 def kernel_trace_summary(trace_csv):
     """Median duration per kernel (name without its argument list) and grid
-    size over every dispatch of a rocprofv3 kernel trace (run_kernel_trace.csv),
-    this library's kernels only, in microseconds."""
+    size (work-items in x, then "x" and the y extent when it is above 1) over
+    every dispatch of a rocprofv3 kernel trace (run_kernel_trace.csv), this
+    library's kernels only, in microseconds."""
     import csv
     import numpy as np
     d = {}
     for r in csv.DictReader(open(trace_csv)):
         n = r["Kernel_Name"].replace("void ", "").replace("hyq::(anonymous namespace)::", "")
         if not n.startswith(("score", "topk", "qmean", "mark", "zero_words", "compact_quant", "gather_rows",
-                             "quant_pack", "decode_kernel", "dequant", "prefill", "kv_", "lists", "per_block")):
+                             "quant_pack", "decode_kernel", "dequant", "prefill", "kv_", "lists", "per_block",
+                             "legacy")):
             continue
         grid = r.get("Grid_Size_X", r.get("Grid_Size", ""))
+        if r.get("Grid_Size_Y", "1") not in ("", "1"):
+            grid += "x" + r["Grid_Size_Y"]
         d.setdefault((n.split("(")[0], grid), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     return [{"kernel": k, "grid": g, "dispatches": len(v), "median_us": round(float(np.median(v)), 1)}
             for (k, g), v in sorted(d.items())]
@@ -831,6 +898,8 @@ def main():
                     help="per-kernel table of a kernel trace of --prefill-only (no GPU)")
     ap.add_argument("--boundary-only", action="store_true",
                     help="run the config-3 boundary section (select, freeze, flush) only")
+    ap.add_argument("--legacy-only", action="store_true",
+                    help="time the legacy-format decode (direct against dequantise-first) only")
     ap.add_argument("--kernel-trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="median duration per kernel and grid of a kernel trace (no GPU)")
     args = ap.parse_args()
@@ -868,6 +937,9 @@ def main():
         return
     if args.boundary_only:
         print(json.dumps({"config3_boundary": bench_boundary(dev)}), flush=True)
+        return
+    if args.legacy_only:
+        print(json.dumps({"legacy_decode": bench_legacy(dev)}), flush=True)
         return
 
     B, HQ, HKV, N = 1, 32, 8, 8192

@@ -1462,8 +1462,13 @@ __device__ __forceinline__ void legacy_dequant(Bf16Raw& b, const LegRaw<KB, VB>&
     }
 }
 
+// Three workgroups per CU (168 VGPRs): the tile loop keeps its registers and
+// the merge at the end spills 236 bytes per lane.  Against two per CU (213
+// VGPRs, no spill), same box, 128 KV heads: 31000 tokens K4V4 171.5 ->
+// 167-169 us, K2V2 184 -> 167-169 us; 62000 tokens 322 -> 294-297 us (waves
+// that wait on memory leave the VALU to the others: 59-67% VALU-busy at two).
 template <int KB, int VB>
-__global__ __launch_bounds__(THREADS, 2) void legacy_decode_kernel(LegArgs a) {
+__global__ __launch_bounds__(THREADS, 3) void legacy_decode_kernel(LegArgs a) {
 #ifdef HYQ_PHASE_TRACE
     uint64_t ph[TRACE_PH] = {};    // (the merge stamps; not stored by this kernel)
 #endif

@@ -1305,7 +1305,7 @@ struct LegArgs {
 };
 
 // the raw loads of one 16-token prefix tile, for the layout of Bf16Raw (the
-// group is a multiple of 16 and pieces start on group boundaries, so the
+// group is a multiple of 16 and tiles start at multiples of 16 tokens, so a
 // tile's tokens share one scale row)
 template <int KB, int VB>
 struct LegRaw {

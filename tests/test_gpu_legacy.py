@@ -276,3 +276,60 @@ def test_legacy_direct_every_code_and_scale(vb):
     got = out.view(BHK, D).view(torch.int16).cpu().numpy().view(np.uint16)
     exp = O.legacy_dequant_bf16(vp, vs, vb)[:, 0, :]
     assert np.array_equal(np.where(got == 0x8000, 0, got), np.where(exp == 0x8000, 0, exp))
+
+
+@pytest.mark.parametrize("kb,vb", [(4, 2), (2, 4)])
+def test_legacy_direct_c_abi_group_and_strides(kb, vb):
+    """hyq_decode_legacy through the C ABI with a 48-token scale group (the
+    16-token tiles never cross a group; 512-token pieces start inside one),
+    code rows and scale rows padded past their data, and a ragged 1000-token
+    prefix, against the fp64 restatement with the same group."""
+    import ctypes
+    from hyquant_amd import _lib
+    print(f"legacy direct C ABI group 48 K{kb}V{vb}", flush=True)
+    L = _lib.lib()
+    rng = np.random.default_rng(48 + kb)
+    BHK, R, N, D, T, S, W, group = 3, 4, 1000, 128, 21, 5, 40, 48
+    G = -(-N // group)
+    kp, _ = _legacy_inputs(rng, BHK, N, D, kb)
+    vp, _ = _legacy_inputs(rng, BHK, N, D, vb)
+    ks = rng.uniform(-0.12, 0.12, (BHK, G, D)).astype(np.float16)
+    vs = rng.uniform(-0.12, 0.12, (BHK, G, D)).astype(np.float16)
+    kbuf = np.zeros((BHK, N, 16 * kb + 16), np.uint8)
+    kbuf[:, :, :16 * kb] = kp
+    vbuf = np.zeros((BHK, N, 16 * vb + 4), np.uint8)
+    vbuf[:, :, :16 * vb] = vp
+    ksbuf = np.zeros((BHK, G, D + 8), np.float16)
+    ksbuf[:, :, :D] = ks
+    vsbuf = np.zeros((BHK, G, D + 8), np.float16)
+    vsbuf[:, :, :D] = vs
+    f = lambda n: O.bf16_round(rng.standard_normal((BHK, n, D)).astype(np.float32))
+    kt, vt, kst, vst, kw, vw = f(T), f(T), f(S), f(S), f(W), f(W)
+    q = O.bf16_round(rng.standard_normal((BHK * R, D)).astype(np.float32))
+    u = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    d = lambda a: to_dev_bf16(a, "cuda")
+    keep = [u(kbuf), u(vbuf), u(ksbuf), u(vsbuf), d(kt), d(vt), d(kst), d(vst), d(kw), d(vw), d(q)]
+    out = torch.empty(BHK * R, D, dtype=torch.bfloat16, device="cuda")
+    p = _lib.LegacyParams()
+    p.q, p.q_stride = keep[10].data_ptr(), D
+    p.out, p.out_stride = out.data_ptr(), D
+    p.k_codes, p.kc_stride_bh, p.kc_stride_n = keep[0].data_ptr(), N * (16 * kb + 16), 16 * kb + 16
+    p.v_codes, p.vc_stride_bh, p.vc_stride_n = keep[1].data_ptr(), N * (16 * vb + 4), 16 * vb + 4
+    p.k_scale, p.ks_stride_bh, p.ks_stride_g = keep[2].data_ptr(), G * (D + 8), D + 8
+    p.v_scale, p.vs_stride_bh, p.vs_stride_g = keep[3].data_ptr(), G * (D + 8), D + 8
+    p.n, p.group, p.k_bits, p.v_bits = N, group, kb, vb
+    for i, (sk, sv, n) in enumerate(((keep[4], keep[5], T), (keep[6], keep[7], S), (keep[8], keep[9], W))):
+        p.seg_k[i], p.seg_v[i], p.seg_k_stride_bh[i], p.seg_v_stride_bh[i], p.seg_n[i] = (
+            sk.data_ptr(), sv.data_ptr(), n * D, n * D, n)
+    p.bh_kv, p.kv_repeat, p.head_dim, p.sm_scale = BHK, R, D, D ** -0.5
+    need = L.hyq_decode_legacy_workspace_size(ctypes.byref(p))
+    assert need > 0
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    st = L.hyq_decode_legacy(ctypes.byref(p), ws.data_ptr(), need, torch.cuda.current_stream().cuda_stream)
+    assert st == 0, L.hyq_last_error()
+    torch.cuda.synchronize()
+    oargs = (q, kp, vp, ks, vs, kt, vt, kst, vst, kw, vw)
+    ref = O.legacy_decode_fp64(*oargs, k_bits=kb, v_bits=vb, kv_repeat=R, group=group, bf16_operands=True)
+    ref_abs = O.legacy_decode_fp64(*oargs, k_bits=kb, v_bits=vb, kv_repeat=R, group=group, bf16_operands=True,
+                                   abs_v=True)
+    _check(f"C ABI group 48 K{kb}V{vb}", out, ref, ref_abs)

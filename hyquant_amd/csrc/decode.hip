@@ -1269,11 +1269,14 @@ __global__ __launch_bounds__(THREADS, 2) void decode_kernel(DecArgs a) {
 // (bf16_compute): the result of dequantising the prefix and decoding bf16
 // rows, without the bf16 copy in HBM.  One workgroup per piece
 // (LEG_PIECE prefix tokens or BF_PIECE rows of one segment, the same number
-// of bytes; doubled together while the prefix still gives every resident
-// workgroup slot a piece, up to LEG_PIECE_MAX tokens, and for long caches
-// until the pieces fit the merge tables), merged by the head's last arriving
-// workgroup with decode_kernel's protocol and merge.
+// of bytes; halved together, down to LEG_PIECE_MIN tokens, while the grid
+// would leave a CU without a workgroup; doubled together while the prefix
+// still gives every resident workgroup slot a piece, up to LEG_PIECE_MAX
+// tokens, and for long caches until the pieces fit the merge tables), merged
+// by the head's last arriving workgroup with decode_kernel's protocol and
+// merge.
 constexpr int LEG_PIECE = 512;
+constexpr int LEG_PIECE_MIN = 128;
 constexpr int LEG_PIECE_MAX = 4096;
 constexpr int BF_PIECE = 128;
 
@@ -1923,7 +1926,16 @@ LegPlan legacy_plan(const hyq_legacy_params* p) {
     LegPlan pl;
     const int64_t n[4] = {p->n, p->seg_n[0], p->seg_n[1], p->seg_n[2]};
     const int sl = legacy_slots(p->k_bits, p->v_bits, p->kv_repeat);
-    const int64_t slots = sl > 0 ? sl : 512;
+    const int64_t slots = sl > 0 ? sl : 768;
+    // few heads: halve the pieces (down to 128 prefix tokens) while the grid
+    // would leave CUs without a workgroup (slots / 3: one per CU)
+    auto pieces = [&]() {
+        int64_t t = 0;
+        for (int s = 0; s < 4; ++s) t += (n[s] + pl.plen[s] - 1) / pl.plen[s];
+        return t * p->bh_kv;
+    };
+    while (pl.plen[0] > LEG_PIECE_MIN && pieces() < slots / 3)
+        for (int s = 0; s < 4; ++s) pl.plen[s] /= 2;
     while (pl.plen[0] < LEG_PIECE_MAX &&
            static_cast<int64_t>(p->bh_kv) * ((n[0] + 2 * pl.plen[0] - 1) / (2 * pl.plen[0])) >= slots)
         for (int s = 0; s < 4; ++s) pl.plen[s] *= 2;

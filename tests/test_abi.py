@@ -242,7 +242,7 @@ def _legacy_params(_lib, **kw):
 def test_legacy_host_validation():
     """hyq_decode_legacy's checks run on the host before any launch: a valid
     parameter block gets a workspace size (arrival counters, then the (m, l)
-    table and partials of 2 + 1 pieces per head); each invalid one gets size 0
+    table and partials of its pieces); each invalid one gets size 0
     and its status, and a valid call without a workspace is refused.  Code
     rows are checked against the loads of their bit width: a 4*k_bits-byte K
     load and v_bits-byte V loads per lane, rows of at least 16*bits bytes."""

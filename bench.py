@@ -688,10 +688,12 @@ def bench_legacy(dev):
     (hyq_decode_legacy: codes and [G, D] group scales read in the decode)
     against the dequantise-first route (legacy_dequantize into bf16 rows, then
     the fused decode's bf16 path), eager calls, kv_repeat 4, bf16 top-k N/20,
-    staging 64, window 128.  Time: best of three runs of 50 calls after 5
-    warm-up calls, events around each run.  Bytes: 16*(k_bits + v_bits) + 4
-    per prefix token and key head (codes and group scales) plus 512 per bf16
-    row."""
+    staging 64, window 128.  The calls rotate over copies of the inputs that
+    cover at least 1 GiB together, so that every call streams its bytes from
+    HBM (not from the 256 MiB Infinity Cache).  Time: best of three runs of
+    50 calls after 5 warm-up calls, events around each run.  Bytes:
+    16*(k_bits + v_bits) + 4 per prefix token and key head (codes and group
+    scales) plus 512 per bf16 row."""
     import hyquant_amd.d_stage_cache as L
     from hyquant_amd.decode_d_stage import GROUP_SIZE, _decode
     def timed(fn, n):
@@ -713,35 +715,48 @@ def bench_legacy(dev):
               (4, 2, 128, 31000), (2, 4, 128, 31000), (2, 2, 128, 31000)]
     for kb, vb, BHK, N in shapes:
         R, T, S, W, D = 4, N // 20, 64, 128, 128
-        g = torch.Generator(device="cpu").manual_seed(0)
-        kp = torch.randint(0, 256, (BHK, N, 16 * kb), generator=g, dtype=torch.uint8).to(dev)
-        vp = torch.randint(0, 256, (BHK, N, 16 * vb), generator=g, dtype=torch.uint8).to(dev)
         G = -(-N // GROUP_SIZE)
-        ks = (torch.rand(BHK, G, D, generator=g) * 0.24 - 0.12).half().to(dev)
-        vs = (torch.rand(BHK, G, D, generator=g) * 0.24 - 0.12).half().to(dev)
-        seg = [torch.randn(BHK, n, D, generator=g).bfloat16().to(dev) for n in (T, T, S, S, W, W)]
-        q = torch.randn(1, BHK * R, 1, D, generator=g).bfloat16().to(dev)
-        direct = lambda: L.splitk_decode_attention_k4v4_mma(q, kp, vp, ks, vs, *seg, kv_repeat=R,
-                                                            k_bits=kb, v_bits=vb)
+        nb = BHK * N * (16 * (kb + vb) + 4) + BHK * (T + S + W) * 512
+        torch.manual_seed(0)
+
+        def inputs():
+            return (torch.randint(0, 256, (BHK, N, 16 * kb), dtype=torch.uint8, device=dev),
+                    torch.randint(0, 256, (BHK, N, 16 * vb), dtype=torch.uint8, device=dev),
+                    (torch.rand(BHK, G, D, device=dev) * 0.24 - 0.12).half(),
+                    (torch.rand(BHK, G, D, device=dev) * 0.24 - 0.12).half(),
+                    [torch.randn(BHK, n, D, device=dev).bfloat16() for n in (T, T, S, S, W, W)],
+                    torch.randn(1, BHK * R, 1, D, device=dev).bfloat16())
+        copies = [inputs() for _ in range(copies_for(nb))]
+        it = [0]
+
+        def nxt():
+            c = copies[it[0] % len(copies)]
+            it[0] += 1
+            return c
+
+        def direct(c=None):
+            kp, vp, ks, vs, seg, q = c or nxt()
+            return L.splitk_decode_attention_k4v4_mma(q, kp, vp, ks, vs, *seg, kv_repeat=R, k_bits=kb, v_bits=vb)
         kf = torch.empty(BHK, N + T, D, dtype=torch.bfloat16, device=dev)
         vf = torch.empty_like(kf)
         n8 = torch.empty(BHK, 0, D // 2, dtype=torch.int8, device=dev)
         n16 = torch.empty(BHK, 0, dtype=torch.float16, device=dev)
-        def first():
+
+        def first(c=None):
+            kp, vp, ks, vs, seg, q = c or nxt()
             L.legacy_dequantize(kp, ks, D, kb, out=kf[:, :N])
             L.legacy_dequantize(vp, vs, D, vb, out=vf[:, :N])
             kf[:, N:].copy_(seg[0])
             vf[:, N:].copy_(seg[1])
             return _decode(q.reshape(BHK * R, D), n8, n8, n16, n16, kf, vf, seg[2], seg[3], seg[4], seg[5],
                            4, 4, R, None, 0, None, None)
-        diff = (direct().float().reshape(BHK * R, D) - first().float()).abs().max().item()
+        diff = (direct(copies[0]).float().reshape(BHK * R, D) - first(copies[0]).float()).abs().max().item()
         td, tf = timed(direct, 50), timed(first, 20)
-        nb = BHK * N * (16 * (kb + vb) + 4) + BHK * (T + S + W) * 512
         rows.append({"k_bits": kb, "v_bits": vb, "kv_heads": BHK, "prefix": N, "direct_us": round(td, 1),
                      "direct_gbs": round(nb / (td * 1e-6) / 1e9, 1), "dequantise_first_us": round(tf, 1),
-                     "max_abs_diff": float(f"{diff:.3g}")})
+                     "max_abs_diff": float(f"{diff:.3g}"), "input_copies": len(copies)})
         print(f"# legacy {rows[-1]}", file=sys.stderr, flush=True)
-        del kp, vp, ks, vs, seg, q, kf, vf
+        del copies, kf, vf
         torch.cuda.empty_cache()
     return rows
 

@@ -1335,19 +1335,23 @@ __device__ __forceinline__ void legacy_fetch(LegRaw<KB, VB>& r, const LegArgs& a
     const uint32_t sks = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(g * a.ks_g * 2));
     const uint32_t svc = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tu * a.vc_n));
     const uint32_t svs = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(g * a.vs_g * 2));
+    // codes are read once: non-temporal, as the fused decode's packed rows
+    // (with inputs rotated over 1 GiB: 128 KV heads at 62000 tokens 300-307
+    // -> 290 us, 32 heads 50.5-51.0 -> 49.0-49.5 us); the scale rows, read by
+    // every tile of their group, keep the default policy
     if constexpr (KB == 4) {
-        const u32x4 w = bld128(rkc, kco, skc);
+        const u32x4 w = bld128<NT>(rkc, kco, skc);
         r.kc[0] = w[0]; r.kc[1] = w[1]; r.kc[2] = w[2]; r.kc[3] = w[3];
     } else {
-        const u32x2 w = bld64(rkc, kco, skc);
+        const u32x2 w = bld64<NT>(rkc, kco, skc);
         r.kc[0] = w[0]; r.kc[1] = w[1];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.ksc[i] = bld128(rks, static_cast<uint32_t>(64 * kb + 16 * i), sks);
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-        r.vc[e] = VB == 4 ? bld32(rvc, vco + static_cast<uint32_t>(e * a.vc_n), svc)
-                          : bld16(rvc, vco + static_cast<uint32_t>(e * a.vc_n), svc);
+        r.vc[e] = VB == 4 ? bld32<NT>(rvc, vco + static_cast<uint32_t>(e * a.vc_n), svc)
+                          : bld16<NT>(rvc, vco + static_cast<uint32_t>(e * a.vc_n), svc);
     r.vsc = bld128(rvs, static_cast<uint32_t>(16 * c), svs);
 }
 
